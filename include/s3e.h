@@ -1,0 +1,199 @@
+/*
+ * s3e.h — C ABI of the MI355X image-encoder engine for sam3.cpp model files.
+ *
+ * The engine replaces the two ggml operators that dominate sam3.cpp's image
+ * encoders (ggml_mul_mat on Q4_0/Q4_1/Q8_0/F16/F32 weights and
+ * ggml_flash_attn_ext) and the encoder graph that strings them together,
+ * behind plain C entry points: pointers, sizes and status codes, no C++ or
+ * torch types.  All calls return 0 (S3E_OK) on success; on failure they
+ * return a non-zero status and s3e_last_error() describes the cause.  No
+ * exception crosses this boundary.
+ *
+ * Memory: pointers documented as "device" are HBM addresses on the context's
+ * device (from s3e_malloc or any HIP allocator); "host" pointers are ordinary
+ * process memory.  Every compute call is asynchronous on the context's HIP
+ * stream; s3e_ctx_sync() waits for it.
+ *
+ * Threading: one caller thread per context at a time, as sam3.cpp allows one
+ * caller per sam3_state (sam3.cpp:1015-1026 resets the backend per call).
+ * Models are read-only after loading and may be shared by contexts on the
+ * same device.
+ */
+#ifndef S3E_H
+#define S3E_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define S3E_ABI_VERSION 1
+
+enum s3e_status {
+    S3E_OK = 0,
+    S3E_ERR_INVALID = 1,     /* bad argument or shape */
+    S3E_ERR_HIP = 2,         /* HIP runtime error */
+    S3E_ERR_IO = 3,          /* file missing, truncated or malformed */
+    S3E_ERR_UNSUPPORTED = 4, /* valid input this engine does not handle */
+    S3E_ERR_NOMEM = 5,       /* allocation failed */
+};
+
+/* ggml type ids as stored in sam3.cpp model files (sam3.cpp:3242-3248). */
+enum s3e_type {
+    S3E_TYPE_F32 = 0,
+    S3E_TYPE_F16 = 1,
+    S3E_TYPE_Q4_0 = 2,
+    S3E_TYPE_Q4_1 = 3,
+    S3E_TYPE_Q8_0 = 8,
+    S3E_TYPE_Q8_1 = 9,
+};
+
+typedef struct s3e_ctx s3e_ctx;       /* device + HIP stream */
+typedef struct s3e_weight s3e_weight; /* one uploaded weight matrix */
+typedef struct s3e_model s3e_model;   /* SAM 3 ViT backbone weights */
+typedef struct s3e_state s3e_state;   /* per-image activations and outputs */
+
+/* Last error message of the calling thread ("" if none). */
+const char *s3e_last_error(void);
+int s3e_abi_version(void);
+
+/* ---- context ------------------------------------------------------------
+ * Replaces the ggml backend selection of sam3_load_model
+ * (sam3.cpp:3274-3288) and the per-call backend setup of sam3_graph_compute
+ * (sam3.cpp:1015-1026). */
+int s3e_ctx_create(int device, s3e_ctx **out);
+void s3e_ctx_destroy(s3e_ctx *ctx);
+int s3e_ctx_sync(s3e_ctx *ctx);
+/* The context's hipStream_t, for callers that record events on it. */
+void *s3e_ctx_stream(s3e_ctx *ctx);
+
+/* Device-memory helpers for FFI callers without their own allocator
+ * (the role ggml_backend_alloc_ctx_tensors / ggml_backend_tensor_set/get play
+ * in sam3.cpp:3300-3330, 6115). */
+int s3e_malloc(s3e_ctx *ctx, size_t bytes, void **out);
+int s3e_free(s3e_ctx *ctx, void *ptr);
+int s3e_memcpy_h2d(s3e_ctx *ctx, void *dst, const void *src, size_t bytes);
+int s3e_memcpy_d2h(s3e_ctx *ctx, void *dst, const void *src, size_t bytes);
+
+/* ---- ggml_mul_mat --------------------------------------------------------
+ * Upload one weight matrix given as ggml bytes: ne0 = K (the contiguous
+ * dimension), ne1 = N rows, in `type` (F32, F16, Q4_0, Q4_1 or Q8_0), exactly
+ * as a sam3.cpp model file stores it (sam3.cpp:3091-3143).  The engine
+ * repacks the blocks into its own HBM layout.  Replaces the weight tensors
+ * that sam3_load_tensors fills (sam3.cpp:3145-3150). */
+int s3e_weight_upload(s3e_ctx *ctx, int type, int64_t ne0, int64_t ne1,
+                      const void *host_data, size_t nbytes, s3e_weight **out);
+void s3e_weight_free(s3e_weight *w);
+/* out[0]=type, out[1]=K, out[2]=N, out[3]=device bytes held. */
+int s3e_weight_info(const s3e_weight *w, int64_t out[4]);
+
+/* Y = ggml_add(ggml_mul_mat(W, X), bias): X is M rows of K f32 (device),
+ * Y is M rows of N f32 (device), bias is N f32 (device) or NULL.  X is first
+ * converted to W's vec_dot type exactly as ggml's CPU path converts src1
+ * (Q8_0 for Q4_0/Q8_0, Q8_1 for Q4_1, F16 for F16, none for F32).
+ * Replaces ggml_mul_mat + ggml_add at sam3.cpp:3738-3739, 3779-3780,
+ * 3792-3796. */
+int s3e_mul_mat(s3e_ctx *ctx, const s3e_weight *w, const float *X, int64_t M,
+                const float *bias, float *Y);
+
+/* Convert M rows of K f32 (device) into a vec_dot type, as ggml's
+ * from_float does for src1 of ggml_mul_mat: `type` is Q8_0, Q8_1 or F16.
+ * For Q8_0/Q8_1 `qs` receives M*K int8 (row-major), `d` receives M*K/32
+ * fp16 scales and, for Q8_1, `s` receives M*K/32 fp16 sums (d·Σq).  For F16
+ * `qs` receives M*K fp16 and d, s are unused.  All device pointers. */
+int s3e_quantize_rows(s3e_ctx *ctx, int type, const float *X, int64_t M, int64_t K,
+                      void *qs, uint16_t *d, uint16_t *s);
+
+/* sam3_layer_norm (sam3.cpp:1037-1047): y = ggml_norm(x, eps)·w + b over rows
+ * of n f32 (device), w/b of n f32 or NULL.  Mean and variance accumulate in
+ * double as ggml_norm does, so the result is bit-identical to the CPU path.
+ * x and y may alias.  n must be a multiple of 32 and at most 4096. */
+int s3e_layer_norm(s3e_ctx *ctx, const float *x, int64_t rows, int64_t n, float eps,
+                   const float *w, const float *b, float *y);
+
+/* ---- ggml_flash_attn_ext -------------------------------------------------
+ * O = softmax(scale·Q·Kᵀ)·V with mask = NULL, max_bias = 0, softcap = 0, as
+ * sam3.cpp:3774 and the isolated core at sam3.cpp:6778-6823 call it.
+ * Tensors are f32 device memory addressed by ggml-style element strides:
+ * Q(b,h,i,d) = q[b*q_nb[3] + h*q_nb[2] + i*q_nb[1] + d] (d contiguous), K and
+ * V likewise (V may be the strided view of sam3.cpp:3762-3763).  O follows
+ * ggml's output layout [D, nh, Nq, B]: o[((b*Nq + i)*nh + h)*D + d].
+ * D must be 64.  `prec` mirrors ggml_flash_attn_ext_set_prec:
+ * S3E_PREC_DEFAULT computes on fp16 MFMA with Q, K, V and the
+ * probabilities rounded to fp16 (fp32 accumulation); S3E_PREC_F32 carries
+ * each operand as an fp16 pair (hi + lo) and reproduces f32 attention,
+ * as ggml's CPU path computes it, to ~1e-7. */
+enum s3e_prec { S3E_PREC_DEFAULT = 0, S3E_PREC_F32 = 1 };
+int s3e_flash_attn_ext(s3e_ctx *ctx,
+                       const float *q, const int64_t q_nb[4],
+                       const float *k, const int64_t k_nb[4],
+                       const float *v, const int64_t v_nb[4],
+                       int64_t D, int64_t Nq, int64_t Nkv, int64_t nh, int64_t B,
+                       float scale, int prec, float *o);
+
+/* ---- encoder -------------------------------------------------------------
+ * Load the SAM 3 ViT backbone of a sam3.cpp model file (magic "sam3",
+ * version 3; sam3.cpp:3200-3344).  Only the "vit." tensors are read; other
+ * records are skipped, so full and visual-only files both load.  Replaces
+ * the encoder part of sam3_load_model (sam3.h:184). */
+int s3e_model_load(s3e_ctx *ctx, const char *path, s3e_model **out);
+void s3e_model_free(s3e_model *m);
+/* out[0..15]: img_size, patch, E, depth, heads, mlp, window, n_global,
+ * global_idx[4], ftype, tokens per side, 0, 0. */
+int s3e_model_hparams(const s3e_model *m, int32_t out[16]);
+
+/* Per-image state holding activations and outputs (sam3_create_state,
+ * sam3.h:196; outputs of sam3.cpp:896-928). */
+int s3e_state_create(s3e_ctx *ctx, const s3e_model *m, s3e_state **out);
+void s3e_state_free(s3e_state *st);
+
+/* Encode a preprocessed CHW f32 image of img_size² (device pointer).
+ * Replaces the graph build + compute of sam3_encode_image
+ * (sam3.cpp:6051-6131) and sam3_encode_image_from_preprocessed
+ * (sam3.cpp:7287-7482) for the backbone; result in state tensor
+ * "vit_output" [E, W, H] = W*H rows of E f32. */
+int s3e_encode_chw(s3e_state *st, const float *chw_device);
+/* Same from host memory (uploads first). */
+int s3e_encode_chw_host(s3e_state *st, const float *chw_host);
+/* sam3_encode_image (sam3.h:216): HWC RGB uint8 of any size; resized and
+ * normalised on the host exactly as sam3_preprocess_image
+ * (sam3.cpp:3441-3514), then encoded. */
+int s3e_encode_image_u8(s3e_state *st, const uint8_t *hwc, int width, int height);
+
+/* Stage hooks (sam3_test_run_vit_block_stage, sam3.h:489 / sam3.cpp:6874):
+ * prefix writes x (device, T rows of E f32) from a device CHW image; block
+ * runs ViT block idx in place on x. */
+int s3e_vit_prefix(s3e_state *st, const float *chw_device, float *x_device);
+int s3e_vit_block(s3e_state *st, int idx, float *x_device);
+
+/* State outputs by name (sam3_get_state_tensor_info / sam3_dump_state_tensor,
+ * sam3.h:407-414, sam3.cpp:14334-14376).  Names: "vit_output".
+ * ne receives the ggml shape; get copies n floats to host memory. */
+int s3e_state_tensor_info(const s3e_state *st, const char *name, int64_t ne[4]);
+int s3e_state_tensor_get(const s3e_state *st, const char *name, float *host, size_t n);
+const float *s3e_state_tensor_device(const s3e_state *st, const char *name);
+
+/* ---- synthetic model files -----------------------------------------------
+ * Write a random-init SAM 3 visual-only model file in sam3.cpp's format
+ * (header + hparams per convert_sam3_to_ggml.py:27-67, 202-255), with
+ * weights N(0, std²) from mt19937_64(seed) via Box-Muller, biases 0,
+ * LayerNorm γ=1 β=0, freqs_cis from sam3_compute_axial_cis
+ * (sam3.cpp:3555-3586; windows scale 1, global scale window/grid), and
+ * linear weights quantized by the reference quantizers the way
+ * examples/quantize.cpp:195-266 decides (ftype 0, 1, 2, 3 or 8).
+ * Replaces the converter + quantize tool for synthetic-weight runs. */
+typedef struct s3e_synth_cfg {
+    int32_t img_size, patch, embed_dim, depth, heads, mlp_ratio_x1000, window;
+    int32_t n_global, global_idx[4];
+    int32_t ftype;
+    uint64_t seed;
+    float std;
+} s3e_synth_cfg;
+int s3e_synth_write(const char *path, const s3e_synth_cfg *cfg);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* S3E_H */

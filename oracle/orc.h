@@ -1,0 +1,124 @@
+/*
+ * orc.h — CPU oracle for the sam3.cpp image-encoder hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This is a plain-C restatement of the arithmetic
+ * that sam3.cpp's encoder graph performs through ggml's CPU backend
+ * (ggml_mul_mat, ggml_flash_attn_ext, ggml_norm, ggml_gelu_erf, RoPE,
+ * window partition, patch-embed conv).  Only tests/, __graft_entry__.smoke()
+ * and bench.py's cpu_baseline leg may load it, and only as the checker or
+ * the timed CPU baseline; the product path never links or calls it.
+ *
+ * ggml itself is not available to this build (the submodule referenced by
+ * .gitmodules:1-3 is empty), so every ggml-internal behaviour restated here
+ * is marked [ext] at its definition, with the public ggml source it follows.
+ *
+ * Layouts follow ggml's ne order, fastest dimension first.  A matrix that
+ * ggml calls [K, M] is stored here as M rows of K contiguous elements.
+ *
+ * Parity status per function is listed in orc_core.c's header comment.
+ */
+#ifndef SAM3_ORACLE_ORC_H
+#define SAM3_ORACLE_ORC_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml type ids (sam3.cpp:3242-3248 switch, examples/quantize.cpp:63). */
+enum {
+    ORC_TYPE_F32  = 0,
+    ORC_TYPE_F16  = 1,
+    ORC_TYPE_Q4_0 = 2,
+    ORC_TYPE_Q4_1 = 3,
+    ORC_TYPE_Q8_0 = 8,
+    ORC_TYPE_Q8_1 = 9,
+};
+
+/* ---- scalar conversions ------------------------------------------------ */
+uint16_t orc_fp32_to_fp16(float f);            /* round to nearest even */
+float    orc_fp16_to_fp32(uint16_t h);
+void     orc_fp32_to_fp16_row(const float *x, uint16_t *y, int64_t n);
+void     orc_fp16_to_fp32_row(const uint16_t *x, float *y, int64_t n);
+
+/* ---- block formats ------------------------------------------------------ */
+int64_t  orc_blck_size(int type);               /* 1 or 32 */
+size_t   orc_type_size(int type);               /* bytes per block */
+size_t   orc_row_size(int type, int64_t ne0);   /* ggml_row_size */
+int      orc_vec_dot_type(int wtype);           /* ggml vec_dot_type */
+
+/* Reference quantizers used by ggml_quantize_chunk (weights). */
+void orc_quantize_row_q4_0_ref(const float *x, void *y, int64_t k);
+void orc_quantize_row_q4_1_ref(const float *x, void *y, int64_t k);
+void orc_quantize_row_q8_0_ref(const float *x, void *y, int64_t k);
+void orc_quantize_row_q8_1_ref(const float *x, void *y, int64_t k);
+/* from_float of the vec_dot type on x86 SIMD (activations). */
+void orc_quantize_row_q8_0(const float *x, void *y, int64_t k);
+void orc_quantize_row_q8_1(const float *x, void *y, int64_t k);
+/* Convert a row of f32 into `type` the way mul_mat converts src1. */
+void orc_from_float(int type, const float *x, void *y, int64_t k);
+void orc_dequantize_row(int type, const void *x, float *y, int64_t k);
+
+/* ---- dot products (ggml vec_dot_<wtype>_<vec_dot_type>, AVX2 order) ---- */
+float orc_vec_dot(int wtype, int64_t n, const void *w_row, const void *x_row);
+/* 0 (default): ggml's x86 AVX2 evaluation order; 1: ggml's generic scalar
+ * order.  Same block math, different fp32 rounding — for measuring the
+ * order sensitivity of the reference itself. */
+void  orc_set_variant(int v);
+/* Exact per-block integer sums Σ q_w·q_x of one (w row, x row) pair. */
+void  orc_block_isums(int wtype, int64_t n, const void *w_row, const void *x_row, int32_t *out);
+
+/* ---- operators ---------------------------------------------------------- */
+/* ggml_mul_mat(W, X): W is N rows of K in `wtype`, X is M rows of K f32,
+ * Y is M rows of N f32.  X is converted to the vec_dot type first. */
+void orc_mul_mat(int wtype, const void *W, int64_t N, int64_t K,
+                 const float *X, int64_t M, float *Y, int nthreads);
+/* Same, with X already in the vec_dot type (row stride orc_row_size). */
+void orc_mul_mat_preq(int wtype, const void *W, int64_t N, int64_t K,
+                      const void *Xq, int64_t M, float *Y, int nthreads);
+
+/* ggml_norm(x, eps) then *w then +b (w, b may be NULL). rows of n. */
+void orc_layer_norm(const float *x, float *y, int64_t rows, int64_t n, float eps,
+                    const float *w, const float *b, int nthreads);
+void orc_gelu_erf(float *x, int64_t n);
+
+/* RoPE (sam3.cpp:3667-3706): x is [HD, N, nh] with HD fastest (a row of HD
+ * per token per head), freqs is [2, HD/2, N] (cos, sin). In place. */
+void orc_rope(float *x, int64_t HD, int64_t N, int64_t nh, const float *freqs);
+
+/* ggml_flash_attn_ext with mask=NULL, max_bias=0, softcap=0, F32 Q/K/V.
+ * Q(b,h,i,d) at q[b*qs3 + h*qs2 + i*qs1 + d] (element strides);
+ * K, V likewise.  O is [D, nh, Nq, B]: o[((b*Nq + i)*nh + h)*D + d]. */
+void orc_flash_attn_ext(const float *q, int64_t qs1, int64_t qs2, int64_t qs3,
+                        const float *k, int64_t ks1, int64_t ks2, int64_t ks3,
+                        const float *v, int64_t vs1, int64_t vs2, int64_t vs3,
+                        int64_t D, int64_t Nq, int64_t Nkv, int64_t nh, int64_t B,
+                        float scale, float *o, int nthreads);
+
+/* sam3_compute_axial_cis (sam3.cpp:3555-3586): out [N=end_x*end_y][dim/2][2]. */
+void orc_compute_axial_cis(float *out, int dim, int end_x, int end_y,
+                           float theta, float scale_pos);
+
+/* sam3_preprocess_image (sam3.cpp:3441-3514): HWC uint8 → CHW f32. */
+void orc_preprocess_sam3(const uint8_t *img, int w, int h, int img_size, float *chw);
+
+/* ---- SAM 3 ViT encoder (sam3.cpp:3706-3849) ----------------------------- */
+typedef struct orc_model orc_model;
+orc_model *orc_model_load(const char *path);      /* NULL on failure */
+void       orc_model_free(orc_model *m);
+const char *orc_last_error(void);
+/* hparams: img_size, patch, E, depth, heads, mlp, window, n_global, g0..g3, ftype */
+void orc_model_hparams(const orc_model *m, int32_t out[16]);
+/* Prefix (patch embed + tiled pos + ln_pre): chw [3][img][img] → x [T][E]. */
+int  orc_vit_prefix(const orc_model *m, const float *chw, float *x, int nthreads);
+/* One block in place on x [T][E]. */
+int  orc_vit_block(const orc_model *m, int idx, float *x, int nthreads);
+/* Whole backbone: chw → vit_output [T][E]. */
+int  orc_vit_encode(const orc_model *m, const float *chw, float *out, int nthreads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,335 @@
+/*
+ * orc_vit.c — CPU oracle: GGML model-file reader and the SAM 3 ViT backbone.
+ * TEST INFRASTRUCTURE ONLY (see orc.h).
+ *
+ * File format: sam3.cpp:3200-3344 (header), :1477-1520 (SAM3 hparams),
+ * :3091-3194 (tensor records, 32-byte aligned data, dtype coercion to the
+ * registered type).  Registered types: sam3.cpp:2461-2557 (T2/T4 use the
+ * file's weight type when ne[0] is a multiple of the block size, F32
+ * otherwise; T1f/T3f/T4f are always F32).
+ *
+ * Backbone graph: sam3_build_vit_prefix_graph (sam3.cpp:3806-3830) and
+ * sam3_vit_block_forward (sam3.cpp:3710-3801).
+ */
+#define _GNU_SOURCE
+#include "orc.h"
+
+#include <fcntl.h>
+#include <math.h>
+#include <omp.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+static __thread char g_err[512];
+const char *orc_last_error(void) { return g_err; }
+#define ORC_FAIL(...) do { snprintf(g_err, sizeof g_err, __VA_ARGS__); goto fail; } while (0)
+
+typedef struct {
+    char name[96];
+    int type;        /* registered (in-memory) type */
+    int64_t ne[4];
+    void *data;      /* owned */
+} orc_tensor;
+
+typedef struct {
+    int32_t img_size, patch, E, depth, heads, mlp, window, n_global, gidx[4];
+} orc_hp;
+
+struct orc_model {
+    orc_hp hp;
+    int ftype, wtype;
+    int n_tensors;
+    orc_tensor *t;
+};
+
+static const orc_tensor *find(const orc_model *m, const char *name) {
+    for (int i = 0; i < m->n_tensors; i++) {
+        if (strcmp(m->t[i].name, name) == 0) return &m->t[i];
+    }
+    return NULL;
+}
+
+static const orc_tensor *findf(const orc_model *m, const char *fmt, int i) {
+    char buf[96];
+    snprintf(buf, sizeof buf, fmt, i);
+    return find(m, buf);
+}
+
+static int is_global(const orc_hp *hp, int idx) {
+    for (int i = 0; i < hp->n_global && i < 4; i++) {
+        if (hp->gidx[i] == idx) return 1;
+    }
+    return 0;
+}
+
+/* Names registered with T1f/T3f/T4f (always F32) among the encoder's tensors
+ * (sam3.cpp:2527-2557). Everything else 2D+ follows the T2/T4 rule. */
+static int registered_type(const char *name, int n_dims, int64_t ne0, int wtype) {
+    if (n_dims < 2) return ORC_TYPE_F32;
+    if (strstr(name, "pos_embed") || strstr(name, "freqs_cis")) return ORC_TYPE_F32;
+    const int64_t blk = orc_blck_size(wtype);
+    return (ne0 % blk == 0) ? wtype : ORC_TYPE_F32;
+}
+
+static int ftype_to_wtype(int ftype) {
+    switch (ftype) {
+        case 0: return ORC_TYPE_F32;
+        case 1: return ORC_TYPE_F16;
+        case 2: return ORC_TYPE_Q4_0;
+        case 3: return ORC_TYPE_Q4_1;
+        case 8: return ORC_TYPE_Q8_0;
+        default: return -1;
+    }
+}
+
+orc_model *orc_model_load(const char *path) {
+    orc_model *m = (orc_model *)calloc(1, sizeof(orc_model));
+    int fd = -1;
+    uint8_t *map = NULL;
+    size_t fsize = 0;
+    fd = open(path, O_RDONLY);
+    if (fd < 0) ORC_FAIL("cannot open %s", path);
+    struct stat st;
+    if (fstat(fd, &st) != 0) ORC_FAIL("stat failed");
+    fsize = (size_t)st.st_size;
+    map = (uint8_t *)mmap(NULL, fsize, PROT_READ, MAP_PRIVATE, fd, 0);
+    if (map == MAP_FAILED) { map = NULL; ORC_FAIL("mmap failed"); }
+    size_t off = 0;
+#define RD32(dst) do { if (off + 4 > fsize) ORC_FAIL("truncated file"); memcpy(&(dst), map + off, 4); off += 4; } while (0)
+    uint32_t magic; int32_t version, ftype, n_tensors;
+    RD32(magic); RD32(version); RD32(ftype); RD32(n_tensors);
+    if (magic != 0x73616D33u) ORC_FAIL("bad magic 0x%08x (expected sam3)", magic);
+    if (version != 3) ORC_FAIL("unsupported version %d", version);
+    m->ftype = ftype;
+    m->wtype = ftype_to_wtype(ftype);
+    if (m->wtype < 0) ORC_FAIL("unsupported ftype %d", ftype);
+    /* SAM3 hparams: 39 int32 fields in the order of sam3_load_hparams. */
+    int32_t hpv[39];
+    {
+        int32_t v[10];
+        for (int i = 0; i < 8; i++) RD32(v[i]);
+        m->hp.img_size = v[0]; m->hp.patch = v[1]; m->hp.E = v[2]; m->hp.depth = v[3];
+        m->hp.heads = v[4];
+        m->hp.mlp = (int32_t)(v[2] * (v[5] / 1000.0f));
+        m->hp.window = v[6];
+        m->hp.n_global = v[7];
+        for (int i = 0; i < m->hp.n_global && i < 4; i++) RD32(m->hp.gidx[i]);
+        /* remaining 27 fields (text .. visual_only) are read and ignored */
+        for (int i = 0; i < 27; i++) RD32(hpv[i]);
+    }
+    m->t = (orc_tensor *)calloc((size_t)(n_tensors > 0 ? n_tensors : 1), sizeof(orc_tensor));
+    for (int ti = 0; ti < n_tensors; ti++) {
+        int32_t n_dims, name_len, dtype;
+        RD32(n_dims); RD32(name_len); RD32(dtype);
+        if (n_dims < 1 || n_dims > 4) ORC_FAIL("bad n_dims %d", n_dims);
+        orc_tensor *t = &m->t[m->n_tensors];
+        int64_t n_el = 1;
+        for (int i = 0; i < 4; i++) t->ne[i] = 1;
+        for (int i = 0; i < n_dims; i++) { int32_t d; RD32(d); t->ne[i] = d; n_el *= d; }
+        if (name_len <= 0 || name_len >= (int)sizeof t->name || off + (size_t)name_len > fsize) ORC_FAIL("bad name length");
+        memcpy(t->name, map + off, (size_t)name_len);
+        t->name[name_len] = 0;
+        off += (size_t)name_len;
+        off += (32 - off % 32) % 32;
+        const size_t bytes = orc_row_size(dtype, t->ne[0]) * (size_t)(n_el / t->ne[0]);
+        if (orc_type_size(dtype) == 0) ORC_FAIL("tensor %s: unsupported dtype %d", t->name, dtype);
+        if (off + bytes > fsize) ORC_FAIL("tensor %s: truncated data", t->name);
+        const uint8_t *src = map + off;
+        off += bytes;
+        if (strncmp(t->name, "vit.", 4) != 0) continue; /* encoder backbone only */
+        const int rt = registered_type(t->name, n_dims, t->ne[0], m->wtype);
+        t->type = rt;
+        const size_t out_bytes = orc_row_size(rt, t->ne[0]) * (size_t)(n_el / t->ne[0]);
+        t->data = malloc(out_bytes);
+        if (rt == dtype) {
+            memcpy(t->data, src, bytes);
+        } else if (rt == ORC_TYPE_F32) {
+            /* F16 → F32 or dequantize → F32 (sam3.cpp:3151-3172) */
+            const int64_t rows = n_el / t->ne[0];
+            const size_t rs = orc_row_size(dtype, t->ne[0]);
+            for (int64_t r = 0; r < rows; r++) {
+                orc_dequantize_row(dtype, src + r * rs, (float *)t->data + r * t->ne[0], t->ne[0]);
+            }
+        } else if (rt == ORC_TYPE_F16 && dtype == ORC_TYPE_F32) {
+            orc_fp32_to_fp16_row((const float *)src, (uint16_t *)t->data, n_el);
+        } else {
+            ORC_FAIL("tensor %s: unsupported conversion %d -> %d", t->name, dtype, rt);
+        }
+        m->n_tensors++;
+    }
+    munmap(map, fsize);
+    close(fd);
+    return m;
+fail:
+    if (map) munmap(map, fsize);
+    if (fd >= 0) close(fd);
+    orc_model_free(m);
+    return NULL;
+#undef RD32
+}
+
+void orc_model_free(orc_model *m) {
+    if (!m) return;
+    for (int i = 0; i < m->n_tensors; i++) free(m->t[i].data);
+    free(m->t);
+    free(m);
+}
+
+void orc_model_hparams(const orc_model *m, int32_t out[16]) {
+    memset(out, 0, 16 * sizeof(int32_t));
+    out[0] = m->hp.img_size; out[1] = m->hp.patch; out[2] = m->hp.E; out[3] = m->hp.depth;
+    out[4] = m->hp.heads; out[5] = m->hp.mlp; out[6] = m->hp.window; out[7] = m->hp.n_global;
+    for (int i = 0; i < 4; i++) out[8 + i] = m->hp.gidx[i];
+    out[12] = m->ftype;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Prefix: ggml_conv_2d_sk_p0 (im2col in the kernel's type, then mul_mat with
+ * the im2col matrix as src0 and the kernel as src1), permute, + tiled
+ * pos_embed (ggml_repeat), ggml_norm(1e-5)·w + b.  sam3.cpp:3806-3830. */
+int orc_vit_prefix(const orc_model *m, const float *chw, float *x, int nthreads) {
+    const orc_hp *hp = &m->hp;
+    const int P = hp->patch, G = hp->img_size / P, E = hp->E, T = G * G;
+    const int64_t Kp = (int64_t)P * P * 3;
+    const orc_tensor *pw = find(m, "vit.patch_embed.proj.weight");
+    const orc_tensor *pos = find(m, "vit.pos_embed");
+    const orc_tensor *lw = find(m, "vit.ln_pre.weight");
+    const orc_tensor *lb = find(m, "vit.ln_pre.bias");
+    if (!pw || !pos || !lw || !lb) { snprintf(g_err, sizeof g_err, "missing prefix tensors"); return -1; }
+    const int pg = (int)pos->ne[1];
+    if (nthreads <= 0) nthreads = omp_get_max_threads();
+    const int ptype = pw->type; /* F32 or F16 */
+    const size_t rs = orc_row_size(ptype, Kp);
+    char *cols = (char *)malloc(rs * (size_t)T);
+    const size_t plane = (size_t)hp->img_size * hp->img_size;
+#pragma omp parallel for num_threads(nthreads)
+    for (int t = 0; t < T; t++) {
+        const int py = t / G, px = t % G;
+        float tmp[3 * 64 * 64];
+        int64_t k = 0;
+        for (int c = 0; c < 3; c++)
+            for (int ky = 0; ky < P; ky++)
+                for (int kx = 0; kx < P; kx++)
+                    tmp[k++] = chw[c * plane + (size_t)(py * P + ky) * hp->img_size + px * P + kx];
+        orc_from_float(ptype, tmp, cols + (size_t)t * rs, Kp);
+    }
+    /* result[t][e] = vec_dot(im2col row t, kernel row e) */
+#pragma omp parallel for num_threads(nthreads)
+    for (int t = 0; t < T; t++) {
+        const int py = t / G, px = t % G;
+        const float *pr = (const float *)pos->data + ((size_t)(py % pg) * pg + (px % pg)) * E;
+        for (int e = 0; e < E; e++) {
+            const float conv = orc_vec_dot(ptype, Kp, cols + (size_t)t * rs, (const char *)pw->data + (size_t)e * rs);
+            x[(size_t)t * E + e] = conv + pr[e];
+        }
+    }
+    free(cols);
+    orc_layer_norm(x, x, T, E, 1e-5f, (const float *)lw->data, (const float *)lb->data, nthreads);
+    return 0;
+}
+
+/* One ViT block, in place on x [T][E] (natural token order).  Windowed blocks
+ * gather tokens in ggml_win_part order: window index py*nwx + px, position
+ * (iy*WS + ix) inside the window. */
+int orc_vit_block(const orc_model *m, int bi, float *x, int nthreads) {
+    const orc_hp *hp = &m->hp;
+    const int G = hp->img_size / hp->patch, E = hp->E, T = G * G, NH = hp->heads, HD = E / NH;
+    const int glob = is_global(hp, bi);
+    const int WS = glob ? G : hp->window;
+    if (G % WS != 0) { snprintf(g_err, sizeof g_err, "grid %d not a multiple of window %d", G, WS); return -1; }
+    const int nw1 = G / WS, NW = nw1 * nw1, N = WS * WS;
+    const orc_tensor *n1w = findf(m, "vit.blocks.%d.norm1.weight", bi), *n1b = findf(m, "vit.blocks.%d.norm1.bias", bi);
+    const orc_tensor *qw = findf(m, "vit.blocks.%d.attn.qkv.weight", bi), *qb = findf(m, "vit.blocks.%d.attn.qkv.bias", bi);
+    const orc_tensor *pjw = findf(m, "vit.blocks.%d.attn.proj.weight", bi), *pjb = findf(m, "vit.blocks.%d.attn.proj.bias", bi);
+    const orc_tensor *n2w = findf(m, "vit.blocks.%d.norm2.weight", bi), *n2b = findf(m, "vit.blocks.%d.norm2.bias", bi);
+    const orc_tensor *f1w = findf(m, "vit.blocks.%d.mlp.lin1.weight", bi), *f1b = findf(m, "vit.blocks.%d.mlp.lin1.bias", bi);
+    const orc_tensor *f2w = findf(m, "vit.blocks.%d.mlp.lin2.weight", bi), *f2b = findf(m, "vit.blocks.%d.mlp.lin2.bias", bi);
+    const orc_tensor *fc = findf(m, "vit.blocks.%d.attn.freqs_cis", bi);
+    if (!n1w || !n1b || !qw || !qb || !pjw || !pjb || !n2w || !n2b || !f1w || !f1b || !f2w || !f2b) {
+        snprintf(g_err, sizeof g_err, "block %d: missing tensors", bi);
+        return -1;
+    }
+    if (fc && fc->ne[2] != N) { snprintf(g_err, sizeof g_err, "block %d: freqs_cis has %lld positions, need %d", bi, (long long)fc->ne[2], N); return -1; }
+    const int MLP = (int)f1w->ne[1];
+    if (nthreads <= 0) nthreads = omp_get_max_threads();
+
+    float *h = (float *)malloc(sizeof(float) * (size_t)T * E);
+    float *hp_ = (float *)malloc(sizeof(float) * (size_t)T * E);
+    int *perm = (int *)malloc(sizeof(int) * (size_t)T); /* partition row → token */
+    for (int w = 0; w < NW; w++) {
+        const int wy = w / nw1, wx = w % nw1;
+        for (int p = 0; p < N; p++) {
+            const int iy = p / WS, ix = p % WS;
+            perm[w * N + p] = (wy * WS + iy) * G + wx * WS + ix;
+        }
+    }
+    /* attention branch */
+    orc_layer_norm(x, h, T, E, 1e-5f, (const float *)n1w->data, (const float *)n1b->data, nthreads);
+    for (int r = 0; r < T; r++) memcpy(hp_ + (size_t)r * E, h + (size_t)perm[r] * E, sizeof(float) * E);
+    float *qkv = (float *)malloc(sizeof(float) * (size_t)T * 3 * E);
+    orc_mul_mat(qw->type, qw->data, 3 * E, E, hp_, T, qkv, nthreads);
+    const float *qbias = (const float *)qb->data;
+    for (int64_t r = 0; r < T; r++)
+        for (int c = 0; c < 3 * E; c++) qkv[r * 3 * E + c] = qkv[r * 3 * E + c] + qbias[c];
+    /* split into Q, K [HD, N, NH*NW] contiguous, V read through strides */
+    float *Q = (float *)malloc(sizeof(float) * (size_t)T * E);
+    float *K = (float *)malloc(sizeof(float) * (size_t)T * E);
+    for (int w = 0; w < NW; w++)
+        for (int hh = 0; hh < NH; hh++)
+            for (int p = 0; p < N; p++) {
+                const float *src = qkv + ((size_t)(w * N + p)) * 3 * E;
+                float *dq = Q + (((size_t)w * NH + hh) * N + p) * HD;
+                float *dk = K + (((size_t)w * NH + hh) * N + p) * HD;
+                memcpy(dq, src + 0 * E + hh * HD, sizeof(float) * HD);
+                memcpy(dk, src + 1 * E + hh * HD, sizeof(float) * HD);
+            }
+    if (fc) {
+        orc_rope(Q, HD, N, (int64_t)NH * NW, (const float *)fc->data);
+        orc_rope(K, HD, N, (int64_t)NH * NW, (const float *)fc->data);
+    }
+    float *O = (float *)malloc(sizeof(float) * (size_t)T * E);
+    /* Q(b,h,i,d): b*NH*N*HD + h*N*HD + i*HD + d; V(b,h,j,d) in qkv rows */
+    orc_flash_attn_ext(Q, HD, (int64_t)N * HD, (int64_t)NH * N * HD,
+                       K, HD, (int64_t)N * HD, (int64_t)NH * N * HD,
+                       qkv + 2 * E, 3 * E, HD, (int64_t)N * 3 * E,
+                       HD, N, N, NH, NW, 1.0f / sqrtf((float)HD), O, nthreads);
+    /* O rows are in partition order, [E] = [NH][HD] per row */
+    float *proj = (float *)malloc(sizeof(float) * (size_t)T * E);
+    orc_mul_mat(pjw->type, pjw->data, E, E, O, T, proj, nthreads);
+    const float *pbias = (const float *)pjb->data;
+    for (int r = 0; r < T; r++) {
+        float *xr = x + (size_t)perm[r] * E;
+        const float *pr = proj + (size_t)r * E;
+        for (int c = 0; c < E; c++) xr[c] = xr[c] + (pr[c] + pbias[c]);
+    }
+    free(Q); free(K); free(O); free(proj); free(qkv);
+    /* MLP branch */
+    orc_layer_norm(x, h, T, E, 1e-5f, (const float *)n2w->data, (const float *)n2b->data, nthreads);
+    float *f1 = (float *)malloc(sizeof(float) * (size_t)T * MLP);
+    orc_mul_mat(f1w->type, f1w->data, MLP, E, h, T, f1, nthreads);
+    const float *b1 = (const float *)f1b->data;
+#pragma omp parallel for num_threads(nthreads)
+    for (int r = 0; r < T; r++) {
+        float *fr = f1 + (size_t)r * MLP;
+        for (int c = 0; c < MLP; c++) fr[c] = fr[c] + b1[c];
+        orc_gelu_erf(fr, MLP);
+    }
+    orc_mul_mat(f2w->type, f2w->data, E, MLP, f1, T, hp_, nthreads);
+    const float *b2 = (const float *)f2b->data;
+    for (int64_t r = 0; r < T; r++)
+        for (int c = 0; c < E; c++) x[r * E + c] = x[r * E + c] + (hp_[r * E + c] + b2[c]);
+    free(f1); free(h); free(hp_); free(perm);
+    return 0;
+}
+
+int orc_vit_encode(const orc_model *m, const float *chw, float *out, int nthreads) {
+    if (orc_vit_prefix(m, chw, out, nthreads) != 0) return -1;
+    for (int i = 0; i < m->hp.depth; i++) {
+        if (orc_vit_block(m, i, out, nthreads) != 0) return -1;
+    }
+    return 0;
+}

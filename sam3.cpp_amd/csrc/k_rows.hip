@@ -1,0 +1,248 @@
+// k_rows.hip — row kernels: LayerNorm fused with the conversion of its output
+// into the next GEMM's activation format, plain activation quantization, the
+// patch-embed im2col, and the f32→fp16 repack used by the stand-alone
+// flash-attention entry point.
+#include "s3e_internal.h"
+
+namespace s3e {
+namespace {
+
+__device__ __forceinline__ uint16_t f2h_bits(float v) { return half_bits(v); }
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Write 16 consecutive values (one lane's chunk, half of a 32-block) in the
+// activation format.  Lanes 2j and 2j+1 together hold one 32-element block.
+__device__ __forceinline__ void emit16(const float *v, const Act &o, int64_t row, int64_t col,
+                                       int lane) {
+    if (o.kind == A_F32) {
+        float4 *dst = (float4 *)((float *)o.x + row * o.ld + col);
+#pragma unroll
+        for (int j = 0; j < 4; j++) dst[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+        return;
+    }
+    if (o.kind == A_F16) {
+        uint32_t w[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) w[j] = (uint32_t)f2h_bits(v[2 * j]) | ((uint32_t)f2h_bits(v[2 * j + 1]) << 16);
+        uint4 *dst = (uint4 *)((_Float16 *)o.x + row * o.ld + col);
+        dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+        dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+        return;
+    }
+    // Q8_0 / Q8_1 as ggml's x86 quantize_row_q8_0 / q8_1: d = amax/127,
+    // id = 127/amax, q = round-half-even(v·id), s = fp16(d·Σq).
+    float amax = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; j++) amax = fmaxf(amax, fabsf(v[j]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    const float d = amax / 127.f;
+    const float id = (amax != 0.f) ? 127.f / amax : 0.f;
+    int sum = 0;
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int q = (int)__builtin_rintf(v[4 * j + i] * id);
+            sum += q;
+            packed |= ((uint32_t)(q & 0xff)) << (8 * i);
+        }
+        w[j] = packed;
+    }
+    *(uint4 *)((int8_t *)o.x + row * o.ld + col) = make_uint4(w[0], w[1], w[2], w[3]);
+    sum += __shfl_xor(sum, 1, 64);
+    if ((lane & 1) == 0) {
+        const int64_t blk = row * (o.ld / QK) + col / QK;
+        o.d[blk] = f2h_bits(d);
+        // s = fp16(fp32(d·Σq)): f2h_bits keeps the fp32 rounding of the product
+        if (o.kind == A_Q8_1) o.s[blk] = f2h_bits(d * (float)sum);
+    }
+}
+
+// One wave per row; lane L holds chunks L, L+64, ... of 16 elements.
+// NIT = ceil(K / 1024) iterations.
+template <int NIT>
+__global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ x, int64_t M, int64_t E,
+                                                   float eps, const float *__restrict__ w,
+                                                   const float *__restrict__ b, Act o,
+                                                   float *__restrict__ y32) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M) return;
+    const int nch = (int)(E / 16);
+    const float *xr = x + row * E;
+    float v[NIT][16];
+    // ggml_norm: mean and variance accumulated in double, each rounded to
+    // float once; centred values and squares in float.  With double sums the
+    // summation order no longer shows in the float results, so the output
+    // matches the CPU path bit for bit.
+    double s = 0.0;
+#pragma unroll
+    for (int it = 0; it < NIT; it++) {
+        const int ch = lane + 64 * it;
+#pragma unroll
+        for (int j = 0; j < 16; j++) v[it][j] = 0.f;
+        if (ch < nch) {
+            const float4 *src = (const float4 *)(xr + ch * 16);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float4 q = src[j];
+                v[it][4 * j] = q.x; v[it][4 * j + 1] = q.y; v[it][4 * j + 2] = q.z; v[it][4 * j + 3] = q.w;
+            }
+#pragma unroll
+            for (int j = 0; j < 16; j++) s += (double)v[it][j];
+        }
+    }
+    s = wave_sum_d(s);
+    const float mean = (float)(s / (double)E);
+    double s2 = 0.0;
+#pragma unroll
+    for (int it = 0; it < NIT; it++) {
+        const int ch = lane + 64 * it;
+        if (ch < nch) {
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const float c = __fsub_rn(v[it][j], mean);
+                v[it][j] = c;
+                s2 += (double)__fmul_rn(c, c);
+            }
+        }
+    }
+    s2 = wave_sum_d(s2);
+    const float var = (float)(s2 / (double)E);
+    const float scale = 1.0f / sqrtf(var + eps);
+#pragma unroll
+    for (int it = 0; it < NIT; it++) {
+        const int ch = lane + 64 * it;
+        if (ch >= nch) continue;
+        const int64_t col = (int64_t)ch * 16;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            float t = __fmul_rn(v[it][j], scale);
+            if (w) t = __fmul_rn(t, w[col + j]);
+            if (b) t = __fadd_rn(t, b[col + j]);
+            v[it][j] = t;
+        }
+        if (y32) {
+            float4 *dst = (float4 *)(y32 + row * E + col);
+#pragma unroll
+            for (int j = 0; j < 4; j++) dst[j] = make_float4(v[it][4 * j], v[it][4 * j + 1], v[it][4 * j + 2], v[it][4 * j + 3]);
+        } else {
+            emit16(v[it], o, row, col, lane);
+        }
+    }
+}
+
+// Plain conversion of f32 rows into an activation format (ggml from_float).
+__global__ __launch_bounds__(256) void k_rows_quant(const float *__restrict__ x, int64_t M, int64_t K, Act o) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.y * 4 + (threadIdx.x >> 6);
+    const int64_t ch = (int64_t)blockIdx.x * 64 + lane;  // chunk of 16
+    if (row >= M) return;
+    const int64_t nch = K / 16;
+    // chunks come in pairs (2j, 2j+1) inside one wave: nch is even (K % 32 == 0)
+    if (ch >= nch) return;
+    float v[16];
+    const float4 *src = (const float4 *)(x + row * K + ch * 16);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float4 q = src[j];
+        v[4 * j] = q.x; v[4 * j + 1] = q.y; v[4 * j + 2] = q.z; v[4 * j + 3] = q.w;
+    }
+    emit16(v, o, row, ch * 16, lane);
+}
+
+// im2col for ggml_conv_2d_sk_p0 with a P×P kernel and stride P on a CHW image:
+// row t = py*G + px, column k = (c*P + ky)*P + kx, zero for k >= 3·P².
+__global__ void k_im2col(const float *__restrict__ chw, int img, int P, int64_t ldk, int kind,
+                         void *out) {
+    const int G = img / P;
+    const int64_t T = (int64_t)G * G;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= T * ldk) return;
+    const int64_t t = idx / ldk;
+    const int k = (int)(idx % ldk);
+    float val = 0.f;
+    if (k < 3 * P * P) {
+        const int c = k / (P * P), r = k % (P * P), ky = r / P, kx = r % P;
+        const int py = (int)(t / G), px = (int)(t % G);
+        val = chw[(int64_t)c * img * img + (int64_t)(py * P + ky) * img + px * P + kx];
+    }
+    if (kind == A_F16) ((_Float16 *)out)[idx] = to_half(val);
+    else ((float *)out)[idx] = val;
+}
+
+// f32 strided Q/K/V → fp16 [BH][N][64] for Q and K, [BH][64][ldt] for V.
+// With lo != null the value is stored as the pair hi = fp16(v),
+// lo = fp16(v − hi) for split-precision attention.
+__global__ void k_attn_prep(const float *__restrict__ src, int64_t s1, int64_t s2, int64_t s3,
+                            int64_t N, int64_t nh, int64_t B, _Float16 *__restrict__ dst,
+                            _Float16 *__restrict__ lo, int64_t ldt, int transpose) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t total = B * nh * N * 64;
+    if (idx >= total) return;
+    const int64_t d = idx % 64;
+    const int64_t i = (idx / 64) % N;
+    const int64_t h = (idx / (64 * N)) % nh;
+    const int64_t b = idx / (64 * N * nh);
+    const float v = src[b * s3 + h * s2 + i * s1 + d];
+    const int64_t bh = b * nh + h;
+    const int64_t o = transpose ? (bh * 64 + d) * ldt + i : (bh * N + i) * 64 + d;
+    const _Float16 hv = to_half(v);
+    dst[o] = hv;
+    if (lo) lo[o] = (_Float16)(v - (float)hv);
+}
+
+}  // namespace
+
+hipError_t launch_layernorm(const float *x, int64_t M, int64_t E, float eps, const float *w,
+                            const float *b, const Act &out, float *y_f32, hipStream_t st) {
+    if (E % 32 != 0 || E > 4096) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((M + 3) / 4));
+    if (E <= 1024) hipLaunchKernelGGL(k_layernorm<1>, grid, dim3(256), 0, st, x, M, E, eps, w, b, out, y_f32);
+    else if (E <= 2048) hipLaunchKernelGGL(k_layernorm<2>, grid, dim3(256), 0, st, x, M, E, eps, w, b, out, y_f32);
+    else hipLaunchKernelGGL(k_layernorm<4>, grid, dim3(256), 0, st, x, M, E, eps, w, b, out, y_f32);
+    return hipGetLastError();
+}
+
+hipError_t launch_rows_quant(AKind kind, const float *x, int64_t M, int64_t K, const Act &out,
+                             hipStream_t st) {
+    (void)kind;
+    if (K % 32 != 0) return hipErrorInvalidValue;
+    const int64_t nch = K / 16;
+    const dim3 grid((unsigned)((nch + 63) / 64), (unsigned)((M + 3) / 4));
+    hipLaunchKernelGGL(k_rows_quant, grid, dim3(256), 0, st, x, M, K, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_im2col(const float *chw, int img, int P, int64_t ldk, AKind kind, void *out,
+                         hipStream_t st) {
+    const int G = img / P;
+    const int64_t total = (int64_t)G * G * ldk;
+    hipLaunchKernelGGL(k_im2col, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, chw, img, P,
+                       ldk, (int)kind, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_prep(const float *q, const int64_t q_nb[4], const float *k,
+                            const int64_t k_nb[4], const float *v, const int64_t v_nb[4],
+                            int64_t Nq, int64_t Nkv, int64_t nh, int64_t B, _Float16 *q16,
+                            _Float16 *k16, _Float16 *vt16, _Float16 *q_lo, _Float16 *k_lo,
+                            _Float16 *vt_lo, int64_t ldv, hipStream_t st) {
+    const int64_t tq = B * nh * Nq * 64, tk = B * nh * Nkv * 64;
+    hipLaunchKernelGGL(k_attn_prep, dim3((unsigned)((tq + 255) / 256)), dim3(256), 0, st, q, q_nb[1],
+                       q_nb[2], q_nb[3], Nq, nh, B, q16, q_lo, (int64_t)0, 0);
+    hipLaunchKernelGGL(k_attn_prep, dim3((unsigned)((tk + 255) / 256)), dim3(256), 0, st, k, k_nb[1],
+                       k_nb[2], k_nb[3], Nkv, nh, B, k16, k_lo, (int64_t)0, 0);
+    hipLaunchKernelGGL(k_attn_prep, dim3((unsigned)((tk + 255) / 256)), dim3(256), 0, st, v, v_nb[1],
+                       v_nb[2], v_nb[3], Nkv, nh, B, vt16, vt_lo, ldv, 1);
+    return hipGetLastError();
+}
+
+}  // namespace s3e

@@ -1,0 +1,146 @@
+// s3e_internal.h — shared declarations of the engine's HIP kernels and host
+// runtime.  Not part of the public ABI (include/s3e.h is).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "../../include/s3e.h"
+
+namespace s3e {
+
+// ggml block size of the quantized types (QK4_0 = QK4_1 = QK8_0 = QK8_1 = 32).
+constexpr int QK = 32;
+
+// Weight kinds as the GEMM kernels see them.
+enum WKind : int { WK_Q4_0 = 0, WK_Q4_1 = 1, WK_Q8_0 = 2, WK_F16 = 3, WK_F32 = 4 };
+
+// Activation formats (what a producer writes for the next GEMM to read).
+//   A_Q8_0 : int8 qs[M][ld] + fp16 d[M][ld/32]          (vec_dot type of Q4_0/Q8_0)
+//   A_Q8_1 : as A_Q8_0 + fp16 s[M][ld/32] = fp16(d·Σq)   (vec_dot type of Q4_1)
+//   A_F16  : fp16 [M][ld]                                 (vec_dot type of F16)
+//   A_F32  : f32  [M][ld]                                 (vec_dot type of F32)
+enum AKind : int { A_Q8_0 = 0, A_Q8_1 = 1, A_F16 = 2, A_F32 = 3 };
+
+inline AKind act_kind_for(WKind w) {
+    switch (w) {
+        case WK_Q4_0: case WK_Q8_0: return A_Q8_0;
+        case WK_Q4_1: return A_Q8_1;
+        case WK_F16: return A_F16;
+        default: return A_F32;
+    }
+}
+
+// A device activation buffer in one of the formats above.
+struct Act {
+    AKind kind = A_F32;
+    void *x = nullptr;      // qs (int8), fp16 or f32 values
+    uint16_t *d = nullptr;  // fp16 block scales (Q8 kinds)
+    uint16_t *s = nullptr;  // fp16 block sums (Q8_1)
+    int64_t ld = 0;         // elements per row (multiple of 32)
+};
+
+// A weight matrix repacked for the GEMM kernels.  N rows of K, stored as
+// column-blocks of the output: row n of the ggml matrix is "column" n here.
+//   Q4_0/Q4_1: qs [Np][Kbp][16] nibble bytes exactly as ggml stores them
+//              (low nibble = element j, high nibble = element j+16),
+//              d [Np][Kbp] fp16, m [Np][Kbp] fp16 (Q4_1).
+//   Q8_0     : qs [Np][Kp] int8, d [Np][Kbp] fp16.
+//   F16/F32  : values [Np][Kp].
+// Kp pads K to the kernel's stage width, Np pads N to the tile width; the
+// padding is zero and contributes nothing.
+struct Weight {
+    WKind kind = WK_F32;
+    int ggml_type = 0;
+    int64_t K = 0, N = 0, Kp = 0, Np = 0, Kbp = 0;
+    void *q = nullptr;
+    uint16_t *d = nullptr;
+    uint16_t *m = nullptr;
+    size_t bytes = 0;
+};
+
+// GEMM epilogues.
+enum Epi : int {
+    EPI_F32 = 0,     // y = acc + bias
+    EPI_RESID = 1,   // y += acc + bias                    (residual add)
+    EPI_POS = 2,     // y = acc + pos[tile(token)]          (patch embed + tiled pos_embed)
+    EPI_GELU = 3,    // act = quant(gelu_erf(acc + bias))   (fc1 → fc2)
+    EPI_QKV = 4,     // split Q/K/V, RoPE, fp16, window layout
+};
+
+struct EpiArgs {
+    const float *bias = nullptr;
+    float *y = nullptr;          // EPI_F32 / EPI_RESID / EPI_POS
+    int64_t ldy = 0;
+    Act out;                     // EPI_GELU
+    // EPI_POS
+    const float *pos = nullptr;  // [pg][pg][E]
+    int pos_grid = 0;
+    // geometry shared by EPI_POS and EPI_QKV
+    int grid = 0;                // tokens per side
+    int window = 0;              // window side (== grid for global attention)
+    // EPI_QKV
+    int E = 0, HD = 0, NH = 0;
+    const float *freqs = nullptr;  // [Nw][HD/2][2] or nullptr (no RoPE)
+    _Float16 *q = nullptr, *k = nullptr, *vt = nullptr;
+    // low halves of the fp16 pairs (x = hi + lo) when attention runs split
+    _Float16 *q_lo = nullptr, *k_lo = nullptr, *vt_lo = nullptr;
+    int vt_ld = 0;                 // row stride of Vᵀ in keys (multiple of 8)
+};
+
+// Attention I/O.
+struct AttnArgs {
+    const _Float16 *q = nullptr;   // [BH][Nq][64]
+    const _Float16 *k = nullptr;   // [BH][Nkv][64]
+    const _Float16 *vt = nullptr;  // [BH][64][Nkv]
+    // low halves (x = hi + lo) for split-precision attention, else null
+    const _Float16 *q_lo = nullptr, *k_lo = nullptr, *vt_lo = nullptr;
+    int Nq = 0, Nkv = 0, NH = 0, BH = 0;
+    float scale = 0.f;
+    // output row of query i of batch b: token(b, i) when grid > 0, else b*Nq + i
+    int grid = 0, window = 0;
+    Act out;                       // A_Q8_0 / A_Q8_1 / A_F16 / A_F32, row = token, col = h*64 + d
+};
+
+// ---- kernel launchers (k_*.hip) ----
+hipError_t launch_gemm(const Weight &w, const Act &a, int64_t M, Epi epi, const EpiArgs &ea,
+                       hipStream_t st);
+hipError_t launch_rows_quant(AKind kind, const float *x, int64_t M, int64_t K, const Act &out,
+                             hipStream_t st);
+hipError_t launch_layernorm(const float *x, int64_t M, int64_t E, float eps, const float *w,
+                            const float *b, const Act &out, float *y_f32, hipStream_t st);
+hipError_t launch_attn(const AttnArgs &a, hipStream_t st);
+hipError_t launch_attn_prep(const float *q, const int64_t q_nb[4], const float *k,
+                            const int64_t k_nb[4], const float *v, const int64_t v_nb[4],
+                            int64_t Nq, int64_t Nkv, int64_t nh, int64_t B, _Float16 *q16,
+                            _Float16 *k16, _Float16 *vt16, _Float16 *q_lo, _Float16 *k_lo,
+                            _Float16 *vt_lo, int64_t ldv, hipStream_t st);
+hipError_t launch_im2col(const float *chw, int img, int P, int64_t ldk, AKind kind, void *out,
+                         hipStream_t st);
+
+// fp32 → fp16 of a value computed in fp32.  The empty asm statement (it emits
+// no instruction) pins the fp32 value in a VGPR: without it LLVM folds
+// fptrunc(fmul/fadd) into v_fma_mix*, rounding the exact result once instead
+// of first to fp32 and then to fp16 as ggml's CPU path does.
+__device__ __forceinline__ _Float16 to_half(float x) {
+    __asm__ volatile("" : "+v"(x));
+    return (_Float16)x;
+}
+__device__ __forceinline__ uint16_t half_bits(float x) { return __builtin_bit_cast(uint16_t, to_half(x)); }
+
+// Stage widths (elements of K per pipeline stage) by weight kind.
+inline int64_t stage_k(WKind w) {
+    switch (w) {
+        case WK_Q4_0: case WK_Q4_1: case WK_Q8_0: return 128;
+        case WK_F16: return 64;
+        default: return 32;
+    }
+}
+constexpr int GEMM_BN = 128;
+
+// ---- error state (s3e_runtime.cpp) ----
+void set_error(const char *fmt, ...);
+
+}  // namespace s3e

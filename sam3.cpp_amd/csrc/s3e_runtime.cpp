@@ -1,0 +1,932 @@
+// s3e_runtime.cpp — host runtime behind include/s3e.h: contexts, weight
+// upload and repacking, the operator entry points (mul_mat, flash attention,
+// activation conversion), the SAM 3 ViT model loader and the encoder
+// schedule.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdlib>
+#include <cstring>
+#include <cstdio>
+#include <fstream>
+#include <algorithm>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "s3e_host.h"
+#include "s3e_internal.h"
+
+namespace s3e {
+
+static thread_local std::string g_err;
+
+void set_error(const char *fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+}
+
+}  // namespace s3e
+
+using namespace s3e;
+
+#define HIP_TRY(expr)                                                                   \
+    do {                                                                                \
+        hipError_t _e = (expr);                                                         \
+        if (_e != hipSuccess) {                                                         \
+            set_error("%s: %s (%s:%d)", #expr, hipGetErrorString(_e), __FILE__, __LINE__); \
+            return S3E_ERR_HIP;                                                         \
+        }                                                                               \
+    } while (0)
+
+struct s3e_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+};
+
+struct s3e_weight {
+    s3e_ctx *ctx = nullptr;
+    Weight w;
+};
+
+namespace {
+
+int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+WKind wkind_of(int type) {
+    switch (type) {
+        case S3E_TYPE_Q4_0: return WK_Q4_0;
+        case S3E_TYPE_Q4_1: return WK_Q4_1;
+        case S3E_TYPE_Q8_0: return WK_Q8_0;
+        case S3E_TYPE_F16: return WK_F16;
+        default: return WK_F32;
+    }
+}
+
+void free_weight(Weight &w) {
+    if (w.q) (void)hipFree(w.q);
+    if (w.d) (void)hipFree(w.d);
+    if (w.m) (void)hipFree(w.m);
+    w.q = nullptr;
+    w.d = w.m = nullptr;
+}
+
+// Repack ggml bytes (N rows of K in `type`) into the GEMM layout and upload.
+int upload_weight(int device, int type, int64_t K, int64_t N, const uint8_t *src, size_t nbytes,
+                  Weight &w) {
+    (void)device;
+    if (type != S3E_TYPE_F32 && type != S3E_TYPE_F16 && type != S3E_TYPE_Q4_0 && type != S3E_TYPE_Q4_1 &&
+        type != S3E_TYPE_Q8_0) {
+        set_error("weight type %d is not supported", type);
+        return S3E_ERR_UNSUPPORTED;
+    }
+    if (K <= 0 || N <= 0 || K % ggml_blck(type) != 0) {
+        set_error("weight shape [%lld, %lld] invalid for type %d", (long long)K, (long long)N, type);
+        return S3E_ERR_INVALID;
+    }
+    const size_t rs = ggml_rowsize(type, K);
+    if (nbytes < rs * (size_t)N) {
+        set_error("weight data holds %zu bytes, need %zu", nbytes, rs * (size_t)N);
+        return S3E_ERR_INVALID;
+    }
+    w = Weight{};
+    w.kind = wkind_of(type);
+    w.ggml_type = type;
+    w.K = K;
+    w.N = N;
+    w.Kp = round_up(K, stage_k(w.kind));
+    w.Np = round_up(N, GEMM_BN);
+    w.Kbp = w.Kp / 32;
+    const int64_t Kb = K / 32;
+    std::vector<uint8_t> q;
+    std::vector<uint16_t> d, m;
+    switch (w.kind) {
+        case WK_Q4_0:
+        case WK_Q4_1: {
+            const int bs = (w.kind == WK_Q4_0) ? 18 : 20, qo = (w.kind == WK_Q4_0) ? 2 : 4;
+            q.assign((size_t)(w.Np * w.Kbp * 16), 0);
+            d.assign((size_t)(w.Np * w.Kbp), 0);
+            if (w.kind == WK_Q4_1) m.assign((size_t)(w.Np * w.Kbp), 0);
+            for (int64_t n = 0; n < N; n++)
+                for (int64_t b = 0; b < Kb; b++) {
+                    const uint8_t *blk = src + (size_t)n * rs + (size_t)b * bs;
+                    std::memcpy(&d[(size_t)(n * w.Kbp + b)], blk, 2);
+                    if (w.kind == WK_Q4_1) std::memcpy(&m[(size_t)(n * w.Kbp + b)], blk + 2, 2);
+                    std::memcpy(&q[(size_t)((n * w.Kbp + b) * 16)], blk + qo, 16);
+                }
+        } break;
+        case WK_Q8_0: {
+            q.assign((size_t)(w.Np * w.Kp), 0);
+            d.assign((size_t)(w.Np * w.Kbp), 0);
+            for (int64_t n = 0; n < N; n++)
+                for (int64_t b = 0; b < Kb; b++) {
+                    const uint8_t *blk = src + (size_t)n * rs + (size_t)b * 34;
+                    std::memcpy(&d[(size_t)(n * w.Kbp + b)], blk, 2);
+                    std::memcpy(&q[(size_t)(n * w.Kp + b * 32)], blk + 2, 32);
+                }
+        } break;
+        case WK_F16:
+        case WK_F32: {
+            const int es = (w.kind == WK_F16) ? 2 : 4;
+            q.assign((size_t)(w.Np * w.Kp * es), 0);
+            for (int64_t n = 0; n < N; n++) std::memcpy(&q[(size_t)(n * w.Kp * es)], src + (size_t)n * rs, (size_t)K * es);
+        } break;
+    }
+    hipError_t e = hipMalloc(&w.q, q.size());
+    if (e == hipSuccess) e = hipMemcpy(w.q, q.data(), q.size(), hipMemcpyHostToDevice);
+    if (e == hipSuccess && !d.empty()) {
+        e = hipMalloc(&w.d, d.size() * 2);
+        if (e == hipSuccess) e = hipMemcpy(w.d, d.data(), d.size() * 2, hipMemcpyHostToDevice);
+    }
+    if (e == hipSuccess && !m.empty()) {
+        e = hipMalloc(&w.m, m.size() * 2);
+        if (e == hipSuccess) e = hipMemcpy(w.m, m.data(), m.size() * 2, hipMemcpyHostToDevice);
+    }
+    if (e != hipSuccess) {
+        free_weight(w);
+        set_error("weight upload: %s", hipGetErrorString(e));
+        return S3E_ERR_HIP;
+    }
+    w.bytes = q.size() + d.size() * 2 + m.size() * 2;
+    return S3E_OK;
+}
+
+// Device activation buffer able to hold M rows of up to K elements in any format.
+struct ActBuf {
+    void *x = nullptr;
+    uint16_t *d = nullptr, *s = nullptr;
+    int64_t cap_rows = 0, cap_k = 0;
+    hipError_t alloc(int64_t M, int64_t K) {
+        cap_rows = M;
+        cap_k = K;
+        hipError_t e = hipMalloc(&x, (size_t)(M * K * 4));
+        if (e == hipSuccess) e = hipMalloc(&d, (size_t)(M * (K / 32) * 2));
+        if (e == hipSuccess) e = hipMalloc(&s, (size_t)(M * (K / 32) * 2));
+        return e;
+    }
+    void release() {
+        if (x) (void)hipFree(x);
+        if (d) (void)hipFree(d);
+        if (s) (void)hipFree(s);
+        x = nullptr;
+        d = s = nullptr;
+    }
+    Act as(AKind kind, int64_t ld) const {
+        Act a;
+        a.kind = kind;
+        a.x = x;
+        a.d = d;
+        a.s = s;
+        a.ld = ld;
+        return a;
+    }
+};
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+extern "C" const char *s3e_last_error(void) { return g_err.c_str(); }
+extern "C" int s3e_abi_version(void) { return S3E_ABI_VERSION; }
+
+extern "C" int s3e_ctx_create(int device, s3e_ctx **out) {
+    if (!out) { set_error("s3e_ctx_create: out is NULL"); return S3E_ERR_INVALID; }
+    *out = nullptr;
+    int n = 0;
+    HIP_TRY(hipGetDeviceCount(&n));
+    if (device < 0 || device >= n) {
+        set_error("s3e_ctx_create: device %d out of range (%d devices)", device, n);
+        return S3E_ERR_INVALID;
+    }
+    HIP_TRY(hipSetDevice(device));
+    auto *c = new s3e_ctx;
+    c->device = device;
+    hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete c;
+        set_error("hipStreamCreate: %s", hipGetErrorString(e));
+        return S3E_ERR_HIP;
+    }
+    *out = c;
+    return S3E_OK;
+}
+
+extern "C" void s3e_ctx_destroy(s3e_ctx *ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+extern "C" int s3e_ctx_sync(s3e_ctx *ctx) {
+    if (!ctx) { set_error("s3e_ctx_sync: NULL context"); return S3E_ERR_INVALID; }
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return S3E_OK;
+}
+
+extern "C" void *s3e_ctx_stream(s3e_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+extern "C" int s3e_malloc(s3e_ctx *ctx, size_t bytes, void **out) {
+    if (!ctx || !out) { set_error("s3e_malloc: NULL argument"); return S3E_ERR_INVALID; }
+    HIP_TRY(hipSetDevice(ctx->device));
+    if (hipMalloc(out, bytes) != hipSuccess) {
+        set_error("s3e_malloc: cannot allocate %zu bytes", bytes);
+        return S3E_ERR_NOMEM;
+    }
+    return S3E_OK;
+}
+
+extern "C" int s3e_free(s3e_ctx *ctx, void *ptr) {
+    if (!ctx) { set_error("s3e_free: NULL context"); return S3E_ERR_INVALID; }
+    if (ptr) HIP_TRY(hipFree(ptr));
+    return S3E_OK;
+}
+
+extern "C" int s3e_memcpy_h2d(s3e_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    if (!ctx) { set_error("s3e_memcpy_h2d: NULL context"); return S3E_ERR_INVALID; }
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return S3E_OK;
+}
+
+extern "C" int s3e_memcpy_d2h(s3e_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    if (!ctx) { set_error("s3e_memcpy_d2h: NULL context"); return S3E_ERR_INVALID; }
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return S3E_OK;
+}
+
+// ---- ggml_mul_mat ---------------------------------------------------------
+extern "C" int s3e_weight_upload(s3e_ctx *ctx, int type, int64_t ne0, int64_t ne1, const void *host_data,
+                                 size_t nbytes, s3e_weight **out) {
+    if (!ctx || !host_data || !out) { set_error("s3e_weight_upload: NULL argument"); return S3E_ERR_INVALID; }
+    *out = nullptr;
+    HIP_TRY(hipSetDevice(ctx->device));
+    auto *w = new s3e_weight;
+    w->ctx = ctx;
+    const int rc = upload_weight(ctx->device, type, ne0, ne1, (const uint8_t *)host_data, nbytes, w->w);
+    if (rc != S3E_OK) {
+        delete w;
+        return rc;
+    }
+    *out = w;
+    return S3E_OK;
+}
+
+extern "C" void s3e_weight_free(s3e_weight *w) {
+    if (!w) return;
+    free_weight(w->w);
+    delete w;
+}
+
+extern "C" int s3e_weight_info(const s3e_weight *w, int64_t out[4]) {
+    if (!w || !out) { set_error("s3e_weight_info: NULL argument"); return S3E_ERR_INVALID; }
+    out[0] = w->w.ggml_type;
+    out[1] = w->w.K;
+    out[2] = w->w.N;
+    out[3] = (int64_t)w->w.bytes;
+    return S3E_OK;
+}
+
+extern "C" int s3e_quantize_rows(s3e_ctx *ctx, int type, const float *X, int64_t M, int64_t K, void *qs,
+                                 uint16_t *d, uint16_t *s) {
+    if (!ctx || !X || !qs) { set_error("s3e_quantize_rows: NULL argument"); return S3E_ERR_INVALID; }
+    if (K % 32 != 0 || M < 0) { set_error("s3e_quantize_rows: K=%lld must be a multiple of 32", (long long)K); return S3E_ERR_INVALID; }
+    Act a;
+    a.x = qs;
+    a.d = d;
+    a.s = s;
+    a.ld = K;
+    if (type == S3E_TYPE_Q8_0) a.kind = A_Q8_0;
+    else if (type == S3E_TYPE_Q8_1) a.kind = A_Q8_1;
+    else if (type == S3E_TYPE_F16) a.kind = A_F16;
+    else { set_error("s3e_quantize_rows: type %d is not a vec_dot type", type); return S3E_ERR_UNSUPPORTED; }
+    if ((a.kind != A_F16 && !d) || (a.kind == A_Q8_1 && !s)) { set_error("s3e_quantize_rows: missing scale buffer"); return S3E_ERR_INVALID; }
+    HIP_TRY(hipSetDevice(ctx->device));
+    HIP_TRY(launch_rows_quant(a.kind, X, M, K, a, ctx->stream));
+    return S3E_OK;
+}
+
+extern "C" int s3e_mul_mat(s3e_ctx *ctx, const s3e_weight *w, const float *X, int64_t M, const float *bias,
+                           float *Y) {
+    if (!ctx || !w || !X || !Y) { set_error("s3e_mul_mat: NULL argument"); return S3E_ERR_INVALID; }
+    if (M < 0) { set_error("s3e_mul_mat: negative M"); return S3E_ERR_INVALID; }
+    const Weight &W = w->w;
+    if (W.K % 32 != 0) {
+        set_error("s3e_mul_mat: K=%lld is not a multiple of 32", (long long)W.K);
+        return S3E_ERR_UNSUPPORTED;
+    }
+    if (M == 0) return S3E_OK;
+    HIP_TRY(hipSetDevice(ctx->device));
+    const AKind ak = act_kind_for(W.kind);
+    EpiArgs ea;
+    ea.bias = bias;
+    ea.y = Y;
+    ea.ldy = W.N;
+    if (ak == A_F32) {
+        Act a;
+        a.kind = A_F32;
+        a.x = (void *)X;
+        a.ld = W.K;
+        HIP_TRY(launch_gemm(W, a, M, EPI_F32, ea, ctx->stream));
+        return S3E_OK;
+    }
+    ActBuf buf;
+    HIP_TRY(buf.alloc(M, W.K));
+    const Act a = buf.as(ak, W.K);
+    hipError_t e = launch_rows_quant(ak, X, M, W.K, a, ctx->stream);
+    if (e == hipSuccess) e = launch_gemm(W, a, M, EPI_F32, ea, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    buf.release();
+    if (e != hipSuccess) { set_error("s3e_mul_mat: %s", hipGetErrorString(e)); return S3E_ERR_HIP; }
+    return S3E_OK;
+}
+
+extern "C" int s3e_layer_norm(s3e_ctx *ctx, const float *x, int64_t rows, int64_t n, float eps, const float *w,
+                              const float *b, float *y) {
+    if (!ctx || !x || !y) { set_error("s3e_layer_norm: NULL argument"); return S3E_ERR_INVALID; }
+    if (rows < 0 || n <= 0 || n % 32 != 0 || n > 4096) {
+        set_error("s3e_layer_norm: row length %lld must be a positive multiple of 32 up to 4096", (long long)n);
+        return S3E_ERR_UNSUPPORTED;
+    }
+    if (rows == 0) return S3E_OK;
+    HIP_TRY(hipSetDevice(ctx->device));
+    Act none;
+    HIP_TRY(launch_layernorm(x, rows, n, eps, w, b, none, y, ctx->stream));
+    return S3E_OK;
+}
+
+// ---- ggml_flash_attn_ext --------------------------------------------------
+extern "C" int s3e_flash_attn_ext(s3e_ctx *ctx, const float *q, const int64_t q_nb[4], const float *k,
+                                  const int64_t k_nb[4], const float *v, const int64_t v_nb[4], int64_t D,
+                                  int64_t Nq, int64_t Nkv, int64_t nh, int64_t B, float scale, int prec,
+                                  float *o) {
+    if (!ctx || !q || !k || !v || !o || !q_nb || !k_nb || !v_nb) {
+        set_error("s3e_flash_attn_ext: NULL argument");
+        return S3E_ERR_INVALID;
+    }
+    if (D != 64) { set_error("s3e_flash_attn_ext: head dim %lld not supported (64 only)", (long long)D); return S3E_ERR_UNSUPPORTED; }
+    if (Nq <= 0 || Nkv <= 0 || nh <= 0 || B <= 0) { set_error("s3e_flash_attn_ext: empty shape"); return S3E_ERR_INVALID; }
+    if (prec != S3E_PREC_DEFAULT && prec != S3E_PREC_F32) { set_error("s3e_flash_attn_ext: unknown precision %d", prec); return S3E_ERR_INVALID; }
+    HIP_TRY(hipSetDevice(ctx->device));
+    const int64_t ldv = round_up(Nkv, 8);
+    const int np = (prec == S3E_PREC_F32) ? 2 : 1;  // hi (+ lo) planes
+    const size_t qn = (size_t)(B * nh * Nq * 64), kn = (size_t)(B * nh * Nkv * 64), vn = (size_t)(B * nh * ldv * 64);
+    _Float16 *q16 = nullptr, *k16 = nullptr, *vt16 = nullptr;
+    hipError_t e = hipMalloc(&q16, qn * 2 * np);
+    if (e == hipSuccess) e = hipMalloc(&k16, kn * 2 * np);
+    if (e == hipSuccess) e = hipMalloc(&vt16, vn * 2 * np);
+    if (e == hipSuccess) e = hipMemsetAsync(vt16, 0, vn * 2 * np, ctx->stream);
+    AttnArgs a;
+    a.q = q16;
+    a.k = k16;
+    a.vt = vt16;
+    if (np == 2) {
+        a.q_lo = q16 + qn;
+        a.k_lo = k16 + kn;
+        a.vt_lo = vt16 + vn;
+    }
+    if (e == hipSuccess)
+        e = launch_attn_prep(q, q_nb, k, k_nb, v, v_nb, Nq, Nkv, nh, B, q16, k16, vt16, (_Float16 *)a.q_lo,
+                             (_Float16 *)a.k_lo, (_Float16 *)a.vt_lo, ldv, ctx->stream);
+    if (e == hipSuccess) {
+        a.Nq = (int)Nq;
+        a.Nkv = (int)Nkv;
+        a.NH = (int)nh;
+        a.BH = (int)(B * nh);
+        a.scale = scale;
+        a.grid = 0;
+        a.out.kind = A_F32;
+        a.out.x = o;
+        a.out.ld = nh * 64;
+        e = launch_attn(a, ctx->stream);
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (q16) (void)hipFree(q16);
+    if (k16) (void)hipFree(k16);
+    if (vt16) (void)hipFree(vt16);
+    if (e != hipSuccess) { set_error("s3e_flash_attn_ext: %s", hipGetErrorString(e)); return S3E_ERR_HIP; }
+    return S3E_OK;
+}
+
+// ---- SAM 3 ViT model -------------------------------------------------------
+namespace {
+
+struct Block {
+    float *n1w = nullptr, *n1b = nullptr, *n2w = nullptr, *n2b = nullptr;
+    float *qkv_b = nullptr, *proj_b = nullptr, *fc1_b = nullptr, *fc2_b = nullptr;
+    float *freqs = nullptr;  // [Nw][HD/2][2] or null
+    int64_t freqs_n = 0;
+    Weight qkv, proj, fc1, fc2;
+    bool global = false;
+};
+
+}  // namespace
+
+struct s3e_model {
+    s3e_ctx *ctx = nullptr;
+    int ftype = 0, wtype = 0;
+    int32_t img = 0, patch = 0, E = 0, depth = 0, heads = 0, mlp = 0, window = 0, n_global = 0, gidx[4] = {0, 0, 0, 0};
+    int grid = 0, pos_grid = 0;
+    Weight patch_w;  // K = 3·P², N = E
+    float *pos = nullptr, *ln_pre_w = nullptr, *ln_pre_b = nullptr;
+    std::vector<Block> blocks;
+    std::vector<void *> owned;  // device f32 arrays
+};
+
+namespace {
+
+int ftype_wtype(int ftype) {
+    switch (ftype) {
+        case 0: return 0;
+        case 1: return 1;
+        case 2: return 2;
+        case 3: return 3;
+        case 8: return 8;
+        default: return -1;
+    }
+}
+
+struct RawTensor {
+    int type = 0;
+    int n_dims = 0;
+    int64_t ne[4] = {1, 1, 1, 1};
+    std::vector<uint8_t> data;
+};
+
+// Convert file bytes to the type sam3.cpp registers for the tensor
+// (sam3.cpp:2461-2557 registration, :3145-3178 conversion).
+bool coerce(RawTensor &t, int want) {
+    if (t.type == want) return true;
+    int64_t n = t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3];
+    if (want == 0) {
+        std::vector<uint8_t> out((size_t)n * 4);
+        const size_t rs = ggml_rowsize(t.type, t.ne[0]);
+        for (int64_t r = 0; r < n / t.ne[0]; r++)
+            dequantize_row(t.type, t.data.data() + r * rs, (float *)out.data() + r * t.ne[0], t.ne[0]);
+        t.data.swap(out);
+        t.type = 0;
+        return true;
+    }
+    if (want == 1 && t.type == 0) {
+        std::vector<uint8_t> out((size_t)n * 2);
+        const float *src = (const float *)t.data.data();
+        for (int64_t i = 0; i < n; i++) {
+            const uint16_t h = host_f2h(src[i]);
+            std::memcpy(out.data() + 2 * i, &h, 2);
+        }
+        t.data.swap(out);
+        t.type = 1;
+        return true;
+    }
+    return false;
+}
+
+int upload_f32(s3e_model *m, const RawTensor &t, int64_t expect, float **dst) {
+    int64_t n = t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3];
+    if (n != expect) { set_error("tensor has %lld elements, expected %lld", (long long)n, (long long)expect); return S3E_ERR_IO; }
+    void *p = nullptr;
+    HIP_TRY(hipMalloc(&p, (size_t)n * 4));
+    m->owned.push_back(p);
+    HIP_TRY(hipMemcpy(p, t.data.data(), (size_t)n * 4, hipMemcpyHostToDevice));
+    *dst = (float *)p;
+    return S3E_OK;
+}
+
+}  // namespace
+
+extern "C" void s3e_model_free(s3e_model *m) {
+    if (!m) return;
+    free_weight(m->patch_w);
+    for (auto &b : m->blocks) {
+        free_weight(b.qkv);
+        free_weight(b.proj);
+        free_weight(b.fc1);
+        free_weight(b.fc2);
+    }
+    for (void *p : m->owned) (void)hipFree(p);
+    delete m;
+}
+
+extern "C" int s3e_model_load(s3e_ctx *ctx, const char *path, s3e_model **out) {
+    if (!ctx || !path || !out) { set_error("s3e_model_load: NULL argument"); return S3E_ERR_INVALID; }
+    *out = nullptr;
+    HIP_TRY(hipSetDevice(ctx->device));
+    std::ifstream fin(path, std::ios::binary);
+    if (!fin) { set_error("s3e_model_load: cannot open '%s'", path); return S3E_ERR_IO; }
+    auto rd = [&](void *dst, size_t n) { fin.read((char *)dst, (std::streamsize)n); return (bool)fin; };
+    uint32_t magic = 0;
+    int32_t version = 0, ftype = 0, n_tensors = 0;
+    if (!rd(&magic, 4) || !rd(&version, 4) || !rd(&ftype, 4) || !rd(&n_tensors, 4)) {
+        set_error("s3e_model_load: truncated header");
+        return S3E_ERR_IO;
+    }
+    if (magic != 0x73616D33u) { set_error("s3e_model_load: unknown magic 0x%08x (expected sam3)", magic); return S3E_ERR_IO; }
+    if (version != 3) { set_error("s3e_model_load: unsupported SAM3 version %d", version); return S3E_ERR_IO; }
+    const int wtype = ftype_wtype(ftype);
+    if (wtype < 0) { set_error("s3e_model_load: unsupported ftype %d", ftype); return S3E_ERR_UNSUPPORTED; }
+    std::unique_ptr<s3e_model, void (*)(s3e_model *)> m(new s3e_model, s3e_model_free);
+    m->ctx = ctx;
+    m->ftype = ftype;
+    m->wtype = wtype;
+    int32_t hv[8];
+    if (!rd(hv, 32)) { set_error("s3e_model_load: truncated hparams"); return S3E_ERR_IO; }
+    m->img = hv[0]; m->patch = hv[1]; m->E = hv[2]; m->depth = hv[3]; m->heads = hv[4];
+    m->mlp = (int32_t)(hv[2] * (hv[5] / 1000.0f));
+    m->window = hv[6];
+    m->n_global = hv[7];
+    for (int i = 0; i < m->n_global && i < 4; i++)
+        if (!rd(&m->gidx[i], 4)) { set_error("s3e_model_load: truncated hparams"); return S3E_ERR_IO; }
+    int32_t rest[27];
+    if (!rd(rest, sizeof rest)) { set_error("s3e_model_load: truncated hparams"); return S3E_ERR_IO; }
+    if (m->patch <= 0 || m->img % m->patch != 0 || m->E <= 0 || m->heads <= 0 || m->E % m->heads != 0 ||
+        m->depth <= 0 || m->depth > 256 || m->window <= 0) {
+        set_error("s3e_model_load: inconsistent hparams");
+        return S3E_ERR_IO;
+    }
+    m->grid = m->img / m->patch;
+    if (m->E / m->heads != 64) { set_error("s3e_model_load: head dim %d not supported (64 only)", m->E / m->heads); return S3E_ERR_UNSUPPORTED; }
+    if (m->E % 128 != 0) { set_error("s3e_model_load: embed dim %d must be a multiple of 128", m->E); return S3E_ERR_UNSUPPORTED; }
+    if (m->grid % m->window != 0) { set_error("s3e_model_load: grid %d is not a multiple of the window %d", m->grid, m->window); return S3E_ERR_UNSUPPORTED; }
+    m->blocks.resize((size_t)m->depth);
+    for (int i = 0; i < m->depth; i++) {
+        for (int j = 0; j < m->n_global && j < 4; j++)
+            if (m->gidx[j] == i) m->blocks[(size_t)i].global = true;
+    }
+    const int64_t E = m->E, MLP = m->mlp;
+    int seen = 0;
+    const int expected = 4 + 13 * m->depth;
+    for (int ti = 0; ti < n_tensors; ti++) {
+        int32_t hdr[3];
+        if (!rd(hdr, 12)) { set_error("s3e_model_load: truncated tensor header %d", ti); return S3E_ERR_IO; }
+        RawTensor t;
+        t.n_dims = hdr[0];
+        const int32_t name_len = hdr[1];
+        t.type = hdr[2];
+        if (t.n_dims < 1 || t.n_dims > 4 || name_len <= 0 || name_len > 256 || ggml_tsize(t.type) == 0) {
+            set_error("s3e_model_load: malformed tensor record %d", ti);
+            return S3E_ERR_IO;
+        }
+        for (int i = 0; i < t.n_dims; i++) {
+            int32_t dd;
+            if (!rd(&dd, 4) || dd <= 0) { set_error("s3e_model_load: bad dims in record %d", ti); return S3E_ERR_IO; }
+            t.ne[i] = dd;
+        }
+        std::string name((size_t)name_len, '\0');
+        if (!rd(&name[0], (size_t)name_len)) { set_error("s3e_model_load: truncated name"); return S3E_ERR_IO; }
+        const std::streamoff pos = fin.tellg();
+        fin.seekg((32 - pos % 32) % 32, std::ios::cur);
+        const int64_t n_el = t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3];
+        if (t.ne[0] % ggml_blck(t.type) != 0) { set_error("s3e_model_load: '%s' ne0 not a block multiple", name.c_str()); return S3E_ERR_IO; }
+        const size_t bytes = ggml_rowsize(t.type, t.ne[0]) * (size_t)(n_el / t.ne[0]);
+        if (name.compare(0, 4, "vit.") != 0) {  // not part of the backbone: skip
+            fin.seekg((std::streamoff)bytes, std::ios::cur);
+            if (!fin) { set_error("s3e_model_load: truncated data of '%s'", name.c_str()); return S3E_ERR_IO; }
+            continue;
+        }
+        t.data.resize(bytes);
+        if (!rd(t.data.data(), bytes)) { set_error("s3e_model_load: truncated data of '%s'", name.c_str()); return S3E_ERR_IO; }
+        // registered type (T1f/T3f/T4f → F32; T2/T4 → weight type iff ne0 % block == 0)
+        int want = 0;
+        const bool f32_reg = t.n_dims < 2 || name.find("pos_embed") != std::string::npos || name.find("freqs_cis") != std::string::npos;
+        if (!f32_reg) want = (t.ne[0] % ggml_blck(wtype) == 0) ? wtype : 0;
+        if (!coerce(t, want)) { set_error("s3e_model_load: cannot convert '%s' from type %d to %d", name.c_str(), t.type, want); return S3E_ERR_IO; }
+        int rc = S3E_OK;
+        if (name == "vit.patch_embed.proj.weight") {
+            if (t.ne[0] != m->patch || t.ne[1] != m->patch || t.ne[2] != 3 || t.ne[3] != E) { set_error("patch_embed shape mismatch"); return S3E_ERR_IO; }
+            const int64_t K = 3LL * m->patch * m->patch;
+            // pad K to a multiple of 32 with zero columns (the im2col rows are padded the same way)
+            const int64_t Kp = round_up(K, 32);
+            const int es = (t.type == 1) ? 2 : 4;
+            std::vector<uint8_t> padded((size_t)(E * Kp * es), 0);
+            for (int64_t n = 0; n < E; n++) std::memcpy(&padded[(size_t)(n * Kp * es)], &t.data[(size_t)(n * K * es)], (size_t)(K * es));
+            rc = upload_weight(ctx->device, t.type, Kp, E, padded.data(), padded.size(), m->patch_w);
+        } else if (name == "vit.pos_embed") {
+            m->pos_grid = (int)t.ne[1];
+            if (t.ne[0] != E || t.ne[1] != t.ne[2] || m->pos_grid <= 0) { set_error("pos_embed shape mismatch"); return S3E_ERR_IO; }
+            rc = upload_f32(m.get(), t, E * t.ne[1] * t.ne[2], &m->pos);
+        } else if (name == "vit.ln_pre.weight") {
+            rc = upload_f32(m.get(), t, E, &m->ln_pre_w);
+        } else if (name == "vit.ln_pre.bias") {
+            rc = upload_f32(m.get(), t, E, &m->ln_pre_b);
+        } else if (name.compare(0, 11, "vit.blocks.") == 0) {
+            const size_t dot = name.find('.', 11);
+            const int bi = std::atoi(name.substr(11, dot - 11).c_str());
+            if (bi < 0 || bi >= m->depth || dot == std::string::npos) { set_error("tensor '%s' has a bad block index", name.c_str()); return S3E_ERR_IO; }
+            Block &b = m->blocks[(size_t)bi];
+            const std::string f = name.substr(dot + 1);
+            const int64_t Nw = b.global ? (int64_t)m->grid * m->grid : (int64_t)m->window * m->window;
+            if (f == "norm1.weight") rc = upload_f32(m.get(), t, E, &b.n1w);
+            else if (f == "norm1.bias") rc = upload_f32(m.get(), t, E, &b.n1b);
+            else if (f == "norm2.weight") rc = upload_f32(m.get(), t, E, &b.n2w);
+            else if (f == "norm2.bias") rc = upload_f32(m.get(), t, E, &b.n2b);
+            else if (f == "attn.qkv.bias") rc = upload_f32(m.get(), t, 3 * E, &b.qkv_b);
+            else if (f == "attn.proj.bias") rc = upload_f32(m.get(), t, E, &b.proj_b);
+            else if (f == "mlp.lin1.bias") rc = upload_f32(m.get(), t, MLP, &b.fc1_b);
+            else if (f == "mlp.lin2.bias") rc = upload_f32(m.get(), t, E, &b.fc2_b);
+            else if (f == "attn.freqs_cis") {
+                if (t.ne[0] != 2 || t.ne[1] != 32 || t.ne[2] != Nw) { set_error("'%s': expected [2, 32, %lld]", name.c_str(), (long long)Nw); return S3E_ERR_IO; }
+                rc = upload_f32(m.get(), t, 64 * Nw, &b.freqs);
+                b.freqs_n = Nw;
+            } else if (f == "attn.qkv.weight" || f == "attn.proj.weight" || f == "mlp.lin1.weight" || f == "mlp.lin2.weight") {
+                Weight &w = (f == "attn.qkv.weight") ? b.qkv : (f == "attn.proj.weight") ? b.proj : (f == "mlp.lin1.weight") ? b.fc1 : b.fc2;
+                const int64_t eK = (f == "mlp.lin2.weight") ? MLP : E;
+                const int64_t eN = (f == "attn.qkv.weight") ? 3 * E : (f == "mlp.lin1.weight") ? MLP : E;
+                if (t.ne[0] != eK || t.ne[1] != eN) { set_error("'%s': expected [%lld, %lld]", name.c_str(), (long long)eK, (long long)eN); return S3E_ERR_IO; }
+                rc = upload_weight(ctx->device, t.type, eK, eN, t.data.data(), t.data.size(), w);
+            } else {
+                continue;  // unknown per-block tensor: not used by the backbone
+            }
+        } else {
+            continue;
+        }
+        if (rc != S3E_OK) return rc;
+        seen++;
+    }
+    if (seen != expected) {
+        set_error("s3e_model_load: found %d of %d backbone tensors", seen, expected);
+        return S3E_ERR_IO;
+    }
+    if (m->mlp % 128 != 0) { set_error("s3e_model_load: MLP width %d must be a multiple of 128", m->mlp); return S3E_ERR_UNSUPPORTED; }
+    *out = m.release();
+    return S3E_OK;
+}
+
+extern "C" int s3e_model_hparams(const s3e_model *m, int32_t out[16]) {
+    if (!m || !out) { set_error("s3e_model_hparams: NULL argument"); return S3E_ERR_INVALID; }
+    std::memset(out, 0, 16 * sizeof(int32_t));
+    out[0] = m->img; out[1] = m->patch; out[2] = m->E; out[3] = m->depth; out[4] = m->heads;
+    out[5] = m->mlp; out[6] = m->window; out[7] = m->n_global;
+    for (int i = 0; i < 4; i++) out[8 + i] = m->gidx[i];
+    out[12] = m->ftype;
+    out[13] = m->grid;
+    return S3E_OK;
+}
+
+// ---- state + encoder --------------------------------------------------------
+struct s3e_state {
+    s3e_ctx *ctx = nullptr;
+    const s3e_model *m = nullptr;
+    int64_t T = 0;
+    float *x = nullptr;       // residual stream, T × E f32 ("vit_output" after encode)
+    float *chw = nullptr;     // uploaded image for the host-pointer entry points
+    ActBuf a1, a2, col;       // E-wide, MLP-wide and im2col activations
+    _Float16 *q16 = nullptr, *k16 = nullptr, *vt16 = nullptr;  // [hi plane | lo plane]
+    int64_t vt_elems = 0;
+};
+
+extern "C" void s3e_state_free(s3e_state *st) {
+    if (!st) return;
+    (void)hipSetDevice(st->ctx->device);
+    (void)hipStreamSynchronize(st->ctx->stream);
+    if (st->x) (void)hipFree(st->x);
+    if (st->chw) (void)hipFree(st->chw);
+    st->a1.release();
+    st->a2.release();
+    st->col.release();
+    if (st->q16) (void)hipFree(st->q16);
+    if (st->k16) (void)hipFree(st->k16);
+    if (st->vt16) (void)hipFree(st->vt16);
+    delete st;
+}
+
+extern "C" int s3e_state_create(s3e_ctx *ctx, const s3e_model *m, s3e_state **out) {
+    if (!ctx || !m || !out) { set_error("s3e_state_create: NULL argument"); return S3E_ERR_INVALID; }
+    *out = nullptr;
+    HIP_TRY(hipSetDevice(ctx->device));
+    auto *st = new s3e_state;
+    st->ctx = ctx;
+    st->m = m;
+    st->T = (int64_t)m->grid * m->grid;
+    const int64_t T = st->T, E = m->E;
+    hipError_t e = hipMalloc(&st->x, (size_t)(T * E * 4));
+    if (e == hipSuccess) e = hipMalloc(&st->chw, (size_t)3 * m->img * m->img * 4);
+    if (e == hipSuccess) e = st->a1.alloc(T, E);
+    if (e == hipSuccess) e = st->a2.alloc(T, m->mlp);
+    if (e == hipSuccess) e = st->col.alloc(T, round_up(3LL * m->patch * m->patch, 32));
+    // Q, K, Vᵀ hold two fp16 planes each (hi, lo) for split-precision attention
+    if (e == hipSuccess) e = hipMalloc(&st->q16, (size_t)(T * E * 2 * 2));
+    if (e == hipSuccess) e = hipMalloc(&st->k16, (size_t)(T * E * 2 * 2));
+    // Vᵀ rows are padded to a multiple of 8 keys: size for the widest block.
+    int64_t vt_elems = T * E;
+    for (const Block &b : m->blocks) {
+        const int64_t WS = b.global ? m->grid : m->window;
+        const int64_t NW = (m->grid / WS) * (m->grid / WS);
+        vt_elems = std::max<int64_t>(vt_elems, NW * m->heads * 64 * round_up(WS * WS, 8));
+    }
+    st->vt_elems = vt_elems;
+    if (e == hipSuccess) e = hipMalloc(&st->vt16, (size_t)(vt_elems * 2 * 2));
+    if (e != hipSuccess) {
+        s3e_state_free(st);
+        set_error("s3e_state_create: %s", hipGetErrorString(e));
+        return S3E_ERR_NOMEM;
+    }
+    *out = st;
+    return S3E_OK;
+}
+
+namespace {
+
+hipError_t run_prefix(s3e_state *st, const float *chw, float *x) {
+    const s3e_model *m = st->m;
+    hipStream_t s = st->ctx->stream;
+    const AKind pk = (m->patch_w.kind == WK_F16) ? A_F16 : A_F32;
+    const int64_t ldk = m->patch_w.K;  // 3·P² padded to 32
+    hipError_t e = launch_im2col(chw, m->img, m->patch, ldk, pk, st->col.x, s);
+    if (e != hipSuccess) return e;
+    EpiArgs ea;
+    ea.y = x;
+    ea.ldy = m->E;
+    ea.pos = m->pos;
+    ea.pos_grid = m->pos_grid;
+    ea.grid = m->grid;
+    e = launch_gemm(m->patch_w, st->col.as(pk, ldk), st->T, EPI_POS, ea, s);
+    if (e != hipSuccess) return e;
+    Act none;
+    return launch_layernorm(x, st->T, m->E, 1e-5f, m->ln_pre_w, m->ln_pre_b, none, x, s);
+}
+
+// sam3_vit_block_forward (sam3.cpp:3710-3801) as 7 launches.
+hipError_t run_block(s3e_state *st, int bi, float *x) {
+    const s3e_model *m = st->m;
+    const Block &b = m->blocks[(size_t)bi];
+    hipStream_t s = st->ctx->stream;
+    const int64_t T = st->T, E = m->E;
+    const int WS = b.global ? m->grid : m->window;
+    const int Nw = WS * WS, NW = (m->grid / WS) * (m->grid / WS);
+    // LN1 → activation for the QKV weight
+    const Act a_qkv = st->a1.as(act_kind_for(b.qkv.kind), E);
+    hipError_t e = launch_layernorm(x, T, E, 1e-5f, b.n1w, b.n1b, a_qkv, nullptr, s);
+    if (e != hipSuccess) return e;
+    // QKV GEMM + bias + RoPE → fp16 Q, K, Vᵀ in window layout
+    EpiArgs eq;
+    eq.bias = b.qkv_b;
+    eq.grid = m->grid;
+    eq.window = WS;
+    eq.E = (int)E;
+    eq.HD = 64;
+    eq.NH = m->heads;
+    eq.freqs = b.freqs;
+    eq.q = st->q16;
+    eq.k = st->k16;
+    eq.vt = st->vt16;
+    // Quantized (and F32) projections re-quantize the attention output: run
+    // attention split so it matches f32 attention; F16 models use plain fp16.
+    const bool split = b.proj.kind != WK_F16;
+    if (split) {
+        eq.q_lo = st->q16 + T * E;
+        eq.k_lo = st->k16 + T * E;
+        eq.vt_lo = st->vt16 + st->vt_elems;
+    }
+    eq.vt_ld = (Nw + 7) / 8 * 8;
+    e = launch_gemm(b.qkv, a_qkv, T, EPI_QKV, eq, s);
+    if (e != hipSuccess) return e;
+    // attention → activation for the proj weight, un-partitioned
+    AttnArgs aa;
+    aa.q = st->q16;
+    aa.k = st->k16;
+    aa.vt = st->vt16;
+    aa.q_lo = eq.q_lo;
+    aa.k_lo = eq.k_lo;
+    aa.vt_lo = eq.vt_lo;
+    aa.Nq = Nw;
+    aa.Nkv = Nw;
+    aa.NH = m->heads;
+    aa.BH = NW * m->heads;
+    aa.scale = 1.0f / std::sqrt(64.0f);
+    aa.grid = m->grid;
+    aa.window = WS;
+    aa.out = st->a1.as(act_kind_for(b.proj.kind), E);
+    e = launch_attn(aa, s);
+    if (e != hipSuccess) return e;
+    // proj + bias + residual
+    EpiArgs ep;
+    ep.bias = b.proj_b;
+    ep.y = x;
+    ep.ldy = E;
+    e = launch_gemm(b.proj, aa.out, T, EPI_RESID, ep, s);
+    if (e != hipSuccess) return e;
+    // LN2 → fc1 + bias + GELU(erf) → activation for fc2 → fc2 + bias + residual
+    const Act a_fc1 = st->a1.as(act_kind_for(b.fc1.kind), E);
+    e = launch_layernorm(x, T, E, 1e-5f, b.n2w, b.n2b, a_fc1, nullptr, s);
+    if (e != hipSuccess) return e;
+    EpiArgs e1;
+    e1.bias = b.fc1_b;
+    e1.out = st->a2.as(act_kind_for(b.fc2.kind), m->mlp);
+    e = launch_gemm(b.fc1, a_fc1, T, EPI_GELU, e1, s);
+    if (e != hipSuccess) return e;
+    EpiArgs e2;
+    e2.bias = b.fc2_b;
+    e2.y = x;
+    e2.ldy = E;
+    return launch_gemm(b.fc2, e1.out, T, EPI_RESID, e2, s);
+}
+
+}  // namespace
+
+extern "C" int s3e_vit_prefix(s3e_state *st, const float *chw_device, float *x_device) {
+    if (!st || !chw_device || !x_device) { set_error("s3e_vit_prefix: NULL argument"); return S3E_ERR_INVALID; }
+    HIP_TRY(hipSetDevice(st->ctx->device));
+    HIP_TRY(run_prefix(st, chw_device, x_device));
+    return S3E_OK;
+}
+
+extern "C" int s3e_vit_block(s3e_state *st, int idx, float *x_device) {
+    if (!st || !x_device) { set_error("s3e_vit_block: NULL argument"); return S3E_ERR_INVALID; }
+    if (idx < 0 || idx >= st->m->depth) { set_error("s3e_vit_block: block %d out of range", idx); return S3E_ERR_INVALID; }
+    HIP_TRY(hipSetDevice(st->ctx->device));
+    HIP_TRY(run_block(st, idx, x_device));
+    return S3E_OK;
+}
+
+extern "C" int s3e_encode_chw(s3e_state *st, const float *chw_device) {
+    if (!st || !chw_device) { set_error("s3e_encode_chw: NULL argument"); return S3E_ERR_INVALID; }
+    HIP_TRY(hipSetDevice(st->ctx->device));
+    HIP_TRY(run_prefix(st, chw_device, st->x));
+    for (int i = 0; i < st->m->depth; i++) HIP_TRY(run_block(st, i, st->x));
+    return S3E_OK;
+}
+
+extern "C" int s3e_encode_chw_host(s3e_state *st, const float *chw_host) {
+    if (!st || !chw_host) { set_error("s3e_encode_chw_host: NULL argument"); return S3E_ERR_INVALID; }
+    HIP_TRY(hipSetDevice(st->ctx->device));
+    HIP_TRY(hipMemcpyAsync(st->chw, chw_host, (size_t)3 * st->m->img * st->m->img * 4, hipMemcpyHostToDevice,
+                           st->ctx->stream));
+    return s3e_encode_chw(st, st->chw);
+}
+
+// sam3_resize_bilinear + sam3_preprocess_image (sam3.cpp:3441-3514), on the host.
+extern "C" int s3e_encode_image_u8(s3e_state *st, const uint8_t *hwc, int width, int height) {
+    if (!st || !hwc || width <= 0 || height <= 0) { set_error("s3e_encode_image_u8: bad argument"); return S3E_ERR_INVALID; }
+    const int S = st->m->img;
+    std::vector<uint8_t> resized;
+    const uint8_t *px = hwc;
+    if (width != S || height != S) {
+        resized.resize((size_t)S * S * 3);
+        const double sx = (double)width / S, sy = (double)height / S;
+        for (int y = 0; y < S; ++y) {
+            double fy = (y + 0.5) * sy - 0.5;
+            if (fy < 0.0) fy = 0.0;
+            const int y0 = (int)fy, y1 = (y0 < height - 1) ? y0 + 1 : y0;
+            const double wy = fy - y0, wy0 = 1.0 - wy;
+            for (int x = 0; x < S; ++x) {
+                double fx = (x + 0.5) * sx - 0.5;
+                if (fx < 0.0) fx = 0.0;
+                const int x0 = (int)fx, x1 = (x0 < width - 1) ? x0 + 1 : x0;
+                const double wx = fx - x0, wx0 = 1.0 - wx;
+                for (int c = 0; c < 3; ++c) {
+                    const double p00 = hwc[(y0 * width + x0) * 3 + c], p01 = hwc[(y0 * width + x1) * 3 + c];
+                    const double p10 = hwc[(y1 * width + x0) * 3 + c], p11 = hwc[(y1 * width + x1) * 3 + c];
+                    const double v = wy0 * (wx0 * p00 + wx * p01) + wy * (wx0 * p10 + wx * p11);
+                    int iv = (int)(v + 0.5);
+                    iv = iv < 0 ? 0 : (iv > 255 ? 255 : iv);
+                    resized[((size_t)y * S + x) * 3 + c] = (uint8_t)iv;
+                }
+            }
+        }
+        px = resized.data();
+    }
+    std::vector<float> chw((size_t)3 * S * S);
+    for (int c = 0; c < 3; ++c)
+        for (int y = 0; y < S; ++y)
+            for (int x = 0; x < S; ++x) {
+                const float v = px[((size_t)y * S + x) * 3 + c] / 255.0f;
+                chw[(size_t)c * S * S + (size_t)y * S + x] = (v - 0.5f) / 0.5f;
+            }
+    const int rc = s3e_encode_chw_host(st, chw.data());
+    if (rc != S3E_OK) return rc;
+    return s3e_ctx_sync(st->ctx);
+}
+
+extern "C" int s3e_state_tensor_info(const s3e_state *st, const char *name, int64_t ne[4]) {
+    if (!st || !name || !ne) { set_error("s3e_state_tensor_info: NULL argument"); return S3E_ERR_INVALID; }
+    if (std::strcmp(name, "vit_output") != 0) { set_error("s3e_state_tensor_info: unknown tensor '%s'", name); return S3E_ERR_INVALID; }
+    ne[0] = st->m->E;
+    ne[1] = st->m->grid;
+    ne[2] = st->m->grid;
+    ne[3] = 1;
+    return S3E_OK;
+}
+
+extern "C" const float *s3e_state_tensor_device(const s3e_state *st, const char *name) {
+    if (!st || !name || std::strcmp(name, "vit_output") != 0) return nullptr;
+    return st->x;
+}
+
+extern "C" int s3e_state_tensor_get(const s3e_state *st, const char *name, float *host, size_t n) {
+    int64_t ne[4];
+    const int rc = s3e_state_tensor_info(st, name, ne);
+    if (rc != S3E_OK) return rc;
+    const size_t need = (size_t)(ne[0] * ne[1] * ne[2] * ne[3]);
+    if (!host || n < need) { set_error("s3e_state_tensor_get: buffer holds %zu floats, need %zu", n, need); return S3E_ERR_INVALID; }
+    HIP_TRY(hipSetDevice(st->ctx->device));
+    HIP_TRY(hipMemcpyAsync(host, st->x, need * 4, hipMemcpyDeviceToHost, st->ctx->stream));
+    HIP_TRY(hipStreamSynchronize(st->ctx->stream));
+    return S3E_OK;
+}

@@ -1,0 +1,333 @@
+"""ctypes binding of the MI355X encoder engine's C ABI (include/s3e.h).
+
+The engine itself is native (sam3.cpp_amd/libs3e.so, built from csrc/); this
+module only marshals numpy arrays and device pointers across the C ABI for
+the tests and the benchmark.  Importing it fails loudly when the library has
+not been built: there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t, c_uint16, c_uint64, c_void_p
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libs3e.so")
+
+TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_Q4_1, TYPE_Q8_0, TYPE_Q8_1 = 0, 1, 2, 3, 8, 9
+PREC_DEFAULT, PREC_F32 = 0, 1
+FTYPE_BY_NAME = {"f32": 0, "f16": 1, "q4_0": 2, "q4_1": 3, "q8_0": 8}
+
+
+class S3EError(RuntimeError):
+    pass
+
+
+class SynthCfg(ctypes.Structure):
+    _fields_ = [
+        ("img_size", c_int32), ("patch", c_int32), ("embed_dim", c_int32), ("depth", c_int32),
+        ("heads", c_int32), ("mlp_ratio_x1000", c_int32), ("window", c_int32),
+        ("n_global", c_int32), ("global_idx", c_int32 * 4),
+        ("ftype", c_int32), ("seed", c_uint64), ("std", c_float),
+    ]
+
+
+def _load() -> ctypes.CDLL:
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is not built; run __graft_entry__.build() first")
+    lib = ctypes.CDLL(LIB_PATH)
+    P64 = POINTER(c_int64)
+    sig = {
+        "s3e_last_error": (c_char_p, []),
+        "s3e_abi_version": (c_int, []),
+        "s3e_ctx_create": (c_int, [c_int, POINTER(c_void_p)]),
+        "s3e_ctx_destroy": (None, [c_void_p]),
+        "s3e_ctx_sync": (c_int, [c_void_p]),
+        "s3e_ctx_stream": (c_void_p, [c_void_p]),
+        "s3e_malloc": (c_int, [c_void_p, c_size_t, POINTER(c_void_p)]),
+        "s3e_free": (c_int, [c_void_p, c_void_p]),
+        "s3e_memcpy_h2d": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t]),
+        "s3e_memcpy_d2h": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t]),
+        "s3e_weight_upload": (c_int, [c_void_p, c_int, c_int64, c_int64, c_void_p, c_size_t, POINTER(c_void_p)]),
+        "s3e_weight_free": (None, [c_void_p]),
+        "s3e_weight_info": (c_int, [c_void_p, P64]),
+        "s3e_mul_mat": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
+        "s3e_quantize_rows": (c_int, [c_void_p, c_int, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
+        "s3e_layer_norm": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_float, c_void_p, c_void_p, c_void_p]),
+        "s3e_flash_attn_ext": (c_int, [c_void_p, c_void_p, P64, c_void_p, P64, c_void_p, P64,
+                                       c_int64, c_int64, c_int64, c_int64, c_int64, c_float, c_int, c_void_p]),
+        "s3e_model_load": (c_int, [c_void_p, c_char_p, POINTER(c_void_p)]),
+        "s3e_model_free": (None, [c_void_p]),
+        "s3e_model_hparams": (c_int, [c_void_p, POINTER(c_int32)]),
+        "s3e_state_create": (c_int, [c_void_p, c_void_p, POINTER(c_void_p)]),
+        "s3e_state_free": (None, [c_void_p]),
+        "s3e_encode_chw": (c_int, [c_void_p, c_void_p]),
+        "s3e_encode_chw_host": (c_int, [c_void_p, c_void_p]),
+        "s3e_encode_image_u8": (c_int, [c_void_p, c_void_p, c_int, c_int]),
+        "s3e_vit_prefix": (c_int, [c_void_p, c_void_p, c_void_p]),
+        "s3e_vit_block": (c_int, [c_void_p, c_int, c_void_p]),
+        "s3e_state_tensor_info": (c_int, [c_void_p, c_char_p, P64]),
+        "s3e_state_tensor_get": (c_int, [c_void_p, c_char_p, c_void_p, c_size_t]),
+        "s3e_state_tensor_device": (c_void_p, [c_void_p, c_char_p]),
+        "s3e_synth_write": (c_int, [c_char_p, POINTER(SynthCfg)]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+LIB = _load()
+DECLARED = [
+    "s3e_last_error", "s3e_abi_version", "s3e_ctx_create", "s3e_ctx_destroy", "s3e_ctx_sync", "s3e_ctx_stream",
+    "s3e_malloc", "s3e_free", "s3e_memcpy_h2d", "s3e_memcpy_d2h", "s3e_weight_upload", "s3e_weight_free",
+    "s3e_weight_info", "s3e_mul_mat", "s3e_quantize_rows", "s3e_layer_norm", "s3e_flash_attn_ext", "s3e_model_load",
+    "s3e_model_free", "s3e_model_hparams", "s3e_state_create", "s3e_state_free", "s3e_encode_chw",
+    "s3e_encode_chw_host", "s3e_encode_image_u8", "s3e_vit_prefix", "s3e_vit_block", "s3e_state_tensor_info",
+    "s3e_state_tensor_get", "s3e_state_tensor_device", "s3e_synth_write",
+]
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc != 0:
+        msg = LIB.s3e_last_error().decode(errors="replace")
+        raise S3EError(f"{what or 's3e'} failed (status {rc}): {msg}")
+
+
+def synth_write(path: str, *, img_size=1008, patch=14, embed_dim=1024, depth=32, heads=16,
+                mlp_ratio_x1000=4625, window=24, global_idx=(7, 15, 23, 31), ftype="q4_0",
+                seed=0, std=0.02, random_affine=False) -> None:
+    """Write a random-init SAM 3 visual-only model file (s3e_synth_write)."""
+    cfg = SynthCfg()
+    cfg.img_size, cfg.patch, cfg.embed_dim, cfg.depth = img_size, patch, embed_dim, depth
+    cfg.heads, cfg.mlp_ratio_x1000, cfg.window = heads, mlp_ratio_x1000, window
+    g = list(global_idx)[:4]
+    cfg.n_global = len(g)
+    for i in range(4):
+        cfg.global_idx[i] = g[i] if i < len(g) else -1
+    cfg.ftype = FTYPE_BY_NAME[ftype] if isinstance(ftype, str) else int(ftype)
+    cfg.seed = seed
+    cfg.std = -abs(std) if random_affine else abs(std)
+    check(LIB.s3e_synth_write(path.encode(), ctypes.byref(cfg)), "s3e_synth_write")
+
+
+class DeviceBuffer:
+    """A device allocation owned by a Context."""
+
+    def __init__(self, ctx: "Context", nbytes: int):
+        self.ctx = ctx
+        self.nbytes = int(nbytes)
+        p = c_void_p()
+        check(LIB.s3e_malloc(ctx.handle, max(self.nbytes, 1), ctypes.byref(p)), "s3e_malloc")
+        self.ptr = p.value
+
+    def upload(self, arr: np.ndarray) -> "DeviceBuffer":
+        arr = np.ascontiguousarray(arr)
+        assert arr.nbytes <= self.nbytes
+        check(LIB.s3e_memcpy_h2d(self.ctx.handle, self.ptr, arr.ctypes.data, arr.nbytes), "h2d")
+        return self
+
+    def download(self, dtype, shape) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        assert out.nbytes <= self.nbytes
+        check(LIB.s3e_memcpy_d2h(self.ctx.handle, out.ctypes.data, self.ptr, out.nbytes), "d2h")
+        return out
+
+    def free(self) -> None:
+        if self.ptr:
+            LIB.s3e_free(self.ctx.handle, self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Weight:
+    def __init__(self, ctx: "Context", ggml_type: int, K: int, N: int, data: np.ndarray):
+        self.ctx = ctx
+        data = np.ascontiguousarray(data)
+        h = c_void_p()
+        check(LIB.s3e_weight_upload(ctx.handle, ggml_type, K, N, data.ctypes.data, data.nbytes, ctypes.byref(h)),
+              "s3e_weight_upload")
+        self.handle = h.value
+        self.K, self.N, self.type = K, N, ggml_type
+
+    def info(self):
+        out = (c_int64 * 4)()
+        check(LIB.s3e_weight_info(self.handle, out), "s3e_weight_info")
+        return list(out)
+
+    def free(self):
+        if self.handle:
+            LIB.s3e_weight_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Context:
+    def __init__(self, device: int = 0):
+        h = c_void_p()
+        check(LIB.s3e_ctx_create(device, ctypes.byref(h)), "s3e_ctx_create")
+        self.handle = h.value
+
+    def close(self):
+        if self.handle:
+            LIB.s3e_ctx_destroy(self.handle)
+            self.handle = None
+
+    def sync(self):
+        check(LIB.s3e_ctx_sync(self.handle), "s3e_ctx_sync")
+
+    @property
+    def stream(self) -> int:
+        return LIB.s3e_ctx_stream(self.handle)
+
+    def buffer(self, nbytes: int) -> DeviceBuffer:
+        return DeviceBuffer(self, nbytes)
+
+    def to_device(self, arr: np.ndarray) -> DeviceBuffer:
+        arr = np.ascontiguousarray(arr)
+        return DeviceBuffer(self, arr.nbytes).upload(arr)
+
+    def weight(self, ggml_type: int, K: int, N: int, data: np.ndarray) -> Weight:
+        return Weight(self, ggml_type, K, N, data)
+
+    def mul_mat(self, w: Weight, X: DeviceBuffer, M: int, Y: DeviceBuffer, bias: DeviceBuffer | None = None):
+        check(LIB.s3e_mul_mat(self.handle, w.handle, X.ptr, M, bias.ptr if bias else None, Y.ptr), "s3e_mul_mat")
+
+    def quantize_rows(self, vdt: int, X: DeviceBuffer, M: int, K: int, qs: DeviceBuffer,
+                      d: DeviceBuffer | None, s: DeviceBuffer | None):
+        check(LIB.s3e_quantize_rows(self.handle, vdt, X.ptr, M, K, qs.ptr, d.ptr if d else None,
+                                    s.ptr if s else None), "s3e_quantize_rows")
+
+    def layer_norm(self, x: DeviceBuffer, rows: int, n: int, eps: float, w: DeviceBuffer | None,
+                   b: DeviceBuffer | None, y: DeviceBuffer):
+        check(LIB.s3e_layer_norm(self.handle, x.ptr, rows, n, c_float(eps), w.ptr if w else None,
+                                 b.ptr if b else None, y.ptr), "s3e_layer_norm")
+
+    def flash_attn_ext(self, q: DeviceBuffer, q_nb, k: DeviceBuffer, k_nb, v: DeviceBuffer, v_nb,
+                       D: int, Nq: int, Nkv: int, nh: int, B: int, scale: float, o: DeviceBuffer,
+                       prec: int = PREC_F32):
+        a = lambda nb: (c_int64 * 4)(*[int(x) for x in nb])
+        check(LIB.s3e_flash_attn_ext(self.handle, q.ptr, a(q_nb), k.ptr, a(k_nb), v.ptr, a(v_nb),
+                                     D, Nq, Nkv, nh, B, c_float(scale), prec, o.ptr), "s3e_flash_attn_ext")
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Model:
+    def __init__(self, ctx: Context, path: str):
+        self.ctx = ctx
+        h = c_void_p()
+        check(LIB.s3e_model_load(ctx.handle, path.encode(), ctypes.byref(h)), "s3e_model_load")
+        self.handle = h.value
+        hp = (c_int32 * 16)()
+        check(LIB.s3e_model_hparams(self.handle, hp), "s3e_model_hparams")
+        self.hparams = list(hp)
+        self.img_size, self.patch, self.E, self.depth = hp[0], hp[1], hp[2], hp[3]
+        self.grid = hp[13]
+
+    def free(self):
+        if self.handle:
+            LIB.s3e_model_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class State:
+    def __init__(self, ctx: Context, model: Model):
+        self.ctx, self.model = ctx, model
+        h = c_void_p()
+        check(LIB.s3e_state_create(ctx.handle, model.handle, ctypes.byref(h)), "s3e_state_create")
+        self.handle = h.value
+
+    def encode_chw(self, chw: DeviceBuffer):
+        check(LIB.s3e_encode_chw(self.handle, chw.ptr), "s3e_encode_chw")
+
+    def encode_chw_host(self, chw: np.ndarray):
+        chw = np.ascontiguousarray(chw, dtype=np.float32)
+        check(LIB.s3e_encode_chw_host(self.handle, chw.ctypes.data), "s3e_encode_chw_host")
+        self.ctx.sync()
+
+    def encode_image_u8(self, hwc: np.ndarray):
+        hwc = np.ascontiguousarray(hwc, dtype=np.uint8)
+        check(LIB.s3e_encode_image_u8(self.handle, hwc.ctypes.data, hwc.shape[1], hwc.shape[0]),
+              "s3e_encode_image_u8")
+
+    def prefix(self, chw: DeviceBuffer, x: DeviceBuffer):
+        check(LIB.s3e_vit_prefix(self.handle, chw.ptr, x.ptr), "s3e_vit_prefix")
+
+    def block(self, idx: int, x: DeviceBuffer):
+        check(LIB.s3e_vit_block(self.handle, idx, x.ptr), "s3e_vit_block")
+
+    def tensor(self, name: str = "vit_output") -> np.ndarray:
+        ne = (c_int64 * 4)()
+        check(LIB.s3e_state_tensor_info(self.handle, name.encode(), ne), "s3e_state_tensor_info")
+        n = ne[0] * ne[1] * ne[2] * ne[3]
+        out = np.empty(n, dtype=np.float32)
+        check(LIB.s3e_state_tensor_get(self.handle, name.encode(), out.ctypes.data, n), "s3e_state_tensor_get")
+        return out.reshape(ne[2] * ne[1], ne[0])
+
+    def free(self):
+        if self.handle:
+            LIB.s3e_state_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+# ---- HIP events on the engine's stream (timing) -----------------------------
+class HipEvents:
+    """hipEvent timing on an arbitrary stream, through libamdhip64."""
+
+    def __init__(self):
+        self.hip = ctypes.CDLL("libamdhip64.so")
+        self.hip.hipEventCreate.argtypes = [POINTER(c_void_p)]
+        self.hip.hipEventRecord.argtypes = [c_void_p, c_void_p]
+        self.hip.hipEventSynchronize.argtypes = [c_void_p]
+        self.hip.hipEventElapsedTime.argtypes = [POINTER(c_float), c_void_p, c_void_p]
+        self.hip.hipEventDestroy.argtypes = [c_void_p]
+
+    def create(self):
+        e = c_void_p()
+        if self.hip.hipEventCreate(ctypes.byref(e)) != 0:
+            raise S3EError("hipEventCreate failed")
+        return e.value
+
+    def record(self, ev, stream):
+        if self.hip.hipEventRecord(ev, stream) != 0:
+            raise S3EError("hipEventRecord failed")
+
+    def elapsed_ms(self, e0, e1) -> float:
+        self.hip.hipEventSynchronize(e1)
+        ms = c_float()
+        if self.hip.hipEventElapsedTime(ctypes.byref(ms), e0, e1) != 0:
+            raise S3EError("hipEventElapsedTime failed")
+        return ms.value
+
+    def destroy(self, ev):
+        self.hip.hipEventDestroy(ev)

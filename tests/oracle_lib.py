@@ -1,0 +1,217 @@
+"""ctypes access to the CPU oracle (oracle/liboracle.so) for the tests.
+
+The oracle is the checker: a C restatement of ggml's CPU arithmetic on the
+sam3.cpp encoder path.  Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg load it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t, c_uint16, c_void_p
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_DIR = os.path.join(ROOT, "oracle")
+LIB_PATH = os.path.join(ORACLE_DIR, "liboracle.so")
+
+F32, F16, Q4_0, Q4_1, Q8_0, Q8_1 = 0, 1, 2, 3, 8, 9
+BLOCK_BYTES = {Q4_0: 18, Q4_1: 20, Q8_0: 34, Q8_1: 36}
+VEC_DOT = {Q4_0: Q8_0, Q8_0: Q8_0, Q4_1: Q8_1, F16: F16, F32: F32}
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        subprocess.run(["make", "-C", ORACLE_DIR], check=True, capture_output=True)
+    lib = ctypes.CDLL(LIB_PATH)
+    P = c_void_p
+    sig = {
+        "orc_fp32_to_fp16": (ctypes.c_uint16, [c_float]),
+        "orc_fp16_to_fp32": (c_float, [ctypes.c_uint16]),
+        "orc_fp32_to_fp16_row": (None, [P, P, c_int64]),
+        "orc_fp16_to_fp32_row": (None, [P, P, c_int64]),
+        "orc_row_size": (c_size_t, [c_int, c_int64]),
+        "orc_vec_dot_type": (c_int, [c_int]),
+        "orc_quantize_row_q4_0_ref": (None, [P, P, c_int64]),
+        "orc_quantize_row_q4_1_ref": (None, [P, P, c_int64]),
+        "orc_quantize_row_q8_0_ref": (None, [P, P, c_int64]),
+        "orc_quantize_row_q8_1_ref": (None, [P, P, c_int64]),
+        "orc_quantize_row_q8_0": (None, [P, P, c_int64]),
+        "orc_quantize_row_q8_1": (None, [P, P, c_int64]),
+        "orc_from_float": (None, [c_int, P, P, c_int64]),
+        "orc_dequantize_row": (None, [c_int, P, P, c_int64]),
+        "orc_vec_dot": (c_float, [c_int, c_int64, P, P]),
+        "orc_block_isums": (None, [c_int, c_int64, P, P, P]),
+        "orc_mul_mat": (None, [c_int, P, c_int64, c_int64, P, c_int64, P, c_int]),
+        "orc_mul_mat_preq": (None, [c_int, P, c_int64, c_int64, P, c_int64, P, c_int]),
+        "orc_layer_norm": (None, [P, P, c_int64, c_int64, c_float, P, P, c_int]),
+        "orc_gelu_erf": (None, [P, c_int64]),
+        "orc_rope": (None, [P, c_int64, c_int64, c_int64, P]),
+        "orc_flash_attn_ext": (None, [P, c_int64, c_int64, c_int64, P, c_int64, c_int64, c_int64,
+                                      P, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,
+                                      c_float, P, c_int]),
+        "orc_compute_axial_cis": (None, [P, c_int, c_int, c_int, c_float, c_float]),
+        "orc_preprocess_sam3": (None, [P, c_int, c_int, c_int, P]),
+        "orc_model_load": (P, [c_char_p]),
+        "orc_model_free": (None, [P]),
+        "orc_last_error": (c_char_p, []),
+        "orc_model_hparams": (None, [P, POINTER(c_int32)]),
+        "orc_vit_prefix": (c_int, [P, P, P, c_int]),
+        "orc_vit_block": (c_int, [P, c_int, P, c_int]),
+        "orc_vit_encode": (c_int, [P, P, P, c_int]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(lib, name)
+        f.restype = res
+        f.argtypes = args
+    return lib
+
+
+LIB = _load()
+
+
+def ptr(a: np.ndarray):
+    return a.ctypes.data
+
+
+def row_size(t: int, k: int) -> int:
+    return int(LIB.orc_row_size(t, k))
+
+
+def quantize_ref(t: int, x: np.ndarray) -> np.ndarray:
+    """ggml_quantize_chunk reference quantizer (weights): rows of x → bytes."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, k = x.reshape(-1, x.shape[-1]).shape
+    out = np.zeros(rows * row_size(t, k), dtype=np.uint8)
+    fn = {Q4_0: LIB.orc_quantize_row_q4_0_ref, Q4_1: LIB.orc_quantize_row_q4_1_ref,
+          Q8_0: LIB.orc_quantize_row_q8_0_ref, Q8_1: LIB.orc_quantize_row_q8_1_ref}[t]
+    rs = row_size(t, k)
+    for r in range(rows):
+        fn(ptr(x) + r * k * 4, ptr(out) + r * rs, k)
+    return out
+
+
+def to_weight_bytes(t: int, w: np.ndarray) -> np.ndarray:
+    """N×K float weights → ggml bytes of type t (reference quantizer / fp16 RNE)."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    if t == F32:
+        return w.view(np.uint8).ravel().copy()
+    if t == F16:
+        out = np.empty(w.size, dtype=np.uint16)
+        LIB.orc_fp32_to_fp16_row(ptr(w), ptr(out), w.size)
+        return out.view(np.uint8)
+    return quantize_ref(t, w)
+
+
+def from_float(t: int, x: np.ndarray) -> np.ndarray:
+    """ggml from_float of the vec_dot type (activation conversion), row by row."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, k = x.shape
+    rs = row_size(t, k)
+    out = np.zeros(rows * rs, dtype=np.uint8)
+    for r in range(rows):
+        LIB.orc_from_float(t, ptr(x) + r * k * 4, ptr(out) + r * rs, k)
+    return out
+
+
+def dequantize(t: int, data: np.ndarray, rows: int, k: int) -> np.ndarray:
+    out = np.empty((rows, k), dtype=np.float32)
+    rs = row_size(t, k)
+    data = np.ascontiguousarray(data)
+    for r in range(rows):
+        LIB.orc_dequantize_row(t, ptr(data) + r * rs, ptr(out) + r * k * 4, k)
+    return out
+
+
+def split_q8(t: int, data: np.ndarray, rows: int, k: int):
+    """Q8_0/Q8_1 ggml bytes → (qs int8 [rows,k], d uint16 [rows,k/32], s uint16 or None)."""
+    bb = BLOCK_BYTES[t]
+    blocks = np.ascontiguousarray(data).reshape(rows, k // 32, bb)
+    d = blocks[:, :, 0:2].copy().view(np.uint16).reshape(rows, k // 32)
+    if t == Q8_1:
+        s = blocks[:, :, 2:4].copy().view(np.uint16).reshape(rows, k // 32)
+        qs = blocks[:, :, 4:].copy().view(np.int8).reshape(rows, k)
+    else:
+        s = None
+        qs = blocks[:, :, 2:].copy().view(np.int8).reshape(rows, k)
+    return qs, d, s
+
+
+def mul_mat(t: int, wbytes: np.ndarray, N: int, K: int, X: np.ndarray, nthreads: int = 0) -> np.ndarray:
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    M = X.shape[0]
+    Y = np.empty((M, N), dtype=np.float32)
+    LIB.orc_mul_mat(t, ptr(wbytes), N, K, ptr(X), M, ptr(Y), nthreads)
+    return Y
+
+
+def layer_norm(x: np.ndarray, eps: float, w=None, b=None) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    LIB.orc_layer_norm(ptr(x), ptr(y), x.shape[0], x.shape[1], eps, ptr(w) if w is not None else None,
+                       ptr(b) if b is not None else None, 0)
+    return y
+
+
+def flash_attn(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, nthreads: int = 0) -> np.ndarray:
+    """q [B, nh, Nq, D], k/v [B, nh, Nkv, D] f32 → O [B, Nq, nh, D] (ggml layout)."""
+    q, k, v = (np.ascontiguousarray(a, dtype=np.float32) for a in (q, k, v))
+    B, nh, Nq, D = q.shape
+    Nkv = k.shape[2]
+    o = np.empty((B, Nq, nh, D), dtype=np.float32)
+    LIB.orc_flash_attn_ext(ptr(q), D, Nq * D, nh * Nq * D, ptr(k), D, Nkv * D, nh * Nkv * D,
+                           ptr(v), D, Nkv * D, nh * Nkv * D, D, Nq, Nkv, nh, B, scale, ptr(o), nthreads)
+    return o
+
+
+class OracleModel:
+    def __init__(self, path: str):
+        self.h = LIB.orc_model_load(path.encode())
+        if not self.h:
+            raise RuntimeError("oracle model load failed: " + LIB.orc_last_error().decode())
+        hp = (c_int32 * 16)()
+        LIB.orc_model_hparams(self.h, hp)
+        self.hp = list(hp)
+        self.img, self.patch, self.E, self.depth = hp[0], hp[1], hp[2], hp[3]
+        self.grid = self.img // self.patch
+
+    def prefix(self, chw: np.ndarray, nthreads: int = 0) -> np.ndarray:
+        x = np.empty((self.grid * self.grid, self.E), dtype=np.float32)
+        chw = np.ascontiguousarray(chw, dtype=np.float32)
+        assert LIB.orc_vit_prefix(self.h, ptr(chw), ptr(x), nthreads) == 0, LIB.orc_last_error()
+        return x
+
+    def block(self, i: int, x: np.ndarray, nthreads: int = 0) -> np.ndarray:
+        x = np.array(x, dtype=np.float32, copy=True)
+        assert LIB.orc_vit_block(self.h, i, ptr(x), nthreads) == 0, LIB.orc_last_error()
+        return x
+
+    def encode(self, chw: np.ndarray, nthreads: int = 0) -> np.ndarray:
+        x = np.empty((self.grid * self.grid, self.E), dtype=np.float32)
+        chw = np.ascontiguousarray(chw, dtype=np.float32)
+        assert LIB.orc_vit_encode(self.h, ptr(chw), ptr(x), nthreads) == 0, LIB.orc_last_error()
+        return x
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            LIB.orc_model_free(self.h)
+            self.h = None
+
+
+def preprocess_sam3(img_hwc: np.ndarray, img_size: int) -> np.ndarray:
+    img = np.ascontiguousarray(img_hwc, dtype=np.uint8)
+    out = np.empty((3, img_size, img_size), dtype=np.float32)
+    LIB.orc_preprocess_sam3(ptr(img), img.shape[1], img.shape[0], img_size, ptr(out))
+    return out
+
+
+def rel_l2(a: np.ndarray, b: np.ndarray) -> float:
+    a = np.asarray(a, dtype=np.float64).ravel()
+    b = np.asarray(b, dtype=np.float64).ravel()
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def max_abs(a: np.ndarray, b: np.ndarray) -> float:
+    return float(np.max(np.abs(np.asarray(a, np.float64) - np.asarray(b, np.float64))))

@@ -1,0 +1,124 @@
+"""GPU parity of the operator entry points against the CPU oracle.
+
+- s3e_quantize_rows: bit-exact with ggml's x86 from_float (Q8_0, Q8_1, F16),
+  including rows built so that x·127/amax lands exactly on k + 0.5.
+- s3e_mul_mat: every weight type at small, ragged and SAM 3 ViT MLP shapes
+  (fc1 N=4736 K=1024, fc2 N=1024 K=4736, M = 5184 and 64).  Both sides use
+  the same quantized activations, so only fp32 accumulation order differs:
+  relative L2 ≤ 1e-5.
+- s3e_flash_attn_ext: windowed (9 × 576) and global (5184) shapes, head dim
+  64.  Default precision rounds Q, K, V and P to fp16 (fp32 accumulation):
+  the F16 tolerance, relative L2 ≤ 2e-3.  F32 precision (fp16 hi/lo pairs)
+  must match f32 attention: relative L2 ≤ 1e-5.
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _tie_rows(K):
+    """Rows whose scaled values sit exactly on k + 0.5 (amax = 127 → id = 1,
+    amax = 63.5 → id = 2), so round-half-even and round-half-away differ."""
+    r0 = np.zeros(K, np.float32)
+    r0[0::32] = 127.0
+    base = np.array([0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.5, -3.5, 100.5, -100.5, 126.5, -126.5], np.float32)
+    for b in range(K // 32):
+        r0[b * 32 + 1:b * 32 + 1 + len(base)] = base
+    r1 = np.zeros(K, np.float32)
+    r1[0::32] = -63.5
+    for b in range(K // 32):
+        r1[b * 32 + 1:b * 32 + 1 + len(base)] = base / 2
+    return np.stack([r0, r1])
+
+
+@pytest.mark.parametrize("vdt", [orc.Q8_0, orc.Q8_1, orc.F16])
+def test_quantize_rows_bit_exact(ctx, vdt):
+    rng = np.random.default_rng(11)
+    M, K = 258, 1024
+    X = (rng.standard_normal((M, K)) * rng.uniform(1e-3, 30, (M, 1))).astype(np.float32)
+    X[:2] = _tie_rows(K)
+    X[2] = 0.0  # all-zero row: d = 0, q = 0
+    ref = orc.from_float(vdt, X)
+    Xd = ctx.to_device(X)
+    if vdt == orc.F16:
+        qs = ctx.buffer(M * K * 2)
+        ctx.quantize_rows(vdt, Xd, M, K, qs, None, None)
+        ctx.sync()
+        got = qs.download(np.uint16, (M, K))
+        assert np.array_equal(got.view(np.uint8).ravel(), ref)
+        return
+    qs, d, s = ctx.buffer(M * K), ctx.buffer(M * K // 32 * 2), ctx.buffer(M * K // 32 * 2)
+    ctx.quantize_rows(vdt, Xd, M, K, qs, d, s)
+    ctx.sync()
+    rq, rd, rs = orc.split_q8(vdt, ref, M, K)
+    assert np.array_equal(qs.download(np.int8, (M, K)), rq)
+    assert np.array_equal(d.download(np.uint16, (M, K // 32)), rd)
+    if vdt == orc.Q8_1:
+        assert np.array_equal(s.download(np.uint16, (M, K // 32)), rs)
+
+
+@pytest.mark.parametrize("rows,n", [(5184, 1024), (77, 96), (33, 4096)])
+def test_layer_norm_bit_exact(ctx, rows, n):
+    rng = np.random.default_rng(rows + n)
+    x = (rng.standard_normal((rows, n)) * rng.uniform(0.01, 20, (rows, 1)) + rng.normal(0, 3, (rows, 1))).astype(np.float32)
+    w = (1 + rng.normal(0, 0.1, n)).astype(np.float32)
+    b = rng.normal(0, 0.1, n).astype(np.float32)
+    ref = orc.layer_norm(x, 1e-5, w, b)
+    xd, wd, bd = ctx.to_device(x), ctx.to_device(w), ctx.to_device(b)
+    ctx.layer_norm(xd, rows, n, 1e-5, wd, bd, xd)  # in place, as the encoder uses it
+    ctx.sync()
+    got = xd.download(np.float32, (rows, n))
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"{np.sum(got != ref)} values differ"
+
+
+SHAPES = [(64, 128, 128), (100, 96, 64), (37, 256, 4736), (5184, 4736, 1024), (5184, 1024, 4736),
+          (64, 4736, 1024), (64, 1024, 4736)]
+WTYPES = [orc.Q4_0, orc.Q4_1, orc.Q8_0, orc.F16, orc.F32]
+
+
+@pytest.mark.parametrize("wt", WTYPES, ids=lambda t: {0: "f32", 1: "f16", 2: "q4_0", 3: "q4_1", 8: "q8_0"}[t])
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_mul_mat(ctx, wt, M, N, K):
+    rng = np.random.default_rng(M * 7 + N * 3 + K + wt)
+    W = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    bias = rng.normal(0, 0.1, N).astype(np.float32)
+    wb = orc.to_weight_bytes(wt, W)
+    ref = orc.mul_mat(wt, wb, N, K, X) + bias
+    w = ctx.weight(wt, K, N, wb)
+    Xd, bd, Yd = ctx.to_device(X), ctx.to_device(bias), ctx.buffer(M * N * 4)
+    ctx.mul_mat(w, Xd, M, Yd, bd)
+    ctx.sync()
+    Y = Yd.download(np.float32, (M, N))
+    err = orc.rel_l2(Y, ref)
+    print(f"mul_mat type={wt} M={M} N={N} K={K}: rel_l2={err:.3e} max_abs={orc.max_abs(Y, ref):.3e}")
+    assert err <= 1e-5
+
+
+@pytest.mark.parametrize("prec", [0, 1], ids=["fp16", "f32"])
+@pytest.mark.parametrize("B,nh,N", [(1, 2, 64), (2, 3, 100), (9, 16, 576), (1, 2, 5184)])
+def test_flash_attn(ctx, B, nh, N, prec):
+    rng = np.random.default_rng(B * 100 + nh * 10 + N)
+    q = rng.standard_normal((B, nh, N, 64)).astype(np.float32)
+    k = rng.standard_normal((B, nh, N, 64)).astype(np.float32)
+    # V laid out [B][N][nh][64] and read through strides, like the strided V
+    # view of sam3.cpp:3762-3763
+    v_tok = rng.standard_normal((B, N, nh, 64)).astype(np.float32)
+    v = np.ascontiguousarray(v_tok.transpose(0, 2, 1, 3))
+    scale = 1.0 / 8.0
+    ref = orc.flash_attn(q, k, v, scale)
+    qd, kd, vd = ctx.to_device(q), ctx.to_device(k), ctx.to_device(v_tok)
+    od = ctx.buffer(B * N * nh * 64 * 4)
+    qk_nb = (1, 64, N * 64, nh * N * 64)
+    v_nb = (1, nh * 64, 64, N * nh * 64)
+    ctx.flash_attn_ext(qd, qk_nb, kd, qk_nb, vd, v_nb, 64, N, N, nh, B, scale, od, prec=prec)
+    ctx.sync()
+    out = od.download(np.float32, (B, N, nh, 64))
+    err = orc.rel_l2(out, ref)
+    print(f"flash_attn prec={prec} B={B} nh={nh} N={N}: rel_l2={err:.3e} max_abs={orc.max_abs(out, ref):.3e}")
+    # fp16 operands: the F16 tolerance; split fp16 pairs: f32 attention up to
+    # accumulation order and exp2 vs expf rounding
+    assert err <= (2e-3 if prec == 0 else 1e-5)
