@@ -1,0 +1,306 @@
+#!/usr/bin/env python3
+"""Benchmark: SAM 3 ViT image encoder (backbone) on one MI355X.
+
+Workload: the SAM 3 visual backbone at 1008×1008 (72×72 tokens, 32 blocks,
+width 1024, 16 heads, MLP 4736, 24×24 windows, global blocks 7/15/23/31),
+random-init weights N(0, 0.02) quantized to Q4_0 (default; --ftype selects
+q8_0, q4_1, f16, f32), one synthetic uniform-uint8 image preprocessed as
+sam3.cpp does.  A step is one full encode of that image with the input
+already resident in HBM; value = ms per frame (lower is better).
+
+Also reported, on the same JSON line:
+  roofline      — the dominant kernel (the fc1 GEMM, M=5184 N=4736 K=1024,
+                  the largest of the four per-block GEMMs) timed alone with
+                  HIP events on the engine's stream: algorithmic ops 2·M·N·K
+                  per launch ÷ average launch time, against the MI355X dense
+                  int8 MFMA peak (fp16 for F16 weights, fp32 for F32).
+                  `traffic` comes from the committed rocprofv3 FETCH_SIZE /
+                  WRITE_SIZE counter summary when present.
+  cpu_baseline  — the CPU oracle (a C restatement of ggml's CPU path, not
+                  the upstream binary) on this host: one whole frame of the
+                  same model and image (about 10 s on 16 host threads).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "sam3.cpp_amd"))
+
+METRIC = "image-encoder ms/frame (SAM3 ViT 1008², q4_0/q8_0/f16) + % MFMA/HBM peak"
+PEAK_TOPS = {"q4_0": 5000.0, "q4_1": 5000.0, "q8_0": 5000.0, "f16": 2500.0, "f32": 157.3}
+CFG = dict(img_size=1008, patch=14, embed_dim=1024, depth=32, heads=16, mlp_ratio_x1000=4625, window=24,
+           global_idx=(7, 15, 23, 31))
+GEMM_KERNEL = "k_gemm"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def synthetic_image(size: int, seed: int = 0) -> np.ndarray:
+    rng = np.random.default_rng(seed)
+    return rng.integers(0, 256, (size, size, 3), dtype=np.uint8)
+
+
+def preprocess(img: np.ndarray) -> np.ndarray:
+    """sam3_preprocess_image for an image already at img_size (sam3.cpp:3486-3514):
+    (v/255 − 0.5)/0.5 in float32, HWC → CHW."""
+    v = img.astype(np.float32) / np.float32(255.0)
+    v = (v - np.float32(0.5)) / np.float32(0.5)
+    return np.ascontiguousarray(v.transpose(2, 0, 1))
+
+
+def read_traffic(path: str):
+    """Bytes per launch from a counter summary line 'traffic_bytes_per_launch: N'."""
+    try:
+        with open(path) as f:
+            for line in f:
+                m = re.match(r"\s*traffic_bytes_per_launch:\s*([0-9.eE+]+)", line)
+                if m:
+                    return float(m.group(1))
+    except OSError:
+        pass
+    return None
+
+
+def gemm_roofline(s3e, ctx, ev, ftype: str, reps: int):
+    """Time the fc1 GEMM kernel alone (s3e_mul_mat_q on pre-converted activations)."""
+    M, N, K = 5184, 4736, 1024
+    rng = np.random.default_rng(1)
+    tmap = {"q4_0": s3e.TYPE_Q4_0, "q4_1": s3e.TYPE_Q4_1, "q8_0": s3e.TYPE_Q8_0, "f16": s3e.TYPE_F16,
+            "f32": s3e.TYPE_F32}
+    wt = tmap[ftype]
+    w = ctx.weight(wt, K, N, _random_ggml_bytes(wt, N, K, rng))
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    Xd = ctx.to_device(X)
+    Y = ctx.buffer(M * N * 4)
+    if wt in (s3e.TYPE_Q4_0, s3e.TYPE_Q8_0, s3e.TYPE_Q4_1):
+        vdt = s3e.TYPE_Q8_1 if wt == s3e.TYPE_Q4_1 else s3e.TYPE_Q8_0
+        qs, d, s = ctx.buffer(M * K), ctx.buffer(M * K // 32 * 2), ctx.buffer(M * K // 32 * 2)
+        ctx.quantize_rows(vdt, Xd, M, K, qs, d, s)
+        args = (qs, d, s)
+    elif wt == s3e.TYPE_F16:
+        qs = ctx.buffer(M * K * 2)
+        ctx.quantize_rows(s3e.TYPE_F16, Xd, M, K, qs, None, None)
+        args = (qs, None, None)
+    else:
+        args = (Xd, None, None)
+    for _ in range(3):
+        ctx.mul_mat_q(w, *args, M, Y)
+    ctx.sync()
+    e0, e1 = ev.create(), ev.create()
+    ev.record(e0, ctx.stream)
+    for _ in range(reps):
+        ctx.mul_mat_q(w, *args, M, Y)
+    ev.record(e1, ctx.stream)
+    ms = ev.elapsed_ms(e0, e1) / reps
+    ctx.sync()
+    ops = 2.0 * M * N * K
+    tops = ops / (ms * 1e-3) / 1e12
+    return ms, tops, ops
+
+
+def _random_ggml_bytes(wt: int, N: int, K: int, rng) -> np.ndarray:
+    """Valid ggml bytes for an N×K weight of type wt with random contents
+    (timing only): random quant bytes, fp16 scales 0.002, Q4_1 minima −0.015."""
+    if wt == 0:
+        return rng.normal(0, 0.02, (N, K)).astype(np.float32).view(np.uint8).ravel()
+    if wt == 1:
+        return rng.normal(0, 0.02, (N, K)).astype(np.float16).view(np.uint8).ravel()
+    bs = {2: 18, 3: 20, 8: 34}[wt]
+    out = rng.integers(0, 256, (N, K // 32, bs), dtype=np.uint8)
+    out[:, :, 0:2] = np.full((N, K // 32), 0.002, np.float16).view(np.uint8).reshape(N, K // 32, 2)
+    if wt == 3:
+        out[:, :, 2:4] = np.full((N, K // 32), -0.015, np.float16).view(np.uint8).reshape(N, K // 32, 2)
+    return out.ravel()
+
+
+def cpu_baseline(path: str, img: np.ndarray, threads: int):
+    """Oracle on the host: one whole frame (prefix + 32 blocks) of the same
+    model and image, after the host preprocessing."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as orc
+
+    om = orc.OracleModel(path)
+    chw = orc.preprocess_sam3(img, om.img)
+    t0 = time.perf_counter()
+    om.encode(chw, threads)
+    return (time.perf_counter() - t0) * 1e3
+
+
+def _short_kernel(name: str) -> str:
+    m = re.search(r"(k_\w+(<[^>]*>)?)", name)
+    return m.group(1) if m else name.split("(")[0][:60]
+
+
+def summarize_stats(stats_csv: str, frames: int) -> str:
+    """Per-kernel table from a rocprofv3 --stats kernel_stats.csv."""
+    import csv
+
+    rows = list(csv.DictReader(open(stats_csv)))
+    lines = [f"{'kernel':28s} {'calls':>7s} {'avg_us':>9s} {'ms/frame':>9s} {'share':>7s}"]
+    for r in rows:
+        tot = float(r["TotalDurationNs"]) / 1e6
+        lines.append(f"{_short_kernel(r['Name']):28s} {int(r['Calls']):7d} {float(r['AverageNs']) / 1e3:9.1f} "
+                     f"{tot / frames:9.3f} {float(r['Percentage']):6.2f}%")
+    return "\n".join(lines)
+
+
+def summarize_counters(fetch_csv: str, write_csv: str, cfetch_csv: str, cwrite_csv: str, copy_bytes: int,
+                       kernel: str) -> str:
+    """HBM bytes per launch of `kernel` from FETCH_SIZE / WRITE_SIZE (KiB per
+    dispatch), each scaled by what the same counter reads for the copy kernel
+    of known size."""
+    import csv
+    import statistics
+
+    def med(path, name):
+        vals = [float(r["Counter_Value"]) for r in csv.DictReader(open(path)) if _short_kernel(r["Kernel_Name"]) == name]
+        return statistics.median(vals), len(vals)
+
+    f, nf = med(fetch_csv, kernel)
+    w, nw = med(write_csv, kernel)
+    cf, _ = med(cfetch_csv, "k_copy")
+    cw, _ = med(cwrite_csv, "k_copy")
+    sf = copy_bytes / (cf * 1024.0)
+    sw = copy_bytes / (cw * 1024.0)
+    traffic = f * 1024.0 * sf + w * 1024.0 * sw
+    return "\n".join([
+        f"kernel: {kernel} ({nf} / {nw} dispatches)",
+        f"FETCH_SIZE median: {f:.1f} KiB/dispatch  x fetch scale {sf:.3f}  = {f * 1024 * sf / 1e6:.2f} MB",
+        f"WRITE_SIZE median: {w:.1f} KiB/dispatch  x write scale {sw:.3f}  = {w * 1024 * sw / 1e6:.2f} MB",
+        f"copy calibration: k_copy of {copy_bytes} bytes reads FETCH_SIZE {cf:.1f} KiB, WRITE_SIZE {cw:.1f} KiB",
+        f"traffic_bytes_per_launch: {traffic:.0f}",
+    ])
+
+
+def main() -> int:
+    if len(sys.argv) > 1 and sys.argv[1] == "--summarize-stats":
+        print(summarize_stats(sys.argv[2], int(sys.argv[3])))
+        return 0
+    if len(sys.argv) > 1 and sys.argv[1] == "--summarize-counters":
+        a = sys.argv[2:]
+        print(summarize_counters(a[0], a[1], a[2], a[3], int(a[4]), a[5]))
+        return 0
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--ftype", default="q4_0", choices=sorted(PEAK_TOPS))
+    ap.add_argument("--gemm-reps", type=int, default=50)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "gemm_fc1_q4_0_counters.txt"))
+    ap.add_argument("--only", choices=["encode", "gemm", "copy"], default=None,
+                    help="run one leg only (for profiling runs)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (every run here uses one "
+              f"MI355X; the path shards by frame, see DESIGN.md)", file=sys.stderr)
+        return 2
+    import s3e
+
+    ctx = s3e.Context(0)
+    ev = s3e.HipEvents()
+    out = {}
+
+    if args.only == "copy":
+        nbytes = 1 << 30
+        a, b = ctx.buffer(nbytes), ctx.buffer(nbytes)
+        for _ in range(5):
+            ctx.copy(b, a, nbytes)
+        ctx.sync()
+        e0, e1 = ev.create(), ev.create()
+        ev.record(e0, ctx.stream)
+        for _ in range(10):
+            ctx.copy(b, a, nbytes)
+        ev.record(e1, ctx.stream)
+        ms = ev.elapsed_ms(e0, e1) / 10
+        log(f"copy 1 GiB: {ms:.3f} ms = {2 * nbytes / ms / 1e6:.1f} GB/s (read+write)")
+        return 0
+
+    if args.only in (None, "gemm"):
+        ms, tops, ops = gemm_roofline(s3e, ctx, ev, args.ftype, args.gemm_reps)
+        log(f"fc1 GEMM {args.ftype}: {ms * 1e3:.1f} us/launch, {tops:.1f} TOPS")
+        out["gemm"] = (ms, tops, ops)
+        if args.only == "gemm":
+            return 0
+
+    tmpdir = os.environ.get("TMPDIR", tempfile.gettempdir())
+    path = os.path.join(tmpdir, f"s3e_bench_sam3_vit_{args.ftype}.ggml")
+    t = time.time()
+    s3e.synth_write(path, ftype=args.ftype, seed=0, std=0.02, **CFG)
+    log(f"synthetic model written in {time.time() - t:.1f}s: {path} ({os.path.getsize(path) / 1e6:.1f} MB)")
+    model = s3e.Model(ctx, path)
+    st = s3e.State(ctx, model)
+    img = synthetic_image(CFG["img_size"])
+    chw_d = ctx.to_device(preprocess(img))
+    for _ in range(args.warmup):
+        st.encode_chw(chw_d)
+    ctx.sync()
+    e0, e1 = ev.create(), ev.create()
+    ctx.sync()
+    ev.record(e0, ctx.stream)
+    for _ in range(args.steps):
+        st.encode_chw(chw_d)
+    ev.record(e1, ctx.stream)
+    total_ms = ev.elapsed_ms(e0, e1)
+    ctx.sync()
+    ms_frame = total_ms / args.steps
+    log(f"encode: {ms_frame:.3f} ms/frame over {args.steps} steps")
+    if args.only == "encode":
+        return 0
+
+    gms, gtops, gops = out["gemm"]
+    peak = PEAK_TOPS[args.ftype]
+    traffic = read_traffic(args.traffic) if args.ftype == "q4_0" else None
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = args.cpu_threads or min(16, len(os.sched_getaffinity(0)))
+        cms = cpu_baseline(path, img, threads)
+        log(f"cpu baseline: {cms / 1e3:.1f} s/frame, {threads} threads")
+        cpu = {"value": round(cms, 1), "unit": "ms/frame", "cores": threads, "kind": "port",
+               "sample": "one full frame (prefix + 32 blocks) of the same Q4_0 model and image on the CPU "
+                         "oracle, a C restatement of ggml's CPU path (AVX2, OpenMP), not the upstream binary"}
+    try:
+        os.remove(path)
+    except OSError:
+        pass
+    line = {
+        "metric": METRIC,
+        "value": round(ms_frame, 3),
+        "unit": "ms/frame",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_frame, 3),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {"q4_0": "int8", "q4_1": "int8", "q8_0": "int8", "f16": "f16", "f32": "f32"}[args.ftype],
+        "data": "synthetic: random-init weights N(0,0.02), uniform uint8 1008x1008 image, seed 0",
+        "config": {"workload": f"SAM 3 ViT image encoder backbone, 1008x1008 (72x72 tokens), 32 blocks, "
+                               f"{args.ftype.upper()} weights, batch 1",
+                   "img_size": 1008, "weights": args.ftype, "blocks": 32, "window": 24,
+                   "global_blocks": [7, 15, 23, 31]},
+        "roofline": {"kernel": f"{GEMM_KERNEL} fc1 M=5184 N=4736 K=1024 ({args.ftype})", "bound": "mfma",
+                     "achieved": round(gtops, 1), "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(gtops / peak, 4), "traffic": traffic,
+                     "us_per_launch": round(gms * 1e3, 2), "ops_per_launch": gops},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

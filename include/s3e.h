@@ -76,6 +76,9 @@ int s3e_malloc(s3e_ctx *ctx, size_t bytes, void **out);
 int s3e_free(s3e_ctx *ctx, void *ptr);
 int s3e_memcpy_h2d(s3e_ctx *ctx, void *dst, const void *src, size_t bytes);
 int s3e_memcpy_d2h(s3e_ctx *ctx, void *dst, const void *src, size_t bytes);
+/* Device-to-device copy by a plain streaming kernel on the context stream
+ * (bytes a multiple of 16, pointers 16-byte aligned).  Asynchronous. */
+int s3e_copy(s3e_ctx *ctx, void *dst, const void *src, size_t bytes);
 
 /* ---- ggml_mul_mat --------------------------------------------------------
  * Upload one weight matrix given as ggml bytes: ne0 = K (the contiguous
@@ -97,6 +100,13 @@ int s3e_weight_info(const s3e_weight *w, int64_t out[4]);
  * 3792-3796. */
 int s3e_mul_mat(s3e_ctx *ctx, const s3e_weight *w, const float *X, int64_t M,
                 const float *bias, float *Y);
+
+/* Same GEMM with X already in W's vec_dot type (ggml_mul_mat with src1 of
+ * that type; ggml skips the conversion then): `xq`, `d`, `s` as written by
+ * s3e_quantize_rows for K = W's ne0.  Launches the GEMM kernel only, with no
+ * allocation, so it is also the entry point to time the kernel alone. */
+int s3e_mul_mat_q(s3e_ctx *ctx, const s3e_weight *w, const void *xq, const uint16_t *d,
+                  const uint16_t *s, int64_t M, const float *bias, float *Y);
 
 /* Convert M rows of K f32 (device) into a vec_dot type, as ggml's
  * from_float does for src1 of ggml_mul_mat: `type` is Q8_0, Q8_1 or F16.

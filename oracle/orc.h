@@ -40,6 +40,7 @@ enum {
 /* ---- scalar conversions ------------------------------------------------ */
 uint16_t orc_fp32_to_fp16(float f);            /* round to nearest even */
 float    orc_fp16_to_fp32(uint16_t h);
+float    orc_fp16_to_fp32_soft(uint16_t h);
 void     orc_fp32_to_fp16_row(const float *x, uint16_t *y, int64_t n);
 void     orc_fp16_to_fp32_row(const uint16_t *x, float *y, int64_t n);
 

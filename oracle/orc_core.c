@@ -80,7 +80,8 @@ uint16_t orc_fp32_to_fp16(float f) {
     return (uint16_t)(sign | h);
 }
 
-float orc_fp16_to_fp32(uint16_t h) {
+/* Software fp16 → fp32 (exact); the tests compare it with F16C and numpy. */
+float orc_fp16_to_fp32_soft(uint16_t h) {
     const uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
     const uint32_t e = (h >> 10) & 0x1fu;
     const uint32_t m = h & 0x3ffu;
@@ -102,6 +103,10 @@ float orc_fp16_to_fp32(uint16_t h) {
     memcpy(&f, &x, 4);
     return f;
 }
+
+/* fp16 → fp32 is exact, so the F16C instruction gives the same value as the
+ * software conversion above; it is used in the dot-product hot loops. */
+float orc_fp16_to_fp32(uint16_t h) { return _cvtsh_ss(h); }
 
 void orc_fp32_to_fp16_row(const float *x, uint16_t *y, int64_t n) {
     for (int64_t i = 0; i < n; ++i) y[i] = orc_fp32_to_fp16(x[i]);
@@ -551,6 +556,68 @@ void orc_block_isums(int wtype, int64_t n, const void *w, const void *x, int32_t
  * to the vec_dot type of src0, then each output element is one vec_dot of a
  * src0 row with a converted src1 row.  Called from the ViT block at
  * sam3.cpp:3738, 3779, 3792, 3795. */
+/* 4×4 block of q4_0/q8_0/q4_1 dot products evaluated together: every one of
+ * the 16 dots keeps exactly the per-dot order of the vec_dot kernels above
+ * (one 8-lane accumulator, one FMA per block, hsum at the end), so results
+ * are bit-identical to 16 separate vec_dot calls; loading each block once
+ * for 4 dots only saves time. */
+static void dot4x4_q(int wtype, int64_t K, const char *W, size_t wrs, const char *X, size_t xrs, float *Y,
+                     int64_t ldy) {
+    const int64_t nb = K / QK;
+    __m256 acc[4][4];
+    float summs[4][4];
+    for (int i = 0; i < 4; i++)
+        for (int j = 0; j < 4; j++) { acc[i][j] = _mm256_setzero_ps(); summs[i][j] = 0.0f; }
+    for (int64_t b = 0; b < nb; b++) {
+        __m256i qw[4], qx[4];
+        float dw[4], dx[4], mw[4] = {0, 0, 0, 0}, sx[4] = {0, 0, 0, 0};
+        for (int j = 0; j < 4; j++) {
+            const char *wr = W + (size_t)j * wrs;
+            if (wtype == ORC_TYPE_Q4_0) {
+                const blk_q4_0 *wb = (const blk_q4_0 *)wr + b;
+                dw[j] = orc_fp16_to_fp32(wb->d);
+                qw[j] = _mm256_sub_epi8(bytes_from_nibbles_32(wb->qs), _mm256_set1_epi8(8));
+            } else if (wtype == ORC_TYPE_Q4_1) {
+                const blk_q4_1 *wb = (const blk_q4_1 *)wr + b;
+                dw[j] = orc_fp16_to_fp32(wb->d);
+                mw[j] = orc_fp16_to_fp32(wb->m);
+                qw[j] = bytes_from_nibbles_32(wb->qs);
+            } else {
+                const blk_q8_0 *wb = (const blk_q8_0 *)wr + b;
+                dw[j] = orc_fp16_to_fp32(wb->d);
+                qw[j] = _mm256_loadu_si256((const __m256i *)wb->qs);
+            }
+        }
+        for (int i = 0; i < 4; i++) {
+            const char *xr = X + (size_t)i * xrs;
+            if (wtype == ORC_TYPE_Q4_1) {
+                const blk_q8_1 *xb = (const blk_q8_1 *)xr + b;
+                dx[i] = orc_fp16_to_fp32(xb->d);
+                sx[i] = orc_fp16_to_fp32(xb->s);
+                qx[i] = _mm256_loadu_si256((const __m256i *)xb->qs);
+            } else {
+                const blk_q8_0 *xb = (const blk_q8_0 *)xr + b;
+                dx[i] = orc_fp16_to_fp32(xb->d);
+                qx[i] = _mm256_loadu_si256((const __m256i *)xb->qs);
+            }
+        }
+        for (int i = 0; i < 4; i++)
+            for (int j = 0; j < 4; j++) {
+                if (wtype == ORC_TYPE_Q4_1) {
+                    summs[i][j] = fmaf(mw[j], sx[i], summs[i][j]);
+                    const __m256 d = _mm256_mul_ps(_mm256_set1_ps(dw[j]), _mm256_set1_ps(dx[i]));
+                    acc[i][j] = _mm256_fmadd_ps(d, mul_sum_us8_pairs_float(qw[j], qx[i]), acc[i][j]);
+                } else {
+                    const __m256 d = _mm256_set1_ps(dw[j] * dx[i]);
+                    acc[i][j] = _mm256_fmadd_ps(d, mul_sum_i8_pairs_float(qw[j], qx[i]), acc[i][j]);
+                }
+            }
+    }
+    for (int i = 0; i < 4; i++)
+        for (int j = 0; j < 4; j++)
+            Y[i * ldy + j] = wtype == ORC_TYPE_Q4_1 ? hsum_float_8(acc[i][j]) + summs[i][j] : hsum_float_8(acc[i][j]);
+}
+
 void orc_mul_mat_preq(int wtype, const void *W, int64_t N, int64_t K,
                       const void *Xq, int64_t M, float *Y, int nthreads) {
     const int vdt = orc_vec_dot_type(wtype);
@@ -558,13 +625,29 @@ void orc_mul_mat_preq(int wtype, const void *W, int64_t N, int64_t K,
     const size_t xrs = orc_row_size(vdt, K);
     const int64_t TM = 32, TN = 32;
     const int64_t tiles_m = (M + TM - 1) / TM, tiles_n = (N + TN - 1) / TN;
+    const int blocked = g_variant == 0 &&
+                        (wtype == ORC_TYPE_Q4_0 || wtype == ORC_TYPE_Q8_0 || wtype == ORC_TYPE_Q4_1);
     if (nthreads <= 0) nthreads = omp_get_max_threads();
 #pragma omp parallel for schedule(dynamic, 1) num_threads(nthreads)
     for (int64_t t = 0; t < tiles_m * tiles_n; t++) {
         const int64_t m0 = (t / tiles_n) * TM, n0 = (t % tiles_n) * TN;
         const int64_t m1 = m0 + TM < M ? m0 + TM : M;
         const int64_t n1 = n0 + TN < N ? n0 + TN : N;
-        for (int64_t m = m0; m < m1; m++) {
+        int64_t m = m0;
+        if (blocked) {
+            for (; m + 4 <= m1; m += 4) {
+                int64_t n = n0;
+                for (; n + 4 <= n1; n += 4) {
+                    dot4x4_q(wtype, K, (const char *)W + (size_t)n * wrs, wrs, (const char *)Xq + (size_t)m * xrs,
+                             xrs, Y + m * N + n, N);
+                }
+                for (int64_t mm = m; mm < m + 4; mm++)
+                    for (int64_t nn = n; nn < n1; nn++)
+                        Y[mm * N + nn] = orc_vec_dot(wtype, K, (const char *)W + (size_t)nn * wrs,
+                                                     (const char *)Xq + (size_t)mm * xrs);
+            }
+        }
+        for (; m < m1; m++) {
             const char *xr = (const char *)Xq + (size_t)m * xrs;
             for (int64_t n = n0; n < n1; n++) {
                 Y[m * N + n] = orc_vec_dot(wtype, K, (const char *)W + (size_t)n * wrs, xr);

@@ -246,3 +246,23 @@ hipError_t launch_attn_prep(const float *q, const int64_t q_nb[4], const float *
 }
 
 }  // namespace s3e
+
+namespace s3e {
+namespace {
+
+// Streaming 16-byte copy, grid-stride (used to calibrate HBM byte counters).
+__global__ __launch_bounds__(256) void k_copy(uint4 *__restrict__ dst, const uint4 *__restrict__ src, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        dst[i] = src[i];
+}
+
+}  // namespace
+
+hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t st) {
+    const int64_t n = (int64_t)(bytes / 16);
+    const int64_t blocks = n / 256 + 1 < 8192 ? n / 256 + 1 : 8192;
+    hipLaunchKernelGGL(k_copy, dim3((unsigned)blocks), dim3(256), 0, st, (uint4 *)dst, (const uint4 *)src, n);
+    return hipGetLastError();
+}
+
+}  // namespace s3e

@@ -119,6 +119,7 @@ hipError_t launch_attn_prep(const float *q, const int64_t q_nb[4], const float *
                             _Float16 *vt_lo, int64_t ldv, hipStream_t st);
 hipError_t launch_im2col(const float *chw, int img, int P, int64_t ldk, AKind kind, void *out,
                          hipStream_t st);
+hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t st);
 
 // fp32 → fp16 of a value computed in fp32.  The empty asm statement (it emits
 // no instruction) pins the fp32 value in a VGPR: without it LLVM folds

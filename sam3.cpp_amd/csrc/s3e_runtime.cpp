@@ -255,6 +255,17 @@ extern "C" int s3e_memcpy_h2d(s3e_ctx *ctx, void *dst, const void *src, size_t b
     return S3E_OK;
 }
 
+extern "C" int s3e_copy(s3e_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    if (!ctx || !dst || !src) { set_error("s3e_copy: NULL argument"); return S3E_ERR_INVALID; }
+    if (bytes % 16 != 0 || ((uintptr_t)dst | (uintptr_t)src) % 16 != 0) {
+        set_error("s3e_copy: size and pointers must be 16-byte multiples");
+        return S3E_ERR_INVALID;
+    }
+    HIP_TRY(hipSetDevice(ctx->device));
+    HIP_TRY(launch_copy(dst, src, bytes, ctx->stream));
+    return S3E_OK;
+}
+
 extern "C" int s3e_memcpy_d2h(s3e_ctx *ctx, void *dst, const void *src, size_t bytes) {
     if (!ctx) { set_error("s3e_memcpy_d2h: NULL context"); return S3E_ERR_INVALID; }
     HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
@@ -345,6 +356,30 @@ extern "C" int s3e_mul_mat(s3e_ctx *ctx, const s3e_weight *w, const float *X, in
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     buf.release();
     if (e != hipSuccess) { set_error("s3e_mul_mat: %s", hipGetErrorString(e)); return S3E_ERR_HIP; }
+    return S3E_OK;
+}
+
+extern "C" int s3e_mul_mat_q(s3e_ctx *ctx, const s3e_weight *w, const void *xq, const uint16_t *d,
+                             const uint16_t *s, int64_t M, const float *bias, float *Y) {
+    if (!ctx || !w || !xq || !Y) { set_error("s3e_mul_mat_q: NULL argument"); return S3E_ERR_INVALID; }
+    const Weight &W = w->w;
+    const AKind ak = act_kind_for(W.kind);
+    if ((ak == A_Q8_0 || ak == A_Q8_1) && !d) { set_error("s3e_mul_mat_q: missing scales"); return S3E_ERR_INVALID; }
+    if (ak == A_Q8_1 && !s) { set_error("s3e_mul_mat_q: missing block sums"); return S3E_ERR_INVALID; }
+    if (W.K % 32 != 0 || M < 0) { set_error("s3e_mul_mat_q: K=%lld must be a multiple of 32", (long long)W.K); return S3E_ERR_UNSUPPORTED; }
+    if (M == 0) return S3E_OK;
+    HIP_TRY(hipSetDevice(ctx->device));
+    Act a;
+    a.kind = ak;
+    a.x = (void *)xq;
+    a.d = (uint16_t *)d;
+    a.s = (uint16_t *)s;
+    a.ld = W.K;
+    EpiArgs ea;
+    ea.bias = bias;
+    ea.y = Y;
+    ea.ldy = W.N;
+    HIP_TRY(launch_gemm(W, a, M, EPI_F32, ea, ctx->stream));
     return S3E_OK;
 }
 

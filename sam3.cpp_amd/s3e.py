@@ -56,6 +56,8 @@ def _load() -> ctypes.CDLL:
         "s3e_mul_mat": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
         "s3e_quantize_rows": (c_int, [c_void_p, c_int, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
         "s3e_layer_norm": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_float, c_void_p, c_void_p, c_void_p]),
+        "s3e_mul_mat_q": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
+        "s3e_copy": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t]),
         "s3e_flash_attn_ext": (c_int, [c_void_p, c_void_p, P64, c_void_p, P64, c_void_p, P64,
                                        c_int64, c_int64, c_int64, c_int64, c_int64, c_float, c_int, c_void_p]),
         "s3e_model_load": (c_int, [c_void_p, c_char_p, POINTER(c_void_p)]),
@@ -84,7 +86,8 @@ LIB = _load()
 DECLARED = [
     "s3e_last_error", "s3e_abi_version", "s3e_ctx_create", "s3e_ctx_destroy", "s3e_ctx_sync", "s3e_ctx_stream",
     "s3e_malloc", "s3e_free", "s3e_memcpy_h2d", "s3e_memcpy_d2h", "s3e_weight_upload", "s3e_weight_free",
-    "s3e_weight_info", "s3e_mul_mat", "s3e_quantize_rows", "s3e_layer_norm", "s3e_flash_attn_ext", "s3e_model_load",
+    "s3e_weight_info", "s3e_mul_mat", "s3e_mul_mat_q", "s3e_quantize_rows", "s3e_layer_norm", "s3e_copy",
+    "s3e_flash_attn_ext", "s3e_model_load",
     "s3e_model_free", "s3e_model_hparams", "s3e_state_create", "s3e_state_free", "s3e_encode_chw",
     "s3e_encode_chw_host", "s3e_encode_image_u8", "s3e_vit_prefix", "s3e_vit_block", "s3e_state_tensor_info",
     "s3e_state_tensor_get", "s3e_state_tensor_device", "s3e_synth_write",
@@ -210,6 +213,14 @@ class Context:
                       d: DeviceBuffer | None, s: DeviceBuffer | None):
         check(LIB.s3e_quantize_rows(self.handle, vdt, X.ptr, M, K, qs.ptr, d.ptr if d else None,
                                     s.ptr if s else None), "s3e_quantize_rows")
+
+    def mul_mat_q(self, w: Weight, xq: DeviceBuffer, d: DeviceBuffer | None, s: DeviceBuffer | None, M: int,
+                  Y: DeviceBuffer, bias: DeviceBuffer | None = None):
+        check(LIB.s3e_mul_mat_q(self.handle, w.handle, xq.ptr, d.ptr if d else None, s.ptr if s else None, M,
+                                bias.ptr if bias else None, Y.ptr), "s3e_mul_mat_q")
+
+    def copy(self, dst: DeviceBuffer, src: DeviceBuffer, nbytes: int):
+        check(LIB.s3e_copy(self.handle, dst.ptr, src.ptr, nbytes), "s3e_copy")
 
     def layer_norm(self, x: DeviceBuffer, rows: int, n: int, eps: float, w: DeviceBuffer | None,
                    b: DeviceBuffer | None, y: DeviceBuffer):
