@@ -30,6 +30,8 @@ def _load():
     sig = {
         "orc_fp32_to_fp16": (ctypes.c_uint16, [c_float]),
         "orc_fp16_to_fp32": (c_float, [ctypes.c_uint16]),
+        "orc_fp16_to_fp32_soft": (c_float, [ctypes.c_uint16]),
+        "orc_set_variant": (None, [c_int]),
         "orc_fp32_to_fp16_row": (None, [P, P, c_int64]),
         "orc_fp16_to_fp32_row": (None, [P, P, c_int64]),
         "orc_row_size": (c_size_t, [c_int, c_int64]),
