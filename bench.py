@@ -85,7 +85,8 @@ def gemm_roofline(s3e, ctx, ev, ftype: str, reps: int):
     Y = ctx.buffer(M * N * 4)
     if wt in (s3e.TYPE_Q4_0, s3e.TYPE_Q8_0, s3e.TYPE_Q4_1):
         vdt = s3e.TYPE_Q8_1 if wt == s3e.TYPE_Q4_1 else s3e.TYPE_Q8_0
-        qs, d, s = ctx.buffer(M * K), ctx.buffer(M * K // 32 * 2), ctx.buffer(M * K // 32 * 2)
+        ns = s3e.act_scale_elems(M, K)
+        qs, d, s = ctx.buffer(M * K), ctx.buffer(ns * 2), ctx.buffer(ns * 2)
         ctx.quantize_rows(vdt, Xd, M, K, qs, d, s)
         args = (qs, d, s)
     elif wt == s3e.TYPE_F16:

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define S3E_ABI_VERSION 1
+#define S3E_ABI_VERSION 2
 
 enum s3e_status {
     S3E_OK = 0,
@@ -103,16 +103,22 @@ int s3e_mul_mat(s3e_ctx *ctx, const s3e_weight *w, const float *X, int64_t M,
 
 /* Same GEMM with X already in W's vec_dot type (ggml_mul_mat with src1 of
  * that type; ggml skips the conversion then): `xq`, `d`, `s` as written by
- * s3e_quantize_rows for K = W's ne0.  Launches the GEMM kernel only, with no
- * allocation, so it is also the entry point to time the kernel alone. */
+ * s3e_quantize_rows for K = W's ne0 (layout there).  Launches the GEMM kernel
+ * only, with no allocation, so it is also the entry point to time the kernel
+ * alone. */
 int s3e_mul_mat_q(s3e_ctx *ctx, const s3e_weight *w, const void *xq, const uint16_t *d,
                   const uint16_t *s, int64_t M, const float *bias, float *Y);
 
 /* Convert M rows of K f32 (device) into a vec_dot type, as ggml's
  * from_float does for src1 of ggml_mul_mat: `type` is Q8_0, Q8_1 or F16.
- * For Q8_0/Q8_1 `qs` receives M*K int8 (row-major), `d` receives M*K/32
- * fp16 scales and, for Q8_1, `s` receives M*K/32 fp16 sums (d·Σq).  For F16
- * `qs` receives M*K fp16 and d, s are unused.  All device pointers. */
+ * F16: `qs` receives M*K fp16, row-major; d and s are unused.
+ * Q8_0/Q8_1: `qs` receives M*K int8 codes, row-major.  `d` receives the fp16
+ * block scales and, for Q8_1, `s` the fp16 block sums fp16(d·Σq), each as a
+ * stage-major plane: with Mp = M rounded up to 128 and G = ceil(K/128),
+ * block b of row r is element ((b/4)·Mp + r)·4 + b%4 of a plane of G·Mp·4
+ * fp16 values (blocks of one row come in groups of 4, and each group is laid
+ * out for all rows before the next).  Blocks from K/32 to 4G−1 are written as
+ * zero; rows from M to Mp−1 are not written.  All device pointers. */
 int s3e_quantize_rows(s3e_ctx *ctx, int type, const float *X, int64_t M, int64_t K,
                       void *qs, uint16_t *d, uint16_t *s);
 

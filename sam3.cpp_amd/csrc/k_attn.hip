@@ -247,7 +247,7 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a, int ldv) {
 #pragma unroll
                 for (int g = 0; g < 4; g++) *(uint32_t *)(dst + 8 * g) = w[g];
                 if (lh == 0) {
-                    const int64_t blk = orow * (out.ld / QK) + (colbase + dt * 32) / QK;
+                    const int64_t blk = scale_index(out.mp, orow, (colbase + dt * 32) / QK);
                     out.d[blk] = f2h_bits(d);
                     if (out.kind == A_Q8_1) out.s[blk] = f2h_bits(d * (float)sum);
                 }

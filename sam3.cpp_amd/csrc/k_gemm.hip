@@ -6,23 +6,31 @@
 // each 32-element block b the kernel forms the exact integer sum
 //     S_b[m][n] = Σ_{k∈b} qx[m][k]·qw[n][k]
 // with one v_mfma_i32_32x32x32_i8 (K = 32 = one ggml block), the exact fp32
-// block scale c_b[m][n] = dx[m][b]·dw[n][b] (both fp16, so the product is
-// exact) with one v_mfma_f32_32x32x16_f16 whose only non-zero K slot holds
-// the two scales, and accumulates acc += float(S_b)·c_b in fp32.  Q4_1 adds
-// Σ_b m_w[n][b]·s_x[m][b] with one more fp16 MFMA per 4 blocks that
-// accumulates straight into acc.  F16 weights run on fp16 MFMA against
-// activations rounded to fp16; F32 weights run on fp32 MFMA.
+// block scale 2·dx[m][b]·dw[n][b] with one v_mfma_f32_32x32x16_f16 whose
+// operands hold each lane's own scale in its first K slot and zeros elsewhere
+// (both lane halves carry the scale, hence the exact factor 2, removed at the
+// end), and accumulates acc += float(S_b)·c_b in fp32 on the VALU.  Q4_1 adds
+// Σ_b m_w[n][b]·s_x[m][b] with one more fp16 MFMA per 4 blocks into its own
+// accumulator.  F16 weights run on fp16 MFMA against activations rounded to
+// fp16; F32 weights run on fp32 MFMA.
 //
-// Tiling: 256 threads (4 waves as 2×2), 128×128 output tile, each wave 64×64
-// = 2×2 MFMA tiles of 32×32.  K advances in stages of 128 bytes per row
-// (4 quant blocks, 64 fp16 or 32 f32), double-buffered in LDS with a
-// register prefetch of the next stage.  Q4 nibbles are expanded to int8 on
-// the way into LDS.  Work-group ids are remapped so that consecutive tiles
-// land on the same XCD (ids are dealt round-robin over 8 XCDs).
+// Per work-group: 512 threads (8 waves as 2 along M × 4 along N), a BM×128
+// output tile (BM = 128, or 64 when there are too few tiles to fill 256
+// CUs), each wave BM/2 × 32.  K advances in stages of 128 bytes per row (4
+// quant blocks, 64 fp16 or 32 f32).  Stages stream through a 3-deep LDS ring
+// filled by global_load_lds_dwordx4 (no register staging): stage s+2 is in
+// flight while stage s is consumed, and one barrier per stage orders reuse.
+// LDS rows are 128 bytes with 16-byte chunks XOR-swizzled by row (chunk c of
+// row r at slot c ^ (r & 7)), which keeps both the lane-ordered DMA writes
+// and the MFMA operand reads free of bank conflicts without padding.  Scales
+// arrive from stage-major planes, so a stage's scales for the tile are one
+// contiguous run.  Work-group ids are remapped so that each XCD (ids are dealt
+// round-robin over 8) gets a contiguous range of tiles, rastered in groups of
+// 8 tile-rows so that concurrently running tiles share operands in its L2.
 //
-// Epilogues run from an fp32 copy of the tile in LDS, one 32-column chunk
-// per thread, so that 32-wide quant blocks, RoPE pairs and fp16 rows are
-// whole inside one thread.
+// Epilogues run from an fp32 copy of the tile in LDS: 32-column chunks per
+// thread where 32-wide quant blocks, RoPE pairs and fp16 rows must be whole
+// inside one thread, float4 columns per lane for plain f32 stores.
 #include "s3e_internal.h"
 
 namespace s3e {
@@ -30,38 +38,52 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 128, BN = GEMM_BN, NTHR = 256;
-constexpr int ROWB = 128;                        // data bytes per tile row per stage
-constexpr int LROW = 144;                        // LDS row stride in bytes
-constexpr int OFF_A = 0;
-constexpr int OFF_B = BM * LROW;
-constexpr int OFF_AD = OFF_B + BN * LROW;        // fp16 [4][BM] activation scales
-constexpr int OFF_AS = OFF_AD + 4 * BM * 2;      // fp16 [4][BM] activation sums (Q8_1)
-constexpr int OFF_BD = OFF_AS + 4 * BM * 2;      // fp16 [4][BN] weight scales
-constexpr int OFF_BMIN = OFF_BD + 4 * BN * 2;    // fp16 [4][BN] weight minima (Q4_1)
-constexpr int STAGE = OFF_BMIN + 4 * BN * 2;
-constexpr int LDS_BYTES = 2 * STAGE;
-constexpr int CLD = BN + 4;                      // fp32 C-tile row stride
-static_assert(BM * CLD * 4 <= LDS_BYTES, "C tile must fit in the stage buffers");
+#define LDS_PTR(p) ((__attribute__((address_space(3))) void *)(p))
 
-struct GemmParams {
-    const uint8_t *a;
-    const uint16_t *a_d, *a_s;
-    int64_t a_ld_bytes, a_nblk;
-    const uint8_t *b;
-    const uint16_t *b_d, *b_m;
-    int64_t b_ld_bytes, b_nblk;
-    int M, N, K, nstages, tiles_m, tiles_n, ntiles;
-    EpiArgs e;
+constexpr int BN = GEMM_BN;   // 128
+constexpr int NTHR = 512;
+constexpr int ROWB = 128;     // bytes per tile row per stage
+constexpr int NBUF = 3;       // LDS ring depth
+
+template <int WK, int BM_>
+struct Cfg {
+    static constexpr int BM = BM_;
+    static constexpr bool quant = (WK == WK_Q4_0 || WK == WK_Q4_1 || WK == WK_Q8_0);
+    static constexpr bool q41 = (WK == WK_Q4_1);
+    static constexpr int esize = quant ? 1 : (WK == WK_F16 ? 2 : 4);
+    static constexpr int MT = BM / 64;                   // 32-row MFMA tiles per wave
+    static constexpr int OFF_A = 0;
+    static constexpr int OFF_B = BM * ROWB;
+    static constexpr int OFF_SC = OFF_B + BN * ROWB;     // scales: AD | BD | AS | BMIN
+    static constexpr int OFF_AD = OFF_SC;
+    static constexpr int OFF_BD = OFF_AD + (quant ? BM * 8 : 0);
+    static constexpr int OFF_AS = OFF_BD + (quant ? BN * 8 : 0);
+    static constexpr int OFF_BMIN = OFF_AS + (q41 ? BM * 8 : 0);
+    static constexpr int STAGE = OFF_BMIN + (q41 ? BN * 8 : 0);
+    static constexpr int NA = BM / 64;                   // 1 KB A loads per wave per stage
+    static constexpr int NB = BN / 64;                   // 1 KB B loads per wave per stage
+    static constexpr int SC = (STAGE - OFF_SC) / 256;    // 256 B scale loads per stage
+    static constexpr int NS = (SC + 7) / 8;              // ... per wave
+    static constexpr int NLOAD = NA + NB + NS;
+    static constexpr int CLD = BN + 4;                   // fp32 C-tile row stride
+    static constexpr int RING = NBUF * STAGE;
+    static constexpr int LDS = RING > BM * CLD * 4 ? RING : BM * CLD * 4;
 };
 
-__device__ __forceinline__ uint32_t q4_center(uint32_t x) {
-    // bytes in [0,15] → bytes (x-8) as int8, without cross-byte borrows
-    return ((x | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
-}
+struct GemmParams {
+    const uint8_t *a;             // activation values, rows of a_ld bytes
+    const uint8_t *a_d, *a_s;     // stage-major fp16 planes, a_mp rows per group
+    int64_t a_ld, a_kbytes, a_mp;
+    const uint8_t *b;             // weight values, rows of b_ld bytes
+    const uint8_t *b_d, *b_m;     // stage-major fp16 planes, b_np rows per group
+    int64_t b_ld, b_np;
+    int M, N, nstages, tiles_m, tiles_n, ntiles;
+    EpiArgs e;
+};
 
 __device__ __forceinline__ float gelu_erf(float x) {
     const float SQRT_2_INV = 0.70710678118654752440084436210484f;
@@ -100,271 +122,242 @@ __device__ __forceinline__ void quant_block32(const float *v, int8_t *qdst, uint
     if (sdst) *sdst = f2h_bits(d * (float)sum);
 }
 
-template <int WK>
-struct Traits {
-    static constexpr bool quant = (WK == WK_Q4_0 || WK == WK_Q4_1 || WK == WK_Q8_0);
-    static constexpr bool q4 = (WK == WK_Q4_0 || WK == WK_Q4_1);
-    static constexpr int esize = quant ? 1 : (WK == WK_F16 ? 2 : 4);   // activation bytes/elem
-    static constexpr int stage_elems = ROWB / esize;
-};
+// Wait until at most N of this wave's vector-memory operations are
+// outstanding and all its LDS reads have returned, then join the work-group.
+// The memory clobber keeps the compiler from moving LDS accesses across it.
+template <int N>
+__device__ __forceinline__ void wait_and_barrier() {
+    __asm__ volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
 
-template <int WK, int EPI>
-__global__ __launch_bounds__(NTHR, 2) void k_gemm(GemmParams p) {
-    using T = Traits<WK>;
-    __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_BYTES];
+template <int WK, int EPI, int BM>
+// 128-row tiles: 1 work-group per CU (LDS), 2 waves per SIMD; 64-row tiles: 2.
+__global__ __launch_bounds__(NTHR, 256 / BM) void k_gemm(GemmParams p) {
+    using C = Cfg<WK, BM>;
+    constexpr int MT = C::MT;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[C::LDS];
 
-    // XCD-aware remap: hardware deals work-group ids round-robin over 8 XCDs;
-    // give each XCD a contiguous run of tiles so they share its L2.
-    const int nb = gridDim.x;
-    const int per = nb >> 3;
+    // ---- tile of this work-group ----
+    const int per = gridDim.x >> 3;
     const int logical = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
     if (logical >= p.ntiles) return;
-    const int tm = logical / p.tiles_n, tn = logical % p.tiles_n;
+    constexpr int GROUP = 8;
+    const int group = logical / (GROUP * p.tiles_n);
+    const int first_m = group * GROUP;
+    const int gsz = min(p.tiles_m - first_m, GROUP);
+    const int rem = logical - group * GROUP * p.tiles_n;
+    const int tm = first_m + rem % gsz, tn = rem / gsz;
     const int m0 = tm * BM, n0 = tn * BN;
 
     const int t = threadIdx.x;
-    const int wave = t >> 6, lane = t & 63;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int lane = t & 63;
+    const int wm = wave >> 2, wn = wave & 3;
     const int lr = lane & 31, lh = lane >> 5;
 
-    const int kbytes = p.K * T::esize;      // valid bytes per activation row
-    const int nblk_valid = p.K / QK;
-
-    // ---- register staging for one pipeline stage ----
-    uint4 ra[4];
-    uint4 rb[4];
-    uint16_t rad[4], ras[4];
-    uint2 rbd, rbm;
-
-    auto gload = [&](int s) {
+    // ---- per-lane DMA sources: lane writes LDS bytes [16·lane, 16·lane+16) of
+    // a 1 KB run = 8 rows; it fetches chunk (lane & 7) ^ (lane >> 3) of row lane >> 3
+    const int dma_row = lane >> 3;
+    const int dma_cofs = (((lane & 7) ^ dma_row) << 4);
+    const uint8_t *a_src[C::NA];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int c = t + NTHR * i;
-            const int row = c >> 3, c16 = c & 7;
-            const int kb = s * ROWB + c16 * 16;
-            const bool ok = (m0 + row < p.M) && (kb < kbytes);
-            ra[i] = ok ? *(const uint4 *)(p.a + (int64_t)(m0 + row) * p.a_ld_bytes + kb)
-                       : make_uint4(0, 0, 0, 0);
-        }
-        if constexpr (T::q4) {
+    for (int j = 0; j < C::NA; j++) {
+        const int row = 8 * (wave * C::NA + j) + dma_row;
+        const int gm = min(m0 + row, p.M - 1);
+        a_src[j] = p.a + (int64_t)gm * p.a_ld;
+    }
+    const int64_t a_last = p.a_kbytes - 16;
+    const uint8_t *b_src[C::NB];
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
-                const int c = t + NTHR * i;
-                const int col = c >> 2, blk = c & 3;
-                rb[i] = *(const uint4 *)(p.b + (int64_t)(n0 + col) * p.b_ld_bytes +
-                                         (int64_t)(s * 4 + blk) * 16);
-            }
-        } else {
+    for (int j = 0; j < C::NB; j++) {
+        const int col = 8 * (wave * C::NB + j) + dma_row;
+        b_src[j] = p.b + (int64_t)(n0 + col) * p.b_ld + dma_cofs;
+    }
+    const uint8_t *s_src[C::NS > 0 ? C::NS : 1];
+    int64_t s_step[C::NS > 0 ? C::NS : 1];
+    int s_dst[C::NS > 0 ? C::NS : 1];
+    if constexpr (C::quant) {
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int c = t + NTHR * i;
-                const int col = c >> 3, c16 = c & 7;
-                rb[i] = *(const uint4 *)(p.b + (int64_t)(n0 + col) * p.b_ld_bytes +
-                                         (int64_t)s * ROWB + c16 * 16);
-            }
-        }
-        if constexpr (T::quant) {
-            if (t < BM) {
-                const bool rok = (m0 + t < p.M);
-#pragma unroll
-                for (int blk = 0; blk < 4; blk++) {
-                    const int kb = s * 4 + blk;
-                    const bool ok = rok && kb < nblk_valid;
-                    rad[blk] = ok ? p.a_d[(int64_t)(m0 + t) * p.a_nblk + kb] : (uint16_t)0;
-                    if constexpr (WK == WK_Q4_1) {
-                        ras[blk] = ok ? p.a_s[(int64_t)(m0 + t) * p.a_nblk + kb] : (uint16_t)0;
-                    }
-                }
+        for (int j = 0; j < C::NS; j++) {
+            // scale run k (256 B); waves past the last run repeat an earlier one
+            // (identical bytes to the identical place)
+            const int k = (wave + 8 * j) % C::SC;
+            int o = k * 256;
+            s_dst[j] = C::OFF_SC + o;
+            if (o < BM * 8) {
+                s_src[j] = p.a_d + ((int64_t)m0 * 4) * 2 + o;
+                s_step[j] = p.a_mp * 8;
+            } else if ((o -= BM * 8) < BN * 8) {
+                s_src[j] = p.b_d + ((int64_t)n0 * 4) * 2 + o;
+                s_step[j] = p.b_np * 8;
+            } else if ((o -= BN * 8) < BM * 8) {
+                s_src[j] = p.a_s + ((int64_t)m0 * 4) * 2 + o;
+                s_step[j] = p.a_mp * 8;
             } else {
-                const int col = t - BM;
-                rbd = *(const uint2 *)(p.b_d + (int64_t)(n0 + col) * p.b_nblk + s * 4);
-                if constexpr (WK == WK_Q4_1) {
-                    rbm = *(const uint2 *)(p.b_m + (int64_t)(n0 + col) * p.b_nblk + s * 4);
-                }
+                o -= BM * 8;
+                s_src[j] = p.b_m + ((int64_t)n0 * 4) * 2 + o;
+                s_step[j] = p.b_np * 8;
             }
+            s_src[j] += lane * 4;
+        }
+    }
+
+    auto issue = [&](int s) {
+        uint8_t *L = lds + (s % NBUF) * C::STAGE;
+#pragma unroll
+        for (int j = 0; j < C::NA; j++) {
+            const int64_t off = min((int64_t)s * ROWB + dma_cofs, a_last);
+            __builtin_amdgcn_global_load_lds((const void *)(a_src[j] + off),
+                                             LDS_PTR(L + C::OFF_A + (wave * C::NA + j) * 1024), 16, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < C::NB; j++)
+            __builtin_amdgcn_global_load_lds((const void *)(b_src[j] + (int64_t)s * ROWB),
+                                             LDS_PTR(L + C::OFF_B + (wave * C::NB + j) * 1024), 16, 0, 0);
+        if constexpr (C::quant) {
+#pragma unroll
+            for (int j = 0; j < C::NS; j++)
+                __builtin_amdgcn_global_load_lds((const void *)(s_src[j] + s * s_step[j]),
+                                                 LDS_PTR(L + s_dst[j]), 4, 0, 0);
         }
     };
 
-    auto lstore = [&](int buf) {
-        uint8_t *L = lds + buf * STAGE;
+    // ---- per-lane operand offsets ----
+    const int xr = lr & 7;
+    int a_off[MT], ad_off[MT];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int c = t + NTHR * i;
-            const int row = c >> 3, c16 = c & 7;
-            *(uint4 *)(L + OFF_A + row * LROW + c16 * 16) = ra[i];
+    for (int i = 0; i < MT; i++) {
+        const int r = wm * (32 * MT) + 32 * i + lr;
+        a_off[i] = C::OFF_A + r * ROWB;
+        ad_off[i] = r * 8;
+    }
+    const int bcol = wn * 32 + lr;
+    const int b_off = C::OFF_B + bcol * ROWB;
+    const int bd_off = bcol * 8;
+    int cofs[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) cofs[q] = ((2 * q + lh) ^ xr) << 4;
+
+    v16f acc[MT], accm[MT];
+#pragma unroll
+    for (int i = 0; i < MT; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) { acc[i][r] = 0.f; accm[i][r] = 0.f; }
+
+    // one quant block step: integer sums and scale products of MT tiles
+    struct QFrag {
+        v4i a[MT];
+        v4i b;
+        uint32_t da[MT];
+        uint32_t db;
+    };
+    auto qread = [&](const uint8_t *L, int blk, QFrag &f) {
+#pragma unroll
+        for (int i = 0; i < MT; i++) {
+            f.a[i] = *(const v4i *)(L + a_off[i] + cofs[blk]);
+            f.da[i] = *(const uint16_t *)(L + C::OFF_AD + ad_off[i] + 2 * blk);
         }
-        if constexpr (T::q4) {
+        f.b = *(const v4i *)(L + b_off + cofs[blk]);
+        f.db = *(const uint16_t *)(L + C::OFF_BD + bd_off + 2 * blk);
+    };
+    auto qmma = [&](const QFrag &f, v16i (&S)[MT], v16f (&Cs)[MT]) {
+        const v16i zi = {};
+        const v16f zf = {};
+        const v4u hb = {f.db, 0u, 0u, 0u};
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
-                const int c = t + NTHR * i;
-                const int col = c >> 2, blk = c & 3;
-                const uint4 w = rb[i];
-                uint4 lo = make_uint4(w.x & 0x0F0F0F0Fu, w.y & 0x0F0F0F0Fu, w.z & 0x0F0F0F0Fu,
-                                      w.w & 0x0F0F0F0Fu);
-                uint4 hi = make_uint4((w.x >> 4) & 0x0F0F0F0Fu, (w.y >> 4) & 0x0F0F0F0Fu,
-                                      (w.z >> 4) & 0x0F0F0F0Fu, (w.w >> 4) & 0x0F0F0F0Fu);
-                if constexpr (WK == WK_Q4_0) {
-                    lo = make_uint4(q4_center(lo.x), q4_center(lo.y), q4_center(lo.z), q4_center(lo.w));
-                    hi = make_uint4(q4_center(hi.x), q4_center(hi.y), q4_center(hi.z), q4_center(hi.w));
-                }
-                uint8_t *dst = L + OFF_B + col * LROW + blk * 32;
-                *(uint4 *)dst = lo;
-                *(uint4 *)(dst + 16) = hi;
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int c = t + NTHR * i;
-                const int col = c >> 3, c16 = c & 7;
-                *(uint4 *)(L + OFF_B + col * LROW + c16 * 16) = rb[i];
-            }
-        }
-        if constexpr (T::quant) {
-            if (t < BM) {
-#pragma unroll
-                for (int blk = 0; blk < 4; blk++) {
-                    *(uint16_t *)(L + OFF_AD + (blk * BM + t) * 2) = rad[blk];
-                    if constexpr (WK == WK_Q4_1) *(uint16_t *)(L + OFF_AS + (blk * BM + t) * 2) = ras[blk];
-                }
-            } else {
-                const int col = t - BM;
-                const uint16_t bd[4] = {(uint16_t)(rbd.x & 0xffff), (uint16_t)(rbd.x >> 16),
-                                        (uint16_t)(rbd.y & 0xffff), (uint16_t)(rbd.y >> 16)};
-#pragma unroll
-                for (int blk = 0; blk < 4; blk++) *(uint16_t *)(L + OFF_BD + (blk * BN + col) * 2) = bd[blk];
-                if constexpr (WK == WK_Q4_1) {
-                    const uint16_t bm[4] = {(uint16_t)(rbm.x & 0xffff), (uint16_t)(rbm.x >> 16),
-                                            (uint16_t)(rbm.y & 0xffff), (uint16_t)(rbm.y >> 16)};
-#pragma unroll
-                    for (int blk = 0; blk < 4; blk++) *(uint16_t *)(L + OFF_BMIN + (blk * BN + col) * 2) = bm[blk];
-                }
-            }
+        for (int i = 0; i < MT; i++) {
+            const v4u ha = {f.da[i], 0u, 0u, 0u};
+            S[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[i], f.b, zi, 0, 0, 0);
+            Cs[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, ha),
+                                                           __builtin_bit_cast(v8h, hb), zf, 0, 0, 0);
         }
     };
+    auto qvalu = [&](const v16i (&S)[MT], const v16f (&Cs)[MT]) {
+#pragma unroll
+        for (int i = 0; i < MT; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][r] = __builtin_fmaf((float)S[i][r], Cs[i][r], acc[i][r]);
+    };
 
-    v16f acc[2][2];
+    auto compute = [&](int s) {
+        const uint8_t *L = lds + (s % NBUF) * C::STAGE;
+        if constexpr (C::quant) {
+            QFrag f0, f1;
+            v16i S0[MT], S1[MT];
+            v16f C0[MT], C1[MT];
+            qread(L, 0, f0);
+            qread(L, 1, f1);
+            qmma(f0, S0, C0);
+            qread(L, 2, f0);
+            qmma(f1, S1, C1);
+            qvalu(S0, C0);
+            qread(L, 3, f1);
+            qmma(f0, S0, C0);
+            qvalu(S1, C1);
+            qmma(f1, S1, C1);
+            qvalu(S0, C0);
+            if constexpr (C::q41) {
+                // Σ_b s_x[m][b]·m_w[n][b] over the stage's 4 blocks, doubled like
+                // the scale products (both lane halves carry the values)
+                const uint2 mb = *(const uint2 *)(L + C::OFF_BMIN + bd_off);
+                const v4u hb = {mb.x, mb.y, 0u, 0u};
 #pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
-
-    const int arow0 = wm * 64 + lr, brow0 = wn * 64 + lr;
-
-    auto compute = [&](int buf) {
-        const uint8_t *L = lds + buf * STAGE;
-        if constexpr (T::quant) {
-            const v16i zi = {};
-            const v16f zf = {};
-            // One block at a time keeps S and C of only the current block live
-            // (4 tiles × 32 registers); unrolling over blocks spills.
-#pragma unroll 1
-            for (int blk = 0; blk < 4; blk++) {
-                v4i av[2], bv[2];
-                v8h ha[2], hb[2];
-#pragma unroll
-                for (int i = 0; i < 2; i++) {
-                    av[i] = *(const v4i *)(L + OFF_A + (arow0 + 32 * i) * LROW + blk * 32 + lh * 16);
-                    bv[i] = *(const v4i *)(L + OFF_B + (brow0 + 32 * i) * LROW + blk * 32 + lh * 16);
-                    const _Float16 da = *(const _Float16 *)(L + OFF_AD + (blk * BM + arow0 + 32 * i) * 2);
-                    const _Float16 db = *(const _Float16 *)(L + OFF_BD + (blk * BN + brow0 + 32 * i) * 2);
-                    v8h x = {};
-                    v8h y = {};
-                    x[0] = lh ? (_Float16)0 : da;
-                    y[0] = lh ? (_Float16)0 : db;
-                    ha[i] = x;
-                    hb[i] = y;
+                for (int i = 0; i < MT; i++) {
+                    const uint2 sa = *(const uint2 *)(L + C::OFF_AS + ad_off[i]);
+                    const v4u ha = {sa.x, sa.y, 0u, 0u};
+                    accm[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, ha),
+                                                                     __builtin_bit_cast(v8h, hb), accm[i], 0, 0, 0);
                 }
-#pragma unroll
-                for (int i = 0; i < 2; i++)
-#pragma unroll
-                    for (int j = 0; j < 2; j++) {
-                        const v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[i], bv[j], zi, 0, 0, 0);
-                        const v16f C = __builtin_amdgcn_mfma_f32_32x32x16_f16(ha[i], hb[j], zf, 0, 0, 0);
-#pragma unroll
-                        for (int r = 0; r < 16; r++) acc[i][j][r] = __builtin_fmaf((float)S[r], C[r], acc[i][j][r]);
-                    }
             }
-            if constexpr (WK == WK_Q4_1) {
-                v8h sa[2], mb[2];
-#pragma unroll
-                for (int i = 0; i < 2; i++) {
-                    v8h x = {};
-                    v8h y = {};
-#pragma unroll
-                    for (int blk = 0; blk < 4; blk++) {
-                        const _Float16 sv = *(const _Float16 *)(L + OFF_AS + (blk * BM + arow0 + 32 * i) * 2);
-                        const _Float16 mv = *(const _Float16 *)(L + OFF_BMIN + (blk * BN + brow0 + 32 * i) * 2);
-                        x[blk] = lh ? (_Float16)0 : sv;
-                        y[blk] = lh ? (_Float16)0 : mv;
-                    }
-                    sa[i] = x;
-                    mb[i] = y;
-                }
-#pragma unroll
-                for (int i = 0; i < 2; i++)
-#pragma unroll
-                    for (int j = 0; j < 2; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sa[i], mb[j], acc[i][j], 0, 0, 0);
-            }
+            qvalu(S1, C1);
         } else if constexpr (WK == WK_F16) {
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) {
-                v8h av[2], bv[2];
+                const v8h bv = *(const v8h *)(L + b_off + cofs[ks]);
 #pragma unroll
-                for (int i = 0; i < 2; i++) {
-                    av[i] = *(const v8h *)(L + OFF_A + (arow0 + 32 * i) * LROW + ks * 32 + lh * 16);
-                    bv[i] = *(const v8h *)(L + OFF_B + (brow0 + 32 * i) * LROW + ks * 32 + lh * 16);
+                for (int i = 0; i < MT; i++) {
+                    const v8h av = *(const v8h *)(L + a_off[i] + cofs[ks]);
+                    acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc[i], 0, 0, 0);
                 }
-#pragma unroll
-                for (int i = 0; i < 2; i++)
-#pragma unroll
-                    for (int j = 0; j < 2; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
             }
         } else {
 #pragma unroll
             for (int ks = 0; ks < 16; ks++) {
-                float av[2], bv[2];
+                const int o = ((((ks >> 1) ^ xr)) << 4) + ((2 * (ks & 1) + lh) << 2);
+                const float bv = *(const float *)(L + b_off + o);
 #pragma unroll
-                for (int i = 0; i < 2; i++) {
-                    av[i] = *(const float *)(L + OFF_A + (arow0 + 32 * i) * LROW + (ks * 2 + lh) * 4);
-                    bv[i] = *(const float *)(L + OFF_B + (brow0 + 32 * i) * LROW + (ks * 2 + lh) * 4);
+                for (int i = 0; i < MT; i++) {
+                    const float av = *(const float *)(L + a_off[i] + o);
+                    acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc[i], 0, 0, 0);
                 }
-#pragma unroll
-                for (int i = 0; i < 2; i++)
-#pragma unroll
-                    for (int j = 0; j < 2; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[j], acc[i][j], 0, 0, 0);
             }
         }
     };
 
-    // ---- main loop: one barrier per stage ----
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    for (int s = 0; s < p.nstages; s++) {
-        const int cur = s & 1;
-        if (s + 1 < p.nstages) gload(s + 1);
-        compute(cur);
-        if (s + 1 < p.nstages) lstore(cur ^ 1);
-        __syncthreads();
+    // ---- main loop: stage s+2 in flight while stage s is consumed ----
+    const int ns = p.nstages;
+    issue(0);
+    if (ns > 1) issue(1);
+    for (int s = 0; s < ns; s++) {
+        if (s + 1 < ns) wait_and_barrier<C::NLOAD>();
+        else wait_and_barrier<0>();
+        if (s + 2 < ns) issue(s + 2);
+        compute(s);
     }
+    wait_and_barrier<0>();
 
     // ---- stage the fp32 tile in LDS ----
     float *Ct = (float *)lds;
+    constexpr float kScale = C::quant ? 0.5f : 1.0f;  // remove the doubled scale products
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < MT; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int row = wm * 64 + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
-                const int col = wn * 64 + 32 * j + lr;
-                Ct[row * CLD + col] = acc[i][j][r];
-            }
+        for (int r = 0; r < 16; r++) {
+            const int row = wm * (32 * MT) + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
+            float v = acc[i][r];
+            if constexpr (C::q41) v += accm[i][r];
+            Ct[row * C::CLD + bcol] = v * kScale;
+        }
     __syncthreads();
 
     const EpiArgs &e = p.e;
@@ -375,21 +368,22 @@ __global__ __launch_bounds__(NTHR, 2) void k_gemm(GemmParams p) {
         if (sel == 2) {
             // V is written transposed, [b][h][d][p]: one token row per thread so
             // that a wave's stores for one d cover consecutive positions.
-            const int row = t & 127, cg = t >> 7;
+            constexpr int NCG = NTHR / BM, CPG = BN / NCG;
+            const int row = t % BM, cg = t / BM;
             const int gm = m0 + row;
             if (gm < p.M) {
                 const int py = gm / e.grid, px = gm % e.grid;
                 const int b = (py / e.window) * nwx + px / e.window;
                 const int pp = (py % e.window) * e.window + px % e.window;
 #pragma unroll 4
-                for (int c4 = 0; c4 < 16; c4++) {
-                    const float4 v = *(const float4 *)(Ct + row * CLD + cg * 64 + c4 * 4);
+                for (int c4 = 0; c4 < CPG / 4; c4++) {
+                    const float4 v = *(const float4 *)(Ct + row * C::CLD + cg * CPG + c4 * 4);
                     const float vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
-                        const int gn = n0 + cg * 64 + c4 * 4 + i;
-                        const int rem = gn - 2 * e.E;
-                        const int h = rem / e.HD, d = rem % e.HD;
+                        const int gn = n0 + cg * CPG + c4 * 4 + i;
+                        const int r2 = gn - 2 * e.E;
+                        const int h = r2 / e.HD, d = r2 % e.HD;
                         const float val = vv[i] + e.bias[gn];
                         const int64_t o = ((int64_t)(b * e.NH + h) * e.HD + d) * e.vt_ld + pp;
                         const _Float16 hv = to_half(val);
@@ -399,9 +393,7 @@ __global__ __launch_bounds__(NTHR, 2) void k_gemm(GemmParams p) {
                 }
             }
         } else {
-#pragma unroll
-            for (int it = 0; it < 2; it++) {
-                const int ch = t + NTHR * it;
+            for (int ch = t; ch < BM * 4; ch += NTHR) {
                 const int row = ch >> 2, cc = ch & 3;
                 const int gm = m0 + row;
                 if (gm >= p.M) continue;
@@ -409,7 +401,7 @@ __global__ __launch_bounds__(NTHR, 2) void k_gemm(GemmParams p) {
                 float v[32];
 #pragma unroll
                 for (int j = 0; j < 32; j += 4) {
-                    const float4 x = *(const float4 *)(Ct + row * CLD + cc * 32 + j);
+                    const float4 x = *(const float4 *)(Ct + row * C::CLD + cc * 32 + j);
                     v[j] = x.x + e.bias[gn0 + j];
                     v[j + 1] = x.y + e.bias[gn0 + j + 1];
                     v[j + 2] = x.z + e.bias[gn0 + j + 2];
@@ -418,8 +410,8 @@ __global__ __launch_bounds__(NTHR, 2) void k_gemm(GemmParams p) {
                 const int py = gm / e.grid, px = gm % e.grid;
                 const int b = (py / e.window) * nwx + px / e.window;
                 const int pp = (py % e.window) * e.window + px % e.window;
-                const int rem = gn0 - sel * e.E;
-                const int h = rem / e.HD, d0 = rem % e.HD;
+                const int r2 = gn0 - sel * e.E;
+                const int h = r2 / e.HD, d0 = r2 % e.HD;
                 if (e.freqs) {
                     // sam3_apply_rope: out_re = re·cos − im·sin, out_im = re·sin + im·cos,
                     // each product rounded on its own (separate ggml ops).
@@ -461,87 +453,109 @@ __global__ __launch_bounds__(NTHR, 2) void k_gemm(GemmParams p) {
                 }
             }
         }
-    } else {
-#pragma unroll
-        for (int it = 0; it < 2; it++) {
-            const int ch = t + NTHR * it;
+    } else if constexpr (EPI == EPI_GELU) {
+        // full 32-column blocks guaranteed by the launcher (N % 32 == 0)
+        for (int ch = t; ch < BM * 4; ch += NTHR) {
             const int row = ch >> 2, cc = ch & 3;
             const int gm = m0 + row;
-            if (gm >= p.M) continue;
             const int gn0 = n0 + cc * 32;
-            if (gn0 >= p.N) continue;
+            if (gm >= p.M || gn0 >= p.N) continue;
             float v[32];
 #pragma unroll
             for (int j = 0; j < 32; j += 4) {
-                const float4 x = *(const float4 *)(Ct + row * CLD + cc * 32 + j);
+                const float4 x = *(const float4 *)(Ct + row * C::CLD + cc * 32 + j);
                 v[j] = x.x; v[j + 1] = x.y; v[j + 2] = x.z; v[j + 3] = x.w;
             }
-            const bool full = (gn0 + 32 <= p.N);
-            if constexpr (EPI == EPI_F32 || EPI == EPI_RESID) {
-                float *y = e.y + (int64_t)gm * e.ldy + gn0;
 #pragma unroll
-                for (int j = 0; j < 32; j++) {
-                    if (!full && gn0 + j >= p.N) break;
-                    const float bv = e.bias ? __fadd_rn(v[j], e.bias[gn0 + j]) : v[j];
-                    if constexpr (EPI == EPI_RESID) y[j] = __fadd_rn(y[j], bv);
-                    else y[j] = bv;
-                }
-            } else if constexpr (EPI == EPI_POS) {
+            for (int j = 0; j < 32; j++) v[j] = gelu_erf(__fadd_rn(v[j], e.bias[gn0 + j]));
+            const Act &o = e.out;
+            if (o.kind == A_F16) {
+                _Float16 *dst = (_Float16 *)o.x + (int64_t)gm * o.ld + gn0;
+                uint32_t w[16];
+#pragma unroll
+                for (int j = 0; j < 16; j++)
+                    w[j] = (uint32_t)f2h_bits(v[2 * j]) | ((uint32_t)f2h_bits(v[2 * j + 1]) << 16);
+                uint4 *d4 = (uint4 *)dst;
+                d4[0] = make_uint4(w[0], w[1], w[2], w[3]);
+                d4[1] = make_uint4(w[4], w[5], w[6], w[7]);
+                d4[2] = make_uint4(w[8], w[9], w[10], w[11]);
+                d4[3] = make_uint4(w[12], w[13], w[14], w[15]);
+            } else if (o.kind == A_F32) {
+                float4 *dst = (float4 *)((float *)o.x + (int64_t)gm * o.ld + gn0);
+#pragma unroll
+                for (int j = 0; j < 8; j++) dst[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+            } else {
+                const int64_t blk = scale_index(o.mp, gm, gn0 / QK);
+                quant_block32(v, (int8_t *)o.x + (int64_t)gm * o.ld + gn0, o.d + blk,
+                              o.kind == A_Q8_1 ? o.s + blk : nullptr);
+            }
+        }
+    } else {
+        // EPI_F32 / EPI_RESID / EPI_POS: lane ↔ 4 consecutive columns, so that one
+        // wave store covers 2 rows × 512 contiguous bytes
+        const int f = t & 31;
+        const int gn = n0 + 4 * f;
+        const bool vec = (p.N % 4) == 0 && gn + 3 < p.N;
+        for (int row = t >> 5; row < BM; row += NTHR / 32) {
+            const int gm = m0 + row;
+            if (gm >= p.M || gn >= p.N) continue;
+            const float4 x = *(const float4 *)(Ct + row * C::CLD + 4 * f);
+            float v[4] = {x.x, x.y, x.z, x.w};
+            float *y = e.y + (int64_t)gm * e.ldy + gn;
+            if constexpr (EPI == EPI_POS) {
                 const int py = gm / e.grid, px = gm % e.grid;
-                const float *pr = e.pos + ((int64_t)(py % e.pos_grid) * e.pos_grid + (px % e.pos_grid)) * p.N + gn0;
-                float *y = e.y + (int64_t)gm * e.ldy + gn0;
+                const float *pr = e.pos + ((int64_t)(py % e.pos_grid) * e.pos_grid + (px % e.pos_grid)) * p.N + gn;
 #pragma unroll
-                for (int j = 0; j < 32; j++) {
-                    if (!full && gn0 + j >= p.N) break;
-                    y[j] = __fadd_rn(v[j], pr[j]);
+                for (int j = 0; j < 4; j++) v[j] = __fadd_rn(v[j], pr[j]);
+            } else {
+                if (e.bias) {
+#pragma unroll
+                    for (int j = 0; j < 4; j++) v[j] = __fadd_rn(v[j], e.bias[gn + j]);
                 }
-            } else if constexpr (EPI == EPI_GELU) {
-                // full 32-column block guaranteed by the launcher (N % 32 == 0)
-#pragma unroll
-                for (int j = 0; j < 32; j++) v[j] = gelu_erf(__fadd_rn(v[j], e.bias[gn0 + j]));
-                const Act &o = e.out;
-                if (o.kind == A_F16) {
-                    _Float16 *dst = (_Float16 *)o.x + (int64_t)gm * o.ld + gn0;
-                    uint32_t w[16];
-#pragma unroll
-                    for (int j = 0; j < 16; j++)
-                        w[j] = (uint32_t)f2h_bits(v[2 * j]) | ((uint32_t)f2h_bits(v[2 * j + 1]) << 16);
-                    uint4 *d4 = (uint4 *)dst;
-                    d4[0] = make_uint4(w[0], w[1], w[2], w[3]);
-                    d4[1] = make_uint4(w[4], w[5], w[6], w[7]);
-                    d4[2] = make_uint4(w[8], w[9], w[10], w[11]);
-                    d4[3] = make_uint4(w[12], w[13], w[14], w[15]);
-                } else if (o.kind == A_F32) {
-                    float *dst = (float *)o.x + (int64_t)gm * o.ld + gn0;
-#pragma unroll
-                    for (int j = 0; j < 32; j++) dst[j] = v[j];
-                } else {
-                    const int64_t blk = (int64_t)gm * (o.ld / QK) + gn0 / QK;
-                    quant_block32(v, (int8_t *)o.x + (int64_t)gm * o.ld + gn0, o.d + blk,
-                                  o.kind == A_Q8_1 ? o.s + blk : nullptr);
+            }
+            if (vec) {
+                if constexpr (EPI == EPI_RESID) {
+                    const float4 o = *(const float4 *)y;
+                    v[0] = __fadd_rn(o.x, v[0]);
+                    v[1] = __fadd_rn(o.y, v[1]);
+                    v[2] = __fadd_rn(o.z, v[2]);
+                    v[3] = __fadd_rn(o.w, v[3]);
+                }
+                *(float4 *)y = make_float4(v[0], v[1], v[2], v[3]);
+            } else {
+                for (int j = 0; j < 4 && gn + j < p.N; j++) {
+                    if constexpr (EPI == EPI_RESID) y[j] = __fadd_rn(y[j], v[j]);
+                    else y[j] = v[j];
                 }
             }
         }
     }
 }
 
-template <int WK, int EPI>
+template <int WK, int EPI, int BM>
 hipError_t launch_one(const GemmParams &p, hipStream_t st) {
     const int grid = ((p.ntiles + 7) / 8) * 8;
-    hipLaunchKernelGGL((k_gemm<WK, EPI>), dim3(grid), dim3(NTHR), 0, st, p);
+    hipLaunchKernelGGL((k_gemm<WK, EPI, BM>), dim3(grid), dim3(NTHR), 0, st, p);
     return hipGetLastError();
 }
 
-template <int WK>
+template <int WK, int BM>
 hipError_t dispatch_epi(Epi epi, const GemmParams &p, hipStream_t st) {
     switch (epi) {
-        case EPI_F32: return launch_one<WK, EPI_F32>(p, st);
-        case EPI_RESID: return launch_one<WK, EPI_RESID>(p, st);
-        case EPI_POS: return launch_one<WK, EPI_POS>(p, st);
-        case EPI_GELU: return launch_one<WK, EPI_GELU>(p, st);
-        case EPI_QKV: return launch_one<WK, EPI_QKV>(p, st);
+        case EPI_F32: return launch_one<WK, EPI_F32, BM>(p, st);
+        case EPI_RESID: return launch_one<WK, EPI_RESID, BM>(p, st);
+        case EPI_POS: return launch_one<WK, EPI_POS, BM>(p, st);
+        case EPI_GELU: return launch_one<WK, EPI_GELU, BM>(p, st);
+        case EPI_QKV: return launch_one<WK, EPI_QKV, BM>(p, st);
     }
     return hipErrorInvalidValue;
+}
+
+template <int WK>
+hipError_t dispatch_bm(int bm, Epi epi, GemmParams &p, hipStream_t st) {
+    p.tiles_m = (p.M + bm - 1) / bm;
+    p.ntiles = p.tiles_m * p.tiles_n;
+    return bm == 64 ? dispatch_epi<WK, 64>(epi, p, st) : dispatch_epi<WK, 128>(epi, p, st);
 }
 
 }  // namespace
@@ -552,34 +566,30 @@ hipError_t launch_gemm(const Weight &w, const Act &a, int64_t M, Epi epi, const 
     GemmParams p{};
     const int esize = (w.kind == WK_F16) ? 2 : (w.kind == WK_F32 ? 4 : 1);
     p.a = (const uint8_t *)a.x;
-    p.a_d = a.d;
-    p.a_s = a.s;
-    p.a_ld_bytes = a.ld * esize;
-    p.a_nblk = a.ld / QK;
+    p.a_d = (const uint8_t *)a.d;
+    p.a_s = (const uint8_t *)a.s;
+    p.a_ld = a.ld * esize;
+    p.a_kbytes = w.K * esize;
+    p.a_mp = a.mp;
     p.b = (const uint8_t *)w.q;
-    p.b_d = w.d;
-    p.b_m = w.m;
-    switch (w.kind) {
-        case WK_Q4_0: case WK_Q4_1: p.b_ld_bytes = w.Kbp * 16; break;
-        case WK_Q8_0: p.b_ld_bytes = w.Kp; break;
-        case WK_F16: p.b_ld_bytes = w.Kp * 2; break;
-        default: p.b_ld_bytes = w.Kp * 4; break;
-    }
-    p.b_nblk = w.Kbp;
+    p.b_d = (const uint8_t *)w.d;
+    p.b_m = (const uint8_t *)w.m;
+    p.b_ld = w.Kp * esize;
+    p.b_np = w.Np;
     p.M = (int)M;
     p.N = (int)w.N;
-    p.K = (int)w.K;
-    p.nstages = (int)((w.K + stage_k(w.kind) - 1) / stage_k(w.kind));
-    p.tiles_m = (int)((M + BM - 1) / BM);
+    p.nstages = (int)(w.Kp / stage_k(w.kind));
     p.tiles_n = (int)(w.Np / BN);
-    p.ntiles = p.tiles_m * p.tiles_n;
     p.e = ea;
+    // 64-row tiles when 128-row tiles would not give every CU three tiles
+    const int64_t tiles128 = ((M + 127) / 128) * p.tiles_n;
+    const int bm = (tiles128 < 3 * 256) ? 64 : 128;
     switch (w.kind) {
-        case WK_Q4_0: return dispatch_epi<WK_Q4_0>(epi, p, st);
-        case WK_Q4_1: return dispatch_epi<WK_Q4_1>(epi, p, st);
-        case WK_Q8_0: return dispatch_epi<WK_Q8_0>(epi, p, st);
-        case WK_F16: return dispatch_epi<WK_F16>(epi, p, st);
-        case WK_F32: return dispatch_epi<WK_F32>(epi, p, st);
+        case WK_Q4_0: return dispatch_bm<WK_Q4_0>(bm, epi, p, st);
+        case WK_Q4_1: return dispatch_bm<WK_Q4_1>(bm, epi, p, st);
+        case WK_Q8_0: return dispatch_bm<WK_Q8_0>(bm, epi, p, st);
+        case WK_F16: return dispatch_bm<WK_F16>(bm, epi, p, st);
+        case WK_F32: return dispatch_bm<WK_F32>(bm, epi, p, st);
     }
     return hipErrorInvalidValue;
 }

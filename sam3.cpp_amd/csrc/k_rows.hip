@@ -58,7 +58,7 @@ __device__ __forceinline__ void emit16(const float *v, const Act &o, int64_t row
     *(uint4 *)((int8_t *)o.x + row * o.ld + col) = make_uint4(w[0], w[1], w[2], w[3]);
     sum += __shfl_xor(sum, 1, 64);
     if ((lane & 1) == 0) {
-        const int64_t blk = row * (o.ld / QK) + col / QK;
+        const int64_t blk = scale_index(o.mp, row, col / QK);
         o.d[blk] = f2h_bits(d);
         // s = fp16(fp32(d·Σq)): f2h_bits keeps the fp32 rounding of the product
         if (o.kind == A_Q8_1) o.s[blk] = f2h_bits(d * (float)sum);
@@ -147,7 +147,17 @@ __global__ __launch_bounds__(256) void k_rows_quant(const float *__restrict__ x,
     if (row >= M) return;
     const int64_t nch = K / 16;
     // chunks come in pairs (2j, 2j+1) inside one wave: nch is even (K % 32 == 0)
-    if (ch >= nch) return;
+    if (ch >= nch) {
+        // blocks between K and the next multiple of 128 get zero scales: the
+        // GEMM reads whole groups of four blocks
+        const int64_t nch4 = (K + 127) / 128 * 8;
+        if (ch < nch4 && (ch & 1) == 0 && (o.kind == A_Q8_0 || o.kind == A_Q8_1)) {
+            const int64_t blk = scale_index(o.mp, row, ch / 2);
+            o.d[blk] = 0;
+            if (o.kind == A_Q8_1) o.s[blk] = 0;
+        }
+        return;
+    }
     float v[16];
     const float4 *src = (const float4 *)(x + row * K + ch * 16);
 #pragma unroll
@@ -215,7 +225,7 @@ hipError_t launch_rows_quant(AKind kind, const float *x, int64_t M, int64_t K, c
                              hipStream_t st) {
     (void)kind;
     if (K % 32 != 0) return hipErrorInvalidValue;
-    const int64_t nch = K / 16;
+    const int64_t nch = (K + 127) / 128 * 8;  // chunks of 16 up to the 128-element group
     const dim3 grid((unsigned)((nch + 63) / 64), (unsigned)((M + 3) / 4));
     hipLaunchKernelGGL(k_rows_quant, grid, dim3(256), 0, st, x, M, K, out);
     return hipGetLastError();

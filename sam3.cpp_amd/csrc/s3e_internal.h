@@ -33,21 +33,35 @@ inline AKind act_kind_for(WKind w) {
     }
 }
 
+// Rows of every activation buffer are padded to a multiple of this, so the
+// GEMM's tile loads never leave the allocation.
+constexpr int ROW_PAD = 128;
+
 // A device activation buffer in one of the formats above.
+//   x : values, row-major [mp][ld] (int8 codes, fp16 or f32)
+//   d : fp16 block scales, and s: fp16 block sums (Q8_1), "stage-major":
+//       block b of row r at ((b / 4) * mp + r) * 4 + b % 4, so the four
+//       blocks one GEMM stage consumes for 128 consecutive rows are 1 KB of
+//       contiguous memory.
 struct Act {
     AKind kind = A_F32;
-    void *x = nullptr;      // qs (int8), fp16 or f32 values
-    uint16_t *d = nullptr;  // fp16 block scales (Q8 kinds)
-    uint16_t *s = nullptr;  // fp16 block sums (Q8_1)
-    int64_t ld = 0;         // elements per row (multiple of 32)
+    void *x = nullptr;
+    uint16_t *d = nullptr;
+    uint16_t *s = nullptr;
+    int64_t ld = 0;   // elements per row (multiple of 32)
+    int64_t mp = 0;   // row pitch of the scale planes (rows rounded up to ROW_PAD)
 };
+
+__host__ __device__ inline int64_t scale_index(int64_t mp, int64_t row, int64_t blk) {
+    return ((blk >> 2) * mp + row) * 4 + (blk & 3);
+}
 
 // A weight matrix repacked for the GEMM kernels.  N rows of K, stored as
 // column-blocks of the output: row n of the ggml matrix is "column" n here.
-//   Q4_0/Q4_1: qs [Np][Kbp][16] nibble bytes exactly as ggml stores them
-//              (low nibble = element j, high nibble = element j+16),
-//              d [Np][Kbp] fp16, m [Np][Kbp] fp16 (Q4_1).
-//   Q8_0     : qs [Np][Kp] int8, d [Np][Kbp] fp16.
+//   Q4_0/Q4_1/Q8_0: q8 [Np][Kp] int8 block codes — the file's integers
+//              (Q4_0 nibble − 8, Q4_1 nibble 0..15, Q8_0 as stored), held
+//              expanded because the weights stay cache-resident in the large-M
+//              GEMM; d, m (Q4_1 minimum) fp16 stage-major [Kp/128][Np][4].
 //   F16/F32  : values [Np][Kp].
 // Kp pads K to the kernel's stage width, Np pads N to the tile width; the
 // padding is zero and contributes nothing.

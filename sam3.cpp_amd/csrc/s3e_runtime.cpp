@@ -106,29 +106,34 @@ int upload_weight(int device, int type, int64_t K, int64_t N, const uint8_t *src
     const int64_t Kb = K / 32;
     std::vector<uint8_t> q;
     std::vector<uint16_t> d, m;
+    // stage-major scale planes: block b of column n at ((b / 4) * Np + n) * 4 + b % 4
+    auto sidx = [&](int64_t n, int64_t b) { return (size_t)(((b >> 2) * w.Np + n) * 4 + (b & 3)); };
     switch (w.kind) {
         case WK_Q4_0:
-        case WK_Q4_1: {
-            const int bs = (w.kind == WK_Q4_0) ? 18 : 20, qo = (w.kind == WK_Q4_0) ? 2 : 4;
-            q.assign((size_t)(w.Np * w.Kbp * 16), 0);
+        case WK_Q4_1:
+        case WK_Q8_0: {
+            const bool q4 = (w.kind != WK_Q8_0);
+            const int bs = (w.kind == WK_Q4_0) ? 18 : (w.kind == WK_Q4_1 ? 20 : 34);
+            const int qo = (w.kind == WK_Q4_1) ? 4 : 2;
+            q.assign((size_t)(w.Np * w.Kp), 0);
             d.assign((size_t)(w.Np * w.Kbp), 0);
             if (w.kind == WK_Q4_1) m.assign((size_t)(w.Np * w.Kbp), 0);
             for (int64_t n = 0; n < N; n++)
                 for (int64_t b = 0; b < Kb; b++) {
                     const uint8_t *blk = src + (size_t)n * rs + (size_t)b * bs;
-                    std::memcpy(&d[(size_t)(n * w.Kbp + b)], blk, 2);
-                    if (w.kind == WK_Q4_1) std::memcpy(&m[(size_t)(n * w.Kbp + b)], blk + 2, 2);
-                    std::memcpy(&q[(size_t)((n * w.Kbp + b) * 16)], blk + qo, 16);
-                }
-        } break;
-        case WK_Q8_0: {
-            q.assign((size_t)(w.Np * w.Kp), 0);
-            d.assign((size_t)(w.Np * w.Kbp), 0);
-            for (int64_t n = 0; n < N; n++)
-                for (int64_t b = 0; b < Kb; b++) {
-                    const uint8_t *blk = src + (size_t)n * rs + (size_t)b * 34;
-                    std::memcpy(&d[(size_t)(n * w.Kbp + b)], blk, 2);
-                    std::memcpy(&q[(size_t)(n * w.Kp + b * 32)], blk + 2, 32);
+                    std::memcpy(&d[sidx(n, b)], blk, 2);
+                    if (w.kind == WK_Q4_1) std::memcpy(&m[sidx(n, b)], blk + 2, 2);
+                    int8_t *dst = (int8_t *)&q[(size_t)(n * w.Kp + b * 32)];
+                    if (q4) {
+                        // byte j holds element j (low nibble) and element j + 16 (high nibble)
+                        const int off = (w.kind == WK_Q4_0) ? 8 : 0;
+                        for (int j = 0; j < 16; j++) {
+                            dst[j] = (int8_t)((blk[qo + j] & 0x0F) - off);
+                            dst[j + 16] = (int8_t)((blk[qo + j] >> 4) - off);
+                        }
+                    } else {
+                        std::memcpy(dst, blk + qo, 32);
+                    }
                 }
         } break;
         case WK_F16:
@@ -157,17 +162,25 @@ int upload_weight(int device, int type, int64_t K, int64_t N, const uint8_t *src
     return S3E_OK;
 }
 
-// Device activation buffer able to hold M rows of up to K elements in any format.
+// Device activation buffer able to hold M rows of up to K elements in any
+// format.  The scale planes are stage-major with a row pitch of M rounded up
+// to ROW_PAD and K rounded up to 128 (4 blocks); they are zeroed on the
+// stream that will use the buffer, so blocks past K and rows past M hold zero
+// scales.
 struct ActBuf {
     void *x = nullptr;
     uint16_t *d = nullptr, *s = nullptr;
-    int64_t cap_rows = 0, cap_k = 0;
-    hipError_t alloc(int64_t M, int64_t K) {
+    int64_t cap_rows = 0, cap_k = 0, mp = 0;
+    hipError_t alloc(int64_t M, int64_t K, hipStream_t st) {
         cap_rows = M;
         cap_k = K;
+        mp = round_up(M, ROW_PAD);
+        const size_t sbytes = (size_t)(mp * (round_up(K, 128) / 32) * 2);
         hipError_t e = hipMalloc(&x, (size_t)(M * K * 4));
-        if (e == hipSuccess) e = hipMalloc(&d, (size_t)(M * (K / 32) * 2));
-        if (e == hipSuccess) e = hipMalloc(&s, (size_t)(M * (K / 32) * 2));
+        if (e == hipSuccess) e = hipMalloc(&d, sbytes);
+        if (e == hipSuccess) e = hipMalloc(&s, sbytes);
+        if (e == hipSuccess) e = hipMemsetAsync(d, 0, sbytes, st);
+        if (e == hipSuccess) e = hipMemsetAsync(s, 0, sbytes, st);
         return e;
     }
     void release() {
@@ -184,6 +197,7 @@ struct ActBuf {
         a.d = d;
         a.s = s;
         a.ld = ld;
+        a.mp = mp;
         return a;
     }
 };
@@ -314,6 +328,7 @@ extern "C" int s3e_quantize_rows(s3e_ctx *ctx, int type, const float *X, int64_t
     a.d = d;
     a.s = s;
     a.ld = K;
+    a.mp = round_up(M, ROW_PAD);
     if (type == S3E_TYPE_Q8_0) a.kind = A_Q8_0;
     else if (type == S3E_TYPE_Q8_1) a.kind = A_Q8_1;
     else if (type == S3E_TYPE_F16) a.kind = A_F16;
@@ -349,7 +364,7 @@ extern "C" int s3e_mul_mat(s3e_ctx *ctx, const s3e_weight *w, const float *X, in
         return S3E_OK;
     }
     ActBuf buf;
-    HIP_TRY(buf.alloc(M, W.K));
+    HIP_TRY(buf.alloc(M, W.K, ctx->stream));
     const Act a = buf.as(ak, W.K);
     hipError_t e = launch_rows_quant(ak, X, M, W.K, a, ctx->stream);
     if (e == hipSuccess) e = launch_gemm(W, a, M, EPI_F32, ea, ctx->stream);
@@ -375,6 +390,7 @@ extern "C" int s3e_mul_mat_q(s3e_ctx *ctx, const s3e_weight *w, const void *xq, 
     a.d = (uint16_t *)d;
     a.s = (uint16_t *)s;
     a.ld = W.K;
+    a.mp = round_up(M, ROW_PAD);
     EpiArgs ea;
     ea.bias = bias;
     ea.y = Y;
@@ -742,9 +758,9 @@ extern "C" int s3e_state_create(s3e_ctx *ctx, const s3e_model *m, s3e_state **ou
     const int64_t T = st->T, E = m->E;
     hipError_t e = hipMalloc(&st->x, (size_t)(T * E * 4));
     if (e == hipSuccess) e = hipMalloc(&st->chw, (size_t)3 * m->img * m->img * 4);
-    if (e == hipSuccess) e = st->a1.alloc(T, E);
-    if (e == hipSuccess) e = st->a2.alloc(T, m->mlp);
-    if (e == hipSuccess) e = st->col.alloc(T, round_up(3LL * m->patch * m->patch, 32));
+    if (e == hipSuccess) e = st->a1.alloc(T, E, ctx->stream);
+    if (e == hipSuccess) e = st->a2.alloc(T, m->mlp, ctx->stream);
+    if (e == hipSuccess) e = st->col.alloc(T, round_up(3LL * m->patch * m->patch, 32), ctx->stream);
     // Q, K, Vᵀ hold two fp16 planes each (hi, lo) for split-precision attention
     if (e == hipSuccess) e = hipMalloc(&st->q16, (size_t)(T * E * 2 * 2));
     if (e == hipSuccess) e = hipMalloc(&st->k16, (size_t)(T * E * 2 * 2));

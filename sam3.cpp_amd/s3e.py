@@ -14,7 +14,8 @@ from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libs3e.so")
+# S3E_LIB_PATH points the binding at another build of the same library.
+LIB_PATH = os.environ.get("S3E_LIB_PATH", os.path.join(HERE, "libs3e.so"))
 
 TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_Q4_1, TYPE_Q8_0, TYPE_Q8_1 = 0, 1, 2, 3, 8, 9
 PREC_DEFAULT, PREC_F32 = 0, 1
@@ -115,6 +116,19 @@ def synth_write(path: str, *, img_size=1008, patch=14, embed_dim=1024, depth=32,
     cfg.seed = seed
     cfg.std = -abs(std) if random_affine else abs(std)
     check(LIB.s3e_synth_write(path.encode(), ctypes.byref(cfg)), "s3e_synth_write")
+
+
+def act_scale_elems(M: int, K: int) -> int:
+    """fp16 elements of one stage-major scale plane written by s3e_quantize_rows
+    (row pitch M rounded up to 128, blocks rounded up to a multiple of 4)."""
+    return ((K + 127) // 128) * ((M + 127) // 128 * 128) * 4
+
+
+def unstage_scales(plane: np.ndarray, M: int, K: int) -> np.ndarray:
+    """[M][K/32] view of a stage-major scale plane (block b of row r at
+    ((b // 4) * Mp + r) * 4 + b % 4)."""
+    G, Mp = (K + 127) // 128, (M + 127) // 128 * 128
+    return plane.reshape(G, Mp, 4).transpose(1, 0, 2).reshape(Mp, G * 4)[:M, :K // 32]
 
 
 class DeviceBuffer:

@@ -15,6 +15,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as orc
+import s3e
 
 pytestmark = pytest.mark.gpu
 
@@ -50,14 +51,40 @@ def test_quantize_rows_bit_exact(ctx, vdt):
         got = qs.download(np.uint16, (M, K))
         assert np.array_equal(got.view(np.uint8).ravel(), ref)
         return
-    qs, d, s = ctx.buffer(M * K), ctx.buffer(M * K // 32 * 2), ctx.buffer(M * K // 32 * 2)
+    ns = s3e.act_scale_elems(M, K)
+    qs, d, s = ctx.buffer(M * K), ctx.buffer(ns * 2), ctx.buffer(ns * 2)
     ctx.quantize_rows(vdt, Xd, M, K, qs, d, s)
     ctx.sync()
     rq, rd, rs = orc.split_q8(vdt, ref, M, K)
     assert np.array_equal(qs.download(np.int8, (M, K)), rq)
-    assert np.array_equal(d.download(np.uint16, (M, K // 32)), rd)
+    assert np.array_equal(s3e.unstage_scales(d.download(np.uint16, (ns,)), M, K), rd)
     if vdt == orc.Q8_1:
-        assert np.array_equal(s.download(np.uint16, (M, K // 32)), rs)
+        assert np.array_equal(s3e.unstage_scales(s.download(np.uint16, (ns,)), M, K), rs)
+
+
+@pytest.mark.parametrize("wt", [orc.Q4_0, orc.Q4_1, orc.Q8_0, orc.F16],
+                         ids=lambda t: {1: "f16", 2: "q4_0", 3: "q4_1", 8: "q8_0"}[t])
+@pytest.mark.parametrize("M,N,K", [(200, 256, 160), (130, 384, 1024)])
+def test_mul_mat_q_matches_mul_mat(ctx, wt, M, N, K):
+    """s3e_mul_mat_q on s3e_quantize_rows output (the documented layout, K not a
+    multiple of 128 included) runs the same kernel as s3e_mul_mat: identical."""
+    rng = np.random.default_rng(M + N + K + wt)
+    W = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    wb = orc.to_weight_bytes(wt, W)
+    w = ctx.weight(wt, K, N, wb)
+    Xd, Y1, Y2 = ctx.to_device(X), ctx.buffer(M * N * 4), ctx.buffer(M * N * 4)
+    ctx.mul_mat(w, Xd, M, Y1)
+    vdt = orc.VEC_DOT[wt]
+    ns = s3e.act_scale_elems(M, K)
+    qs, d, s = ctx.buffer(M * K * 2), ctx.buffer(ns * 2), ctx.buffer(ns * 2)
+    ctx.quantize_rows(vdt, Xd, M, K, qs, d if wt != orc.F16 else None, s if wt != orc.F16 else None)
+    ctx.mul_mat_q(w, qs, d if wt != orc.F16 else None, s if wt == orc.Q4_1 else None, M, Y2)
+    ctx.sync()
+    a, b = Y1.download(np.float32, (M, N)), Y2.download(np.float32, (M, N))
+    assert np.array_equal(a, b)
+    ref = orc.mul_mat(wt, wb, N, K, X)
+    assert orc.rel_l2(b, ref) <= 1e-5
 
 
 @pytest.mark.parametrize("rows,n", [(5184, 1024), (77, 96), (33, 4096)])
