@@ -21,8 +21,8 @@
 // filled by global_load_lds_dwordx4 (no register staging): stage s+2 is in
 // flight while stage s is consumed, and one barrier per stage orders reuse.
 // LDS rows are 128 bytes with 16-byte chunks XOR-swizzled by row (chunk c of
-// row r at slot c ^ (r & 7)), which keeps both the lane-ordered DMA writes
-// and the MFMA operand reads free of bank conflicts without padding.  Scales
+// row r at slot c ^ ((r >> 1) & 7)), which keeps both the lane-ordered DMA
+// writes and the MFMA operand reads free of bank conflicts without padding.  Scales
 // arrive from stage-major planes, so a stage's scales for the tile are one
 // contiguous run.  Work-group ids are remapped so that each XCD (ids are dealt
 // round-robin over 8) gets a contiguous range of tiles, rastered in groups of
@@ -122,6 +122,15 @@ __device__ __forceinline__ void quant_block32(const float *v, int8_t *qdst, uint
     if (sdst) *sdst = f2h_bits(d * (float)sum);
 }
 
+// XOR swizzle of the 16-byte chunks of LDS row r: chunk c lives at slot
+// c ^ swz(r).  gfx950's LDS has 64 banks of 4 bytes, so one 128-byte row
+// covers half of them and rows r, r+2, ... share banks: swz(r) = (r >> 1) & 7
+// gives the 16 rows that one ds_read_b128 phase touches distinct bank groups.
+#ifndef S3E_SWZ_SHIFT
+#define S3E_SWZ_SHIFT 1
+#endif
+__device__ __forceinline__ int swz(int r) { return (r >> S3E_SWZ_SHIFT) & 7; }
+
 // Wait until at most N of this wave's vector-memory operations are
 // outstanding and all its LDS reads have returned, then join the work-group.
 // The memory clobber keeps the compiler from moving LDS accesses across it.
@@ -156,22 +165,24 @@ __global__ __launch_bounds__(NTHR, 256 / BM) void k_gemm(GemmParams p) {
     const int lr = lane & 31, lh = lane >> 5;
 
     // ---- per-lane DMA sources: lane writes LDS bytes [16·lane, 16·lane+16) of
-    // a 1 KB run = 8 rows; it fetches chunk (lane & 7) ^ (lane >> 3) of row lane >> 3
+    // a 1 KB run = 8 rows, i.e. slot lane & 7 of row lane >> 3 of the run; it
+    // fetches the chunk that belongs there
     const int dma_row = lane >> 3;
-    const int dma_cofs = (((lane & 7) ^ dma_row) << 4);
     const uint8_t *a_src[C::NA];
+    int a_cofs[C::NA];
 #pragma unroll
     for (int j = 0; j < C::NA; j++) {
         const int row = 8 * (wave * C::NA + j) + dma_row;
         const int gm = min(m0 + row, p.M - 1);
         a_src[j] = p.a + (int64_t)gm * p.a_ld;
+        a_cofs[j] = ((lane & 7) ^ swz(row)) << 4;
     }
     const int64_t a_last = p.a_kbytes - 16;
     const uint8_t *b_src[C::NB];
 #pragma unroll
     for (int j = 0; j < C::NB; j++) {
         const int col = 8 * (wave * C::NB + j) + dma_row;
-        b_src[j] = p.b + (int64_t)(n0 + col) * p.b_ld + dma_cofs;
+        b_src[j] = p.b + (int64_t)(n0 + col) * p.b_ld + (((lane & 7) ^ swz(col)) << 4);
     }
     const uint8_t *s_src[C::NS > 0 ? C::NS : 1];
     int64_t s_step[C::NS > 0 ? C::NS : 1];
@@ -206,7 +217,7 @@ __global__ __launch_bounds__(NTHR, 256 / BM) void k_gemm(GemmParams p) {
         uint8_t *L = lds + (s % NBUF) * C::STAGE;
 #pragma unroll
         for (int j = 0; j < C::NA; j++) {
-            const int64_t off = min((int64_t)s * ROWB + dma_cofs, a_last);
+            const int64_t off = min((int64_t)s * ROWB + a_cofs[j], a_last);
             __builtin_amdgcn_global_load_lds((const void *)(a_src[j] + off),
                                              LDS_PTR(L + C::OFF_A + (wave * C::NA + j) * 1024), 16, 0, 0);
         }
@@ -223,7 +234,7 @@ __global__ __launch_bounds__(NTHR, 256 / BM) void k_gemm(GemmParams p) {
     };
 
     // ---- per-lane operand offsets ----
-    const int xr = lr & 7;
+    const int xr = swz(lr);  // tile rows start at multiples of 32
     int a_off[MT], ad_off[MT];
 #pragma unroll
     for (int i = 0; i < MT; i++) {

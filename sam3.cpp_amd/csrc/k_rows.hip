@@ -15,49 +15,41 @@ __device__ __forceinline__ double wave_sum_d(double v) {
     return v;
 }
 
-// Write 16 consecutive values (one lane's chunk, half of a 32-block) in the
-// activation format.  Lanes 2j and 2j+1 together hold one 32-element block.
-__device__ __forceinline__ void emit16(const float *v, const Act &o, int64_t row, int64_t col,
-                                       int lane) {
+// Write 4 consecutive values (columns col..col+3, col % 4 == 0) in the
+// activation format.  For the Q8 formats the 8 lanes 8k..8k+7 of the wave
+// must hold the 8 float4 of one 32-element block, in order.
+__device__ __forceinline__ void emit4(const float *v, const Act &o, int64_t row, int64_t col, int lane) {
     if (o.kind == A_F32) {
-        float4 *dst = (float4 *)((float *)o.x + row * o.ld + col);
-#pragma unroll
-        for (int j = 0; j < 4; j++) dst[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+        *(float4 *)((float *)o.x + row * o.ld + col) = make_float4(v[0], v[1], v[2], v[3]);
         return;
     }
     if (o.kind == A_F16) {
-        uint32_t w[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) w[j] = (uint32_t)f2h_bits(v[2 * j]) | ((uint32_t)f2h_bits(v[2 * j + 1]) << 16);
-        uint4 *dst = (uint4 *)((_Float16 *)o.x + row * o.ld + col);
-        dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
-        dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+        *(uint2 *)((_Float16 *)o.x + row * o.ld + col) =
+            make_uint2((uint32_t)f2h_bits(v[0]) | ((uint32_t)f2h_bits(v[1]) << 16),
+                       (uint32_t)f2h_bits(v[2]) | ((uint32_t)f2h_bits(v[3]) << 16));
         return;
     }
     // Q8_0 / Q8_1 as ggml's x86 quantize_row_q8_0 / q8_1: d = amax/127,
     // id = 127/amax, q = round-half-even(v·id), s = fp16(d·Σq).
-    float amax = 0.f;
-#pragma unroll
-    for (int j = 0; j < 16; j++) amax = fmaxf(amax, fabsf(v[j]));
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
     amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
     const float d = amax / 127.f;
     const float id = (amax != 0.f) ? 127.f / amax : 0.f;
     int sum = 0;
-    uint32_t w[4];
+    uint32_t packed = 0;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        uint32_t packed = 0;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int q = (int)__builtin_rintf(v[4 * j + i] * id);
-            sum += q;
-            packed |= ((uint32_t)(q & 0xff)) << (8 * i);
-        }
-        w[j] = packed;
+    for (int i = 0; i < 4; i++) {
+        const int q = (int)__builtin_rintf(v[i] * id);
+        sum += q;
+        packed |= ((uint32_t)(q & 0xff)) << (8 * i);
     }
-    *(uint4 *)((int8_t *)o.x + row * o.ld + col) = make_uint4(w[0], w[1], w[2], w[3]);
+    *(uint32_t *)((int8_t *)o.x + row * o.ld + col) = packed;
     sum += __shfl_xor(sum, 1, 64);
-    if ((lane & 1) == 0) {
+    sum += __shfl_xor(sum, 2, 64);
+    sum += __shfl_xor(sum, 4, 64);
+    if ((lane & 7) == 0) {
         const int64_t blk = scale_index(o.mp, row, col / QK);
         o.d[blk] = f2h_bits(d);
         // s = fp16(fp32(d·Σq)): f2h_bits keeps the fp32 rounding of the product
@@ -65,8 +57,9 @@ __device__ __forceinline__ void emit16(const float *v, const Act &o, int64_t row
     }
 }
 
-// One wave per row; lane L holds chunks L, L+64, ... of 16 elements.
-// NIT = ceil(K / 1024) iterations.
+// One wave per row; lane L holds float4 number L + 64·it of the row
+// (it < NIT = ceil(E / 256)), so every load and store of the wave is one
+// contiguous run.
 template <int NIT>
 __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ x, int64_t M, int64_t E,
                                                    float eps, const float *__restrict__ w,
@@ -75,43 +68,35 @@ __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ x, 
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= M) return;
-    const int nch = (int)(E / 16);
-    const float *xr = x + row * E;
-    float v[NIT][16];
+    const int nf4 = (int)(E / 4);
+    const float4 *xr = (const float4 *)(x + row * E);
+    float v[NIT][4];
     // ggml_norm: mean and variance accumulated in double, each rounded to
     // float once; centred values and squares in float.  With double sums the
     // summation order no longer shows in the float results, so the output
     // matches the CPU path bit for bit.
-    double s = 0.0;
 #pragma unroll
     for (int it = 0; it < NIT; it++) {
-        const int ch = lane + 64 * it;
-#pragma unroll
-        for (int j = 0; j < 16; j++) v[it][j] = 0.f;
-        if (ch < nch) {
-            const float4 *src = (const float4 *)(xr + ch * 16);
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const float4 q = src[j];
-                v[it][4 * j] = q.x; v[it][4 * j + 1] = q.y; v[it][4 * j + 2] = q.z; v[it][4 * j + 3] = q.w;
-            }
-#pragma unroll
-            for (int j = 0; j < 16; j++) s += (double)v[it][j];
-        }
+        const int f = lane + 64 * it;
+        const float4 q = (f < nf4) ? xr[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+        v[it][0] = q.x; v[it][1] = q.y; v[it][2] = q.z; v[it][3] = q.w;
     }
+    double s = 0.0;
+#pragma unroll
+    for (int it = 0; it < NIT; it++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) s += (double)v[it][j];
     s = wave_sum_d(s);
     const float mean = (float)(s / (double)E);
     double s2 = 0.0;
 #pragma unroll
     for (int it = 0; it < NIT; it++) {
-        const int ch = lane + 64 * it;
-        if (ch < nch) {
+        const bool ok = lane + 64 * it < nf4;
 #pragma unroll
-            for (int j = 0; j < 16; j++) {
-                const float c = __fsub_rn(v[it][j], mean);
-                v[it][j] = c;
-                s2 += (double)__fmul_rn(c, c);
-            }
+        for (int j = 0; j < 4; j++) {
+            const float c = __fsub_rn(v[it][j], mean);
+            v[it][j] = c;
+            if (ok) s2 += (double)__fmul_rn(c, c);
         }
     }
     s2 = wave_sum_d(s2);
@@ -119,53 +104,50 @@ __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ x, 
     const float scale = 1.0f / sqrtf(var + eps);
 #pragma unroll
     for (int it = 0; it < NIT; it++) {
-        const int ch = lane + 64 * it;
-        if (ch >= nch) continue;
-        const int64_t col = (int64_t)ch * 16;
+        const int f = lane + 64 * it;
+        if (64 * it >= nf4) break;  // whole wave past the row (nf4 is a multiple of 8)
+        if (f < nf4) {
+            const float4 wf = w ? ((const float4 *)w)[f] : make_float4(1.f, 1.f, 1.f, 1.f);
+            const float4 bf = b ? ((const float4 *)b)[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float wv[4] = {wf.x, wf.y, wf.z, wf.w}, bv[4] = {bf.x, bf.y, bf.z, bf.w};
 #pragma unroll
-        for (int j = 0; j < 16; j++) {
-            float t = __fmul_rn(v[it][j], scale);
-            if (w) t = __fmul_rn(t, w[col + j]);
-            if (b) t = __fadd_rn(t, b[col + j]);
-            v[it][j] = t;
+            for (int j = 0; j < 4; j++) {
+                float t = __fmul_rn(v[it][j], scale);
+                if (w) t = __fmul_rn(t, wv[j]);
+                if (b) t = __fadd_rn(t, bv[j]);
+                v[it][j] = t;
+            }
         }
-        if (y32) {
-            float4 *dst = (float4 *)(y32 + row * E + col);
-#pragma unroll
-            for (int j = 0; j < 4; j++) dst[j] = make_float4(v[it][4 * j], v[it][4 * j + 1], v[it][4 * j + 2], v[it][4 * j + 3]);
-        } else {
-            emit16(v[it], o, row, col, lane);
+        // the 8 lanes of a Q8 block are all inside or all past the row
+        if (f < nf4) {
+            if (y32) *(float4 *)(y32 + row * E + 4 * f) = make_float4(v[it][0], v[it][1], v[it][2], v[it][3]);
+            else emit4(v[it], o, row, 4 * (int64_t)f, lane);
         }
     }
 }
 
-// Plain conversion of f32 rows into an activation format (ggml from_float).
+// Plain conversion of f32 rows into an activation format (ggml from_float):
+// lane L of a wave converts float4 number 64·blockIdx.x + L of its row.
 __global__ __launch_bounds__(256) void k_rows_quant(const float *__restrict__ x, int64_t M, int64_t K, Act o) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.y * 4 + (threadIdx.x >> 6);
-    const int64_t ch = (int64_t)blockIdx.x * 64 + lane;  // chunk of 16
+    const int64_t f = (int64_t)blockIdx.x * 64 + lane;
     if (row >= M) return;
-    const int64_t nch = K / 16;
-    // chunks come in pairs (2j, 2j+1) inside one wave: nch is even (K % 32 == 0)
-    if (ch >= nch) {
+    // K % 32 == 0: the 8 lanes of a block are all inside or all past the row
+    if (f >= K / 4) {
         // blocks between K and the next multiple of 128 get zero scales: the
         // GEMM reads whole groups of four blocks
-        const int64_t nch4 = (K + 127) / 128 * 8;
-        if (ch < nch4 && (ch & 1) == 0 && (o.kind == A_Q8_0 || o.kind == A_Q8_1)) {
-            const int64_t blk = scale_index(o.mp, row, ch / 2);
+        const int64_t f4 = (K + 127) / 128 * 32;
+        if (f < f4 && (lane & 7) == 0 && (o.kind == A_Q8_0 || o.kind == A_Q8_1)) {
+            const int64_t blk = scale_index(o.mp, row, f / 8);
             o.d[blk] = 0;
             if (o.kind == A_Q8_1) o.s[blk] = 0;
         }
         return;
     }
-    float v[16];
-    const float4 *src = (const float4 *)(x + row * K + ch * 16);
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const float4 q = src[j];
-        v[4 * j] = q.x; v[4 * j + 1] = q.y; v[4 * j + 2] = q.z; v[4 * j + 3] = q.w;
-    }
-    emit16(v, o, row, ch * 16, lane);
+    const float4 q = ((const float4 *)(x + row * K))[f];
+    const float v[4] = {q.x, q.y, q.z, q.w};
+    emit4(v, o, row, 4 * f, lane);
 }
 
 // im2col for ggml_conv_2d_sk_p0 with a P×P kernel and stride P on a CHW image:
@@ -215,9 +197,11 @@ hipError_t launch_layernorm(const float *x, int64_t M, int64_t E, float eps, con
                             const float *b, const Act &out, float *y_f32, hipStream_t st) {
     if (E % 32 != 0 || E > 4096) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((M + 3) / 4));
-    if (E <= 1024) hipLaunchKernelGGL(k_layernorm<1>, grid, dim3(256), 0, st, x, M, E, eps, w, b, out, y_f32);
-    else if (E <= 2048) hipLaunchKernelGGL(k_layernorm<2>, grid, dim3(256), 0, st, x, M, E, eps, w, b, out, y_f32);
-    else hipLaunchKernelGGL(k_layernorm<4>, grid, dim3(256), 0, st, x, M, E, eps, w, b, out, y_f32);
+    if (E <= 256) hipLaunchKernelGGL(k_layernorm<1>, grid, dim3(256), 0, st, x, M, E, eps, w, b, out, y_f32);
+    else if (E <= 512) hipLaunchKernelGGL(k_layernorm<2>, grid, dim3(256), 0, st, x, M, E, eps, w, b, out, y_f32);
+    else if (E <= 1024) hipLaunchKernelGGL(k_layernorm<4>, grid, dim3(256), 0, st, x, M, E, eps, w, b, out, y_f32);
+    else if (E <= 2048) hipLaunchKernelGGL(k_layernorm<8>, grid, dim3(256), 0, st, x, M, E, eps, w, b, out, y_f32);
+    else hipLaunchKernelGGL(k_layernorm<16>, grid, dim3(256), 0, st, x, M, E, eps, w, b, out, y_f32);
     return hipGetLastError();
 }
 
@@ -225,8 +209,8 @@ hipError_t launch_rows_quant(AKind kind, const float *x, int64_t M, int64_t K, c
                              hipStream_t st) {
     (void)kind;
     if (K % 32 != 0) return hipErrorInvalidValue;
-    const int64_t nch = (K + 127) / 128 * 8;  // chunks of 16 up to the 128-element group
-    const dim3 grid((unsigned)((nch + 63) / 64), (unsigned)((M + 3) / 4));
+    const int64_t nf4 = (K + 127) / 128 * 32;  // float4 up to the 128-element group
+    const dim3 grid((unsigned)((nf4 + 63) / 64), (unsigned)((M + 3) / 4));
     hipLaunchKernelGGL(k_rows_quant, grid, dim3(256), 0, st, x, M, K, out);
     return hipGetLastError();
 }
