@@ -85,15 +85,36 @@ struct GemmParams {
     EpiArgs e;
 };
 
+// gelu_erf(x) = 0.5·x·(1 + erf(x/√2)) (ggml_vec_gelu_erf_f32), branch-free.
+// With z = |x|/√2, erfc(z) = t·P(t)·e^(−z²), t = 1/(1 + 0.63·z), P a degree-8
+// polynomial fitted by least squares to erfc(z)·e^(z²)/t on z ∈ [0, 6]
+// (relative error ≤ 3.1e-7 in float32; beyond z = 6, e^(−z²) < 3e-16 makes
+// the product vanish).  1 + erf(x/√2) is 2 − erfc(z) for x ≥ 0 and erfc(z)
+// for x < 0, so neither branch cancels.
 __device__ __forceinline__ float gelu_erf(float x) {
-    const float SQRT_2_INV = 0.70710678118654752440084436210484f;
-    return 0.5f * x * (1.0f + erff(x * SQRT_2_INV));
+    const float z = fabsf(x) * 0.70710678118654752440f;
+    const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.63f, z, 1.0f));
+    float P = 0.06951001286506653f;
+    P = __builtin_fmaf(P, t, -0.4178536534309387f);
+    P = __builtin_fmaf(P, t, 1.0159318447113037f);
+    P = __builtin_fmaf(P, t, -1.1790587902069092f);
+    P = __builtin_fmaf(P, t, 0.5140861868858337f);
+    P = __builtin_fmaf(P, t, -0.02842715010046959f);
+    P = __builtin_fmaf(P, t, 0.3184112310409546f);
+    P = __builtin_fmaf(P, t, 0.35179051756858826f);
+    P = __builtin_fmaf(P, t, 0.3556097745895386f);
+    const float e = __builtin_amdgcn_exp2f(-(z * z) * 1.4426950408889634f);
+    const float E = t * P * e;
+    const float w = (x >= 0.f) ? 2.0f - E : E;
+    return 0.5f * x * w;
 }
 
 __device__ __forceinline__ uint16_t f2h_bits(float v) { return half_bits(v); }
 
 // Quantize 32 values to one Q8 block the way ggml's x86 quantize_row_q8_0 /
-// q8_1 do: d = amax/127, id = 127/amax, q = round-half-even(v·id).
+// q8_1 do: d = amax/127, id = 127/amax, q = round-half-even(v·id).  The
+// product v·id is rounded to float first, then to an integer by adding
+// 1.5·2^23 (exact round-half-even for |v·id| ≤ 127), whose low byte is q.
 __device__ __forceinline__ void quant_block32(const float *v, int8_t *qdst, uint16_t *ddst,
                                               uint16_t *sdst) {
     float amax = 0.f;
@@ -101,19 +122,22 @@ __device__ __forceinline__ void quant_block32(const float *v, int8_t *qdst, uint
     for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(v[j]));
     const float d = amax / 127.f;
     const float id = (amax != 0.f) ? 127.f / amax : 0.f;
-    int sum = 0;
+    constexpr uint32_t MAGIC = 0x4B400000u;  // bits of 1.5·2^23
+    uint32_t usum = 0;
     uint32_t w[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-        uint32_t packed = 0;
+        uint32_t u[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int q = (int)__builtin_rintf(v[4 * j + i] * id);
-            sum += q;
-            packed |= ((uint32_t)(q & 0xff)) << (8 * i);
+            u[i] = __builtin_bit_cast(uint32_t, __fadd_rn(__fmul_rn(v[4 * j + i], id), 12582912.0f));
+            usum += u[i];
         }
-        w[j] = packed;
+        const uint32_t lo = __builtin_amdgcn_perm(u[1], u[0], 0x0c0c0400u);
+        const uint32_t hi = __builtin_amdgcn_perm(u[3], u[2], 0x0c0c0400u);
+        w[j] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
     }
+    const int sum = (int)(usum - 32u * MAGIC);
     uint4 *dst = (uint4 *)qdst;
     dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
     dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
@@ -478,7 +502,13 @@ __global__ __launch_bounds__(NTHR, 256 / BM) void k_gemm(GemmParams p) {
                 v[j] = x.x; v[j + 1] = x.y; v[j + 2] = x.z; v[j + 3] = x.w;
             }
 #pragma unroll
-            for (int j = 0; j < 32; j++) v[j] = gelu_erf(__fadd_rn(v[j], e.bias[gn0 + j]));
+            for (int j = 0; j < 32; j += 4) {
+                const float4 bb = *(const float4 *)(e.bias + gn0 + j);
+                v[j] = gelu_erf(__fadd_rn(v[j], bb.x));
+                v[j + 1] = gelu_erf(__fadd_rn(v[j + 1], bb.y));
+                v[j + 2] = gelu_erf(__fadd_rn(v[j + 2], bb.z));
+                v[j + 3] = gelu_erf(__fadd_rn(v[j + 3], bb.w));
+            }
             const Act &o = e.out;
             if (o.kind == A_F16) {
                 _Float16 *dst = (_Float16 *)o.x + (int64_t)gm * o.ld + gn0;
