@@ -15,8 +15,8 @@
 // fp16; F32 weights run on fp32 MFMA.
 //
 // Per work-group: 512 threads (8 waves as 2 along M × 4 along N), a BM×128
-// output tile (BM = 128, or 64 when there are too few tiles to fill 256
-// CUs), each wave BM/2 × 32.  K advances in stages of 128 bytes per row (4
+// output tile (BM = 64 is what the launcher uses; 128 also compiles), each
+// wave BM/2 × 32.  K advances in stages of 128 bytes per row (4
 // quant blocks, 64 fp16 or 32 f32).  Stages stream through a 3-deep LDS ring
 // filled by global_load_lds_dwordx4 (no register staging): stage s+2 is in
 // flight while stage s is consumed, and one barrier per stage orders reuse.
@@ -401,46 +401,51 @@ __global__ __launch_bounds__(NTHR, 256 / BM) void k_gemm(GemmParams p) {
         const int Nw = e.window * e.window;
         const int nwx = e.grid / e.window;
         if (sel == 2) {
-            // V is written transposed, [b][h][d][p]: one token row per thread so
-            // that a wave's stores for one d cover consecutive positions.
-            constexpr int NCG = NTHR / BM, CPG = BN / NCG;
-            const int row = t % BM, cg = t / BM;
-            const int gm = m0 + row;
-            if (gm < p.M) {
+            // Vᵀ [b][h][d][p]: a unit is one column d and 8 consecutive tokens.
+            // Window and image-row boundaries fall on multiples of 8 tokens
+            // (the launcher checks), so the 8 tokens are 8 consecutive
+            // positions p of one window: one 16-byte store per plane.
+            for (int u = t; u < BN * (BM / 8); u += NTHR) {
+                const int col = u / (BM / 8), r0 = (u % (BM / 8)) * 8;
+                const int gm = m0 + r0;
+                if (gm >= p.M) continue;
+                const int gn = n0 + col;
+                const float bv = e.bias[gn];
+                const int r2 = gn - 2 * e.E;
+                const int h = r2 / e.HD, d = r2 % e.HD;
                 const int py = gm / e.grid, px = gm % e.grid;
                 const int b = (py / e.window) * nwx + px / e.window;
                 const int pp = (py % e.window) * e.window + px % e.window;
-#pragma unroll 4
-                for (int c4 = 0; c4 < CPG / 4; c4++) {
-                    const float4 v = *(const float4 *)(Ct + row * C::CLD + cg * CPG + c4 * 4);
-                    const float vv[4] = {v.x, v.y, v.z, v.w};
+                uint32_t w[4], wl[4];
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const int gn = n0 + cg * CPG + c4 * 4 + i;
-                        const int r2 = gn - 2 * e.E;
-                        const int h = r2 / e.HD, d = r2 % e.HD;
-                        const float val = vv[i] + e.bias[gn];
-                        const int64_t o = ((int64_t)(b * e.NH + h) * e.HD + d) * e.vt_ld + pp;
-                        const _Float16 hv = to_half(val);
-                        e.vt[o] = hv;
-                        if (e.vt_lo) e.vt_lo[o] = (_Float16)(val - (float)hv);
-                    }
+                for (int j = 0; j < 4; j++) {
+                    const float v0 = Ct[(r0 + 2 * j) * C::CLD + col] + bv;
+                    const float v1 = Ct[(r0 + 2 * j + 1) * C::CLD + col] + bv;
+                    const _Float16 h0 = to_half(v0), h1 = to_half(v1);
+                    w[j] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+                    const _Float16 l0 = (_Float16)(v0 - (float)h0), l1 = (_Float16)(v1 - (float)h1);
+                    wl[j] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
                 }
+                const int64_t o = ((int64_t)(b * e.NH + h) * e.HD + d) * e.vt_ld + pp;
+                *(uint4 *)(e.vt + o) = make_uint4(w[0], w[1], w[2], w[3]);
+                if (e.vt_lo) *(uint4 *)(e.vt_lo + o) = make_uint4(wl[0], wl[1], wl[2], wl[3]);
             }
         } else {
-            for (int ch = t; ch < BM * 4; ch += NTHR) {
-                const int row = ch >> 2, cc = ch & 3;
+            // Q, K [b][h][p][d] with RoPE: a unit is one token and 16 columns
+            for (int u = t; u < BM * (BN / 16); u += NTHR) {
+                const int row = u / (BN / 16), cc = u % (BN / 16);
                 const int gm = m0 + row;
                 if (gm >= p.M) continue;
-                const int gn0 = n0 + cc * 32;
-                float v[32];
+                const int gn0 = n0 + cc * 16;
+                float v[16];
 #pragma unroll
-                for (int j = 0; j < 32; j += 4) {
-                    const float4 x = *(const float4 *)(Ct + row * C::CLD + cc * 32 + j);
-                    v[j] = x.x + e.bias[gn0 + j];
-                    v[j + 1] = x.y + e.bias[gn0 + j + 1];
-                    v[j + 2] = x.z + e.bias[gn0 + j + 2];
-                    v[j + 3] = x.w + e.bias[gn0 + j + 3];
+                for (int j = 0; j < 16; j += 4) {
+                    const float4 x = *(const float4 *)(Ct + row * C::CLD + cc * 16 + j);
+                    const float4 bb = *(const float4 *)(e.bias + gn0 + j);
+                    v[j] = x.x + bb.x;
+                    v[j + 1] = x.y + bb.y;
+                    v[j + 2] = x.z + bb.z;
+                    v[j + 3] = x.w + bb.w;
                 }
                 const int py = gm / e.grid, px = gm % e.grid;
                 const int b = (py / e.window) * nwx + px / e.window;
@@ -450,22 +455,23 @@ __global__ __launch_bounds__(NTHR, 256 / BM) void k_gemm(GemmParams p) {
                 if (e.freqs) {
                     // sam3_apply_rope: out_re = re·cos − im·sin, out_im = re·sin + im·cos,
                     // each product rounded on its own (separate ggml ops).
-                    const float *f = e.freqs + ((int64_t)pp * (e.HD / 2) + d0 / 2) * 2;
+                    const float4 *f4 = (const float4 *)(e.freqs + ((int64_t)pp * (e.HD / 2) + d0 / 2) * 2);
 #pragma unroll
-                    for (int j = 0; j < 32; j += 2) {
-                        const float c = f[j], s = f[j + 1];
-                        const float re = v[j], im = v[j + 1];
-                        const float a0 = __fmul_rn(re, c), a1 = __fmul_rn(im, s);
-                        const float a2 = __fmul_rn(re, s), a3 = __fmul_rn(im, c);
-                        v[j] = __fsub_rn(a0, a1);
-                        v[j + 1] = __fadd_rn(a2, a3);
+                    for (int j = 0; j < 16; j += 4) {
+                        const float4 cs = f4[j / 4];  // cos, sin of pairs j/2 and j/2 + 1
+                        const float c0 = cs.x, s0 = cs.y, c1 = cs.z, s1 = cs.w;
+                        const float re0 = v[j], im0 = v[j + 1], re1 = v[j + 2], im1 = v[j + 3];
+                        v[j] = __fsub_rn(__fmul_rn(re0, c0), __fmul_rn(im0, s0));
+                        v[j + 1] = __fadd_rn(__fmul_rn(re0, s0), __fmul_rn(im0, c0));
+                        v[j + 2] = __fsub_rn(__fmul_rn(re1, c1), __fmul_rn(im1, s1));
+                        v[j + 3] = __fadd_rn(__fmul_rn(re1, s1), __fmul_rn(im1, c1));
                     }
                 }
                 const int64_t o = ((int64_t)(b * e.NH + h) * Nw + pp) * e.HD + d0;
                 _Float16 *lo = sel == 0 ? e.q_lo : e.k_lo;
-                uint32_t w[16], wl[16];
+                uint32_t w[8], wl[8];
 #pragma unroll
-                for (int j = 0; j < 16; j++) {
+                for (int j = 0; j < 8; j++) {
                     const _Float16 h0 = to_half(v[2 * j]), h1 = to_half(v[2 * j + 1]);
                     w[j] = (uint32_t)__builtin_bit_cast(uint16_t, h0) |
                            ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
@@ -477,14 +483,10 @@ __global__ __launch_bounds__(NTHR, 256 / BM) void k_gemm(GemmParams p) {
                 uint4 *d4 = (uint4 *)((sel == 0 ? e.q : e.k) + o);
                 d4[0] = make_uint4(w[0], w[1], w[2], w[3]);
                 d4[1] = make_uint4(w[4], w[5], w[6], w[7]);
-                d4[2] = make_uint4(w[8], w[9], w[10], w[11]);
-                d4[3] = make_uint4(w[12], w[13], w[14], w[15]);
                 if (lo) {
                     uint4 *l4 = (uint4 *)(lo + o);
                     l4[0] = make_uint4(wl[0], wl[1], wl[2], wl[3]);
                     l4[1] = make_uint4(wl[4], wl[5], wl[6], wl[7]);
-                    l4[2] = make_uint4(wl[8], wl[9], wl[10], wl[11]);
-                    l4[3] = make_uint4(wl[12], wl[13], wl[14], wl[15]);
                 }
             }
         }
@@ -596,7 +598,7 @@ template <int WK>
 hipError_t dispatch_bm(int bm, Epi epi, GemmParams &p, hipStream_t st) {
     p.tiles_m = (p.M + bm - 1) / bm;
     p.ntiles = p.tiles_m * p.tiles_n;
-    return bm == 64 ? dispatch_epi<WK, 64>(epi, p, st) : dispatch_epi<WK, 128>(epi, p, st);
+    return dispatch_epi<WK, 64>(epi, p, st);
 }
 
 }  // namespace
@@ -622,9 +624,10 @@ hipError_t launch_gemm(const Weight &w, const Act &a, int64_t M, Epi epi, const 
     p.nstages = (int)(w.Kp / stage_k(w.kind));
     p.tiles_n = (int)(w.Np / BN);
     p.e = ea;
-    // 64-row tiles when 128-row tiles would not give every CU three tiles
-    const int64_t tiles128 = ((M + 127) / 128) * p.tiles_n;
-    const int bm = (tiles128 < 3 * 256) ? 64 : 128;
+    // 64-row tiles: two work-groups fit a CU (LDS and 128 VGPRs), so one
+    // work-group's epilogue overlaps the other's main loop; with 128-row tiles
+    // (one per CU) every CU alternates between the two phases.
+    const int bm = 64;
     switch (w.kind) {
         case WK_Q4_0: return dispatch_bm<WK_Q4_0>(bm, epi, p, st);
         case WK_Q4_1: return dispatch_bm<WK_Q4_1>(bm, epi, p, st);

@@ -605,6 +605,8 @@ extern "C" int s3e_model_load(s3e_ctx *ctx, const char *path, s3e_model **out) {
     if (m->E / m->heads != 64) { set_error("s3e_model_load: head dim %d not supported (64 only)", m->E / m->heads); return S3E_ERR_UNSUPPORTED; }
     if (m->E % 128 != 0) { set_error("s3e_model_load: embed dim %d must be a multiple of 128", m->E); return S3E_ERR_UNSUPPORTED; }
     if (m->grid % m->window != 0) { set_error("s3e_model_load: grid %d is not a multiple of the window %d", m->grid, m->window); return S3E_ERR_UNSUPPORTED; }
+    // the QKV epilogue moves 8 consecutive tokens of one window row at a time
+    if (m->window % 8 != 0) { set_error("s3e_model_load: window %d must be a multiple of 8", m->window); return S3E_ERR_UNSUPPORTED; }
     m->blocks.resize((size_t)m->depth);
     for (int i = 0; i < m->depth; i++) {
         for (int j = 0; j < m->n_global && j < 4; j++)
