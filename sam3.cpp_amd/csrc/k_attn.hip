@@ -2,17 +2,24 @@
 // replacement for ggml_flash_attn_ext (sam3.cpp:3774; isolated core at
 // sam3.cpp:6778-6823): O = softmax(scale·QKᵀ)·V, no mask, head dim 64.
 //
-// Layout: Q, K are fp16 [BH][N][64]; V arrives transposed, fp16 [BH][64][ldv],
-// which the QKV GEMM epilogue writes directly.  One work-group = 4 waves =
-// 128 queries of one (batch, head); each wave owns 32 queries.  The scores
-// are computed transposed, Sᵀ = K·Qᵀ (v_mfma_f32_32x32x16_f16, A = 32 keys ×
-// 16 d from LDS, B = Qᵀ held in registers for the whole kernel), so that in
-// the accumulator every lane holds 16 keys of ONE query (column = lane % 32)
-// and the softmax statistics are per-lane scalars.  The output is formed
+// Layout: Q, K are fp16 [BH][N][64]; V arrives transposed, fp16
+// [BH][64][vt_ld] with keys in vt_slot order, which the QKV GEMM epilogue
+// writes directly.  One work-group = 4 waves (one per SIMD) = 128 queries
+// of one (batch, head); each wave owns 32 queries, and waves past the last
+// query only help move tiles.  The scores are computed
+// transposed, Sᵀ = K·Qᵀ (v_mfma_f32_32x32x16_f16, A = 32 keys × 16 d from
+// LDS, B = Qᵀ held in registers for the whole kernel), so that in the
+// accumulator every lane holds 16 keys of ONE query (column = lane % 32) and
+// the softmax statistics are per-lane scalars.  The output is formed
 // transposed too, Oᵀ = Vᵀ·Pᵀ: the probabilities go from the Sᵀ accumulator
 // registers straight into the B operand (fp16) with no data movement, and the
-// keys of each K=16 MFMA step are the ones that lane already holds; the Vᵀ
-// A-operand is read from LDS with the same key order.
+// keys of each K=16 MFMA step are the ones that lane already holds; thanks to
+// the vt_slot order the matching Vᵀ A-operand is one 16-byte LDS read.
+//
+// K and Vᵀ tiles of 64 keys stream through a 2-deep LDS ring filled by
+// global_load_lds_dwordx4 (rows of 128 bytes, 16-byte chunks XOR-swizzled
+// by row for the 64-bank LDS): tile j+1 is in flight while tile j is used,
+// one barrier per tile.
 //
 // Precision.  SPLIT = false rounds Q, K, V and P to fp16 (fp32 accumulate).
 // SPLIT = true carries every operand as an fp16 pair x = hi + lo (hi =
@@ -23,29 +30,37 @@
 // rounding decisions, turning a 1e-4 difference into whole quantization
 // steps.
 //
-// Online softmax in the exp2 domain: x = s·scale·log2(e), running max m and
-// per-lane partial sum l, rescale of Oᵀ by exp2(m_old − m_new) per 64-key
-// tile; the two lanes sharing a query (l, l^32) agree on m through one
-// cross-half shuffle per tile and add their partial l at the end.
+// Online softmax in the exp2 domain: x = s·scale·log2(e), per-lane running
+// reference m and partial sum l.  m is only raised when a tile's maximum
+// exceeds it by more than 8 (p ≤ 2^8 meanwhile, well inside fp16 and fp32),
+// so the rescale of Oᵀ by exp2(m_old − m_new) is rare; the result is the
+// same quotient.  The two lanes sharing a query (l, l^32) agree on m through
+// one cross-half shuffle per tile and add their partial l at the end.
 //
 // The result leaves the kernel already in the next GEMM's activation format
 // (Q8_0 / Q8_1 per 32-d block exactly as ggml quantizes a row, fp16, or
 // f32), at row token(b, i) — the window un-partition of sam3.cpp:3784 folded
 // into the store address.
+#include <type_traits>
+
 #include "s3e_internal.h"
 
 namespace s3e {
 namespace {
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
-constexpr int AW = 4;           // waves per work-group
-constexpr int QT = 32 * AW;     // queries per work-group
-constexpr int KT = 64;          // keys per tile
-constexpr int KROW = 72;        // LDS row stride in halves (144 B)
-constexpr int TILE = KT * KROW; // halves per LDS tile
+#define LDS_PTR(p) ((__attribute__((address_space(3))) void *)(p))
+
+constexpr int AW = 4;             // waves per work-group (one per SIMD)
+constexpr int NTHR = 64 * AW;
+constexpr int QT = 32 * AW;       // queries per work-group
+constexpr int KT = 32;            // keys per tile
+constexpr int KPL = KT * 128;     // bytes of one K plane of a tile: 32 keys × 64 d
+constexpr int VPL = 64 * KT * 2;  // bytes of one Vᵀ plane of a tile: 64 d × 32 keys
 
 __device__ __forceinline__ uint16_t f2h_bits(float v) { return half_bits(v); }
 
@@ -53,15 +68,42 @@ __device__ __forceinline__ v16f mfma(const v8h &a, const v8h &b, const v16f &c) 
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// 16-byte chunk c of LDS row r sits at slot c ^ swz(r).  With 64 banks of 4
+// bytes, 128-byte K rows r and r+2 share banks (swzk), and 64-byte Vᵀ rows
+// r, r+4, r+8, r+12 do (swzv); either way the 16 rows one ds_read_b128 phase
+// touches land on distinct banks.
+__device__ __forceinline__ int swzk(int r) { return (r >> 1) & 7; }
+__device__ __forceinline__ int swzv(int r) { return (r >> 2) & 3; }
+
+// p − h for the fp16 value h in the low or high half of h2, exact, in one
+// v_fma_mix_f32 (h2·(−1) + p with h2 read as fp16)
+__device__ __forceinline__ float sub_lo_half(float p, uint32_t h2) {
+    float r;
+    __asm__("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(p));
+    return r;
+}
+__device__ __forceinline__ float sub_hi_half(float p, uint32_t h2) {
+    float r;
+    __asm__("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(p));
+    return r;
+}
+
+template <int N>
+__device__ __forceinline__ void wait_and_barrier() {
+    __asm__ volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
 template <bool SPLIT>
-__global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a, int ldv) {
+__global__ __launch_bounds__(NTHR, 3) void k_attn(AttnArgs a, int ldv) {
     constexpr int NP = SPLIT ? 2 : 1;  // planes: hi (and lo)
-    __shared__ __attribute__((aligned(16))) _Float16 Ks[NP * TILE];
-    __shared__ __attribute__((aligned(16))) _Float16 Vs[NP * TILE];
+    constexpr int KBUF = NP * KPL, VBUF = NP * VPL;
+    // K ring (2 tiles) then Vᵀ ring (2 tiles)
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * KBUF + 2 * VBUF];
 
     const int bh = blockIdx.y;
     const int q0 = blockIdx.x * QT;
-    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, lr = lane & 31, lh = lane >> 5;
+    const int t = threadIdx.x, lane = t & 63, lr = lane & 31, lh = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int qi = q0 + wave * 32 + lr;
     const bool qvalid = qi < a.Nq;
 
@@ -86,118 +128,186 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a, int ldv) {
 
     const int64_t koff = (int64_t)bh * a.Nkv * 64, voff = (int64_t)bh * 64 * ldv;
     const int ntiles = (a.Nkv + KT - 1) / KT;
+    uint8_t *const Kring = lds, *const Vring = lds + 2 * KBUF;
 
-    uint4 rk[NP][2], rv[NP][2];
-    auto gload = [&](int j) {
+    // DMA: per plane, a K tile is 4 runs of 1 KB (8 rows of 128 B) and a Vᵀ
+    // tile 4 runs of 1 KB (16 rows of 64 B); wave w moves run w.  A lane writes
+    // the 16 bytes at 16·lane of its run and fetches the chunk that belongs there.
+    // Rows past the keys are clamped onto real ones (their scores are masked,
+    // and Vᵀ keys past Nkv are zero).
+    auto issue_k = [&](int tt) {
+        uint8_t *L = Kring + (tt & 1) * KBUF;
+        const int r = 8 * wave + (lane >> 3);
+        const int ch = (lane & 7) ^ swzk(r);
+        const int64_t key = min(tt * KT + r, a.Nkv - 1);
 #pragma unroll
         for (int pl = 0; pl < NP; pl++) {
-            const _Float16 *kb = (pl == 0 ? a.k : a.k_lo) + koff;
-            const _Float16 *vb = (pl == 0 ? a.vt : a.vt_lo) + voff;
-#pragma unroll
-            for (int i = 0; i < 2; i++) {
-                const int cidx = t + 256 * i;
-                const int row = cidx >> 3, c16 = cidx & 7;
-                const int key = j * KT + row;
-                rk[pl][i] = key < a.Nkv ? *(const uint4 *)(kb + (int64_t)key * 64 + c16 * 8) : make_uint4(0, 0, 0, 0);
-                const int k0 = j * KT + c16 * 8;
-                rv[pl][i] = k0 < ldv ? *(const uint4 *)(vb + (int64_t)row * ldv + k0) : make_uint4(0, 0, 0, 0);
-            }
+            const _Float16 *src = (pl == 0 ? a.k : a.k_lo) + koff + key * 64 + ch * 8;
+            __builtin_amdgcn_global_load_lds((const void *)src, LDS_PTR(L + pl * KPL + wave * 1024), 16, 0, 0);
         }
     };
-    auto lstore = [&]() {
+    auto issue_v = [&](int tt) {
+        uint8_t *L = Vring + (tt & 1) * VBUF;
+        const int r = 16 * wave + (lane >> 2);
+        const int ch = (lane & 3) ^ swzv(r);
+        const int k0 = min(tt * KT + ch * 8, ldv - 8);
 #pragma unroll
-        for (int pl = 0; pl < NP; pl++)
-#pragma unroll
-            for (int i = 0; i < 2; i++) {
-                const int cidx = t + 256 * i;
-                const int row = cidx >> 3, c16 = cidx & 7;
-                *(uint4 *)(Ks + pl * TILE + row * KROW + c16 * 8) = rk[pl][i];
-                *(uint4 *)(Vs + pl * TILE + row * KROW + c16 * 8) = rv[pl][i];
-            }
+        for (int pl = 0; pl < NP; pl++) {
+            const _Float16 *src = (pl == 0 ? a.vt : a.vt_lo) + voff + (int64_t)r * ldv + k0;
+            __builtin_amdgcn_global_load_lds((const void *)src, LDS_PTR(L + pl * VPL + wave * 1024), 16, 0, 0);
+        }
     };
 
-    gload(0);
-    for (int j = 0; j < ntiles; j++) {
-        __syncthreads();  // previous tile fully consumed
-        lstore();
-        __syncthreads();
-        if (j + 1 < ntiles) gload(j + 1);
+    const int xk = swzk(lr), xv = swzv(lr);  // operand rows start at multiples of 32
 
-        // Sᵀ = K·Qᵀ for 64 keys × 32 queries
-        v16f s[2];
+    // Sᵀ = K·Qᵀ for the 32 keys of tile tt × 32 queries
+    auto qk = [&](int tt) {
+        const uint8_t *L = Kring + (tt & 1) * KBUF;
+        v16f acc = {};
 #pragma unroll
-        for (int kt = 0; kt < 2; kt++) {
-            v16f acc = {};
-#pragma unroll
-            for (int ds = 0; ds < 4; ds++) {
-                const int o_ = (kt * 32 + lr) * KROW + ds * 16 + lh * 8;
-                const v8h kh = *(const v8h *)(Ks + o_);
-                if constexpr (SPLIT) {
-                    const v8h kl = *(const v8h *)(Ks + TILE + o_);
-                    acc = mfma(kl, qf[0][ds], acc);
-                    acc = mfma(kh, qf[1][ds], acc);
-                }
-                acc = mfma(kh, qf[0][ds], acc);
+        for (int ds = 0; ds < 4; ds++) {
+            const int o_ = lr * 128 + (((2 * ds + lh) ^ xk) << 4);
+            const v8h kh = *(const v8h *)(L + o_);
+            if constexpr (SPLIT) {
+                const v8h kl = *(const v8h *)(L + KPL + o_);
+                acc = mfma(kl, qf[0][ds], acc);
+                acc = mfma(kh, qf[1][ds], acc);
             }
-            s[kt] = acc;
+            acc = mfma(kh, qf[0][ds], acc);
         }
-        const bool tail = (j + 1) * KT > a.Nkv;
-        float mloc = -INFINITY;
-#pragma unroll
-        for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                float x = s[kt][r] * c;
-                if (tail) {
-                    const int key = j * KT + kt * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                    if (key >= a.Nkv) x = -INFINITY;
-                }
-                s[kt][r] = x;
-                mloc = fmaxf(mloc, x);
-            }
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-        const float mnew = fmaxf(mrun, mloc);
-        const float alpha = exp2f(mrun - mnew);
-        mrun = mnew;
-        float ps = 0.f;
-        v8h pb[NP][2][2];
-#pragma unroll
-        for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-            for (int jj = 0; jj < 2; jj++)
-#pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    const float pv = exp2f(s[kt][8 * jj + i] - mnew);
-                    ps += pv;
-                    const _Float16 ph = (_Float16)pv;
-                    pb[0][kt][jj][i] = ph;
-                    if constexpr (SPLIT) pb[NP - 1][kt][jj][i] = (_Float16)(pv - (float)ph);
-                }
-        lsum = lsum * alpha + ps;
-#pragma unroll
-        for (int r = 0; r < 16; r++) { o[0][r] *= alpha; o[1][r] *= alpha; }
-
-        // Oᵀ += Vᵀ·Pᵀ
+        return acc;
+    };
+    // Oᵀ += Vᵀ·Pᵀ for the 32 keys of tile tt
+    auto pv = [&](int tt, const v8h (&ph)[2], const v8h (&pl)[2]) {
+        const uint8_t *L = Vring + (tt & 1) * VBUF;
 #pragma unroll
         for (int dt = 0; dt < 2; dt++)
 #pragma unroll
-            for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-                for (int jj = 0; jj < 2; jj++) {
-                    const int o_ = (dt * 32 + lr) * KROW + kt * 32 + 16 * jj + 4 * lh;
-                    const v4h lo = *(const v4h *)(Vs + o_);
-                    const v4h hi = *(const v4h *)(Vs + o_ + 8);
-                    const v8h vh = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                    if constexpr (SPLIT) {
-                        const v4h lo2 = *(const v4h *)(Vs + TILE + o_);
-                        const v4h hi2 = *(const v4h *)(Vs + TILE + o_ + 8);
-                        const v8h vl = {lo2[0], lo2[1], lo2[2], lo2[3], hi2[0], hi2[1], hi2[2], hi2[3]};
-                        o[dt] = mfma(vl, pb[0][kt][jj], o[dt]);
-                        o[dt] = mfma(vh, pb[NP - 1][kt][jj], o[dt]);
-                    }
-                    o[dt] = mfma(vh, pb[0][kt][jj], o[dt]);
+            for (int jj = 0; jj < 2; jj++) {
+                const int o_ = (dt * 32 + lr) * 64 + (((2 * jj + lh) ^ xv) << 4);
+                const v8h vh = *(const v8h *)(L + o_);
+                if constexpr (SPLIT) {
+                    const v8h vl = *(const v8h *)(L + VPL + o_);
+                    o[dt] = mfma(vl, ph[jj], o[dt]);
+                    o[dt] = mfma(vh, pl[jj], o[dt]);
                 }
+                o[dt] = mfma(vh, ph[jj], o[dt]);
+            }
+    };
+    // scaled maximum over the tile's 32 keys (both lane halves)
+    auto tmax = [&](const v16f &sv) {
+        float m = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; r++) m = fmaxf(m, sv[r]);
+        return fmaxf(m, __shfl_xor(m, 32, 64)) * c;
+    };
+    // keys past Nkv score −inf (only the last, partial tile)
+    auto mask = [&](v16f &sv, int tt) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int key = tt * KT + 8 * (r >> 2) + 4 * lh + (r & 3);
+            if (key >= a.Nkv) sv[r] = -INFINITY;
+        }
+    };
+    // P = exp2(s·c − m) as fp16 hi (+ lo) B operands; returns Σp
+    auto softmax = [&](const v16f &sv, float m, v8h (&ph)[2], v8h (&pl)[2]) {
+        const float nm = -m;
+        float ps = 0.f;
+#pragma unroll
+        for (int jj = 0; jj < 2; jj++) {
+            v4u hw, lw;
+#pragma unroll
+            for (int i = 0; i < 8; i += 2) {
+                const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[8 * jj + i], c, nm));
+                const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[8 * jj + i + 1], c, nm));
+                ps += p0;
+                ps += p1;
+                const uint32_t h2 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p0, p1));
+                hw[i / 2] = h2;
+                if constexpr (SPLIT)
+                    lw[i / 2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(sub_lo_half(p0, h2), sub_hi_half(p1, h2)));
+            }
+            ph[jj] = __builtin_bit_cast(v8h, hw);
+            if constexpr (SPLIT) pl[jj] = __builtin_bit_cast(v8h, lw);
+        }
+        return ps;
+    };
+    // Issue is in order within a wave: the scheduling barriers interleave the
+    // MFMA stream (Sᵀ of the next tile, Oᵀ of the previous) with the softmax
+    // VALU of the current tile, which then runs in the MFMA shadow.
+    auto interleave = [&]() {
+#pragma unroll
+        for (int i = 0; i < 24; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+            __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // VALU
+        }
+    };
+
+    // Software pipeline over tiles: iteration j forms Sᵀ(j+1) and Oᵀ += P(j−1)
+    // on MFMA while the VALU turns Sᵀ(j) into P(j).  The K ring holds tiles
+    // j+1 (read) and j+2 (in flight), the Vᵀ ring j−1 (read) and j (in
+    // flight).  The running reference m is raised only when a tile's maximum
+    // exceeds it by more than 8 (p ≤ 2^8 meanwhile); then Oᵀ, which then
+    // holds P(j−1) terms under the old m, is rescaled after this iteration's
+    // MFMAs.  (Two alternating register sets instead of the copies at the end
+    // of an iteration need more VGPRs than 3 waves per SIMD allow; the
+    // occupancy is worth more.)
+    const bool wave_live = q0 + wave * 32 < a.Nq;  // waves past the queries only move tiles
+    v16f s_cur = {}, s_next = {};
+    v8h ph_prev[2], pl_prev[2], ph_cur[2], pl_cur[2];
+    auto iter = [&](int j, auto has_qk, auto has_sm, auto masked, auto has_pv) {
+        wait_and_barrier<0>();  // K(j+1), Vᵀ(j−1) landed; tiles of j−1 released
+        if (j + 2 < ntiles) issue_k(j + 2);
+        if (j < ntiles) issue_v(j);
+        if (!wave_live) return;
+        bool raise = false;
+        float mnew = mrun, alpha = 1.f, ps = 0.f;
+        if constexpr (decltype(has_sm)::value) {
+            if constexpr (decltype(masked)::value) mask(s_cur, j);
+            const float mt = tmax(s_cur);
+            raise = mt > mrun + 8.f;
+            mnew = raise ? mt : mrun;
+            alpha = __builtin_amdgcn_exp2f(mrun - mnew);
+        }
+        if constexpr (decltype(has_qk)::value) s_next = qk(j + 1);
+        if constexpr (decltype(has_pv)::value) pv(j - 1, ph_prev, pl_prev);
+        if constexpr (decltype(has_sm)::value) ps = softmax(s_cur, mnew, ph_cur, pl_cur);
+        interleave();
+        if constexpr (decltype(has_sm)::value) {
+            lsum = lsum * alpha + ps;
+            if (__any(raise)) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) { o[0][r] *= alpha; o[1][r] *= alpha; }
+            }
+            mrun = mnew;
+        }
+        if constexpr (decltype(has_qk)::value) s_cur = s_next;
+        if constexpr (decltype(has_sm)::value) {
+#pragma unroll
+            for (int jj = 0; jj < 2; jj++) { ph_prev[jj] = ph_cur[jj]; pl_prev[jj] = pl_cur[jj]; }
+        }
+    };
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+    const bool partial = (a.Nkv % KT) != 0;
+
+    issue_k(0);
+    if (ntiles > 1) issue_k(1);
+    wait_and_barrier<0>();
+    if (wave_live) s_cur = qk(0);
+    // j = 0 .. ntiles: Sᵀ(j+1) while j+1 < ntiles, P(j) while j < ntiles
+    // (masked on a partial last tile), Oᵀ += P(j−1) from j = 1
+    if (ntiles == 1) {
+        if (partial) iter(0, F_{}, T_{}, T_{}, F_{});
+        else iter(0, F_{}, T_{}, F_{}, F_{});
+    } else {
+        iter(0, T_{}, T_{}, F_{}, F_{});
+        for (int j = 1; j + 1 < ntiles; j++) iter(j, T_{}, T_{}, F_{}, T_{});
+        if (partial) iter(ntiles - 1, F_{}, T_{}, T_{}, T_{});
+        else iter(ntiles - 1, F_{}, T_{}, F_{}, T_{});
     }
+    iter(ntiles, F_{}, F_{}, F_{}, T_{});
 
     lsum += __shfl_xor(lsum, 32, 64);
     const float inv = (lsum == 0.f) ? 0.f : 1.0f / lsum;
@@ -272,12 +382,11 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a, int ldv) {
 }  // namespace
 
 hipError_t launch_attn(const AttnArgs &a, hipStream_t st) {
-    // V rows are read 8 keys at a time: their stride is Nkv rounded up to 8
-    // (the producers pad with zeros).
-    const int ldv = (a.Nkv + 7) / 8 * 8;
+    // Vᵀ rows hold vt_ld_for(Nkv) keys (zero past Nkv, in vt_slot order)
+    const int ldv = (int)vt_ld_for(a.Nkv);
     const dim3 grid((unsigned)((a.Nq + QT - 1) / QT), (unsigned)a.BH);
-    if (a.q_lo) hipLaunchKernelGGL(k_attn<true>, grid, dim3(256), 0, st, a, ldv);
-    else hipLaunchKernelGGL(k_attn<false>, grid, dim3(256), 0, st, a, ldv);
+    if (a.q_lo) hipLaunchKernelGGL(k_attn<true>, grid, dim3(NTHR), 0, st, a, ldv);
+    else hipLaunchKernelGGL(k_attn<false>, grid, dim3(NTHR), 0, st, a, ldv);
     return hipGetLastError();
 }
 

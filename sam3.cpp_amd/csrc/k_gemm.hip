@@ -401,10 +401,11 @@ __global__ __launch_bounds__(NTHR, 256 / BM) void k_gemm(GemmParams p) {
         const int Nw = e.window * e.window;
         const int nwx = e.grid / e.window;
         if (sel == 2) {
-            // Vᵀ [b][h][d][p]: a unit is one column d and 8 consecutive tokens.
-            // Window and image-row boundaries fall on multiples of 8 tokens
-            // (the launcher checks), so the 8 tokens are 8 consecutive
-            // positions p of one window: one 16-byte store per plane.
+            // Vᵀ [b][h][d][slot]: a unit is one column d and 8 consecutive
+            // tokens.  Window and image-row boundaries fall on multiples of 8
+            // tokens (the model loader checks), so the 8 tokens are positions
+            // p..p+7 of one window, p % 8 == 0: two runs of 4 keys, each one
+            // 8-byte store per plane at its vt_slot.
             for (int u = t; u < BN * (BM / 8); u += NTHR) {
                 const int col = u / (BM / 8), r0 = (u % (BM / 8)) * 8;
                 const int gm = m0 + r0;
@@ -426,9 +427,14 @@ __global__ __launch_bounds__(NTHR, 256 / BM) void k_gemm(GemmParams p) {
                     const _Float16 l0 = (_Float16)(v0 - (float)h0), l1 = (_Float16)(v1 - (float)h1);
                     wl[j] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
                 }
-                const int64_t o = ((int64_t)(b * e.NH + h) * e.HD + d) * e.vt_ld + pp;
-                *(uint4 *)(e.vt + o) = make_uint4(w[0], w[1], w[2], w[3]);
-                if (e.vt_lo) *(uint4 *)(e.vt_lo + o) = make_uint4(wl[0], wl[1], wl[2], wl[3]);
+                const int64_t row = ((int64_t)(b * e.NH + h) * e.HD + d) * e.vt_ld;
+                const int64_t o0 = row + vt_slot(pp), o1 = row + vt_slot(pp + 4);
+                *(uint2 *)(e.vt + o0) = make_uint2(w[0], w[1]);
+                *(uint2 *)(e.vt + o1) = make_uint2(w[2], w[3]);
+                if (e.vt_lo) {
+                    *(uint2 *)(e.vt_lo + o0) = make_uint2(wl[0], wl[1]);
+                    *(uint2 *)(e.vt_lo + o1) = make_uint2(wl[2], wl[3]);
+                }
             }
         } else {
             // Q, K [b][h][p][d] with RoPE: a unit is one token and 16 columns

@@ -170,7 +170,8 @@ __global__ void k_im2col(const float *__restrict__ chw, int img, int P, int64_t 
     else ((float *)out)[idx] = val;
 }
 
-// f32 strided Q/K/V → fp16 [BH][N][64] for Q and K, [BH][64][ldt] for V.
+// f32 strided Q/K/V → fp16 [BH][N][64] for Q and K, [BH][64][ldt] for V
+// (keys in vt_slot order).
 // With lo != null the value is stored as the pair hi = fp16(v),
 // lo = fp16(v − hi) for split-precision attention.
 __global__ void k_attn_prep(const float *__restrict__ src, int64_t s1, int64_t s2, int64_t s3,
@@ -185,7 +186,7 @@ __global__ void k_attn_prep(const float *__restrict__ src, int64_t s1, int64_t s
     const int64_t b = idx / (64 * N * nh);
     const float v = src[b * s3 + h * s2 + i * s1 + d];
     const int64_t bh = b * nh + h;
-    const int64_t o = transpose ? (bh * 64 + d) * ldt + i : (bh * N + i) * 64 + d;
+    const int64_t o = transpose ? (bh * 64 + d) * ldt + vt_slot(i) : (bh * N + i) * 64 + d;
     const _Float16 hv = to_half(v);
     dst[o] = hv;
     if (lo) lo[o] = (_Float16)(v - (float)hv);

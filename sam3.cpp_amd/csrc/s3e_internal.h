@@ -101,14 +101,25 @@ struct EpiArgs {
     _Float16 *q = nullptr, *k = nullptr, *vt = nullptr;
     // low halves of the fp16 pairs (x = hi + lo) when attention runs split
     _Float16 *q_lo = nullptr, *k_lo = nullptr, *vt_lo = nullptr;
-    int vt_ld = 0;                 // row stride of Vᵀ in keys (multiple of 8)
+    int vt_ld = 0;                 // row stride of Vᵀ in keys (vt_ld_for of the window size)
 };
+
+// Vᵀ rows (fp16 [BH][64][vt_ld]) hold the keys of each aligned 16-key group
+// with the middle two quarters swapped: key q of a group sits at slot
+// vt_slot(q).  One 16-byte chunk then holds keys {0-3, 8-11} or {4-7, 12-15}
+// of a group, the 8 keys one lane half feeds to a K=16 MFMA step of the
+// attention kernel, so that operand is one LDS read.  vt_ld is the key count
+// rounded up to 16; keys past the count are zero.
+__host__ __device__ inline int64_t vt_slot(int64_t q) {
+    return (q & ~(int64_t)15) | (q & 3) | ((q & 4) << 1) | ((q & 8) >> 1);
+}
+__host__ __device__ inline int64_t vt_ld_for(int64_t nkv) { return (nkv + 15) / 16 * 16; }
 
 // Attention I/O.
 struct AttnArgs {
     const _Float16 *q = nullptr;   // [BH][Nq][64]
     const _Float16 *k = nullptr;   // [BH][Nkv][64]
-    const _Float16 *vt = nullptr;  // [BH][64][Nkv]
+    const _Float16 *vt = nullptr;  // [BH][64][vt_ld_for(Nkv)], keys in vt_slot order
     // low halves (x = hi + lo) for split-precision attention, else null
     const _Float16 *q_lo = nullptr, *k_lo = nullptr, *vt_lo = nullptr;
     int Nq = 0, Nkv = 0, NH = 0, BH = 0;

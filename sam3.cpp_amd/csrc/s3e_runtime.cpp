@@ -426,7 +426,7 @@ extern "C" int s3e_flash_attn_ext(s3e_ctx *ctx, const float *q, const int64_t q_
     if (Nq <= 0 || Nkv <= 0 || nh <= 0 || B <= 0) { set_error("s3e_flash_attn_ext: empty shape"); return S3E_ERR_INVALID; }
     if (prec != S3E_PREC_DEFAULT && prec != S3E_PREC_F32) { set_error("s3e_flash_attn_ext: unknown precision %d", prec); return S3E_ERR_INVALID; }
     HIP_TRY(hipSetDevice(ctx->device));
-    const int64_t ldv = round_up(Nkv, 8);
+    const int64_t ldv = vt_ld_for(Nkv);
     const int np = (prec == S3E_PREC_F32) ? 2 : 1;  // hi (+ lo) planes
     const size_t qn = (size_t)(B * nh * Nq * 64), kn = (size_t)(B * nh * Nkv * 64), vn = (size_t)(B * nh * ldv * 64);
     _Float16 *q16 = nullptr, *k16 = nullptr, *vt16 = nullptr;
@@ -766,12 +766,12 @@ extern "C" int s3e_state_create(s3e_ctx *ctx, const s3e_model *m, s3e_state **ou
     // Q, K, Vᵀ hold two fp16 planes each (hi, lo) for split-precision attention
     if (e == hipSuccess) e = hipMalloc(&st->q16, (size_t)(T * E * 2 * 2));
     if (e == hipSuccess) e = hipMalloc(&st->k16, (size_t)(T * E * 2 * 2));
-    // Vᵀ rows are padded to a multiple of 8 keys: size for the widest block.
+    // Vᵀ rows are padded to a multiple of 16 keys: size for the widest block.
     int64_t vt_elems = T * E;
     for (const Block &b : m->blocks) {
         const int64_t WS = b.global ? m->grid : m->window;
         const int64_t NW = (m->grid / WS) * (m->grid / WS);
-        vt_elems = std::max<int64_t>(vt_elems, NW * m->heads * 64 * round_up(WS * WS, 8));
+        vt_elems = std::max<int64_t>(vt_elems, NW * m->heads * 64 * vt_ld_for(WS * WS));
     }
     st->vt_elems = vt_elems;
     if (e == hipSuccess) e = hipMalloc(&st->vt16, (size_t)(vt_elems * 2 * 2));
@@ -837,7 +837,7 @@ hipError_t run_block(s3e_state *st, int bi, float *x) {
         eq.k_lo = st->k16 + T * E;
         eq.vt_lo = st->vt16 + st->vt_elems;
     }
-    eq.vt_ld = (Nw + 7) / 8 * 8;
+    eq.vt_ld = (int)vt_ld_for(Nw);
     e = launch_gemm(b.qkv, a_qkv, T, EPI_QKV, eq, s);
     if (e != hipSuccess) return e;
     // attention → activation for the proj weight, un-partitioned
