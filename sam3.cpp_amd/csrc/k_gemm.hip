@@ -14,12 +14,13 @@
 // accumulator.  F16 weights run on fp16 MFMA against activations rounded to
 // fp16; F32 weights run on fp32 MFMA.
 //
-// Per work-group: 512 threads (8 waves as 2 along M × 4 along N), a BM×128
-// output tile (BM = 64 is what the launcher uses; 128 also compiles), each
-// wave BM/2 × 32.  K advances in stages of 128 bytes per row (4
-// quant blocks, 64 fp16 or 32 f32).  Stages stream through a 3-deep LDS ring
-// filled by global_load_lds_dwordx4 (no register staging): stage s+2 is in
-// flight while stage s is consumed, and one barrier per stage orders reuse.
+// Per work-group: a 64×128 output tile and 4 waves (2 along M × 2 along N,
+// each 32×64; three work-groups per CU) or, for Q4_1, 8 waves (2 × 4, each
+// 32×32; two per CU).  K advances in stages of 128 bytes per row (4 quant
+// blocks, 64 fp16 or 32 f32).  Stages stream through a 2- or 3-deep LDS ring
+// filled by global_load_lds_dwordx4 (no register staging): the next stages
+// are in flight while stage s is consumed, and one barrier per stage orders
+// reuse.
 // LDS rows are 128 bytes with 16-byte chunks XOR-swizzled by row (chunk c of
 // row r at slot c ^ ((r >> 1) & 7)), which keeps both the lane-ordered DMA
 // writes and the MFMA operand reads free of bank conflicts without padding.  Scales
@@ -45,17 +46,25 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 #define LDS_PTR(p) ((__attribute__((address_space(3))) void *)(p))
 
 constexpr int BN = GEMM_BN;   // 128
-constexpr int NTHR = 512;
 constexpr int ROWB = 128;     // bytes per tile row per stage
-constexpr int NBUF = 3;       // LDS ring depth
+constexpr int CLD = BN + 4;   // fp32 C-tile row stride
 
-template <int WK, int BM_>
+// Tile configurations.  WAVES = 8: waves 2 (M) × 4 (N), each BM/2 × 32,
+// 3-deep ring, 4 waves per SIMD at BM = 64 (two work-groups per CU).
+// WAVES = 4: waves 2 × 2, each BM/2 × 64 (two MFMA column tiles share one A
+// fragment and one scale operand), 2-deep ring, three work-groups per CU.
+template <int WK, int BM_, int WAVES_>
 struct Cfg {
     static constexpr int BM = BM_;
+    static constexpr int WAVES = WAVES_;
+    static constexpr int NTH = 64 * WAVES;
     static constexpr bool quant = (WK == WK_Q4_0 || WK == WK_Q4_1 || WK == WK_Q8_0);
     static constexpr bool q41 = (WK == WK_Q4_1);
     static constexpr int esize = quant ? 1 : (WK == WK_F16 ? 2 : 4);
-    static constexpr int MT = BM / 64;                   // 32-row MFMA tiles per wave
+    static constexpr int WM = 2, WN = WAVES / 2;
+    static constexpr int MT = BM / (32 * WM);            // 32-row MFMA tiles per wave
+    static constexpr int NT = BN / (32 * WN);            // 32-column MFMA tiles per wave
+    static constexpr int NBUF = WAVES == 4 ? 2 : 3;      // LDS ring depth
     static constexpr int OFF_A = 0;
     static constexpr int OFF_B = BM * ROWB;
     static constexpr int OFF_SC = OFF_B + BN * ROWB;     // scales: AD | BD | AS | BMIN
@@ -64,14 +73,18 @@ struct Cfg {
     static constexpr int OFF_AS = OFF_BD + (quant ? BN * 8 : 0);
     static constexpr int OFF_BMIN = OFF_AS + (q41 ? BM * 8 : 0);
     static constexpr int STAGE = OFF_BMIN + (q41 ? BN * 8 : 0);
-    static constexpr int NA = BM / 64;                   // 1 KB A loads per wave per stage
-    static constexpr int NB = BN / 64;                   // 1 KB B loads per wave per stage
+    static constexpr int NA = BM / (8 * WAVES);          // 1 KB A loads per wave per stage
+    static constexpr int NB = BN / (8 * WAVES);          // 1 KB B loads per wave per stage
     static constexpr int SC = (STAGE - OFF_SC) / 256;    // 256 B scale loads per stage
-    static constexpr int NS = (SC + 7) / 8;              // ... per wave
+    static constexpr int NS = (SC + WAVES - 1) / WAVES;  // ... per wave
     static constexpr int NLOAD = NA + NB + NS;
-    static constexpr int CLD = BN + 4;                   // fp32 C-tile row stride
     static constexpr int RING = NBUF * STAGE;
     static constexpr int LDS = RING > BM * CLD * 4 ? RING : BM * CLD * 4;
+    // quant blocks: with one MFMA column tile per wave, blocks are software
+    // pipelined (MFMAs of block b+1 in flight during the VALU of block b);
+    // with two, the second tile's MFMAs cover the first tile's VALU and the
+    // registers of a second block set are not needed
+    static constexpr bool PIPE = NT * MT <= 1;
 };
 
 struct GemmParams {
@@ -163,238 +176,10 @@ __device__ __forceinline__ void wait_and_barrier() {
     __asm__ volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-template <int WK, int EPI, int BM>
-// 128-row tiles: 1 work-group per CU (LDS), 2 waves per SIMD; 64-row tiles: 2.
-__global__ __launch_bounds__(NTHR, 256 / BM) void k_gemm(GemmParams p) {
-    using C = Cfg<WK, BM>;
-    constexpr int MT = C::MT;
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[C::LDS];
-
-    // ---- tile of this work-group ----
-    const int per = gridDim.x >> 3;
-    const int logical = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
-    if (logical >= p.ntiles) return;
-    constexpr int GROUP = 8;
-    const int group = logical / (GROUP * p.tiles_n);
-    const int first_m = group * GROUP;
-    const int gsz = min(p.tiles_m - first_m, GROUP);
-    const int rem = logical - group * GROUP * p.tiles_n;
-    const int tm = first_m + rem % gsz, tn = rem / gsz;
-    const int m0 = tm * BM, n0 = tn * BN;
-
-    const int t = threadIdx.x;
-    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const int lane = t & 63;
-    const int wm = wave >> 2, wn = wave & 3;
-    const int lr = lane & 31, lh = lane >> 5;
-
-    // ---- per-lane DMA sources: lane writes LDS bytes [16·lane, 16·lane+16) of
-    // a 1 KB run = 8 rows, i.e. slot lane & 7 of row lane >> 3 of the run; it
-    // fetches the chunk that belongs there
-    const int dma_row = lane >> 3;
-    const uint8_t *a_src[C::NA];
-    int a_cofs[C::NA];
-#pragma unroll
-    for (int j = 0; j < C::NA; j++) {
-        const int row = 8 * (wave * C::NA + j) + dma_row;
-        const int gm = min(m0 + row, p.M - 1);
-        a_src[j] = p.a + (int64_t)gm * p.a_ld;
-        a_cofs[j] = ((lane & 7) ^ swz(row)) << 4;
-    }
-    const int64_t a_last = p.a_kbytes - 16;
-    const uint8_t *b_src[C::NB];
-#pragma unroll
-    for (int j = 0; j < C::NB; j++) {
-        const int col = 8 * (wave * C::NB + j) + dma_row;
-        b_src[j] = p.b + (int64_t)(n0 + col) * p.b_ld + (((lane & 7) ^ swz(col)) << 4);
-    }
-    const uint8_t *s_src[C::NS > 0 ? C::NS : 1];
-    int64_t s_step[C::NS > 0 ? C::NS : 1];
-    int s_dst[C::NS > 0 ? C::NS : 1];
-    if constexpr (C::quant) {
-#pragma unroll
-        for (int j = 0; j < C::NS; j++) {
-            // scale run k (256 B); waves past the last run repeat an earlier one
-            // (identical bytes to the identical place)
-            const int k = (wave + 8 * j) % C::SC;
-            int o = k * 256;
-            s_dst[j] = C::OFF_SC + o;
-            if (o < BM * 8) {
-                s_src[j] = p.a_d + ((int64_t)m0 * 4) * 2 + o;
-                s_step[j] = p.a_mp * 8;
-            } else if ((o -= BM * 8) < BN * 8) {
-                s_src[j] = p.b_d + ((int64_t)n0 * 4) * 2 + o;
-                s_step[j] = p.b_np * 8;
-            } else if ((o -= BN * 8) < BM * 8) {
-                s_src[j] = p.a_s + ((int64_t)m0 * 4) * 2 + o;
-                s_step[j] = p.a_mp * 8;
-            } else {
-                o -= BM * 8;
-                s_src[j] = p.b_m + ((int64_t)n0 * 4) * 2 + o;
-                s_step[j] = p.b_np * 8;
-            }
-            s_src[j] += lane * 4;
-        }
-    }
-
-    auto issue = [&](int s) {
-        uint8_t *L = lds + (s % NBUF) * C::STAGE;
-#pragma unroll
-        for (int j = 0; j < C::NA; j++) {
-            const int64_t off = min((int64_t)s * ROWB + a_cofs[j], a_last);
-            __builtin_amdgcn_global_load_lds((const void *)(a_src[j] + off),
-                                             LDS_PTR(L + C::OFF_A + (wave * C::NA + j) * 1024), 16, 0, 0);
-        }
-#pragma unroll
-        for (int j = 0; j < C::NB; j++)
-            __builtin_amdgcn_global_load_lds((const void *)(b_src[j] + (int64_t)s * ROWB),
-                                             LDS_PTR(L + C::OFF_B + (wave * C::NB + j) * 1024), 16, 0, 0);
-        if constexpr (C::quant) {
-#pragma unroll
-            for (int j = 0; j < C::NS; j++)
-                __builtin_amdgcn_global_load_lds((const void *)(s_src[j] + s * s_step[j]),
-                                                 LDS_PTR(L + s_dst[j]), 4, 0, 0);
-        }
-    };
-
-    // ---- per-lane operand offsets ----
-    const int xr = swz(lr);  // tile rows start at multiples of 32
-    int a_off[MT], ad_off[MT];
-#pragma unroll
-    for (int i = 0; i < MT; i++) {
-        const int r = wm * (32 * MT) + 32 * i + lr;
-        a_off[i] = C::OFF_A + r * ROWB;
-        ad_off[i] = r * 8;
-    }
-    const int bcol = wn * 32 + lr;
-    const int b_off = C::OFF_B + bcol * ROWB;
-    const int bd_off = bcol * 8;
-    int cofs[4];
-#pragma unroll
-    for (int q = 0; q < 4; q++) cofs[q] = ((2 * q + lh) ^ xr) << 4;
-
-    v16f acc[MT], accm[MT];
-#pragma unroll
-    for (int i = 0; i < MT; i++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) { acc[i][r] = 0.f; accm[i][r] = 0.f; }
-
-    // one quant block step: integer sums and scale products of MT tiles
-    struct QFrag {
-        v4i a[MT];
-        v4i b;
-        uint32_t da[MT];
-        uint32_t db;
-    };
-    auto qread = [&](const uint8_t *L, int blk, QFrag &f) {
-#pragma unroll
-        for (int i = 0; i < MT; i++) {
-            f.a[i] = *(const v4i *)(L + a_off[i] + cofs[blk]);
-            f.da[i] = *(const uint16_t *)(L + C::OFF_AD + ad_off[i] + 2 * blk);
-        }
-        f.b = *(const v4i *)(L + b_off + cofs[blk]);
-        f.db = *(const uint16_t *)(L + C::OFF_BD + bd_off + 2 * blk);
-    };
-    auto qmma = [&](const QFrag &f, v16i (&S)[MT], v16f (&Cs)[MT]) {
-        const v16i zi = {};
-        const v16f zf = {};
-        const v4u hb = {f.db, 0u, 0u, 0u};
-#pragma unroll
-        for (int i = 0; i < MT; i++) {
-            const v4u ha = {f.da[i], 0u, 0u, 0u};
-            S[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[i], f.b, zi, 0, 0, 0);
-            Cs[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, ha),
-                                                           __builtin_bit_cast(v8h, hb), zf, 0, 0, 0);
-        }
-    };
-    auto qvalu = [&](const v16i (&S)[MT], const v16f (&Cs)[MT]) {
-#pragma unroll
-        for (int i = 0; i < MT; i++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) acc[i][r] = __builtin_fmaf((float)S[i][r], Cs[i][r], acc[i][r]);
-    };
-
-    auto compute = [&](int s) {
-        const uint8_t *L = lds + (s % NBUF) * C::STAGE;
-        if constexpr (C::quant) {
-            QFrag f0, f1;
-            v16i S0[MT], S1[MT];
-            v16f C0[MT], C1[MT];
-            qread(L, 0, f0);
-            qread(L, 1, f1);
-            qmma(f0, S0, C0);
-            qread(L, 2, f0);
-            qmma(f1, S1, C1);
-            qvalu(S0, C0);
-            qread(L, 3, f1);
-            qmma(f0, S0, C0);
-            qvalu(S1, C1);
-            qmma(f1, S1, C1);
-            qvalu(S0, C0);
-            if constexpr (C::q41) {
-                // Σ_b s_x[m][b]·m_w[n][b] over the stage's 4 blocks, doubled like
-                // the scale products (both lane halves carry the values)
-                const uint2 mb = *(const uint2 *)(L + C::OFF_BMIN + bd_off);
-                const v4u hb = {mb.x, mb.y, 0u, 0u};
-#pragma unroll
-                for (int i = 0; i < MT; i++) {
-                    const uint2 sa = *(const uint2 *)(L + C::OFF_AS + ad_off[i]);
-                    const v4u ha = {sa.x, sa.y, 0u, 0u};
-                    accm[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, ha),
-                                                                     __builtin_bit_cast(v8h, hb), accm[i], 0, 0, 0);
-                }
-            }
-            qvalu(S1, C1);
-        } else if constexpr (WK == WK_F16) {
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++) {
-                const v8h bv = *(const v8h *)(L + b_off + cofs[ks]);
-#pragma unroll
-                for (int i = 0; i < MT; i++) {
-                    const v8h av = *(const v8h *)(L + a_off[i] + cofs[ks]);
-                    acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc[i], 0, 0, 0);
-                }
-            }
-        } else {
-#pragma unroll
-            for (int ks = 0; ks < 16; ks++) {
-                const int o = ((((ks >> 1) ^ xr)) << 4) + ((2 * (ks & 1) + lh) << 2);
-                const float bv = *(const float *)(L + b_off + o);
-#pragma unroll
-                for (int i = 0; i < MT; i++) {
-                    const float av = *(const float *)(L + a_off[i] + o);
-                    acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc[i], 0, 0, 0);
-                }
-            }
-        }
-    };
-
-    // ---- main loop: stage s+2 in flight while stage s is consumed ----
-    const int ns = p.nstages;
-    issue(0);
-    if (ns > 1) issue(1);
-    for (int s = 0; s < ns; s++) {
-        if (s + 1 < ns) wait_and_barrier<C::NLOAD>();
-        else wait_and_barrier<0>();
-        if (s + 2 < ns) issue(s + 2);
-        compute(s);
-    }
-    wait_and_barrier<0>();
-
-    // ---- stage the fp32 tile in LDS ----
-    float *Ct = (float *)lds;
-    constexpr float kScale = C::quant ? 0.5f : 1.0f;  // remove the doubled scale products
-#pragma unroll
-    for (int i = 0; i < MT; i++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int row = wm * (32 * MT) + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
-            float v = acc[i][r];
-            if constexpr (C::q41) v += accm[i][r];
-            Ct[row * C::CLD + bcol] = v * kScale;
-        }
-    __syncthreads();
-
+// Epilogue from the fp32 tile Ct [BM][CLD] in LDS (scaled, complete), run by
+// the NT_ threads of the work-group.
+template <int EPI, int BM, int NT_>
+__device__ __forceinline__ void epilogue(const GemmParams &p, const float *Ct, int m0, int n0, int t) {
     const EpiArgs &e = p.e;
     if constexpr (EPI == EPI_QKV) {
         const int sel = n0 / e.E;  // 0 = Q, 1 = K, 2 = V (a tile never straddles)
@@ -406,7 +191,7 @@ __global__ __launch_bounds__(NTHR, 256 / BM) void k_gemm(GemmParams p) {
             // tokens (the model loader checks), so the 8 tokens are positions
             // p..p+7 of one window, p % 8 == 0: two runs of 4 keys, each one
             // 8-byte store per plane at its vt_slot.
-            for (int u = t; u < BN * (BM / 8); u += NTHR) {
+            for (int u = t; u < BN * (BM / 8); u += NT_) {
                 const int col = u / (BM / 8), r0 = (u % (BM / 8)) * 8;
                 const int gm = m0 + r0;
                 if (gm >= p.M) continue;
@@ -420,8 +205,8 @@ __global__ __launch_bounds__(NTHR, 256 / BM) void k_gemm(GemmParams p) {
                 uint32_t w[4], wl[4];
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    const float v0 = Ct[(r0 + 2 * j) * C::CLD + col] + bv;
-                    const float v1 = Ct[(r0 + 2 * j + 1) * C::CLD + col] + bv;
+                    const float v0 = Ct[(r0 + 2 * j) * CLD + col] + bv;
+                    const float v1 = Ct[(r0 + 2 * j + 1) * CLD + col] + bv;
                     const _Float16 h0 = to_half(v0), h1 = to_half(v1);
                     w[j] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
                     const _Float16 l0 = (_Float16)(v0 - (float)h0), l1 = (_Float16)(v1 - (float)h1);
@@ -438,7 +223,7 @@ __global__ __launch_bounds__(NTHR, 256 / BM) void k_gemm(GemmParams p) {
             }
         } else {
             // Q, K [b][h][p][d] with RoPE: a unit is one token and 16 columns
-            for (int u = t; u < BM * (BN / 16); u += NTHR) {
+            for (int u = t; u < BM * (BN / 16); u += NT_) {
                 const int row = u / (BN / 16), cc = u % (BN / 16);
                 const int gm = m0 + row;
                 if (gm >= p.M) continue;
@@ -446,7 +231,7 @@ __global__ __launch_bounds__(NTHR, 256 / BM) void k_gemm(GemmParams p) {
                 float v[16];
 #pragma unroll
                 for (int j = 0; j < 16; j += 4) {
-                    const float4 x = *(const float4 *)(Ct + row * C::CLD + cc * 16 + j);
+                    const float4 x = *(const float4 *)(Ct + row * CLD + cc * 16 + j);
                     const float4 bb = *(const float4 *)(e.bias + gn0 + j);
                     v[j] = x.x + bb.x;
                     v[j + 1] = x.y + bb.y;
@@ -498,7 +283,7 @@ __global__ __launch_bounds__(NTHR, 256 / BM) void k_gemm(GemmParams p) {
         }
     } else if constexpr (EPI == EPI_GELU) {
         // full 32-column blocks guaranteed by the launcher (N % 32 == 0)
-        for (int ch = t; ch < BM * 4; ch += NTHR) {
+        for (int ch = t; ch < BM * 4; ch += NT_) {
             const int row = ch >> 2, cc = ch & 3;
             const int gm = m0 + row;
             const int gn0 = n0 + cc * 32;
@@ -506,7 +291,7 @@ __global__ __launch_bounds__(NTHR, 256 / BM) void k_gemm(GemmParams p) {
             float v[32];
 #pragma unroll
             for (int j = 0; j < 32; j += 4) {
-                const float4 x = *(const float4 *)(Ct + row * C::CLD + cc * 32 + j);
+                const float4 x = *(const float4 *)(Ct + row * CLD + cc * 32 + j);
                 v[j] = x.x; v[j + 1] = x.y; v[j + 2] = x.z; v[j + 3] = x.w;
             }
 #pragma unroll
@@ -545,10 +330,10 @@ __global__ __launch_bounds__(NTHR, 256 / BM) void k_gemm(GemmParams p) {
         const int f = t & 31;
         const int gn = n0 + 4 * f;
         const bool vec = (p.N % 4) == 0 && gn + 3 < p.N;
-        for (int row = t >> 5; row < BM; row += NTHR / 32) {
+        for (int row = t >> 5; row < BM; row += NT_ / 32) {
             const int gm = m0 + row;
             if (gm >= p.M || gn >= p.N) continue;
-            const float4 x = *(const float4 *)(Ct + row * C::CLD + 4 * f);
+            const float4 x = *(const float4 *)(Ct + row * CLD + 4 * f);
             float v[4] = {x.x, x.y, x.z, x.w};
             float *y = e.y + (int64_t)gm * e.ldy + gn;
             if constexpr (EPI == EPI_POS) {
@@ -581,30 +366,316 @@ __global__ __launch_bounds__(NTHR, 256 / BM) void k_gemm(GemmParams p) {
     }
 }
 
-template <int WK, int EPI, int BM>
+template <int WK, int EPI, int BM, int WAVES>
+__global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 3 : 256 / BM) void k_gemm(GemmParams p) {
+    using C = Cfg<WK, BM, WAVES>;
+    constexpr int MT = C::MT, NT = C::NT, NBUF = C::NBUF;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[C::LDS];
+
+    // ---- tile of this work-group ----
+    const int per = gridDim.x >> 3;
+    const int logical = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    if (logical >= p.ntiles) return;
+    constexpr int GROUP = 8;
+    const int group = logical / (GROUP * p.tiles_n);
+    const int first_m = group * GROUP;
+    const int gsz = min(p.tiles_m - first_m, GROUP);
+    const int rem = logical - group * GROUP * p.tiles_n;
+    const int tm = first_m + rem % gsz, tn = rem / gsz;
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    const int t = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int lane = t & 63;
+    const int wm = wave / C::WN, wn = wave % C::WN;
+    const int lr = lane & 31, lh = lane >> 5;
+
+    // ---- per-lane DMA sources: lane writes LDS bytes [16·lane, 16·lane+16) of
+    // a 1 KB run = 8 rows, i.e. slot lane & 7 of row lane >> 3 of the run; it
+    // fetches the chunk that belongs there
+    const int dma_row = lane >> 3;
+    const uint8_t *a_src[C::NA];
+    int a_cofs[C::NA];
+#pragma unroll
+    for (int j = 0; j < C::NA; j++) {
+        const int row = 8 * (wave * C::NA + j) + dma_row;
+        const int gm = min(m0 + row, p.M - 1);
+        a_src[j] = p.a + (int64_t)gm * p.a_ld;
+        a_cofs[j] = ((lane & 7) ^ swz(row)) << 4;
+    }
+    const int64_t a_last = p.a_kbytes - 16;
+    const uint8_t *b_src[C::NB];
+#pragma unroll
+    for (int j = 0; j < C::NB; j++) {
+        const int col = 8 * (wave * C::NB + j) + dma_row;
+        b_src[j] = p.b + (int64_t)(n0 + col) * p.b_ld + (((lane & 7) ^ swz(col)) << 4);
+    }
+    const uint8_t *s_src[C::NS > 0 ? C::NS : 1];
+    int64_t s_step[C::NS > 0 ? C::NS : 1];
+    int s_dst[C::NS > 0 ? C::NS : 1];
+    if constexpr (C::quant) {
+#pragma unroll
+        for (int j = 0; j < C::NS; j++) {
+            // scale run k (256 B); waves past the last run repeat an earlier one
+            // (identical bytes to the identical place)
+            const int k = (wave + WAVES * j) % C::SC;
+            int o = k * 256;
+            s_dst[j] = C::OFF_SC + o;
+            if (o < BM * 8) {
+                s_src[j] = p.a_d + ((int64_t)m0 * 4) * 2 + o;
+                s_step[j] = p.a_mp * 8;
+            } else if ((o -= BM * 8) < BN * 8) {
+                s_src[j] = p.b_d + ((int64_t)n0 * 4) * 2 + o;
+                s_step[j] = p.b_np * 8;
+            } else if ((o -= BN * 8) < BM * 8) {
+                s_src[j] = p.a_s + ((int64_t)m0 * 4) * 2 + o;
+                s_step[j] = p.a_mp * 8;
+            } else {
+                o -= BM * 8;
+                s_src[j] = p.b_m + ((int64_t)n0 * 4) * 2 + o;
+                s_step[j] = p.b_np * 8;
+            }
+            s_src[j] += lane * 4;
+        }
+    }
+
+    auto issue = [&](int s) {
+        uint8_t *L = lds + (s % NBUF) * C::STAGE;
+#pragma unroll
+        for (int j = 0; j < C::NA; j++) {
+            const int64_t off = min((int64_t)s * ROWB + a_cofs[j], a_last);
+            __builtin_amdgcn_global_load_lds((const void *)(a_src[j] + off),
+                                             LDS_PTR(L + C::OFF_A + (wave * C::NA + j) * 1024), 16, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < C::NB; j++)
+            __builtin_amdgcn_global_load_lds((const void *)(b_src[j] + (int64_t)s * ROWB),
+                                             LDS_PTR(L + C::OFF_B + (wave * C::NB + j) * 1024), 16, 0, 0);
+        if constexpr (C::quant) {
+#pragma unroll
+            for (int j = 0; j < C::NS; j++)
+                __builtin_amdgcn_global_load_lds((const void *)(s_src[j] + s * s_step[j]),
+                                                 LDS_PTR(L + s_dst[j]), 4, 0, 0);
+        }
+    };
+
+    // ---- per-lane operand offsets ----
+    const int xr = swz(lr);  // tile rows start at multiples of 32
+    int a_off[MT], ad_off[MT];
+#pragma unroll
+    for (int i = 0; i < MT; i++) {
+        const int r = wm * (32 * MT) + 32 * i + lr;
+        a_off[i] = C::OFF_A + r * ROWB;
+        ad_off[i] = r * 8;
+    }
+    int b_off[NT], bd_off[NT];
+#pragma unroll
+    for (int n = 0; n < NT; n++) {
+        const int bcol = wn * (32 * NT) + 32 * n + lr;
+        b_off[n] = C::OFF_B + bcol * ROWB;
+        bd_off[n] = bcol * 8;
+    }
+    int cofs[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) cofs[q] = ((2 * q + lh) ^ xr) << 4;
+
+    v16f acc[MT][NT], accm[MT][NT];
+#pragma unroll
+    for (int i = 0; i < MT; i++)
+#pragma unroll
+        for (int n = 0; n < NT; n++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) { acc[i][n][r] = 0.f; accm[i][n][r] = 0.f; }
+
+    // one quant block step: integer sums and scale products of MT × NT tiles
+    struct QFrag {
+        v4i a[MT], b[NT];
+        uint32_t da[MT], db[NT];
+    };
+    auto qread = [&](const uint8_t *L, int blk, QFrag &f) {
+#pragma unroll
+        for (int i = 0; i < MT; i++) {
+            f.a[i] = *(const v4i *)(L + a_off[i] + cofs[blk]);
+            f.da[i] = *(const uint16_t *)(L + C::OFF_AD + ad_off[i] + 2 * blk);
+        }
+#pragma unroll
+        for (int n = 0; n < NT; n++) {
+            f.b[n] = *(const v4i *)(L + b_off[n] + cofs[blk]);
+            f.db[n] = *(const uint16_t *)(L + C::OFF_BD + bd_off[n] + 2 * blk);
+        }
+    };
+    auto qmma = [&](const QFrag &f, v16i (&S)[MT][NT], v16f (&Cs)[MT][NT]) {
+        const v16i zi = {};
+        const v16f zf = {};
+#pragma unroll
+        for (int n = 0; n < NT; n++) {
+            const v4u hb = {f.db[n], 0u, 0u, 0u};
+#pragma unroll
+            for (int i = 0; i < MT; i++) {
+                const v4u ha = {f.da[i], 0u, 0u, 0u};
+                S[i][n] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[i], f.b[n], zi, 0, 0, 0);
+                Cs[i][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, ha),
+                                                                  __builtin_bit_cast(v8h, hb), zf, 0, 0, 0);
+            }
+        }
+    };
+    auto qvalu = [&](const v16i (&S)[MT][NT], const v16f (&Cs)[MT][NT]) {
+#pragma unroll
+        for (int n = 0; n < NT; n++)
+#pragma unroll
+            for (int i = 0; i < MT; i++)
+#pragma unroll
+                for (int r = 0; r < 16; r++)
+                    acc[i][n][r] = __builtin_fmaf((float)S[i][n][r], Cs[i][n][r], acc[i][n][r]);
+    };
+
+    auto compute = [&](int s) {
+        const uint8_t *L = lds + (s % NBUF) * C::STAGE;
+        if constexpr (C::quant) {
+            if constexpr (C::PIPE) {
+                QFrag f0, f1;
+                v16i S0[MT][NT], S1[MT][NT];
+                v16f C0[MT][NT], C1[MT][NT];
+                qread(L, 0, f0);
+                qread(L, 1, f1);
+                qmma(f0, S0, C0);
+                qread(L, 2, f0);
+                qmma(f1, S1, C1);
+                qvalu(S0, C0);
+                qread(L, 3, f1);
+                qmma(f0, S0, C0);
+                qvalu(S1, C1);
+                qmma(f1, S1, C1);
+                qvalu(S0, C0);
+                qvalu(S1, C1);
+            } else {
+#pragma unroll
+                for (int blk = 0; blk < 4; blk++) {
+                    QFrag f;
+                    v16i S[MT][NT];
+                    v16f Cs[MT][NT];
+                    qread(L, blk, f);
+                    qmma(f, S, Cs);
+                    qvalu(S, Cs);
+                }
+            }
+            if constexpr (C::q41) {
+                // Σ_b s_x[m][b]·m_w[n][b] over the stage's 4 blocks, doubled like
+                // the scale products (both lane halves carry the values)
+#pragma unroll
+                for (int n = 0; n < NT; n++) {
+                    const uint2 mb = *(const uint2 *)(L + C::OFF_BMIN + bd_off[n]);
+                    const v4u hb = {mb.x, mb.y, 0u, 0u};
+#pragma unroll
+                    for (int i = 0; i < MT; i++) {
+                        const uint2 sa = *(const uint2 *)(L + C::OFF_AS + ad_off[i]);
+                        const v4u ha = {sa.x, sa.y, 0u, 0u};
+                        accm[i][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                            __builtin_bit_cast(v8h, ha), __builtin_bit_cast(v8h, hb), accm[i][n], 0, 0, 0);
+                    }
+                }
+            }
+        } else if constexpr (WK == WK_F16) {
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) {
+                v8h bv[NT];
+#pragma unroll
+                for (int n = 0; n < NT; n++) bv[n] = *(const v8h *)(L + b_off[n] + cofs[ks]);
+#pragma unroll
+                for (int i = 0; i < MT; i++) {
+                    const v8h av = *(const v8h *)(L + a_off[i] + cofs[ks]);
+#pragma unroll
+                    for (int n = 0; n < NT; n++)
+                        acc[i][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv[n], acc[i][n], 0, 0, 0);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int ks = 0; ks < 16; ks++) {
+                const int o = ((((ks >> 1) ^ xr)) << 4) + ((2 * (ks & 1) + lh) << 2);
+                float bv[NT];
+#pragma unroll
+                for (int n = 0; n < NT; n++) bv[n] = *(const float *)(L + b_off[n] + o);
+#pragma unroll
+                for (int i = 0; i < MT; i++) {
+                    const float av = *(const float *)(L + a_off[i] + o);
+#pragma unroll
+                    for (int n = 0; n < NT; n++)
+                        acc[i][n] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv[n], acc[i][n], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    // ---- main loop: stage s+NBUF−1 in flight while stage s is consumed ----
+    const int ns = p.nstages;
+    if constexpr (NBUF == 3) {
+        issue(0);
+        if (ns > 1) issue(1);
+        for (int s = 0; s < ns; s++) {
+            if (s + 1 < ns) wait_and_barrier<C::NLOAD>();
+            else wait_and_barrier<0>();
+            if (s + 2 < ns) issue(s + 2);
+            compute(s);
+        }
+    } else {
+        issue(0);
+        for (int s = 0; s < ns; s++) {
+            wait_and_barrier<0>();  // stage s landed; every wave is done with stage s−1
+            if (s + 1 < ns) issue(s + 1);
+            compute(s);
+        }
+    }
+    wait_and_barrier<0>();
+
+    // ---- stage the fp32 tile in LDS ----
+    float *Ct = (float *)lds;
+    constexpr float kScale = C::quant ? 0.5f : 1.0f;  // remove the doubled scale products
+#pragma unroll
+    for (int i = 0; i < MT; i++)
+#pragma unroll
+        for (int n = 0; n < NT; n++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int row = wm * (32 * MT) + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
+                float v = acc[i][n][r];
+                if constexpr (C::q41) v += accm[i][n][r];
+                Ct[row * CLD + wn * (32 * NT) + 32 * n + lr] = v * kScale;
+            }
+    __syncthreads();
+
+    epilogue<EPI, BM, C::NTH>(p, Ct, m0, n0, t);
+}
+
+template <int WK, int EPI, int BM, int WAVES>
 hipError_t launch_one(const GemmParams &p, hipStream_t st) {
     const int grid = ((p.ntiles + 7) / 8) * 8;
-    hipLaunchKernelGGL((k_gemm<WK, EPI, BM>), dim3(grid), dim3(NTHR), 0, st, p);
+    hipLaunchKernelGGL((k_gemm<WK, EPI, BM, WAVES>), dim3(grid), dim3(64 * WAVES), 0, st, p);
     return hipGetLastError();
 }
 
-template <int WK, int BM>
+template <int WK, int WAVES>
 hipError_t dispatch_epi(Epi epi, const GemmParams &p, hipStream_t st) {
     switch (epi) {
-        case EPI_F32: return launch_one<WK, EPI_F32, BM>(p, st);
-        case EPI_RESID: return launch_one<WK, EPI_RESID, BM>(p, st);
-        case EPI_POS: return launch_one<WK, EPI_POS, BM>(p, st);
-        case EPI_GELU: return launch_one<WK, EPI_GELU, BM>(p, st);
-        case EPI_QKV: return launch_one<WK, EPI_QKV, BM>(p, st);
+        case EPI_F32: return launch_one<WK, EPI_F32, 64, WAVES>(p, st);
+        case EPI_RESID: return launch_one<WK, EPI_RESID, 64, WAVES>(p, st);
+        case EPI_POS: return launch_one<WK, EPI_POS, 64, WAVES>(p, st);
+        case EPI_GELU: return launch_one<WK, EPI_GELU, 64, WAVES>(p, st);
+        case EPI_QKV: return launch_one<WK, EPI_QKV, 64, WAVES>(p, st);
     }
     return hipErrorInvalidValue;
 }
 
 template <int WK>
-hipError_t dispatch_bm(int bm, Epi epi, GemmParams &p, hipStream_t st) {
-    p.tiles_m = (p.M + bm - 1) / bm;
+hipError_t dispatch_waves(Epi epi, GemmParams &p, hipStream_t st) {
+    constexpr int BM = 64;
+    p.tiles_m = (p.M + BM - 1) / BM;
     p.ntiles = p.tiles_m * p.tiles_n;
-    return dispatch_epi<WK, 64>(epi, p, st);
+    // 4-wave work-groups (three per CU, 4-12% faster on the SAM 3 shapes)
+    // except for Q4_1, whose extra minimum term needs more registers than
+    // three work-groups per CU leave
+    const int waves = (WK == WK_Q4_1) ? 8 : 4;
+    return waves == 4 ? dispatch_epi<WK, 4>(epi, p, st) : dispatch_epi<WK, 8>(epi, p, st);
 }
 
 }  // namespace
@@ -630,16 +701,15 @@ hipError_t launch_gemm(const Weight &w, const Act &a, int64_t M, Epi epi, const 
     p.nstages = (int)(w.Kp / stage_k(w.kind));
     p.tiles_n = (int)(w.Np / BN);
     p.e = ea;
-    // 64-row tiles: two work-groups fit a CU (LDS and 128 VGPRs), so one
-    // work-group's epilogue overlaps the other's main loop; with 128-row tiles
-    // (one per CU) every CU alternates between the two phases.
-    const int bm = 64;
+    // 64-row tiles: two or three work-groups share a CU, so one work-group's
+    // epilogue overlaps another's main loop; with 128-row tiles (one per CU)
+    // every CU alternates between the two phases.
     switch (w.kind) {
-        case WK_Q4_0: return dispatch_bm<WK_Q4_0>(bm, epi, p, st);
-        case WK_Q4_1: return dispatch_bm<WK_Q4_1>(bm, epi, p, st);
-        case WK_Q8_0: return dispatch_bm<WK_Q8_0>(bm, epi, p, st);
-        case WK_F16: return dispatch_bm<WK_F16>(bm, epi, p, st);
-        case WK_F32: return dispatch_bm<WK_F32>(bm, epi, p, st);
+        case WK_Q4_0: return dispatch_waves<WK_Q4_0>(epi, p, st);
+        case WK_Q4_1: return dispatch_waves<WK_Q4_1>(epi, p, st);
+        case WK_Q8_0: return dispatch_waves<WK_Q8_0>(epi, p, st);
+        case WK_F16: return dispatch_waves<WK_F16>(epi, p, st);
+        case WK_F32: return dispatch_waves<WK_F32>(epi, p, st);
     }
     return hipErrorInvalidValue;
 }
