@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define S3E_ABI_VERSION 2
+#define S3E_ABI_VERSION 3
 
 enum s3e_status {
     S3E_OK = 0,
@@ -206,6 +206,9 @@ typedef struct s3e_synth_cfg {
     int32_t ftype;
     uint64_t seed;
     float std;
+    /* necks (sam3.cpp:2562-2591): 0 none, 1 tracker only (visual-only
+     * file), 2 detector and tracker; neck_dim 0 means 256 */
+    int32_t neck, neck_dim;
 } s3e_synth_cfg;
 int s3e_synth_write(const char *path, const s3e_synth_cfg *cfg);
 

@@ -110,14 +110,41 @@ typedef struct orc_model orc_model;
 orc_model *orc_model_load(const char *path);      /* NULL on failure */
 void       orc_model_free(orc_model *m);
 const char *orc_last_error(void);
-/* hparams: img_size, patch, E, depth, heads, mlp, window, n_global, g0..g3, ftype */
+/* hparams: img_size, patch, E, depth, heads, mlp, window, n_global, g0..g3,
+ * ftype, neck_dim, visual_only, necks present (bit 0 trk, bit 1 det) */
 void orc_model_hparams(const orc_model *m, int32_t out[16]);
+/* A loaded tensor in its registered type (sam3.cpp:2461-2591). */
+typedef struct {
+    int type;
+    int64_t ne[4];
+    const void *data;
+} orc_tensor_view;
+int  orc_model_tensor(const orc_model *m, const char *prefix, const char *suffix, orc_tensor_view *out);
+void orc_set_error(const char *fmt, ...);
 /* Prefix (patch embed + tiled pos + ln_pre): chw [3][img][img] → x [T][E]. */
 int  orc_vit_prefix(const orc_model *m, const float *chw, float *x, int nthreads);
 /* One block in place on x [T][E]. */
 int  orc_vit_block(const orc_model *m, int idx, float *x, int nthreads);
 /* Whole backbone: chw → vit_output [T][E]. */
 int  orc_vit_encode(const orc_model *m, const float *chw, float *out, int nthreads);
+
+/* ---- SimpleFPN neck (sam3.cpp:3863-3921), NHWC activations --------------- */
+/* ggml_conv_transpose_2d_p0 with a 2×2 fp16 kernel ggml [2, 2, Cout, Cin]:
+ * x [H][W][Cin] → y [2H][2W][Cout] (no bias). */
+void orc_conv_transpose_2x2(const uint16_t *w16, int64_t Cin, int64_t Cout, const float *x, int64_t H,
+                            int64_t W, float *y, int nthreads);
+/* ggml_conv_2d, stride 1, padding pad: kernel ggml [KW, KH, Cin, Cout] of
+ * type ktype (F32 or F16); x [H][W][Cin] → y [OH][OW][Cout] (no bias). */
+void orc_conv2d(int ktype, const void *w, int64_t KW, int64_t KH, int64_t Cin, int64_t Cout, int64_t pad,
+                const float *x, int64_t H, int64_t W, float *y, int nthreads);
+/* ggml_pool_2d MAX 2×2 stride 2: x [H][W][C] → y [H/2][W/2][C]. */
+void orc_maxpool2x2(const float *x, int64_t H, int64_t W, int64_t C, float *y);
+/* sam3_sinusoidal_pe_2d (sam3.cpp:3597-3633): out [H][W][d_model]. */
+void orc_sinusoidal_pe_2d(int H, int W, int d_model, float *out);
+/* Sides of the four levels and their width D for neck "trk" or "det". */
+int  orc_neck_dims(const orc_model *m, const char *which, int64_t side[4], int64_t *D);
+/* The neck on vit_output x [G²][E]: out[i] receives side[i]² rows of D. */
+int  orc_neck(const orc_model *m, const char *which, const float *x, float *out[4], int nthreads);
 
 #ifdef __cplusplus
 }

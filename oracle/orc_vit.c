@@ -17,6 +17,7 @@
 #include <fcntl.h>
 #include <math.h>
 #include <omp.h>
+#include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -26,6 +27,12 @@
 
 static __thread char g_err[512];
 const char *orc_last_error(void) { return g_err; }
+void orc_set_error(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+}
 #define ORC_FAIL(...) do { snprintf(g_err, sizeof g_err, __VA_ARGS__); goto fail; } while (0)
 
 typedef struct {
@@ -37,6 +44,7 @@ typedef struct {
 
 typedef struct {
     int32_t img_size, patch, E, depth, heads, mlp, window, n_global, gidx[4];
+    int32_t neck_dim, visual_only;
 } orc_hp;
 
 struct orc_model {
@@ -118,8 +126,11 @@ orc_model *orc_model_load(const char *path) {
         m->hp.window = v[6];
         m->hp.n_global = v[7];
         for (int i = 0; i < m->hp.n_global && i < 4; i++) RD32(m->hp.gidx[i]);
-        /* remaining 27 fields (text .. visual_only) are read and ignored */
+        /* remaining 27 fields (text .. visual_only); the neck width and
+         * visual_only are kept */
         for (int i = 0; i < 27; i++) RD32(hpv[i]);
+        m->hp.neck_dim = hpv[6];
+        m->hp.visual_only = hpv[26];
     }
     m->t = (orc_tensor *)calloc((size_t)(n_tensors > 0 ? n_tensors : 1), sizeof(orc_tensor));
     for (int ti = 0; ti < n_tensors; ti++) {
@@ -140,7 +151,8 @@ orc_model *orc_model_load(const char *path) {
         if (off + bytes > fsize) ORC_FAIL("tensor %s: truncated data", t->name);
         const uint8_t *src = map + off;
         off += bytes;
-        if (strncmp(t->name, "vit.", 4) != 0) continue; /* encoder backbone only */
+        /* encoder backbone and necks only */
+        if (strncmp(t->name, "vit.", 4) != 0 && strncmp(t->name, "neck.", 5) != 0) continue;
         const int rt = registered_type(t->name, n_dims, t->ne[0], m->wtype);
         t->type = rt;
         const size_t out_bytes = orc_row_size(rt, t->ne[0]) * (size_t)(n_el / t->ne[0]);
@@ -185,6 +197,23 @@ void orc_model_hparams(const orc_model *m, int32_t out[16]) {
     out[4] = m->hp.heads; out[5] = m->hp.mlp; out[6] = m->hp.window; out[7] = m->hp.n_global;
     for (int i = 0; i < 4; i++) out[8 + i] = m->hp.gidx[i];
     out[12] = m->ftype;
+    out[13] = m->hp.neck_dim;
+    out[14] = m->hp.visual_only;
+    out[15] = (find(m, "neck.trk.0.conv_3x3.weight") ? 1 : 0) | (find(m, "neck.det.0.conv_3x3.weight") ? 2 : 0);
+}
+
+int orc_model_tensor(const orc_model *m, const char *prefix, const char *suffix, orc_tensor_view *out) {
+    char buf[96];
+    snprintf(buf, sizeof buf, "%s%s", prefix, suffix);
+    const orc_tensor *t = find(m, buf);
+    if (!t) {
+        snprintf(g_err, sizeof g_err, "tensor %s not in the model", buf);
+        return -1;
+    }
+    out->type = t->type;
+    for (int i = 0; i < 4; i++) out->ne[i] = t->ne[i];
+    out->data = t->data;
+    return 0;
 }
 
 /* ------------------------------------------------------------------------ */

@@ -195,7 +195,8 @@ extern "C" int s3e_synth_write(const char *path, const s3e_synth_cfg *cfg) {
     }
     const int E = cfg->embed_dim, P = cfg->patch, img = cfg->img_size, WS = cfg->window;
     if (E <= 0 || P <= 0 || img % P != 0 || cfg->heads <= 0 || E % cfg->heads != 0 || E % 32 != 0 ||
-        cfg->depth <= 0 || WS <= 0 || (img / P) % WS != 0 || (img / P) % 3 != 0) {
+        cfg->depth <= 0 || WS <= 0 || (img / P) % WS != 0 || (img / P) % 3 != 0 || cfg->neck < 0 ||
+        cfg->neck > 2 || cfg->neck_dim < 0) {
         set_error("s3e_synth_write: inconsistent hparams");
         return S3E_ERR_INVALID;
     }
@@ -234,6 +235,36 @@ extern "C" int s3e_synth_write(const char *path, const s3e_synth_cfg *cfg) {
         f.freq_scale = is_glob(i) ? (float)WS / (float)G : 1.0f;
         ts.push_back(f);
     }
+    // SimpleFPN necks (sam3.cpp:2562-2591): ggml conv kernels [kW, kH, Cin, Cout],
+    // deconvolution kernels [kW, kH, Cout, Cin]; 512 is the reference's
+    // fixed intermediate width.
+    const int D = cfg->neck_dim > 0 ? cfg->neck_dim : 256;
+    const int MID = 512;
+    auto add_neck = [&](const std::string &p) {
+        ts.push_back({p + "0.dconv_2x2_0.weight", {2, 2, MID, E}, 0, false, false});
+        ts.push_back({p + "0.dconv_2x2_0.bias", {MID}, 2, false, false});
+        ts.push_back({p + "0.dconv_2x2_1.weight", {2, 2, D, MID}, 0, false, false});
+        ts.push_back({p + "0.dconv_2x2_1.bias", {D}, 2, false, false});
+        ts.push_back({p + "0.conv_1x1.weight", {1, 1, D, D}, 0, false, false});
+        ts.push_back({p + "0.conv_1x1.bias", {D}, 2, false, false});
+        ts.push_back({p + "0.conv_3x3.weight", {3, 3, D, D}, 0, false, false});
+        ts.push_back({p + "0.conv_3x3.bias", {D}, 2, false, false});
+        ts.push_back({p + "1.dconv_2x2.weight", {2, 2, MID, E}, 0, false, false});
+        ts.push_back({p + "1.dconv_2x2.bias", {MID}, 2, false, false});
+        ts.push_back({p + "1.conv_1x1.weight", {1, 1, MID, D}, 0, false, false});
+        ts.push_back({p + "1.conv_1x1.bias", {D}, 2, false, false});
+        ts.push_back({p + "1.conv_3x3.weight", {3, 3, D, D}, 0, false, false});
+        ts.push_back({p + "1.conv_3x3.bias", {D}, 2, false, false});
+        for (int sc = 2; sc < 4; sc++) {
+            const std::string q = p + std::to_string(sc);
+            ts.push_back({q + ".conv_1x1.weight", {1, 1, E, D}, 0, false, false});
+            ts.push_back({q + ".conv_1x1.bias", {D}, 2, false, false});
+            ts.push_back({q + ".conv_3x3.weight", {3, 3, D, D}, 0, false, false});
+            ts.push_back({q + ".conv_3x3.bias", {D}, 2, false, false});
+        }
+    };
+    if (cfg->neck == 2) add_neck("neck.det.");
+    if (cfg->neck >= 1) add_neck("neck.trk.");
 
     // Generate and encode every tensor (in parallel: each has its own seed).
     std::vector<std::vector<uint8_t>> data(ts.size());
@@ -311,10 +342,10 @@ extern "C" int s3e_synth_write(const char *path, const s3e_synth_cfg *cfg) {
                             cfg->n_global > 2 ? cfg->global_idx[2] : -1,
                             cfg->n_global > 3 ? cfg->global_idx[3] : -1,
                             1024, 16, 24, 32, 49408, 256,  // text
-                            256,                           // neck_dim
+                            D,                             // neck_dim
                             6, 8, 2048, 6, 8, 2048, 200, 3, 1, 4,
                             256, 2, 3, 3, 64, 4, 7, 16, 2,
-                            1};                            // visual_only
+                            cfg->neck == 2 ? 0 : 1};       // visual_only
     for (int i = 0; i < 39; i++) w32(hp[i]);
     long pos = 16 + 39 * 4;
     for (size_t i = 0; i < ts.size(); i++) {

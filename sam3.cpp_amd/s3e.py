@@ -32,6 +32,7 @@ class SynthCfg(ctypes.Structure):
         ("heads", c_int32), ("mlp_ratio_x1000", c_int32), ("window", c_int32),
         ("n_global", c_int32), ("global_idx", c_int32 * 4),
         ("ftype", c_int32), ("seed", c_uint64), ("std", c_float),
+        ("neck", c_int32), ("neck_dim", c_int32),
     ]
 
 
@@ -103,8 +104,10 @@ def check(rc: int, what: str = "") -> None:
 
 def synth_write(path: str, *, img_size=1008, patch=14, embed_dim=1024, depth=32, heads=16,
                 mlp_ratio_x1000=4625, window=24, global_idx=(7, 15, 23, 31), ftype="q4_0",
-                seed=0, std=0.02, random_affine=False) -> None:
-    """Write a random-init SAM 3 visual-only model file (s3e_synth_write)."""
+                seed=0, std=0.02, random_affine=False, neck=1, neck_dim=256) -> None:
+    """Write a random-init SAM 3 model file (s3e_synth_write): the ViT
+    backbone plus the tracker neck (neck=1, a visual-only file), both necks
+    (neck=2) or none (neck=0)."""
     cfg = SynthCfg()
     cfg.img_size, cfg.patch, cfg.embed_dim, cfg.depth = img_size, patch, embed_dim, depth
     cfg.heads, cfg.mlp_ratio_x1000, cfg.window = heads, mlp_ratio_x1000, window
@@ -115,6 +118,7 @@ def synth_write(path: str, *, img_size=1008, patch=14, embed_dim=1024, depth=32,
     cfg.ftype = FTYPE_BY_NAME[ftype] if isinstance(ftype, str) else int(ftype)
     cfg.seed = seed
     cfg.std = -abs(std) if random_affine else abs(std)
+    cfg.neck, cfg.neck_dim = int(neck), int(neck_dim)
     check(LIB.s3e_synth_write(path.encode(), ctypes.byref(cfg)), "s3e_synth_write")
 
 

@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import struct
 import subprocess
 from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t, c_uint16, c_void_p
 
@@ -63,6 +64,13 @@ def _load():
         "orc_vit_prefix": (c_int, [P, P, P, c_int]),
         "orc_vit_block": (c_int, [P, c_int, P, c_int]),
         "orc_vit_encode": (c_int, [P, P, P, c_int]),
+        "orc_conv_transpose_2x2": (None, [P, c_int64, c_int64, P, c_int64, c_int64, P, c_int]),
+        "orc_conv2d": (None, [c_int, P, c_int64, c_int64, c_int64, c_int64, c_int64, P, c_int64, c_int64, P,
+                              c_int]),
+        "orc_maxpool2x2": (None, [P, c_int64, c_int64, c_int64, P]),
+        "orc_sinusoidal_pe_2d": (None, [c_int, c_int, c_int, P]),
+        "orc_neck_dims": (c_int, [P, c_char_p, P, P]),
+        "orc_neck": (c_int, [P, c_char_p, P, P, c_int]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -196,10 +204,93 @@ class OracleModel:
         assert LIB.orc_vit_encode(self.h, ptr(chw), ptr(x), nthreads) == 0, LIB.orc_last_error()
         return x
 
+    def neck_dims(self, which: str = "trk"):
+        side = np.zeros(4, np.int64)
+        D = np.zeros(1, np.int64)
+        assert LIB.orc_neck_dims(self.h, which.encode(), ptr(side), ptr(D)) == 0, LIB.orc_last_error()
+        return [int(v) for v in side], int(D[0])
+
+    def neck(self, x: np.ndarray, which: str = "trk", nthreads: int = 0):
+        """sam3_build_neck_graph on vit_output x [G², E] → four [side², D] levels."""
+        side, D = self.neck_dims(which)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        outs = [np.empty((s * s, D), np.float32) for s in side]
+        arr = (c_void_p * 4)(*[o.ctypes.data for o in outs])
+        rc = LIB.orc_neck(self.h, which.encode(), ptr(x), ctypes.cast(arr, c_void_p), nthreads)
+        assert rc == 0, LIB.orc_last_error()
+        return outs
+
     def __del__(self):
         if getattr(self, "h", None):
             LIB.orc_model_free(self.h)
             self.h = None
+
+
+def conv_transpose_2x2(w16: np.ndarray, x: np.ndarray, nthreads: int = 0) -> np.ndarray:
+    """w16: fp16 bits in ggml order [Cin][Cout][2][2] (ne = [2, 2, Cout, Cin]);
+    x: [H, W, Cin] f32 → [2H, 2W, Cout]."""
+    Cin, Cout = w16.shape[0], w16.shape[1]
+    H, W = x.shape[0], x.shape[1]
+    w16 = np.ascontiguousarray(w16, dtype=np.uint16)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty((2 * H, 2 * W, Cout), np.float32)
+    LIB.orc_conv_transpose_2x2(ptr(w16), Cin, Cout, ptr(x), H, W, ptr(y), nthreads)
+    return y
+
+
+def conv2d(ktype: int, w: np.ndarray, x: np.ndarray, pad: int, nthreads: int = 0) -> np.ndarray:
+    """w in ggml order [Cout][Cin][KH][KW] (ne = [KW, KH, Cin, Cout]) as f32 or
+    fp16 bits; x: [H, W, Cin] f32 → [OH, OW, Cout]."""
+    Cout, Cin, KH, KW = w.shape
+    H, W = x.shape[0], x.shape[1]
+    w = np.ascontiguousarray(w, dtype=np.uint16 if ktype == F16 else np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    OH, OW = H + 2 * pad - KH + 1, W + 2 * pad - KW + 1
+    y = np.empty((OH, OW, Cout), np.float32)
+    LIB.orc_conv2d(ktype, ptr(w), KW, KH, Cin, Cout, pad, ptr(x), H, W, ptr(y), nthreads)
+    return y
+
+
+def maxpool2x2(x: np.ndarray) -> np.ndarray:
+    H, W, C = x.shape
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(((H - 2) // 2 + 1, (W - 2) // 2 + 1, C), np.float32)
+    LIB.orc_maxpool2x2(ptr(x), H, W, C, ptr(y))
+    return y
+
+
+def sinusoidal_pe_2d(H: int, W: int, d: int) -> np.ndarray:
+    out = np.empty((H, W, d), np.float32)
+    LIB.orc_sinusoidal_pe_2d(H, W, d, ptr(out))
+    return out
+
+
+def read_model_file(path: str):
+    """Tensor records of a sam3.cpp model file (sam3.cpp:3091-3143):
+    name → (dtype, ne, array in file order).  F32/F16 records are returned as
+    float32 / float16 arrays of shape ne reversed; others as raw bytes."""
+    data = open(path, "rb").read()
+    n = struct.unpack_from("<i", data, 12)[0]
+    off = 16 + 39 * 4
+    out = {}
+    for _ in range(n):
+        nd, nl, dt = struct.unpack_from("<iii", data, off)
+        off += 12
+        ne = struct.unpack_from(f"<{nd}i", data, off)
+        off += 4 * nd
+        name = data[off:off + nl].decode()
+        off += nl
+        off += (32 - off % 32) % 32
+        nel = int(np.prod(ne))
+        nbytes = {0: 4 * nel, 1: 2 * nel, 2: nel // 32 * 18, 3: nel // 32 * 20, 8: nel // 32 * 34}[dt]
+        raw = data[off:off + nbytes]
+        if dt in (0, 1):
+            arr = np.frombuffer(raw, np.float32 if dt == 0 else np.float16).reshape(tuple(reversed(ne)))
+        else:
+            arr = np.frombuffer(raw, np.uint8)
+        out[name] = (dt, tuple(ne), arr)
+        off += nbytes
+    return out
 
 
 def preprocess_sam3(img_hwc: np.ndarray, img_size: int) -> np.ndarray:

@@ -43,7 +43,7 @@ def test_exports_every_declared_symbol(s3e):
     for n in names:
         assert hasattr(s3e.LIB, n), n
     assert sorted(s3e.DECLARED) == names
-    assert s3e.LIB.s3e_abi_version() == 2
+    assert s3e.LIB.s3e_abi_version() == 3
 
 
 def read_file(path):
@@ -76,7 +76,8 @@ def test_synth_file_format(s3e, tmp_path, ft, code):
     assert (magic, version, ftype) == (0x73616D33, 3, code)
     assert hp[:8] == (168, 14, 1024, 2, 16, 4625, 4, 4) and hp[8:12] == (1, -1, -1, -1)
     assert hp[-1] == 1  # visual_only
-    assert len(t) == 4 + 13 * 2
+    assert hp[18] == 256  # neck_dim
+    assert len(t) == 4 + 13 * 2 + 22  # backbone + tracker neck
     for name, (dt, ne, off, raw) in t.items():
         assert off % 32 == 0, name
         if len(ne) == 1 or "pos_embed" in name or "freqs_cis" in name:
@@ -88,9 +89,30 @@ def test_synth_file_format(s3e, tmp_path, ft, code):
     assert t["vit.blocks.1.attn.freqs_cis"][1] == (2, 32, 144)
     assert t["vit.blocks.0.attn.freqs_cis"][1] == (2, 32, 16)
     assert t["vit.patch_embed.proj.weight"][1] == (14, 14, 3, 1024)
+    # neck kernels: conv [kW, kH, Cin, Cout], deconvolution [kW, kH, Cout, Cin]
+    assert t["neck.trk.0.dconv_2x2_0.weight"][1] == (2, 2, 512, 1024)
+    assert t["neck.trk.0.dconv_2x2_1.weight"][1] == (2, 2, 256, 512)
+    assert t["neck.trk.1.conv_1x1.weight"][1] == (1, 1, 512, 256)
+    assert t["neck.trk.3.conv_1x1.weight"][1] == (1, 1, 1024, 256)
+    assert t["neck.trk.2.conv_3x3.weight"][1] == (3, 3, 256, 256)
+    assert t["neck.trk.0.conv_3x3.bias"][1] == (256,)
     # the oracle reads the same file
     om = orc.OracleModel(p)
     assert om.hp[:8] == [168, 14, 1024, 2, 16, 4736, 4, 4]
+    assert om.hp[13:16] == [256, 1, 1]
+
+
+@pytest.mark.parametrize("neck,n_extra,visual_only", [(0, 0, 1), (2, 44, 0)])
+def test_synth_neck_options(s3e, tmp_path, neck, n_extra, visual_only):
+    p = str(tmp_path / f"n{neck}.ggml")
+    s3e.synth_write(p, img_size=168, depth=1, window=4, global_idx=(), ftype="q8_0", seed=2, neck=neck,
+                    neck_dim=128)
+    _, _, _, hp, t = read_file(p)
+    assert len(t) == 4 + 13 + n_extra
+    assert hp[-1] == visual_only and hp[18] == 128
+    if neck == 2:
+        assert t["neck.det.2.conv_3x3.weight"][1] == (3, 3, 128, 128)
+        assert orc.OracleModel(p).hp[15] == 3
 
 
 @pytest.mark.parametrize("ft,code", [("q4_0", 2), ("q4_1", 3), ("q8_0", 8)])
