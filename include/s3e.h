@@ -150,14 +150,17 @@ int s3e_flash_attn_ext(s3e_ctx *ctx,
                        float scale, int prec, float *o);
 
 /* ---- encoder -------------------------------------------------------------
- * Load the SAM 3 ViT backbone of a sam3.cpp model file (magic "sam3",
- * version 3; sam3.cpp:3200-3344).  Only the "vit." tensors are read; other
- * records are skipped, so full and visual-only files both load.  Replaces
- * the encoder part of sam3_load_model (sam3.h:184). */
+ * Load the SAM 3 image encoder of a sam3.cpp model file (magic "sam3",
+ * version 3; sam3.cpp:3200-3344): the ViT backbone ("vit.") and the
+ * SimpleFPN necks ("neck.trk.", and "neck.det." in full files;
+ * sam3.cpp:2562-2596).  Other records are skipped, so full and visual-only
+ * files both load; a file without neck records loads as a backbone-only
+ * encoder.  Replaces the encoder part of sam3_load_model (sam3.h:184). */
 int s3e_model_load(s3e_ctx *ctx, const char *path, s3e_model **out);
 void s3e_model_free(s3e_model *m);
 /* out[0..15]: img_size, patch, E, depth, heads, mlp, window, n_global,
- * global_idx[4], ftype, tokens per side, 0, 0. */
+ * global_idx[4], ftype, tokens per side, neck_dim, necks present (bit 0
+ * tracker, bit 1 detector). */
 int s3e_model_hparams(const s3e_model *m, int32_t out[16]);
 
 /* Per-image state holding activations and outputs (sam3_create_state,
@@ -168,8 +171,10 @@ void s3e_state_free(s3e_state *st);
 /* Encode a preprocessed CHW f32 image of img_size² (device pointer).
  * Replaces the graph build + compute of sam3_encode_image
  * (sam3.cpp:6051-6131) and sam3_encode_image_from_preprocessed
- * (sam3.cpp:7287-7482) for the backbone; result in state tensor
- * "vit_output" [E, W, H] = W*H rows of E f32. */
+ * (sam3.cpp:7287-7482): the backbone ("vit_output" [E, W, H] = W*H rows of
+ * E f32) and every neck of the model ("neck_trk_0..3", "neck_det_0..3"
+ * [D, S, S] with S = 4W, 2W, W, W/2; sam3_build_neck_graph,
+ * sam3.cpp:3863-3921). */
 int s3e_encode_chw(s3e_state *st, const float *chw_device);
 /* Same from host memory (uploads first). */
 int s3e_encode_chw_host(s3e_state *st, const float *chw_host);
@@ -183,10 +188,18 @@ int s3e_encode_image_u8(s3e_state *st, const uint8_t *hwc, int width, int height
  * runs ViT block idx in place on x. */
 int s3e_vit_prefix(s3e_state *st, const float *chw_device, float *x_device);
 int s3e_vit_block(s3e_state *st, int idx, float *x_device);
+/* Neck stage hook: run the model's necks on a backbone output given on the
+ * device (W*H rows of E f32), filling the state's neck_* tensors exactly as
+ * s3e_encode_chw does after the backbone (the neck part of the encode graph,
+ * sam3.cpp:6072-6075). */
+int s3e_run_neck(s3e_state *st, const float *x_device);
 
 /* State outputs by name (sam3_get_state_tensor_info / sam3_dump_state_tensor,
- * sam3.h:407-414, sam3.cpp:14334-14376).  Names: "vit_output".
- * ne receives the ggml shape; get copies n floats to host memory. */
+ * sam3.h:407-414, sam3.cpp:14334-14376).  Names: "vit_output",
+ * "neck_trk_<i>", "neck_det_<i>", "neck_det_pe_<i>", "neck_trk_pe_<i>" and
+ * "pe_<i>" (i = 0..3; the PEs of sam3_sinusoidal_pe_2d, sam3.cpp:6146-6193).
+ * A name the model does not produce is an error.  ne receives the ggml
+ * shape; get copies n floats to host memory. */
 int s3e_state_tensor_info(const s3e_state *st, const char *name, int64_t ne[4]);
 int s3e_state_tensor_get(const s3e_state *st, const char *name, float *host, size_t n);
 const float *s3e_state_tensor_device(const s3e_state *st, const char *name);

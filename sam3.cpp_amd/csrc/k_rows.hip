@@ -23,10 +23,21 @@ __device__ __forceinline__ void emit4(const float *v, const Act &o, int64_t row,
         *(float4 *)((float *)o.x + row * o.ld + col) = make_float4(v[0], v[1], v[2], v[3]);
         return;
     }
-    if (o.kind == A_F16) {
-        *(uint2 *)((_Float16 *)o.x + row * o.ld + col) =
-            make_uint2((uint32_t)f2h_bits(v[0]) | ((uint32_t)f2h_bits(v[1]) << 16),
-                       (uint32_t)f2h_bits(v[2]) | ((uint32_t)f2h_bits(v[3]) << 16));
+    if (o.kind == A_F16 || o.kind == A_F16X2) {
+        _Float16 h[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) h[i] = to_half(v[i]);
+        auto pack = [](_Float16 a, _Float16 b) {
+            return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+        };
+        *(uint2 *)((_Float16 *)o.x + row * o.ld + col) = make_uint2(pack(h[0], h[1]), pack(h[2], h[3]));
+        if (o.kind == A_F16X2) {
+            // low half: fp16 of the exact fp32 difference
+            _Float16 l[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) l[i] = (_Float16)(v[i] - (float)h[i]);
+            *(uint2 *)((_Float16 *)o.lo + row * o.ld + col) = make_uint2(pack(l[0], l[1]), pack(l[2], l[3]));
+        }
         return;
     }
     // Q8_0 / Q8_1 as ggml's x86 quantize_row_q8_0 / q8_1: d = amax/127,
@@ -192,7 +203,44 @@ __global__ void k_attn_prep(const float *__restrict__ src, int64_t s1, int64_t s
     if (lo) lo[o] = (_Float16)(v - (float)hv);
 }
 
+// NHWC f32 pixels → fp16 / split-fp16 activation rows, optionally through
+// the 2×2 stride-2 max pool (ggml_pool_2d MAX, sam3.cpp:3914): one thread per
+// 4 channels of an output pixel.
+__global__ __launch_bounds__(256) void k_pool_act(const float *__restrict__ x, int w, int c, int pool, int ow,
+                                                  int64_t n4, Act o) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    const int c4 = c / 4;
+    const int64_t pix = i / c4;
+    const int cc = (int)(i - pix * c4) * 4;
+    float4 v;
+    if (pool == 1) {
+        v = *(const float4 *)(x + pix * c + cc);
+    } else {
+        const int64_t oy = pix / ow, ox = pix - oy * ow;
+        const float *p0 = x + ((2 * oy) * w + 2 * ox) * c + cc;
+        const float4 a = *(const float4 *)p0, b = *(const float4 *)(p0 + c);
+        const float4 d = *(const float4 *)(p0 + (int64_t)w * c), e = *(const float4 *)(p0 + (int64_t)w * c + c);
+        v.x = fmaxf(fmaxf(a.x, b.x), fmaxf(d.x, e.x));
+        v.y = fmaxf(fmaxf(a.y, b.y), fmaxf(d.y, e.y));
+        v.z = fmaxf(fmaxf(a.z, b.z), fmaxf(d.z, e.z));
+        v.w = fmaxf(fmaxf(a.w, b.w), fmaxf(d.w, e.w));
+    }
+    const float vv[4] = {v.x, v.y, v.z, v.w};
+    emit4(vv, o, pix, cc, 0);
+}
+
 }  // namespace
+
+hipError_t launch_pool_act(const float *x, int h, int w, int c, int pool, const Act &out, hipStream_t st) {
+    if ((pool != 1 && pool != 2) || c % 4 != 0 || (out.kind != A_F16 && out.kind != A_F16X2) || out.ld != c ||
+        h < pool || w < pool)
+        return hipErrorInvalidValue;
+    const int oh = pool == 1 ? h : (h - 2) / 2 + 1, ow = pool == 1 ? w : (w - 2) / 2 + 1;
+    const int64_t n4 = (int64_t)oh * ow * (c / 4);
+    hipLaunchKernelGGL(k_pool_act, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, x, w, c, pool, ow, n4, out);
+    return hipGetLastError();
+}
 
 hipError_t launch_layernorm(const float *x, int64_t M, int64_t E, float eps, const float *w,
                             const float *b, const Act &out, float *y_f32, hipStream_t st) {

@@ -14,21 +14,25 @@ namespace s3e {
 // ggml block size of the quantized types (QK4_0 = QK4_1 = QK8_0 = QK8_1 = 32).
 constexpr int QK = 32;
 
-// Weight kinds as the GEMM kernels see them.
-enum WKind : int { WK_Q4_0 = 0, WK_Q4_1 = 1, WK_Q8_0 = 2, WK_F16 = 3, WK_F32 = 4 };
+// Weight kinds as the GEMM kernels see them.  WK_F16X3 holds f32 weights as
+// two fp16 planes (w·2^k = hi + lo) and multiplies f32 activations held the
+// same way: hi·hi + hi·lo + lo·hi on fp16 MFMA, fp32-accurate products.
+enum WKind : int { WK_Q4_0 = 0, WK_Q4_1 = 1, WK_Q8_0 = 2, WK_F16 = 3, WK_F32 = 4, WK_F16X3 = 5 };
 
 // Activation formats (what a producer writes for the next GEMM to read).
 //   A_Q8_0 : int8 qs[M][ld] + fp16 d[M][ld/32]          (vec_dot type of Q4_0/Q8_0)
 //   A_Q8_1 : as A_Q8_0 + fp16 s[M][ld/32] = fp16(d·Σq)   (vec_dot type of Q4_1)
 //   A_F16  : fp16 [M][ld]                                 (vec_dot type of F16)
 //   A_F32  : f32  [M][ld]                                 (vec_dot type of F32)
-enum AKind : int { A_Q8_0 = 0, A_Q8_1 = 1, A_F16 = 2, A_F32 = 3 };
+//   A_F16X2: fp16 hi [M][ld] + fp16 lo [M][ld], x = hi + lo  (f32 input of WK_F16X3)
+enum AKind : int { A_Q8_0 = 0, A_Q8_1 = 1, A_F16 = 2, A_F32 = 3, A_F16X2 = 4 };
 
 inline AKind act_kind_for(WKind w) {
     switch (w) {
         case WK_Q4_0: case WK_Q8_0: return A_Q8_0;
         case WK_Q4_1: return A_Q8_1;
         case WK_F16: return A_F16;
+        case WK_F16X3: return A_F16X2;
         default: return A_F32;
     }
 }
@@ -39,6 +43,7 @@ constexpr int ROW_PAD = 128;
 
 // A device activation buffer in one of the formats above.
 //   x : values, row-major [mp][ld] (int8 codes, fp16 or f32)
+//   lo: A_F16X2 only, the fp16 low plane, same shape as x
 //   d : fp16 block scales, and s: fp16 block sums (Q8_1), "stage-major":
 //       block b of row r at ((b / 4) * mp + r) * 4 + b % 4, so the four
 //       blocks one GEMM stage consumes for 128 consecutive rows are 1 KB of
@@ -48,6 +53,7 @@ struct Act {
     void *x = nullptr;
     uint16_t *d = nullptr;
     uint16_t *s = nullptr;
+    void *lo = nullptr;
     int64_t ld = 0;   // elements per row (multiple of 32)
     int64_t mp = 0;   // row pitch of the scale planes (rows rounded up to ROW_PAD)
 };
@@ -63,6 +69,10 @@ __host__ __device__ inline int64_t scale_index(int64_t mp, int64_t row, int64_t 
 //              expanded because the weights stay cache-resident in the large-M
 //              GEMM; d, m (Q4_1 minimum) fp16 stage-major [Kp/128][Np][4].
 //   F16/F32  : values [Np][Kp].
+//   F16X3    : q = hi, lo = low plane, both fp16 [Np][Kp], of the f32 weights
+//              scaled by 2^k so that the largest is in [2^14, 2^15): the low
+//              plane stays out of the fp16 subnormal range; alpha = 2^-k
+//              undoes the scale on the accumulator (exactly).
 // Kp pads K to the kernel's stage width, Np pads N to the tile width; the
 // padding is zero and contributes nothing.
 struct Weight {
@@ -72,6 +82,8 @@ struct Weight {
     void *q = nullptr;
     uint16_t *d = nullptr;
     uint16_t *m = nullptr;
+    void *lo = nullptr;
+    float alpha = 1.0f;
     size_t bytes = 0;
 };
 
@@ -82,6 +94,8 @@ enum Epi : int {
     EPI_POS = 2,     // y = acc + pos[tile(token)]          (patch embed + tiled pos_embed)
     EPI_GELU = 3,    // act = quant(gelu_erf(acc + bias))   (fc1 → fc2)
     EPI_QKV = 4,     // split Q/K/V, RoPE, fp16, window layout
+    EPI_DECONV = 5,  // 2×2 stride-2 transposed conv: (+ bias, GELU) → pixel shuffle into act
+    EPI_ACT = 6,     // act = acc + bias                     (conv → next conv)
 };
 
 struct EpiArgs {
@@ -102,6 +116,21 @@ struct EpiArgs {
     // low halves of the fp16 pairs (x = hi + lo) when attention runs split
     _Float16 *q_lo = nullptr, *k_lo = nullptr, *vt_lo = nullptr;
     int vt_ld = 0;                 // row stride of Vᵀ in keys (vt_ld_for of the window size)
+    // EPI_DECONV: input width (pixels per row) and output channels; column n
+    // of the GEMM is kernel tap q = n / cout (ky = q / 2, kx = q % 2),
+    // channel n % cout, written to output pixel (2y + ky, 2x + kx)
+    int dc_w = 0, dc_cout = 0;
+    int gelu = 0;                  // EPI_DECONV: gelu_erf after the bias
+};
+
+// Implicit-GEMM geometry of a 3×3 stride-1 pad-1 convolution over an NHWC
+// image: row m of A is output pixel (m / w, m % w); stage s of K reads the
+// input pixel shifted by tap s / spt ((dy, dx) = (tap / 3 − 1, tap % 3 − 1))
+// at channels [64·(s % spt), +64), or the zero row outside the image.
+struct ConvGeom {
+    int w = 0, h = 0;
+    int spt = 0;                   // stages per tap = Cin / 64
+    const void *zero = nullptr;    // ≥ 128 zero bytes, 16-byte aligned
 };
 
 // Vᵀ rows (fp16 [BH][64][vt_ld]) hold the keys of each aligned 16-key group
@@ -132,6 +161,13 @@ struct AttnArgs {
 // ---- kernel launchers (k_*.hip) ----
 hipError_t launch_gemm(const Weight &w, const Act &a, int64_t M, Epi epi, const EpiArgs &ea,
                        hipStream_t st);
+// Neck GEMMs (WK_F16 or WK_F16X3 weights): EPI_DECONV / EPI_ACT / EPI_F32 on
+// plain rows, or EPI_F32 as a 3×3 implicit GEMM when g is given.
+hipError_t launch_conv(const Weight &w, const Act &a, int64_t M, Epi epi, const EpiArgs &ea,
+                       const ConvGeom *g, hipStream_t st);
+// NHWC f32 [h][w][c] → act (A_F16 or A_F16X2) of the same pixels (pool = 1)
+// or of the 2×2 stride-2 max pool (pool = 2, floor((h − 2)/2) + 1 rows).
+hipError_t launch_pool_act(const float *x, int h, int w, int c, int pool, const Act &out, hipStream_t st);
 hipError_t launch_rows_quant(AKind kind, const float *x, int64_t M, int64_t K, const Act &out,
                              hipStream_t st);
 hipError_t launch_layernorm(const float *x, int64_t M, int64_t E, float eps, const float *w,
@@ -160,7 +196,7 @@ __device__ __forceinline__ uint16_t half_bits(float x) { return __builtin_bit_ca
 inline int64_t stage_k(WKind w) {
     switch (w) {
         case WK_Q4_0: case WK_Q4_1: case WK_Q8_0: return 128;
-        case WK_F16: return 64;
+        case WK_F16: case WK_F16X3: return 64;
         default: return 32;
     }
 }

@@ -73,8 +73,52 @@ void free_weight(Weight &w) {
     if (w.q) (void)hipFree(w.q);
     if (w.d) (void)hipFree(w.d);
     if (w.m) (void)hipFree(w.m);
+    if (w.lo) (void)hipFree(w.lo);
     w.q = nullptr;
     w.d = w.m = nullptr;
+    w.lo = nullptr;
+}
+
+// f32 weights (N rows of K) as two fp16 planes for the split-precision GEMM:
+// w·2^k = hi + lo with hi = fp16(w·2^k) and lo = fp16(w·2^k − hi), k chosen
+// so that the largest |w|·2^k lies in [2^14, 2^15); alpha = 2^-k.
+int upload_weight_split(const float *src, int64_t K, int64_t N, Weight &w) {
+    w = Weight{};
+    w.kind = WK_F16X3;
+    w.ggml_type = S3E_TYPE_F32;
+    w.K = K;
+    w.N = N;
+    w.Kp = round_up(K, stage_k(WK_F16X3));
+    w.Np = round_up(N, GEMM_BN);
+    float amax = 0.f;
+    for (int64_t i = 0; i < K * N; i++) amax = std::max(amax, std::fabs(src[i]));
+    int k = 0;
+    if (amax > 0.f && std::isfinite(amax)) {
+        int e = 0;
+        (void)std::frexp(amax, &e);  // amax = f·2^e, f in [0.5, 1)
+        k = std::min(100, std::max(-100, 15 - e));
+    }
+    w.alpha = std::ldexp(1.0f, -k);
+    std::vector<uint16_t> hi((size_t)(w.Np * w.Kp), 0), lo((size_t)(w.Np * w.Kp), 0);
+    for (int64_t n = 0; n < N; n++)
+        for (int64_t i = 0; i < K; i++) {
+            const float v = std::ldexp(src[n * K + i], k);
+            const uint16_t h = host_f2h(v);
+            hi[(size_t)(n * w.Kp + i)] = h;
+            lo[(size_t)(n * w.Kp + i)] = host_f2h(v - host_h2f(h));
+        }
+    const size_t bytes = hi.size() * 2;
+    hipError_t e = hipMalloc(&w.q, bytes);
+    if (e == hipSuccess) e = hipMemcpy(w.q, hi.data(), bytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMalloc(&w.lo, bytes);
+    if (e == hipSuccess) e = hipMemcpy(w.lo, lo.data(), bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        free_weight(w);
+        set_error("weight upload: %s", hipGetErrorString(e));
+        return S3E_ERR_HIP;
+    }
+    w.bytes = 2 * bytes;
+    return S3E_OK;
 }
 
 // Repack ggml bytes (N rows of K in `type`) into the GEMM layout and upload.
@@ -478,6 +522,22 @@ struct Block {
     bool global = false;
 };
 
+// One level of a SimpleFPN neck (sam3.cpp:2562-2591).  dc[0], dc[1]: the
+// 2×2 stride-2 deconvolutions (scale 0 has two, scale 1 one) as fp16 GEMM
+// weights N = 4·Cout, K = Cin with column (2·ky + kx)·Cout + co; c1: the 1×1
+// conv, c3: the 3×3 conv with K ordered [ky][kx][Cin]; both fp16 in F16
+// files, split fp16 (WK_F16X3) otherwise.
+struct NeckScale {
+    Weight dc[2], c1, c3;
+    float *dc_b[2] = {nullptr, nullptr}, *c1_b = nullptr, *c3_b = nullptr;
+    int64_t dc_b_n[2] = {0, 0}, c1_b_n = 0, c3_b_n = 0;
+};
+
+struct Neck {
+    NeckScale s[4];
+    int found = 0;  // tensors read
+};
+
 }  // namespace
 
 struct s3e_model {
@@ -488,6 +548,9 @@ struct s3e_model {
     Weight patch_w;  // K = 3·P², N = E
     float *pos = nullptr, *ln_pre_w = nullptr, *ln_pre_b = nullptr;
     std::vector<Block> blocks;
+    Neck necks[2];              // 0 = "neck.det.", 1 = "neck.trk."
+    int necks_present = 0;      // bit 0 trk, bit 1 det
+    int32_t neck_dim = 0, visual_only = 1;
     std::vector<void *> owned;  // device f32 arrays
 };
 
@@ -552,9 +615,111 @@ int upload_f32(s3e_model *m, const RawTensor &t, int64_t expect, float **dst) {
 
 }  // namespace
 
+namespace {
+
+// One "neck.{det,trk}.<scale>.<layer>.{weight,bias}" record, already in its
+// registered type (F32, or F16 in F16 files).  Shapes are checked across the
+// neck once every record is in (check_neck).
+int load_neck_tensor(s3e_model *m, const std::string &name, const RawTensor &t) {
+    const int which = name.compare(0, 9, "neck.det.") == 0 ? 0 : 1;
+    Neck &nk = m->necks[which];
+    if (name.size() < 12 || name[9] < '0' || name[9] > '3' || name[10] != '.') return S3E_OK;  // not ours
+    NeckScale &sc = nk.s[name[9] - '0'];
+    const std::string f = name.substr(11);
+    const int64_t n_el = t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3];
+    int rc = S3E_OK;
+    auto bias = [&](float **dst, int64_t *len) {
+        if (t.n_dims != 1) { set_error("'%s': expected a 1-D bias", name.c_str()); return (int)S3E_ERR_IO; }
+        *len = t.ne[0];
+        return upload_f32(m, t, t.ne[0], dst);
+    };
+    if (f == "dconv_2x2_0.bias" || f == "dconv_2x2.bias") rc = bias(&sc.dc_b[0], &sc.dc_b_n[0]);
+    else if (f == "dconv_2x2_1.bias") rc = bias(&sc.dc_b[1], &sc.dc_b_n[1]);
+    else if (f == "conv_1x1.bias") rc = bias(&sc.c1_b, &sc.c1_b_n);
+    else if (f == "conv_3x3.bias") rc = bias(&sc.c3_b, &sc.c3_b_n);
+    else if (f == "dconv_2x2_0.weight" || f == "dconv_2x2.weight" || f == "dconv_2x2_1.weight") {
+        // ggml [kW=2, kH=2, Cout, Cin]: element (kx, ky, co, ci) at ((ci·Cout + co)·2 + ky)·2 + kx;
+        // cast to fp16 as sam3_conv_transpose_weight does (sam3.cpp:1083-1086)
+        if (t.ne[0] != 2 || t.ne[1] != 2) { set_error("'%s': expected a 2x2 kernel", name.c_str()); return S3E_ERR_IO; }
+        const int64_t Cout = t.ne[2], Cin = t.ne[3];
+        std::vector<uint16_t> w((size_t)(4 * Cout * Cin));
+        for (int64_t ci = 0; ci < Cin; ci++)
+            for (int64_t co = 0; co < Cout; co++)
+                for (int q = 0; q < 4; q++) {
+                    const int64_t src = (ci * Cout + co) * 4 + q;  // q = 2·ky + kx
+                    uint16_t h;
+                    if (t.type == 1) std::memcpy(&h, t.data.data() + 2 * src, 2);
+                    else h = host_f2h(((const float *)t.data.data())[src]);
+                    w[(size_t)((q * Cout + co) * Cin + ci)] = h;
+                }
+        Weight &dst = sc.dc[f == "dconv_2x2_1.weight" ? 1 : 0];
+        rc = upload_weight(m->ctx->device, S3E_TYPE_F16, Cin, 4 * Cout, (const uint8_t *)w.data(), w.size() * 2, dst);
+    } else if (f == "conv_1x1.weight" || f == "conv_3x3.weight") {
+        // ggml [kW, kH, Cin, Cout]: element (kx, ky, ci, co) at ((co·Cin + ci)·kH + ky)·kW + kx;
+        // the GEMM's K order is [ky][kx][Cin] so that one stage stays inside one tap
+        const int64_t k = (f == "conv_1x1.weight") ? 1 : 3;
+        if (t.ne[0] != k || t.ne[1] != k) { set_error("'%s': expected a %lldx%lld kernel", name.c_str(), (long long)k, (long long)k); return S3E_ERR_IO; }
+        const int64_t Cin = t.ne[2], Cout = t.ne[3], K = k * k * Cin;
+        Weight &dst = (k == 1) ? sc.c1 : sc.c3;
+        std::vector<float> wf((size_t)(K * Cout));
+        std::vector<uint16_t> wh(t.type == 1 ? (size_t)(K * Cout) : 0);
+        for (int64_t co = 0; co < Cout; co++)
+            for (int64_t ci = 0; ci < Cin; ci++)
+                for (int64_t ky = 0; ky < k; ky++)
+                    for (int64_t kx = 0; kx < k; kx++) {
+                        const int64_t src = ((co * Cin + ci) * k + ky) * k + kx;
+                        const size_t d = (size_t)(co * K + (ky * k + kx) * Cin + ci);
+                        if (t.type == 1) std::memcpy(&wh[d], t.data.data() + 2 * src, 2);
+                        else wf[d] = ((const float *)t.data.data())[src];
+                    }
+        if (t.type == 1) rc = upload_weight(m->ctx->device, S3E_TYPE_F16, K, Cout, (const uint8_t *)wh.data(), wh.size() * 2, dst);
+        else rc = upload_weight_split(wf.data(), K, Cout, dst);
+    } else {
+        return S3E_OK;
+    }
+    (void)n_el;
+    if (rc == S3E_OK) nk.found++;
+    return rc;
+}
+
+// Shapes of a complete neck: the graph of sam3.cpp:3863-3921 on E channels.
+int check_neck(const s3e_model *m, int which) {
+    const Neck &nk = m->necks[which];
+    const char *nm = which == 0 ? "neck.det" : "neck.trk";
+    if (nk.found != 22) { set_error("%s: found %d of 22 tensors", nm, nk.found); return S3E_ERR_IO; }
+    const int64_t E = m->E;
+    const NeckScale &s0 = nk.s[0], &s1 = nk.s[1], &s2 = nk.s[2], &s3 = nk.s[3];
+    const int64_t mid0 = s0.dc[0].N / 4, D = s0.dc[1].N / 4, mid1 = s1.dc[0].N / 4;
+    bool ok = s0.dc[0].K == E && s0.dc[1].K == mid0 && s1.dc[0].K == E && s0.dc_b_n[0] == mid0 &&
+              s0.dc_b_n[1] == D && s1.dc_b_n[0] == mid1 && s0.c1.K == D && s1.c1.K == mid1 && s2.c1.K == E &&
+              s3.c1.K == E;
+    for (int i = 0; i < 4; i++) {
+        const NeckScale &sc = nk.s[i];
+        ok = ok && sc.c1.N == D && sc.c3.N == D && sc.c3.K == 9 * D && sc.c1_b_n == D && sc.c3_b_n == D &&
+             sc.c1.q && sc.c3.q && sc.c1_b && sc.c3_b;
+    }
+    if (!ok) { set_error("%s: tensor shapes do not form the SimpleFPN graph", nm); return S3E_ERR_IO; }
+    // fp16 GEMM rows are read 64 channels per stage; the 3×3 needs whole stages per tap
+    if (D % 64 != 0 || mid0 % 64 != 0 || mid1 % 64 != 0) {
+        set_error("%s: channel counts (%lld, %lld, %lld) must be multiples of 64", nm, (long long)D, (long long)mid0, (long long)mid1);
+        return S3E_ERR_UNSUPPORTED;
+    }
+    if (D != m->neck_dim) { set_error("%s: width %lld differs from neck_dim %d", nm, (long long)D, m->neck_dim); return S3E_ERR_IO; }
+    return S3E_OK;
+}
+
+}  // namespace
+
 extern "C" void s3e_model_free(s3e_model *m) {
     if (!m) return;
     free_weight(m->patch_w);
+    for (auto &nk : m->necks)
+        for (auto &sc : nk.s) {
+            free_weight(sc.dc[0]);
+            free_weight(sc.dc[1]);
+            free_weight(sc.c1);
+            free_weight(sc.c3);
+        }
     for (auto &b : m->blocks) {
         free_weight(b.qkv);
         free_weight(b.proj);
@@ -596,6 +761,8 @@ extern "C" int s3e_model_load(s3e_ctx *ctx, const char *path, s3e_model **out) {
         if (!rd(&m->gidx[i], 4)) { set_error("s3e_model_load: truncated hparams"); return S3E_ERR_IO; }
     int32_t rest[27];
     if (!rd(rest, sizeof rest)) { set_error("s3e_model_load: truncated hparams"); return S3E_ERR_IO; }
+    m->neck_dim = rest[6];
+    m->visual_only = rest[26];
     if (m->patch <= 0 || m->img % m->patch != 0 || m->E <= 0 || m->heads <= 0 || m->E % m->heads != 0 ||
         m->depth <= 0 || m->depth > 256 || m->window <= 0) {
         set_error("s3e_model_load: inconsistent hparams");
@@ -638,7 +805,8 @@ extern "C" int s3e_model_load(s3e_ctx *ctx, const char *path, s3e_model **out) {
         const int64_t n_el = t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3];
         if (t.ne[0] % ggml_blck(t.type) != 0) { set_error("s3e_model_load: '%s' ne0 not a block multiple", name.c_str()); return S3E_ERR_IO; }
         const size_t bytes = ggml_rowsize(t.type, t.ne[0]) * (size_t)(n_el / t.ne[0]);
-        if (name.compare(0, 4, "vit.") != 0) {  // not part of the backbone: skip
+        const bool is_neck = name.compare(0, 9, "neck.det.") == 0 || name.compare(0, 9, "neck.trk.") == 0;
+        if (name.compare(0, 4, "vit.") != 0 && !is_neck) {  // not part of the encoder: skip
             fin.seekg((std::streamoff)bytes, std::ios::cur);
             if (!fin) { set_error("s3e_model_load: truncated data of '%s'", name.c_str()); return S3E_ERR_IO; }
             continue;
@@ -650,6 +818,11 @@ extern "C" int s3e_model_load(s3e_ctx *ctx, const char *path, s3e_model **out) {
         const bool f32_reg = t.n_dims < 2 || name.find("pos_embed") != std::string::npos || name.find("freqs_cis") != std::string::npos;
         if (!f32_reg) want = (t.ne[0] % ggml_blck(wtype) == 0) ? wtype : 0;
         if (!coerce(t, want)) { set_error("s3e_model_load: cannot convert '%s' from type %d to %d", name.c_str(), t.type, want); return S3E_ERR_IO; }
+        if (is_neck) {
+            const int rc = load_neck_tensor(m.get(), name, t);
+            if (rc != S3E_OK) return rc;
+            continue;
+        }
         int rc = S3E_OK;
         if (name == "vit.patch_embed.proj.weight") {
             if (t.ne[0] != m->patch || t.ne[1] != m->patch || t.ne[2] != 3 || t.ne[3] != E) { set_error("patch_embed shape mismatch"); return S3E_ERR_IO; }
@@ -707,6 +880,13 @@ extern "C" int s3e_model_load(s3e_ctx *ctx, const char *path, s3e_model **out) {
         return S3E_ERR_IO;
     }
     if (m->mlp % 128 != 0) { set_error("s3e_model_load: MLP width %d must be a multiple of 128", m->mlp); return S3E_ERR_UNSUPPORTED; }
+    // necks: optional (an encoder-only file has none); a partial one is an error
+    for (int which = 0; which < 2; which++) {
+        if (m->necks[which].found == 0) continue;
+        const int rc = check_neck(m.get(), which);
+        if (rc != S3E_OK) return rc;
+        m->necks_present |= which == 1 ? 1 : 2;
+    }
     *out = m.release();
     return S3E_OK;
 }
@@ -719,6 +899,8 @@ extern "C" int s3e_model_hparams(const s3e_model *m, int32_t out[16]) {
     for (int i = 0; i < 4; i++) out[8 + i] = m->gidx[i];
     out[12] = m->ftype;
     out[13] = m->grid;
+    out[14] = m->neck_dim;
+    out[15] = m->necks_present;
     return S3E_OK;
 }
 
@@ -732,6 +914,14 @@ struct s3e_state {
     ActBuf a1, a2, col;       // E-wide, MLP-wide and im2col activations
     _Float16 *q16 = nullptr, *k16 = nullptr, *vt16 = nullptr;  // [hi plane | lo plane]
     int64_t vt_elems = 0;
+    // necks: level sides, outputs (f32 [side²][D]) per neck, the shared PEs,
+    // and fp16 work planes, each [hi | lo] of cap halves
+    int64_t side[4] = {0, 0, 0, 0};
+    float *neck_out[2][4] = {{nullptr, nullptr, nullptr, nullptr}, {nullptr, nullptr, nullptr, nullptr}};
+    float *pe[4] = {nullptr, nullptr, nullptr, nullptr};
+    _Float16 *nx = nullptr, *n_dc = nullptr, *n_a = nullptr, *n_b = nullptr;
+    int64_t nx_cap = 0, n_a_cap = 0, n_b_cap = 0;
+    void *zero = nullptr;
 };
 
 extern "C" void s3e_state_free(s3e_state *st) {
@@ -746,8 +936,77 @@ extern "C" void s3e_state_free(s3e_state *st) {
     if (st->q16) (void)hipFree(st->q16);
     if (st->k16) (void)hipFree(st->k16);
     if (st->vt16) (void)hipFree(st->vt16);
+    for (auto &lv : st->neck_out)
+        for (float *p : lv)
+            if (p) (void)hipFree(p);
+    for (float *p : st->pe)
+        if (p) (void)hipFree(p);
+    for (void *p : {(void *)st->nx, (void *)st->n_dc, (void *)st->n_a, (void *)st->n_b, st->zero})
+        if (p) (void)hipFree(p);
     delete st;
 }
+
+namespace {
+
+// sam3_sinusoidal_pe_2d (sam3.cpp:3597-3633): [H][W][d] with channels
+// [0, d/2) following y and [d/2, d) following x, even channels sin, odd cos.
+std::vector<float> sinusoidal_pe_2d(int H, int W, int d) {
+    const int half = d / 2;
+    const float scale = 2.0f * (float)M_PI;
+    std::vector<float> pe((size_t)d * H * W);
+    for (int y = 0; y < H; ++y)
+        for (int x = 0; x < W; ++x) {
+            const float py = ((float)(y + 1) / (float)H) * scale;
+            const float px = ((float)(x + 1) / (float)W) * scale;
+            float *o = pe.data() + ((size_t)y * W + x) * d;
+            for (int i = 0; i < half; ++i) {
+                const float dim_t = std::pow(10000.0f, (float)(i & ~1) / (float)half);
+                o[i] = (i % 2 == 0) ? std::sin(py / dim_t) : std::cos(py / dim_t);
+                o[i + half] = (i % 2 == 0) ? std::sin(px / dim_t) : std::cos(px / dim_t);
+            }
+        }
+    return pe;
+}
+
+// Neck buffers and PEs of a state (sizes from the loaded necks).
+hipError_t alloc_neck(s3e_state *st) {
+    const s3e_model *m = st->m;
+    if (!m->necks_present) return hipSuccess;
+    const int64_t G = m->grid, T = G * G, E = m->E;
+    st->side[0] = 4 * G;
+    st->side[1] = 2 * G;
+    st->side[2] = G;
+    st->side[3] = (G - 2) / 2 + 1;
+    int64_t D = m->neck_dim, mid0 = 0, mid1 = 0;
+    for (const Neck &nk : m->necks) {
+        if (!nk.found) continue;
+        mid0 = std::max(mid0, nk.s[0].dc[0].N / 4);
+        mid1 = std::max(mid1, nk.s[1].dc[0].N / 4);
+    }
+    const int64_t S3 = st->side[3] * st->side[3];
+    st->nx_cap = T * E;
+    st->n_a_cap = std::max({16 * T * D, 4 * T * mid1, S3 * E});
+    st->n_b_cap = 16 * T * D;
+    hipError_t e = hipMalloc(&st->nx, (size_t)st->nx_cap * 2 * 2);
+    if (e == hipSuccess) e = hipMalloc(&st->n_dc, (size_t)(4 * T * mid0) * 2);
+    if (e == hipSuccess) e = hipMalloc(&st->n_a, (size_t)st->n_a_cap * 2 * 2);
+    if (e == hipSuccess) e = hipMalloc(&st->n_b, (size_t)st->n_b_cap * 2 * 2);
+    if (e == hipSuccess) e = hipMalloc(&st->zero, 256);
+    if (e == hipSuccess) e = hipMemsetAsync(st->zero, 0, 256, st->ctx->stream);
+    for (int which = 0; which < 2 && e == hipSuccess; which++) {
+        if (!m->necks[which].found) continue;
+        for (int i = 0; i < 4 && e == hipSuccess; i++)
+            e = hipMalloc(&st->neck_out[which][i], (size_t)(st->side[i] * st->side[i] * D) * 4);
+    }
+    for (int i = 0; i < 4 && e == hipSuccess; i++) {
+        const std::vector<float> pe = sinusoidal_pe_2d((int)st->side[i], (int)st->side[i], (int)D);
+        e = hipMalloc(&st->pe[i], pe.size() * 4);
+        if (e == hipSuccess) e = hipMemcpy(st->pe[i], pe.data(), pe.size() * 4, hipMemcpyHostToDevice);
+    }
+    return e;
+}
+
+}  // namespace
 
 extern "C" int s3e_state_create(s3e_ctx *ctx, const s3e_model *m, s3e_state **out) {
     if (!ctx || !m || !out) { set_error("s3e_state_create: NULL argument"); return S3E_ERR_INVALID; }
@@ -775,6 +1034,7 @@ extern "C" int s3e_state_create(s3e_ctx *ctx, const s3e_model *m, s3e_state **ou
     }
     st->vt_elems = vt_elems;
     if (e == hipSuccess) e = hipMalloc(&st->vt16, (size_t)(vt_elems * 2 * 2));
+    if (e == hipSuccess) e = alloc_neck(st);
     if (e != hipSuccess) {
         s3e_state_free(st);
         set_error("s3e_state_create: %s", hipGetErrorString(e));
@@ -881,6 +1141,116 @@ hipError_t run_block(s3e_state *st, int bi, float *x) {
     return launch_gemm(b.fc2, e1.out, T, EPI_RESID, e2, s);
 }
 
+Act plane_act(AKind kind, _Float16 *base, int64_t cap, int64_t ld) {
+    Act a;
+    a.kind = kind;
+    a.x = base;
+    a.lo = base + cap;
+    a.ld = ld;
+    return a;
+}
+
+// sam3_build_neck_graph (sam3.cpp:3863-3921) for one neck on vit_output x
+// (G² rows of E f32): 4 levels into st->neck_out[which].  NHWC throughout:
+// a pixel is a row of channels, so a 1×1 conv is a plain GEMM, a 2×2
+// stride-2 deconvolution is a GEMM with N = 4·Cout whose epilogue scatters
+// each tap to its output pixel, and the 3×3 conv is an implicit GEMM over
+// shifted pixel rows.  The vit_output conversion to fp16 planes (nx) is
+// shared by both necks and done by the caller.
+hipError_t run_neck(s3e_state *st, int which, const float *x) {
+    const s3e_model *m = st->m;
+    const Neck &nk = m->necks[which];
+    hipStream_t s = st->ctx->stream;
+    const int G = m->grid;
+    const int64_t T = (int64_t)G * G, E = m->E, D = m->neck_dim;
+    float *const *out = st->neck_out[which];
+    auto conv3 = [&](const NeckScale &sc, const Act &in, int side, float *y) {
+        EpiArgs e;
+        e.bias = sc.c3_b;
+        e.y = y;
+        e.ldy = D;
+        ConvGeom g;
+        g.w = g.h = side;
+        g.spt = (int)(D / 64);
+        g.zero = st->zero;
+        return launch_conv(sc.c3, in, (int64_t)side * side, EPI_F32, e, &g, s);
+    };
+    auto conv1 = [&](const NeckScale &sc, const Act &in, int64_t M, const Act &o) {
+        EpiArgs e;
+        e.bias = sc.c1_b;
+        e.out = o;
+        return launch_conv(sc.c1, in, M, EPI_ACT, e, nullptr, s);
+    };
+    auto deconv = [&](const Weight &w, const float *b, const Act &in, int in_side, int gelu, const Act &o) {
+        EpiArgs e;
+        e.bias = b;
+        e.dc_w = in_side;
+        e.dc_cout = (int)(w.N / 4);
+        e.gelu = gelu;
+        e.out = o;
+        return launch_conv(w, in, (int64_t)in_side * in_side, EPI_DECONV, e, nullptr, s);
+    };
+    const Act x16 = plane_act(A_F16, st->nx, st->nx_cap, E);  // fp16(x): the deconvolutions' input
+    hipError_t err;
+    // scale 0 (4×): deconv + bias + gelu_erf (fp16, the next deconv's input), deconv + bias, 1×1, 3×3
+    {
+        const NeckScale &sc = nk.s[0];
+        const int64_t mid = sc.dc[0].N / 4;
+        const AKind k1 = act_kind_for(sc.c1.kind), k3 = act_kind_for(sc.c3.kind);
+        const Act a_dc = plane_act(A_F16, st->n_dc, 0, mid);
+        const Act a_1 = plane_act(k1, st->n_a, st->n_a_cap, D);
+        const Act a_3 = plane_act(k3, st->n_b, st->n_b_cap, D);
+        if ((err = deconv(sc.dc[0], sc.dc_b[0], x16, G, 1, a_dc)) != hipSuccess) return err;
+        if ((err = deconv(sc.dc[1], sc.dc_b[1], a_dc, 2 * G, 0, a_1)) != hipSuccess) return err;
+        if ((err = conv1(sc, a_1, 16 * T, a_3)) != hipSuccess) return err;
+        if ((err = conv3(sc, a_3, 4 * G, out[0])) != hipSuccess) return err;
+    }
+    // scale 1 (2×): deconv + bias, 1×1, 3×3
+    {
+        const NeckScale &sc = nk.s[1];
+        const int64_t mid = sc.dc[0].N / 4;
+        const Act a_1 = plane_act(act_kind_for(sc.c1.kind), st->n_a, st->n_a_cap, mid);
+        const Act a_3 = plane_act(act_kind_for(sc.c3.kind), st->n_b, st->n_b_cap, D);
+        if ((err = deconv(sc.dc[0], sc.dc_b[0], x16, G, 0, a_1)) != hipSuccess) return err;
+        if ((err = conv1(sc, a_1, 4 * T, a_3)) != hipSuccess) return err;
+        if ((err = conv3(sc, a_3, 2 * G, out[1])) != hipSuccess) return err;
+    }
+    // scale 2 (1×): 1×1 on x itself, 3×3
+    {
+        const NeckScale &sc = nk.s[2];
+        const Act a_1 = plane_act(act_kind_for(sc.c1.kind), st->nx, st->nx_cap, E);
+        const Act a_3 = plane_act(act_kind_for(sc.c3.kind), st->n_b, st->n_b_cap, D);
+        if ((err = conv1(sc, a_1, T, a_3)) != hipSuccess) return err;
+        if ((err = conv3(sc, a_3, G, out[2])) != hipSuccess) return err;
+    }
+    // scale 3 (0.5×): 2×2 max pool, 1×1, 3×3
+    {
+        const NeckScale &sc = nk.s[3];
+        const int g3 = (int)st->side[3];
+        const Act a_1 = plane_act(act_kind_for(sc.c1.kind), st->n_a, st->n_a_cap, E);
+        const Act a_3 = plane_act(act_kind_for(sc.c3.kind), st->n_b, st->n_b_cap, D);
+        if ((err = launch_pool_act(x, G, G, (int)E, 2, a_1, s)) != hipSuccess) return err;
+        if ((err = conv1(sc, a_1, (int64_t)g3 * g3, a_3)) != hipSuccess) return err;
+        if ((err = conv3(sc, a_3, g3, out[3])) != hipSuccess) return err;
+    }
+    return hipSuccess;
+}
+
+// Both necks (detector first, as sam3.cpp:6072-6075 builds them) on x.
+hipError_t run_necks(s3e_state *st, const float *x) {
+    const s3e_model *m = st->m;
+    if (!m->necks_present) return hipSuccess;
+    // fp16 planes of x: hi feeds the deconvolutions, hi + lo the scale-2 1×1
+    bool split = false;
+    for (const Neck &nk : m->necks)
+        if (nk.found && nk.s[2].c1.kind == WK_F16X3) split = true;
+    hipError_t e = launch_pool_act(x, m->grid, m->grid, m->E, 1,
+                                   plane_act(split ? A_F16X2 : A_F16, st->nx, st->nx_cap, m->E), st->ctx->stream);
+    for (int which = 0; which < 2 && e == hipSuccess; which++)
+        if (m->necks[which].found) e = run_neck(st, which, x);
+    return e;
+}
+
 }  // namespace
 
 extern "C" int s3e_vit_prefix(s3e_state *st, const float *chw_device, float *x_device) {
@@ -903,6 +1273,15 @@ extern "C" int s3e_encode_chw(s3e_state *st, const float *chw_device) {
     HIP_TRY(hipSetDevice(st->ctx->device));
     HIP_TRY(run_prefix(st, chw_device, st->x));
     for (int i = 0; i < st->m->depth; i++) HIP_TRY(run_block(st, i, st->x));
+    HIP_TRY(run_necks(st, st->x));
+    return S3E_OK;
+}
+
+extern "C" int s3e_run_neck(s3e_state *st, const float *x_device) {
+    if (!st || !x_device) { set_error("s3e_run_neck: NULL argument"); return S3E_ERR_INVALID; }
+    if (!st->m->necks_present) { set_error("s3e_run_neck: the model has no neck"); return S3E_ERR_INVALID; }
+    HIP_TRY(hipSetDevice(st->ctx->device));
+    HIP_TRY(run_necks(st, x_device));
     return S3E_OK;
 }
 
@@ -957,29 +1336,59 @@ extern "C" int s3e_encode_image_u8(s3e_state *st, const uint8_t *hwc, int width,
     return s3e_ctx_sync(st->ctx);
 }
 
+namespace {
+
+// Names of sam3_find_state_tensor (sam3.cpp:14334-14376): vit_output,
+// neck_{det,trk}_<i>, neck_det_pe_<i> and the PE tensors pe_<i>, plus
+// neck_trk_pe_<i> (the same PEs: sam3.cpp:6190-6192).  A tensor the model
+// does not produce (neck_det_* of a visual-only model) does not resolve.
+const float *find_tensor(const s3e_state *st, const char *name, int64_t ne[4]) {
+    const s3e_model *m = st->m;
+    if (std::strcmp(name, "vit_output") == 0) {
+        ne[0] = m->E; ne[1] = m->grid; ne[2] = m->grid; ne[3] = 1;
+        return st->x;
+    }
+    int i = -1;
+    const float *p = nullptr;
+    auto level = [&](const char *prefix) {
+        const size_t n = std::strlen(prefix);
+        if (std::strncmp(name, prefix, n) == 0 && name[n] >= '0' && name[n] <= '3' && name[n + 1] == 0) {
+            i = name[n] - '0';
+            return true;
+        }
+        return false;
+    };
+    if (level("neck_det_pe_") || level("neck_trk_pe_") || level("pe_")) p = st->pe[i];
+    else if (level("neck_det_")) p = st->neck_out[0][i];
+    else if (level("neck_trk_")) p = st->neck_out[1][i];
+    if (!p) return nullptr;
+    ne[0] = m->neck_dim; ne[1] = st->side[i]; ne[2] = st->side[i]; ne[3] = 1;
+    return p;
+}
+
+}  // namespace
+
 extern "C" int s3e_state_tensor_info(const s3e_state *st, const char *name, int64_t ne[4]) {
     if (!st || !name || !ne) { set_error("s3e_state_tensor_info: NULL argument"); return S3E_ERR_INVALID; }
-    if (std::strcmp(name, "vit_output") != 0) { set_error("s3e_state_tensor_info: unknown tensor '%s'", name); return S3E_ERR_INVALID; }
-    ne[0] = st->m->E;
-    ne[1] = st->m->grid;
-    ne[2] = st->m->grid;
-    ne[3] = 1;
+    if (!find_tensor(st, name, ne)) { set_error("s3e_state_tensor_info: unknown tensor '%s'", name); return S3E_ERR_INVALID; }
     return S3E_OK;
 }
 
 extern "C" const float *s3e_state_tensor_device(const s3e_state *st, const char *name) {
-    if (!st || !name || std::strcmp(name, "vit_output") != 0) return nullptr;
-    return st->x;
+    int64_t ne[4];
+    if (!st || !name) return nullptr;
+    return find_tensor(st, name, ne);
 }
 
 extern "C" int s3e_state_tensor_get(const s3e_state *st, const char *name, float *host, size_t n) {
     int64_t ne[4];
-    const int rc = s3e_state_tensor_info(st, name, ne);
-    if (rc != S3E_OK) return rc;
+    if (!st || !name) { set_error("s3e_state_tensor_get: NULL argument"); return S3E_ERR_INVALID; }
+    const float *src = find_tensor(st, name, ne);
+    if (!src) { set_error("s3e_state_tensor_get: unknown tensor '%s'", name); return S3E_ERR_INVALID; }
     const size_t need = (size_t)(ne[0] * ne[1] * ne[2] * ne[3]);
     if (!host || n < need) { set_error("s3e_state_tensor_get: buffer holds %zu floats, need %zu", n, need); return S3E_ERR_INVALID; }
     HIP_TRY(hipSetDevice(st->ctx->device));
-    HIP_TRY(hipMemcpyAsync(host, st->x, need * 4, hipMemcpyDeviceToHost, st->ctx->stream));
+    HIP_TRY(hipMemcpyAsync(host, src, need * 4, hipMemcpyDeviceToHost, st->ctx->stream));
     HIP_TRY(hipStreamSynchronize(st->ctx->stream));
     return S3E_OK;
 }
