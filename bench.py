@@ -1,12 +1,16 @@
 #!/usr/bin/env python3
-"""Benchmark: SAM 3 ViT image encoder (backbone) on one MI355X.
+"""Benchmark: SAM 3 image encoder (ViT backbone + SimpleFPN neck) on one MI355X.
 
-Workload: the SAM 3 visual backbone at 1008×1008 (72×72 tokens, 32 blocks,
-width 1024, 16 heads, MLP 4736, 24×24 windows, global blocks 7/15/23/31),
-random-init weights N(0, 0.02) quantized to Q4_0 (default; --ftype selects
-q8_0, q4_1, f16, f32), one synthetic uniform-uint8 image preprocessed as
-sam3.cpp does.  A step is one full encode of that image with the input
-already resident in HBM; value = ms per frame (lower is better).
+Workload: the SAM 3 visual encoder at 1008×1008 (72×72 tokens, 32 blocks,
+width 1024, 16 heads, MLP 4736, 24×24 windows, global blocks 7/15/23/31)
+followed by the tracker neck to 256-channel features at 288², 144², 72² and
+36² (a visual-only model), random-init weights N(0, 0.02) with the ViT's
+linear weights quantized to Q4_0 (default; --ftype selects q8_0, q4_1, f16,
+f32), one synthetic uniform-uint8 image preprocessed as sam3.cpp does.  A
+step is one full encode of that image with the input already resident in
+HBM; value = ms per frame (lower is better).  The neck's share is measured
+separately (s3e_run_neck on the same backbone output) and reported as
+breakdown.neck_ms.
 
 Also reported, on the same JSON line:
   roofline      — the dominant kernel (the fc1 GEMM, M=5184 N=4736 K=1024,
@@ -18,7 +22,8 @@ Also reported, on the same JSON line:
                   WRITE_SIZE counter summary when present.
   cpu_baseline  — the CPU oracle (a C restatement of ggml's CPU path, not
                   the upstream binary) on this host: one whole frame of the
-                  same model and image (about 10 s on 16 host threads).
+                  same model and image, backbone and neck (about 12 s on 16
+                  host threads).
 """
 from __future__ import annotations
 
@@ -126,15 +131,16 @@ def _random_ggml_bytes(wt: int, N: int, K: int, rng) -> np.ndarray:
 
 
 def cpu_baseline(path: str, img: np.ndarray, threads: int):
-    """Oracle on the host: one whole frame (prefix + 32 blocks) of the same
-    model and image, after the host preprocessing."""
+    """Oracle on the host: one whole frame (prefix + 32 blocks + tracker neck)
+    of the same model and image, after the host preprocessing."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as orc
 
     om = orc.OracleModel(path)
     chw = orc.preprocess_sam3(img, om.img)
     t0 = time.perf_counter()
-    om.encode(chw, threads)
+    x = om.encode(chw, threads)
+    om.neck(x, "trk", threads)
     return (time.perf_counter() - t0) * 1e3
 
 
@@ -201,7 +207,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "gemm_fc1_q4_0_counters.txt"))
-    ap.add_argument("--only", choices=["encode", "gemm", "copy"], default=None,
+    ap.add_argument("--only", choices=["encode", "gemm", "copy", "neck"], default=None,
                     help="run one leg only (for profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -260,6 +266,20 @@ def main() -> int:
     log(f"encode: {ms_frame:.3f} ms/frame over {args.steps} steps")
     if args.only == "encode":
         return 0
+    # the neck alone on the backbone output just computed
+    xd = st.device_view("vit_output")
+    for _ in range(2):
+        st.run_neck(xd)
+    ctx.sync()
+    ev.record(e0, ctx.stream)
+    for _ in range(args.steps):
+        st.run_neck(xd)
+    ev.record(e1, ctx.stream)
+    neck_ms = ev.elapsed_ms(e0, e1) / args.steps
+    ctx.sync()
+    log(f"neck: {neck_ms:.3f} ms/frame")
+    if args.only == "neck":
+        return 0
 
     gms, gtops, gops = out["gemm"]
     peak = PEAK_TOPS[args.ftype]
@@ -270,8 +290,9 @@ def main() -> int:
         cms = cpu_baseline(path, img, threads)
         log(f"cpu baseline: {cms / 1e3:.1f} s/frame, {threads} threads")
         cpu = {"value": round(cms, 1), "unit": "ms/frame", "cores": threads, "kind": "port",
-               "sample": "one full frame (prefix + 32 blocks) of the same Q4_0 model and image on the CPU "
-                         "oracle, a C restatement of ggml's CPU path (AVX2, OpenMP), not the upstream binary"}
+               "sample": f"one full frame (prefix + 32 blocks + tracker neck) of the same {args.ftype.upper()} "
+                         "model and image on the CPU oracle, a C restatement of ggml's CPU path (AVX2, "
+                         "OpenMP), not the upstream binary"}
     try:
         os.remove(path)
     except OSError:
@@ -289,10 +310,12 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": {"q4_0": "int8", "q4_1": "int8", "q8_0": "int8", "f16": "f16", "f32": "f32"}[args.ftype],
         "data": "synthetic: random-init weights N(0,0.02), uniform uint8 1008x1008 image, seed 0",
-        "config": {"workload": f"SAM 3 ViT image encoder backbone, 1008x1008 (72x72 tokens), 32 blocks, "
-                               f"{args.ftype.upper()} weights, batch 1",
+        "config": {"workload": f"SAM 3 visual-only image encoder, 1008x1008 (72x72 tokens): ViT backbone "
+                               f"(32 blocks, {args.ftype.upper()} linear weights) + tracker SimpleFPN neck to "
+                               f"256-ch features at 288/144/72/36, batch 1",
                    "img_size": 1008, "weights": args.ftype, "blocks": 32, "window": 24,
-                   "global_blocks": [7, 15, 23, 31]},
+                   "global_blocks": [7, 15, 23, 31], "neck_levels": [288, 144, 72, 36]},
+        "breakdown": {"neck_ms": round(neck_ms, 3), "backbone_ms": round(ms_frame - neck_ms, 3)},
         "roofline": {"kernel": f"{GEMM_KERNEL} fc1 M=5184 N=4736 K=1024 ({args.ftype})", "bound": "mfma",
                      "achieved": round(gtops, 1), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(gtops / peak, 4), "traffic": traffic,

@@ -136,6 +136,13 @@ def unstage_scales(plane: np.ndarray, M: int, K: int) -> np.ndarray:
     return plane.reshape(G, Mp, 4).transpose(1, 0, 2).reshape(Mp, G * 4)[:M, :K // 32]
 
 
+class DeviceView:
+    """A non-owning device pointer (a state tensor)."""
+
+    def __init__(self, ptr: int, nbytes: int):
+        self.ptr, self.nbytes = ptr, nbytes
+
+
 class DeviceBuffer:
     """A device allocation owned by a Context."""
 
@@ -313,6 +320,12 @@ class State:
 
     def run_neck(self, x: DeviceBuffer):
         check(LIB.s3e_run_neck(self.handle, x.ptr), "s3e_run_neck")
+
+    def device_view(self, name: str = "vit_output") -> DeviceView:
+        ne = (c_int64 * 4)()
+        check(LIB.s3e_state_tensor_info(self.handle, name.encode(), ne), "s3e_state_tensor_info")
+        p = LIB.s3e_state_tensor_device(self.handle, name.encode())
+        return DeviceView(p, 4 * ne[0] * ne[1] * ne[2] * ne[3])
 
     def tensor(self, name: str = "vit_output") -> np.ndarray:
         ne = (c_int64 * 4)()
