@@ -60,28 +60,24 @@ struct Cfg {
     static constexpr int NTH = 64 * WAVES;
     static constexpr bool quant = (WK == WK_Q4_0 || WK == WK_Q4_1 || WK == WK_Q8_0);
     static constexpr bool q41 = (WK == WK_Q4_1);
-    static constexpr bool split = (WK == WK_F16X3);      // hi and lo planes of A and B
-    static constexpr int planes = split ? 2 : 1;
-    static constexpr int esize = quant ? 1 : ((WK == WK_F16 || split) ? 2 : 4);
+    static constexpr int esize = quant ? 1 : (WK == WK_F16 ? 2 : 4);
     static constexpr int WM = 2, WN = WAVES / 2;
     static constexpr int MT = BM / (32 * WM);            // 32-row MFMA tiles per wave
     static constexpr int NT = BN / (32 * WN);            // 32-column MFMA tiles per wave
     static constexpr int NBUF = WAVES == 4 ? 2 : 3;      // LDS ring depth
     static constexpr int OFF_A = 0;
-    static constexpr int OFF_ALO = BM * ROWB;            // split: A low plane
-    static constexpr int OFF_B = planes * BM * ROWB;
-    static constexpr int OFF_BLO = OFF_B + BN * ROWB;    // split: B low plane
-    static constexpr int OFF_SC = OFF_B + planes * BN * ROWB;  // scales: AD | BD | AS | BMIN
+    static constexpr int OFF_B = BM * ROWB;
+    static constexpr int OFF_SC = OFF_B + BN * ROWB;     // scales: AD | BD | AS | BMIN
     static constexpr int OFF_AD = OFF_SC;
     static constexpr int OFF_BD = OFF_AD + (quant ? BM * 8 : 0);
     static constexpr int OFF_AS = OFF_BD + (quant ? BN * 8 : 0);
     static constexpr int OFF_BMIN = OFF_AS + (q41 ? BM * 8 : 0);
     static constexpr int STAGE = OFF_BMIN + (q41 ? BN * 8 : 0);
-    static constexpr int NA = BM / (8 * WAVES);          // 1 KB A loads per wave per stage and plane
-    static constexpr int NB = BN / (8 * WAVES);          // 1 KB B loads per wave per stage and plane
+    static constexpr int NA = BM / (8 * WAVES);          // 1 KB A loads per wave per stage
+    static constexpr int NB = BN / (8 * WAVES);          // 1 KB B loads per wave per stage
     static constexpr int SC = (STAGE - OFF_SC) / 256;    // 256 B scale loads per stage
     static constexpr int NS = (SC + WAVES - 1) / WAVES;  // ... per wave
-    static constexpr int NLOAD = planes * (NA + NB) + NS;
+    static constexpr int NLOAD = NA + NB + NS;
     static constexpr int RING = NBUF * STAGE;
     static constexpr int LDS = RING > BM * CLD * 4 ? RING : BM * CLD * 4;
     // quant blocks: with one MFMA column tile per wave, blocks are software
@@ -99,36 +95,8 @@ struct GemmParams {
     const uint8_t *b_d, *b_m;     // stage-major fp16 planes, b_np rows per group
     int64_t b_ld, b_np;
     int M, N, nstages, tiles_m, tiles_n, ntiles;
-    const uint8_t *a_lo, *b_lo;   // split: low planes (same layout as a, b)
-    float alpha;                  // split: accumulator scale (2^-k of the weight planes)
-    int cw, ch, spt;              // 3×3 implicit GEMM geometry (ConvGeom)
-    const uint8_t *zero;
     EpiArgs e;
 };
-
-// gelu_erf(x) = 0.5·x·(1 + erf(x/√2)) (ggml_vec_gelu_erf_f32), branch-free.
-// With z = |x|/√2, erfc(z) = t·P(t)·e^(−z²), t = 1/(1 + 0.63·z), P a degree-8
-// polynomial fitted by least squares to erfc(z)·e^(z²)/t on z ∈ [0, 6]
-// (relative error ≤ 3.1e-7 in float32; beyond z = 6, e^(−z²) < 3e-16 makes
-// the product vanish).  1 + erf(x/√2) is 2 − erfc(z) for x ≥ 0 and erfc(z)
-// for x < 0, so neither branch cancels.
-__device__ __forceinline__ float gelu_erf(float x) {
-    const float z = fabsf(x) * 0.70710678118654752440f;
-    const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.63f, z, 1.0f));
-    float P = 0.06951001286506653f;
-    P = __builtin_fmaf(P, t, -0.4178536534309387f);
-    P = __builtin_fmaf(P, t, 1.0159318447113037f);
-    P = __builtin_fmaf(P, t, -1.1790587902069092f);
-    P = __builtin_fmaf(P, t, 0.5140861868858337f);
-    P = __builtin_fmaf(P, t, -0.02842715010046959f);
-    P = __builtin_fmaf(P, t, 0.3184112310409546f);
-    P = __builtin_fmaf(P, t, 0.35179051756858826f);
-    P = __builtin_fmaf(P, t, 0.3556097745895386f);
-    const float e = __builtin_amdgcn_exp2f(-(z * z) * 1.4426950408889634f);
-    const float E = t * P * e;
-    const float w = (x >= 0.f) ? 2.0f - E : E;
-    return 0.5f * x * w;
-}
 
 __device__ __forceinline__ uint16_t f2h_bits(float v) { return half_bits(v); }
 
@@ -175,38 +143,6 @@ __device__ __forceinline__ void quant_block32(const float *v, int8_t *qdst, uint
 #define S3E_SWZ_SHIFT 1
 #endif
 __device__ __forceinline__ int swz(int r) { return (r >> S3E_SWZ_SHIFT) & 7; }
-
-// Wait until at most N of this wave's vector-memory operations are
-// outstanding and all its LDS reads have returned, then join the work-group.
-// The memory clobber keeps the compiler from moving LDS accesses across it.
-template <int N>
-__device__ __forceinline__ void wait_and_barrier() {
-    __asm__ volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
-}
-
-// Four consecutive values of one row into an fp16 / split-fp16 / f32
-// activation (col % 4 == 0).  The split low half is the fp16 rounding of the
-// exact fp32 difference x − hi.
-__device__ __forceinline__ void store4_act(const Act &o, int64_t row, int col, const float v[4]) {
-    if (o.kind == A_F32) {
-        *(float4 *)((float *)o.x + row * o.ld + col) = make_float4(v[0], v[1], v[2], v[3]);
-        return;
-    }
-    _Float16 h[4];
-    uint32_t w[2], wl[2];
-#pragma unroll
-    for (int j = 0; j < 4; j++) h[j] = to_half(v[j]);
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-        w[j] = (uint32_t)__builtin_bit_cast(uint16_t, h[2 * j]) | ((uint32_t)__builtin_bit_cast(uint16_t, h[2 * j + 1]) << 16);
-        const _Float16 l0 = (_Float16)(v[2 * j] - (float)h[2 * j]);
-        const _Float16 l1 = (_Float16)(v[2 * j + 1] - (float)h[2 * j + 1]);
-        wl[j] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
-    }
-    const int64_t o16 = row * o.ld + col;
-    *(uint2 *)((_Float16 *)o.x + o16) = make_uint2(w[0], w[1]);
-    if (o.kind == A_F16X2) *(uint2 *)((_Float16 *)o.lo + o16) = make_uint2(wl[0], wl[1]);
-}
 
 // Epilogue from the fp32 tile Ct [BM][CLD] in LDS (scaled, complete), run by
 // the NT_ threads of the work-group.
@@ -356,32 +292,6 @@ __device__ __forceinline__ void epilogue(const GemmParams &p, const float *Ct, i
                               o.kind == A_Q8_1 ? o.s + blk : nullptr);
             }
         }
-    } else if constexpr (EPI == EPI_DECONV || EPI == EPI_ACT) {
-        // lane ↔ 4 consecutive columns (N % 4 == 0, checked by the launcher)
-        const int f = t & 31;
-        const int gn = n0 + 4 * f;
-        int q = 0, co = gn;
-        if constexpr (EPI == EPI_DECONV) {
-            q = gn / e.dc_cout;  // kernel tap: ky = q / 2, kx = q % 2
-            co = gn - q * e.dc_cout;
-        }
-        for (int row = t >> 5; row < BM; row += NT_ / 32) {
-            const int gm = m0 + row;
-            if (gm >= p.M || gn >= p.N) continue;
-            const float4 x = *(const float4 *)(Ct + row * CLD + 4 * f);
-            const float4 bb = *(const float4 *)(e.bias + co);
-            float v[4] = {__fadd_rn(x.x, bb.x), __fadd_rn(x.y, bb.y), __fadd_rn(x.z, bb.z), __fadd_rn(x.w, bb.w)};
-            int64_t orow = gm;
-            if constexpr (EPI == EPI_DECONV) {
-                if (e.gelu) {
-#pragma unroll
-                    for (int j = 0; j < 4; j++) v[j] = gelu_erf(v[j]);
-                }
-                const int iy = gm / e.dc_w, ix = gm - iy * e.dc_w;
-                orow = (int64_t)(2 * iy + (q >> 1)) * (2 * e.dc_w) + 2 * ix + (q & 1);
-            }
-            store4_act(e.out, orow, co, v);
-        }
     } else {
         // EPI_F32 / EPI_RESID / EPI_POS: lane ↔ 4 consecutive columns, so that one
         // wave store covers 2 rows × 512 contiguous bytes
@@ -424,7 +334,7 @@ __device__ __forceinline__ void epilogue(const GemmParams &p, const float *Ct, i
     }
 }
 
-template <int WK, int EPI, int BM, int WAVES, int CONV = 0>
+template <int WK, int EPI, int BM, int WAVES>
 __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 3 : 256 / BM) void k_gemm(GemmParams p) {
     using C = Cfg<WK, BM, WAVES>;
     constexpr int MT = C::MT, NT = C::NT, NBUF = C::NBUF;
@@ -452,26 +362,21 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 3 : 256 / BM) void k_gemm(
     // a 1 KB run = 8 rows, i.e. slot lane & 7 of row lane >> 3 of the run; it
     // fetches the chunk that belongs there
     const int dma_row = lane >> 3;
-    int64_t a_row[C::NA];
+    const uint8_t *a_src[C::NA];
     int a_cofs[C::NA];
-    int a_y[C::NA], a_x[C::NA];  // CONV: output pixel of the row
 #pragma unroll
     for (int j = 0; j < C::NA; j++) {
         const int row = 8 * (wave * C::NA + j) + dma_row;
         const int gm = min(m0 + row, p.M - 1);
-        a_row[j] = (int64_t)gm * p.a_ld;
+        a_src[j] = p.a + (int64_t)gm * p.a_ld;
         a_cofs[j] = ((lane & 7) ^ swz(row)) << 4;
-        if constexpr (CONV) {
-            a_y[j] = gm / p.cw;
-            a_x[j] = gm - a_y[j] * p.cw;
-        }
     }
     const int64_t a_last = p.a_kbytes - 16;
-    int64_t b_row[C::NB];
+    const uint8_t *b_src[C::NB];
 #pragma unroll
     for (int j = 0; j < C::NB; j++) {
         const int col = 8 * (wave * C::NB + j) + dma_row;
-        b_row[j] = (int64_t)(n0 + col) * p.b_ld + (((lane & 7) ^ swz(col)) << 4);
+        b_src[j] = p.b + (int64_t)(n0 + col) * p.b_ld + (((lane & 7) ^ swz(col)) << 4);
     }
     const uint8_t *s_src[C::NS > 0 ? C::NS : 1];
     int64_t s_step[C::NS > 0 ? C::NS : 1];
@@ -504,41 +409,16 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 3 : 256 / BM) void k_gemm(
 
     auto issue = [&](int s) {
         uint8_t *L = lds + (s % NBUF) * C::STAGE;
-        if constexpr (CONV) {
-            // 3×3 implicit GEMM: stage s is tap s / spt, channels 64·(s % spt)
-            const int tap = s / p.spt, kc = s - tap * p.spt;
-            const int dy = tap / 3 - 1, dx = tap - (tap / 3) * 3 - 1;
-            const int64_t shift = (int64_t)(dy * p.cw + dx) * p.a_ld + kc * ROWB;
 #pragma unroll
-            for (int j = 0; j < C::NA; j++) {
-                const bool in = (unsigned)(a_y[j] + dy) < (unsigned)p.ch && (unsigned)(a_x[j] + dx) < (unsigned)p.cw;
-                const int64_t o = a_row[j] + shift + a_cofs[j];
-                const uint8_t *z = p.zero + a_cofs[j];
-                __builtin_amdgcn_global_load_lds((const void *)(in ? p.a + o : z),
-                                                 LDS_PTR(L + C::OFF_A + (wave * C::NA + j) * 1024), 16, 0, 0);
-                if constexpr (C::split)
-                    __builtin_amdgcn_global_load_lds((const void *)(in ? p.a_lo + o : z),
-                                                     LDS_PTR(L + C::OFF_ALO + (wave * C::NA + j) * 1024), 16, 0, 0);
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < C::NA; j++) {
-                const int64_t off = a_row[j] + min((int64_t)s * ROWB + a_cofs[j], a_last);
-                __builtin_amdgcn_global_load_lds((const void *)(p.a + off),
-                                                 LDS_PTR(L + C::OFF_A + (wave * C::NA + j) * 1024), 16, 0, 0);
-                if constexpr (C::split)
-                    __builtin_amdgcn_global_load_lds((const void *)(p.a_lo + off),
-                                                     LDS_PTR(L + C::OFF_ALO + (wave * C::NA + j) * 1024), 16, 0, 0);
-            }
+        for (int j = 0; j < C::NA; j++) {
+            const int64_t off = min((int64_t)s * ROWB + a_cofs[j], a_last);
+            __builtin_amdgcn_global_load_lds((const void *)(a_src[j] + off),
+                                             LDS_PTR(L + C::OFF_A + (wave * C::NA + j) * 1024), 16, 0, 0);
         }
 #pragma unroll
-        for (int j = 0; j < C::NB; j++) {
-            __builtin_amdgcn_global_load_lds((const void *)(p.b + b_row[j] + (int64_t)s * ROWB),
+        for (int j = 0; j < C::NB; j++)
+            __builtin_amdgcn_global_load_lds((const void *)(b_src[j] + (int64_t)s * ROWB),
                                              LDS_PTR(L + C::OFF_B + (wave * C::NB + j) * 1024), 16, 0, 0);
-            if constexpr (C::split)
-                __builtin_amdgcn_global_load_lds((const void *)(p.b_lo + b_row[j] + (int64_t)s * ROWB),
-                                                 LDS_PTR(L + C::OFF_BLO + (wave * C::NB + j) * 1024), 16, 0, 0);
-        }
         if constexpr (C::quant) {
 #pragma unroll
             for (int j = 0; j < C::NS; j++)
@@ -663,31 +543,18 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 3 : 256 / BM) void k_gemm(
                     }
                 }
             }
-        } else if constexpr (WK == WK_F16 || WK == WK_F16X3) {
+        } else if constexpr (WK == WK_F16) {
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) {
-                v8h bv[NT], bl[NT];
+                v8h bv[NT];
 #pragma unroll
-                for (int n = 0; n < NT; n++) {
-                    bv[n] = *(const v8h *)(L + b_off[n] + cofs[ks]);
-                    if constexpr (C::split) bl[n] = *(const v8h *)(L + b_off[n] + (C::OFF_BLO - C::OFF_B) + cofs[ks]);
-                }
+                for (int n = 0; n < NT; n++) bv[n] = *(const v8h *)(L + b_off[n] + cofs[ks]);
 #pragma unroll
                 for (int i = 0; i < MT; i++) {
                     const v8h av = *(const v8h *)(L + a_off[i] + cofs[ks]);
 #pragma unroll
                     for (int n = 0; n < NT; n++)
                         acc[i][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv[n], acc[i][n], 0, 0, 0);
-                    if constexpr (C::split) {
-                        // x·w = (xh + xl)(wh + wl) ≈ xh·wh + xh·wl + xl·wh (xl·wl ~ 2^-22 relative)
-                        const v8h al = *(const v8h *)(L + a_off[i] + (C::OFF_ALO - C::OFF_A) + cofs[ks]);
-#pragma unroll
-                        for (int n = 0; n < NT; n++)
-                            acc[i][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bl[n], acc[i][n], 0, 0, 0);
-#pragma unroll
-                        for (int n = 0; n < NT; n++)
-                            acc[i][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bv[n], acc[i][n], 0, 0, 0);
-                    }
                 }
             }
         } else {
@@ -731,8 +598,7 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 3 : 256 / BM) void k_gemm(
 
     // ---- stage the fp32 tile in LDS ----
     float *Ct = (float *)lds;
-    // quant: remove the doubled scale products; split: undo the weight scale
-    const float kScale = C::quant ? 0.5f : (C::split ? p.alpha : 1.0f);
+    constexpr float kScale = C::quant ? 0.5f : 1.0f;  // remove the doubled scale products
 #pragma unroll
     for (int i = 0; i < MT; i++)
 #pragma unroll
@@ -764,6 +630,7 @@ hipError_t dispatch_epi(Epi epi, const GemmParams &p, hipStream_t st) {
         case EPI_POS: return launch_one<WK, EPI_POS, 64, WAVES>(p, st);
         case EPI_GELU: return launch_one<WK, EPI_GELU, 64, WAVES>(p, st);
         case EPI_QKV: return launch_one<WK, EPI_QKV, 64, WAVES>(p, st);
+        default: break;  // the neck epilogues belong to k_conv
     }
     return hipErrorInvalidValue;
 }
@@ -782,23 +649,20 @@ hipError_t dispatch_waves(Epi epi, GemmParams &p, hipStream_t st) {
 
 }  // namespace
 
-namespace {
-
-GemmParams make_params(const Weight &w, const Act &a, int64_t M, const EpiArgs &ea) {
+hipError_t launch_gemm(const Weight &w, const Act &a, int64_t M, Epi epi, const EpiArgs &ea,
+                       hipStream_t st) {
+    if (M <= 0) return hipSuccess;
     GemmParams p{};
-    const int esize = (w.kind == WK_F16 || w.kind == WK_F16X3) ? 2 : (w.kind == WK_F32 ? 4 : 1);
+    const int esize = (w.kind == WK_F16) ? 2 : (w.kind == WK_F32 ? 4 : 1);
     p.a = (const uint8_t *)a.x;
     p.a_d = (const uint8_t *)a.d;
     p.a_s = (const uint8_t *)a.s;
-    p.a_lo = (const uint8_t *)a.lo;
     p.a_ld = a.ld * esize;
     p.a_kbytes = w.K * esize;
     p.a_mp = a.mp;
     p.b = (const uint8_t *)w.q;
     p.b_d = (const uint8_t *)w.d;
     p.b_m = (const uint8_t *)w.m;
-    p.b_lo = (const uint8_t *)w.lo;
-    p.alpha = w.alpha;
     p.b_ld = w.Kp * esize;
     p.b_np = w.Np;
     p.M = (int)M;
@@ -806,58 +670,6 @@ GemmParams make_params(const Weight &w, const Act &a, int64_t M, const EpiArgs &
     p.nstages = (int)(w.Kp / stage_k(w.kind));
     p.tiles_n = (int)(w.Np / BN);
     p.e = ea;
-    return p;
-}
-
-template <int WK, int EPI, int CONV>
-hipError_t launch_conv_one(GemmParams &p, hipStream_t st) {
-    constexpr int BM = 64, WAVES = 4;
-    p.tiles_m = (p.M + BM - 1) / BM;
-    p.ntiles = p.tiles_m * p.tiles_n;
-    const int grid = ((p.ntiles + 7) / 8) * 8;
-    hipLaunchKernelGGL((k_gemm<WK, EPI, BM, WAVES, CONV>), dim3(grid), dim3(64 * WAVES), 0, st, p);
-    return hipGetLastError();
-}
-
-template <int WK>
-hipError_t dispatch_conv(Epi epi, bool conv3, GemmParams &p, hipStream_t st) {
-    if (conv3) return epi == EPI_F32 ? launch_conv_one<WK, EPI_F32, 1>(p, st) : hipErrorInvalidValue;
-    switch (epi) {
-        case EPI_F32: return launch_conv_one<WK, EPI_F32, 0>(p, st);
-        case EPI_DECONV: return launch_conv_one<WK, EPI_DECONV, 0>(p, st);
-        case EPI_ACT: return launch_conv_one<WK, EPI_ACT, 0>(p, st);
-        default: return hipErrorInvalidValue;
-    }
-}
-
-}  // namespace
-
-hipError_t launch_conv(const Weight &w, const Act &a, int64_t M, Epi epi, const EpiArgs &ea,
-                       const ConvGeom *g, hipStream_t st) {
-    if (M <= 0) return hipSuccess;
-    if ((w.kind != WK_F16 && w.kind != WK_F16X3) || w.N % 4 != 0) return hipErrorInvalidValue;
-    if ((w.kind == WK_F16X3) != (a.kind == A_F16X2)) return hipErrorInvalidValue;
-    GemmParams p = make_params(w, a, M, ea);
-    if (g) {
-        if (g->spt <= 0 || w.K != 9LL * 64 * g->spt || a.ld != 64LL * g->spt || (int64_t)g->w * g->h != M ||
-            !g->zero)
-            return hipErrorInvalidValue;
-        p.cw = g->w;
-        p.ch = g->h;
-        p.spt = g->spt;
-        p.zero = (const uint8_t *)g->zero;
-    }
-    if (epi == EPI_DECONV && (ea.dc_w <= 0 || ea.dc_cout <= 0 || ea.dc_cout % 4 != 0 || w.N % ea.dc_cout != 0 ||
-                              M % ea.dc_w != 0))
-        return hipErrorInvalidValue;
-    return w.kind == WK_F16 ? dispatch_conv<WK_F16>(epi, g != nullptr, p, st)
-                            : dispatch_conv<WK_F16X3>(epi, g != nullptr, p, st);
-}
-
-hipError_t launch_gemm(const Weight &w, const Act &a, int64_t M, Epi epi, const EpiArgs &ea,
-                       hipStream_t st) {
-    if (M <= 0) return hipSuccess;
-    GemmParams p = make_params(w, a, M, ea);
     // 64-row tiles: two or three work-groups share a CU, so one work-group's
     // epilogue overlaps another's main loop; with 128-row tiles (one per CU)
     // every CU alternates between the two phases.

@@ -126,10 +126,10 @@ struct EpiArgs {
 // Implicit-GEMM geometry of a 3×3 stride-1 pad-1 convolution over an NHWC
 // image: row m of A is output pixel (m / w, m % w); stage s of K reads the
 // input pixel shifted by tap s / spt ((dy, dx) = (tap / 3 − 1, tap % 3 − 1))
-// at channels [64·(s % spt), +64), or the zero row outside the image.
+// at channels [32·(s % spt), +32), or the zero row outside the image.
 struct ConvGeom {
     int w = 0, h = 0;
-    int spt = 0;                   // stages per tap = Cin / 64
+    int spt = 0;                   // stages per tap = Cin / 32
     const void *zero = nullptr;    // ≥ 128 zero bytes, 16-byte aligned
 };
 
@@ -161,8 +161,9 @@ struct AttnArgs {
 // ---- kernel launchers (k_*.hip) ----
 hipError_t launch_gemm(const Weight &w, const Act &a, int64_t M, Epi epi, const EpiArgs &ea,
                        hipStream_t st);
-// Neck GEMMs (WK_F16 or WK_F16X3 weights): EPI_DECONV / EPI_ACT / EPI_F32 on
-// plain rows, or EPI_F32 as a 3×3 implicit GEMM when g is given.
+// Neck GEMMs (k_conv.hip; WK_F16 or WK_F16X3 weights with N padded to
+// CONV_BN): EPI_DECONV / EPI_ACT / EPI_F32 on plain rows, or EPI_F32 as a
+// 3×3 implicit GEMM when g is given.
 hipError_t launch_conv(const Weight &w, const Act &a, int64_t M, Epi epi, const EpiArgs &ea,
                        const ConvGeom *g, hipStream_t st);
 // NHWC f32 [h][w][c] → act (A_F16 or A_F16X2) of the same pixels (pool = 1)
@@ -192,6 +193,38 @@ __device__ __forceinline__ _Float16 to_half(float x) {
 }
 __device__ __forceinline__ uint16_t half_bits(float x) { return __builtin_bit_cast(uint16_t, to_half(x)); }
 
+// gelu_erf(x) = 0.5·x·(1 + erf(x/√2)) (ggml_vec_gelu_erf_f32), branch-free.
+// With z = |x|/√2, erfc(z) = t·P(t)·e^(−z²), t = 1/(1 + 0.63·z), P a degree-8
+// polynomial fitted by least squares to erfc(z)·e^(z²)/t on z ∈ [0, 6]
+// (relative error ≤ 3.1e-7 in float32; beyond z = 6, e^(−z²) < 3e-16 makes
+// the product vanish).  1 + erf(x/√2) is 2 − erfc(z) for x ≥ 0 and erfc(z)
+// for x < 0, so neither branch cancels.
+__device__ __forceinline__ float gelu_erf(float x) {
+    const float z = fabsf(x) * 0.70710678118654752440f;
+    const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.63f, z, 1.0f));
+    float P = 0.06951001286506653f;
+    P = __builtin_fmaf(P, t, -0.4178536534309387f);
+    P = __builtin_fmaf(P, t, 1.0159318447113037f);
+    P = __builtin_fmaf(P, t, -1.1790587902069092f);
+    P = __builtin_fmaf(P, t, 0.5140861868858337f);
+    P = __builtin_fmaf(P, t, -0.02842715010046959f);
+    P = __builtin_fmaf(P, t, 0.3184112310409546f);
+    P = __builtin_fmaf(P, t, 0.35179051756858826f);
+    P = __builtin_fmaf(P, t, 0.3556097745895386f);
+    const float e = __builtin_amdgcn_exp2f(-(z * z) * 1.4426950408889634f);
+    const float E = t * P * e;
+    const float w = (x >= 0.f) ? 2.0f - E : E;
+    return 0.5f * x * w;
+}
+
+// Wait until at most N of this wave's vector-memory operations are
+// outstanding and all its LDS reads have returned, then join the work-group.
+// The memory clobber keeps the compiler from moving LDS accesses across it.
+template <int N>
+__device__ __forceinline__ void wait_and_barrier() {
+    __asm__ volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
 // Stage widths (elements of K per pipeline stage) by weight kind.
 inline int64_t stage_k(WKind w) {
     switch (w) {
@@ -201,6 +234,7 @@ inline int64_t stage_k(WKind w) {
     }
 }
 constexpr int GEMM_BN = 128;
+constexpr int CONV_BN = 256;
 
 // ---- error state (s3e_runtime.cpp) ----
 void set_error(const char *fmt, ...);

@@ -82,14 +82,14 @@ void free_weight(Weight &w) {
 // f32 weights (N rows of K) as two fp16 planes for the split-precision GEMM:
 // w·2^k = hi + lo with hi = fp16(w·2^k) and lo = fp16(w·2^k − hi), k chosen
 // so that the largest |w|·2^k lies in [2^14, 2^15); alpha = 2^-k.
-int upload_weight_split(const float *src, int64_t K, int64_t N, Weight &w) {
+int upload_weight_split(const float *src, int64_t K, int64_t N, Weight &w, int64_t npad) {
     w = Weight{};
     w.kind = WK_F16X3;
     w.ggml_type = S3E_TYPE_F32;
     w.K = K;
     w.N = N;
     w.Kp = round_up(K, stage_k(WK_F16X3));
-    w.Np = round_up(N, GEMM_BN);
+    w.Np = round_up(N, npad);
     float amax = 0.f;
     for (int64_t i = 0; i < K * N; i++) amax = std::max(amax, std::fabs(src[i]));
     int k = 0;
@@ -123,7 +123,7 @@ int upload_weight_split(const float *src, int64_t K, int64_t N, Weight &w) {
 
 // Repack ggml bytes (N rows of K in `type`) into the GEMM layout and upload.
 int upload_weight(int device, int type, int64_t K, int64_t N, const uint8_t *src, size_t nbytes,
-                  Weight &w) {
+                  Weight &w, int64_t npad = GEMM_BN) {
     (void)device;
     if (type != S3E_TYPE_F32 && type != S3E_TYPE_F16 && type != S3E_TYPE_Q4_0 && type != S3E_TYPE_Q4_1 &&
         type != S3E_TYPE_Q8_0) {
@@ -145,7 +145,7 @@ int upload_weight(int device, int type, int64_t K, int64_t N, const uint8_t *src
     w.K = K;
     w.N = N;
     w.Kp = round_up(K, stage_k(w.kind));
-    w.Np = round_up(N, GEMM_BN);
+    w.Np = round_up(N, npad);
     w.Kbp = w.Kp / 32;
     const int64_t Kb = K / 32;
     std::vector<uint8_t> q;
@@ -186,6 +186,7 @@ int upload_weight(int device, int type, int64_t K, int64_t N, const uint8_t *src
             q.assign((size_t)(w.Np * w.Kp * es), 0);
             for (int64_t n = 0; n < N; n++) std::memcpy(&q[(size_t)(n * w.Kp * es)], src + (size_t)n * rs, (size_t)K * es);
         } break;
+        default: break;  // WK_F16X3 comes from upload_weight_split
     }
     hipError_t e = hipMalloc(&w.q, q.size());
     if (e == hipSuccess) e = hipMemcpy(w.q, q.data(), q.size(), hipMemcpyHostToDevice);
@@ -653,7 +654,8 @@ int load_neck_tensor(s3e_model *m, const std::string &name, const RawTensor &t) 
                     w[(size_t)((q * Cout + co) * Cin + ci)] = h;
                 }
         Weight &dst = sc.dc[f == "dconv_2x2_1.weight" ? 1 : 0];
-        rc = upload_weight(m->ctx->device, S3E_TYPE_F16, Cin, 4 * Cout, (const uint8_t *)w.data(), w.size() * 2, dst);
+        rc = upload_weight(m->ctx->device, S3E_TYPE_F16, Cin, 4 * Cout, (const uint8_t *)w.data(), w.size() * 2, dst,
+                           CONV_BN);
     } else if (f == "conv_1x1.weight" || f == "conv_3x3.weight") {
         // ggml [kW, kH, Cin, Cout]: element (kx, ky, ci, co) at ((co·Cin + ci)·kH + ky)·kW + kx;
         // the GEMM's K order is [ky][kx][Cin] so that one stage stays inside one tap
@@ -672,8 +674,11 @@ int load_neck_tensor(s3e_model *m, const std::string &name, const RawTensor &t) 
                         if (t.type == 1) std::memcpy(&wh[d], t.data.data() + 2 * src, 2);
                         else wf[d] = ((const float *)t.data.data())[src];
                     }
-        if (t.type == 1) rc = upload_weight(m->ctx->device, S3E_TYPE_F16, K, Cout, (const uint8_t *)wh.data(), wh.size() * 2, dst);
-        else rc = upload_weight_split(wf.data(), K, Cout, dst);
+        if (t.type == 1)
+            rc = upload_weight(m->ctx->device, S3E_TYPE_F16, K, Cout, (const uint8_t *)wh.data(), wh.size() * 2, dst,
+                               CONV_BN);
+        else
+            rc = upload_weight_split(wf.data(), K, Cout, dst, CONV_BN);
     } else {
         return S3E_OK;
     }
@@ -919,9 +924,16 @@ struct s3e_state {
     int64_t side[4] = {0, 0, 0, 0};
     float *neck_out[2][4] = {{nullptr, nullptr, nullptr, nullptr}, {nullptr, nullptr, nullptr, nullptr}};
     float *pe[4] = {nullptr, nullptr, nullptr, nullptr};
-    _Float16 *nx = nullptr, *n_dc = nullptr, *n_a = nullptr, *n_b = nullptr;
-    int64_t nx_cap = 0, n_a_cap = 0, n_b_cap = 0;
+    // fp16 planes of vit_output (nx), the scale-0 first deconvolution output
+    // (n_dc), and per level the 1×1 input (lv_a) and 3×3 input (lv_b)
+    _Float16 *nx = nullptr, *n_dc = nullptr, *lv_a[4] = {}, *lv_b[4] = {};
+    int64_t nx_cap = 0, lv_a_cap[4] = {}, lv_b_cap[4] = {};
     void *zero = nullptr;
+    // the four levels are independent after the shared conversion: levels 1
+    // and 2-3 run on two more streams (default priority) joined back into
+    // the context stream by events
+    hipStream_t aux[2] = {nullptr, nullptr};
+    hipEvent_t ev_fork = nullptr, ev_join[2] = {nullptr, nullptr};
 };
 
 extern "C" void s3e_state_free(s3e_state *st) {
@@ -941,8 +953,17 @@ extern "C" void s3e_state_free(s3e_state *st) {
             if (p) (void)hipFree(p);
     for (float *p : st->pe)
         if (p) (void)hipFree(p);
-    for (void *p : {(void *)st->nx, (void *)st->n_dc, (void *)st->n_a, (void *)st->n_b, st->zero})
+    for (void *p : {(void *)st->nx, (void *)st->n_dc, st->zero})
         if (p) (void)hipFree(p);
+    for (int i = 0; i < 4; i++) {
+        if (st->lv_a[i]) (void)hipFree(st->lv_a[i]);
+        if (st->lv_b[i]) (void)hipFree(st->lv_b[i]);
+    }
+    for (int i = 0; i < 2; i++) {
+        if (st->aux[i]) (void)hipStreamDestroy(st->aux[i]);
+        if (st->ev_join[i]) (void)hipEventDestroy(st->ev_join[i]);
+    }
+    if (st->ev_fork) (void)hipEventDestroy(st->ev_fork);
     delete st;
 }
 
@@ -985,12 +1006,20 @@ hipError_t alloc_neck(s3e_state *st) {
     }
     const int64_t S3 = st->side[3] * st->side[3];
     st->nx_cap = T * E;
-    st->n_a_cap = std::max({16 * T * D, 4 * T * mid1, S3 * E});
-    st->n_b_cap = 16 * T * D;
+    const int64_t a_cap[4] = {16 * T * D, 4 * T * mid1, 0, S3 * E};
     hipError_t e = hipMalloc(&st->nx, (size_t)st->nx_cap * 2 * 2);
     if (e == hipSuccess) e = hipMalloc(&st->n_dc, (size_t)(4 * T * mid0) * 2);
-    if (e == hipSuccess) e = hipMalloc(&st->n_a, (size_t)st->n_a_cap * 2 * 2);
-    if (e == hipSuccess) e = hipMalloc(&st->n_b, (size_t)st->n_b_cap * 2 * 2);
+    for (int i = 0; i < 4 && e == hipSuccess; i++) {
+        st->lv_a_cap[i] = a_cap[i];
+        st->lv_b_cap[i] = st->side[i] * st->side[i] * D;
+        if (a_cap[i]) e = hipMalloc(&st->lv_a[i], (size_t)a_cap[i] * 2 * 2);
+        if (e == hipSuccess) e = hipMalloc(&st->lv_b[i], (size_t)st->lv_b_cap[i] * 2 * 2);
+    }
+    for (int i = 0; i < 2 && e == hipSuccess; i++) {
+        e = hipStreamCreateWithFlags(&st->aux[i], hipStreamNonBlocking);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&st->ev_join[i], hipEventDisableTiming);
+    }
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&st->ev_fork, hipEventDisableTiming);
     if (e == hipSuccess) e = hipMalloc(&st->zero, 256);
     if (e == hipSuccess) e = hipMemsetAsync(st->zero, 0, 256, st->ctx->stream);
     for (int which = 0; which < 2 && e == hipSuccess; which++) {
@@ -1150,35 +1179,24 @@ Act plane_act(AKind kind, _Float16 *base, int64_t cap, int64_t ld) {
     return a;
 }
 
-// sam3_build_neck_graph (sam3.cpp:3863-3921) for one neck on vit_output x
-// (G² rows of E f32): 4 levels into st->neck_out[which].  NHWC throughout:
-// a pixel is a row of channels, so a 1×1 conv is a plain GEMM, a 2×2
-// stride-2 deconvolution is a GEMM with N = 4·Cout whose epilogue scatters
-// each tap to its output pixel, and the 3×3 conv is an implicit GEMM over
-// shifted pixel rows.  The vit_output conversion to fp16 planes (nx) is
-// shared by both necks and done by the caller.
-hipError_t run_neck(s3e_state *st, int which, const float *x) {
+// One level of sam3_build_neck_graph (sam3.cpp:3863-3921) for one neck on
+// vit_output x (G² rows of E f32), into st->neck_out[which][lvl], on stream
+// s.  NHWC throughout: a pixel is a row of channels, so a 1×1 conv is a plain
+// GEMM, a 2×2 stride-2 deconvolution is a GEMM with N = 4·Cout whose
+// epilogue scatters each tap to its output pixel, and the 3×3 conv is an
+// implicit GEMM over shifted pixel rows.  nx (the fp16 planes of x) is
+// written by the caller before any level runs.
+hipError_t run_level(s3e_state *st, int which, int lvl, const float *x, hipStream_t s) {
     const s3e_model *m = st->m;
-    const Neck &nk = m->necks[which];
-    hipStream_t s = st->ctx->stream;
+    const NeckScale &sc = m->necks[which].s[lvl];
     const int G = m->grid;
     const int64_t T = (int64_t)G * G, E = m->E, D = m->neck_dim;
-    float *const *out = st->neck_out[which];
-    auto conv3 = [&](const NeckScale &sc, const Act &in, int side, float *y) {
-        EpiArgs e;
-        e.bias = sc.c3_b;
-        e.y = y;
-        e.ldy = D;
-        ConvGeom g;
-        g.w = g.h = side;
-        g.spt = (int)(D / 64);
-        g.zero = st->zero;
-        return launch_conv(sc.c3, in, (int64_t)side * side, EPI_F32, e, &g, s);
-    };
-    auto conv1 = [&](const NeckScale &sc, const Act &in, int64_t M, const Act &o) {
+    const int side = (int)st->side[lvl];
+    const Act a_3 = plane_act(act_kind_for(sc.c3.kind), st->lv_b[lvl], st->lv_b_cap[lvl], D);
+    auto conv1 = [&](const Act &in, int64_t M) {
         EpiArgs e;
         e.bias = sc.c1_b;
-        e.out = o;
+        e.out = a_3;
         return launch_conv(sc.c1, in, M, EPI_ACT, e, nullptr, s);
     };
     auto deconv = [&](const Weight &w, const float *b, const Act &in, int in_side, int gelu, const Act &o) {
@@ -1191,63 +1209,71 @@ hipError_t run_neck(s3e_state *st, int which, const float *x) {
         return launch_conv(w, in, (int64_t)in_side * in_side, EPI_DECONV, e, nullptr, s);
     };
     const Act x16 = plane_act(A_F16, st->nx, st->nx_cap, E);  // fp16(x): the deconvolutions' input
-    hipError_t err;
-    // scale 0 (4×): deconv + bias + gelu_erf (fp16, the next deconv's input), deconv + bias, 1×1, 3×3
-    {
-        const NeckScale &sc = nk.s[0];
-        const int64_t mid = sc.dc[0].N / 4;
-        const AKind k1 = act_kind_for(sc.c1.kind), k3 = act_kind_for(sc.c3.kind);
-        const Act a_dc = plane_act(A_F16, st->n_dc, 0, mid);
-        const Act a_1 = plane_act(k1, st->n_a, st->n_a_cap, D);
-        const Act a_3 = plane_act(k3, st->n_b, st->n_b_cap, D);
+    hipError_t err = hipSuccess;
+    if (lvl == 0) {
+        // 4×: deconv + bias + gelu_erf (fp16: the next deconv's input), deconv + bias, 1×1
+        const Act a_dc = plane_act(A_F16, st->n_dc, 0, sc.dc[0].N / 4);
+        const Act a_1 = plane_act(act_kind_for(sc.c1.kind), st->lv_a[0], st->lv_a_cap[0], D);
         if ((err = deconv(sc.dc[0], sc.dc_b[0], x16, G, 1, a_dc)) != hipSuccess) return err;
         if ((err = deconv(sc.dc[1], sc.dc_b[1], a_dc, 2 * G, 0, a_1)) != hipSuccess) return err;
-        if ((err = conv1(sc, a_1, 16 * T, a_3)) != hipSuccess) return err;
-        if ((err = conv3(sc, a_3, 4 * G, out[0])) != hipSuccess) return err;
-    }
-    // scale 1 (2×): deconv + bias, 1×1, 3×3
-    {
-        const NeckScale &sc = nk.s[1];
-        const int64_t mid = sc.dc[0].N / 4;
-        const Act a_1 = plane_act(act_kind_for(sc.c1.kind), st->n_a, st->n_a_cap, mid);
-        const Act a_3 = plane_act(act_kind_for(sc.c3.kind), st->n_b, st->n_b_cap, D);
+        err = conv1(a_1, 16 * T);
+    } else if (lvl == 1) {
+        // 2×: deconv + bias, 1×1
+        const Act a_1 = plane_act(act_kind_for(sc.c1.kind), st->lv_a[1], st->lv_a_cap[1], sc.dc[0].N / 4);
         if ((err = deconv(sc.dc[0], sc.dc_b[0], x16, G, 0, a_1)) != hipSuccess) return err;
-        if ((err = conv1(sc, a_1, 4 * T, a_3)) != hipSuccess) return err;
-        if ((err = conv3(sc, a_3, 2 * G, out[1])) != hipSuccess) return err;
-    }
-    // scale 2 (1×): 1×1 on x itself, 3×3
-    {
-        const NeckScale &sc = nk.s[2];
-        const Act a_1 = plane_act(act_kind_for(sc.c1.kind), st->nx, st->nx_cap, E);
-        const Act a_3 = plane_act(act_kind_for(sc.c3.kind), st->n_b, st->n_b_cap, D);
-        if ((err = conv1(sc, a_1, T, a_3)) != hipSuccess) return err;
-        if ((err = conv3(sc, a_3, G, out[2])) != hipSuccess) return err;
-    }
-    // scale 3 (0.5×): 2×2 max pool, 1×1, 3×3
-    {
-        const NeckScale &sc = nk.s[3];
-        const int g3 = (int)st->side[3];
-        const Act a_1 = plane_act(act_kind_for(sc.c1.kind), st->n_a, st->n_a_cap, E);
-        const Act a_3 = plane_act(act_kind_for(sc.c3.kind), st->n_b, st->n_b_cap, D);
+        err = conv1(a_1, 4 * T);
+    } else if (lvl == 2) {
+        // 1×: 1×1 on x itself
+        err = conv1(plane_act(act_kind_for(sc.c1.kind), st->nx, st->nx_cap, E), T);
+    } else {
+        // 0.5×: 2×2 max pool, 1×1
+        const Act a_1 = plane_act(act_kind_for(sc.c1.kind), st->lv_a[3], st->lv_a_cap[3], E);
         if ((err = launch_pool_act(x, G, G, (int)E, 2, a_1, s)) != hipSuccess) return err;
-        if ((err = conv1(sc, a_1, (int64_t)g3 * g3, a_3)) != hipSuccess) return err;
-        if ((err = conv3(sc, a_3, g3, out[3])) != hipSuccess) return err;
+        err = conv1(a_1, (int64_t)side * side);
     }
-    return hipSuccess;
+    if (err != hipSuccess) return err;
+    // 3×3 + bias → the level's f32 output
+    EpiArgs e;
+    e.bias = sc.c3_b;
+    e.y = st->neck_out[which][lvl];
+    e.ldy = D;
+    ConvGeom g;
+    g.w = g.h = side;
+    g.spt = (int)(D / 32);
+    g.zero = st->zero;
+    return launch_conv(sc.c3, a_3, (int64_t)side * side, EPI_F32, e, &g, s);
 }
 
 // Both necks (detector first, as sam3.cpp:6072-6075 builds them) on x.
+// Level 0 runs on the context stream, level 1 on aux[0], levels 2 and 3 on
+// aux[1]; a level's buffers are its own, so the streams share nothing but
+// the read-only nx and x.
 hipError_t run_necks(s3e_state *st, const float *x) {
     const s3e_model *m = st->m;
     if (!m->necks_present) return hipSuccess;
+    hipStream_t s = st->ctx->stream;
     // fp16 planes of x: hi feeds the deconvolutions, hi + lo the scale-2 1×1
     bool split = false;
     for (const Neck &nk : m->necks)
         if (nk.found && nk.s[2].c1.kind == WK_F16X3) split = true;
     hipError_t e = launch_pool_act(x, m->grid, m->grid, m->E, 1,
-                                   plane_act(split ? A_F16X2 : A_F16, st->nx, st->nx_cap, m->E), st->ctx->stream);
-    for (int which = 0; which < 2 && e == hipSuccess; which++)
-        if (m->necks[which].found) e = run_neck(st, which, x);
+                                   plane_act(split ? A_F16X2 : A_F16, st->nx, st->nx_cap, m->E), s);
+    if (e == hipSuccess) e = hipEventRecord(st->ev_fork, s);
+    for (int i = 0; i < 2 && e == hipSuccess; i++) e = hipStreamWaitEvent(st->aux[i], st->ev_fork, 0);
+    for (int which = 0; which < 2 && e == hipSuccess; which++) {
+        if (!m->necks[which].found) continue;
+        e = run_level(st, which, 0, x, s);
+        if (e == hipSuccess) e = run_level(st, which, 1, x, st->aux[0]);
+        if (e == hipSuccess) e = run_level(st, which, 2, x, st->aux[1]);
+        if (e == hipSuccess) e = run_level(st, which, 3, x, st->aux[1]);
+    }
+    // join (also on error, so that the context stream never runs ahead of work
+    // already queued on the side streams)
+    for (int i = 0; i < 2; i++) {
+        const hipError_t r = hipEventRecord(st->ev_join[i], st->aux[i]);
+        const hipError_t w = r == hipSuccess ? hipStreamWaitEvent(s, st->ev_join[i], 0) : r;
+        if (e == hipSuccess) e = w;
+    }
     return e;
 }
 
