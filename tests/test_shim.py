@@ -1,0 +1,131 @@
+"""The sam3.h encoder API (include/sam3_encoder.h) on the engine.
+
+CPU part: every declared function is exported by libs3e.so with the C++
+signature of sam3.h, and the example program (sam3.cpp_amd/sam3_encode)
+fails the way sam3_load_model does (nullptr + a message) for a missing file
+and for a file that is not a SAM 3 model — both decided before any GPU call.
+
+GPU part: the example encodes a PPM image through sam3_encode_image and
+dumps state tensors in sam3_dump_state_tensor's format; the dumps must match
+the oracle's backbone + tracker neck on the same image (end-to-end bound as
+in tests/test_gpu_neck.py), and the preprocessed-input path
+(sam3_encode_image_from_preprocessed) must give bit-identical dumps.
+"""
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle_lib as orc
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+EXE = os.path.join(ROOT, "sam3.cpp_amd", "sam3_encode")
+LIB = os.path.join(ROOT, "sam3.cpp_amd", "libs3e.so")
+HEADER = os.path.join(ROOT, "include", "sam3_encoder.h")
+
+
+def declared():
+    src = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(sam3_\w+)\s*\(", src)) - {"operator"})
+
+
+def test_header_functions_are_exported():
+    out = subprocess.run(["nm", "-DC", "--defined-only", LIB], capture_output=True, text=True, check=True).stdout
+    names = declared()
+    assert len(names) == 10, names
+    for n in names:
+        assert re.search(rf"\b{n}\(", out), n
+    # the C++ signatures of sam3.h (demangled)
+    assert "sam3_load_model(sam3_params const&)" in out
+    assert "sam3_encode_image(sam3_state&, sam3_model const&, sam3_image const&)" in out
+    assert "sam3_dump_state_tensor(sam3_state const&, std::__cxx11::basic_string" in out
+    assert "sam3_state_deleter::operator()(sam3_state*) const" in out
+
+
+def test_example_fails_like_sam3_load_model(tmp_path):
+    r = subprocess.run([EXE, "-m", str(tmp_path / "missing.ggml"), "-i", "x.ppm", "-o", str(tmp_path)],
+                       capture_output=True, text=True)
+    assert r.returncode == 1 and "failed to open" in r.stderr
+    bad = tmp_path / "sam2.ggml"
+    bad.write_bytes(b"2mas" + b"\0" * 64)
+    r = subprocess.run([EXE, "-m", str(bad), "-i", "x.ppm", "-o", str(tmp_path)], capture_output=True, text=True)
+    assert r.returncode == 1 and "not a SAM 3 model file" in r.stderr
+    r = subprocess.run([EXE], capture_output=True, text=True)
+    assert r.returncode == 1 and "usage" in r.stderr
+
+
+@pytest.fixture(scope="module")
+def s3e_lib():
+    import s3e
+
+    return s3e
+
+
+def _write_ppm(path, img):
+    h, w, _ = img.shape
+    with open(path, "wb") as f:
+        f.write(f"P6\n# synthetic\n{w} {h}\n255\n".encode())
+        f.write(np.ascontiguousarray(img, np.uint8).tobytes())
+
+
+def _read_dump(prefix):
+    shape = [int(v) for v in open(prefix + ".shape").read().strip().split(",")]
+    data = np.fromfile(prefix + ".bin", dtype=np.float32)
+    assert data.size == int(np.prod(shape))
+    return shape, data
+
+
+@pytest.mark.gpu
+def test_example_encode_matches_oracle(tmp_path, s3e_lib):
+    import ctypes
+
+    path = str(tmp_path / "m.ggml")
+    s3e_lib.synth_write(path, img_size=336, patch=14, embed_dim=1024, depth=2, heads=16, window=8,
+                        global_idx=(1,), ftype="q8_0", seed=21, std=0.02, random_affine=True, neck=1)
+    rng = np.random.default_rng(9)
+    img = rng.integers(0, 256, (400, 300, 3), dtype=np.uint8)  # resized to 336² on the host
+    _write_ppm(str(tmp_path / "img.ppm"), img)
+    out = str(tmp_path / "a_")
+    print("sam3_encode on a 300x400 PPM", flush=True)
+    r = subprocess.run([EXE, "-m", path, "-i", str(tmp_path / "img.ppm"), "-o", out, "-r", "2"],
+                       capture_output=True, text=True, timeout=120)
+    print(r.stdout, r.stderr[-2000:], flush=True)
+    assert r.returncode == 0
+    assert "visual_only=1" in r.stdout
+    om = orc.OracleModel(path)
+    chw = orc.preprocess_sam3(img, 336)
+    orc.LIB.orc_set_variant.argtypes = [ctypes.c_int]
+    refs = []
+    for variant in (0, 1):
+        orc.LIB.orc_set_variant(variant)
+        try:
+            v = om.encode(chw)
+            refs.append([v] + om.neck(v, "trk"))
+        finally:
+            orc.LIB.orc_set_variant(0)
+    names = ["vit_output"] + [f"neck_trk_{i}" for i in range(4)]
+    shapes = [[1024, 24, 24]] + [[256, s, s] for s in (96, 48, 24, 12)]
+    for k, (name, shp) in enumerate(zip(names, shapes)):
+        shape, got = _read_dump(out + name)
+        assert shape == shp, name
+        ref = refs[0][k].ravel()
+        gap = orc.rel_l2(refs[1][k], refs[0][k])
+        gma = orc.max_abs(refs[1][k], refs[0][k])
+        rl, ma = orc.rel_l2(got, ref), orc.max_abs(got, ref)
+        print(f"{name}: rel_l2={rl:.3e} max_abs={ma:.3e} (ggml order gap {gap:.2e}/{gma:.2e})", flush=True)
+        assert rl <= max(1e-3, 3.0 * gap) and ma <= max(5e-3, 3.0 * gma), name
+
+    # preprocessed input of the same image: identical dumps
+    chw.astype(np.float32).tofile(str(tmp_path / "img.chw.f32"))
+    out2 = str(tmp_path / "b_")
+    r = subprocess.run([EXE, "-m", path, "-p", str(tmp_path / "img.chw.f32"), "-s", "336", "-o", out2],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr[-2000:]
+    for name in names:
+        assert np.array_equal(_read_dump(out + name)[1], _read_dump(out2 + name)[1]), name
+    # img_size mismatch is refused (sam3.cpp:7004-7008)
+    r = subprocess.run([EXE, "-m", path, "-p", str(tmp_path / "img.chw.f32"), "-s", "224", "-o", out2],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 1
