@@ -225,6 +225,24 @@ typedef struct s3e_synth_cfg {
 } s3e_synth_cfg;
 int s3e_synth_write(const char *path, const s3e_synth_cfg *cfg);
 
+/* Write a random-init SAM 2.x model file's image encoder (Hiera backbone +
+ * FPN neck) in sam3.cpp's SAM 2 format (magic "sam2", version 1; header and
+ * 57 hparams per convert_sam2_to_ggml.py:205-277, tensors per
+ * sam2_register_tensors, sam3.cpp:1745-1847), weights N(0, std²) as above,
+ * stored and quantized by the same rules.  Hiera-T: embed 96, heads 1,
+ * stages {1,2,7,2}, global {5,7,9}, windows {8,4,14,7}, bkg 7×7; Hiera-B+:
+ * 112, 2, {2,3,16,3}, {12,16,20}, {8,4,14,7}, 14×14 (convert_sam2_to_ggml.py:
+ * 79-106).  Replaces the SAM 2 converter for synthetic-weight runs. */
+typedef struct s3e_synth_sam2_cfg {
+    int32_t img_size, embed_dim, num_heads, stages[4];
+    int32_t global_n, global_idx[8], q_pool, window_spec[4], bkg_h, bkg_w, scalp;
+    int32_t neck_dim, fpn_td_n, fpn_td[4];
+    int32_t ftype;
+    uint64_t seed;
+    float std;  /* negative: also randomise biases and LayerNorm affine */
+} s3e_synth_sam2_cfg;
+int s3e_synth_write_sam2(const char *path, const s3e_synth_sam2_cfg *cfg);
+
 #ifdef __cplusplus
 }
 #endif

@@ -104,9 +104,19 @@ void orc_compute_axial_cis(float *out, int dim, int end_x, int end_y,
 
 /* sam3_preprocess_image (sam3.cpp:3441-3514): HWC uint8 → CHW f32. */
 void orc_preprocess_sam3(const uint8_t *img, int w, int h, int img_size, float *chw);
+/* sam3_resize_bilinear (sam3.cpp:3441-3484) alone: HWC uint8 → HWC uint8. */
+void orc_resize_bilinear_u8(const uint8_t *img, int w, int h, uint8_t *out, int ow, int oh);
+/* sam2_preprocess_image (sam3.cpp:3518-3544): resize + ImageNet mean/std. */
+void orc_preprocess_sam2(const uint8_t *img, int w, int h, int img_size, float *chw);
 
 /* ---- SAM 3 ViT encoder (sam3.cpp:3706-3849) ----------------------------- */
 typedef struct orc_model orc_model;
+/* Hiera / FPN hparams of a SAM 2 file (sam2_load_hparams, sam3.cpp:1564-1626) */
+typedef struct {
+    int32_t img_size, embed_dim, num_heads, num_stages, stages[4];
+    int32_t global_n, global_idx[8], q_pool, window_spec[4], bkg_h, bkg_w, scalp;
+    int32_t neck_dim, fpn_td_n, fpn_td[4];
+} orc_hiera_hp;
 orc_model *orc_model_load(const char *path);      /* NULL on failure */
 void       orc_model_free(orc_model *m);
 const char *orc_last_error(void);
@@ -120,6 +130,8 @@ typedef struct {
     const void *data;
 } orc_tensor_view;
 int  orc_model_tensor(const orc_model *m, const char *prefix, const char *suffix, orc_tensor_view *out);
+/* NULL unless the model is a SAM 2 (Hiera) file */
+const orc_hiera_hp *orc_model_hiera(const orc_model *m);
 void orc_set_error(const char *fmt, ...);
 /* Prefix (patch embed + tiled pos + ln_pre): chw [3][img][img] → x [T][E]. */
 int  orc_vit_prefix(const orc_model *m, const float *chw, float *x, int nthreads);
@@ -145,6 +157,29 @@ void orc_sinusoidal_pe_2d(int H, int W, int d_model, float *out);
 int  orc_neck_dims(const orc_model *m, const char *which, int64_t side[4], int64_t *D);
 /* The neck on vit_output x [G²][E]: out[i] receives side[i]² rows of D. */
 int  orc_neck(const orc_model *m, const char *which, const float *x, float *out[4], int nthreads);
+
+/* ---- SAM 2.x Hiera encoder + FPN (sam3.cpp:4066-4603), NHWC ------------- */
+/* ggml_gelu on f32 through ggml's fp16 table; the 65536-entry table itself */
+void orc_gelu_tanh(float *x, int64_t n);
+void orc_gelu_tanh_table(uint16_t *out);
+/* sam2_bicubic_interpolate_cpu: src [C][Hi][Wi] → dst [C][Ho][Wo] */
+void orc_bicubic(const float *src, int C, int Hi, int Wi, float *dst, int Ho, int Wo);
+int  orc_hiera_num_blocks(const orc_model *m);
+/* dim_in, dim_out, heads, window (0 global), q_stride, stage, stage end */
+int  orc_hiera_block_info(const orc_model *m, int i, int32_t out[7]);
+/* per stage: side and channel width */
+int  orc_hiera_dims(const orc_model *m, int side[4], int width[4]);
+/* sam2_compute_pos_embed: out [H][W][E] */
+int  orc_hiera_pos_embed(const orc_model *m, int H, int W, float *out);
+/* patch embed + bias + PE: chw [3][S][S] → x [S/4][S/4][E] */
+int  orc_hiera_prefix(const orc_model *m, const float *chw, float *x, int nthreads);
+/* one block: x [H][W][Cin] → y [Ho][Wo][Cout] */
+int  orc_hiera_block(const orc_model *m, int bi, const float *x, int H, int W, float *y, int *Ho, int *Wo,
+                     int nthreads);
+/* FPN over the four stage outputs; out[i] NULL skips a level */
+int  orc_hiera_fpn(const orc_model *m, float *const stage[4], const int side[4], float *out[4], int nthreads);
+/* whole encoder; stage_out may be NULL */
+int  orc_hiera_encode(const orc_model *m, const float *chw, float *out[4], float *stage_out[4], int nthreads);
 
 #ifdef __cplusplus
 }

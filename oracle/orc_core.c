@@ -818,35 +818,41 @@ void orc_compute_axial_cis(float *out, int dim, int end_x, int end_y, float thet
 }
 
 /* sam3_resize_bilinear + sam3_preprocess_image (sam3.cpp:3441-3514). */
+/* sam3_resize_bilinear (sam3.cpp:3441-3484): uint8 bilinear, half-pixel
+ * centres, double arithmetic, round half up. */
+void orc_resize_bilinear_u8(const uint8_t *img, int w, int h, uint8_t *out, int ow, int oh) {
+    const double sx = (double)w / ow, sy = (double)h / oh;
+    for (int y = 0; y < oh; ++y) {
+        double fy = (y + 0.5) * sy - 0.5;
+        if (fy < 0.0) fy = 0.0;
+        const int y0 = (int)fy;
+        const int y1 = (y0 < h - 1) ? y0 + 1 : y0;
+        const double wy = fy - y0, wy0 = 1.0 - wy;
+        for (int x = 0; x < ow; ++x) {
+            double fx = (x + 0.5) * sx - 0.5;
+            if (fx < 0.0) fx = 0.0;
+            const int x0 = (int)fx;
+            const int x1 = (x0 < w - 1) ? x0 + 1 : x0;
+            const double wx = fx - x0, wx0 = 1.0 - wx;
+            for (int c = 0; c < 3; ++c) {
+                const double p00 = img[(y0 * w + x0) * 3 + c], p01 = img[(y0 * w + x1) * 3 + c];
+                const double p10 = img[(y1 * w + x0) * 3 + c], p11 = img[(y1 * w + x1) * 3 + c];
+                const double vv = wy0 * (wx0 * p00 + wx * p01) + wy * (wx0 * p10 + wx * p11);
+                int iv = (int)(vv + 0.5);
+                if (iv < 0) iv = 0;
+                if (iv > 255) iv = 255;
+                out[((size_t)y * ow + x) * 3 + c] = (uint8_t)iv;
+            }
+        }
+    }
+}
+
 void orc_preprocess_sam3(const uint8_t *img, int w, int h, int img_size, float *chw) {
     uint8_t *resized = NULL;
     const uint8_t *px = img;
     if (w != img_size || h != img_size) {
         resized = (uint8_t *)malloc((size_t)img_size * img_size * 3);
-        const double sx = (double)w / img_size, sy = (double)h / img_size;
-        for (int y = 0; y < img_size; ++y) {
-            double fy = (y + 0.5) * sy - 0.5;
-            if (fy < 0.0) fy = 0.0;
-            const int y0 = (int)fy;
-            const int y1 = (y0 < h - 1) ? y0 + 1 : y0;
-            const double wy = fy - y0, wy0 = 1.0 - wy;
-            for (int x = 0; x < img_size; ++x) {
-                double fx = (x + 0.5) * sx - 0.5;
-                if (fx < 0.0) fx = 0.0;
-                const int x0 = (int)fx;
-                const int x1 = (x0 < w - 1) ? x0 + 1 : x0;
-                const double wx = fx - x0, wx0 = 1.0 - wx;
-                for (int c = 0; c < 3; ++c) {
-                    const double p00 = img[(y0 * w + x0) * 3 + c], p01 = img[(y0 * w + x1) * 3 + c];
-                    const double p10 = img[(y1 * w + x0) * 3 + c], p11 = img[(y1 * w + x1) * 3 + c];
-                    const double vv = wy0 * (wx0 * p00 + wx * p01) + wy * (wx0 * p10 + wx * p11);
-                    int iv = (int)(vv + 0.5);
-                    if (iv < 0) iv = 0;
-                    if (iv > 255) iv = 255;
-                    resized[(y * img_size + x) * 3 + c] = (uint8_t)iv;
-                }
-            }
-        }
+        orc_resize_bilinear_u8(img, w, h, resized, img_size, img_size);
         px = resized;
     }
     const size_t plane = (size_t)img_size * img_size;

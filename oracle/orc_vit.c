@@ -49,6 +49,8 @@ typedef struct {
 
 struct orc_model {
     orc_hp hp;
+    int is_sam2;
+    orc_hiera_hp h2;  /* SAM 2 files (sam2_load_hparams, sam3.cpp:1564-1626) */
     int ftype, wtype;
     int n_tensors;
     orc_tensor *t;
@@ -110,11 +112,37 @@ orc_model *orc_model_load(const char *path) {
 #define RD32(dst) do { if (off + 4 > fsize) ORC_FAIL("truncated file"); memcpy(&(dst), map + off, 4); off += 4; } while (0)
     uint32_t magic; int32_t version, ftype, n_tensors;
     RD32(magic); RD32(version); RD32(ftype); RD32(n_tensors);
-    if (magic != 0x73616D33u) ORC_FAIL("bad magic 0x%08x (expected sam3)", magic);
-    if (version != 3) ORC_FAIL("unsupported version %d", version);
+    if (magic == 0x73616D32u) { /* "sam2" */
+        if (version != 1) ORC_FAIL("unsupported SAM2 version %d", version);
+        m->is_sam2 = 1;
+    } else {
+        if (magic != 0x73616D33u) ORC_FAIL("bad magic 0x%08x (expected sam3 or sam2)", magic);
+        if (version != 3) ORC_FAIL("unsupported version %d", version);
+    }
     m->ftype = ftype;
     m->wtype = ftype_to_wtype(ftype);
     if (m->wtype < 0) ORC_FAIL("unsupported ftype %d", ftype);
+    if (m->is_sam2) {
+        /* 57 int32 fields in sam2_load_hparams order; the encoder keeps the
+         * Hiera and FPN ones */
+        int32_t v[57];
+        for (int i = 0; i < 57; i++) RD32(v[i]);
+        orc_hiera_hp *h = &m->h2;
+        h->img_size = v[0];
+        if (v[1] != 1) ORC_FAIL("backbone type %d is not Hiera", v[1]);
+        h->embed_dim = v[2]; h->num_heads = v[3]; h->num_stages = v[4];
+        for (int i = 0; i < 4; i++) h->stages[i] = v[5 + i];
+        h->global_n = v[9];
+        for (int i = 0; i < 8; i++) h->global_idx[i] = v[10 + i];
+        h->q_pool = v[18];
+        for (int i = 0; i < 4; i++) h->window_spec[i] = v[19 + i];
+        h->bkg_h = v[23]; h->bkg_w = v[24]; h->scalp = v[25];
+        h->neck_dim = v[26]; h->fpn_td_n = v[27];
+        for (int i = 0; i < 4; i++) h->fpn_td[i] = v[28 + i];
+        if (h->num_stages != 4 || h->global_n > 8 || h->embed_dim <= 0 || h->img_size % 4 != 0)
+            ORC_FAIL("inconsistent Hiera hparams");
+        goto tensors;
+    }
     /* SAM3 hparams: 39 int32 fields in the order of sam3_load_hparams. */
     int32_t hpv[39];
     {
@@ -132,6 +160,7 @@ orc_model *orc_model_load(const char *path) {
         m->hp.neck_dim = hpv[6];
         m->hp.visual_only = hpv[26];
     }
+tensors:
     m->t = (orc_tensor *)calloc((size_t)(n_tensors > 0 ? n_tensors : 1), sizeof(orc_tensor));
     for (int ti = 0; ti < n_tensors; ti++) {
         int32_t n_dims, name_len, dtype;
@@ -151,8 +180,10 @@ orc_model *orc_model_load(const char *path) {
         if (off + bytes > fsize) ORC_FAIL("tensor %s: truncated data", t->name);
         const uint8_t *src = map + off;
         off += bytes;
-        /* encoder backbone and necks only */
-        if (strncmp(t->name, "vit.", 4) != 0 && strncmp(t->name, "neck.", 5) != 0) continue;
+        /* encoder backbones and necks only */
+        if (strncmp(t->name, "vit.", 4) != 0 && strncmp(t->name, "neck.", 5) != 0 &&
+            strncmp(t->name, "hiera.", 6) != 0 && strncmp(t->name, "fpn.", 4) != 0)
+            continue;
         const int rt = registered_type(t->name, n_dims, t->ne[0], m->wtype);
         t->type = rt;
         const size_t out_bytes = orc_row_size(rt, t->ne[0]) * (size_t)(n_el / t->ne[0]);
@@ -201,6 +232,8 @@ void orc_model_hparams(const orc_model *m, int32_t out[16]) {
     out[14] = m->hp.visual_only;
     out[15] = (find(m, "neck.trk.0.conv_3x3.weight") ? 1 : 0) | (find(m, "neck.det.0.conv_3x3.weight") ? 2 : 0);
 }
+
+const orc_hiera_hp *orc_model_hiera(const orc_model *m) { return m->is_sam2 ? &m->h2 : NULL; }
 
 int orc_model_tensor(const orc_model *m, const char *prefix, const char *suffix, orc_tensor_view *out) {
     char buf[96];

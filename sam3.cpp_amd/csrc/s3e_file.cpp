@@ -179,6 +179,110 @@ void fill_normal(float *x, int64_t n, uint64_t seed, float stdv) {
 
 }  // namespace s3e
 
+namespace s3e {
+namespace {
+
+// Generate every tensor of ts (in parallel: each has its own seed) and write
+// the file: header, hparams, records.  Stored dtypes follow the converters
+// and the quantize tool: 1-D, pos_embed and freqs tensors F32; in F16 files
+// every other 2-D+ tensor F16 unless its name contains "embed"
+// (convert_sam3_to_ggml.py:220-232, convert_sam2_to_ggml.py:281-293); in
+// quantized files 2-D+ tensors whose ne0 is a multiple of 32 are quantized
+// (examples/quantize.cpp:195-223).
+int write_model(const char *path, uint32_t magic, int32_t version, int ftype, int wtype,
+                const std::vector<int32_t> &hp, const std::vector<SynthTensor> &ts, uint64_t seed, float sd,
+                bool rnd_affine, int freq_dim) {
+    std::vector<std::vector<uint8_t>> data(ts.size());
+    std::vector<int> dtypes(ts.size());
+    auto work = [&](size_t idx) {
+        const SynthTensor &t = ts[idx];
+        int64_t n = 1;
+        for (auto d : t.ne) n *= d;
+        std::vector<float> v((size_t)n);
+        const uint64_t sseed = seed * 0x9E3779B97F4A7C15ull + (uint64_t)idx * 0xBF58476D1CE4E5B9ull + 1;
+        if (t.kind == 0) {
+            fill_normal(v.data(), n, sseed, sd);
+        } else if (t.kind == 1) {
+            if (rnd_affine) { fill_normal(v.data(), n, sseed, sd); for (auto &x : v) x += 1.0f; }
+            else std::fill(v.begin(), v.end(), 1.0f);
+        } else if (t.kind == 2) {
+            if (rnd_affine) fill_normal(v.data(), n, sseed, sd);
+            else std::fill(v.begin(), v.end(), 0.0f);
+        } else {
+            axial_cis(v.data(), freq_dim, t.freq_side, t.freq_side, 10000.0f, t.freq_scale);
+        }
+        int dt = 0;
+        if (t.ne.size() >= 2 && !t.pos) {
+            if (wtype == 1) dt = (t.name.find("embed") == std::string::npos) ? 1 : 0;
+            else if (wtype >= 2 && t.ne[0] % 32 == 0) dt = wtype;
+        }
+        dtypes[idx] = dt;
+        const int64_t rows = n / t.ne[0];
+        std::vector<uint8_t> &out = data[idx];
+        out.resize(ggml_rowsize(dt, t.ne[0]) * (size_t)rows);
+        if (dt == 0) {
+            std::memcpy(out.data(), v.data(), out.size());
+        } else if (dt == 1) {
+            for (int64_t i = 0; i < n; i++) {
+                const uint16_t h = host_f2h(v[(size_t)i]);
+                std::memcpy(out.data() + 2 * i, &h, 2);
+            }
+        } else {
+            const size_t rs = ggml_rowsize(dt, t.ne[0]);
+            for (int64_t r = 0; r < rows; r++) {
+                const float *src = v.data() + r * t.ne[0];
+                uint8_t *dst = out.data() + (size_t)r * rs;
+                if (dt == 2) quantize_q4_0(src, dst, t.ne[0]);
+                else if (dt == 3) quantize_q4_1(src, dst, t.ne[0]);
+                else quantize_q8_0(src, dst, t.ne[0]);
+            }
+        }
+    };
+    {
+        const unsigned nth = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+        std::vector<std::thread> pool;
+        std::atomic_size_t next{0};
+        for (unsigned i = 0; i < nth; i++) {
+            pool.emplace_back([&]() {
+                for (size_t idx = next++; idx < ts.size(); idx = next++) work(idx);
+            });
+        }
+        for (auto &th : pool) th.join();
+    }
+
+    FILE *f = std::fopen(path, "wb");
+    if (!f) { set_error("s3e_synth_write: cannot open %s", path); return S3E_ERR_IO; }
+    auto w32 = [&](int32_t v) { std::fwrite(&v, 4, 1, f); };
+    std::fwrite(&magic, 4, 1, f);
+    w32(version);
+    w32(ftype);
+    w32((int32_t)ts.size());
+    for (int32_t v : hp) w32(v);
+    long pos = 16 + 4 * (long)hp.size();
+    for (size_t i = 0; i < ts.size(); i++) {
+        const SynthTensor &t = ts[i];
+        w32((int32_t)t.ne.size());
+        w32((int32_t)t.name.size());
+        w32(dtypes[i]);
+        for (auto d : t.ne) w32((int32_t)d);
+        std::fwrite(t.name.data(), 1, t.name.size(), f);
+        pos += 12 + 4 * (long)t.ne.size() + (long)t.name.size();
+        const long pad = (32 - pos % 32) % 32;
+        static const char zeros[32] = {0};
+        std::fwrite(zeros, 1, (size_t)pad, f);
+        pos += pad;
+        std::fwrite(data[i].data(), 1, data[i].size(), f);
+        pos += (long)data[i].size();
+    }
+    const bool ok = std::ferror(f) == 0;
+    std::fclose(f);
+    if (!ok) { set_error("s3e_synth_write: write error on %s", path); return S3E_ERR_IO; }
+    return S3E_OK;
+}
+
+}  // namespace
+}  // namespace s3e
+
 using namespace s3e;
 
 extern "C" int s3e_synth_write(const char *path, const s3e_synth_cfg *cfg) {
@@ -266,105 +370,98 @@ extern "C" int s3e_synth_write(const char *path, const s3e_synth_cfg *cfg) {
     if (cfg->neck == 2) add_neck("neck.det.");
     if (cfg->neck >= 1) add_neck("neck.trk.");
 
-    // Generate and encode every tensor (in parallel: each has its own seed).
-    std::vector<std::vector<uint8_t>> data(ts.size());
-    std::vector<int> dtypes(ts.size());
-    auto work = [&](size_t idx) {
-        const SynthTensor &t = ts[idx];
-        int64_t n = 1;
-        for (auto d : t.ne) n *= d;
-        std::vector<float> v((size_t)n);
-        const uint64_t seed = cfg->seed * 0x9E3779B97F4A7C15ull + (uint64_t)idx * 0xBF58476D1CE4E5B9ull + 1;
-        if (t.kind == 0) {
-            fill_normal(v.data(), n, seed, sd);
-        } else if (t.kind == 1) {
-            if (rnd_affine) { fill_normal(v.data(), n, seed, sd); for (auto &x : v) x += 1.0f; }
-            else std::fill(v.begin(), v.end(), 1.0f);
-        } else if (t.kind == 2) {
-            if (rnd_affine) fill_normal(v.data(), n, seed, sd);
-            else std::fill(v.begin(), v.end(), 0.0f);
-        } else {
-            axial_cis(v.data(), HD, t.freq_side, t.freq_side, 10000.0f, t.freq_scale);
-        }
-        // Stored dtype: 1-D, pos/freqs → F32; 2-D+ weights: the quantize tool's
-        // rule (ne0 % 32 == 0) for Q types, F16 for F16 files, F32 otherwise.
-        int dt = 0;
-        if (t.ne.size() >= 2 && !t.pos) {
-            if (wtype == 1) dt = 1;
-            else if (wtype >= 2 && t.ne[0] % 32 == 0) dt = wtype;
-        }
-        dtypes[idx] = dt;
-        const int64_t rows = n / t.ne[0];
-        std::vector<uint8_t> &out = data[idx];
-        out.resize(ggml_rowsize(dt, t.ne[0]) * (size_t)rows);
-        if (dt == 0) {
-            std::memcpy(out.data(), v.data(), out.size());
-        } else if (dt == 1) {
-            for (int64_t i = 0; i < n; i++) {
-                const uint16_t h = host_f2h(v[(size_t)i]);
-                std::memcpy(out.data() + 2 * i, &h, 2);
-            }
-        } else {
-            const size_t rs = ggml_rowsize(dt, t.ne[0]);
-            for (int64_t r = 0; r < rows; r++) {
-                const float *src = v.data() + r * t.ne[0];
-                uint8_t *dst = out.data() + (size_t)r * rs;
-                if (dt == 2) quantize_q4_0(src, dst, t.ne[0]);
-                else if (dt == 3) quantize_q4_1(src, dst, t.ne[0]);
-                else quantize_q8_0(src, dst, t.ne[0]);
-            }
-        }
-    };
-    {
-        const unsigned nth = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
-        std::vector<std::thread> pool;
-        std::atomic_size_t next{0};
-        for (unsigned i = 0; i < nth; i++) {
-            pool.emplace_back([&]() {
-                for (size_t idx = next++; idx < ts.size(); idx = next++) work(idx);
-            });
-        }
-        for (auto &th : pool) th.join();
-    }
-
-    FILE *f = std::fopen(path, "wb");
-    if (!f) { set_error("s3e_synth_write: cannot open %s", path); return S3E_ERR_IO; }
-    auto w32 = [&](int32_t v) { std::fwrite(&v, 4, 1, f); };
-    const uint32_t magic = 0x73616D33u;
-    std::fwrite(&magic, 4, 1, f);
-    w32(3);
-    w32(ftype);
-    w32((int32_t)ts.size());
     // hparams in sam3_load_hparams order (sam3.cpp:1477-1520)
-    const int32_t hp[39] = {img, P, E, cfg->depth, cfg->heads, cfg->mlp_ratio_x1000, WS, 4,
-                            cfg->n_global > 0 ? cfg->global_idx[0] : -1,
-                            cfg->n_global > 1 ? cfg->global_idx[1] : -1,
-                            cfg->n_global > 2 ? cfg->global_idx[2] : -1,
-                            cfg->n_global > 3 ? cfg->global_idx[3] : -1,
-                            1024, 16, 24, 32, 49408, 256,  // text
-                            D,                             // neck_dim
-                            6, 8, 2048, 6, 8, 2048, 200, 3, 1, 4,
-                            256, 2, 3, 3, 64, 4, 7, 16, 2,
-                            cfg->neck == 2 ? 0 : 1};       // visual_only
-    for (int i = 0; i < 39; i++) w32(hp[i]);
-    long pos = 16 + 39 * 4;
-    for (size_t i = 0; i < ts.size(); i++) {
-        const SynthTensor &t = ts[i];
-        w32((int32_t)t.ne.size());
-        w32((int32_t)t.name.size());
-        w32(dtypes[i]);
-        for (auto d : t.ne) w32((int32_t)d);
-        std::fwrite(t.name.data(), 1, t.name.size(), f);
-        pos += 12 + 4 * (long)t.ne.size() + (long)t.name.size();
-        const long pad = (32 - pos % 32) % 32;
-        static const char zeros[32] = {0};
-        std::fwrite(zeros, 1, (size_t)pad, f);
-        pos += pad;
-        std::fwrite(data[i].data(), 1, data[i].size(), f);
-        pos += (long)data[i].size();
+    const std::vector<int32_t> hp = {img, P, E, cfg->depth, cfg->heads, cfg->mlp_ratio_x1000, WS, 4,
+                                     cfg->n_global > 0 ? cfg->global_idx[0] : -1,
+                                     cfg->n_global > 1 ? cfg->global_idx[1] : -1,
+                                     cfg->n_global > 2 ? cfg->global_idx[2] : -1,
+                                     cfg->n_global > 3 ? cfg->global_idx[3] : -1,
+                                     1024, 16, 24, 32, 49408, 256,  // text
+                                     D,                             // neck_dim
+                                     6, 8, 2048, 6, 8, 2048, 200, 3, 1, 4,
+                                     256, 2, 3, 3, 64, 4, 7, 16, 2,
+                                     cfg->neck == 2 ? 0 : 1};       // visual_only
+    return write_model(path, 0x73616D33u, 3, ftype, wtype, hp, ts, cfg->seed, sd, rnd_affine, HD);
+}
+
+// SAM 2.x (Hiera) encoder file: convert_sam2_to_ggml.py:205-277 header (magic
+// "sam2", version 1, 57 hparams), the Hiera and FPN tensors of
+// sam2_register_tensors (sam3.cpp:1745-1847), block dimensions from
+// sam2_precompute_hiera_metadata (sam3.cpp:1676-1742).
+extern "C" int s3e_synth_write_sam2(const char *path, const s3e_synth_sam2_cfg *cfg) {
+    if (!path || !cfg) { set_error("s3e_synth_write_sam2: null argument"); return S3E_ERR_INVALID; }
+    const int ftype = cfg->ftype;
+    if (ftype != 0 && ftype != 1 && ftype != 2 && ftype != 3 && ftype != 8) {
+        set_error("s3e_synth_write_sam2: unsupported ftype %d", ftype);
+        return S3E_ERR_UNSUPPORTED;
     }
-    const bool ok = std::ferror(f) == 0;
-    std::fclose(f);
-    if (!ok) { set_error("s3e_synth_write: write error on %s", path); return S3E_ERR_IO; }
-    return S3E_OK;
+    const int E0 = cfg->embed_dim, S = cfg->img_size, D = cfg->neck_dim > 0 ? cfg->neck_dim : 256;
+    int total = 0;
+    for (int i = 0; i < 4; i++) total += cfg->stages[i];
+    if (E0 <= 0 || cfg->num_heads <= 0 || S <= 0 || S % 4 != 0 || total <= 0 || cfg->global_n < 0 ||
+        cfg->global_n > 8 || cfg->q_pool < 0 || cfg->q_pool > 3 || cfg->bkg_h <= 0 || cfg->bkg_w <= 0 ||
+        cfg->window_spec[0] <= 0 || cfg->fpn_td_n < 0 || cfg->fpn_td_n > 4 || cfg->scalp < 0 || cfg->scalp > 3) {
+        set_error("s3e_synth_write_sam2: inconsistent hparams");
+        return S3E_ERR_INVALID;
+    }
+    for (int i = 0; i < 4; i++)
+        if (cfg->stages[i] <= 0) { set_error("s3e_synth_write_sam2: every stage needs a block"); return S3E_ERR_INVALID; }
+    const bool rnd_affine = cfg->std < 0;
+    const float sd = std::fabs(cfg->std);
+    std::vector<SynthTensor> ts;
+    ts.push_back({"hiera.patch_embed.weight", {7, 7, 3, E0}, 0, false, false});
+    ts.push_back({"hiera.patch_embed.bias", {E0}, 2, false, false});
+    ts.push_back({"hiera.pos_embed", {cfg->bkg_w, cfg->bkg_h, E0, 1}, 0, false, true});
+    ts.push_back({"hiera.pos_embed_window", {cfg->window_spec[0], cfg->window_spec[0], E0, 1}, 0, false, true});
+    int stage_end[4], cum = 0;
+    for (int i = 0; i < 4; i++) { cum += cfg->stages[i]; stage_end[i] = cum - 1; }
+    int dim = E0, cur = 0;
+    for (int b = 0; b < total; b++) {
+        int dout = dim;
+        if (b > 0 && b - 1 == stage_end[cur]) { dout = dim * 2; cur++; }
+        const std::string p = "hiera.blocks." + std::to_string(b);
+        ts.push_back({p + ".norm1.weight", {dim}, 1, false, false});
+        ts.push_back({p + ".norm1.bias", {dim}, 2, false, false});
+        ts.push_back({p + ".attn.qkv.weight", {dim, 3 * dout}, 0, true, false});
+        ts.push_back({p + ".attn.qkv.bias", {3 * dout}, 2, false, false});
+        ts.push_back({p + ".attn.proj.weight", {dout, dout}, 0, true, false});
+        ts.push_back({p + ".attn.proj.bias", {dout}, 2, false, false});
+        ts.push_back({p + ".norm2.weight", {dout}, 1, false, false});
+        ts.push_back({p + ".norm2.bias", {dout}, 2, false, false});
+        ts.push_back({p + ".mlp.fc1.weight", {dout, 4 * dout}, 0, true, false});
+        ts.push_back({p + ".mlp.fc1.bias", {4 * dout}, 2, false, false});
+        ts.push_back({p + ".mlp.fc2.weight", {4 * dout, dout}, 0, true, false});
+        ts.push_back({p + ".mlp.fc2.bias", {dout}, 2, false, false});
+        if (dout != dim) {
+            ts.push_back({p + ".proj.weight", {dim, dout}, 0, true, false});
+            ts.push_back({p + ".proj.bias", {dout}, 2, false, false});
+        }
+        dim = dout;
+    }
+    for (int i = 0; i < 4; i++) {
+        const int stage = 3 - i;  // convs[0] maps the widest stage
+        const int ch = E0 << stage;
+        const std::string p = "fpn.convs." + std::to_string(i);
+        ts.push_back({p + ".weight", {1, 1, ch, D}, 0, false, false});
+        ts.push_back({p + ".bias", {D}, 2, false, false});
+    }
+    std::vector<int32_t> hp = {S, 1, E0, cfg->num_heads, 4};
+    for (int i = 0; i < 4; i++) hp.push_back(cfg->stages[i]);
+    hp.push_back(cfg->global_n);
+    for (int i = 0; i < 8; i++) hp.push_back(i < cfg->global_n ? cfg->global_idx[i] : 0);
+    hp.push_back(cfg->q_pool);
+    for (int i = 0; i < 4; i++) hp.push_back(cfg->window_spec[i]);
+    hp.push_back(cfg->bkg_h);
+    hp.push_back(cfg->bkg_w);
+    hp.push_back(cfg->scalp);
+    hp.push_back(D);
+    hp.push_back(cfg->fpn_td_n);
+    for (int i = 0; i < 4; i++) hp.push_back(i < cfg->fpn_td_n ? cfg->fpn_td[i] : 0);
+    // SAM decoder, memory, sigmoid scale/bias and flags: SAM 2.1 defaults
+    // (convert_sam2_to_ggml.py:44-75)
+    for (int32_t v : {256, 2, 3, 3, 64, 4, 7, 16, 2000, -1000, 1, 1, 1, 1, 1, 1, 0, 1, 0, 1, 1, 1, 1, 1, 1})
+        hp.push_back(v);
+    if (hp.size() != 57) { set_error("s3e_synth_write_sam2: internal hparams count"); return S3E_ERR_INVALID; }
+    const int wtype = ftype;  // ggml type ids equal the ftype codes used here
+    return write_model(path, 0x73616D32u, 1, ftype, wtype, hp, ts, cfg->seed, sd, rnd_affine, 0);
 }

@@ -36,6 +36,29 @@ class SynthCfg(ctypes.Structure):
     ]
 
 
+class SynthSam2Cfg(ctypes.Structure):
+    _fields_ = [
+        ("img_size", c_int32), ("embed_dim", c_int32), ("num_heads", c_int32), ("stages", c_int32 * 4),
+        ("global_n", c_int32), ("global_idx", c_int32 * 8), ("q_pool", c_int32), ("window_spec", c_int32 * 4),
+        ("bkg_h", c_int32), ("bkg_w", c_int32), ("scalp", c_int32),
+        ("neck_dim", c_int32), ("fpn_td_n", c_int32), ("fpn_td", c_int32 * 4),
+        ("ftype", c_int32), ("seed", c_uint64), ("std", c_float),
+    ]
+
+
+# Hiera variants of convert_sam2_to_ggml.py:79-106
+HIERA_VARIANTS = {
+    "hiera_t": dict(embed_dim=96, num_heads=1, stages=(1, 2, 7, 2), global_idx=(5, 7, 9),
+                    window_spec=(8, 4, 14, 7), bkg=(7, 7)),
+    "hiera_s": dict(embed_dim=96, num_heads=1, stages=(1, 2, 11, 2), global_idx=(7, 10, 13),
+                    window_spec=(8, 4, 14, 7), bkg=(7, 7)),
+    "hiera_b+": dict(embed_dim=112, num_heads=2, stages=(2, 3, 16, 3), global_idx=(12, 16, 20),
+                     window_spec=(8, 4, 14, 7), bkg=(14, 14)),
+    "hiera_l": dict(embed_dim=144, num_heads=2, stages=(2, 6, 36, 4), global_idx=(23, 33, 43),
+                    window_spec=(8, 4, 16, 8), bkg=(7, 7)),
+}
+
+
 def _load() -> ctypes.CDLL:
     if not os.path.exists(LIB_PATH):
         raise ImportError(f"{LIB_PATH} is not built; run __graft_entry__.build() first")
@@ -77,6 +100,7 @@ def _load() -> ctypes.CDLL:
         "s3e_state_tensor_get": (c_int, [c_void_p, c_char_p, c_void_p, c_size_t]),
         "s3e_state_tensor_device": (c_void_p, [c_void_p, c_char_p]),
         "s3e_synth_write": (c_int, [c_char_p, POINTER(SynthCfg)]),
+        "s3e_synth_write_sam2": (c_int, [c_char_p, POINTER(SynthSam2Cfg)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -93,7 +117,7 @@ DECLARED = [
     "s3e_flash_attn_ext", "s3e_model_load",
     "s3e_model_free", "s3e_model_hparams", "s3e_state_create", "s3e_state_free", "s3e_encode_chw",
     "s3e_encode_chw_host", "s3e_encode_image_u8", "s3e_vit_prefix", "s3e_vit_block", "s3e_run_neck", "s3e_state_tensor_info",
-    "s3e_state_tensor_get", "s3e_state_tensor_device", "s3e_synth_write",
+    "s3e_state_tensor_get", "s3e_state_tensor_device", "s3e_synth_write", "s3e_synth_write_sam2",
 ]
 
 
@@ -121,6 +145,34 @@ def synth_write(path: str, *, img_size=1008, patch=14, embed_dim=1024, depth=32,
     cfg.std = -abs(std) if random_affine else abs(std)
     cfg.neck, cfg.neck_dim = int(neck), int(neck_dim)
     check(LIB.s3e_synth_write(path.encode(), ctypes.byref(cfg)), "s3e_synth_write")
+
+
+def synth_write_sam2(path: str, variant: str = "hiera_t", *, img_size=1024, ftype="f16", seed=0, std=0.02,
+                     random_affine=False, neck_dim=256, q_pool=3, scalp=1, fpn_td=(2, 3), **over) -> None:
+    """Write a random-init SAM 2.x encoder file (s3e_synth_write_sam2); keyword
+    overrides replace the variant's hparams (embed_dim, num_heads, stages,
+    global_idx, window_spec, bkg)."""
+    v = dict(HIERA_VARIANTS[variant])
+    v.update(over)
+    cfg = SynthSam2Cfg()
+    cfg.img_size, cfg.embed_dim, cfg.num_heads = img_size, v["embed_dim"], v["num_heads"]
+    for i in range(4):
+        cfg.stages[i] = v["stages"][i]
+        cfg.window_spec[i] = v["window_spec"][i]
+    g = list(v["global_idx"])
+    cfg.global_n = len(g)
+    for i in range(8):
+        cfg.global_idx[i] = g[i] if i < len(g) else 0
+    cfg.q_pool = q_pool
+    cfg.bkg_h, cfg.bkg_w = v["bkg"]
+    cfg.scalp, cfg.neck_dim = scalp, neck_dim
+    cfg.fpn_td_n = len(fpn_td)
+    for i in range(4):
+        cfg.fpn_td[i] = fpn_td[i] if i < len(fpn_td) else 0
+    cfg.ftype = FTYPE_BY_NAME[ftype] if isinstance(ftype, str) else int(ftype)
+    cfg.seed = seed
+    cfg.std = -abs(std) if random_affine else abs(std)
+    check(LIB.s3e_synth_write_sam2(path.encode(), ctypes.byref(cfg)), "s3e_synth_write_sam2")
 
 
 def act_scale_elems(M: int, K: int) -> int:

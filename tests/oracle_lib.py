@@ -71,6 +71,20 @@ def _load():
         "orc_sinusoidal_pe_2d": (None, [c_int, c_int, c_int, P]),
         "orc_neck_dims": (c_int, [P, c_char_p, P, P]),
         "orc_neck": (c_int, [P, c_char_p, P, P, c_int]),
+        "orc_resize_bilinear_u8": (None, [P, c_int, c_int, P, c_int, c_int]),
+        "orc_preprocess_sam2": (None, [P, c_int, c_int, c_int, P]),
+        "orc_gelu_tanh": (None, [P, c_int64]),
+        "orc_gelu_tanh_table": (None, [P]),
+        "orc_bicubic": (None, [P, c_int, c_int, c_int, P, c_int, c_int]),
+        "orc_model_hiera": (P, [P]),
+        "orc_hiera_num_blocks": (c_int, [P]),
+        "orc_hiera_block_info": (c_int, [P, c_int, P]),
+        "orc_hiera_dims": (c_int, [P, P, P]),
+        "orc_hiera_pos_embed": (c_int, [P, c_int, c_int, P]),
+        "orc_hiera_prefix": (c_int, [P, P, P, c_int]),
+        "orc_hiera_block": (c_int, [P, c_int, P, c_int, c_int, P, P, P, c_int]),
+        "orc_hiera_fpn": (c_int, [P, P, P, P, c_int]),
+        "orc_hiera_encode": (c_int, [P, P, P, P, c_int]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -226,6 +240,102 @@ class OracleModel:
             self.h = None
 
 
+class HieraHp(ctypes.Structure):
+    _fields_ = [
+        ("img_size", c_int32), ("embed_dim", c_int32), ("num_heads", c_int32), ("num_stages", c_int32),
+        ("stages", c_int32 * 4), ("global_n", c_int32), ("global_idx", c_int32 * 8), ("q_pool", c_int32),
+        ("window_spec", c_int32 * 4), ("bkg_h", c_int32), ("bkg_w", c_int32), ("scalp", c_int32),
+        ("neck_dim", c_int32), ("fpn_td_n", c_int32), ("fpn_td", c_int32 * 4),
+    ]
+
+
+class OracleHiera:
+    """The oracle's SAM 2.x encoder (oracle/orc_hiera.c) on a model file."""
+
+    def __init__(self, path: str):
+        self.h = LIB.orc_model_load(path.encode())
+        if not self.h:
+            raise RuntimeError("oracle model load failed: " + LIB.orc_last_error().decode())
+        hp = LIB.orc_model_hiera(self.h)
+        assert hp, "not a SAM 2 model"
+        self.hp = HieraHp.from_address(hp)
+        self.img = self.hp.img_size
+        self.nblocks = LIB.orc_hiera_num_blocks(self.h)
+        side, width = np.zeros(4, np.int32), np.zeros(4, np.int32)
+        LIB.orc_hiera_dims(self.h, ptr(side), ptr(width))
+        self.side, self.width = [int(v) for v in side], [int(v) for v in width]
+
+    def block_info(self, i: int):
+        out = np.zeros(7, np.int32)
+        assert LIB.orc_hiera_block_info(self.h, i, ptr(out)) == 0, LIB.orc_last_error()
+        return dict(zip(("dim_in", "dim_out", "heads", "window", "q_stride", "stage", "stage_end"),
+                        (int(v) for v in out)))
+
+    def pos_embed(self, H: int, W: int) -> np.ndarray:
+        out = np.empty((H, W, self.hp.embed_dim), np.float32)
+        assert LIB.orc_hiera_pos_embed(self.h, H, W, ptr(out)) == 0, LIB.orc_last_error()
+        return out
+
+    def prefix(self, chw: np.ndarray, nthreads: int = 0) -> np.ndarray:
+        G = self.img // 4
+        x = np.empty((G * G, self.hp.embed_dim), np.float32)
+        chw = np.ascontiguousarray(chw, np.float32)
+        assert LIB.orc_hiera_prefix(self.h, ptr(chw), ptr(x), nthreads) == 0, LIB.orc_last_error()
+        return x
+
+    def block(self, i: int, x: np.ndarray, H: int, W: int, nthreads: int = 0):
+        info = self.block_info(i)
+        Ho, Wo = (H // 2, W // 2) if info["q_stride"] else (H, W)
+        y = np.empty((Ho * Wo, info["dim_out"]), np.float32)
+        ho, wo = np.zeros(1, np.int32), np.zeros(1, np.int32)
+        x = np.ascontiguousarray(x, np.float32)
+        assert LIB.orc_hiera_block(self.h, i, ptr(x), H, W, ptr(y), ptr(ho), ptr(wo), nthreads) == 0, \
+            LIB.orc_last_error()
+        assert (int(ho[0]), int(wo[0])) == (Ho, Wo)
+        return y, Ho, Wo
+
+    def fpn(self, stages, nthreads: int = 0):
+        D = self.hp.neck_dim
+        st = [np.ascontiguousarray(s, np.float32) for s in stages]
+        outs = [np.empty((s * s, D), np.float32) for s in self.side]
+        sarr = (c_void_p * 4)(*[a.ctypes.data for a in st])
+        oarr = (c_void_p * 4)(*[a.ctypes.data for a in outs])
+        side = np.array(self.side, np.int32)
+        assert LIB.orc_hiera_fpn(self.h, ctypes.cast(sarr, c_void_p), ptr(side), ctypes.cast(oarr, c_void_p),
+                                 nthreads) == 0, LIB.orc_last_error()
+        return outs
+
+    def encode(self, chw: np.ndarray, nthreads: int = 0):
+        """FPN levels 0 .. 3 − scalp and the four stage outputs."""
+        D = self.hp.neck_dim
+        outs = [np.empty((s * s, D), np.float32) for s in self.side]
+        stages = [np.empty((s * s, w), np.float32) for s, w in zip(self.side, self.width)]
+        oarr = (c_void_p * 4)(*[a.ctypes.data for a in outs])
+        sarr = (c_void_p * 4)(*[a.ctypes.data for a in stages])
+        chw = np.ascontiguousarray(chw, np.float32)
+        assert LIB.orc_hiera_encode(self.h, ptr(chw), ctypes.cast(oarr, c_void_p), ctypes.cast(sarr, c_void_p),
+                                    nthreads) == 0, LIB.orc_last_error()
+        return outs[:4 - self.hp.scalp], stages
+
+    def __del__(self):
+        if getattr(self, "h", None) and LIB is not None:
+            LIB.orc_model_free(self.h)
+            self.h = None
+
+
+def preprocess_sam2(img_hwc: np.ndarray, img_size: int) -> np.ndarray:
+    img = np.ascontiguousarray(img_hwc, dtype=np.uint8)
+    out = np.empty((3, img_size, img_size), dtype=np.float32)
+    LIB.orc_preprocess_sam2(ptr(img), img.shape[1], img.shape[0], img_size, ptr(out))
+    return out
+
+
+def gelu_tanh(x: np.ndarray) -> np.ndarray:
+    y = np.array(x, np.float32, copy=True)
+    LIB.orc_gelu_tanh(ptr(y), y.size)
+    return y
+
+
 def conv_transpose_2x2(w16: np.ndarray, x: np.ndarray, nthreads: int = 0) -> np.ndarray:
     """w16: fp16 bits in ggml order [Cin][Cout][2][2] (ne = [2, 2, Cout, Cin]);
     x: [H, W, Cin] f32 → [2H, 2W, Cout]."""
@@ -270,8 +380,8 @@ def read_model_file(path: str):
     name → (dtype, ne, array in file order).  F32/F16 records are returned as
     float32 / float16 arrays of shape ne reversed; others as raw bytes."""
     data = open(path, "rb").read()
-    n = struct.unpack_from("<i", data, 12)[0]
-    off = 16 + 39 * 4
+    magic, n = struct.unpack_from("<I", data, 0)[0], struct.unpack_from("<i", data, 12)[0]
+    off = 16 + (57 if magic == 0x73616D32 else 39) * 4  # SAM 2 files carry 57 hparams
     out = {}
     for _ in range(n):
         nd, nl, dt = struct.unpack_from("<iii", data, off)

@@ -84,6 +84,9 @@ def test_synth_file_format(s3e, tmp_path, ft, code):
             assert dt == 0, name
         elif code >= 2:
             assert dt == (code if ne[0] % 32 == 0 else 0), name
+        elif code == 1:
+            # the converters keep "embed" tensors F32 in F16 files (the loader casts them)
+            assert dt == (0 if "embed" in name else 1), name
         else:
             assert dt == code, name
     assert t["vit.blocks.1.attn.freqs_cis"][1] == (2, 32, 144)
