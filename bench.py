@@ -20,6 +20,10 @@ Also reported, on the same JSON line:
                   int8 MFMA peak (fp16 for F16 weights, fp32 for F32).
                   `traffic` comes from the committed rocprofv3 FETCH_SIZE /
                   WRITE_SIZE counter summary when present.
+  sam2_encoders — the SAM 2.1 Hiera encoders (backbone + FPN to 256-ch
+                  levels at 256², 128², 64²) at 1024×1024 on the same kind of
+                  input: Hiera-Tiny with F16 weights and Hiera-Base+ with
+                  Q8_0 weights, ms per frame.
   cpu_baseline  — the CPU oracle (a C restatement of ggml's CPU path, not
                   the upstream binary) on this host: one whole frame of the
                   same model and image, backbone and neck (about 12 s on 16
@@ -45,6 +49,7 @@ PEAK_TOPS = {"q4_0": 5000.0, "q4_1": 5000.0, "q8_0": 5000.0, "f16": 2500.0, "f32
 CFG = dict(img_size=1008, patch=14, embed_dim=1024, depth=32, heads=16, mlp_ratio_x1000=4625, window=24,
            global_idx=(7, 15, 23, 31))
 GEMM_KERNEL = "k_gemm"
+SAM2_RUNS = [("hiera_t", "f16"), ("hiera_b+", "q8_0")]
 
 
 def log(msg: str) -> None:
@@ -113,6 +118,42 @@ def gemm_roofline(s3e, ctx, ev, ftype: str, reps: int):
     ops = 2.0 * M * N * K
     tops = ops / (ms * 1e-3) / 1e12
     return ms, tops, ops
+
+
+def sam2_encoders(s3e, ctx, ev, steps: int, warmup: int) -> dict:
+    """ms/frame of the SAM 2.1 Hiera encoders at 1024² (input resident in HBM)."""
+    res = {}
+    tmpdir = os.environ.get("TMPDIR", tempfile.gettempdir())
+    for variant, ft in SAM2_RUNS:
+        path = os.path.join(tmpdir, f"s3e_bench_{variant}_{ft}.ggml")
+        s3e.synth_write_sam2(path, variant, img_size=1024, ftype=ft, seed=0, std=0.02)
+        model = s3e.Model(ctx, path)
+        st = s3e.State(ctx, model)
+        img = synthetic_image(1024)
+        mean = np.array([0.485, 0.456, 0.406], np.float32)[:, None, None]
+        std = np.array([0.229, 0.224, 0.225], np.float32)[:, None, None]
+        chw = ((img.astype(np.float32) / np.float32(255)).transpose(2, 0, 1) - mean) / std
+        chw_d = ctx.to_device(np.ascontiguousarray(chw, np.float32))
+        for _ in range(warmup):
+            st.encode_chw(chw_d)
+        ctx.sync()
+        e0, e1 = ev.create(), ev.create()
+        ev.record(e0, ctx.stream)
+        for _ in range(steps):
+            st.encode_chw(chw_d)
+        ev.record(e1, ctx.stream)
+        ms = ev.elapsed_ms(e0, e1) / steps
+        ctx.sync()
+        name = f"{variant.replace('+', 'plus')}_{ft}_1024_ms"
+        res[name] = round(ms, 3)
+        log(f"{variant} {ft} 1024: {ms:.3f} ms/frame")
+        st.free()
+        model.free()
+        try:
+            os.remove(path)
+        except OSError:
+            pass
+    return res
 
 
 def _random_ggml_bytes(wt: int, N: int, K: int, rng) -> np.ndarray:
@@ -207,7 +248,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "gemm_fc1_q4_0_counters.txt"))
-    ap.add_argument("--only", choices=["encode", "gemm", "copy", "neck"], default=None,
+    ap.add_argument("--only", choices=["encode", "gemm", "copy", "neck", "sam2"], default=None,
                     help="run one leg only (for profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -233,6 +274,10 @@ def main() -> int:
         ev.record(e1, ctx.stream)
         ms = ev.elapsed_ms(e0, e1) / 10
         log(f"copy 1 GiB: {ms:.3f} ms = {2 * nbytes / ms / 1e6:.1f} GB/s (read+write)")
+        return 0
+
+    if args.only == "sam2":
+        sam2_encoders(s3e, ctx, ev, args.steps, args.warmup)
         return 0
 
     if args.only in (None, "gemm"):
@@ -281,6 +326,8 @@ def main() -> int:
     if args.only == "neck":
         return 0
 
+    sam2 = sam2_encoders(s3e, ctx, ev, max(3, args.steps // 2), 2)
+
     gms, gtops, gops = out["gemm"]
     peak = PEAK_TOPS[args.ftype]
     traffic = read_traffic(args.traffic) if args.ftype == "q4_0" else None
@@ -316,6 +363,7 @@ def main() -> int:
                    "img_size": 1008, "weights": args.ftype, "blocks": 32, "window": 24,
                    "global_blocks": [7, 15, 23, 31], "neck_levels": [288, 144, 72, 36]},
         "breakdown": {"neck_ms": round(neck_ms, 3), "backbone_ms": round(ms_frame - neck_ms, 3)},
+        "sam2_encoders": sam2,
         "roofline": {"kernel": f"{GEMM_KERNEL} fc1 M=5184 N=4736 K=1024 ({args.ftype})", "bound": "mfma",
                      "achieved": round(gtops, 1), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(gtops / peak, 4), "traffic": traffic,

@@ -150,18 +150,24 @@ int s3e_flash_attn_ext(s3e_ctx *ctx,
                        float scale, int prec, float *o);
 
 /* ---- encoder -------------------------------------------------------------
- * Load the SAM 3 image encoder of a sam3.cpp model file (magic "sam3",
- * version 3; sam3.cpp:3200-3344): the ViT backbone ("vit.") and the
- * SimpleFPN necks ("neck.trk.", and "neck.det." in full files;
- * sam3.cpp:2562-2596).  Other records are skipped, so full and visual-only
+ * Load the image encoder of a sam3.cpp model file (sam3.cpp:3200-3344):
+ * for SAM 3 files (magic "sam3", version 3) the ViT backbone ("vit.") and
+ * the SimpleFPN necks ("neck.trk.", and "neck.det." in full files;
+ * sam3.cpp:2562-2596); for SAM 2.x files (magic "sam2", version 1) the
+ * Hiera backbone ("hiera.") and its FPN ("fpn."; sam3.cpp:1745-1847).
+ * Other records are skipped, so full and visual-only
  * files both load; a file without neck records loads as a backbone-only
  * encoder.  Replaces the encoder part of sam3_load_model (sam3.h:184). */
 int s3e_model_load(s3e_ctx *ctx, const char *path, s3e_model **out);
 void s3e_model_free(s3e_model *m);
-/* out[0..15]: img_size, patch, E, depth, heads, mlp, window, n_global,
- * global_idx[4], ftype, tokens per side, neck_dim, necks present (bit 0
- * tracker, bit 1 detector). */
+/* SAM 3 files: out[0..15] = img_size, patch, E, depth, heads, mlp, window,
+ * n_global, global_idx[4], ftype, tokens per side, neck_dim, necks present
+ * (bit 0 tracker, bit 1 detector).  SAM 2 files: img_size, −1, embed_dim,
+ * blocks, heads, stages[4], q_pool, window_spec[0], scalp, ftype, level-0
+ * side, neck_dim, 1. */
 int s3e_model_hparams(const s3e_model *m, int32_t out[16]);
+/* sam3_get_model_type (sam3.h:194): 0 SAM 3, 1 SAM 3 visual-only, 2 SAM 2. */
+int s3e_model_type(const s3e_model *m);
 
 /* Per-image state holding activations and outputs (sam3_create_state,
  * sam3.h:196; outputs of sam3.cpp:896-928). */
@@ -193,12 +199,19 @@ int s3e_vit_block(s3e_state *st, int idx, float *x_device);
  * s3e_encode_chw does after the backbone (the neck part of the encode graph,
  * sam3.cpp:6072-6075). */
 int s3e_run_neck(s3e_state *st, const float *x_device);
+/* SAM 2 stage hook: Hiera block idx (sam2_hiera_block_forward,
+ * sam3.cpp:4295-4457) on x (device, H·W rows of the block's input width,
+ * NHWC) into y (H/2·W/2 rows under Q stride, else H·W, of its output
+ * width).  x and y may be the same buffer when the block keeps its size. */
+int s3e_hiera_block(s3e_state *st, int idx, const float *x_device, int H, int W, float *y_device);
 
 /* State outputs by name (sam3_get_state_tensor_info / sam3_dump_state_tensor,
  * sam3.h:407-414, sam3.cpp:14334-14376).  Names: "vit_output",
  * "neck_trk_<i>", "neck_det_<i>", "neck_det_pe_<i>", "neck_trk_pe_<i>" and
  * "pe_<i>" (i = 0..3; the PEs of sam3_sinusoidal_pe_2d, sam3.cpp:6146-6193).
- * A name the model does not produce is an error.  ne receives the ggml
+ * SAM 2 models: "neck_trk_<i>" and "neck_trk_pe_<i>" / "pe_<i>" for the
+ * levels kept after scalp (sam3.cpp:5959-6003), and "hiera_stage_<i>", the
+ * four stage outputs.  A name the model does not produce is an error.  ne receives the ggml
  * shape; get copies n floats to host memory. */
 int s3e_state_tensor_info(const s3e_state *st, const char *name, int64_t ne[4]);
 int s3e_state_tensor_get(const s3e_state *st, const char *name, float *host, size_t n);

@@ -59,8 +59,18 @@ constexpr int AW = 4;             // waves per work-group (one per SIMD)
 constexpr int NTHR = 64 * AW;
 constexpr int QT = 32 * AW;       // queries per work-group
 constexpr int KT = 32;            // keys per tile
-constexpr int KPL = KT * 128;     // bytes of one K plane of a tile: 32 keys × 64 d
-constexpr int VPL = 64 * KT * 2;  // bytes of one Vᵀ plane of a tile: 64 d × 32 keys
+
+// Geometry by head dimension (64, or 128 for wider heads zero-padded to it).
+template <int HD>
+struct AG {
+    static constexpr int ROWK = HD * 2;        // bytes of one K row
+    static constexpr int KPL = KT * ROWK;      // bytes of one K plane of a tile
+    static constexpr int VPL = HD * KT * 2;    // bytes of one Vᵀ plane of a tile: HD rows × 32 keys
+    static constexpr int KRUNS = KPL / 1024 / AW;  // 1 KB DMA runs per wave per K plane
+    static constexpr int VRUNS = VPL / 1024 / AW;  // ... per Vᵀ plane
+    static constexpr int DS = HD / 16;         // K=16 steps of Sᵀ
+    static constexpr int DT = HD / 32;         // 32-row tiles of Oᵀ
+};
 
 __device__ __forceinline__ uint16_t f2h_bits(float v) { return half_bits(v); }
 
@@ -73,6 +83,11 @@ __device__ __forceinline__ v16f mfma(const v8h &a, const v8h &b, const v16f &c) 
 // r, r+4, r+8, r+12 do (swzv); either way the 16 rows one ds_read_b128 phase
 // touches land on distinct banks.
 __device__ __forceinline__ int swzk(int r) { return (r >> 1) & 7; }
+// 256-byte K rows (HD = 128) each span all 64 banks: 16 consecutive rows need
+// 16 distinct slots
+__device__ __forceinline__ int swzk256(int r) { return r & 15; }
+template <int HD>
+__device__ __forceinline__ int swzk_hd(int r) { return HD == 64 ? swzk(r) : swzk256(r); }
 __device__ __forceinline__ int swzv(int r) { return (r >> 2) & 3; }
 
 // p − h for the fp16 value h in the low or high half of h2, exact, in one
@@ -93,9 +108,13 @@ __device__ __forceinline__ void wait_and_barrier() {
     __asm__ volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-template <bool SPLIT>
-__global__ __launch_bounds__(NTHR, 3) void k_attn(AttnArgs a, int ldv) {
+// CROP: the windowed, cropped output mapping and narrower real heads
+// (a.wo, a.hd_out; the Hiera layouts), kept out of the plain variants.
+template <bool SPLIT, int HD, bool CROP>
+__global__ __launch_bounds__(NTHR, HD == 64 ? 3 : 2) void k_attn(AttnArgs a, int ldv) {
+    using G = AG<HD>;
     constexpr int NP = SPLIT ? 2 : 1;  // planes: hi (and lo)
+    constexpr int KPL = G::KPL, VPL = G::VPL;
     constexpr int KBUF = NP * KPL, VBUF = NP * VPL;
     // K ring (2 tiles) then Vᵀ ring (2 tiles)
     __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * KBUF + 2 * VBUF];
@@ -107,14 +126,14 @@ __global__ __launch_bounds__(NTHR, 3) void k_attn(AttnArgs a, int ldv) {
     const int qi = q0 + wave * 32 + lr;
     const bool qvalid = qi < a.Nq;
 
-    v8h qf[NP][4];
+    v8h qf[NP][G::DS];
     {
-        const int64_t off = ((int64_t)bh * a.Nq + (qvalid ? qi : 0)) * 64;
+        const int64_t off = ((int64_t)bh * a.Nq + (qvalid ? qi : 0)) * HD;
 #pragma unroll
         for (int pl = 0; pl < NP; pl++) {
             const _Float16 *qrow = (pl == 0 ? a.q : a.q_lo) + off;
 #pragma unroll
-            for (int ds = 0; ds < 4; ds++) {
+            for (int ds = 0; ds < G::DS; ds++) {
                 v8h z = {};
                 qf[pl][ds] = qvalid ? *(const v8h *)(qrow + ds * 16 + lh * 8) : z;
             }
@@ -122,51 +141,64 @@ __global__ __launch_bounds__(NTHR, 3) void k_attn(AttnArgs a, int ldv) {
     }
     const float c = a.scale * 1.44269504088896340736f;
     float mrun = -INFINITY, lsum = 0.f;
-    v16f o[2];
+    v16f o[G::DT];
 #pragma unroll
-    for (int r = 0; r < 16; r++) { o[0][r] = 0.f; o[1][r] = 0.f; }
+    for (int dt = 0; dt < G::DT; dt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[dt][r] = 0.f;
 
-    const int64_t koff = (int64_t)bh * a.Nkv * 64, voff = (int64_t)bh * 64 * ldv;
+    const int64_t koff = (int64_t)bh * a.Nkv * HD, voff = (int64_t)bh * HD * ldv;
     const int ntiles = (a.Nkv + KT - 1) / KT;
     uint8_t *const Kring = lds, *const Vring = lds + 2 * KBUF;
 
-    // DMA: per plane, a K tile is 4 runs of 1 KB (8 rows of 128 B) and a Vᵀ
-    // tile 4 runs of 1 KB (16 rows of 64 B); wave w moves run w.  A lane writes
-    // the 16 bytes at 16·lane of its run and fetches the chunk that belongs there.
-    // Rows past the keys are clamped onto real ones (their scores are masked,
-    // and Vᵀ keys past Nkv are zero).
+    // DMA: per plane, a K tile is runs of 1 KB (8 rows of 128 B, or 4 of 256 B)
+    // and a Vᵀ tile runs of 1 KB (16 rows of 64 B); wave w moves runs
+    // w·RUNS .. w·RUNS + RUNS − 1.  A lane writes the 16 bytes at 16·lane of its
+    // run and fetches the chunk that belongs there.  Rows past the keys are
+    // clamped onto real ones (their scores are masked, and Vᵀ keys past Nkv
+    // are zero).
     auto issue_k = [&](int tt) {
         uint8_t *L = Kring + (tt & 1) * KBUF;
-        const int r = 8 * wave + (lane >> 3);
-        const int ch = (lane & 7) ^ swzk(r);
-        const int64_t key = min(tt * KT + r, a.Nkv - 1);
+        constexpr int RPR = 1024 / G::ROWK;      // rows per run
+        constexpr int CPR = G::ROWK / 16;        // chunks per row
 #pragma unroll
-        for (int pl = 0; pl < NP; pl++) {
-            const _Float16 *src = (pl == 0 ? a.k : a.k_lo) + koff + key * 64 + ch * 8;
-            __builtin_amdgcn_global_load_lds((const void *)src, LDS_PTR(L + pl * KPL + wave * 1024), 16, 0, 0);
+        for (int j = 0; j < G::KRUNS; j++) {
+            const int run = wave * G::KRUNS + j;
+            const int r = RPR * run + lane / CPR;
+            const int ch = (lane % CPR) ^ swzk_hd<HD>(r);
+            const int64_t key = min(tt * KT + r, a.Nkv - 1);
+#pragma unroll
+            for (int pl = 0; pl < NP; pl++) {
+                const _Float16 *src = (pl == 0 ? a.k : a.k_lo) + koff + key * HD + ch * 8;
+                __builtin_amdgcn_global_load_lds((const void *)src, LDS_PTR(L + pl * KPL + run * 1024), 16, 0, 0);
+            }
         }
     };
     auto issue_v = [&](int tt) {
         uint8_t *L = Vring + (tt & 1) * VBUF;
-        const int r = 16 * wave + (lane >> 2);
-        const int ch = (lane & 3) ^ swzv(r);
-        const int k0 = min(tt * KT + ch * 8, ldv - 8);
 #pragma unroll
-        for (int pl = 0; pl < NP; pl++) {
-            const _Float16 *src = (pl == 0 ? a.vt : a.vt_lo) + voff + (int64_t)r * ldv + k0;
-            __builtin_amdgcn_global_load_lds((const void *)src, LDS_PTR(L + pl * VPL + wave * 1024), 16, 0, 0);
+        for (int j = 0; j < G::VRUNS; j++) {
+            const int run = wave * G::VRUNS + j;
+            const int r = 16 * run + (lane >> 2);
+            const int ch = (lane & 3) ^ swzv(r);
+            const int k0 = min(tt * KT + ch * 8, ldv - 8);
+#pragma unroll
+            for (int pl = 0; pl < NP; pl++) {
+                const _Float16 *src = (pl == 0 ? a.vt : a.vt_lo) + voff + (int64_t)r * ldv + k0;
+                __builtin_amdgcn_global_load_lds((const void *)src, LDS_PTR(L + pl * VPL + run * 1024), 16, 0, 0);
+            }
         }
     };
 
-    const int xk = swzk(lr), xv = swzv(lr);  // operand rows start at multiples of 32
+    const int xk = swzk_hd<HD>(lr), xv = swzv(lr);  // operand rows start at multiples of 32
 
     // Sᵀ = K·Qᵀ for the 32 keys of tile tt × 32 queries
     auto qk = [&](int tt) {
         const uint8_t *L = Kring + (tt & 1) * KBUF;
         v16f acc = {};
 #pragma unroll
-        for (int ds = 0; ds < 4; ds++) {
-            const int o_ = lr * 128 + (((2 * ds + lh) ^ xk) << 4);
+        for (int ds = 0; ds < G::DS; ds++) {
+            const int o_ = lr * G::ROWK + (((2 * ds + lh) ^ xk) << 4);
             const v8h kh = *(const v8h *)(L + o_);
             if constexpr (SPLIT) {
                 const v8h kl = *(const v8h *)(L + KPL + o_);
@@ -181,7 +213,7 @@ __global__ __launch_bounds__(NTHR, 3) void k_attn(AttnArgs a, int ldv) {
     auto pv = [&](int tt, const v8h (&ph)[2], const v8h (&pl)[2]) {
         const uint8_t *L = Vring + (tt & 1) * VBUF;
 #pragma unroll
-        for (int dt = 0; dt < 2; dt++)
+        for (int dt = 0; dt < G::DT; dt++)
 #pragma unroll
             for (int jj = 0; jj < 2; jj++) {
                 const int o_ = (dt * 32 + lr) * 64 + (((2 * jj + lh) ^ xv) << 4);
@@ -278,7 +310,9 @@ __global__ __launch_bounds__(NTHR, 3) void k_attn(AttnArgs a, int ldv) {
             lsum = lsum * alpha + ps;
             if (__any(raise)) {
 #pragma unroll
-                for (int r = 0; r < 16; r++) { o[0][r] *= alpha; o[1][r] *= alpha; }
+                for (int dt = 0; dt < G::DT; dt++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) o[dt][r] *= alpha;
             }
             mrun = mnew;
         }
@@ -312,12 +346,23 @@ __global__ __launch_bounds__(NTHR, 3) void k_attn(AttnArgs a, int ldv) {
     lsum += __shfl_xor(lsum, 32, 64);
     const float inv = (lsum == 0.f) ? 0.f : 1.0f / lsum;
 #pragma unroll
-    for (int r = 0; r < 16; r++) { o[0][r] *= inv; o[1][r] *= inv; }
+    for (int dt = 0; dt < G::DT; dt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[dt][r] *= inv;
 
     // output row for (batch b, query qi)
     const int b = bh / a.NH, h = bh % a.NH;
     int64_t orow;
-    if (a.grid > 0) {
+    bool ovalid = qvalid;
+    if (CROP && a.wo > 0) {
+        // windows of wo×wo queries, row-major over nwx windows per row, on an
+        // out_h × out_w grid; positions past it (window padding) are dropped
+        const int wy = b / a.nwx, wx = b % a.nwx;
+        const int qq = qvalid ? qi : 0;
+        const int y = wy * a.wo + qq / a.wo, x = wx * a.wo + qq % a.wo;
+        ovalid = ovalid && y < a.out_h && x < a.out_w;
+        orow = (int64_t)y * a.out_w + x;
+    } else if (a.grid > 0) {
         const int nwx = a.grid / a.window;
         const int wy = b / nwx, wx = b % nwx;
         const int iy = (qvalid ? qi : 0) / a.window, ix = (qvalid ? qi : 0) % a.window;
@@ -326,9 +371,11 @@ __global__ __launch_bounds__(NTHR, 3) void k_attn(AttnArgs a, int ldv) {
         orow = (int64_t)b * a.Nq + qi;
     }
     const Act &out = a.out;
-    const int64_t colbase = (int64_t)h * 64;
+    const int hdo = (CROP && a.hd_out > 0) ? a.hd_out : HD;  // real head dim: padded columns are not stored
+    const int64_t colbase = (int64_t)h * hdo;
 #pragma unroll
-    for (int dt = 0; dt < 2; dt++) {
+    for (int dt = 0; dt < G::DT; dt++) {
+        if (CROP && dt * 32 >= hdo) break;
         if (out.kind == A_Q8_0 || out.kind == A_Q8_1) {
             // ggml quantize_row_q8_0/q8_1 of the 32 values d = dt*32 .. dt*32+31,
             // split 16/16 between lanes l and l^32
@@ -352,7 +399,7 @@ __global__ __launch_bounds__(NTHR, 3) void k_attn(AttnArgs a, int ldv) {
                 w[g] = packed;
             }
             sum += __shfl_xor(sum, 32, 64);
-            if (qvalid) {
+            if (ovalid) {
                 int8_t *dst = (int8_t *)out.x + orow * out.ld + colbase + dt * 32 + 4 * lh;
 #pragma unroll
                 for (int g = 0; g < 4; g++) *(uint32_t *)(dst + 8 * g) = w[g];
@@ -362,9 +409,10 @@ __global__ __launch_bounds__(NTHR, 3) void k_attn(AttnArgs a, int ldv) {
                     if (out.kind == A_Q8_1) out.s[blk] = f2h_bits(d * (float)sum);
                 }
             }
-        } else if (qvalid) {
+        } else if (ovalid) {
 #pragma unroll
             for (int g = 0; g < 4; g++) {
+                if (CROP && dt * 32 + 8 * g + 4 * lh >= hdo) continue;  // zero-padded head dims
                 const int64_t col = colbase + dt * 32 + 8 * g + 4 * lh;
                 if (out.kind == A_F32) {
                     *(float4 *)((float *)out.x + orow * out.ld + col) =
@@ -384,9 +432,23 @@ __global__ __launch_bounds__(NTHR, 3) void k_attn(AttnArgs a, int ldv) {
 hipError_t launch_attn(const AttnArgs &a, hipStream_t st) {
     // Vᵀ rows hold vt_ld_for(Nkv) keys (zero past Nkv, in vt_slot order)
     const int ldv = (int)vt_ld_for(a.Nkv);
+    const int hd = a.hd > 0 ? a.hd : 64;
+    if ((hd != 64 && hd != 128) || a.BH <= 0 || a.BH > 65535 || a.Nq <= 0 || a.Nkv <= 0) return hipErrorInvalidValue;
+    // a Q8 output block must lie inside one head
+    if ((a.out.kind == A_Q8_0 || a.out.kind == A_Q8_1) && a.hd_out > 0 && a.hd_out % 32 != 0)
+        return hipErrorInvalidValue;
     const dim3 grid((unsigned)((a.Nq + QT - 1) / QT), (unsigned)a.BH);
-    if (a.q_lo) hipLaunchKernelGGL(k_attn<true>, grid, dim3(NTHR), 0, st, a, ldv);
-    else hipLaunchKernelGGL(k_attn<false>, grid, dim3(NTHR), 0, st, a, ldv);
+    const bool crop = a.wo > 0 || (a.hd_out > 0 && a.hd_out != hd);
+    if (hd == 64 && !crop) {
+        if (a.q_lo) hipLaunchKernelGGL((k_attn<true, 64, false>), grid, dim3(NTHR), 0, st, a, ldv);
+        else hipLaunchKernelGGL((k_attn<false, 64, false>), grid, dim3(NTHR), 0, st, a, ldv);
+    } else if (hd == 64) {
+        if (a.q_lo) hipLaunchKernelGGL((k_attn<true, 64, true>), grid, dim3(NTHR), 0, st, a, ldv);
+        else hipLaunchKernelGGL((k_attn<false, 64, true>), grid, dim3(NTHR), 0, st, a, ldv);
+    } else {
+        if (a.q_lo) hipLaunchKernelGGL((k_attn<true, 128, true>), grid, dim3(NTHR), 0, st, a, ldv);
+        else hipLaunchKernelGGL((k_attn<false, 128, true>), grid, dim3(NTHR), 0, st, a, ldv);
+    }
     return hipGetLastError();
 }
 

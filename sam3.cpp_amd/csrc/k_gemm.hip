@@ -262,13 +262,29 @@ __device__ __forceinline__ void epilogue(const GemmParams &p, const float *Ct, i
                 const float4 x = *(const float4 *)(Ct + row * CLD + cc * 32 + j);
                 v[j] = x.x; v[j + 1] = x.y; v[j + 2] = x.z; v[j + 3] = x.w;
             }
+            if (e.gelu_tab) {
+                // ggml_vec_gelu_f32 with GGML_GELU_FP16: x ≤ −10 → 0, x ≥ 10 → x,
+                // else the table entry at fp16(x)
 #pragma unroll
-            for (int j = 0; j < 32; j += 4) {
-                const float4 bb = *(const float4 *)(e.bias + gn0 + j);
-                v[j] = gelu_erf(__fadd_rn(v[j], bb.x));
-                v[j + 1] = gelu_erf(__fadd_rn(v[j + 1], bb.y));
-                v[j + 2] = gelu_erf(__fadd_rn(v[j + 2], bb.z));
-                v[j + 3] = gelu_erf(__fadd_rn(v[j + 3], bb.w));
+                for (int j = 0; j < 32; j += 4) {
+                    const float4 bb = *(const float4 *)(e.bias + gn0 + j);
+                    const float bj[4] = {bb.x, bb.y, bb.z, bb.w};
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const float x = __fadd_rn(v[j + i], bj[i]);
+                        const float t = (float)__builtin_bit_cast(_Float16, e.gelu_tab[half_bits(x)]);
+                        v[j + i] = x <= -10.f ? 0.f : (x >= 10.f ? x : t);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 32; j += 4) {
+                    const float4 bb = *(const float4 *)(e.bias + gn0 + j);
+                    v[j] = gelu_erf(__fadd_rn(v[j], bb.x));
+                    v[j + 1] = gelu_erf(__fadd_rn(v[j + 1], bb.y));
+                    v[j + 2] = gelu_erf(__fadd_rn(v[j + 2], bb.z));
+                    v[j + 3] = gelu_erf(__fadd_rn(v[j + 3], bb.w));
+                }
             }
             const Act &o = e.out;
             if (o.kind == A_F16) {
@@ -307,6 +323,10 @@ __device__ __forceinline__ void epilogue(const GemmParams &p, const float *Ct, i
             if constexpr (EPI == EPI_POS) {
                 const int py = gm / e.grid, px = gm % e.grid;
                 const float *pr = e.pos + ((int64_t)(py % e.pos_grid) * e.pos_grid + (px % e.pos_grid)) * p.N + gn;
+                if (e.bias) {
+#pragma unroll
+                    for (int j = 0; j < 4; j++) v[j] = __fadd_rn(v[j], e.bias[gn + j]);
+                }
 #pragma unroll
                 for (int j = 0; j < 4; j++) v[j] = __fadd_rn(v[j], pr[j]);
             } else {

@@ -1,0 +1,152 @@
+// k_hiera.hip — data movement of the SAM 2.x Hiera encoder around the shared
+// GEMM and attention kernels (sam2_build_hiera_graph, sam3.cpp:4462-4527;
+// sam2_hiera_block_forward, sam3.cpp:4295-4457; the FPN top-down path,
+// sam3.cpp:4567-4590).  All activations are NHWC: token (y, x) is a row of
+// channels.
+#include "s3e_internal.h"
+
+namespace s3e {
+namespace {
+
+// im2col of the patch embedding (Conv2d 3→E, k×k, stride, pad): CHW f32
+// [3][S][S] → rows [OH·OW][ldk] in F32 or F16 (ggml's im2col in the kernel
+// type), K ordered [c][ky][kx] as the kernel rows are; taps outside the image
+// and columns K..ldk are zero.
+__global__ void k_im2col_conv(const float *__restrict__ chw, int S, int k, int stride, int pad, int OW, int64_t T,
+                              int64_t ldk, int kind, void *out) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= T * ldk) return;
+    const int64_t t = idx / ldk;
+    const int kk = (int)(idx % ldk);
+    float val = 0.f;
+    if (kk < 3 * k * k) {
+        const int c = kk / (k * k), r = kk % (k * k), ky = r / k, kx = r % k;
+        const int oy = (int)(t / OW), ox = (int)(t % OW);
+        const int iy = oy * stride + ky - pad, ix = ox * stride + kx - pad;
+        if (iy >= 0 && iy < S && ix >= 0 && ix < S) val = chw[(int64_t)c * S * S + (int64_t)iy * S + ix];
+    }
+    if (kind == A_F16) ((_Float16 *)out)[idx] = to_half(val);
+    else ((float *)out)[idx] = val;
+}
+
+// Attention operands of one Hiera block from the QKV GEMM output (f32
+// [H·W][3C], bias already added).  Windows of wh × ww tokens, row-major over
+// nwx per row, cover the zero-padded grid; a padded position takes the QKV
+// bias, as ggml_pad's zero rows do after the projection.  Q is max-pooled
+// 2×2 inside each window under Q stride (sam2_maxpool_2d on the window's
+// grid).  Heads are zero-padded from HD to HDp channels.  Q, K: [b·NH + h]
+// [pos][HDp]; Vᵀ: [b·NH + h][HDp][ldv] with keys in vt_slot order and zeros
+// for keys Nkv .. ldv − 1.  With lo planes the values are split hi + lo.
+struct Prep {
+    const float *qkv, *bias;
+    int H, W, C, NH, HD, HDp;
+    int wh, ww, nwx, qs;
+    int Nq, Nkv, ldv, NW;
+    _Float16 *q, *k, *vt, *q_lo, *k_lo, *vt_lo;
+};
+
+__device__ __forceinline__ float qkv_at(const Prep &p, int b, int py, int px, int col) {
+    const int wy = b / p.nwx, wx = b % p.nwx;
+    const int y = wy * p.wh + py, x = wx * p.ww + px;
+    if (y < p.H && x < p.W) return p.qkv[((int64_t)y * p.W + x) * 3 * p.C + col];
+    return p.bias[col];
+}
+
+__device__ __forceinline__ void put(_Float16 *hi, _Float16 *lo, int64_t i, float v) {
+    const _Float16 h = to_half(v);
+    hi[i] = h;
+    if (lo) lo[i] = (_Float16)(v - (float)h);
+}
+
+// mode 0: Q (one thread per (b, h, query, d)); 1: K; 2: Vᵀ (keys up to ldv)
+__global__ void k_hiera_prep(Prep p, int mode, int64_t total) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    const int d = (int)(i % p.HDp);
+    const int64_t r = i / p.HDp;
+    const int npos = mode == 0 ? p.Nq : (mode == 1 ? p.Nkv : p.ldv);
+    const int pos = (int)(r % npos);
+    const int64_t bh = r / npos;
+    const int b = (int)(bh / p.NH), h = (int)(bh % p.NH);
+    float v = 0.f;
+    if (d < p.HD && pos < (mode == 0 ? p.Nq : p.Nkv)) {
+        const int col = mode * p.C + h * p.HD + d;
+        if (mode == 0 && p.qs) {
+            const int qw = p.ww / 2;
+            const int qy = pos / qw, qx = pos % qw;
+            v = fmaxf(fmaxf(qkv_at(p, b, 2 * qy, 2 * qx, col), qkv_at(p, b, 2 * qy, 2 * qx + 1, col)),
+                      fmaxf(qkv_at(p, b, 2 * qy + 1, 2 * qx, col), qkv_at(p, b, 2 * qy + 1, 2 * qx + 1, col)));
+        } else {
+            v = qkv_at(p, b, pos / p.ww, pos % p.ww, col);
+        }
+    }
+    if (mode == 0) put(p.q, p.q_lo, (bh * p.Nq + pos) * p.HDp + d, v);
+    else if (mode == 1) put(p.k, p.k_lo, (bh * p.Nkv + pos) * p.HDp + d, v);
+    else put(p.vt, p.vt_lo, (bh * p.HDp + d) * p.ldv + vt_slot(pos), v);
+}
+
+// dst [side²][D] += nearest ×2 upsampling of src [(side/2)²][D]
+// (ggml_upscale NEAREST, then ggml_add; sam3.cpp:4575-4580)
+__global__ void k_upsample_add(float *__restrict__ dst, const float *__restrict__ src, int side, int D,
+                               int64_t n4) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n4) return;
+    const int d4 = D / 4;
+    const int64_t pix = i / d4;
+    const int c = (int)(i % d4) * 4;
+    const int y = (int)(pix / side), x = (int)(pix % side);
+    const float4 u = *(const float4 *)(src + ((int64_t)(y / 2) * (side / 2) + x / 2) * D + c);
+    float4 *o = (float4 *)(dst + pix * D + c);
+    const float4 a = *o;
+    *o = make_float4(__fadd_rn(a.x, u.x), __fadd_rn(a.y, u.y), __fadd_rn(a.z, u.z), __fadd_rn(a.w, u.w));
+}
+
+}  // namespace
+
+hipError_t launch_im2col_conv(const float *chw, int S, int k, int stride, int pad, int64_t ldk, AKind kind,
+                              void *out, hipStream_t st) {
+    const int O = (S + 2 * pad - k) / stride + 1;
+    if ((kind != A_F16 && kind != A_F32) || ldk < 3LL * k * k) return hipErrorInvalidValue;
+    const int64_t T = (int64_t)O * O, total = T * ldk;
+    hipLaunchKernelGGL(k_im2col_conv, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, chw, S, k, stride,
+                       pad, O, T, ldk, (int)kind, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_hiera_prep(const HieraPrepArgs &a, hipStream_t st) {
+    Prep p;
+    p.qkv = a.qkv;
+    p.bias = a.bias;
+    p.H = a.H; p.W = a.W; p.C = a.C; p.NH = a.NH; p.HD = a.HD; p.HDp = a.HDp;
+    p.qs = a.q_stride;
+    if (a.window > 0) {
+        p.wh = p.ww = a.window;
+        p.nwx = (a.W + a.window - 1) / a.window;
+        p.NW = p.nwx * ((a.H + a.window - 1) / a.window);
+    } else {
+        p.wh = a.H;
+        p.ww = a.W;
+        p.nwx = 1;
+        p.NW = 1;
+    }
+    p.Nkv = p.wh * p.ww;
+    p.Nq = a.q_stride ? (p.wh / 2) * (p.ww / 2) : p.Nkv;
+    p.ldv = (int)vt_ld_for(p.Nkv);
+    p.q = a.q; p.k = a.k; p.vt = a.vt; p.q_lo = a.q_lo; p.k_lo = a.k_lo; p.vt_lo = a.vt_lo;
+    if (p.HD > p.HDp || p.HDp % 8 != 0) return hipErrorInvalidValue;
+    const int64_t bh = (int64_t)p.NW * p.NH;
+    const int64_t tq = bh * p.Nq * p.HDp, tk = bh * p.Nkv * p.HDp, tv = bh * p.ldv * p.HDp;
+    hipLaunchKernelGGL(k_hiera_prep, dim3((unsigned)((tq + 255) / 256)), dim3(256), 0, st, p, 0, tq);
+    hipLaunchKernelGGL(k_hiera_prep, dim3((unsigned)((tk + 255) / 256)), dim3(256), 0, st, p, 1, tk);
+    hipLaunchKernelGGL(k_hiera_prep, dim3((unsigned)((tv + 255) / 256)), dim3(256), 0, st, p, 2, tv);
+    return hipGetLastError();
+}
+
+hipError_t launch_upsample_add(float *dst, const float *src, int side, int D, hipStream_t st) {
+    if (D % 4 != 0 || side % 2 != 0) return hipErrorInvalidValue;
+    const int64_t n4 = (int64_t)side * side * (D / 4);
+    hipLaunchKernelGGL(k_upsample_add, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, dst, src, side, D, n4);
+    return hipGetLastError();
+}
+
+}  // namespace s3e

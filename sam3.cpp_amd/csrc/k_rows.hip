@@ -233,8 +233,8 @@ __global__ __launch_bounds__(256) void k_pool_act(const float *__restrict__ x, i
 }  // namespace
 
 hipError_t launch_pool_act(const float *x, int h, int w, int c, int pool, const Act &out, hipStream_t st) {
-    if ((pool != 1 && pool != 2) || c % 4 != 0 || (out.kind != A_F16 && out.kind != A_F16X2) || out.ld != c ||
-        h < pool || w < pool)
+    if ((pool != 1 && pool != 2) || c % 4 != 0 || (out.kind != A_F16 && out.kind != A_F16X2 && out.kind != A_F32) ||
+        out.ld != c || h < pool || w < pool)
         return hipErrorInvalidValue;
     const int oh = pool == 1 ? h : (h - 2) / 2 + 1, ow = pool == 1 ? w : (w - 2) / 2 + 1;
     const int64_t n4 = (int64_t)oh * ow * (c / 4);
@@ -244,7 +244,9 @@ hipError_t launch_pool_act(const float *x, int h, int w, int c, int pool, const 
 
 hipError_t launch_layernorm(const float *x, int64_t M, int64_t E, float eps, const float *w,
                             const float *b, const Act &out, float *y_f32, hipStream_t st) {
-    if (E % 32 != 0 || E > 4096) return hipErrorInvalidValue;
+    // float4 lanes; a Q8 block must be whole inside the row
+    const bool q8 = !y_f32 && (out.kind == A_Q8_0 || out.kind == A_Q8_1);
+    if (E % 4 != 0 || E > 4096 || (q8 && E % 32 != 0)) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((M + 3) / 4));
     if (E <= 256) hipLaunchKernelGGL(k_layernorm<1>, grid, dim3(256), 0, st, x, M, E, eps, w, b, out, y_f32);
     else if (E <= 512) hipLaunchKernelGGL(k_layernorm<2>, grid, dim3(256), 0, st, x, M, E, eps, w, b, out, y_f32);

@@ -91,7 +91,7 @@ struct Weight {
 enum Epi : int {
     EPI_F32 = 0,     // y = acc + bias
     EPI_RESID = 1,   // y += acc + bias                    (residual add)
-    EPI_POS = 2,     // y = acc + pos[tile(token)]          (patch embed + tiled pos_embed)
+    EPI_POS = 2,     // y = (acc + bias) + pos[tile(token)]  (patch embed + tiled pos_embed; bias optional)
     EPI_GELU = 3,    // act = quant(gelu_erf(acc + bias))   (fc1 → fc2)
     EPI_QKV = 4,     // split Q/K/V, RoPE, fp16, window layout
     EPI_DECONV = 5,  // 2×2 stride-2 transposed conv: (+ bias, GELU) → pixel shuffle into act
@@ -121,6 +121,9 @@ struct EpiArgs {
     // channel n % cout, written to output pixel (2y + ky, 2x + kx)
     int dc_w = 0, dc_cout = 0;
     int gelu = 0;                  // EPI_DECONV: gelu_erf after the bias
+    // EPI_GELU: ggml_gelu (tanh form) through this fp16 table (65536 entries,
+    // ggml_vec_gelu_f32 with GGML_GELU_FP16) instead of gelu_erf
+    const uint16_t *gelu_tab = nullptr;
 };
 
 // Implicit-GEMM geometry of a 3×3 stride-1 pad-1 convolution over an NHWC
@@ -146,15 +149,21 @@ __host__ __device__ inline int64_t vt_ld_for(int64_t nkv) { return (nkv + 15) / 
 
 // Attention I/O.
 struct AttnArgs {
-    const _Float16 *q = nullptr;   // [BH][Nq][64]
-    const _Float16 *k = nullptr;   // [BH][Nkv][64]
-    const _Float16 *vt = nullptr;  // [BH][64][vt_ld_for(Nkv)], keys in vt_slot order
+    const _Float16 *q = nullptr;   // [BH][Nq][hd]
+    const _Float16 *k = nullptr;   // [BH][Nkv][hd]
+    const _Float16 *vt = nullptr;  // [BH][hd][vt_ld_for(Nkv)], keys in vt_slot order
     // low halves (x = hi + lo) for split-precision attention, else null
     const _Float16 *q_lo = nullptr, *k_lo = nullptr, *vt_lo = nullptr;
     int Nq = 0, Nkv = 0, NH = 0, BH = 0;
+    int hd = 64;                   // head dim of the q/k/vt rows: 64, or 128 (narrower heads zero-padded)
+    int hd_out = 0;                // real head dim (0: = hd); output columns h·hd_out + d for d < hd_out
     float scale = 0.f;
     // output row of query i of batch b: token(b, i) when grid > 0, else b*Nq + i
     int grid = 0, window = 0;
+    // windowed output with cropping (wo > 0): query i of window b = (b / nwx,
+    // b % nwx) sits at (y, x) = (wy·wo + i / wo, wx·wo + i % wo) of an
+    // out_h × out_w grid, row y·out_w + x; positions outside are dropped
+    int wo = 0, nwx = 0, out_h = 0, out_w = 0;
     Act out;                       // A_Q8_0 / A_Q8_1 / A_F16 / A_F32, row = token, col = h*64 + d
 };
 
@@ -182,6 +191,26 @@ hipError_t launch_attn_prep(const float *q, const int64_t q_nb[4], const float *
 hipError_t launch_im2col(const float *chw, int img, int P, int64_t ldk, AKind kind, void *out,
                          hipStream_t st);
 hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t st);
+
+// ---- Hiera (k_hiera.hip) ----
+// Patch-embedding im2col: CHW f32 [3][S][S], k×k / stride / pad → rows of ldk.
+hipError_t launch_im2col_conv(const float *chw, int S, int k, int stride, int pad, int64_t ldk, AKind kind,
+                              void *out, hipStream_t st);
+// Attention operands of a Hiera block from its QKV GEMM output (window
+// partition with bias-valued padding, Q max-pool, head split, zero-padded
+// head dim, fp16 hi/lo).
+struct HieraPrepArgs {
+    const float *qkv = nullptr;   // [H·W][3C] f32, bias added
+    const float *bias = nullptr;  // [3C]: the value of padded window positions
+    int H = 0, W = 0, C = 0, NH = 0, HD = 0, HDp = 0;
+    int window = 0;               // 0: one window of the whole grid (global attention)
+    int q_stride = 0;
+    _Float16 *q = nullptr, *k = nullptr, *vt = nullptr;
+    _Float16 *q_lo = nullptr, *k_lo = nullptr, *vt_lo = nullptr;
+};
+hipError_t launch_hiera_prep(const HieraPrepArgs &a, hipStream_t st);
+// dst [side²][D] += nearest-×2 upsampling of src [(side/2)²][D]
+hipError_t launch_upsample_add(float *dst, const float *src, int side, int D, hipStream_t st);
 
 // fp32 → fp16 of a value computed in fp32.  The empty asm statement (it emits
 // no instruction) pins the fp32 value in a VGPR: without it LLVM folds

@@ -1,0 +1,80 @@
+// s3e_rt.h — host-side helpers shared by the runtime translation units
+// (s3e_runtime.cpp: contexts, weights, SAM 3 model and state; s3e_hiera.cpp:
+// the SAM 2.x Hiera model and state).  Not part of the public ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <vector>
+
+#include "s3e_host.h"
+#include "s3e_internal.h"
+
+namespace s3e {
+
+int64_t round_up(int64_t x, int64_t m);
+WKind wkind_of(int type);
+void free_weight(Weight &w);
+// Repack ggml bytes (N rows of K in `type`) into the GEMM layout and upload;
+// N is padded to npad.
+int upload_weight(int device, int type, int64_t K, int64_t N, const uint8_t *src, size_t nbytes, Weight &w,
+                  int64_t npad = GEMM_BN);
+// f32 weights as the two fp16 planes of WK_F16X3, N padded to npad.
+int upload_weight_split(const float *src, int64_t K, int64_t N, Weight &w, int64_t npad);
+
+// A tensor record as read from a model file.
+struct RawTensor {
+    int type = 0;
+    int n_dims = 0;
+    int64_t ne[4] = {1, 1, 1, 1};
+    std::vector<uint8_t> data;
+};
+
+// Convert to the registered type (F32, or F16 from F32); false if impossible.
+bool coerce(RawTensor &t, int want);
+
+// sam3_sinusoidal_pe_2d (sam3.cpp:3597-3633): [H][W][d].
+std::vector<float> sinusoidal_pe_2d(int H, int W, int d);
+
+// Device activation buffer able to hold M rows of up to K elements in any
+// format.  The scale planes are stage-major with a row pitch of M rounded up
+// to ROW_PAD and K rounded up to 128 (4 blocks); they are zeroed on the
+// stream that will use the buffer, so blocks past K and rows past M hold zero
+// scales.
+struct ActBuf {
+    void *x = nullptr;
+    uint16_t *d = nullptr, *s = nullptr;
+    int64_t cap_rows = 0, cap_k = 0, mp = 0;
+    hipError_t alloc(int64_t M, int64_t K, hipStream_t st) {
+        cap_rows = M;
+        cap_k = K;
+        mp = round_up(M, ROW_PAD);
+        const size_t sbytes = (size_t)(mp * (round_up(K, 128) / 32) * 2);
+        hipError_t e = hipMalloc(&x, (size_t)(M * K * 4));
+        if (e == hipSuccess) e = hipMalloc(&d, sbytes);
+        if (e == hipSuccess) e = hipMalloc(&s, sbytes);
+        if (e == hipSuccess) e = hipMemsetAsync(d, 0, sbytes, st);
+        if (e == hipSuccess) e = hipMemsetAsync(s, 0, sbytes, st);
+        return e;
+    }
+    void release() {
+        if (x) (void)hipFree(x);
+        if (d) (void)hipFree(d);
+        if (s) (void)hipFree(s);
+        x = nullptr;
+        d = s = nullptr;
+    }
+    Act as(AKind kind, int64_t ld) const {
+        Act a;
+        a.kind = kind;
+        a.x = x;
+        a.d = d;
+        a.s = s;
+        a.ld = ld;
+        a.mp = mp;
+        return a;
+    }
+};
+
+}  // namespace s3e

@@ -18,6 +18,8 @@
 
 #include "s3e_host.h"
 #include "s3e_internal.h"
+#include "s3e_rt.h"
+#include "s3e_hiera.h"
 
 namespace s3e {
 
@@ -55,7 +57,8 @@ struct s3e_weight {
     Weight w;
 };
 
-namespace {
+// ---- host helpers shared with s3e_hiera.cpp (declared in s3e_rt.h) ----
+namespace s3e {
 
 int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
@@ -123,7 +126,7 @@ int upload_weight_split(const float *src, int64_t K, int64_t N, Weight &w, int64
 
 // Repack ggml bytes (N rows of K in `type`) into the GEMM layout and upload.
 int upload_weight(int device, int type, int64_t K, int64_t N, const uint8_t *src, size_t nbytes,
-                  Weight &w, int64_t npad = GEMM_BN) {
+                  Weight &w, int64_t npad) {
     (void)device;
     if (type != S3E_TYPE_F32 && type != S3E_TYPE_F16 && type != S3E_TYPE_Q4_0 && type != S3E_TYPE_Q4_1 &&
         type != S3E_TYPE_Q8_0) {
@@ -207,47 +210,56 @@ int upload_weight(int device, int type, int64_t K, int64_t N, const uint8_t *src
     return S3E_OK;
 }
 
-// Device activation buffer able to hold M rows of up to K elements in any
-// format.  The scale planes are stage-major with a row pitch of M rounded up
-// to ROW_PAD and K rounded up to 128 (4 blocks); they are zeroed on the
-// stream that will use the buffer, so blocks past K and rows past M hold zero
-// scales.
-struct ActBuf {
-    void *x = nullptr;
-    uint16_t *d = nullptr, *s = nullptr;
-    int64_t cap_rows = 0, cap_k = 0, mp = 0;
-    hipError_t alloc(int64_t M, int64_t K, hipStream_t st) {
-        cap_rows = M;
-        cap_k = K;
-        mp = round_up(M, ROW_PAD);
-        const size_t sbytes = (size_t)(mp * (round_up(K, 128) / 32) * 2);
-        hipError_t e = hipMalloc(&x, (size_t)(M * K * 4));
-        if (e == hipSuccess) e = hipMalloc(&d, sbytes);
-        if (e == hipSuccess) e = hipMalloc(&s, sbytes);
-        if (e == hipSuccess) e = hipMemsetAsync(d, 0, sbytes, st);
-        if (e == hipSuccess) e = hipMemsetAsync(s, 0, sbytes, st);
-        return e;
+// Convert file bytes to the type sam3.cpp registers for the tensor
+// (sam3.cpp:2461-2557 registration, :3145-3178 conversion).
+bool coerce(RawTensor &t, int want) {
+    if (t.type == want) return true;
+    int64_t n = t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3];
+    if (want == 0) {
+        std::vector<uint8_t> out((size_t)n * 4);
+        const size_t rs = ggml_rowsize(t.type, t.ne[0]);
+        for (int64_t r = 0; r < n / t.ne[0]; r++)
+            dequantize_row(t.type, t.data.data() + r * rs, (float *)out.data() + r * t.ne[0], t.ne[0]);
+        t.data.swap(out);
+        t.type = 0;
+        return true;
     }
-    void release() {
-        if (x) (void)hipFree(x);
-        if (d) (void)hipFree(d);
-        if (s) (void)hipFree(s);
-        x = nullptr;
-        d = s = nullptr;
+    if (want == 1 && t.type == 0) {
+        std::vector<uint8_t> out((size_t)n * 2);
+        const float *src = (const float *)t.data.data();
+        for (int64_t i = 0; i < n; i++) {
+            const uint16_t h = host_f2h(src[i]);
+            std::memcpy(out.data() + 2 * i, &h, 2);
+        }
+        t.data.swap(out);
+        t.type = 1;
+        return true;
     }
-    Act as(AKind kind, int64_t ld) const {
-        Act a;
-        a.kind = kind;
-        a.x = x;
-        a.d = d;
-        a.s = s;
-        a.ld = ld;
-        a.mp = mp;
-        return a;
-    }
-};
+    return false;
+}
 
-}  // namespace
+// sam3_sinusoidal_pe_2d (sam3.cpp:3597-3633): [H][W][d] with channels
+// [0, d/2) following y and [d/2, d) following x, even channels sin, odd cos.
+std::vector<float> sinusoidal_pe_2d(int H, int W, int d) {
+    const int half = d / 2;
+    const float scale = 2.0f * (float)M_PI;
+    std::vector<float> pe((size_t)d * H * W);
+    for (int y = 0; y < H; ++y)
+        for (int x = 0; x < W; ++x) {
+            const float py = ((float)(y + 1) / (float)H) * scale;
+            const float px = ((float)(x + 1) / (float)W) * scale;
+            float *o = pe.data() + ((size_t)y * W + x) * d;
+            for (int i = 0; i < half; ++i) {
+                const float dim_t = std::pow(10000.0f, (float)(i & ~1) / (float)half);
+                o[i] = (i % 2 == 0) ? std::sin(py / dim_t) : std::cos(py / dim_t);
+                o[i + half] = (i % 2 == 0) ? std::sin(px / dim_t) : std::cos(px / dim_t);
+            }
+        }
+    return pe;
+}
+
+}  // namespace s3e
+// ---- end of shared host helpers ----
 
 // ---------------------------------------------------------------------------
 extern "C" const char *s3e_last_error(void) { return g_err.c_str(); }
@@ -553,6 +565,7 @@ struct s3e_model {
     int necks_present = 0;      // bit 0 trk, bit 1 det
     int32_t neck_dim = 0, visual_only = 1;
     std::vector<void *> owned;  // device f32 arrays
+    HieraModel *hiera = nullptr;  // SAM 2.x files: the Hiera encoder instead of the ViT
 };
 
 namespace {
@@ -566,41 +579,6 @@ int ftype_wtype(int ftype) {
         case 8: return 8;
         default: return -1;
     }
-}
-
-struct RawTensor {
-    int type = 0;
-    int n_dims = 0;
-    int64_t ne[4] = {1, 1, 1, 1};
-    std::vector<uint8_t> data;
-};
-
-// Convert file bytes to the type sam3.cpp registers for the tensor
-// (sam3.cpp:2461-2557 registration, :3145-3178 conversion).
-bool coerce(RawTensor &t, int want) {
-    if (t.type == want) return true;
-    int64_t n = t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3];
-    if (want == 0) {
-        std::vector<uint8_t> out((size_t)n * 4);
-        const size_t rs = ggml_rowsize(t.type, t.ne[0]);
-        for (int64_t r = 0; r < n / t.ne[0]; r++)
-            dequantize_row(t.type, t.data.data() + r * rs, (float *)out.data() + r * t.ne[0], t.ne[0]);
-        t.data.swap(out);
-        t.type = 0;
-        return true;
-    }
-    if (want == 1 && t.type == 0) {
-        std::vector<uint8_t> out((size_t)n * 2);
-        const float *src = (const float *)t.data.data();
-        for (int64_t i = 0; i < n; i++) {
-            const uint16_t h = host_f2h(src[i]);
-            std::memcpy(out.data() + 2 * i, &h, 2);
-        }
-        t.data.swap(out);
-        t.type = 1;
-        return true;
-    }
-    return false;
 }
 
 int upload_f32(s3e_model *m, const RawTensor &t, int64_t expect, float **dst) {
@@ -717,6 +695,7 @@ int check_neck(const s3e_model *m, int which) {
 
 extern "C" void s3e_model_free(s3e_model *m) {
     if (!m) return;
+    if (m->hiera) hiera_free(m->hiera);
     free_weight(m->patch_w);
     for (auto &nk : m->necks)
         for (auto &sc : nk.s) {
@@ -748,7 +727,19 @@ extern "C" int s3e_model_load(s3e_ctx *ctx, const char *path, s3e_model **out) {
         set_error("s3e_model_load: truncated header");
         return S3E_ERR_IO;
     }
-    if (magic != 0x73616D33u) { set_error("s3e_model_load: unknown magic 0x%08x (expected sam3)", magic); return S3E_ERR_IO; }
+    if (magic == 0x73616D32u) {  // "sam2": Hiera backbone + FPN (sam3.cpp:3224-3231)
+        if (version != 1) { set_error("s3e_model_load: unsupported SAM2 version %d", version); return S3E_ERR_IO; }
+        std::unique_ptr<s3e_model, void (*)(s3e_model *)> m2(new s3e_model, s3e_model_free);
+        m2->ctx = ctx;
+        m2->ftype = ftype;
+        const int rc = hiera_load(ctx->device, fin, ftype, n_tensors, &m2->hiera);
+        if (rc != S3E_OK) return rc;
+        m2->img = hiera_img_size(m2->hiera);
+        m2->necks_present = 1;
+        *out = m2.release();
+        return S3E_OK;
+    }
+    if (magic != 0x73616D33u) { set_error("s3e_model_load: unknown magic 0x%08x (expected sam3 or sam2)", magic); return S3E_ERR_IO; }
     if (version != 3) { set_error("s3e_model_load: unsupported SAM3 version %d", version); return S3E_ERR_IO; }
     const int wtype = ftype_wtype(ftype);
     if (wtype < 0) { set_error("s3e_model_load: unsupported ftype %d", ftype); return S3E_ERR_UNSUPPORTED; }
@@ -896,8 +887,19 @@ extern "C" int s3e_model_load(s3e_ctx *ctx, const char *path, s3e_model **out) {
     return S3E_OK;
 }
 
+extern "C" int s3e_model_type(const s3e_model *m) {
+    if (!m) return -1;
+    if (m->hiera) return 2;           // SAM3_MODEL_SAM2
+    return m->necks_present & 2 ? 0   // SAM3_MODEL_SAM3
+                                : 1;  // SAM3_MODEL_SAM3_VISUAL
+}
+
 extern "C" int s3e_model_hparams(const s3e_model *m, int32_t out[16]) {
     if (!m || !out) { set_error("s3e_model_hparams: NULL argument"); return S3E_ERR_INVALID; }
+    if (m->hiera) {
+        hiera_hparams(m->hiera, out);
+        return S3E_OK;
+    }
     std::memset(out, 0, 16 * sizeof(int32_t));
     out[0] = m->img; out[1] = m->patch; out[2] = m->E; out[3] = m->depth; out[4] = m->heads;
     out[5] = m->mlp; out[6] = m->window; out[7] = m->n_global;
@@ -934,6 +936,7 @@ struct s3e_state {
     // the context stream by events
     hipStream_t aux[2] = {nullptr, nullptr};
     hipEvent_t ev_fork = nullptr, ev_join[2] = {nullptr, nullptr};
+    HieraState *hst = nullptr;  // SAM 2.x models
 };
 
 extern "C" void s3e_state_free(s3e_state *st) {
@@ -964,30 +967,11 @@ extern "C" void s3e_state_free(s3e_state *st) {
         if (st->ev_join[i]) (void)hipEventDestroy(st->ev_join[i]);
     }
     if (st->ev_fork) (void)hipEventDestroy(st->ev_fork);
+    if (st->hst) hiera_state_free(st->hst);
     delete st;
 }
 
 namespace {
-
-// sam3_sinusoidal_pe_2d (sam3.cpp:3597-3633): [H][W][d] with channels
-// [0, d/2) following y and [d/2, d) following x, even channels sin, odd cos.
-std::vector<float> sinusoidal_pe_2d(int H, int W, int d) {
-    const int half = d / 2;
-    const float scale = 2.0f * (float)M_PI;
-    std::vector<float> pe((size_t)d * H * W);
-    for (int y = 0; y < H; ++y)
-        for (int x = 0; x < W; ++x) {
-            const float py = ((float)(y + 1) / (float)H) * scale;
-            const float px = ((float)(x + 1) / (float)W) * scale;
-            float *o = pe.data() + ((size_t)y * W + x) * d;
-            for (int i = 0; i < half; ++i) {
-                const float dim_t = std::pow(10000.0f, (float)(i & ~1) / (float)half);
-                o[i] = (i % 2 == 0) ? std::sin(py / dim_t) : std::cos(py / dim_t);
-                o[i + half] = (i % 2 == 0) ? std::sin(px / dim_t) : std::cos(px / dim_t);
-            }
-        }
-    return pe;
-}
 
 // Neck buffers and PEs of a state (sizes from the loaded necks).
 hipError_t alloc_neck(s3e_state *st) {
@@ -1044,6 +1028,17 @@ extern "C" int s3e_state_create(s3e_ctx *ctx, const s3e_model *m, s3e_state **ou
     auto *st = new s3e_state;
     st->ctx = ctx;
     st->m = m;
+    if (m->hiera) {
+        hipError_t e = hipMalloc(&st->chw, (size_t)3 * m->img * m->img * 4);
+        const int rc = e == hipSuccess ? hiera_state_create(m->hiera, ctx->stream, &st->hst) : (int)S3E_ERR_NOMEM;
+        if (rc != S3E_OK) {
+            if (e != hipSuccess) set_error("s3e_state_create: %s", hipGetErrorString(e));
+            s3e_state_free(st);
+            return rc;
+        }
+        *out = st;
+        return S3E_OK;
+    }
     st->T = (int64_t)m->grid * m->grid;
     const int64_t T = st->T, E = m->E;
     hipError_t e = hipMalloc(&st->x, (size_t)(T * E * 4));
@@ -1281,6 +1276,7 @@ hipError_t run_necks(s3e_state *st, const float *x) {
 
 extern "C" int s3e_vit_prefix(s3e_state *st, const float *chw_device, float *x_device) {
     if (!st || !chw_device || !x_device) { set_error("s3e_vit_prefix: NULL argument"); return S3E_ERR_INVALID; }
+    if (st->m->hiera) { set_error("s3e_vit_prefix: the model is a SAM 2 (Hiera) encoder"); return S3E_ERR_INVALID; }
     HIP_TRY(hipSetDevice(st->ctx->device));
     HIP_TRY(run_prefix(st, chw_device, x_device));
     return S3E_OK;
@@ -1288,6 +1284,7 @@ extern "C" int s3e_vit_prefix(s3e_state *st, const float *chw_device, float *x_d
 
 extern "C" int s3e_vit_block(s3e_state *st, int idx, float *x_device) {
     if (!st || !x_device) { set_error("s3e_vit_block: NULL argument"); return S3E_ERR_INVALID; }
+    if (st->m->hiera) { set_error("s3e_vit_block: the model is a SAM 2 (Hiera) encoder"); return S3E_ERR_INVALID; }
     if (idx < 0 || idx >= st->m->depth) { set_error("s3e_vit_block: block %d out of range", idx); return S3E_ERR_INVALID; }
     HIP_TRY(hipSetDevice(st->ctx->device));
     HIP_TRY(run_block(st, idx, x_device));
@@ -1297,6 +1294,10 @@ extern "C" int s3e_vit_block(s3e_state *st, int idx, float *x_device) {
 extern "C" int s3e_encode_chw(s3e_state *st, const float *chw_device) {
     if (!st || !chw_device) { set_error("s3e_encode_chw: NULL argument"); return S3E_ERR_INVALID; }
     HIP_TRY(hipSetDevice(st->ctx->device));
+    if (st->m->hiera) {
+        HIP_TRY(hiera_encode(st->m->hiera, st->hst, chw_device, st->ctx->stream));
+        return S3E_OK;
+    }
     HIP_TRY(run_prefix(st, chw_device, st->x));
     for (int i = 0; i < st->m->depth; i++) HIP_TRY(run_block(st, i, st->x));
     HIP_TRY(run_necks(st, st->x));
@@ -1305,9 +1306,29 @@ extern "C" int s3e_encode_chw(s3e_state *st, const float *chw_device) {
 
 extern "C" int s3e_run_neck(s3e_state *st, const float *x_device) {
     if (!st || !x_device) { set_error("s3e_run_neck: NULL argument"); return S3E_ERR_INVALID; }
-    if (!st->m->necks_present) { set_error("s3e_run_neck: the model has no neck"); return S3E_ERR_INVALID; }
+    if (!st->m->necks_present || st->m->hiera) { set_error("s3e_run_neck: the model has no SimpleFPN neck"); return S3E_ERR_INVALID; }
     HIP_TRY(hipSetDevice(st->ctx->device));
     HIP_TRY(run_necks(st, x_device));
+    return S3E_OK;
+}
+
+extern "C" int s3e_hiera_block(s3e_state *st, int idx, const float *x_device, int H, int W, float *y_device) {
+    if (!st || !x_device || !y_device) { set_error("s3e_hiera_block: NULL argument"); return S3E_ERR_INVALID; }
+    if (!st->m->hiera) { set_error("s3e_hiera_block: the model is not a SAM 2 (Hiera) encoder"); return S3E_ERR_INVALID; }
+    int32_t hp[16];
+    hiera_hparams(st->m->hiera, hp);
+    if (idx < 0 || idx >= hp[3] || H <= 0 || W <= 0 || H > hp[13] || W > hp[13]) {
+        set_error("s3e_hiera_block: block %d on %dx%d is out of range", idx, H, W);
+        return S3E_ERR_INVALID;
+    }
+    HIP_TRY(hipSetDevice(st->ctx->device));
+    const hipError_t e = hiera_block(st->m->hiera, st->hst, idx, x_device, H, W, y_device, st->ctx->stream);
+    if (e == hipErrorInvalidValue) {
+        set_error("s3e_hiera_block: block %d cannot run on a %dx%d input%s (larger than its encoder grid, odd "
+                  "under Q stride, or in place across a size change)", idx, H, W, x_device == y_device ? " in place" : "");
+        return S3E_ERR_INVALID;
+    }
+    HIP_TRY(e);
     return S3E_OK;
 }
 
@@ -1319,7 +1340,9 @@ extern "C" int s3e_encode_chw_host(s3e_state *st, const float *chw_host) {
     return s3e_encode_chw(st, st->chw);
 }
 
-// sam3_resize_bilinear + sam3_preprocess_image (sam3.cpp:3441-3514), on the host.
+// sam3_resize_bilinear + sam3_preprocess_image (sam3.cpp:3441-3514), or for
+// SAM 2 models sam2_preprocess_image's ImageNet mean/std (sam3.cpp:3518-3544),
+// on the host.
 extern "C" int s3e_encode_image_u8(s3e_state *st, const uint8_t *hwc, int width, int height) {
     if (!st || !hwc || width <= 0 || height <= 0) { set_error("s3e_encode_image_u8: bad argument"); return S3E_ERR_INVALID; }
     const int S = st->m->img;
@@ -1351,11 +1374,13 @@ extern "C" int s3e_encode_image_u8(s3e_state *st, const uint8_t *hwc, int width,
         px = resized.data();
     }
     std::vector<float> chw((size_t)3 * S * S);
+    static const float mean2[3] = {0.485f, 0.456f, 0.406f}, std2[3] = {0.229f, 0.224f, 0.225f};
+    const bool sam2 = st->m->hiera != nullptr;
     for (int c = 0; c < 3; ++c)
         for (int y = 0; y < S; ++y)
             for (int x = 0; x < S; ++x) {
                 const float v = px[((size_t)y * S + x) * 3 + c] / 255.0f;
-                chw[(size_t)c * S * S + (size_t)y * S + x] = (v - 0.5f) / 0.5f;
+                chw[(size_t)c * S * S + (size_t)y * S + x] = sam2 ? (v - mean2[c]) / std2[c] : (v - 0.5f) / 0.5f;
             }
     const int rc = s3e_encode_chw_host(st, chw.data());
     if (rc != S3E_OK) return rc;
@@ -1370,6 +1395,7 @@ namespace {
 // does not produce (neck_det_* of a visual-only model) does not resolve.
 const float *find_tensor(const s3e_state *st, const char *name, int64_t ne[4]) {
     const s3e_model *m = st->m;
+    if (m->hiera) return hiera_find_tensor(m->hiera, st->hst, name, ne);
     if (std::strcmp(name, "vit_output") == 0) {
         ne[0] = m->E; ne[1] = m->grid; ne[2] = m->grid; ne[3] = 1;
         return st->x;

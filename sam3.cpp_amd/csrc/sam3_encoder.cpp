@@ -6,7 +6,7 @@
 // (sam3.cpp:3200-3344, :6024-6212, :6997-7008); no exception leaves the
 // library.  The host-side preprocessing is the engine's
 // (s3e_encode_image_u8: sam3_resize_bilinear + sam3_preprocess_image,
-// sam3.cpp:3441-3514).
+// sam3.cpp:3441-3514, or sam2_preprocess_image, :3518-3544, for SAM 2 files).
 #include <cstdio>
 #include <cstring>
 #include <fstream>
@@ -31,7 +31,7 @@ struct sam3_state {
 namespace {
 
 // hparams slots of s3e_model_hparams
-constexpr int HP_IMG = 0, HP_NECKS = 15;
+constexpr int HP_IMG = 0;
 
 bool read_magic(const std::string &path, uint32_t *magic) {
     std::ifstream f(path, std::ios::binary);
@@ -50,9 +50,9 @@ std::shared_ptr<sam3_model> sam3_load_model(const sam3_params &params) {
         fprintf(stderr, "%s: failed to open '%s'\n", __func__, params.model_path.c_str());
         return nullptr;
     }
-    if (magic != 0x73616D33u) {  // "sam3"
-        fprintf(stderr, "%s: '%s' is not a SAM 3 model file (magic 0x%08x); SAM 2 / EdgeTAM encoders are not "
-                        "built\n", __func__, params.model_path.c_str(), magic);
+    if (magic != 0x73616D33u && magic != 0x73616D32u) {  // "sam3", "sam2"
+        fprintf(stderr, "%s: '%s' is not a SAM 3 or SAM 2 model file (magic 0x%08x)\n", __func__,
+                params.model_path.c_str(), magic);
         return nullptr;
     }
     std::shared_ptr<sam3_model> m(new (std::nothrow) sam3_model);
@@ -72,11 +72,13 @@ void sam3_free_model(sam3_model &model) {
     model.ctx = nullptr;
 }
 
-// sam3.cpp:3361-3367: a file without the detector neck is visual-only
-bool sam3_is_visual_only(const sam3_model &model) { return (model.hp[HP_NECKS] & 2) == 0; }
+// sam3.cpp:3361-3367: SAM 2 models, and SAM 3 files without the detector
+// neck, are visual-only
+bool sam3_is_visual_only(const sam3_model &model) { return sam3_get_model_type(model) != SAM3_MODEL_SAM3; }
 
 sam3_model_type sam3_get_model_type(const sam3_model &model) {
-    return sam3_is_visual_only(model) ? SAM3_MODEL_SAM3_VISUAL : SAM3_MODEL_SAM3;
+    const int t = model.enc ? s3e_model_type(model.enc) : 0;
+    return t == 2 ? SAM3_MODEL_SAM2 : (t == 1 ? SAM3_MODEL_SAM3_VISUAL : SAM3_MODEL_SAM3);
 }
 
 void sam3_state_deleter::operator()(sam3_state *p) const { delete p; }

@@ -1,4 +1,4 @@
-// sam3_encode — encode one image with a SAM 3 model file through the sam3.h
+// sam3_encode — encode one image with a SAM 3 or SAM 2 model file through the sam3.h
 // encoder API (include/sam3_encoder.h, libs3e.so) and dump state tensors in
 // sam3_dump_state_tensor's format (<prefix><name>.bin / .shape).
 //
@@ -8,7 +8,9 @@
 // -i takes a binary PPM (P6, maxval 255): RGB bytes in HWC order, which is
 // sam3_image's layout.  -p takes a preprocessed CHW float32 image
 // (sam3_encode_image_from_preprocessed).  Default tensors: vit_output and
-// the tracker levels neck_trk_0..3.  Exit status 0 on success, 1 on failure.
+// the tracker levels neck_trk_0..3 for SAM 3 files; the FPN levels
+// neck_trk_0..2 and the Hiera stage outputs hiera_stage_0..3 for SAM 2
+// files.  Exit status 0 on success, 1 on failure.
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
@@ -67,7 +69,7 @@ int usage() {
 }  // namespace
 
 int main(int argc, char **argv) {
-    std::string model_path, image_path, chw_path, out = "./", tensors = "vit_output,neck_trk_0,neck_trk_1,neck_trk_2,neck_trk_3";
+    std::string model_path, image_path, chw_path, out = "./", tensors;
     int img_size = 0, repeats = 1;
     for (int i = 1; i < argc; i++) {
         const std::string a = argv[i];
@@ -90,8 +92,14 @@ int main(int argc, char **argv) {
     if (!model) return 1;
     auto state = sam3_create_state(*model, params);
     if (!state) return 1;
-    printf("model: %s, visual_only=%d\n", sam3_get_model_type(*model) == SAM3_MODEL_SAM3 ? "SAM3" : "SAM3 visual",
+    const sam3_model_type type = sam3_get_model_type(*model);
+    printf("model: %s, visual_only=%d\n",
+           type == SAM3_MODEL_SAM3 ? "SAM3" : (type == SAM3_MODEL_SAM2 ? "SAM2" : "SAM3 visual"),
            (int)sam3_is_visual_only(*model));
+    if (tensors.empty())
+        tensors = type == SAM3_MODEL_SAM2
+                      ? "neck_trk_0,neck_trk_1,neck_trk_2,hiera_stage_0,hiera_stage_1,hiera_stage_2,hiera_stage_3"
+                      : "vit_output,neck_trk_0,neck_trk_1,neck_trk_2,neck_trk_3";
 
     sam3_image img;
     std::vector<float> chw;

@@ -96,6 +96,8 @@ def _load() -> ctypes.CDLL:
         "s3e_vit_prefix": (c_int, [c_void_p, c_void_p, c_void_p]),
         "s3e_vit_block": (c_int, [c_void_p, c_int, c_void_p]),
         "s3e_run_neck": (c_int, [c_void_p, c_void_p]),
+        "s3e_hiera_block": (c_int, [c_void_p, c_int, c_void_p, c_int, c_int, c_void_p]),
+        "s3e_model_type": (c_int, [c_void_p]),
         "s3e_state_tensor_info": (c_int, [c_void_p, c_char_p, P64]),
         "s3e_state_tensor_get": (c_int, [c_void_p, c_char_p, c_void_p, c_size_t]),
         "s3e_state_tensor_device": (c_void_p, [c_void_p, c_char_p]),
@@ -116,7 +118,8 @@ DECLARED = [
     "s3e_weight_info", "s3e_mul_mat", "s3e_mul_mat_q", "s3e_quantize_rows", "s3e_layer_norm", "s3e_copy",
     "s3e_flash_attn_ext", "s3e_model_load",
     "s3e_model_free", "s3e_model_hparams", "s3e_state_create", "s3e_state_free", "s3e_encode_chw",
-    "s3e_encode_chw_host", "s3e_encode_image_u8", "s3e_vit_prefix", "s3e_vit_block", "s3e_run_neck", "s3e_state_tensor_info",
+    "s3e_encode_chw_host", "s3e_encode_image_u8", "s3e_vit_prefix", "s3e_vit_block", "s3e_run_neck", "s3e_hiera_block", "s3e_model_type",
+    "s3e_state_tensor_info",
     "s3e_state_tensor_get", "s3e_state_tensor_device", "s3e_synth_write", "s3e_synth_write_sam2",
 ]
 
@@ -331,6 +334,8 @@ class Model:
         self.img_size, self.patch, self.E, self.depth = hp[0], hp[1], hp[2], hp[3]
         self.grid = hp[13]
         self.neck_dim, self.necks = hp[14], hp[15]  # necks: bit 0 tracker, bit 1 detector
+        self.model_type = LIB.s3e_model_type(self.handle)  # 0 SAM 3, 1 SAM 3 visual-only, 2 SAM 2
+        self.is_sam2 = self.model_type == 2
 
     def free(self):
         if self.handle:
@@ -372,6 +377,12 @@ class State:
 
     def run_neck(self, x: DeviceBuffer):
         check(LIB.s3e_run_neck(self.handle, x.ptr), "s3e_run_neck")
+
+    def hiera_block(self, idx: int, x, H: int, W: int, y):
+        """Hiera block idx on device rows x ([H·W][dim_in]) into y."""
+        xp = x.ptr if hasattr(x, "ptr") else x
+        yp = y.ptr if hasattr(y, "ptr") else y
+        check(LIB.s3e_hiera_block(self.handle, idx, xp, H, W, yp), "s3e_hiera_block")
 
     def device_view(self, name: str = "vit_output") -> DeviceView:
         ne = (c_int64 * 4)()

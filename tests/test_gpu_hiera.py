@@ -1,0 +1,246 @@
+"""GPU parity of the SAM 2.x Hiera encoder and its FPN (sam2_build_hiera_graph,
+sam3.cpp:4462-4527; sam2_hiera_block_forward, :4295-4457; the FPN neck,
+:4532-4603) against the CPU oracle (oracle/orc_hiera.c).
+
+Models are random-init files in sam3.cpp's SAM 2 format:
+* a small Hiera (width 32, 1 head, stages 1/2/3/2, windows 8/6/4/4, block
+  4 global) at 192 px, whose grids exercise window padding, Q pooling inside
+  windows and at every stage change, a global block and the dimension
+  projection with head dims 32 .. 256;
+* Hiera-T (head dim 96, run as 128 zero-padded) and Hiera-B+ (head dim 56,
+  run as 64; width 112 is not a Q8 block multiple, so the first stage stays
+  F32 in quantized files and its attention output is re-quantized from f32)
+  at 512 px for the per-block and end-to-end tests, and at their real
+  1024 px for the end-to-end test.
+
+Each block runs on the same input as the oracle's block (s3e_hiera_block),
+and the encoder runs end to end from the same image.  Tolerances follow the
+SAM 3 backbone tests: F16 files to the F16 specification (relative L2 ≤
+2e-3); F32 and quantized files within 3× the reference's own noise floor,
+with the specification as the lower bound (F32: relative L2 ≤ 2e-4;
+quantized: relative L2 ≤ 1e-3 and max-abs ≤ 5e-3).
+
+The noise floor is what the reference itself moves by when nothing but fp32
+evaluation order changes.  End to end it is the distance between ggml's two
+dot-product evaluation orders (AVX2 and generic C, both restated in the
+oracle) on the same model and image.  Per block it is the larger of that and
+the block's largest response to four seeded 2e-7 relative (one- to
+two-ulp) perturbations of its input: every GEMM input is re-quantized to Q8 per 32-block and every
+hidden unit goes through ggml's fp16 GELU table, so a last-bit difference
+ahead of a rounding boundary flips a quantum, and a Q-stride block of the
+oracle moves by up to 2.7e-3 relative (8e-2 absolute) under such a
+perturbation — more than the dot-product order alone shows for that block.
+"""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+import oracle_lib as orc
+
+pytestmark = pytest.mark.gpu
+
+orc.LIB.orc_set_variant.argtypes = [ctypes.c_int]
+FLOOR_FACTOR = 3.0
+SMALL = dict(embed_dim=32, num_heads=1, stages=(1, 2, 3, 2), global_idx=(4,), window_spec=(8, 6, 4, 4), bkg=(5, 5))
+
+CASES = [
+    ("small", 192, "f32"), ("small", 192, "q8_0"), ("small", 192, "f16"),
+    ("hiera_t", 512, "q4_0"), ("hiera_t", 512, "q4_1"), ("hiera_t", 512, "q8_0"), ("hiera_t", 512, "f16"),
+    ("hiera_b+", 512, "q4_0"), ("hiera_b+", 512, "f32"),
+]
+
+
+def _variant_gap(fn):
+    """fn() in ggml's AVX2 order, and its distance to the generic-C order."""
+    orc.LIB.orc_set_variant(0)
+    a = fn()
+    orc.LIB.orc_set_variant(1)
+    try:
+        b = fn()
+    finally:
+        orc.LIB.orc_set_variant(0)
+    return a, b
+
+
+def _report(tag, what, got, ref, gap=None):
+    rl, ma = orc.rel_l2(got, ref), orc.max_abs(got, ref)
+    g = "" if gap is None else f" | noise floor rel_l2={gap[0]:.3e} max_abs={gap[1]:.3e}"
+    print(f"{tag} {what}: rel_l2={rl:.3e} max_abs={ma:.3e} |ref|max={np.abs(ref).max():.3f}{g}", flush=True)
+    return rl, ma
+
+
+def _check(ft, rl, ma, gap, what):
+    if ft == "f32":
+        assert rl <= max(2e-4, FLOOR_FACTOR * gap[0]), what
+    elif ft == "f16":
+        assert rl <= 2e-3, what
+    else:
+        assert rl <= max(1e-3, FLOOR_FACTOR * gap[0]), what
+        assert ma <= max(5e-3, FLOOR_FACTOR * gap[1]), what
+
+
+def _write(path, variant, img, ft):
+    import s3e
+
+    over = SMALL if variant == "small" else {}
+    base = "hiera_t" if variant == "small" else variant
+    s3e.synth_write_sam2(path, base, img_size=img, ftype=ft, seed=21, std=0.05, random_affine=True,
+                         neck_dim=64 if variant == "small" else 256, **over)
+
+
+@pytest.fixture(scope="module", params=CASES, ids=lambda c: f"{c[0]}-{c[1]}-{c[2]}")
+def hiera(request, tmpdir_session, ctx):
+    import s3e
+
+    variant, img, ft = request.param
+    path = os.path.join(str(tmpdir_session), f"{variant}_{img}_{ft}.ggml")
+    _write(path, variant, img, ft)
+    om = orc.OracleHiera(path)
+    gm = s3e.Model(ctx, path)
+    st = s3e.State(ctx, gm)
+    yield f"{variant}@{img} {ft}", ft, om, gm, st
+    st.free()
+    gm.free()
+
+
+def test_model_metadata(hiera):
+    tag, ft, om, gm, st = hiera
+    assert gm.model_type == 2 and gm.is_sam2
+    hp = gm.hparams
+    assert hp[0] == om.img and hp[1] == -1 and hp[2] == om.hp.embed_dim and hp[3] == om.nblocks
+    assert hp[13] == om.side[0] and hp[14] == om.hp.neck_dim
+    # levels after scalp = 1: three FPN outputs and their PEs; no ViT output
+    for i in range(3):
+        ne = st.device_view(f"neck_trk_{i}")
+        assert ne.nbytes == 4 * om.side[i] ** 2 * om.hp.neck_dim
+    import s3e
+
+    with pytest.raises(s3e.S3EError):
+        st.device_view("neck_trk_3")
+    with pytest.raises(s3e.S3EError):
+        st.device_view("vit_output")
+
+
+def test_blocks(hiera, ctx):
+    """Every block on the oracle's own input for it."""
+    tag, ft, om, gm, st = hiera
+    rng = np.random.default_rng(9)
+    chw = rng.standard_normal((3, om.img, om.img)).astype(np.float32)
+    x = om.prefix(chw)
+    H = W = om.img // 4
+    print(f"{tag}: {om.nblocks} blocks from a {H}x{W} grid", flush=True)
+    for bi in range(om.nblocks):
+        info = om.block_info(bi)
+        (ref, Ho, Wo), (alt, _, _) = _variant_gap(lambda: om.block(bi, x, H, W))
+        floor = [orc.rel_l2(alt, ref), orc.max_abs(alt, ref)]
+        for seed in range(4):
+            noise = np.random.default_rng(seed).standard_normal(x.shape)
+            yp, _, _ = om.block(bi, (x * (1 + 2e-7 * noise)).astype(np.float32), H, W)
+            floor = [max(floor[0], orc.rel_l2(yp, ref)), max(floor[1], orc.max_abs(yp, ref))]
+        xd = ctx.to_device(x)
+        yd = ctx.buffer(ref.nbytes)
+        print(f"{tag} block {bi} {info} on {H}x{W}", flush=True)
+        st.hiera_block(bi, xd, H, W, yd)
+        ctx.sync()
+        got = yd.download(np.float32, ref.shape)
+        rl, ma = _report(tag, f"block {bi}", got, ref, floor)
+        _check(ft, rl, ma, floor, f"block {bi}")
+        x, H, W = ref, Ho, Wo
+
+
+def test_block_in_place_and_rejections(hiera, ctx):
+    """A same-size block may run in place; a size change in place, a grid
+    larger than the block's and an odd grid under Q stride are refused."""
+    import s3e
+
+    tag, ft, om, gm, st = hiera
+    infos = [om.block_info(i) for i in range(om.nblocks)]
+    same = next(i for i, b in enumerate(infos) if not b["q_stride"] and b["dim_in"] == b["dim_out"])
+    grids, side = [], om.img // 4
+    for b in infos:
+        grids.append(side)
+        side = side // 2 if b["q_stride"] else side
+    G = grids[same]
+    x = np.random.default_rng(2).standard_normal((G * G, infos[same]["dim_in"])).astype(np.float32)
+    ref, _, _ = om.block(same, x, G, G)
+    xd = ctx.to_device(x)
+    yd = ctx.buffer(x.nbytes)
+    st.hiera_block(same, xd, G, G, yd)
+    st.hiera_block(same, xd, G, G, xd)
+    ctx.sync()
+    got = xd.download(np.float32, ref.shape)
+    assert np.array_equal(got, yd.download(np.float32, ref.shape))
+    tol = 2e-4 if ft == "f32" else (2e-3 if ft == "f16" else 1e-3)
+    assert orc.rel_l2(got, ref) <= tol
+    qs = next(i for i, b in enumerate(infos) if b["q_stride"])
+    big = ctx.buffer(4 * (grids[0] + 2) ** 2 * max(b["dim_out"] for b in infos))
+    with pytest.raises(s3e.S3EError):
+        st.hiera_block(qs, big, grids[qs], grids[qs], big)  # in place across a size change
+    with pytest.raises(s3e.S3EError):
+        st.hiera_block(same, big, G + 2, G + 2, big)  # larger than the block's grid
+    with pytest.raises(s3e.S3EError):
+        st.hiera_block(qs, big, grids[qs] - 1, grids[qs] - 1, xd)  # odd grid under Q stride
+    with pytest.raises(s3e.S3EError):
+        st.hiera_block(om.nblocks, big, 2, 2, xd)
+
+
+def _encode_and_compare(tag, ft, om, st, img_hwc):
+    chw = orc.preprocess_sam2(img_hwc, om.img)
+    (levels, stages), (alt_levels, alt_stages) = _variant_gap(lambda: om.encode(chw))
+    st.encode_image_u8(img_hwc)
+    for i, s in enumerate(stages):
+        got = st.tensor(f"hiera_stage_{i}")
+        gap = (orc.rel_l2(alt_stages[i], s), orc.max_abs(alt_stages[i], s))
+        rl, ma = _report(tag, f"hiera_stage_{i}", got, s, gap)
+        _check(ft, rl, ma, gap, f"stage {i}")
+    for i, lv in enumerate(levels):
+        got = st.tensor(f"neck_trk_{i}")
+        assert got.shape == lv.shape
+        gap = (orc.rel_l2(alt_levels[i], lv), orc.max_abs(alt_levels[i], lv))
+        rl, ma = _report(tag, f"neck_trk_{i}", got, lv, gap)
+        _check(ft, rl, ma, gap, f"level {i}")
+        pe = st.tensor(f"neck_trk_pe_{i}")
+        side = om.side[i]
+        ref_pe = orc.sinusoidal_pe_2d(side, side, om.hp.neck_dim).reshape(side * side, -1)
+        assert np.max(np.abs(pe - ref_pe)) <= 1e-6
+        assert np.array_equal(st.tensor(f"pe_{i}"), pe)
+
+
+def test_encode_image(hiera):
+    """End to end from a non-square image (host resize + ImageNet
+    normalisation) to the stage outputs and FPN levels."""
+    tag, ft, om, gm, st = hiera
+    rng = np.random.default_rng(4)
+    img = rng.integers(0, 256, (om.img * 3 // 4, om.img + 40, 3), dtype=np.uint8)
+    _encode_and_compare(tag, ft, om, st, img)
+
+
+def test_encode_is_repeatable(hiera):
+    tag, ft, om, gm, st = hiera
+    img = np.random.default_rng(5).integers(0, 256, (om.img, om.img, 3), dtype=np.uint8)
+    st.encode_image_u8(img)
+    a = [st.tensor(f"neck_trk_{i}") for i in range(3)]
+    st.encode_image_u8(img)
+    for i in range(3):
+        assert np.array_equal(st.tensor(f"neck_trk_{i}"), a[i])
+
+
+@pytest.mark.parametrize("variant,ft", [("hiera_t", "q4_0"), ("hiera_b+", "q4_0"), ("hiera_t", "f16")])
+def test_encode_full_size(variant, ft, tmpdir_session, ctx):
+    """The SAM 2.1 encoders at their real 1024 px size."""
+    import s3e
+
+    path = os.path.join(str(tmpdir_session), f"{variant}_1024_{ft}.ggml")
+    _write(path, variant, 1024, ft)
+    om = orc.OracleHiera(path)
+    gm = s3e.Model(ctx, path)
+    st = s3e.State(ctx, gm)
+    try:
+        img = np.random.default_rng(6).integers(0, 256, (1024, 1024, 3), dtype=np.uint8)
+        print(f"{variant}@1024 {ft}: encode", flush=True)
+        _encode_and_compare(f"{variant}@1024 {ft}", ft, om, st, img)
+    finally:
+        st.free()
+        gm.free()

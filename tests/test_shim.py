@@ -48,10 +48,10 @@ def test_example_fails_like_sam3_load_model(tmp_path):
     r = subprocess.run([EXE, "-m", str(tmp_path / "missing.ggml"), "-i", "x.ppm", "-o", str(tmp_path)],
                        capture_output=True, text=True)
     assert r.returncode == 1 and "failed to open" in r.stderr
-    bad = tmp_path / "sam2.ggml"
-    bad.write_bytes(b"2mas" + b"\0" * 64)
+    bad = tmp_path / "other.ggml"
+    bad.write_bytes(b"ggjt" + b"\0" * 64)
     r = subprocess.run([EXE, "-m", str(bad), "-i", "x.ppm", "-o", str(tmp_path)], capture_output=True, text=True)
-    assert r.returncode == 1 and "not a SAM 3 model file" in r.stderr
+    assert r.returncode == 1 and "not a SAM 3 or SAM 2 model file" in r.stderr
     r = subprocess.run([EXE], capture_output=True, text=True)
     assert r.returncode == 1 and "usage" in r.stderr
 
@@ -129,3 +129,45 @@ def test_example_encode_matches_oracle(tmp_path, s3e_lib):
     r = subprocess.run([EXE, "-m", path, "-p", str(tmp_path / "img.chw.f32"), "-s", "224", "-o", out2],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 1
+
+
+@pytest.mark.gpu
+def test_example_encode_sam2_matches_oracle(tmp_path, s3e_lib):
+    """The same program on a SAM 2 file (Hiera-T at 512 px): model type SAM2,
+    visual-only, and the default dumps (three FPN levels after scalp, four
+    stage outputs) equal to the oracle's to the quantized specification."""
+    import ctypes
+
+    path = str(tmp_path / "h.ggml")
+    s3e_lib.synth_write_sam2(path, "hiera_t", img_size=512, ftype="q4_0", seed=23, std=0.05, random_affine=True)
+    img = np.random.default_rng(10).integers(0, 256, (300, 500, 3), dtype=np.uint8)
+    _write_ppm(str(tmp_path / "img.ppm"), img)
+    out = str(tmp_path / "h_")
+    print("sam3_encode (SAM 2) on a 500x300 PPM", flush=True)
+    r = subprocess.run([EXE, "-m", path, "-i", str(tmp_path / "img.ppm"), "-o", out],
+                       capture_output=True, text=True, timeout=120)
+    print(r.stdout, r.stderr[-2000:], flush=True)
+    assert r.returncode == 0
+    assert "model: SAM2, visual_only=1" in r.stdout
+    om = orc.OracleHiera(path)
+    chw = orc.preprocess_sam2(img, 512)
+    orc.LIB.orc_set_variant.argtypes = [ctypes.c_int]
+    refs = []
+    for variant in (0, 1):
+        orc.LIB.orc_set_variant(variant)
+        try:
+            levels, stages = om.encode(chw)
+            refs.append(levels + stages)
+        finally:
+            orc.LIB.orc_set_variant(0)
+    names = [f"neck_trk_{i}" for i in range(3)] + [f"hiera_stage_{i}" for i in range(4)]
+    shapes = [[256, s, s] for s in (128, 64, 32)] + [[96 << i, 128 >> i, 128 >> i] for i in range(4)]
+    for k, (name, shp) in enumerate(zip(names, shapes)):
+        shape, got = _read_dump(out + name)
+        assert shape == shp, name
+        ref = refs[0][k].ravel()
+        gap = orc.rel_l2(refs[1][k], refs[0][k])
+        gma = orc.max_abs(refs[1][k], refs[0][k])
+        rl, ma = orc.rel_l2(got, ref), orc.max_abs(got, ref)
+        print(f"{name}: rel_l2={rl:.3e} max_abs={ma:.3e} (ggml order gap {gap:.2e}/{gma:.2e})", flush=True)
+        assert rl <= max(1e-3, 3.0 * gap) and ma <= max(5e-3, 3.0 * gma), name
