@@ -120,11 +120,11 @@ def gemm_roofline(s3e, ctx, ev, ftype: str, reps: int):
     return ms, tops, ops
 
 
-def sam2_encoders(s3e, ctx, ev, steps: int, warmup: int) -> dict:
+def sam2_encoders(s3e, ctx, ev, steps: int, warmup: int, runs=SAM2_RUNS) -> dict:
     """ms/frame of the SAM 2.1 Hiera encoders at 1024² (input resident in HBM)."""
     res = {}
     tmpdir = os.environ.get("TMPDIR", tempfile.gettempdir())
-    for variant, ft in SAM2_RUNS:
+    for variant, ft in runs:
         path = os.path.join(tmpdir, f"s3e_bench_{variant}_{ft}.ggml")
         s3e.synth_write_sam2(path, variant, img_size=1024, ftype=ft, seed=0, std=0.02)
         model = s3e.Model(ctx, path)
@@ -250,6 +250,7 @@ def main() -> int:
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "gemm_fc1_q4_0_counters.txt"))
     ap.add_argument("--only", choices=["encode", "gemm", "copy", "neck", "sam2"], default=None,
                     help="run one leg only (for profiling runs)")
+    ap.add_argument("--sam2-run", default=None, help="with --only sam2: one encoder, e.g. hiera_t:f16")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (every run here uses one "
@@ -277,7 +278,8 @@ def main() -> int:
         return 0
 
     if args.only == "sam2":
-        sam2_encoders(s3e, ctx, ev, args.steps, args.warmup)
+        runs = [tuple(args.sam2_run.split(":"))] if args.sam2_run else SAM2_RUNS
+        sam2_encoders(s3e, ctx, ev, args.steps, args.warmup, runs)
         return 0
 
     if args.only in (None, "gemm"):
