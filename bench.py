@@ -20,6 +20,10 @@ Also reported, on the same JSON line:
                   int8 MFMA peak (fp16 for F16 weights, fp32 for F32).
                   `traffic` comes from the committed rocprofv3 FETCH_SIZE /
                   WRITE_SIZE counter summary when present.
+  small_m       — weight streaming at M = 64 rows (the C2 small-M shapes):
+                  fc1 and fc2 alone, and all four ViT linears of 64 distinct
+                  layers in one batched launch, as algorithmic GB/s against
+                  the 8 TB/s HBM peak.
   sam2_encoders — the SAM 2.1 Hiera encoders (backbone + FPN to 256-ch
                   levels at 256², 128², 64²) at 1024×1024 on the same kind of
                   input: Hiera-Tiny with F16 weights and Hiera-Base+ with
@@ -118,6 +122,82 @@ def gemm_roofline(s3e, ctx, ev, ftype: str, reps: int):
     ops = 2.0 * M * N * K
     tops = ops / (ms * 1e-3) / 1e12
     return ms, tops, ops
+
+
+BPW = {"q4_0": 18 / 32, "q4_1": 20 / 32, "q8_0": 34 / 32, "f16": 2.0}
+VIT_LINEARS = [(3072, 1024), (1024, 1024), (4736, 1024), (1024, 4736)]  # qkv, proj, fc1, fc2 (N, K)
+
+
+def small_m(s3e, ctx, ev, ftype: str, reps: int = 10) -> dict:
+    """Weight streaming at M = 64 rows: fc1 and fc2 alone (s3e_mul_mat_q), and
+    the four ViT linears of enough distinct layers for ≈ 500 MB of weights in
+    one batched launch (s3e_mul_mat_q_batch; 64 layers of Q4_0), twice the
+    256 MB Infinity Cache, so every run streams from HBM.  Algorithmic bytes
+    per product N·K·bpw + 4·M·K + 4·M·N (ggml bytes per weight, f32 in and
+    out)."""
+    M = 64
+    per_layer = sum(N * K for N, K in VIT_LINEARS) * BPW[ftype]
+    layers = max(8, int(round(500e6 / per_layer)))
+    tmap = {"q4_0": s3e.TYPE_Q4_0, "q4_1": s3e.TYPE_Q4_1, "q8_0": s3e.TYPE_Q8_0, "f16": s3e.TYPE_F16}
+    wt = tmap[ftype]
+    vdt = s3e.TYPE_F16 if wt == s3e.TYPE_F16 else (s3e.TYPE_Q8_1 if wt == s3e.TYPE_Q4_1 else s3e.TYPE_Q8_0)
+    rng = np.random.default_rng(2)
+    acts = {}
+    for K in (1024, 4736):
+        Xd = ctx.to_device(rng.standard_normal((M, K)).astype(np.float32))
+        ns = s3e.act_scale_elems(M, K)
+        q, d, sx = ctx.buffer(M * K * 2), ctx.buffer(ns * 2), ctx.buffer(ns * 2)
+        ctx.quantize_rows(vdt, Xd, M, K, q, None if wt == s3e.TYPE_F16 else d, None if wt == s3e.TYPE_F16 else sx)
+        acts[K] = (q, None if wt == s3e.TYPE_F16 else d, sx if wt == s3e.TYPE_Q4_1 else None)
+
+    def nbytes(N, K):
+        return N * K * BPW[ftype] + 4 * M * K + 4 * M * N
+
+    res = {"rows": M, "weights": ftype}
+    e0, e1 = ev.create(), ev.create()
+    for name, (N, K) in (("fc1", VIT_LINEARS[2]), ("fc2", VIT_LINEARS[3])):
+        w = ctx.weight(wt, K, N, _random_ggml_bytes(wt, N, K, rng))
+        Y = ctx.buffer(M * N * 4)
+        for _ in range(3):
+            ctx.mul_mat_q(w, *acts[K], M, Y)
+        ctx.sync()
+        ev.record(e0, ctx.stream)
+        for _ in range(50):
+            ctx.mul_mat_q(w, *acts[K], M, Y)
+        ev.record(e1, ctx.stream)
+        us = ev.elapsed_ms(e0, e1) / 50 * 1e3
+        ctx.sync()
+        res[f"{name}_us"] = round(us, 2)
+        res[f"{name}_GBps"] = round(nbytes(N, K) / (us * 1e-6) / 1e9, 1)
+        w.free()
+    ws, xs, ds, ss, ys = [], [], [], [], []
+    total = 0.0
+    for _ in range(layers):
+        for N, K in VIT_LINEARS:
+            ws.append(ctx.weight(wt, K, N, _random_ggml_bytes(wt, N, K, rng)))
+            q, d, sx = acts[K]
+            xs.append(q)
+            ds.append(d)
+            ss.append(sx)
+            ys.append(ctx.buffer(M * N * 4))
+            total += nbytes(N, K)
+    for _ in range(2):
+        ctx.mul_mat_q_batch(ws, xs, ds, ss, M, None, ys)
+    ctx.sync()
+    ev.record(e0, ctx.stream)
+    for _ in range(reps):
+        ctx.mul_mat_q_batch(ws, xs, ds, ss, M, None, ys)
+    ev.record(e1, ctx.stream)
+    us = ev.elapsed_ms(e0, e1) / reps * 1e3
+    ctx.sync()
+    gbps = total / (us * 1e-6) / 1e9
+    res["sweep"] = {"products": len(ws), "layers": layers, "bytes": int(total), "us": round(us, 1),
+                    "GBps": round(gbps, 1), "frac_hbm": round(gbps / 8000.0, 4)}
+    for w in ws:
+        w.free()
+    log(f"small-M {ftype}: fc1 {res['fc1_us']} us ({res['fc1_GBps']} GB/s), fc2 {res['fc2_us']} us "
+        f"({res['fc2_GBps']} GB/s); {len(ws)}-product sweep {total / 1e6:.0f} MB in {us:.1f} us = {gbps:.0f} GB/s")
+    return res
 
 
 def sam2_encoders(s3e, ctx, ev, steps: int, warmup: int, runs=SAM2_RUNS) -> dict:
@@ -248,7 +328,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "gemm_fc1_q4_0_counters.txt"))
-    ap.add_argument("--only", choices=["encode", "gemm", "copy", "neck", "sam2"], default=None,
+    ap.add_argument("--only", choices=["encode", "gemm", "copy", "neck", "sam2", "small_m"], default=None,
                     help="run one leg only (for profiling runs)")
     ap.add_argument("--sam2-run", default=None, help="with --only sam2: one encoder, e.g. hiera_t:f16")
     args = ap.parse_args()
@@ -275,6 +355,11 @@ def main() -> int:
         ev.record(e1, ctx.stream)
         ms = ev.elapsed_ms(e0, e1) / 10
         log(f"copy 1 GiB: {ms:.3f} ms = {2 * nbytes / ms / 1e6:.1f} GB/s (read+write)")
+        return 0
+
+    if args.only == "small_m":
+        for ft in ("q4_0", "q8_0", "q4_1", "f16"):
+            small_m(s3e, ctx, ev, ft)
         return 0
 
     if args.only == "sam2":
@@ -329,6 +414,7 @@ def main() -> int:
         return 0
 
     sam2 = sam2_encoders(s3e, ctx, ev, max(3, args.steps // 2), 2)
+    sm = small_m(s3e, ctx, ev, args.ftype) if args.ftype in BPW else None
 
     gms, gtops, gops = out["gemm"]
     peak = PEAK_TOPS[args.ftype]
@@ -366,6 +452,7 @@ def main() -> int:
                    "global_blocks": [7, 15, 23, 31], "neck_levels": [288, 144, 72, 36]},
         "breakdown": {"neck_ms": round(neck_ms, 3), "backbone_ms": round(ms_frame - neck_ms, 3)},
         "sam2_encoders": sam2,
+        "small_m": sm,
         "roofline": {"kernel": f"{GEMM_KERNEL} fc1 M=5184 N=4736 K=1024 ({args.ftype})", "bound": "mfma",
                      "achieved": round(gtops, 1), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(gtops / peak, 4), "traffic": traffic,

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define S3E_ABI_VERSION 3
+#define S3E_ABI_VERSION 4
 
 enum s3e_status {
     S3E_OK = 0,
@@ -104,10 +104,25 @@ int s3e_mul_mat(s3e_ctx *ctx, const s3e_weight *w, const float *X, int64_t M,
 /* Same GEMM with X already in W's vec_dot type (ggml_mul_mat with src1 of
  * that type; ggml skips the conversion then): `xq`, `d`, `s` as written by
  * s3e_quantize_rows for K = W's ne0 (layout there).  Launches the GEMM kernel
- * only, with no allocation, so it is also the entry point to time the kernel
- * alone. */
+ * only, so it is also the entry point to time the kernel alone.  Products of
+ * at most 64 rows with Q4_0/Q4_1/Q8_0/F16 weights run on the weight-streaming
+ * kernel, whose block-interleaved copy of the weight is made (allocated and
+ * packed on the device) by the first such call on that weight; every other
+ * call allocates nothing. */
 int s3e_mul_mat_q(s3e_ctx *ctx, const s3e_weight *w, const void *xq, const uint16_t *d,
                   const uint16_t *s, int64_t M, const float *bias, float *Y);
+/* Several independent products of one graph level in one launch: Y[i] =
+ * ggml_add(ggml_mul_mat(W[i], X[i]), bias[i]) for i < n, each as in
+ * s3e_mul_mat_q (activations already in the weight's vec_dot format, device
+ * pointers), all weights of one type among Q4_0/Q4_1/Q8_0/F16 and
+ * 1 <= M <= 64 rows shared by the products.  ggml evaluates such nodes one
+ * by one (ggml_backend_graph_compute over the graph, sam3.cpp:1015-1026);
+ * there is no single reference entry point: at a few rows each product is a
+ * weight stream too short to fill the GPU, and one launch streams them
+ * together.  bias may be NULL, or hold NULL entries. */
+int s3e_mul_mat_q_batch(s3e_ctx *ctx, int n, const s3e_weight *const *w, const void *const *xq,
+                        const uint16_t *const *d, const uint16_t *const *s, int64_t M,
+                        const float *const *bias, float *const *Y);
 
 /* Convert M rows of K f32 (device) into a vec_dot type, as ggml's
  * from_float does for src1 of ggml_mul_mat: `type` is Q8_0, Q8_1 or F16.

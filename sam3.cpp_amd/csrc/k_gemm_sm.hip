@@ -1,0 +1,295 @@
+// k_gemm_sm.hip — small-M products Y[M][N] = X[M][K] · W[N][K]ᵀ for M ≤ 64
+// (ggml_mul_mat at a few rows: the weight-streaming regime), one or many
+// independent products per launch.
+//
+// At 64 rows each weight byte feeds at most 64 multiply-adds, so the product
+// is bound by streaming the weights from HBM, not by MFMA.  The kernel
+// therefore reads the weights once, at their ggml size (Q4 as nibbles, 18 or
+// 20 bytes per 32 weights with the scales), from a block-interleaved copy
+// made on the device at first use:
+//     block b of column n at  (b·Np + n)·BB   (BB = 16 / 32 / 64 bytes for
+//                                              Q4_* nibbles / Q8_0 / F16)
+// so that the 32 columns of a wave read 32 consecutive chunks of a block.
+// Nibble j of a Q4 chunk is ggml's: byte j holds element j (low) and
+// element j + 16 (high).  Scales stay in the engine's stage-major planes.
+//
+// Work: a wave owns a strip of 32 columns and a range of the K stages (4
+// blocks each).  A work-group's 4 waves cover 4/KS adjacent strips × KS
+// K ranges (KS = 4 is built: four waves share one strip's K range, which
+// keeps each wave's dependent chain short; a whole strip per wave measured
+// no faster and needs more registers); split partial sums are added in LDS
+// in a fixed order (deterministic).  The next stage is loaded while one is
+// consumed.  Per 32-element block and 32-row tile
+// the arithmetic is the large-M kernel's: the exact integer block sum on
+// v_mfma_i32_32x32x32_i8 (the Q4_0 offset −8 applied by a second MFMA against
+// a constant −8 operand, so the nibbles need only a mask or a shift), the
+// exact scale product 2·dx·dw on a one-hot v_mfma_f32_32x32x16_f16, and
+// acc += float(S)·c on the VALU; Q4_1 adds Σ m_w·s_x per stage on fp16 MFMA.
+// F16 weights run on v_mfma_f32_32x32x16_f16 directly.
+#include "s3e_internal.h"
+
+namespace s3e {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+constexpr int SM_WAVES = 4;
+
+template <int WK>
+struct SmCfg {
+    static constexpr bool quant = WK != WK_F16;
+    static constexpr bool q4 = WK == WK_Q4_0 || WK == WK_Q4_1;
+    static constexpr bool q41 = WK == WK_Q4_1;
+    static constexpr int BB = q4 ? 16 : (WK == WK_Q8_0 ? 32 : 64);  // bytes per column per block
+    static constexpr int WL = WK == WK_F16 ? 8 : 4;                  // 16-byte weight loads per stage per lane
+};
+
+// Operands of one stage (4 blocks) for MT row tiles.
+template <int WK, int MT>
+struct SmStage {
+    uint4 w[SmCfg<WK>::WL];
+    uint2 wd, wm;
+    uint4 a[MT][SmCfg<WK>::WL];
+    uint2 ad[MT], as[MT];
+};
+
+template <int WK, int MT, int KS>
+__global__ __launch_bounds__(64 * SM_WAVES, 2) void k_gemm_sm(SmArgs p) {
+    using C = SmCfg<WK>;
+    constexpr int SPW = SM_WAVES / KS;  // strips per work-group
+    __shared__ float red[KS > 1 ? SM_WAVES : 1][MT * 32][33];
+
+    const int wg = blockIdx.x;
+    const SmGemm G = p.many ? p.many[p.wg_gemm[wg]] : p.one;
+    const int t = threadIdx.x, lane = t & 63, lr = lane & 31, lh = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int ls = wave / KS, kr = wave % KS;
+    const int n0 = ((wg - G.wg0) * SPW + ls) * 32;
+    const int n = n0 + lr;  // < Np: weights are padded to whole 128-column groups
+    const bool live = n0 < G.N;
+    const int s0 = G.nst * kr / KS, s1 = live ? G.nst * (kr + 1) / KS : s0;
+    const int M = p.M;
+
+    int rows[MT];
+#pragma unroll
+    for (int i = 0; i < MT; i++) rows[i] = min(32 * i + lr, M - 1);
+
+    auto load = [&](int s, SmStage<WK, MT> &f) {
+        const int b0 = 4 * s;
+#pragma unroll
+        for (int j = 0; j < C::WL; j++) {
+            // Q4: block j (both lane halves read the same 16 bytes); Q8_0: block j,
+            // half lh; F16: block j / 2, slab j % 2, half lh
+            const int blk = C::q4 ? b0 + j : (WK == WK_Q8_0 ? b0 + j : b0 + j / 2);
+            const int sub = C::q4 ? 0 : (WK == WK_Q8_0 ? lh : 2 * (j & 1) + lh);
+            f.w[j] = *(const uint4 *)(G.w + ((int64_t)blk * G.np + n) * C::BB + sub * 16);
+        }
+        if constexpr (C::quant) {
+            f.wd = *(const uint2 *)(G.wd + ((int64_t)s * G.np + n) * 4);
+            if constexpr (C::q41) f.wm = *(const uint2 *)(G.wm + ((int64_t)s * G.np + n) * 4);
+        }
+#pragma unroll
+        for (int i = 0; i < MT; i++) {
+            if constexpr (C::quant) {
+                const int8_t *xr = (const int8_t *)G.x + (int64_t)rows[i] * G.ldx;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int k = min((b0 + j) * 32 + lh * 16, G.K - 16);
+                    f.a[i][j] = *(const uint4 *)(xr + k);
+                }
+                f.ad[i] = *(const uint2 *)(G.xd + ((int64_t)s * G.xmp + rows[i]) * 4);
+                if constexpr (C::q41) f.as[i] = *(const uint2 *)(G.xs + ((int64_t)s * G.xmp + rows[i]) * 4);
+            } else {
+                const _Float16 *xr = (const _Float16 *)G.x + (int64_t)rows[i] * G.ldx;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const int k = min((b0 + j / 2) * 32 + (j & 1) * 16 + lh * 8, G.K - 8);
+                    f.a[i][j] = *(const uint4 *)(xr + k);
+                }
+            }
+        }
+    };
+
+    v16f acc[MT];  // Q4_1: the minimum term accumulates here too
+#pragma unroll
+    for (int i = 0; i < MT; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[i][r] = 0.f;
+
+    auto compute = [&](const SmStage<WK, MT> &f) {
+        if constexpr (C::quant) {
+            const v16i zi = {};
+            const v16f zf = {};
+            const v4i minus8 = {(int)0xF8F8F8F8, (int)0xF8F8F8F8, (int)0xF8F8F8F8, (int)0xF8F8F8F8};
+            const uint32_t wdw[2] = {f.wd.x, f.wd.y};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                v4i b;
+                if constexpr (C::q4) {
+                    const int sh = 4 * lh;  // low nibbles: elements 0..15, high: 16..31
+                    b[0] = (int)((f.w[j].x >> sh) & 0x0F0F0F0Fu);
+                    b[1] = (int)((f.w[j].y >> sh) & 0x0F0F0F0Fu);
+                    b[2] = (int)((f.w[j].z >> sh) & 0x0F0F0F0Fu);
+                    b[3] = (int)((f.w[j].w >> sh) & 0x0F0F0F0Fu);
+                } else {
+                    b = __builtin_bit_cast(v4i, f.w[j]);
+                }
+                const uint32_t hw = (wdw[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
+                const v4u hb = {hw, 0u, 0u, 0u};
+#pragma unroll
+                for (int i = 0; i < MT; i++) {
+                    const v4i a = __builtin_bit_cast(v4i, f.a[i][j]);
+                    v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, zi, 0, 0, 0);
+                    if constexpr (WK == WK_Q4_0) S = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, minus8, S, 0, 0, 0);
+                    const uint32_t adw[2] = {f.ad[i].x, f.ad[i].y};
+                    const uint32_t ha_ = (adw[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
+                    const v4u ha = {ha_, 0u, 0u, 0u};
+                    const v16f Cs = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, ha),
+                                                                          __builtin_bit_cast(v8h, hb), zf, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 16; r++) acc[i][r] = __builtin_fmaf((float)S[r], Cs[r], acc[i][r]);
+                }
+            }
+            if constexpr (C::q41) {
+                const v4u hb = {f.wm.x, f.wm.y, 0u, 0u};
+#pragma unroll
+                for (int i = 0; i < MT; i++) {
+                    const v4u ha = {f.as[i].x, f.as[i].y, 0u, 0u};
+                    acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, ha),
+                                                                    __builtin_bit_cast(v8h, hb), acc[i], 0, 0, 0);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const v8h b = __builtin_bit_cast(v8h, f.w[j]);
+#pragma unroll
+                for (int i = 0; i < MT; i++)
+                    acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, f.a[i][j]), b, acc[i], 0,
+                                                                    0, 0);
+            }
+        }
+    };
+
+    // stage s + 1 is in flight while stage s is consumed
+    if (s0 < s1) {
+        SmStage<WK, MT> cur, nxt;
+        load(s0, cur);
+        for (int s = s0; s < s1; s++) {
+            const bool more = s + 1 < s1;
+            if (more) load(s + 1, nxt);
+            compute(cur);
+            if (more) cur = nxt;
+        }
+    }
+
+    constexpr float kScale = C::quant ? 0.5f : 1.0f;  // the scale products are doubled
+    if constexpr (KS == 1) {
+        if (!live) return;
+        const int gn = n0 + lr;
+        const float bv = (G.bias && gn < G.N) ? G.bias[gn] : 0.f;
+#pragma unroll
+        for (int i = 0; i < MT; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int row = 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
+                if (row < M && gn < G.N) G.y[(int64_t)row * G.ldy + gn] = acc[i][r] * kScale + bv;
+            }
+    } else {
+        // partial sums of the KS K ranges of each strip → LDS → fixed-order sum
+#pragma unroll
+        for (int i = 0; i < MT; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                red[wave][32 * i + 8 * (r >> 2) + 4 * lh + (r & 3)][lr] = acc[i][r];
+        __syncthreads();
+        for (int o = t; o < SPW * MT * 32 * 32; o += 64 * SM_WAVES) {
+            const int st = o / (MT * 32 * 32), row = (o >> 5) % (MT * 32), col = o & 31;
+            const int gn = ((wg - G.wg0) * SPW + st) * 32 + col;
+            if (row >= M || gn >= G.N) continue;
+            float v = red[st * KS][row][col];
+#pragma unroll
+            for (int w = 1; w < KS; w++) v += red[st * KS + w][row][col];
+            v *= kScale;
+            if (G.bias) v += G.bias[gn];
+            G.y[(int64_t)row * G.ldy + gn] = v;
+        }
+    }
+}
+
+// Block-interleaved copy for the small-M kernel from the large-M layout
+// ([Np][Kp] codes, Q4_0 stored as nibble − 8).  One thread per (block, column).
+__global__ void k_pack_sm(const uint8_t *__restrict__ q, int64_t kp, int64_t np, int64_t kb, int wk,
+                          uint8_t *__restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= kb * np) return;
+    const int64_t b = i / np, nn = i % np;
+    if (wk == WK_Q4_0 || wk == WK_Q4_1) {
+        const int8_t *src = (const int8_t *)q + nn * kp + b * 32;
+        const int off = wk == WK_Q4_0 ? 8 : 0;
+        uint32_t w[4];
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+            uint32_t v = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int j = 4 * d + e;
+                const uint32_t lo = (uint32_t)(src[j] + off) & 15u, hi = (uint32_t)(src[j + 16] + off) & 15u;
+                v |= (lo | (hi << 4)) << (8 * e);
+            }
+            w[d] = v;
+        }
+        *(uint4 *)(out + i * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+        const int bb = wk == WK_Q8_0 ? 32 : 64;
+        const uint4 *src = (const uint4 *)(q + (nn * kp + b * 32) * (bb / 32));
+        uint4 *dst = (uint4 *)(out + i * bb);
+        for (int c = 0; c < bb / 16; c++) dst[c] = src[c];
+    }
+}
+
+}  // namespace
+
+int64_t sm_weight_bytes(const Weight &w) {
+    const int64_t kb4 = (w.Kp + 127) / 128 * 4;
+    const int bb = (w.kind == WK_Q4_0 || w.kind == WK_Q4_1) ? 16 : (w.kind == WK_Q8_0 ? 32 : 64);
+    return kb4 * w.Np * bb;
+}
+
+hipError_t launch_pack_sm(const Weight &w, void *out, hipStream_t st) {
+    if (w.kind != WK_Q4_0 && w.kind != WK_Q4_1 && w.kind != WK_Q8_0 && w.kind != WK_F16) return hipErrorInvalidValue;
+    hipError_t e = hipMemsetAsync(out, 0, (size_t)sm_weight_bytes(w), st);
+    if (e != hipSuccess) return e;
+    const int64_t kb = w.Kp / 32, total = kb * w.Np;
+    hipLaunchKernelGGL(k_pack_sm, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, (const uint8_t *)w.q, w.Kp,
+                       w.Np, kb, (int)w.kind, (uint8_t *)out);
+    return hipGetLastError();
+}
+
+int sm_wgs(int64_t N, int ks) { return (int)(((N + 31) / 32 + SM_WAVES / ks - 1) / (SM_WAVES / ks)); }
+
+hipError_t launch_gemm_sm(WKind kind, const SmArgs &a, int wgs, int ks, hipStream_t st) {
+    if (a.M <= 0 || a.M > 64 || wgs <= 0 || ks != 4 || (a.many && !a.wg_gemm)) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)wgs), block(64 * SM_WAVES);
+    const bool two = a.M > 32;
+#define S3E_SM(WK)                                                                                       \
+    do {                                                                                                 \
+        if (two) hipLaunchKernelGGL((k_gemm_sm<WK, 2, 4>), grid, block, 0, st, a);                       \
+        else hipLaunchKernelGGL((k_gemm_sm<WK, 1, 4>), grid, block, 0, st, a);                           \
+    } while (0)
+    switch (kind) {
+        case WK_Q4_0: S3E_SM(WK_Q4_0); break;
+        case WK_Q4_1: S3E_SM(WK_Q4_1); break;
+        case WK_Q8_0: S3E_SM(WK_Q8_0); break;
+        case WK_F16: S3E_SM(WK_F16); break;
+        default: return hipErrorInvalidValue;
+    }
+#undef S3E_SM
+    return hipGetLastError();
+}
+
+}  // namespace s3e

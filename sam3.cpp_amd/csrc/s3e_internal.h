@@ -167,9 +167,41 @@ struct AttnArgs {
     Act out;                       // A_Q8_0 / A_Q8_1 / A_F16 / A_F32, row = token, col = h*64 + d
 };
 
+// One product of a small-M launch (k_gemm_sm.hip): weights in the
+// block-interleaved copy (block b of column n at (b·np + n)·BB bytes, BB =
+// 16 / 32 / 64 for Q4 nibbles / Q8_0 / F16) with the usual stage-major scale
+// planes; activations in the weight's vec_dot format.  Work-group w works on
+// column group w − wg0 of this product (sm_wgs: 32-column strips, 4 / ks of
+// them per work-group).
+struct SmGemm {
+    const uint8_t *w = nullptr;
+    const uint16_t *wd = nullptr, *wm = nullptr;
+    const void *x = nullptr;
+    const uint16_t *xd = nullptr, *xs = nullptr;
+    const float *bias = nullptr;
+    float *y = nullptr;
+    int64_t ldx = 0, ldy = 0, xmp = 0, np = 0;
+    int K = 0, N = 0, nst = 0;   // nst: stages of 4 blocks (Kp rounded up to 128, over 128)
+    int wg0 = 0;                 // first work-group of this product
+};
+struct SmArgs {
+    SmGemm one;                  // used when many == nullptr
+    const SmGemm *many = nullptr;  // device array of n products
+    const uint16_t *wg_gemm = nullptr;  // device: product index of each work-group (with many)
+    int n = 1;
+    int M = 0;                   // rows, 1..64, shared by the products
+};
+
 // ---- kernel launchers (k_*.hip) ----
 hipError_t launch_gemm(const Weight &w, const Act &a, int64_t M, Epi epi, const EpiArgs &ea,
                        hipStream_t st);
+// Small-M products (k_gemm_sm.hip): Q4_0 / Q4_1 / Q8_0 / F16 weights, M ≤ 64.
+// ks = 4 (four waves split the K range of one 32-column strip); wgs = total
+// of sm_wgs(N, ks) over the products.
+int64_t sm_weight_bytes(const Weight &w);
+int sm_wgs(int64_t N, int ks);
+hipError_t launch_pack_sm(const Weight &w, void *out, hipStream_t st);
+hipError_t launch_gemm_sm(WKind kind, const SmArgs &a, int wgs, int ks, hipStream_t st);
 // Neck GEMMs (k_conv.hip; WK_F16 or WK_F16X3 weights with N padded to
 // CONV_BN): EPI_DECONV / EPI_ACT / EPI_F32 on plain rows, or EPI_F32 as a
 // 3×3 implicit GEMM when g is given.

@@ -13,6 +13,7 @@
 #include <algorithm>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -50,11 +51,19 @@ using namespace s3e;
 struct s3e_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
+    // descriptors of the last batched small-M launch (device copy + host copy,
+    // reused while a caller repeats the same batch)
+    void *sm_dev = nullptr;
+    size_t sm_cap = 0;
+    std::vector<uint8_t> sm_last;
 };
 
 struct s3e_weight {
     s3e_ctx *ctx = nullptr;
     Weight w;
+    // the small-M kernel's block-interleaved copy, made at first use
+    mutable std::mutex mu;
+    mutable void *sm = nullptr;
 };
 
 // ---- host helpers shared with s3e_hiera.cpp (declared in s3e_rt.h) ----
@@ -292,6 +301,7 @@ extern "C" void s3e_ctx_destroy(s3e_ctx *ctx) {
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     (void)hipStreamDestroy(ctx->stream);
+    if (ctx->sm_dev) (void)hipFree(ctx->sm_dev);
     delete ctx;
 }
 
@@ -364,8 +374,75 @@ extern "C" int s3e_weight_upload(s3e_ctx *ctx, int type, int64_t ne0, int64_t ne
 extern "C" void s3e_weight_free(s3e_weight *w) {
     if (!w) return;
     free_weight(w->w);
+    if (w->sm) (void)hipFree(w->sm);
     delete w;
 }
+
+namespace {
+
+// Products of at most 64 rows stream their weights: they run on the small-M
+// kernel (k_gemm_sm.hip) from its block-interleaved weight copy.
+bool sm_eligible(const Weight &W, int64_t M) {
+    return M >= 1 && M <= 64 &&
+           (W.kind == WK_Q4_0 || W.kind == WK_Q4_1 || W.kind == WK_Q8_0 || W.kind == WK_F16);
+}
+
+hipError_t sm_weights(const s3e_weight *w, hipStream_t st, const uint8_t **out) {
+    std::lock_guard<std::mutex> lock(w->mu);
+    if (!w->sm) {
+        void *p = nullptr;
+        hipError_t e = hipMalloc(&p, (size_t)sm_weight_bytes(w->w));
+        if (e != hipSuccess) return e;
+        e = launch_pack_sm(w->w, p, st);
+        // finished before another context's stream may read it
+        if (e == hipSuccess) e = hipStreamSynchronize(st);
+        if (e != hipSuccess) {
+            (void)hipFree(p);
+            return e;
+        }
+        w->sm = p;
+    }
+    *out = (const uint8_t *)w->sm;
+    return hipSuccess;
+}
+
+SmGemm sm_desc(const Weight &W, const uint8_t *wsm, const Act &a, const float *bias, float *Y, int wg0) {
+    SmGemm g;
+    g.w = wsm;
+    g.wd = W.d;
+    g.wm = W.m;
+    g.x = a.x;
+    g.xd = a.d;
+    g.xs = a.s;
+    g.bias = bias;
+    g.y = Y;
+    g.ldx = a.ld;
+    g.ldy = W.N;
+    g.xmp = a.mp;
+    g.np = W.Np;
+    g.K = (int)W.K;
+    g.N = (int)W.N;
+    g.nst = (int)((W.Kp + 127) / 128);
+    g.wg0 = wg0;
+    return g;
+}
+
+// Four waves share each 32-column strip's K range.
+constexpr int SM_KS = 4;
+
+hipError_t run_mul_mat(const s3e_weight *w, const Act &a, int64_t M, const EpiArgs &ea, hipStream_t st) {
+    const Weight &W = w->w;
+    if (!sm_eligible(W, M)) return launch_gemm(W, a, M, EPI_F32, ea, st);
+    const uint8_t *wsm = nullptr;
+    hipError_t e = sm_weights(w, st, &wsm);
+    if (e != hipSuccess) return e;
+    SmArgs sa;
+    sa.one = sm_desc(W, wsm, a, ea.bias, ea.y, 0);
+    sa.M = (int)M;
+    return launch_gemm_sm(W.kind, sa, sm_wgs(W.N, SM_KS), SM_KS, st);
+}
+
+}  // namespace
 
 extern "C" int s3e_weight_info(const s3e_weight *w, int64_t out[4]) {
     if (!w || !out) { set_error("s3e_weight_info: NULL argument"); return S3E_ERR_INVALID; }
@@ -424,7 +501,7 @@ extern "C" int s3e_mul_mat(s3e_ctx *ctx, const s3e_weight *w, const float *X, in
     HIP_TRY(buf.alloc(M, W.K, ctx->stream));
     const Act a = buf.as(ak, W.K);
     hipError_t e = launch_rows_quant(ak, X, M, W.K, a, ctx->stream);
-    if (e == hipSuccess) e = launch_gemm(W, a, M, EPI_F32, ea, ctx->stream);
+    if (e == hipSuccess) e = run_mul_mat(w, a, M, ea, ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     buf.release();
     if (e != hipSuccess) { set_error("s3e_mul_mat: %s", hipGetErrorString(e)); return S3E_ERR_HIP; }
@@ -452,7 +529,73 @@ extern "C" int s3e_mul_mat_q(s3e_ctx *ctx, const s3e_weight *w, const void *xq, 
     ea.bias = bias;
     ea.y = Y;
     ea.ldy = W.N;
-    HIP_TRY(launch_gemm(W, a, M, EPI_F32, ea, ctx->stream));
+    HIP_TRY(run_mul_mat(w, a, M, ea, ctx->stream));
+    return S3E_OK;
+}
+
+extern "C" int s3e_mul_mat_q_batch(s3e_ctx *ctx, int n, const s3e_weight *const *w, const void *const *xq,
+                                   const uint16_t *const *d, const uint16_t *const *s, int64_t M,
+                                   const float *const *bias, float *const *Y) {
+    if (!ctx || n <= 0 || !w || !xq || !Y) { set_error("s3e_mul_mat_q_batch: NULL argument or n <= 0"); return S3E_ERR_INVALID; }
+    if (M < 1 || M > 64) { set_error("s3e_mul_mat_q_batch: M=%lld is outside 1..64", (long long)M); return S3E_ERR_UNSUPPORTED; }
+    const WKind kind = w[0] ? w[0]->w.kind : WK_F32;
+    std::vector<SmGemm> g((size_t)n);
+    const int ks = SM_KS;
+    int wgs = 0;
+    HIP_TRY(hipSetDevice(ctx->device));
+    for (int i = 0; i < n; i++) {
+        if (!w[i] || !xq[i] || !Y[i]) { set_error("s3e_mul_mat_q_batch: NULL entry %d", i); return S3E_ERR_INVALID; }
+        const Weight &W = w[i]->w;
+        if (W.kind != kind || !sm_eligible(W, M)) {
+            set_error("s3e_mul_mat_q_batch: product %d: all weights must share one of Q4_0/Q4_1/Q8_0/F16", i);
+            return S3E_ERR_UNSUPPORTED;
+        }
+        const AKind ak = act_kind_for(W.kind);
+        if ((ak == A_Q8_0 || ak == A_Q8_1) && (!d || !d[i])) { set_error("s3e_mul_mat_q_batch: missing scales of %d", i); return S3E_ERR_INVALID; }
+        if (ak == A_Q8_1 && (!s || !s[i])) { set_error("s3e_mul_mat_q_batch: missing block sums of %d", i); return S3E_ERR_INVALID; }
+        const uint8_t *wsm = nullptr;
+        HIP_TRY(sm_weights(w[i], ctx->stream, &wsm));
+        Act a;
+        a.kind = ak;
+        a.x = (void *)xq[i];
+        a.d = d ? (uint16_t *)d[i] : nullptr;
+        a.s = s ? (uint16_t *)s[i] : nullptr;
+        a.ld = W.K;
+        a.mp = round_up(M, ROW_PAD);
+        g[(size_t)i] = sm_desc(W, wsm, a, bias ? bias[i] : nullptr, Y[i], wgs);
+        wgs += sm_wgs(W.N, ks);
+        if (n > 65535 || wgs > (1 << 30)) { set_error("s3e_mul_mat_q_batch: batch too large"); return S3E_ERR_UNSUPPORTED; }
+    }
+    // descriptors, then the product index of every work-group
+    const size_t desc_bytes = sizeof(SmGemm) * (size_t)n;
+    std::vector<uint8_t> blob(desc_bytes + sizeof(uint16_t) * (size_t)wgs);
+    std::memcpy(blob.data(), g.data(), desc_bytes);
+    uint16_t *tab = (uint16_t *)(blob.data() + desc_bytes);
+    for (int i = 0; i < n; i++) {
+        const int end = i + 1 < n ? g[(size_t)i + 1].wg0 : wgs;
+        for (int b = g[(size_t)i].wg0; b < end; b++) tab[b] = (uint16_t)i;
+    }
+    // the descriptors go to the device once per distinct batch, after every
+    // launch that still reads the previous ones
+    if (ctx->sm_last != blob) {
+        HIP_TRY(hipStreamSynchronize(ctx->stream));
+        ctx->sm_last.clear();
+        if (blob.size() > ctx->sm_cap) {
+            if (ctx->sm_dev) (void)hipFree(ctx->sm_dev);
+            ctx->sm_dev = nullptr;
+            ctx->sm_cap = 0;
+            HIP_TRY(hipMalloc(&ctx->sm_dev, blob.size()));
+            ctx->sm_cap = blob.size();
+        }
+        HIP_TRY(hipMemcpy(ctx->sm_dev, blob.data(), blob.size(), hipMemcpyHostToDevice));
+        ctx->sm_last = blob;
+    }
+    SmArgs sa;
+    sa.many = (const SmGemm *)ctx->sm_dev;
+    sa.wg_gemm = (const uint16_t *)((const uint8_t *)ctx->sm_dev + desc_bytes);
+    sa.n = n;
+    sa.M = (int)M;
+    HIP_TRY(launch_gemm_sm(kind, sa, wgs, ks, ctx->stream));
     return S3E_OK;
 }
 

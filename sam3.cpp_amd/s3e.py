@@ -82,6 +82,8 @@ def _load() -> ctypes.CDLL:
         "s3e_quantize_rows": (c_int, [c_void_p, c_int, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
         "s3e_layer_norm": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_float, c_void_p, c_void_p, c_void_p]),
         "s3e_mul_mat_q": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
+        "s3e_mul_mat_q_batch": (c_int, [c_void_p, c_int, POINTER(c_void_p), POINTER(c_void_p), POINTER(c_void_p),
+                                        POINTER(c_void_p), c_int64, POINTER(c_void_p), POINTER(c_void_p)]),
         "s3e_copy": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t]),
         "s3e_flash_attn_ext": (c_int, [c_void_p, c_void_p, P64, c_void_p, P64, c_void_p, P64,
                                        c_int64, c_int64, c_int64, c_int64, c_int64, c_float, c_int, c_void_p]),
@@ -115,7 +117,7 @@ LIB = _load()
 DECLARED = [
     "s3e_last_error", "s3e_abi_version", "s3e_ctx_create", "s3e_ctx_destroy", "s3e_ctx_sync", "s3e_ctx_stream",
     "s3e_malloc", "s3e_free", "s3e_memcpy_h2d", "s3e_memcpy_d2h", "s3e_weight_upload", "s3e_weight_free",
-    "s3e_weight_info", "s3e_mul_mat", "s3e_mul_mat_q", "s3e_quantize_rows", "s3e_layer_norm", "s3e_copy",
+    "s3e_weight_info", "s3e_mul_mat", "s3e_mul_mat_q", "s3e_mul_mat_q_batch", "s3e_quantize_rows", "s3e_layer_norm", "s3e_copy",
     "s3e_flash_attn_ext", "s3e_model_load",
     "s3e_model_free", "s3e_model_hparams", "s3e_state_create", "s3e_state_free", "s3e_encode_chw",
     "s3e_encode_chw_host", "s3e_encode_image_u8", "s3e_vit_prefix", "s3e_vit_block", "s3e_run_neck", "s3e_hiera_block", "s3e_model_type",
@@ -299,6 +301,17 @@ class Context:
                   Y: DeviceBuffer, bias: DeviceBuffer | None = None):
         check(LIB.s3e_mul_mat_q(self.handle, w.handle, xq.ptr, d.ptr if d else None, s.ptr if s else None, M,
                                 bias.ptr if bias else None, Y.ptr), "s3e_mul_mat_q")
+
+    def mul_mat_q_batch(self, ws, xqs, ds, ss, M: int, biases, Ys):
+        """Independent small-M products in one launch (lists of equal length;
+        ds / ss / biases may be None or hold None entries)."""
+        n = len(ws)
+        arr = lambda items: (c_void_p * n)(*[(x.ptr if hasattr(x, "ptr") else x) if x is not None else None
+                                             for x in items])
+        none = [None] * n
+        check(LIB.s3e_mul_mat_q_batch(self.handle, n, (c_void_p * n)(*[w.handle for w in ws]), arr(xqs),
+                                      arr(ds or none), arr(ss or none), M, arr(biases or none), arr(Ys)),
+              "s3e_mul_mat_q_batch")
 
     def copy(self, dst: DeviceBuffer, src: DeviceBuffer, nbytes: int):
         check(LIB.s3e_copy(self.handle, dst.ptr, src.ptr, nbytes), "s3e_copy")

@@ -3,9 +3,12 @@
 - s3e_quantize_rows: bit-exact with ggml's x86 from_float (Q8_0, Q8_1, F16),
   including rows built so that x·127/amax lands exactly on k + 0.5.
 - s3e_mul_mat: every weight type at small, ragged and SAM 3 ViT MLP shapes
-  (fc1 N=4736 K=1024, fc2 N=1024 K=4736, M = 5184 and 64).  Both sides use
-  the same quantized activations, so only fp32 accumulation order differs:
-  relative L2 ≤ 1e-5.
+  (fc1 N=4736 K=1024, fc2 N=1024 K=4736, M = 5184 and 64), and the
+  weight-streaming kernel of products with at most 64 rows (M = 1 .. 64,
+  ragged N and K).  Both sides use the same quantized activations, so only
+  fp32 accumulation order differs: relative L2 ≤ 1e-5.
+- s3e_mul_mat_q_batch: several products in one launch, bit-identical to one
+  s3e_mul_mat_q call each.
 - s3e_flash_attn_ext: windowed (9 × 576) and global (5184) shapes, head dim
   64.  Default precision rounds Q, K, V and P to fp16 (fp32 accumulation):
   the F16 tolerance, relative L2 ≤ 2e-3.  F32 precision (fp16 hi/lo pairs)
@@ -123,6 +126,90 @@ def test_mul_mat(ctx, wt, M, N, K):
     err = orc.rel_l2(Y, ref)
     print(f"mul_mat type={wt} M={M} N={N} K={K}: rel_l2={err:.3e} max_abs={orc.max_abs(Y, ref):.3e}")
     assert err <= 1e-5
+
+
+SMALL_M = [1, 5, 32, 33, 64]
+
+
+@pytest.mark.parametrize("wt", [orc.Q4_0, orc.Q4_1, orc.Q8_0, orc.F16],
+                         ids=lambda t: {1: "f16", 2: "q4_0", 3: "q4_1", 8: "q8_0"}[t])
+@pytest.mark.parametrize("N,K", [(40, 96), (4736, 1024), (1024, 4736), (200, 160)])
+def test_mul_mat_small_m(ctx, wt, N, K):
+    """The weight-streaming kernel (M ≤ 64) against the oracle at ragged N, K
+    not a multiple of 128 and row counts around its 32-row tiles; one weight
+    serves every M, so its packed copy is made once and reused."""
+    rng = np.random.default_rng(N + K + wt)
+    W = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    bias = rng.normal(0, 0.1, N).astype(np.float32)
+    wb = orc.to_weight_bytes(wt, W)
+    w = ctx.weight(wt, K, N, wb)
+    bd = ctx.to_device(bias)
+    for M in SMALL_M:
+        X = rng.standard_normal((M, K)).astype(np.float32)
+        ref = orc.mul_mat(wt, wb, N, K, X) + bias
+        Xd, Yd = ctx.to_device(X), ctx.buffer(M * N * 4)
+        ctx.mul_mat(w, Xd, M, Yd, bd)
+        ctx.sync()
+        Y = Yd.download(np.float32, (M, N))
+        err = orc.rel_l2(Y, ref)
+        print(f"small-M type={wt} M={M} N={N} K={K}: rel_l2={err:.3e}", flush=True)
+        assert err <= 1e-5, M
+
+
+@pytest.mark.parametrize("wt", [orc.Q4_0, orc.Q4_1, orc.Q8_0, orc.F16],
+                         ids=lambda t: {1: "f16", 2: "q4_0", 3: "q4_1", 8: "q8_0"}[t])
+def test_mul_mat_q_batch_matches_single(ctx, wt):
+    """Independent products of different shapes in one launch give exactly
+    what s3e_mul_mat_q gives for each of them; a repeated batch reuses its
+    descriptors and a different one replaces them."""
+    rng = np.random.default_rng(wt + 3)
+    M = 48
+    shapes = [(3072, 1024), (1024, 1024), (40, 96), (4736, 1024), (1024, 4736)]
+    vdt = orc.VEC_DOT[wt]
+    ws, xq, ds, ss, ys, bs, ref = [], [], [], [], [], [], []
+    for N, K in shapes:
+        W = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+        ws.append(ctx.weight(wt, K, N, orc.to_weight_bytes(wt, W)))
+        X = rng.standard_normal((M, K)).astype(np.float32)
+        ns = s3e.act_scale_elems(M, K)
+        q, d, s_ = ctx.buffer(M * K * 2), ctx.buffer(ns * 2), ctx.buffer(ns * 2)
+        ctx.quantize_rows(vdt, ctx.to_device(X), M, K, q, d if wt != orc.F16 else None,
+                          s_ if wt != orc.F16 else None)
+        xq.append(q)
+        ds.append(d if wt != orc.F16 else None)
+        ss.append(s_ if wt == orc.Q4_1 else None)
+        bs.append(ctx.to_device(rng.normal(0, 0.1, N).astype(np.float32)))
+        ys.append(ctx.buffer(M * N * 4))
+        y1 = ctx.buffer(M * N * 4)
+        ctx.mul_mat_q(ws[-1], q, ds[-1], ss[-1], M, y1, bs[-1])
+        ref.append(y1)
+    for rep in range(2):
+        ctx.mul_mat_q_batch(ws, xq, ds, ss, M, bs, ys)
+        ctx.sync()
+        for (N, K), y, r in zip(shapes, ys, ref):
+            assert np.array_equal(y.download(np.float32, (M, N)), r.download(np.float32, (M, N))), (rep, N, K)
+    # a different batch (two of the products, no bias) replaces the descriptors
+    ctx.mul_mat_q_batch(ws[2:4], xq[2:4], ds[2:4], ss[2:4], M, None, ys[2:4])
+    ctx.sync()
+    for i in (2, 3):
+        N, K = shapes[i]
+        r = ctx.buffer(M * N * 4)
+        ctx.mul_mat_q(ws[i], xq[i], ds[i], ss[i], M, r)
+        ctx.sync()
+        assert np.array_equal(ys[i].download(np.float32, (M, N)), r.download(np.float32, (M, N)))
+
+
+def test_mul_mat_q_batch_rejects(ctx):
+    W = np.zeros((64, 64), np.float32)
+    a = ctx.weight(orc.Q8_0, 64, 64, orc.to_weight_bytes(orc.Q8_0, W))
+    b = ctx.weight(orc.F16, 64, 64, orc.to_weight_bytes(orc.F16, W))
+    q, d, y = ctx.buffer(64 * 64), ctx.buffer(4096), ctx.buffer(64 * 64 * 4)
+    with pytest.raises(s3e.S3EError):
+        ctx.mul_mat_q_batch([a, b], [q, q], [d, d], None, 8, None, [y, y])  # mixed weight types
+    with pytest.raises(s3e.S3EError):
+        ctx.mul_mat_q_batch([a], [q], [d], None, 65, None, [y])  # more than 64 rows
+    with pytest.raises(s3e.S3EError):
+        ctx.mul_mat_q_batch([a], [q], None, None, 8, None, [y])  # quantized without scales
 
 
 @pytest.mark.parametrize("prec", [0, 1], ids=["fp16", "f32"])
