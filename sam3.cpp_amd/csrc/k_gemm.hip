@@ -249,6 +249,77 @@ __device__ __forceinline__ void epilogue(const GemmParams &p, const float *Ct, i
                 }
             }
         }
+    } else if constexpr (EPI == EPI_HQKV) {
+        // Hiera (sam2_hiera_block_forward, sam3.cpp:4330-4395): columns [0, C) are Q,
+        // [C, 2C) K, [2C, 3C) V of tokens in raster order over a grid_h × grid grid.
+        // Windows of wh × ww (window 0: the whole grid) are row-major over nwx per
+        // row; heads of HD channels go to rows of hdp (zeros past HD).
+        const int C = e.E, HD = e.HD, HDp = e.hdp, W = e.grid;
+        const int wh = e.window > 0 ? e.window : e.grid_h, ww = e.window > 0 ? e.window : W;
+        const int nwx = (W + ww - 1) / ww, Nkv = wh * ww;
+        // Q, K: a unit is one token and 8 columns (one 16-byte store per plane)
+        for (int u = t; u < BM * (BN / 8); u += NT_) {
+            const int row = u / (BN / 8), cc = u % (BN / 8);
+            const int gm = m0 + row, gn0 = n0 + cc * 8;
+            if (gm >= p.M || gn0 >= 2 * C) continue;
+            float v[8];
+            {
+                const float4 x0 = *(const float4 *)(Ct + row * CLD + cc * 8);
+                const float4 x1 = *(const float4 *)(Ct + row * CLD + cc * 8 + 4);
+                const float4 b0 = *(const float4 *)(e.bias + gn0);
+                const float4 b1 = *(const float4 *)(e.bias + gn0 + 4);
+                v[0] = x0.x + b0.x; v[1] = x0.y + b0.y; v[2] = x0.z + b0.z; v[3] = x0.w + b0.w;
+                v[4] = x1.x + b1.x; v[5] = x1.y + b1.y; v[6] = x1.z + b1.z; v[7] = x1.w + b1.w;
+            }
+            const int sel = gn0 >= C;
+            const int r2 = gn0 - sel * C;
+            if (sel == 0 && e.qpool) {  // Q rows for the pooling pass
+                float4 *dst = (float4 *)(e.y + (int64_t)gm * e.ldy + r2);
+                dst[0] = make_float4(v[0], v[1], v[2], v[3]);
+                dst[1] = make_float4(v[4], v[5], v[6], v[7]);
+                continue;
+            }
+            const int h = r2 / HD, d0 = r2 % HD;
+            const int py = gm / W, px = gm % W;
+            const int b = (py / wh) * nwx + px / ww;
+            const int pp = (py % wh) * ww + px % ww;
+            const int64_t o = ((int64_t)(b * e.NH + h) * Nkv + pp) * HDp + d0;
+            _Float16 *hi = sel == 0 ? e.q : e.k;
+            _Float16 *lo = sel == 0 ? e.q_lo : e.k_lo;
+            uint32_t w[4], wl[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const _Float16 h0 = to_half(v[2 * j]), h1 = to_half(v[2 * j + 1]);
+                w[j] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+                const _Float16 l0 = (_Float16)(v[2 * j] - (float)h0), l1 = (_Float16)(v[2 * j + 1] - (float)h1);
+                wl[j] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+            }
+            *(uint4 *)(hi + o) = make_uint4(w[0], w[1], w[2], w[3]);
+            if (lo) *(uint4 *)(lo + o) = make_uint4(wl[0], wl[1], wl[2], wl[3]);
+            if (d0 + 8 == HD) {  // the head's padding columns
+                for (int z = 8; z < HDp - d0; z += 8) {
+                    *(uint4 *)(hi + o + z) = make_uint4(0u, 0u, 0u, 0u);
+                    if (lo) *(uint4 *)(lo + o + z) = make_uint4(0u, 0u, 0u, 0u);
+                }
+            }
+        }
+        // Vᵀ [b][h][d][slot]: lanes run along tokens of one column, so a store
+        // instruction covers runs of consecutive key slots
+        for (int u = t; u < BM * BN; u += NT_) {
+            const int row = u % BM, col = u / BM;
+            const int gm = m0 + row, gn = n0 + col;
+            if (gm >= p.M || gn < 2 * C || gn >= 3 * C) continue;
+            const float v = Ct[row * CLD + col] + e.bias[gn];
+            const int r2 = gn - 2 * C;
+            const int h = r2 / HD, d = r2 % HD;
+            const int py = gm / W, px = gm % W;
+            const int b = (py / wh) * nwx + px / ww;
+            const int pp = (py % wh) * ww + px % ww;
+            const int64_t o = ((int64_t)(b * e.NH + h) * HDp + d) * e.vt_ld + vt_slot(pp);
+            const _Float16 hv = to_half(v);
+            e.vt[o] = hv;
+            if (e.vt_lo) e.vt_lo[o] = (_Float16)(v - (float)hv);
+        }
     } else if constexpr (EPI == EPI_GELU) {
         // full 32-column blocks guaranteed by the launcher (N % 32 == 0)
         for (int ch = t; ch < BM * 4; ch += NT_) {
@@ -650,6 +721,7 @@ hipError_t dispatch_epi(Epi epi, const GemmParams &p, hipStream_t st) {
         case EPI_POS: return launch_one<WK, EPI_POS, 64, WAVES>(p, st);
         case EPI_GELU: return launch_one<WK, EPI_GELU, 64, WAVES>(p, st);
         case EPI_QKV: return launch_one<WK, EPI_QKV, 64, WAVES>(p, st);
+        case EPI_HQKV: return launch_one<WK, EPI_HQKV, 64, WAVES>(p, st);
         default: break;  // the neck epilogues belong to k_conv
     }
     return hipErrorInvalidValue;
@@ -690,6 +762,14 @@ hipError_t launch_gemm(const Weight &w, const Act &a, int64_t M, Epi epi, const 
     p.nstages = (int)(w.Kp / stage_k(w.kind));
     p.tiles_n = (int)(w.Np / BN);
     p.e = ea;
+    if (epi == EPI_HQKV) {
+        // 8-column units stay inside one head; Q/K rows are 16-byte aligned
+        if (ea.E <= 0 || w.N != 3LL * ea.E || ea.HD <= 0 || ea.HD % 8 != 0 || ea.E % ea.HD != 0 ||
+            ea.hdp < ea.HD || ea.hdp % 8 != 0 || ea.NH * ea.HD != ea.E || ea.grid <= 0 || ea.grid_h <= 0 ||
+            (int64_t)ea.grid * ea.grid_h != M || ea.window < 0 || !ea.bias || !ea.k || !ea.vt || ea.vt_ld <= 0 ||
+            (ea.qpool ? (!ea.y || ea.ldy < ea.E) : !ea.q))
+            return hipErrorInvalidValue;
+    }
     // 64-row tiles: two or three work-groups share a CU, so one work-group's
     // epilogue overlaps another's main loop; with 128-row tiles (one per CU)
     // every CU alternates between the two phases.

@@ -39,6 +39,7 @@ __global__ void k_im2col_conv(const float *__restrict__ chw, int S, int k, int s
 // for keys Nkv .. ldv − 1.  With lo planes the values are split hi + lo.
 struct Prep {
     const float *qkv, *bias;
+    int64_t ld;  // row stride of qkv in floats
     int H, W, C, NH, HD, HDp;
     int wh, ww, nwx, qs;
     int Nq, Nkv, ldv, NW;
@@ -48,7 +49,7 @@ struct Prep {
 __device__ __forceinline__ float qkv_at(const Prep &p, int b, int py, int px, int col) {
     const int wy = b / p.nwx, wx = b % p.nwx;
     const int y = wy * p.wh + py, x = wx * p.ww + px;
-    if (y < p.H && x < p.W) return p.qkv[((int64_t)y * p.W + x) * 3 * p.C + col];
+    if (y < p.H && x < p.W) return p.qkv[((int64_t)y * p.W + x) * p.ld + col];
     return p.bias[col];
 }
 
@@ -70,7 +71,7 @@ __global__ void k_hiera_prep(Prep p, int mode, int64_t total) {
     const int b = (int)(bh / p.NH), h = (int)(bh % p.NH);
     float v = 0.f;
     if (d < p.HD && pos < (mode == 0 ? p.Nq : p.Nkv)) {
-        const int col = mode * p.C + h * p.HD + d;
+        const int col = (p.ld == 3LL * p.C ? mode * p.C : 0) + h * p.HD + d;
         if (mode == 0 && p.qs) {
             const int qw = p.ww / 2;
             const int qy = pos / qw, qx = pos % qw;
@@ -83,6 +84,39 @@ __global__ void k_hiera_prep(Prep p, int mode, int64_t total) {
     if (mode == 0) put(p.q, p.q_lo, (bh * p.Nq + pos) * p.HDp + d, v);
     else if (mode == 1) put(p.k, p.k_lo, (bh * p.Nkv + pos) * p.HDp + d, v);
     else put(p.vt, p.vt_lo, (bh * p.HDp + d) * p.ldv + vt_slot(pos), v);
+}
+
+// Window positions outside the grid (ggml pads the normed input with zeros, so
+// after the projection they hold the QKV bias; zeros past HD) for Q (without
+// Q stride), K and Vᵀ, and the Vᵀ slots from Nkv to ldv (zeros).  One thread
+// per (window·head, position < ldv); positions inside the grid return at once.
+__global__ void k_hiera_pad(Prep p, int with_q, int64_t total) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    const int pos = (int)(i % p.ldv);
+    const int64_t bh = i / p.ldv;
+    const int b = (int)(bh / p.NH), h = (int)(bh % p.NH);
+    const int64_t vrow = bh * p.HDp;
+    if (pos >= p.Nkv) {
+        const int64_t slot = vt_slot(pos);
+        for (int d = 0; d < p.HDp; d++) {
+            p.vt[(vrow + d) * p.ldv + slot] = (_Float16)0.f;
+            if (p.vt_lo) p.vt_lo[(vrow + d) * p.ldv + slot] = (_Float16)0.f;
+        }
+        return;
+    }
+    const int wy = b / p.nwx, wx = b % p.nwx;
+    const int y = wy * p.wh + pos / p.ww, x = wx * p.ww + pos % p.ww;
+    if (y < p.H && x < p.W) return;
+    const int64_t slot = vt_slot(pos);
+    for (int d = 0; d < p.HDp; d++) {
+        const bool real = d < p.HD;
+        const float bk = real ? p.bias[p.C + h * p.HD + d] : 0.f;
+        const float bv = real ? p.bias[2 * p.C + h * p.HD + d] : 0.f;
+        put(p.k, p.k_lo, (bh * p.Nkv + pos) * p.HDp + d, bk);
+        if (real) put(p.vt, p.vt_lo, (vrow + d) * p.ldv + slot, bv);
+        if (with_q) put(p.q, p.q_lo, (bh * p.Nkv + pos) * p.HDp + d, real ? p.bias[h * p.HD + d] : 0.f);
+    }
 }
 
 // dst [side²][D] += nearest ×2 upsampling of src [(side/2)²][D]
@@ -113,10 +147,13 @@ hipError_t launch_im2col_conv(const float *chw, int S, int k, int stride, int pa
     return hipGetLastError();
 }
 
-hipError_t launch_hiera_prep(const HieraPrepArgs &a, hipStream_t st) {
+namespace {
+
+Prep make_prep(const HieraPrepArgs &a) {
     Prep p;
     p.qkv = a.qkv;
     p.bias = a.bias;
+    p.ld = a.qkv_ld > 0 ? a.qkv_ld : 3LL * a.C;
     p.H = a.H; p.W = a.W; p.C = a.C; p.NH = a.NH; p.HD = a.HD; p.HDp = a.HDp;
     p.qs = a.q_stride;
     if (a.window > 0) {
@@ -133,12 +170,32 @@ hipError_t launch_hiera_prep(const HieraPrepArgs &a, hipStream_t st) {
     p.Nq = a.q_stride ? (p.wh / 2) * (p.ww / 2) : p.Nkv;
     p.ldv = (int)vt_ld_for(p.Nkv);
     p.q = a.q; p.k = a.k; p.vt = a.vt; p.q_lo = a.q_lo; p.k_lo = a.k_lo; p.vt_lo = a.vt_lo;
-    if (p.HD > p.HDp || p.HDp % 8 != 0) return hipErrorInvalidValue;
+    return p;
+}
+
+}  // namespace
+
+// With qkv_ld = C (Q rows only), the Q pass alone; with the full QKV rows,
+// all three operands.
+hipError_t launch_hiera_prep(const HieraPrepArgs &a, hipStream_t st) {
+    const Prep p = make_prep(a);
+    if (p.HD > p.HDp || p.HDp % 8 != 0 || (p.ld != 3LL * p.C && p.ld != p.C)) return hipErrorInvalidValue;
     const int64_t bh = (int64_t)p.NW * p.NH;
     const int64_t tq = bh * p.Nq * p.HDp, tk = bh * p.Nkv * p.HDp, tv = bh * p.ldv * p.HDp;
     hipLaunchKernelGGL(k_hiera_prep, dim3((unsigned)((tq + 255) / 256)), dim3(256), 0, st, p, 0, tq);
-    hipLaunchKernelGGL(k_hiera_prep, dim3((unsigned)((tk + 255) / 256)), dim3(256), 0, st, p, 1, tk);
-    hipLaunchKernelGGL(k_hiera_prep, dim3((unsigned)((tv + 255) / 256)), dim3(256), 0, st, p, 2, tv);
+    if (p.ld == 3LL * p.C) {
+        hipLaunchKernelGGL(k_hiera_prep, dim3((unsigned)((tk + 255) / 256)), dim3(256), 0, st, p, 1, tk);
+        hipLaunchKernelGGL(k_hiera_prep, dim3((unsigned)((tv + 255) / 256)), dim3(256), 0, st, p, 2, tv);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_hiera_pad(const HieraPrepArgs &a, hipStream_t st) {
+    const Prep p = make_prep(a);
+    if (p.HD > p.HDp || !p.k || !p.vt || !p.bias || (!a.q_stride && !p.q)) return hipErrorInvalidValue;
+    const int64_t total = (int64_t)p.NW * p.NH * p.ldv;
+    hipLaunchKernelGGL(k_hiera_pad, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, p, a.q_stride ? 0 : 1,
+                       total);
     return hipGetLastError();
 }
 

@@ -13,9 +13,10 @@
 //   LayerNorm(1e-6) → the QKV weight's activation format
 //   shortcut: dim projection GEMM (+ bias) and 2×2 max pool under Q stride,
 //             written into the block's output buffer (the residual stream)
-//   QKV GEMM (+ bias, f32) → k_hiera_prep: window partition with
-//             bias-valued padding, Q max pool, heads zero-padded to 64/128,
-//             fp16 hi/lo planes
+//   QKV GEMM (+ bias) whose epilogue writes Q, K, Vᵀ in window order as
+//             fp16 (hi, lo) planes, heads zero-padded to 64/128; a small
+//             pass fills window padding with the bias; under Q stride Q goes
+//             out as f32 rows and k_hiera_prep max-pools it inside windows
 //   attention (k_attn, head dim 64 or 128) → proj input, written at the
 //             un-partitioned, cropped token rows
 //   proj GEMM + bias + residual; LayerNorm; fc1 + bias + ggml_gelu (fp16
@@ -74,7 +75,7 @@ struct HieraModel {
 struct HieraState {
     ActBuf col, a1, a2;             // im2col rows; GEMM inputs (E-wide, MLP-wide)
     float *xs[4] = {};              // stage residual streams = stage outputs
-    float *qkv = nullptr, *dp = nullptr, *attn_f32 = nullptr;
+    float *qkv = nullptr, *dp = nullptr, *attn_f32 = nullptr;  // qkv: Q rows of Q-stride blocks
     _Float16 *q16 = nullptr, *k16 = nullptr, *vt16 = nullptr;  // [hi | lo] planes
     int64_t q_cap = 0, k_cap = 0, v_cap = 0;
     _Float16 *fin = nullptr;        // FPN inputs as fp16 planes [hi | lo]
@@ -242,7 +243,7 @@ int hiera_load(int device, std::ifstream &fin, int ftype, int32_t n_tensors, Hie
     // what the kernels need: heads of at most 128 channels, float4 rows, 32-wide
     // K blocks where a layer is quantized (checked below per weight)
     for (const HBlock &b : m->blocks) {
-        if (b.dout % b.heads != 0 || b.dout / b.heads > 128 || b.din % 4 != 0) {
+        if (b.dout % b.heads != 0 || b.dout / b.heads > 128 || (b.dout / b.heads) % 8 != 0 || b.din % 4 != 0) {
             set_error("s3e_model_load: Hiera block with width %d and %d heads is not supported", b.dout, b.heads);
             return S3E_ERR_UNSUPPORTED;
         }
@@ -434,7 +435,7 @@ int hiera_state_create(const HieraModel *m, hipStream_t st, HieraState **out) {
             const int64_t T = (int64_t)H * W;
             const int Ht = b.qs ? H / 2 : H, Wt = b.qs ? W / 2 : W;
             emax = std::max<int64_t>({emax, b.din, b.dout});
-            qkv_cap = std::max(qkv_cap, T * 3 * b.dout);
+            if (b.qs) qkv_cap = std::max(qkv_cap, T * b.dout);  // Q rows before pooling
             dp_cap = std::max(dp_cap, T * b.dout);
             attn_cap = std::max(attn_cap, (int64_t)Ht * Wt * b.dout);
             int wh = b.ws > 0 ? b.ws : H, ww = b.ws > 0 ? b.ws : W;
@@ -452,7 +453,7 @@ int hiera_state_create(const HieraModel *m, hipStream_t st, HieraState **out) {
     if (e == hipSuccess) e = s->a2.alloc(T0, 4 * emax, st);
     for (int i = 0; i < 4 && e == hipSuccess; i++)
         e = hipMalloc(&s->xs[i], (size_t)m->side[i] * m->side[i] * m->width[i] * 4);
-    if (e == hipSuccess) e = hipMalloc(&s->qkv, (size_t)qkv_cap * 4);
+    if (e == hipSuccess) e = hipMalloc(&s->qkv, (size_t)std::max<int64_t>(qkv_cap, 1) * 4);
     if (e == hipSuccess) e = hipMalloc(&s->dp, (size_t)dp_cap * 4);
     if (e == hipSuccess) e = hipMalloc(&s->attn_f32, (size_t)attn_cap * 4);
     s->q_cap = q_cap;
@@ -517,17 +518,15 @@ hipError_t hiera_block(const HieraModel *m, HieraState *s, int bi, const float *
     } else if (y != x) {
         if ((e = hipMemcpyAsync(y, x, (size_t)T * C * 4, hipMemcpyDeviceToDevice, st)) != hipSuccess) return e;
     }
-    // 3. QKV + bias (f32), then the attention operands
-    EpiArgs eq;
-    eq.bias = b.qkv_b;
-    eq.y = s->qkv;
-    eq.ldy = 3 * C;
-    if ((e = launch_gemm(b.qkv, a_in, T, EPI_F32, eq, st)) != hipSuccess) return e;
-    // quantized and F32 projections re-quantize the attention output: split
-    // fp16 pairs keep it at f32 accuracy; F16 models use plain fp16
+    // 3. QKV + bias straight into the attention operands (window order, fp16
+    // planes); Q of a Q-stride block goes out as f32 rows for the pooling pass.
+    // Quantized and F32 projections re-quantize the attention output: split
+    // fp16 pairs keep attention at f32 accuracy; F16 models use plain fp16.
     const bool split = b.proj.kind != WK_F16;
+    const int wh = b.ws > 0 ? b.ws : H, ww = b.ws > 0 ? b.ws : W;
     HieraPrepArgs pa;
     pa.qkv = s->qkv;
+    pa.qkv_ld = C;
     pa.bias = b.qkv_b;
     pa.H = H; pa.W = W; pa.C = C; pa.NH = NH; pa.HD = HD; pa.HDp = HDp;
     pa.window = b.ws;
@@ -538,9 +537,20 @@ hipError_t hiera_block(const HieraModel *m, HieraState *s, int bi, const float *
         pa.k_lo = s->k16 + s->k_cap;
         pa.vt_lo = s->vt16 + s->v_cap;
     }
-    if ((e = launch_hiera_prep(pa, st)) != hipSuccess) return e;
+    EpiArgs eq;
+    eq.bias = b.qkv_b;
+    eq.E = C; eq.HD = HD; eq.NH = NH; eq.hdp = HDp;
+    eq.grid = W; eq.grid_h = H; eq.window = b.ws;
+    eq.vt_ld = (int)vt_ld_for((int64_t)wh * ww);
+    eq.q = pa.q; eq.k = pa.k; eq.vt = pa.vt;
+    eq.q_lo = pa.q_lo; eq.k_lo = pa.k_lo; eq.vt_lo = pa.vt_lo;
+    eq.qpool = b.qs;
+    eq.y = s->qkv;
+    eq.ldy = C;
+    if ((e = launch_gemm(b.qkv, a_in, T, EPI_HQKV, eq, st)) != hipSuccess) return e;
+    if ((e = launch_hiera_pad(pa, st)) != hipSuccess) return e;
+    if (b.qs && (e = launch_hiera_prep(pa, st)) != hipSuccess) return e;
     // 4. attention → the proj input at the un-partitioned, cropped token rows
-    const int wh = b.ws > 0 ? b.ws : H, ww = b.ws > 0 ? b.ws : W;
     const int nwx = b.ws > 0 ? (W + b.ws - 1) / b.ws : 1, nwy = b.ws > 0 ? (H + b.ws - 1) / b.ws : 1;
     AttnArgs aa;
     aa.q = s->q16; aa.k = s->k16; aa.vt = s->vt16;

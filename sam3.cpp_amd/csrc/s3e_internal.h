@@ -96,6 +96,8 @@ enum Epi : int {
     EPI_QKV = 4,     // split Q/K/V, RoPE, fp16, window layout
     EPI_DECONV = 5,  // 2×2 stride-2 transposed conv: (+ bias, GELU) → pixel shuffle into act
     EPI_ACT = 6,     // act = acc + bias                     (conv → next conv)
+    EPI_HQKV = 7,    // Hiera: Q/K/Vᵀ in window order (padded grid, heads padded to hdp), fp16
+                     // (hi, lo); with qpool, Q as f32 rows into y for the pooling pass
 };
 
 struct EpiArgs {
@@ -116,6 +118,8 @@ struct EpiArgs {
     // low halves of the fp16 pairs (x = hi + lo) when attention runs split
     _Float16 *q_lo = nullptr, *k_lo = nullptr, *vt_lo = nullptr;
     int vt_ld = 0;                 // row stride of Vᵀ in keys (vt_ld_for of the window size)
+    // EPI_HQKV: grid height (grid = width), padded head dim, Q pooled later
+    int grid_h = 0, hdp = 0, qpool = 0;
     // EPI_DECONV: input width (pixels per row) and output channels; column n
     // of the GEMM is kernel tap q = n / cout (ky = q / 2, kx = q % 2),
     // channel n % cout, written to output pixel (2y + ky, 2x + kx)
@@ -237,10 +241,15 @@ struct HieraPrepArgs {
     int H = 0, W = 0, C = 0, NH = 0, HD = 0, HDp = 0;
     int window = 0;               // 0: one window of the whole grid (global attention)
     int q_stride = 0;
+    int qkv_ld = 0;               // row stride of qkv in floats (0: 3C); Q columns start at 0
     _Float16 *q = nullptr, *k = nullptr, *vt = nullptr;
     _Float16 *q_lo = nullptr, *k_lo = nullptr, *vt_lo = nullptr;
 };
 hipError_t launch_hiera_prep(const HieraPrepArgs &a, hipStream_t st);
+// The attention operands that the EPI_HQKV epilogue does not write: window
+// positions outside the grid (the QKV bias; zeros past HD), Q only without Q
+// stride, and the Vᵀ key slots from the window size up to vt_ld (zeros).
+hipError_t launch_hiera_pad(const HieraPrepArgs &a, hipStream_t st);
 // dst [side²][D] += nearest-×2 upsampling of src [(side/2)²][D]
 hipError_t launch_upsample_add(float *dst, const float *src, int side, int D, hipStream_t st);
 
