@@ -89,17 +89,21 @@ __global__ void k_hiera_prep(Prep p, int mode, int64_t total) {
 // Window positions outside the grid (ggml pads the normed input with zeros, so
 // after the projection they hold the QKV bias; zeros past HD) for Q (without
 // Q stride), K and Vᵀ, and the Vᵀ slots from Nkv to ldv (zeros).  One thread
-// per (window·head, position < ldv); positions inside the grid return at once.
+// per (window·head, position < ldv, 8 channels); positions inside the grid
+// return at once.
 __global__ void k_hiera_pad(Prep p, int with_q, int64_t total) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= total) return;
-    const int pos = (int)(i % p.ldv);
-    const int64_t bh = i / p.ldv;
+    const int nch = p.HDp / 8;
+    const int d0 = (int)(i % nch) * 8;
+    const int64_t r = i / nch;
+    const int pos = (int)(r % p.ldv);
+    const int64_t bh = r / p.ldv;
     const int b = (int)(bh / p.NH), h = (int)(bh % p.NH);
     const int64_t vrow = bh * p.HDp;
+    const int64_t slot = vt_slot(pos);
     if (pos >= p.Nkv) {
-        const int64_t slot = vt_slot(pos);
-        for (int d = 0; d < p.HDp; d++) {
+        for (int d = d0; d < d0 + 8; d++) {
             p.vt[(vrow + d) * p.ldv + slot] = (_Float16)0.f;
             if (p.vt_lo) p.vt_lo[(vrow + d) * p.ldv + slot] = (_Float16)0.f;
         }
@@ -108,13 +112,11 @@ __global__ void k_hiera_pad(Prep p, int with_q, int64_t total) {
     const int wy = b / p.nwx, wx = b % p.nwx;
     const int y = wy * p.wh + pos / p.ww, x = wx * p.ww + pos % p.ww;
     if (y < p.H && x < p.W) return;
-    const int64_t slot = vt_slot(pos);
-    for (int d = 0; d < p.HDp; d++) {
+    for (int d = d0; d < d0 + 8; d++) {
         const bool real = d < p.HD;
         const float bk = real ? p.bias[p.C + h * p.HD + d] : 0.f;
-        const float bv = real ? p.bias[2 * p.C + h * p.HD + d] : 0.f;
         put(p.k, p.k_lo, (bh * p.Nkv + pos) * p.HDp + d, bk);
-        if (real) put(p.vt, p.vt_lo, (vrow + d) * p.ldv + slot, bv);
+        if (real) put(p.vt, p.vt_lo, (vrow + d) * p.ldv + slot, p.bias[2 * p.C + h * p.HD + d]);
         if (with_q) put(p.q, p.q_lo, (bh * p.Nkv + pos) * p.HDp + d, real ? p.bias[h * p.HD + d] : 0.f);
     }
 }
@@ -193,7 +195,9 @@ hipError_t launch_hiera_prep(const HieraPrepArgs &a, hipStream_t st) {
 hipError_t launch_hiera_pad(const HieraPrepArgs &a, hipStream_t st) {
     const Prep p = make_prep(a);
     if (p.HD > p.HDp || !p.k || !p.vt || !p.bias || (!a.q_stride && !p.q)) return hipErrorInvalidValue;
-    const int64_t total = (int64_t)p.NW * p.NH * p.ldv;
+    // nothing to fill when the windows tile the grid and hold whole 16-key groups
+    if ((int64_t)p.nwx * p.ww == p.W && (int64_t)(p.NW / p.nwx) * p.wh == p.H && p.ldv == p.Nkv) return hipSuccess;
+    const int64_t total = (int64_t)p.NW * p.NH * p.ldv * (p.HDp / 8);
     hipLaunchKernelGGL(k_hiera_pad, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, p, a.q_stride ? 0 : 1,
                        total);
     return hipGetLastError();
