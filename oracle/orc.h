@@ -181,6 +181,16 @@ int  orc_hiera_fpn(const orc_model *m, float *const stage[4], const int side[4],
 /* whole encoder; stage_out may be NULL */
 int  orc_hiera_encode(const orc_model *m, const float *chw, float *out[4], float *stage_out[4], int nthreads);
 
+/* ---- memory attention (orc_memattn.c) ----------------------------------- */
+/* layers, D (neck_dim), MD (mem_out_dim), FFN of the model's memory attention */
+int  orc_mem_attn_dims(const orc_model *m, int32_t out[4]);
+/* sam3_build_mem_attn_graph (sam3.cpp:9224-9337): curr, src_pos [N][D];
+ * prompt, prompt_pos [M_total][MD], the last n_ptr rows object-pointer
+ * tokens; rope_q [N][D/2][2], rope_k [M_total − n_ptr][D/2][2]; out [N][D]. */
+int  orc_mem_attn(const orc_model *m, const float *curr, const float *src_pos, int64_t N, const float *prompt,
+                  const float *prompt_pos, int64_t M_total, int64_t n_ptr, const float *rope_q,
+                  const float *rope_k, float *out, int nthreads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -180,9 +180,10 @@ tensors:
         if (off + bytes > fsize) ORC_FAIL("tensor %s: truncated data", t->name);
         const uint8_t *src = map + off;
         off += bytes;
-        /* encoder backbones and necks only */
+        /* encoder backbones, necks and the memory attention only */
         if (strncmp(t->name, "vit.", 4) != 0 && strncmp(t->name, "neck.", 5) != 0 &&
-            strncmp(t->name, "hiera.", 6) != 0 && strncmp(t->name, "fpn.", 4) != 0)
+            strncmp(t->name, "hiera.", 6) != 0 && strncmp(t->name, "fpn.", 4) != 0 &&
+            strncmp(t->name, "mem_attn.", 9) != 0)
             continue;
         const int rt = registered_type(t->name, n_dims, t->ne[0], m->wtype);
         t->type = rt;

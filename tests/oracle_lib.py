@@ -56,6 +56,8 @@ def _load():
                                       P, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,
                                       c_float, P, c_int]),
         "orc_compute_axial_cis": (None, [P, c_int, c_int, c_int, c_float, c_float]),
+        "orc_mem_attn_dims": (c_int, [P, POINTER(c_int32)]),
+        "orc_mem_attn": (c_int, [P, P, P, c_int64, P, P, c_int64, c_int64, P, P, P, c_int]),
         "orc_preprocess_sam3": (None, [P, c_int, c_int, c_int, P]),
         "orc_model_load": (P, [c_char_p]),
         "orc_model_free": (None, [P]),
@@ -372,6 +374,35 @@ def maxpool2x2(x: np.ndarray) -> np.ndarray:
 def sinusoidal_pe_2d(H: int, W: int, d: int) -> np.ndarray:
     out = np.empty((H, W, d), np.float32)
     LIB.orc_sinusoidal_pe_2d(H, W, d, ptr(out))
+    return out
+
+
+def axial_cis(dim: int, end_x: int, end_y: int, theta: float = 10000.0, scale: float = 1.0) -> np.ndarray:
+    """sam3_compute_axial_cis: [end_x·end_y][dim/2][2] (cos, sin)."""
+    out = np.empty((end_x * end_y, dim // 2, 2), np.float32)
+    LIB.orc_compute_axial_cis(ptr(out), dim, end_x, end_y, theta, scale)
+    return out
+
+
+def mem_attn_dims(handle) -> tuple:
+    """(layers, D, MD, FFN) of a loaded model's memory attention."""
+    out = (c_int32 * 4)()
+    assert LIB.orc_mem_attn_dims(handle, out) == 0, LIB.orc_last_error()
+    return tuple(out)
+
+
+def mem_attn(handle, curr, src_pos, prompt, prompt_pos, n_ptr: int, rope_q, rope_k, nthreads: int = 0):
+    """The oracle's sam3_build_mem_attn_graph on a loaded model (handle)."""
+    L, D, MD, FFN = mem_attn_dims(handle)
+    curr, src_pos = (np.ascontiguousarray(a, np.float32) for a in (curr, src_pos))
+    prompt, prompt_pos = (np.ascontiguousarray(a, np.float32) for a in (prompt, prompt_pos))
+    rope_q = np.ascontiguousarray(rope_q, np.float32)
+    rope_k = None if rope_k is None else np.ascontiguousarray(rope_k, np.float32)
+    N, M = curr.shape[0], prompt.shape[0]
+    out = np.empty((N, D), np.float32)
+    rc = LIB.orc_mem_attn(handle, ptr(curr), ptr(src_pos), N, ptr(prompt), ptr(prompt_pos), M, n_ptr, ptr(rope_q),
+                          None if rope_k is None else ptr(rope_k), ptr(out), nthreads)
+    assert rc == 0, LIB.orc_last_error()
     return out
 
 
