@@ -214,6 +214,23 @@ int s3e_vit_block(s3e_state *st, int idx, float *x_device);
  * s3e_encode_chw does after the backbone (the neck part of the encode graph,
  * sam3.cpp:6072-6075). */
 int s3e_run_neck(s3e_state *st, const float *x_device);
+/* ---- memory attention ---------------------------------------------------
+ * The tracker's memory attention (sam3_build_mem_attn_graph,
+ * sam3.cpp:9224-9337), loaded from the "mem_attn.*" records of either file
+ * type.  out[0..3] = layers, D (neck_dim), MD (mem_out_dim), FFN width; an
+ * error if the file has none. */
+int s3e_mem_attn_dims(const s3e_model *m, int32_t out[4]);
+/* Condition N current-frame tokens on the memory bank, on device f32
+ * buffers, with the layouts sam3_propagate_single gives the graph
+ * (sam3.cpp:11232-11304): curr and src_pos [N][D]; prompt and prompt_pos
+ * [M_total][MD], whose last num_obj_ptr_tokens rows are object-pointer
+ * tokens (no RoPE on their keys); rope_q [N][D/2][2] and rope_k
+ * [M_total − num_obj_ptr_tokens][D/2][2] (cos, sin; NULL when every memory
+ * token is a pointer token); out [N][D].  The state keeps the scratch, grown
+ * to the largest sizes seen (allocated on first use).  Asynchronous. */
+int s3e_mem_attn(s3e_state *st, const float *curr, const float *src_pos, int64_t N, const float *prompt,
+                 const float *prompt_pos, int64_t M_total, int64_t num_obj_ptr_tokens, const float *rope_q,
+                 const float *rope_k, float *out);
 /* SAM 2 stage hook: Hiera block idx (sam2_hiera_block_forward,
  * sam3.cpp:4295-4457) on x (device, H·W rows of the block's input width,
  * NHWC) into y (H/2·W/2 rows under Q stride, else H·W, of its output
@@ -250,6 +267,10 @@ typedef struct s3e_synth_cfg {
     /* necks (sam3.cpp:2562-2591): 0 none, 1 tracker only (visual-only
      * file), 2 detector and tracker; neck_dim 0 means 256 */
     int32_t neck, neck_dim;
+    /* memory-attention layers to write (0: none; the reference has 4):
+     * "mem_attn.layers.<l>.*" and "mem_attn.norm.*" of sam3.cpp:3034-3060,
+     * D = neck_dim, mem_out_dim 64, FFN 2048 */
+    int32_t mem_attn_layers;
 } s3e_synth_cfg;
 int s3e_synth_write(const char *path, const s3e_synth_cfg *cfg);
 
@@ -268,6 +289,7 @@ typedef struct s3e_synth_sam2_cfg {
     int32_t ftype;
     uint64_t seed;
     float std;  /* negative: also randomise biases and LayerNorm affine */
+    int32_t mem_attn_layers;  /* as in s3e_synth_cfg (sam3.cpp:2004-2040) */
 } s3e_synth_sam2_cfg;
 int s3e_synth_write_sam2(const char *path, const s3e_synth_sam2_cfg *cfg);
 

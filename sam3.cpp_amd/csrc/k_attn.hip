@@ -111,7 +111,7 @@ __device__ __forceinline__ void wait_and_barrier() {
 // CROP: the windowed, cropped output mapping and narrower real heads
 // (a.wo, a.hd_out; the Hiera layouts), kept out of the plain variants.
 template <bool SPLIT, int HD, bool CROP>
-__global__ __launch_bounds__(NTHR, HD == 64 ? 3 : 2) void k_attn(AttnArgs a, int ldv) {
+__global__ __launch_bounds__(NTHR, HD == 64 ? 3 : (HD == 128 ? 2 : 1)) void k_attn(AttnArgs a, int ldv) {
     using G = AG<HD>;
     constexpr int NP = SPLIT ? 2 : 1;  // planes: hi (and lo)
     constexpr int KPL = G::KPL, VPL = G::VPL;
@@ -148,7 +148,12 @@ __global__ __launch_bounds__(NTHR, HD == 64 ? 3 : 2) void k_attn(AttnArgs a, int
         for (int r = 0; r < 16; r++) o[dt][r] = 0.f;
 
     const int64_t koff = (int64_t)bh * a.Nkv * HD, voff = (int64_t)bh * HD * ldv;
-    const int ntiles = (a.Nkv + KT - 1) / KT;
+    // key tiles of this work-group: all, or with nsplit > 1 the blockIdx.z-th
+    // of nsplit consecutive ranges (each holds at least one tile)
+    const int ntiles_all = (a.Nkv + KT - 1) / KT;
+    const int per = (ntiles_all + a.nsplit - 1) / a.nsplit;
+    const int t0 = (int)blockIdx.z * per;
+    const int ntiles = min(ntiles_all, t0 + per) - t0;
     uint8_t *const Kring = lds, *const Vring = lds + 2 * KBUF;
 
     // DMA: per plane, a K tile is runs of 1 KB (8 rows of 128 B, or 4 of 256 B)
@@ -166,7 +171,7 @@ __global__ __launch_bounds__(NTHR, HD == 64 ? 3 : 2) void k_attn(AttnArgs a, int
             const int run = wave * G::KRUNS + j;
             const int r = RPR * run + lane / CPR;
             const int ch = (lane % CPR) ^ swzk_hd<HD>(r);
-            const int64_t key = min(tt * KT + r, a.Nkv - 1);
+            const int64_t key = min((t0 + tt) * KT + r, a.Nkv - 1);
 #pragma unroll
             for (int pl = 0; pl < NP; pl++) {
                 const _Float16 *src = (pl == 0 ? a.k : a.k_lo) + koff + key * HD + ch * 8;
@@ -181,7 +186,7 @@ __global__ __launch_bounds__(NTHR, HD == 64 ? 3 : 2) void k_attn(AttnArgs a, int
             const int run = wave * G::VRUNS + j;
             const int r = 16 * run + (lane >> 2);
             const int ch = (lane & 3) ^ swzv(r);
-            const int k0 = min(tt * KT + ch * 8, ldv - 8);
+            const int k0 = min((t0 + tt) * KT + ch * 8, ldv - 8);
 #pragma unroll
             for (int pl = 0; pl < NP; pl++) {
                 const _Float16 *src = (pl == 0 ? a.vt : a.vt_lo) + voff + (int64_t)r * ldv + k0;
@@ -237,7 +242,7 @@ __global__ __launch_bounds__(NTHR, HD == 64 ? 3 : 2) void k_attn(AttnArgs a, int
     auto mask = [&](v16f &sv, int tt) {
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-            const int key = tt * KT + 8 * (r >> 2) + 4 * lh + (r & 3);
+            const int key = (t0 + tt) * KT + 8 * (r >> 2) + 4 * lh + (r & 3);
             if (key >= a.Nkv) sv[r] = -INFINITY;
         }
     };
@@ -324,7 +329,7 @@ __global__ __launch_bounds__(NTHR, HD == 64 ? 3 : 2) void k_attn(AttnArgs a, int
     };
     using T_ = std::true_type;
     using F_ = std::false_type;
-    const bool partial = (a.Nkv % KT) != 0;
+    const bool partial = (a.Nkv % KT) != 0 && t0 + ntiles == ntiles_all;
 
     issue_k(0);
     if (ntiles > 1) issue_k(1);
@@ -344,6 +349,21 @@ __global__ __launch_bounds__(NTHR, HD == 64 ? 3 : 2) void k_attn(AttnArgs a, int
     iter(ntiles, F_{}, F_{}, F_{}, T_{});
 
     lsum += __shfl_xor(lsum, 32, 64);
+    if (a.nsplit > 1) {
+        // unnormalised partial output and its statistics (exp2 domain) for
+        // the combining pass
+        if (qvalid) {
+            const int64_t prow = ((int64_t)blockIdx.z * a.BH + bh) * a.Nq + qi;
+#pragma unroll
+            for (int dt = 0; dt < G::DT; dt++)
+#pragma unroll
+                for (int g = 0; g < 4; g++)
+                    *(float4 *)(a.part_o + prow * HD + dt * 32 + 8 * g + 4 * lh) =
+                        make_float4(o[dt][4 * g], o[dt][4 * g + 1], o[dt][4 * g + 2], o[dt][4 * g + 3]);
+            if (lh == 0) *(float2 *)(a.part_ml + prow * 2) = make_float2(mrun, lsum);
+        }
+        return;
+    }
     const float inv = (lsum == 0.f) ? 0.f : 1.0f / lsum;
 #pragma unroll
     for (int dt = 0; dt < G::DT; dt++)
@@ -427,19 +447,62 @@ __global__ __launch_bounds__(NTHR, HD == 64 ? 3 : 2) void k_attn(AttnArgs a, int
     }
 }
 
+// Combine the key-range partials: O = Σ_s 2^(m_s − M)·O_s / Σ_s 2^(m_s − M)·l_s.
+// One thread per (batch·head, query, 4 channels).
+__global__ void k_attn_combine(AttnArgs a, int hd, int64_t total) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    const int d = (int)(i % (hd / 4)) * 4;
+    const int64_t r = i / (hd / 4);  // bh·Nq + q
+    const int64_t plane = (int64_t)a.BH * a.Nq;
+    float M = -INFINITY;
+    for (int s = 0; s < a.nsplit; s++) M = fmaxf(M, a.part_ml[(s * plane + r) * 2]);
+    float den = 0.f;
+    float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s = 0; s < a.nsplit; s++) {
+        const float2 ml = *(const float2 *)(a.part_ml + (s * plane + r) * 2);
+        const float w = __builtin_amdgcn_exp2f(ml.x - M);
+        den = __builtin_fmaf(w, ml.y, den);
+        const float4 o = *(const float4 *)(a.part_o + (s * plane + r) * hd + d);
+        num.x = __builtin_fmaf(w, o.x, num.x);
+        num.y = __builtin_fmaf(w, o.y, num.y);
+        num.z = __builtin_fmaf(w, o.z, num.z);
+        num.w = __builtin_fmaf(w, o.w, num.w);
+    }
+    const float inv = den == 0.f ? 0.f : 1.0f / den;
+    const int64_t bh = r / a.Nq, q = r % a.Nq;
+    const int64_t b = bh / a.NH, h = bh % a.NH;
+    float *dst = (float *)a.out.x + (b * a.Nq + q) * a.out.ld + h * hd + d;
+    *(float4 *)dst = make_float4(num.x * inv, num.y * inv, num.z * inv, num.w * inv);
+}
+
 }  // namespace
 
 hipError_t launch_attn(const AttnArgs &a, hipStream_t st) {
     // Vᵀ rows hold vt_ld_for(Nkv) keys (zero past Nkv, in vt_slot order)
     const int ldv = (int)vt_ld_for(a.Nkv);
     const int hd = a.hd > 0 ? a.hd : 64;
-    if ((hd != 64 && hd != 128) || a.BH <= 0 || a.BH > 65535 || a.Nq <= 0 || a.Nkv <= 0) return hipErrorInvalidValue;
+    if ((hd != 64 && hd != 128 && hd != 256) || a.BH <= 0 || a.BH > 65535 || a.Nq <= 0 || a.Nkv <= 0)
+        return hipErrorInvalidValue;
+    const int ntiles = (a.Nkv + 31) / 32;
+    if (a.nsplit < 1 || a.nsplit > ntiles) return hipErrorInvalidValue;
+    if (a.nsplit > 1) {
+        // every range must hold a tile; plain layouts, f32 output
+        const int per = (ntiles + a.nsplit - 1) / a.nsplit;
+        if ((int64_t)per * (a.nsplit - 1) >= ntiles || !a.part_o || !a.part_ml || a.out.kind != A_F32 ||
+            a.wo > 0 || a.grid > 0 || (a.hd_out > 0 && a.hd_out != hd))
+            return hipErrorInvalidValue;
+    }
+    // head dim 256: fp16 operands only
+    if (hd == 256 && (a.q_lo || a.wo > 0 || (a.hd_out > 0 && a.hd_out != hd))) return hipErrorInvalidValue;
     // a Q8 output block must lie inside one head
     if ((a.out.kind == A_Q8_0 || a.out.kind == A_Q8_1) && a.hd_out > 0 && a.hd_out % 32 != 0)
         return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((a.Nq + QT - 1) / QT), (unsigned)a.BH);
+    const dim3 grid((unsigned)((a.Nq + QT - 1) / QT), (unsigned)a.BH, (unsigned)a.nsplit);
     const bool crop = a.wo > 0 || (a.hd_out > 0 && a.hd_out != hd);
-    if (hd == 64 && !crop) {
+    if (hd == 256) {
+        hipLaunchKernelGGL((k_attn<false, 256, false>), grid, dim3(NTHR), 0, st, a, ldv);
+    } else if (hd == 64 && !crop) {
         if (a.q_lo) hipLaunchKernelGGL((k_attn<true, 64, false>), grid, dim3(NTHR), 0, st, a, ldv);
         else hipLaunchKernelGGL((k_attn<false, 64, false>), grid, dim3(NTHR), 0, st, a, ldv);
     } else if (hd == 64) {
@@ -448,6 +511,10 @@ hipError_t launch_attn(const AttnArgs &a, hipStream_t st) {
     } else {
         if (a.q_lo) hipLaunchKernelGGL((k_attn<true, 128, true>), grid, dim3(NTHR), 0, st, a, ldv);
         else hipLaunchKernelGGL((k_attn<false, 128, true>), grid, dim3(NTHR), 0, st, a, ldv);
+    }
+    if (a.nsplit > 1) {
+        const int64_t total = (int64_t)a.BH * a.Nq * (hd / 4);
+        hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, a, hd, total);
     }
     return hipGetLastError();
 }

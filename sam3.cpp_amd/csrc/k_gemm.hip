@@ -150,7 +150,7 @@ template <int EPI, int BM, int NT_>
 __device__ __forceinline__ void epilogue(const GemmParams &p, const float *Ct, int m0, int n0, int t) {
     const EpiArgs &e = p.e;
     if constexpr (EPI == EPI_QKV) {
-        const int sel = n0 / e.E;  // 0 = Q, 1 = K, 2 = V (a tile never straddles)
+        const int sel = n0 / e.E + e.sel0;  // 0 = Q, 1 = K, 2 = V (a tile never straddles)
         const int Nw = e.window * e.window;
         const int nwx = e.grid / e.window;
         if (sel == 2) {
@@ -165,7 +165,7 @@ __device__ __forceinline__ void epilogue(const GemmParams &p, const float *Ct, i
                 if (gm >= p.M) continue;
                 const int gn = n0 + col;
                 const float bv = e.bias[gn];
-                const int r2 = gn - 2 * e.E;
+                const int r2 = gn - (2 - e.sel0) * e.E;
                 const int h = r2 / e.HD, d = r2 % e.HD;
                 const int py = gm / e.grid, px = gm % e.grid;
                 const int b = (py / e.window) * nwx + px / e.window;
@@ -209,9 +209,9 @@ __device__ __forceinline__ void epilogue(const GemmParams &p, const float *Ct, i
                 const int py = gm / e.grid, px = gm % e.grid;
                 const int b = (py / e.window) * nwx + px / e.window;
                 const int pp = (py % e.window) * e.window + px % e.window;
-                const int r2 = gn0 - sel * e.E;
+                const int r2 = gn0 - (sel - e.sel0) * e.E;
                 const int h = r2 / e.HD, d0 = r2 % e.HD;
-                if (e.freqs) {
+                if (e.freqs && (e.rope_rows <= 0 || gm < e.rope_rows)) {
                     // sam3_apply_rope: out_re = re·cos − im·sin, out_im = re·sin + im·cos,
                     // each product rounded on its own (separate ggml ops).
                     const float4 *f4 = (const float4 *)(e.freqs + ((int64_t)pp * (e.HD / 2) + d0 / 2) * 2);
@@ -345,6 +345,18 @@ __device__ __forceinline__ void epilogue(const GemmParams &p, const float *Ct, i
                         const float x = __fadd_rn(v[j + i], bj[i]);
                         const float t = (float)__builtin_bit_cast(_Float16, e.gelu_tab[half_bits(x)]);
                         v[j + i] = x <= -10.f ? 0.f : (x >= 10.f ? x : t);
+                    }
+                }
+            } else if (e.relu) {
+                // ggml_relu: x > 0 ? x : 0
+#pragma unroll
+                for (int j = 0; j < 32; j += 4) {
+                    const float4 bb = *(const float4 *)(e.bias + gn0 + j);
+                    const float bj[4] = {bb.x, bb.y, bb.z, bb.w};
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const float x = __fadd_rn(v[j + i], bj[i]);
+                        v[j + i] = x > 0.f ? x : 0.f;
                     }
                 }
             } else {

@@ -301,7 +301,20 @@ __global__ __launch_bounds__(256) void k_copy(uint4 *__restrict__ dst, const uin
         dst[i] = src[i];
 }
 
+// y = a + b·s (ggml_scale, then ggml_add: the product is rounded first)
+__global__ __launch_bounds__(256) void k_add_scaled(float *__restrict__ y, const float *__restrict__ a,
+                                                    const float *__restrict__ b, float s, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = __fadd_rn(a[i], __fmul_rn(b[i], s));
+}
+
 }  // namespace
+
+hipError_t launch_add_scaled(float *y, const float *a, const float *b, float s, int64_t n, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_add_scaled, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, y, a, b, s, n);
+    return hipGetLastError();
+}
 
 hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t st) {
     const int64_t n = (int64_t)(bytes / 16);

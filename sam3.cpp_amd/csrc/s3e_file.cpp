@@ -285,6 +285,45 @@ int write_model(const char *path, uint32_t magic, int32_t version, int ftype, in
 
 using namespace s3e;
 
+namespace {
+
+// Memory attention (sam3.cpp:3034-3060, :2004-2040): D = neck_dim, MD = 64,
+// FFN 2048; appended after the encoder's tensors.
+void add_mem_attn(std::vector<SynthTensor> &ts, int layers, int D) {
+    const int MD = 64, FFN = 2048;
+    for (int l = 0; l < layers; l++) {
+        const std::string p = "mem_attn.layers." + std::to_string(l);
+        for (const char *a : {".sa.q_proj", ".sa.k_proj", ".sa.v_proj", ".sa.out_proj"}) {
+            ts.push_back({p + a + ".weight", {D, D}, 0, true, false});
+            ts.push_back({p + a + ".bias", {D}, 2, false, false});
+        }
+        ts.push_back({p + ".norm1.weight", {D}, 1, false, false});
+        ts.push_back({p + ".norm1.bias", {D}, 2, false, false});
+        ts.push_back({p + ".ca.q_proj.weight", {D, D}, 0, true, false});
+        ts.push_back({p + ".ca.q_proj.bias", {D}, 2, false, false});
+        ts.push_back({p + ".ca.k_proj.weight", {MD, D}, 0, true, false});
+        ts.push_back({p + ".ca.k_proj.bias", {D}, 2, false, false});
+        ts.push_back({p + ".ca.v_proj.weight", {MD, D}, 0, true, false});
+        ts.push_back({p + ".ca.v_proj.bias", {D}, 2, false, false});
+        ts.push_back({p + ".ca.out_proj.weight", {D, D}, 0, true, false});
+        ts.push_back({p + ".ca.out_proj.bias", {D}, 2, false, false});
+        ts.push_back({p + ".norm2.weight", {D}, 1, false, false});
+        ts.push_back({p + ".norm2.bias", {D}, 2, false, false});
+        ts.push_back({p + ".linear1.weight", {D, FFN}, 0, true, false});
+        ts.push_back({p + ".linear1.bias", {FFN}, 2, false, false});
+        ts.push_back({p + ".linear2.weight", {FFN, D}, 0, true, false});
+        ts.push_back({p + ".linear2.bias", {D}, 2, false, false});
+        ts.push_back({p + ".norm3.weight", {D}, 1, false, false});
+        ts.push_back({p + ".norm3.bias", {D}, 2, false, false});
+    }
+    if (layers > 0) {
+        ts.push_back({"mem_attn.norm.weight", {D}, 1, false, false});
+        ts.push_back({"mem_attn.norm.bias", {D}, 2, false, false});
+    }
+}
+
+}  // namespace
+
 extern "C" int s3e_synth_write(const char *path, const s3e_synth_cfg *cfg) {
     if (!path || !cfg) { set_error("s3e_synth_write: null argument"); return S3E_ERR_INVALID; }
     const int ftype = cfg->ftype;
@@ -369,6 +408,11 @@ extern "C" int s3e_synth_write(const char *path, const s3e_synth_cfg *cfg) {
     };
     if (cfg->neck == 2) add_neck("neck.det.");
     if (cfg->neck >= 1) add_neck("neck.trk.");
+    if (cfg->mem_attn_layers < 0 || cfg->mem_attn_layers > 16) {
+        set_error("s3e_synth_write: mem_attn_layers %d out of range", cfg->mem_attn_layers);
+        return S3E_ERR_INVALID;
+    }
+    add_mem_attn(ts, cfg->mem_attn_layers, D);
 
     // hparams in sam3_load_hparams order (sam3.cpp:1477-1520)
     const std::vector<int32_t> hp = {img, P, E, cfg->depth, cfg->heads, cfg->mlp_ratio_x1000, WS, 4,
@@ -379,7 +423,7 @@ extern "C" int s3e_synth_write(const char *path, const s3e_synth_cfg *cfg) {
                                      1024, 16, 24, 32, 49408, 256,  // text
                                      D,                             // neck_dim
                                      6, 8, 2048, 6, 8, 2048, 200, 3, 1, 4,
-                                     256, 2, 3, 3, 64, 4, 7, 16, 2,
+                                     256, 2, 3, 3, 64, cfg->mem_attn_layers > 0 ? cfg->mem_attn_layers : 4, 7, 16, 2,
                                      cfg->neck == 2 ? 0 : 1};       // visual_only
     return write_model(path, 0x73616D33u, 3, ftype, wtype, hp, ts, cfg->seed, sd, rnd_affine, HD);
 }
@@ -445,6 +489,11 @@ extern "C" int s3e_synth_write_sam2(const char *path, const s3e_synth_sam2_cfg *
         ts.push_back({p + ".weight", {1, 1, ch, D}, 0, false, false});
         ts.push_back({p + ".bias", {D}, 2, false, false});
     }
+    if (cfg->mem_attn_layers < 0 || cfg->mem_attn_layers > 16) {
+        set_error("s3e_synth_write_sam2: mem_attn_layers %d out of range", cfg->mem_attn_layers);
+        return S3E_ERR_INVALID;
+    }
+    add_mem_attn(ts, cfg->mem_attn_layers, D);
     std::vector<int32_t> hp = {S, 1, E0, cfg->num_heads, 4};
     for (int i = 0; i < 4; i++) hp.push_back(cfg->stages[i]);
     hp.push_back(cfg->global_n);
@@ -461,6 +510,7 @@ extern "C" int s3e_synth_write_sam2(const char *path, const s3e_synth_sam2_cfg *
     // (convert_sam2_to_ggml.py:44-75)
     for (int32_t v : {256, 2, 3, 3, 64, 4, 7, 16, 2000, -1000, 1, 1, 1, 1, 1, 1, 0, 1, 0, 1, 1, 1, 1, 1, 1})
         hp.push_back(v);
+    if (cfg->mem_attn_layers > 0) hp[32 + 5] = cfg->mem_attn_layers;  // mem_attn_layers
     if (hp.size() != 57) { set_error("s3e_synth_write_sam2: internal hparams count"); return S3E_ERR_INVALID; }
     const int wtype = ftype;  // ggml type ids equal the ftype codes used here
     return write_model(path, 0x73616D32u, 1, ftype, wtype, hp, ts, cfg->seed, sd, rnd_affine, 0);

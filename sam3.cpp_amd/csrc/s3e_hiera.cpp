@@ -30,6 +30,7 @@
 #include <vector>
 
 #include "s3e_hiera.h"
+#include "s3e_memattn.h"
 #include "s3e_rt.h"
 
 namespace s3e {
@@ -209,7 +210,7 @@ int hd_pad(int hd) { return hd <= 64 ? 64 : 128; }
 
 }  // namespace
 
-int hiera_load(int device, std::ifstream &fin, int ftype, int32_t n_tensors, HieraModel **out) {
+int hiera_load(int device, std::ifstream &fin, int ftype, int32_t n_tensors, HieraModel **out, MemAttnModel **ma) {
     (void)device;
     *out = nullptr;
     std::unique_ptr<HieraModel> m(new HieraModel);
@@ -277,6 +278,13 @@ int hiera_load(int device, std::ifstream &fin, int ftype, int32_t n_tensors, Hie
         const int64_t n_el = t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3];
         if (t.ne[0] % ggml_blck(t.type) != 0) { set_error("s3e_model_load: '%s' ne0 not a block multiple", name.c_str()); return S3E_ERR_IO; }
         const size_t bytes = ggml_rowsize(t.type, t.ne[0]) * (size_t)(n_el / t.ne[0]);
+        if (memattn_wants(name)) {
+            t.data.resize(bytes);
+            if (!fin.read((char *)t.data.data(), (std::streamsize)bytes)) { set_error("s3e_model_load: truncated data of '%s'", name.c_str()); return S3E_ERR_IO; }
+            const int rc = memattn_take(ma, name, std::move(t), wtype);
+            if (rc != S3E_OK) return rc;
+            continue;
+        }
         if (name.compare(0, 6, "hiera.") != 0 && name.compare(0, 4, "fpn.") != 0) {
             fin.seekg((std::streamoff)bytes, std::ios::cur);
             if (!fin) { set_error("s3e_model_load: truncated data of '%s'", name.c_str()); return S3E_ERR_IO; }

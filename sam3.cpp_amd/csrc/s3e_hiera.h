@@ -15,7 +15,9 @@ struct HieraState;
 
 // Read the SAM 2 hparams and tensor records that follow the 16-byte header
 // (sam2_load_hparams + sam3_load_tensors, sam3.cpp:1564-1626, :3091-3194).
-int hiera_load(int device, std::ifstream &fin, int ftype, int32_t n_tensors, HieraModel **out);
+struct MemAttnModel;
+// "mem_attn.*" records go to *ma (s3e_memattn.h), created when present.
+int hiera_load(int device, std::ifstream &fin, int ftype, int32_t n_tensors, HieraModel **out, MemAttnModel **ma);
 void hiera_free(HieraModel *m);
 // img_size, −1 (marks a Hiera model), embed_dim, blocks, heads, stages[4],
 // q_pool, window_spec[0], scalp, ftype, level-0 side, neck_dim, 1 (tracker FPN)

@@ -120,6 +120,10 @@ struct EpiArgs {
     int vt_ld = 0;                 // row stride of Vᵀ in keys (vt_ld_for of the window size)
     // EPI_HQKV: grid height (grid = width), padded head dim, Q pooled later
     int grid_h = 0, hdp = 0, qpool = 0;
+    // EPI_QKV: the first column block is sel0 (0 Q, 1 K, 2 V) — a product with
+    // only K or only V columns; RoPE only on tokens below rope_rows (0: all)
+    int sel0 = 0, rope_rows = 0;
+    int relu = 0;                  // EPI_GELU: ReLU instead of GELU
     // EPI_DECONV: input width (pixels per row) and output channels; column n
     // of the GEMM is kernel tap q = n / cout (ky = q / 2, kx = q % 2),
     // channel n % cout, written to output pixel (2y + ky, 2x + kx)
@@ -168,6 +172,12 @@ struct AttnArgs {
     // b % nwx) sits at (y, x) = (wy·wo + i / wo, wx·wo + i % wo) of an
     // out_h × out_w grid, row y·out_w + x; positions outside are dropped
     int wo = 0, nwx = 0, out_h = 0, out_w = 0;
+    // split over keys (nsplit > 1): each of nsplit key ranges writes its
+    // unnormalised output to part_o [nsplit][BH][Nq][hd] and (m, l) to
+    // part_ml [nsplit][BH][Nq][2]; a combining pass then writes out (A_F32,
+    // row b·Nq + i, column h·hd + d).  Plain layouts only (no crop, grid 0).
+    int nsplit = 1;
+    float *part_o = nullptr, *part_ml = nullptr;
     Act out;                       // A_Q8_0 / A_Q8_1 / A_F16 / A_F32, row = token, col = h*64 + d
 };
 
@@ -227,6 +237,8 @@ hipError_t launch_attn_prep(const float *q, const int64_t q_nb[4], const float *
 hipError_t launch_im2col(const float *chw, int img, int P, int64_t ldk, AKind kind, void *out,
                          hipStream_t st);
 hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t st);
+// y = a + b·s elementwise (n floats; y may alias a)
+hipError_t launch_add_scaled(float *y, const float *a, const float *b, float s, int64_t n, hipStream_t st);
 
 // ---- Hiera (k_hiera.hip) ----
 // Patch-embedding im2col: CHW f32 [3][S][S], k×k / stride / pad → rows of ldk.

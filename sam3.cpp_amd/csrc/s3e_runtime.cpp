@@ -21,6 +21,7 @@
 #include "s3e_internal.h"
 #include "s3e_rt.h"
 #include "s3e_hiera.h"
+#include "s3e_memattn.h"
 
 namespace s3e {
 
@@ -709,6 +710,7 @@ struct s3e_model {
     int32_t neck_dim = 0, visual_only = 1;
     std::vector<void *> owned;  // device f32 arrays
     HieraModel *hiera = nullptr;  // SAM 2.x files: the Hiera encoder instead of the ViT
+    MemAttnModel *ma = nullptr;   // the tracker's memory attention, when the file has it
 };
 
 namespace {
@@ -839,6 +841,7 @@ int check_neck(const s3e_model *m, int which) {
 extern "C" void s3e_model_free(s3e_model *m) {
     if (!m) return;
     if (m->hiera) hiera_free(m->hiera);
+    if (m->ma) memattn_free(m->ma);
     free_weight(m->patch_w);
     for (auto &nk : m->necks)
         for (auto &sc : nk.s) {
@@ -875,7 +878,8 @@ extern "C" int s3e_model_load(s3e_ctx *ctx, const char *path, s3e_model **out) {
         std::unique_ptr<s3e_model, void (*)(s3e_model *)> m2(new s3e_model, s3e_model_free);
         m2->ctx = ctx;
         m2->ftype = ftype;
-        const int rc = hiera_load(ctx->device, fin, ftype, n_tensors, &m2->hiera);
+        int rc = hiera_load(ctx->device, fin, ftype, n_tensors, &m2->hiera, &m2->ma);
+        if (rc == S3E_OK) rc = memattn_finish(m2->ma);
         if (rc != S3E_OK) return rc;
         m2->img = hiera_img_size(m2->hiera);
         m2->necks_present = 1;
@@ -945,6 +949,13 @@ extern "C" int s3e_model_load(s3e_ctx *ctx, const char *path, s3e_model **out) {
         if (t.ne[0] % ggml_blck(t.type) != 0) { set_error("s3e_model_load: '%s' ne0 not a block multiple", name.c_str()); return S3E_ERR_IO; }
         const size_t bytes = ggml_rowsize(t.type, t.ne[0]) * (size_t)(n_el / t.ne[0]);
         const bool is_neck = name.compare(0, 9, "neck.det.") == 0 || name.compare(0, 9, "neck.trk.") == 0;
+        if (memattn_wants(name)) {
+            t.data.resize(bytes);
+            if (!rd(t.data.data(), bytes)) { set_error("s3e_model_load: truncated data of '%s'", name.c_str()); return S3E_ERR_IO; }
+            const int rc = memattn_take(&m->ma, name, std::move(t), wtype);
+            if (rc != S3E_OK) return rc;
+            continue;
+        }
         if (name.compare(0, 4, "vit.") != 0 && !is_neck) {  // not part of the encoder: skip
             fin.seekg((std::streamoff)bytes, std::ios::cur);
             if (!fin) { set_error("s3e_model_load: truncated data of '%s'", name.c_str()); return S3E_ERR_IO; }
@@ -1058,6 +1069,7 @@ extern "C" int s3e_model_hparams(const s3e_model *m, int32_t out[16]) {
 struct s3e_state {
     s3e_ctx *ctx = nullptr;
     const s3e_model *m = nullptr;
+    MemAttnState *mas = nullptr;  // memory-attention scratch, made at first use
     int64_t T = 0;
     float *x = nullptr;       // residual stream, T × E f32 ("vit_output" after encode)
     float *chw = nullptr;     // uploaded image for the host-pointer entry points
@@ -1086,6 +1098,7 @@ extern "C" void s3e_state_free(s3e_state *st) {
     if (!st) return;
     (void)hipSetDevice(st->ctx->device);
     (void)hipStreamSynchronize(st->ctx->stream);
+    if (st->mas) memattn_state_free(st->mas);
     if (st->x) (void)hipFree(st->x);
     if (st->chw) (void)hipFree(st->chw);
     st->a1.release();
@@ -1453,6 +1466,23 @@ extern "C" int s3e_run_neck(s3e_state *st, const float *x_device) {
     HIP_TRY(hipSetDevice(st->ctx->device));
     HIP_TRY(run_necks(st, x_device));
     return S3E_OK;
+}
+
+extern "C" int s3e_mem_attn_dims(const s3e_model *m, int32_t out[4]) {
+    if (!m || !out) { set_error("s3e_mem_attn_dims: NULL argument"); return S3E_ERR_INVALID; }
+    if (!m->ma) { set_error("s3e_mem_attn_dims: the model file has no memory attention"); return S3E_ERR_UNSUPPORTED; }
+    memattn_dims(m->ma, out);
+    return S3E_OK;
+}
+
+extern "C" int s3e_mem_attn(s3e_state *st, const float *curr, const float *src_pos, int64_t N, const float *prompt,
+                            const float *prompt_pos, int64_t M_total, int64_t num_obj_ptr_tokens, const float *rope_q,
+                            const float *rope_k, float *out) {
+    if (!st) { set_error("s3e_mem_attn: NULL state"); return S3E_ERR_INVALID; }
+    if (!st->m->ma) { set_error("s3e_mem_attn: the model file has no memory attention"); return S3E_ERR_UNSUPPORTED; }
+    HIP_TRY(hipSetDevice(st->ctx->device));
+    return memattn_run(st->m->ma, &st->mas, curr, src_pos, N, prompt, prompt_pos, M_total, num_obj_ptr_tokens, rope_q,
+                       rope_k, out, st->ctx->stream);
 }
 
 extern "C" int s3e_hiera_block(s3e_state *st, int idx, const float *x_device, int H, int W, float *y_device) {

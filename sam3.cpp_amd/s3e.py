@@ -32,7 +32,7 @@ class SynthCfg(ctypes.Structure):
         ("heads", c_int32), ("mlp_ratio_x1000", c_int32), ("window", c_int32),
         ("n_global", c_int32), ("global_idx", c_int32 * 4),
         ("ftype", c_int32), ("seed", c_uint64), ("std", c_float),
-        ("neck", c_int32), ("neck_dim", c_int32),
+        ("neck", c_int32), ("neck_dim", c_int32), ("mem_attn_layers", c_int32),
     ]
 
 
@@ -42,7 +42,7 @@ class SynthSam2Cfg(ctypes.Structure):
         ("global_n", c_int32), ("global_idx", c_int32 * 8), ("q_pool", c_int32), ("window_spec", c_int32 * 4),
         ("bkg_h", c_int32), ("bkg_w", c_int32), ("scalp", c_int32),
         ("neck_dim", c_int32), ("fpn_td_n", c_int32), ("fpn_td", c_int32 * 4),
-        ("ftype", c_int32), ("seed", c_uint64), ("std", c_float),
+        ("ftype", c_int32), ("seed", c_uint64), ("std", c_float), ("mem_attn_layers", c_int32),
     ]
 
 
@@ -99,6 +99,9 @@ def _load() -> ctypes.CDLL:
         "s3e_vit_block": (c_int, [c_void_p, c_int, c_void_p]),
         "s3e_run_neck": (c_int, [c_void_p, c_void_p]),
         "s3e_hiera_block": (c_int, [c_void_p, c_int, c_void_p, c_int, c_int, c_void_p]),
+        "s3e_mem_attn_dims": (c_int, [c_void_p, POINTER(c_int32)]),
+        "s3e_mem_attn": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64,
+                                 c_void_p, c_void_p, c_void_p]),
         "s3e_model_type": (c_int, [c_void_p]),
         "s3e_state_tensor_info": (c_int, [c_void_p, c_char_p, P64]),
         "s3e_state_tensor_get": (c_int, [c_void_p, c_char_p, c_void_p, c_size_t]),
@@ -120,7 +123,7 @@ DECLARED = [
     "s3e_weight_info", "s3e_mul_mat", "s3e_mul_mat_q", "s3e_mul_mat_q_batch", "s3e_quantize_rows", "s3e_layer_norm", "s3e_copy",
     "s3e_flash_attn_ext", "s3e_model_load",
     "s3e_model_free", "s3e_model_hparams", "s3e_state_create", "s3e_state_free", "s3e_encode_chw",
-    "s3e_encode_chw_host", "s3e_encode_image_u8", "s3e_vit_prefix", "s3e_vit_block", "s3e_run_neck", "s3e_hiera_block", "s3e_model_type",
+    "s3e_encode_chw_host", "s3e_encode_image_u8", "s3e_vit_prefix", "s3e_vit_block", "s3e_run_neck", "s3e_hiera_block", "s3e_model_type", "s3e_mem_attn_dims", "s3e_mem_attn",
     "s3e_state_tensor_info",
     "s3e_state_tensor_get", "s3e_state_tensor_device", "s3e_synth_write", "s3e_synth_write_sam2",
 ]
@@ -134,10 +137,10 @@ def check(rc: int, what: str = "") -> None:
 
 def synth_write(path: str, *, img_size=1008, patch=14, embed_dim=1024, depth=32, heads=16,
                 mlp_ratio_x1000=4625, window=24, global_idx=(7, 15, 23, 31), ftype="q4_0",
-                seed=0, std=0.02, random_affine=False, neck=1, neck_dim=256) -> None:
+                seed=0, std=0.02, random_affine=False, neck=1, neck_dim=256, mem_attn_layers=0) -> None:
     """Write a random-init SAM 3 model file (s3e_synth_write): the ViT
     backbone plus the tracker neck (neck=1, a visual-only file), both necks
-    (neck=2) or none (neck=0)."""
+    (neck=2) or none (neck=0), and mem_attn_layers memory-attention layers."""
     cfg = SynthCfg()
     cfg.img_size, cfg.patch, cfg.embed_dim, cfg.depth = img_size, patch, embed_dim, depth
     cfg.heads, cfg.mlp_ratio_x1000, cfg.window = heads, mlp_ratio_x1000, window
@@ -149,11 +152,13 @@ def synth_write(path: str, *, img_size=1008, patch=14, embed_dim=1024, depth=32,
     cfg.seed = seed
     cfg.std = -abs(std) if random_affine else abs(std)
     cfg.neck, cfg.neck_dim = int(neck), int(neck_dim)
+    cfg.mem_attn_layers = int(mem_attn_layers)
     check(LIB.s3e_synth_write(path.encode(), ctypes.byref(cfg)), "s3e_synth_write")
 
 
 def synth_write_sam2(path: str, variant: str = "hiera_t", *, img_size=1024, ftype="f16", seed=0, std=0.02,
-                     random_affine=False, neck_dim=256, q_pool=3, scalp=1, fpn_td=(2, 3), **over) -> None:
+                     random_affine=False, neck_dim=256, q_pool=3, scalp=1, fpn_td=(2, 3), mem_attn_layers=0,
+                     **over) -> None:
     """Write a random-init SAM 2.x encoder file (s3e_synth_write_sam2); keyword
     overrides replace the variant's hparams (embed_dim, num_heads, stages,
     global_idx, window_spec, bkg)."""
@@ -177,6 +182,7 @@ def synth_write_sam2(path: str, variant: str = "hiera_t", *, img_size=1024, ftyp
     cfg.ftype = FTYPE_BY_NAME[ftype] if isinstance(ftype, str) else int(ftype)
     cfg.seed = seed
     cfg.std = -abs(std) if random_affine else abs(std)
+    cfg.mem_attn_layers = int(mem_attn_layers)
     check(LIB.s3e_synth_write_sam2(path.encode(), ctypes.byref(cfg)), "s3e_synth_write_sam2")
 
 
@@ -348,6 +354,8 @@ class Model:
         self.grid = hp[13]
         self.neck_dim, self.necks = hp[14], hp[15]  # necks: bit 0 tracker, bit 1 detector
         self.model_type = LIB.s3e_model_type(self.handle)  # 0 SAM 3, 1 SAM 3 visual-only, 2 SAM 2
+        md = (c_int32 * 4)()
+        self.mem_attn = tuple(md) if LIB.s3e_mem_attn_dims(self.handle, md) == 0 else None  # (L, D, MD, FFN)
         self.is_sam2 = self.model_type == 2
 
     def free(self):
@@ -390,6 +398,12 @@ class State:
 
     def run_neck(self, x: DeviceBuffer):
         check(LIB.s3e_run_neck(self.handle, x.ptr), "s3e_run_neck")
+
+    def mem_attn(self, curr, src_pos, N: int, prompt, prompt_pos, M_total: int, n_ptr: int, rope_q, rope_k, out):
+        """Memory attention on device buffers (s3e_mem_attn)."""
+        p = lambda b: None if b is None else (b.ptr if hasattr(b, "ptr") else b)
+        check(LIB.s3e_mem_attn(self.handle, p(curr), p(src_pos), N, p(prompt), p(prompt_pos), M_total, n_ptr,
+                               p(rope_q), p(rope_k), p(out)), "s3e_mem_attn")
 
     def hiera_block(self, idx: int, x, H: int, W: int, y):
         """Hiera block idx on device rows x ([H·W][dim_in]) into y."""

@@ -1,0 +1,167 @@
+"""GPU parity of the tracker's memory attention (sam3_build_mem_attn_graph,
+sam3.cpp:9224-9337) against the CPU oracle (oracle/orc_memattn.c, pinned by
+test_oracle_memattn.py), through s3e_mem_attn.
+
+Models are random-init SAM 2 files with the SAM 2.1 memory attention (D 256,
+MD 64, FFN 2048).  Inputs follow sam3_propagate_single (sam3.cpp:11232-11304):
+image tokens and their sinusoidal PE, a memory bank of a few frames of
+N tokens (MD channels) with PEs, object-pointer tokens at the end (keys
+without RoPE), axial RoPE tables for the queries and the spatial keys.
+
+The engine runs the attention on fp16 operands (head dim 256) with fp32
+accumulation and the GEMMs on the weight type as ggml does; tolerances:
+F32 and F16 files relative L2 ≤ 2e-3 (the F16 specification: fp16
+attention operands are the intended difference); quantized files within 3×
+the reference's noise floor — ggml's two dot-product orders and the
+oracle's own response to a one- to two-ulp perturbation of its inputs, as
+in the encoder tests — with the 1e-3 / 5e-3 specification as the floor.
+The C5 size (64×64 tokens against 7 frames of 4096 tokens + 16 pointers =
+28 736 keys, Q8_0) runs once end to end.
+"""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+import oracle_lib as orc
+
+pytestmark = pytest.mark.gpu
+
+orc.LIB.orc_set_variant.argtypes = [ctypes.c_int]
+FLOOR = 3.0
+
+
+def _inputs(D, MD, h, frames, n_ptr, seed):
+    rng = np.random.default_rng(seed)
+    N = h * h
+    curr = rng.standard_normal((N, D)).astype(np.float32)
+    src_pos = orc.sinusoidal_pe_2d(h, h, D).reshape(N, D)
+    prompt = rng.standard_normal((frames * N + n_ptr, MD)).astype(np.float32)
+    pe = orc.sinusoidal_pe_2d(h, h, MD).reshape(N, MD)
+    tpos = rng.standard_normal((frames, MD)).astype(np.float32) * 0.1  # temporal encodings per frame
+    prompt_pos = np.concatenate([pe + tpos[f] for f in range(frames)] +
+                                [rng.standard_normal((n_ptr, MD)).astype(np.float32) * 0.1]).astype(np.float32)
+    rope_q = orc.axial_cis(D, h, h)
+    rope_k = np.concatenate([rope_q] * frames) if frames else None
+    return curr, src_pos, prompt, prompt_pos, rope_q, rope_k
+
+
+def _oracle(h, args, n_ptr, variant=0):
+    orc.LIB.orc_set_variant(variant)
+    try:
+        return orc.mem_attn(h, *args[:4], n_ptr, *args[4:])
+    finally:
+        orc.LIB.orc_set_variant(0)
+
+
+def _floor(h, args, n_ptr, ref):
+    alt = _oracle(h, args, n_ptr, 1)
+    fl = [orc.rel_l2(alt, ref), orc.max_abs(alt, ref)]
+    for seed in range(2):
+        noise = np.random.default_rng(50 + seed)
+        pert = [a * (1 + 2e-7 * noise.standard_normal(a.shape)).astype(np.float32) if i in (0, 2) else a
+                for i, a in enumerate(args)]
+        y = _oracle(h, pert, n_ptr)
+        fl = [max(fl[0], orc.rel_l2(y, ref)), max(fl[1], orc.max_abs(y, ref))]
+    return fl
+
+
+def _run(ctx, st, args, n_ptr):
+    curr, src_pos, prompt, prompt_pos, rope_q, rope_k = args
+    N, D = curr.shape
+    M = prompt.shape[0]
+    bufs = [ctx.to_device(a) for a in (curr, src_pos, prompt, prompt_pos, rope_q)]
+    rk = ctx.to_device(rope_k) if rope_k is not None else None
+    out = ctx.buffer(N * D * 4)
+    st.mem_attn(bufs[0], bufs[1], N, bufs[2], bufs[3], M, n_ptr, bufs[4], rk, out)
+    ctx.sync()
+    return out.download(np.float32, (N, D))
+
+
+def _check(tag, ft, got, ref, fl):
+    rl, ma = orc.rel_l2(got, ref), orc.max_abs(got, ref)
+    print(f"{tag} {ft}: rel_l2={rl:.3e} max_abs={ma:.3e} |ref|max={np.abs(ref).max():.3f} "
+          f"noise floor {fl[0]:.2e}/{fl[1]:.2e}", flush=True)
+    if ft in ("f32", "f16"):
+        assert rl <= 2e-3
+    else:
+        assert rl <= max(1e-3, FLOOR * fl[0])
+        assert ma <= max(5e-3, FLOOR * fl[1])
+
+
+@pytest.fixture(scope="module", params=["q8_0", "q4_0", "f16", "f32"])
+def ma_model(request, tmpdir_session, ctx):
+    import s3e
+
+    ft = request.param
+    path = os.path.join(str(tmpdir_session), f"memattn_{ft}.ggml")
+    s3e.synth_write_sam2(path, "hiera_t", img_size=64, ftype=ft, seed=13, std=0.05, random_affine=True,
+                         mem_attn_layers=4, embed_dim=32, stages=(1, 1, 1, 1), global_idx=(), window_spec=(4, 4, 2, 2),
+                         bkg=(2, 2))
+    h = orc.LIB.orc_model_load(path.encode())
+    assert h, orc.LIB.orc_last_error()
+    gm = s3e.Model(ctx, path)
+    st = s3e.State(ctx, gm)
+    yield ft, h, gm, st
+    st.free()
+    gm.free()
+    orc.LIB.orc_model_free(h)
+
+
+def test_dims(ma_model):
+    ft, h, gm, st = ma_model
+    assert gm.mem_attn == (4, 256, 64, 2048) == orc.mem_attn_dims(h)
+
+
+@pytest.mark.parametrize("hside,frames,n_ptr", [(16, 2, 8), (12, 3, 16), (16, 0, 12), (8, 1, 0)])
+def test_mem_attn_matches_oracle(ma_model, ctx, hside, frames, n_ptr):
+    """Grids of 64-256 tokens, memory banks with and without pointer tokens
+    (and pointer tokens only)."""
+    ft, h, gm, st = ma_model
+    args = _inputs(256, 64, hside, frames, n_ptr, seed=hside + frames)
+    ref = _oracle(h, args, n_ptr)
+    fl = _floor(h, args, n_ptr, ref) if ft not in ("f32", "f16") else (0.0, 0.0)
+    print(f"mem_attn {ft}: N={hside * hside} M_total={args[2].shape[0]} pointer tokens={n_ptr}", flush=True)
+    got = _run(ctx, st, args, n_ptr)
+    _check(f"N={hside * hside} M={args[2].shape[0]}", ft, got, ref, fl)
+
+
+def test_mem_attn_repeatable_and_rejects(ma_model, ctx):
+    import s3e
+
+    ft, h, gm, st = ma_model
+    args = _inputs(256, 64, 8, 1, 4, seed=1)
+    a = _run(ctx, st, args, 4)
+    b = _run(ctx, st, args, 4)
+    assert np.array_equal(a, b)
+    curr = ctx.to_device(args[0])
+    with pytest.raises(s3e.S3EError):  # spatial keys without their RoPE table
+        st.mem_attn(curr, curr, 64, curr, curr, 68, 4, curr, None, curr)
+    with pytest.raises(s3e.S3EError):  # more pointer tokens than memory tokens
+        st.mem_attn(curr, curr, 64, curr, curr, 4, 8, curr, None, curr)
+
+
+def test_mem_attn_c5_size(ctx, tmpdir_session):
+    """The C5 tracking-frame shape: 64×64 tokens, 7 memory frames of 4096
+    tokens and 16 object pointers (64 tokens), Q8_0, 4 layers."""
+    import s3e
+
+    path = os.path.join(str(tmpdir_session), "memattn_c5_q8_0.ggml")
+    s3e.synth_write_sam2(path, "hiera_t", img_size=64, ftype="q8_0", seed=17, std=0.02, mem_attn_layers=4,
+                         embed_dim=32, stages=(1, 1, 1, 1), global_idx=(), window_spec=(4, 4, 2, 2), bkg=(2, 2))
+    h = orc.LIB.orc_model_load(path.encode())
+    gm = s3e.Model(ctx, path)
+    st = s3e.State(ctx, gm)
+    try:
+        args = _inputs(256, 64, 64, 7, 64, seed=7)
+        print("mem_attn C5: N=4096 M_total=28736", flush=True)
+        got = _run(ctx, st, args, 64)
+        ref = _oracle(h, args, 64)
+        alt = _oracle(h, args, 64, 1)
+        fl = (orc.rel_l2(alt, ref), orc.max_abs(alt, ref))
+        _check("C5 N=4096 M=28736", "q8_0", got, ref, fl)
+    finally:
+        st.free()
+        gm.free()
+        orc.LIB.orc_model_free(h)
