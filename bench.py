@@ -200,13 +200,31 @@ def small_m(s3e, ctx, ev, ftype: str, reps: int = 10) -> dict:
     return res
 
 
+def axial_rope(dim: int, side: int) -> np.ndarray:
+    """Axial RoPE table [side²][dim/2][2] (cos, sin) of sam3_compute_axial_cis
+    (sam3.cpp:3555-3586), theta 10000, scale 1: synthetic tracker input."""
+    q = dim // 4
+    freqs = (1.0 / np.power(np.float32(10000.0), np.arange(q, dtype=np.float32) * 4 / np.float32(dim))).astype(np.float32)
+    idx = np.arange(side * side)
+    tx = (idx % side).astype(np.float32)[:, None] * freqs[None]
+    ty = (idx // side).astype(np.float32)[:, None] * freqs[None]
+    ang = np.concatenate([tx, ty], axis=1)
+    return np.stack([np.cos(ang), np.sin(ang)], axis=-1).astype(np.float32)
+
+
 def sam2_encoders(s3e, ctx, ev, steps: int, warmup: int, runs=SAM2_RUNS) -> dict:
-    """ms/frame of the SAM 2.1 Hiera encoders at 1024² (input resident in HBM)."""
+    """ms/frame of the SAM 2.1 Hiera encoders at 1024² (input resident in HBM);
+    for Hiera-B+ also the C5 tracking frame: the encoder, then the 4-layer
+    memory attention of its 64×64 level against 7 memory frames of 4096
+    tokens (MD 64, N(0,1)) plus 16 object pointers (64 tokens), timed over
+    consecutive frames."""
     res = {}
     tmpdir = os.environ.get("TMPDIR", tempfile.gettempdir())
     for variant, ft in runs:
         path = os.path.join(tmpdir, f"s3e_bench_{variant}_{ft}.ggml")
-        s3e.synth_write_sam2(path, variant, img_size=1024, ftype=ft, seed=0, std=0.02)
+        c5 = variant == "hiera_b+"
+        s3e.synth_write_sam2(path, variant, img_size=1024, ftype=ft, seed=0, std=0.02,
+                             mem_attn_layers=4 if c5 else 0)
         model = s3e.Model(ctx, path)
         st = s3e.State(ctx, model)
         img = synthetic_image(1024)
@@ -227,6 +245,42 @@ def sam2_encoders(s3e, ctx, ev, steps: int, warmup: int, runs=SAM2_RUNS) -> dict
         name = f"{variant.replace('+', 'plus')}_{ft}_1024_ms"
         res[name] = round(ms, 3)
         log(f"{variant} {ft} 1024: {ms:.3f} ms/frame")
+        if c5:
+            rng = np.random.default_rng(5)
+            H, D, MD, frames, ptr = 64, 256, 64, 7, 64
+            N, M = H * H, frames * H * H + ptr
+            curr = st.device_view("neck_trk_2")
+            pos = st.device_view("neck_trk_pe_2")
+            prompt = ctx.to_device(rng.standard_normal((M, MD)).astype(np.float32))
+            ppos = ctx.to_device((rng.standard_normal((M, MD)) * 0.1).astype(np.float32))
+            rq = axial_rope(D, H)
+            rope_q, rope_k = ctx.to_device(rq), ctx.to_device(np.concatenate([rq] * frames))
+            out = ctx.buffer(N * D * 4)
+
+            def frame(with_encoder=True):
+                if with_encoder:
+                    st.encode_chw(chw_d)
+                st.mem_attn(curr, pos, N, prompt, ppos, M, ptr, rope_q, rope_k, out)
+
+            for _ in range(2):
+                frame()
+            ctx.sync()
+            ev.record(e0, ctx.stream)
+            for _ in range(5):
+                frame()
+            ev.record(e1, ctx.stream)
+            fms = ev.elapsed_ms(e0, e1) / 5
+            ctx.sync()
+            ev.record(e0, ctx.stream)
+            for _ in range(5):
+                frame(False)
+            ev.record(e1, ctx.stream)
+            mms = ev.elapsed_ms(e0, e1) / 5
+            ctx.sync()
+            res["c5_frame_ms"] = round(fms, 3)
+            res["c5_mem_attn_ms"] = round(mms, 3)
+            log(f"C5 tracking frame (Hiera-B+ {ft} encoder + memory attention 4096 x 28736): {fms:.3f} ms/frame, "
+                f"memory attention {mms:.3f} ms")
         st.free()
         model.free()
         try:
