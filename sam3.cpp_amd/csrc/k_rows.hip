@@ -144,7 +144,7 @@ __global__ __launch_bounds__(256) void k_rows_quant(const float *__restrict__ x,
     const int64_t row = (int64_t)blockIdx.y * 4 + (threadIdx.x >> 6);
     const int64_t f = (int64_t)blockIdx.x * 64 + lane;
     if (row >= M) return;
-    // K % 32 == 0: the 8 lanes of a block are all inside or all past the row
+    // Q8: K % 32 == 0, so the 8 lanes of a block are all inside or all past the row
     if (f >= K / 4) {
         // blocks between K and the next multiple of 128 get zero scales: the
         // GEMM reads whole groups of four blocks
@@ -259,7 +259,9 @@ hipError_t launch_layernorm(const float *x, int64_t M, int64_t E, float eps, con
 hipError_t launch_rows_quant(AKind kind, const float *x, int64_t M, int64_t K, const Act &out,
                              hipStream_t st) {
     (void)kind;
-    if (K % 32 != 0) return hipErrorInvalidValue;
+    // a Q8 block must be whole inside the row; other formats go by float4
+    const bool q8 = out.kind == A_Q8_0 || out.kind == A_Q8_1;
+    if ((q8 && K % 32 != 0) || K % 4 != 0) return hipErrorInvalidValue;
     const int64_t nf4 = (K + 127) / 128 * 32;  // float4 up to the 128-element group
     const dim3 grid((unsigned)((nf4 + 63) / 64), (unsigned)((M + 3) / 4));
     hipLaunchKernelGGL(k_rows_quant, grid, dim3(256), 0, st, x, M, K, out);

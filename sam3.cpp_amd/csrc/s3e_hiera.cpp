@@ -576,7 +576,8 @@ hipError_t hiera_block(const HieraModel *m, HieraState *s, int bi, const float *
     aa.out_w = Wt;
     const AKind kp = act_kind_for(b.proj.kind);
     const bool q8 = kp == A_Q8_0 || kp == A_Q8_1;
-    const bool direct = !q8 || HD % 32 == 0;  // a Q8 block must lie inside one head
+    // a Q8 block must lie inside one head; split pairs go through f32
+    const bool direct = kp != A_F16X2 && (!q8 || HD % 32 == 0);
     const Act a_proj = s->a1.as(kp, C);
     aa.out = direct ? a_proj : f32_act(s->attn_f32, C);
     if ((e = launch_attn(aa, st)) != hipSuccess) return e;

@@ -73,6 +73,8 @@ struct ActBuf {
         a.s = s;
         a.ld = ld;
         a.mp = mp;
+        // split fp16 pairs: the low plane fills the second half of the buffer
+        if (kind == A_F16X2) a.lo = (void *)((_Float16 *)x + cap_rows * cap_k);
         return a;
     }
 };
