@@ -303,22 +303,45 @@ __device__ __forceinline__ void epilogue(const GemmParams &p, const float *Ct, i
                 }
             }
         }
-        // Vᵀ [b][h][d][slot]: lanes run along tokens of one column, so a store
-        // instruction covers runs of consecutive key slots
-        for (int u = t; u < BM * BN; u += NT_) {
-            const int row = u % BM, col = u / BM;
-            const int gm = m0 + row, gn = n0 + col;
+        // Vᵀ [b][h][d][slot]: lanes run along pairs of tokens of one column, so a
+        // store instruction covers runs of consecutive key slots; a pair that
+        // stays inside one window row at an even position fills two adjacent
+        // slots (vt_slot keeps aligned pairs together) with one 4-byte store
+        for (int u = t; u < (BM / 2) * BN; u += NT_) {
+            const int rp = u % (BM / 2), col = u / (BM / 2);
+            const int gm = m0 + 2 * rp, gn = n0 + col;
             if (gm >= p.M || gn < 2 * C || gn >= 3 * C) continue;
-            const float v = Ct[row * CLD + col] + e.bias[gn];
+            const float bv = e.bias[gn];
+            const float v0 = Ct[(2 * rp) * CLD + col] + bv, v1 = Ct[(2 * rp + 1) * CLD + col] + bv;
             const int r2 = gn - 2 * C;
             const int h = r2 / HD, d = r2 % HD;
             const int py = gm / W, px = gm % W;
             const int b = (py / wh) * nwx + px / ww;
             const int pp = (py % wh) * ww + px % ww;
-            const int64_t o = ((int64_t)(b * e.NH + h) * HDp + d) * e.vt_ld + vt_slot(pp);
-            const _Float16 hv = to_half(v);
-            e.vt[o] = hv;
-            if (e.vt_lo) e.vt_lo[o] = (_Float16)(v - (float)hv);
+            const int64_t base = ((int64_t)(b * e.NH + h) * HDp + d) * e.vt_ld;
+            const _Float16 h0 = to_half(v0), h1 = to_half(v1);
+            const _Float16 l0 = (_Float16)(v0 - (float)h0), l1 = (_Float16)(v1 - (float)h1);
+            const bool pair = gm + 1 < p.M && px + 1 < W && (px % ww) + 1 < ww && (pp & 1) == 0;
+            if (pair) {
+                const int64_t o = base + vt_slot(pp);
+                *(uint32_t *)(e.vt + o) =
+                    (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+                if (e.vt_lo)
+                    *(uint32_t *)(e.vt_lo + o) =
+                        (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+            } else {
+                const int64_t o = base + vt_slot(pp);
+                e.vt[o] = h0;
+                if (e.vt_lo) e.vt_lo[o] = l0;
+                if (gm + 1 < p.M) {
+                    const int pyb = (gm + 1) / W, pxb = (gm + 1) % W;
+                    const int bb = (pyb / wh) * nwx + pxb / ww;
+                    const int ppb = (pyb % wh) * ww + pxb % ww;
+                    const int64_t ob = ((int64_t)(bb * e.NH + h) * HDp + d) * e.vt_ld + vt_slot(ppb);
+                    e.vt[ob] = h1;
+                    if (e.vt_lo) e.vt_lo[ob] = l1;
+                }
+            }
         }
     } else if constexpr (EPI == EPI_GELU) {
         // full 32-column blocks guaranteed by the launcher (N % 32 == 0)
