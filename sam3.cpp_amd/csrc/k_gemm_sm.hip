@@ -221,6 +221,198 @@ __global__ __launch_bounds__(64 * SM_WAVES, 2) void k_gemm_sm(SmArgs p) {
     }
 }
 
+#define LDS_PTR(p) ((__attribute__((address_space(3))) void *)(p))
+
+// Batched variant: a work-group owns 4 adjacent strips (128 columns), one
+// per wave, over the whole K range, so the activation stage (the same for
+// the four waves) is staged once in LDS by direct-to-LDS loads (rows of 128
+// bytes, 256 for F16, 16-byte chunks XOR-swizzled by row) while each wave
+// streams its own weights into registers one stage ahead.  One barrier per
+// stage releases the previous activation buffer.
+template <int WK, int MT>
+struct SmbCfg {
+    static constexpr bool quant = WK != WK_F16;
+    static constexpr int ROWB = quant ? 128 : 256;
+    static constexpr int A_BYTES = MT * 32 * ROWB;
+    static constexpr int SC_BYTES = quant ? MT * 32 * 8 : 0;               // 4 block scales per row
+    static constexpr int SS_BYTES = (WK == WK_Q4_1) ? MT * 32 * 8 : 0;      // 4 block sums per row
+    static constexpr int STAGE = A_BYTES + SC_BYTES + SS_BYTES;
+    static constexpr int NA = A_BYTES / 4096;                               // 1 KB DMA runs per wave
+    static constexpr int NBUF = 2;                                           // stages s, s+1
+};
+
+template <int R>
+__device__ __forceinline__ int smb_swz(int r) { return R == 128 ? ((r >> 1) & 7) : (r & 15); }
+
+template <int WK, int MT>
+__global__ __launch_bounds__(64 * SM_WAVES, 2) void k_gemm_smb(SmArgs p) {
+    using C = SmCfg<WK>;
+    using B = SmbCfg<WK, MT>;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[B::NBUF * B::STAGE];
+
+    const int wg = blockIdx.x;
+    const SmGemm G = p.many ? p.many[p.wg_gemm[wg]] : p.one;
+    const int t = threadIdx.x, lane = t & 63, lr = lane & 31, lh = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int n0 = ((wg - G.wg0) * SM_WAVES + wave) * 32;
+    const int n = n0 + lr;  // < Np (weights padded to 128-column groups)
+    const bool live = n0 < G.N;
+    const int nst = G.nst, M = p.M;
+    const int esize = B::quant ? 1 : 2;
+    const int64_t kbytes = (int64_t)G.K * esize;
+
+    // DMA sources of this wave's activation runs: lane fills LDS bytes
+    // [16·lane, 16·lane + 16) of run r, i.e. row (1024·r + 16·lane) / ROWB at
+    // slot c; it fetches the chunk c ^ swz(row) of that row
+    int64_t a_row[B::NA];
+    int a_ch[B::NA], a_dst[B::NA];
+#pragma unroll
+    for (int j = 0; j < B::NA; j++) {
+        const int run = wave + SM_WAVES * j;
+        const int byte = run * 1024 + lane * 16;
+        const int row = byte / B::ROWB, slot = (byte % B::ROWB) / 16;
+        a_row[j] = (int64_t)min(row, M - 1) * G.ldx * esize;
+        a_ch[j] = (slot ^ smb_swz<B::ROWB>(row)) * 16;
+        a_dst[j] = run * 1024;
+    }
+    auto issue_a = [&](int s) {
+        uint8_t *L = lds + (s % B::NBUF) * B::STAGE;
+#pragma unroll
+        for (int j = 0; j < B::NA; j++) {
+            const int64_t off = min((int64_t)s * B::ROWB + a_ch[j], kbytes - 16);
+            __builtin_amdgcn_global_load_lds((const void *)((const uint8_t *)G.x + a_row[j] + off),
+                                             LDS_PTR(L + a_dst[j]), 16, 0, 0);
+        }
+        if constexpr (B::quant) {
+            // the rows' 4 block scales of stage s are one run of MT·32·8 bytes in
+            // the stage-major plane; every wave moves it (identical bytes)
+            const int run = (wave * 256) % B::SC_BYTES;  // this wave's 256-byte run
+            const int64_t src = ((int64_t)s * G.xmp) * 8 + run + lane * 4;
+            __builtin_amdgcn_global_load_lds((const void *)((const uint8_t *)G.xd + src),
+                                             LDS_PTR(L + B::A_BYTES + run), 4, 0, 0);
+            if constexpr (WK == WK_Q4_1)
+                __builtin_amdgcn_global_load_lds((const void *)((const uint8_t *)G.xs + src),
+                                                 LDS_PTR(L + B::A_BYTES + B::SC_BYTES + run), 4, 0, 0);
+        }
+    };
+    struct WStage {
+        uint4 w[C::WL];
+        uint2 wd, wm;
+    };
+    auto load_w = [&](int s, WStage &f) {
+        const int b0 = 4 * s;
+#pragma unroll
+        for (int j = 0; j < C::WL; j++) {
+            const int blk = C::q4 ? b0 + j : (WK == WK_Q8_0 ? b0 + j : b0 + j / 2);
+            const int sub = C::q4 ? 0 : (WK == WK_Q8_0 ? lh : 2 * (j & 1) + lh);
+            f.w[j] = *(const uint4 *)(G.w + ((int64_t)blk * G.np + n) * C::BB + sub * 16);
+        }
+        if constexpr (C::quant) {
+            f.wd = *(const uint2 *)(G.wd + ((int64_t)s * G.np + n) * 4);
+            if constexpr (C::q41) f.wm = *(const uint2 *)(G.wm + ((int64_t)s * G.np + n) * 4);
+        }
+    };
+
+    v16f acc[MT];
+#pragma unroll
+    for (int i = 0; i < MT; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[i][r] = 0.f;
+
+    auto compute = [&](int s, const WStage &f) {
+        const uint8_t *L = lds + (s % B::NBUF) * B::STAGE;
+        if constexpr (C::quant) {
+            const v16i zi = {};
+            const v16f zf = {};
+            const v4i minus8 = {(int)0xF8F8F8F8, (int)0xF8F8F8F8, (int)0xF8F8F8F8, (int)0xF8F8F8F8};
+            uint2 ad[MT], as[MT];
+#pragma unroll
+            for (int i = 0; i < MT; i++) {
+                ad[i] = *(const uint2 *)(L + B::A_BYTES + (32 * i + lr) * 8);
+                if constexpr (C::q41) as[i] = *(const uint2 *)(L + B::A_BYTES + B::SC_BYTES + (32 * i + lr) * 8);
+            }
+            const uint32_t wdw[2] = {f.wd.x, f.wd.y};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                v4i b;
+                if constexpr (C::q4) {
+                    const int sh = 4 * lh;
+                    b[0] = (int)((f.w[j].x >> sh) & 0x0F0F0F0Fu);
+                    b[1] = (int)((f.w[j].y >> sh) & 0x0F0F0F0Fu);
+                    b[2] = (int)((f.w[j].z >> sh) & 0x0F0F0F0Fu);
+                    b[3] = (int)((f.w[j].w >> sh) & 0x0F0F0F0Fu);
+                } else {
+                    b = __builtin_bit_cast(v4i, f.w[j]);
+                }
+                const uint32_t hw = (wdw[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
+                const v4u hb = {hw, 0u, 0u, 0u};
+#pragma unroll
+                for (int i = 0; i < MT; i++) {
+                    const int r = 32 * i + lr;
+                    const v4i a = *(const v4i *)(L + r * B::ROWB + (((2 * j + lh) ^ smb_swz<B::ROWB>(r)) << 4));
+                    v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, zi, 0, 0, 0);
+                    if constexpr (WK == WK_Q4_0) S = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, minus8, S, 0, 0, 0);
+                    const uint32_t adw[2] = {ad[i].x, ad[i].y};
+                    const uint32_t ha_ = (adw[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
+                    const v4u ha = {ha_, 0u, 0u, 0u};
+                    const v16f Cs = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, ha),
+                                                                          __builtin_bit_cast(v8h, hb), zf, 0, 0, 0);
+#pragma unroll
+                    for (int r2 = 0; r2 < 16; r2++) acc[i][r2] = __builtin_fmaf((float)S[r2], Cs[r2], acc[i][r2]);
+                }
+            }
+            if constexpr (C::q41) {
+                const v4u hb = {f.wm.x, f.wm.y, 0u, 0u};
+#pragma unroll
+                for (int i = 0; i < MT; i++) {
+                    const v4u ha = {as[i].x, as[i].y, 0u, 0u};
+                    acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, ha),
+                                                                    __builtin_bit_cast(v8h, hb), acc[i], 0, 0, 0);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const v8h b = __builtin_bit_cast(v8h, f.w[j]);
+#pragma unroll
+                for (int i = 0; i < MT; i++) {
+                    const int r = 32 * i + lr;
+                    const v8h a = *(const v8h *)(L + r * B::ROWB + (((2 * j + lh) ^ smb_swz<B::ROWB>(r)) << 4));
+                    acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[i], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    // stage s + 1 (activations in LDS, weights in registers) is in flight while
+    // stage s is consumed; the barrier at the top of an iteration also frees
+    // the buffer stage s + 1 overwrites
+    WStage cur, nxt;
+    issue_a(0);
+    if (live) load_w(0, cur);
+    for (int s = 0; s < nst; s++) {
+        wait_and_barrier<0>();
+        const bool more = s + 1 < nst;
+        if (more) issue_a(s + 1);
+        if (more && live) load_w(s + 1, nxt);
+        if (live) compute(s, cur);
+        if (more && live) cur = nxt;
+    }
+
+    if (!live) return;
+    constexpr float kScale = C::quant ? 0.5f : 1.0f;  // the scale products are doubled
+    const int gn = n0 + lr;
+    if (gn >= G.N) return;
+    const float bv = G.bias ? G.bias[gn] : 0.f;
+#pragma unroll
+    for (int i = 0; i < MT; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int row = 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
+            if (row < M) G.y[(int64_t)row * G.ldy + gn] = acc[i][r] * kScale + bv;
+        }
+}
+
 // Block-interleaved copy for the small-M kernel from the large-M layout
 // ([Np][Kp] codes, Q4_0 stored as nibble − 8).  One thread per (block, column).
 __global__ void k_pack_sm(const uint8_t *__restrict__ q, int64_t kp, int64_t np, int64_t kb, int wk,
@@ -271,6 +463,26 @@ hipError_t launch_pack_sm(const Weight &w, void *out, hipStream_t st) {
 }
 
 int sm_wgs(int64_t N, int ks) { return (int)(((N + 31) / 32 + SM_WAVES / ks - 1) / (SM_WAVES / ks)); }
+
+hipError_t launch_gemm_smb(WKind kind, const SmArgs &a, int wgs, hipStream_t st) {
+    if (a.M <= 0 || a.M > 64 || wgs <= 0 || (a.many && !a.wg_gemm)) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)wgs), block(64 * SM_WAVES);
+    const bool two = a.M > 32;
+#define S3E_SMB(WK)                                                                              \
+    do {                                                                                         \
+        if (two) hipLaunchKernelGGL((k_gemm_smb<WK, 2>), grid, block, 0, st, a);                 \
+        else hipLaunchKernelGGL((k_gemm_smb<WK, 1>), grid, block, 0, st, a);                     \
+    } while (0)
+    switch (kind) {
+        case WK_Q4_0: S3E_SMB(WK_Q4_0); break;
+        case WK_Q4_1: S3E_SMB(WK_Q4_1); break;
+        case WK_Q8_0: S3E_SMB(WK_Q8_0); break;
+        case WK_F16: S3E_SMB(WK_F16); break;
+        default: return hipErrorInvalidValue;
+    }
+#undef S3E_SMB
+    return hipGetLastError();
+}
 
 hipError_t launch_gemm_sm(WKind kind, const SmArgs &a, int wgs, int ks, hipStream_t st) {
     if (a.M <= 0 || a.M > 64 || wgs <= 0 || ks != 4 || (a.many && !a.wg_gemm)) return hipErrorInvalidValue;

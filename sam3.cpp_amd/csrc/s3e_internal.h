@@ -216,6 +216,9 @@ int64_t sm_weight_bytes(const Weight &w);
 int sm_wgs(int64_t N, int ks);
 hipError_t launch_pack_sm(const Weight &w, void *out, hipStream_t st);
 hipError_t launch_gemm_sm(WKind kind, const SmArgs &a, int wgs, int ks, hipStream_t st);
+// Batched products (many): 4 strips per work-group, activations staged in
+// LDS; wgs = total of sm_wgs(N, 1).
+hipError_t launch_gemm_smb(WKind kind, const SmArgs &a, int wgs, hipStream_t st);
 // Neck GEMMs (k_conv.hip; WK_F16 or WK_F16X3 weights with N padded to
 // CONV_BN): EPI_DECONV / EPI_ACT / EPI_F32 on plain rows, or EPI_F32 as a
 // 3×3 implicit GEMM when g is given.

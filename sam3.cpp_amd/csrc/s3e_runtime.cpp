@@ -541,7 +541,8 @@ extern "C" int s3e_mul_mat_q_batch(s3e_ctx *ctx, int n, const s3e_weight *const 
     if (M < 1 || M > 64) { set_error("s3e_mul_mat_q_batch: M=%lld is outside 1..64", (long long)M); return S3E_ERR_UNSUPPORTED; }
     const WKind kind = w[0] ? w[0]->w.kind : WK_F32;
     std::vector<SmGemm> g((size_t)n);
-    const int ks = SM_KS;
+    // batches: four strips per work-group, activations shared through LDS
+    const int ks = 1;
     int wgs = 0;
     HIP_TRY(hipSetDevice(ctx->device));
     for (int i = 0; i < n; i++) {
@@ -596,7 +597,7 @@ extern "C" int s3e_mul_mat_q_batch(s3e_ctx *ctx, int n, const s3e_weight *const 
     sa.wg_gemm = (const uint16_t *)((const uint8_t *)ctx->sm_dev + desc_bytes);
     sa.n = n;
     sa.M = (int)M;
-    HIP_TRY(launch_gemm_sm(kind, sa, wgs, ks, ctx->stream));
+    HIP_TRY(launch_gemm_smb(kind, sa, wgs, ctx->stream));
     return S3E_OK;
 }
 

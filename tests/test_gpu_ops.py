@@ -7,8 +7,9 @@
   weight-streaming kernel of products with at most 64 rows (M = 1 .. 64,
   ragged N and K).  Both sides use the same quantized activations, so only
   fp32 accumulation order differs: relative L2 ≤ 1e-5.
-- s3e_mul_mat_q_batch: several products in one launch, bit-identical to one
-  s3e_mul_mat_q call each.
+- s3e_mul_mat_q_batch: several products in one launch, equal to one
+  s3e_mul_mat_q call each up to the order of the K-range accumulation
+  (relative L2 ≤ 1e-6), and deterministic.
 - s3e_flash_attn_ext: windowed (9 × 576) and global (5184) shapes, head dim
   64.  Default precision rounds Q, K, V and P to fp16 (fp32 accumulation):
   the F16 tolerance, relative L2 ≤ 2e-3.  F32 precision (fp16 hi/lo pairs)
@@ -159,9 +160,11 @@ def test_mul_mat_small_m(ctx, wt, N, K):
 @pytest.mark.parametrize("wt", [orc.Q4_0, orc.Q4_1, orc.Q8_0, orc.F16],
                          ids=lambda t: {1: "f16", 2: "q4_0", 3: "q4_1", 8: "q8_0"}[t])
 def test_mul_mat_q_batch_matches_single(ctx, wt):
-    """Independent products of different shapes in one launch give exactly
-    what s3e_mul_mat_q gives for each of them; a repeated batch reuses its
-    descriptors and a different one replaces them."""
+    """Independent products of different shapes in one launch match what
+    s3e_mul_mat_q gives for each of them (same block sums, the K range
+    accumulated in another order: relative L2 ≤ 1e-6) and the oracle; a
+    repeated batch reuses its descriptors and reproduces itself bit for bit,
+    and a different batch replaces them."""
     rng = np.random.default_rng(wt + 3)
     M = 48
     shapes = [(3072, 1024), (1024, 1024), (40, 96), (4736, 1024), (1024, 4736)]
@@ -183,20 +186,26 @@ def test_mul_mat_q_batch_matches_single(ctx, wt):
         y1 = ctx.buffer(M * N * 4)
         ctx.mul_mat_q(ws[-1], q, ds[-1], ss[-1], M, y1, bs[-1])
         ref.append(y1)
+    first = None
     for rep in range(2):
         ctx.mul_mat_q_batch(ws, xq, ds, ss, M, bs, ys)
         ctx.sync()
-        for (N, K), y, r in zip(shapes, ys, ref):
-            assert np.array_equal(y.download(np.float32, (M, N)), r.download(np.float32, (M, N))), (rep, N, K)
-    # a different batch (two of the products, no bias) replaces the descriptors
+        outs = [y.download(np.float32, (M, N)) for (N, K), y in zip(shapes, ys)]
+        for (N, K), o, r in zip(shapes, outs, ref):
+            assert orc.rel_l2(o, r.download(np.float32, (M, N))) <= 1e-6, (rep, N, K)
+        if first is None:
+            first = outs
+        else:
+            assert all(np.array_equal(a, b) for a, b in zip(first, outs))
+    # a different batch (two of the products, no bias) replaces the descriptors;
+    # a product does not depend on its neighbours in the batch
     ctx.mul_mat_q_batch(ws[2:4], xq[2:4], ds[2:4], ss[2:4], M, None, ys[2:4])
     ctx.sync()
     for i in (2, 3):
         N, K = shapes[i]
-        r = ctx.buffer(M * N * 4)
-        ctx.mul_mat_q(ws[i], xq[i], ds[i], ss[i], M, r)
-        ctx.sync()
-        assert np.array_equal(ys[i].download(np.float32, (M, N)), r.download(np.float32, (M, N)))
+        bias = bs[i].download(np.float32, (N,))
+        got = ys[i].download(np.float32, (M, N))
+        assert np.array_equal(got + bias, first[i]) or orc.rel_l2(got + bias, first[i]) <= 1e-6
 
 
 def test_mul_mat_q_batch_rejects(ctx):
