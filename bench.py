@@ -337,6 +337,29 @@ def summarize_stats(stats_csv: str, frames: int) -> str:
     return "\n".join(lines)
 
 
+def summarize_trace(trace_csv: str, marker: str, first: int, last: int, frames: int) -> str:
+    """Per-kernel table over a window of a rocprofv3 kernel_trace.csv: the
+    launches from the `first`-th launch of kernel `marker` (0-based) up to
+    before its `last`-th, e.g. the encoder-only frames of a run that also
+    times other work."""
+    import collections
+    import csv
+
+    rows = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"]))
+    seen, agg = -1, collections.defaultdict(list)
+    for r in rows:
+        k = _short_kernel(r["Kernel_Name"])
+        seen += k == marker
+        if first <= seen < last:
+            agg[k].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    tot = sum(sum(v) for v in agg.values())
+    lines = [f"{'kernel':28s} {'calls':>7s} {'avg_us':>9s} {'ms/frame':>9s} {'share':>7s}"]
+    for k, v in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"{k:28s} {len(v):7d} {sum(v) / len(v):9.1f} {sum(v) / 1e3 / frames:9.3f} "
+                     f"{100 * sum(v) / tot:6.2f}%")
+    return "\n".join(lines)
+
+
 def summarize_counters(fetch_csv: str, write_csv: str, cfetch_csv: str, cwrite_csv: str, copy_bytes: int,
                        kernel: str) -> str:
     """HBM bytes per launch of `kernel` from FETCH_SIZE / WRITE_SIZE (KiB per
@@ -368,6 +391,10 @@ def summarize_counters(fetch_csv: str, write_csv: str, cfetch_csv: str, cwrite_c
 def main() -> int:
     if len(sys.argv) > 1 and sys.argv[1] == "--summarize-stats":
         print(summarize_stats(sys.argv[2], int(sys.argv[3])))
+        return 0
+    if len(sys.argv) > 1 and sys.argv[1] == "--summarize-trace":
+        a = sys.argv[2:]
+        print(summarize_trace(a[0], a[1], int(a[2]), int(a[3]), int(a[4])))
         return 0
     if len(sys.argv) > 1 and sys.argv[1] == "--summarize-counters":
         a = sys.argv[2:]
