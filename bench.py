@@ -28,6 +28,10 @@ Also reported, on the same JSON line:
                   levels at 256², 128², 64²) at 1024×1024 on the same kind of
                   input: Hiera-Tiny with F16 weights and Hiera-Base+ with
                   Q8_0 weights, ms per frame.
+  preprocess    — sam3_encode_image's preprocessing on the device for a
+                  1920×1080 camera frame (resize to 1008² + normalisation):
+                  kernel time, the frame's host→device copy, and the whole
+                  s3e_encode_image_u8 call against the resident encode.
   cpu_baseline  — the CPU oracle (a C restatement of ggml's CPU path, not
                   the upstream binary) on this host: one whole frame of the
                   same model and image, backbone and neck (about 12 s on 16
@@ -305,6 +309,65 @@ def _random_ggml_bytes(wt: int, N: int, K: int, rng) -> np.ndarray:
     return out.ravel()
 
 
+CAMERA = (1920, 1080)  # a camera frame for the preprocessing leg
+
+
+def preprocess_leg(s3e, ctx, ev, st, S: int, encode_ms: float, reps: int = 20) -> dict:
+    """sam3_encode_image's preprocessing on the device (s3e_preprocess_image:
+    uint8 bilinear resize of a 1920×1080 frame to S² + normalisation into
+    CHW f32): kernel time with HIP events, algorithmic bytes w·h·3 read +
+    12·S² written (the kernel reads each source pixel about once at this
+    ratio); the pageable host→device copy of the frame; and the whole
+    s3e_encode_image_u8 call (copy + preprocessing + encode + sync) by the
+    host clock, against the resident-input encode."""
+    w, h = CAMERA
+    img = np.random.default_rng(1).integers(0, 256, (h, w, 3), dtype=np.uint8)
+    src = ctx.to_device(img)
+    chw = ctx.buffer(3 * S * S * 4)
+    for _ in range(3):
+        ctx.preprocess_image(src, w, h, S, s3e.NORM_SAM3, chw)
+    ctx.sync()
+    e0, e1 = ev.create(), ev.create()
+    ev.record(e0, ctx.stream)
+    for _ in range(reps):
+        ctx.preprocess_image(src, w, h, S, s3e.NORM_SAM3, chw)
+    ev.record(e1, ctx.stream)
+    us = ev.elapsed_ms(e0, e1) / reps * 1e3
+    ctx.sync()
+    nbytes = w * h * 3 + 12 * S * S
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        src.upload(img)
+    ctx.sync()
+    up_ms = (time.perf_counter() - t0) / reps * 1e3
+    st.encode_image_u8(img)
+    t0 = time.perf_counter()
+    for _ in range(5):
+        st.encode_image_u8(img)
+    e2e_ms = (time.perf_counter() - t0) / 5 * 1e3
+    res = {"input": f"{w}x{h} uint8 RGB -> {S}x{S}", "kernel_us": round(us, 2),
+           "kernel_GBps": round(nbytes / (us * 1e-6) / 1e9, 1), "upload_ms": round(up_ms, 3),
+           "encode_image_u8_ms": round(e2e_ms, 3), "encode_resident_ms": round(encode_ms, 3)}
+    log(f"preprocess {w}x{h} -> {S}: kernel {us:.1f} us ({res['kernel_GBps']} GB/s), upload {up_ms:.2f} ms, "
+        f"s3e_encode_image_u8 {e2e_ms:.2f} ms/frame vs {encode_ms:.2f} resident")
+    return res
+
+
+def cpu_preprocess_ms(S: int, reps: int = 3) -> float:
+    """The oracle's single-threaded sam3_resize_bilinear + sam3_preprocess_image
+    (the reference's host loop) on the same 1920×1080 frame."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as orc
+
+    w, h = CAMERA
+    img = np.random.default_rng(1).integers(0, 256, (h, w, 3), dtype=np.uint8)
+    orc.preprocess_sam3(img, S)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        orc.preprocess_sam3(img, S)
+    return (time.perf_counter() - t0) / reps * 1e3
+
+
 def cpu_baseline(path: str, img: np.ndarray, threads: int):
     """Oracle on the host: one whole frame (prefix + 32 blocks + tracker neck)
     of the same model and image, after the host preprocessing."""
@@ -409,7 +472,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "gemm_fc1_q4_0_counters.txt"))
-    ap.add_argument("--only", choices=["encode", "gemm", "copy", "neck", "sam2", "small_m"], default=None,
+    ap.add_argument("--only", choices=["encode", "gemm", "copy", "neck", "preprocess", "sam2", "small_m"], default=None,
                     help="run one leg only (for profiling runs)")
     ap.add_argument("--sam2-run", default=None, help="with --only sam2: one encoder, e.g. hiera_t:f16")
     args = ap.parse_args()
@@ -494,6 +557,9 @@ def main() -> int:
     if args.only == "neck":
         return 0
 
+    pre = preprocess_leg(s3e, ctx, ev, st, CFG["img_size"], ms_frame)
+    if args.only == "preprocess":
+        return 0
     sam2 = sam2_encoders(s3e, ctx, ev, max(3, args.steps // 2), 2)
     sm = small_m(s3e, ctx, ev, args.ftype) if args.ftype in BPW else None
 
@@ -505,10 +571,14 @@ def main() -> int:
         threads = args.cpu_threads or min(16, len(os.sched_getaffinity(0)))
         cms = cpu_baseline(path, img, threads)
         log(f"cpu baseline: {cms / 1e3:.1f} s/frame, {threads} threads")
+        pms = cpu_preprocess_ms(CFG["img_size"])
+        log(f"cpu preprocessing of a {CAMERA[0]}x{CAMERA[1]} frame: {pms:.1f} ms, 1 thread")
         cpu = {"value": round(cms, 1), "unit": "ms/frame", "cores": threads, "kind": "port",
+               "preprocess_ms": round(pms, 2),
                "sample": f"one full frame (prefix + 32 blocks + tracker neck) of the same {args.ftype.upper()} "
                          "model and image on the CPU oracle, a C restatement of ggml's CPU path (AVX2, "
-                         "OpenMP), not the upstream binary"}
+                         "OpenMP), not the upstream binary; preprocess_ms: the oracle's single-threaded resize + "
+                         "normalisation of a 1920x1080 frame to 1008x1008, the reference's host loop"}
     try:
         os.remove(path)
     except OSError:
@@ -534,6 +604,7 @@ def main() -> int:
         "breakdown": {"neck_ms": round(neck_ms, 3), "backbone_ms": round(ms_frame - neck_ms, 3)},
         "sam2_encoders": sam2,
         "small_m": sm,
+        "preprocess": pre,
         "roofline": {"kernel": f"{GEMM_KERNEL} fc1 M=5184 N=4736 K=1024 ({args.ftype})", "bound": "mfma",
                      "achieved": round(gtops, 1), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(gtops / peak, 4), "traffic": traffic,

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define S3E_ABI_VERSION 4
+#define S3E_ABI_VERSION 5
 
 enum s3e_status {
     S3E_OK = 0,
@@ -199,10 +199,25 @@ void s3e_state_free(s3e_state *st);
 int s3e_encode_chw(s3e_state *st, const float *chw_device);
 /* Same from host memory (uploads first). */
 int s3e_encode_chw_host(s3e_state *st, const float *chw_host);
-/* sam3_encode_image (sam3.h:216): HWC RGB uint8 of any size; resized and
- * normalised on the host exactly as sam3_preprocess_image
- * (sam3.cpp:3441-3514), then encoded. */
+/* sam3_encode_image (sam3.h:216): HWC RGB uint8 of any size (host memory);
+ * uploaded, resized and normalised on the device by s3e_preprocess_image
+ * with the model's normalisation (SAM 3: sam3_preprocess_image,
+ * sam3.cpp:3441-3514; SAM 2: sam2_preprocess_image, :3518-3544), then
+ * encoded.  Returns after the encode has finished. */
 int s3e_encode_image_u8(s3e_state *st, const uint8_t *hwc, int width, int height);
+
+#define S3E_NORM_SAM3 0     /* (v/255 − 0.5)/0.5 */
+#define S3E_NORM_IMAGENET 1 /* (v/255 − mean[c])/std[c], SAM 2 */
+/* Device-side preprocessing, replacing sam3_resize_bilinear + the
+ * normalisation loop of sam3_preprocess_image (sam3.cpp:3441-3514) and
+ * sam2_preprocess_image (:3518-3544): hwc_device is width × height × 3 uint8
+ * (RGB, row-major), chw_device receives 3 × img_size × img_size f32.  The
+ * resize (skipped when width = height = img_size) is the reference's
+ * half-pixel bilinear in double precision with round-half-up, so the
+ * resized bytes, and hence the output, equal the reference's bit for bit.
+ * Enqueued on the context's stream; no synchronisation. */
+int s3e_preprocess_image(s3e_ctx *ctx, const uint8_t *hwc_device, int width, int height, int img_size, int norm,
+                         float *chw_device);
 
 /* Stage hooks (sam3_test_run_vit_block_stage, sam3.h:489 / sam3.cpp:6874):
  * prefix writes x (device, T rows of E f32) from a device CHW image; block

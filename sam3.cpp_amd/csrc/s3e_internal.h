@@ -242,6 +242,9 @@ hipError_t launch_im2col(const float *chw, int img, int P, int64_t ldk, AKind ki
 hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t st);
 // y = a + b·s elementwise (n floats; y may alias a)
 hipError_t launch_add_scaled(float *y, const float *a, const float *b, float s, int64_t n, hipStream_t st);
+// HWC uint8 image of w × h → CHW f32 of S × S: bilinear resize (skipped when
+// w = h = S) and normalisation (norm 0: (v − 0.5)/0.5, 1: ImageNet mean/std).
+hipError_t launch_preprocess(const uint8_t *hwc, int w, int h, int S, int norm, float *chw, hipStream_t st);
 
 // ---- Hiera (k_hiera.hip) ----
 // Patch-embedding im2col: CHW f32 [3][S][S], k×k / stride / pad → rows of ldk.

@@ -1074,6 +1074,8 @@ struct s3e_state {
     int64_t T = 0;
     float *x = nullptr;       // residual stream, T × E f32 ("vit_output" after encode)
     float *chw = nullptr;     // uploaded image for the host-pointer entry points
+    uint8_t *img8 = nullptr;  // uint8 image of s3e_encode_image_u8, grown to the largest seen
+    size_t img8_cap = 0;
     ActBuf a1, a2, col;       // E-wide, MLP-wide and im2col activations
     _Float16 *q16 = nullptr, *k16 = nullptr, *vt16 = nullptr;  // [hi plane | lo plane]
     int64_t vt_elems = 0;
@@ -1102,6 +1104,7 @@ extern "C" void s3e_state_free(s3e_state *st) {
     if (st->mas) memattn_state_free(st->mas);
     if (st->x) (void)hipFree(st->x);
     if (st->chw) (void)hipFree(st->chw);
+    if (st->img8) (void)hipFree(st->img8);
     st->a1.release();
     st->a2.release();
     st->col.release();
@@ -1514,49 +1517,37 @@ extern "C" int s3e_encode_chw_host(s3e_state *st, const float *chw_host) {
     return s3e_encode_chw(st, st->chw);
 }
 
-// sam3_resize_bilinear + sam3_preprocess_image (sam3.cpp:3441-3514), or for
-// SAM 2 models sam2_preprocess_image's ImageNet mean/std (sam3.cpp:3518-3544),
-// on the host.
+extern "C" int s3e_preprocess_image(s3e_ctx *ctx, const uint8_t *hwc_device, int width, int height, int img_size,
+                                    int norm, float *chw_device) {
+    if (!ctx || !hwc_device || !chw_device || width <= 0 || height <= 0 || img_size <= 0 ||
+        (norm != S3E_NORM_SAM3 && norm != S3E_NORM_IMAGENET)) {
+        set_error("s3e_preprocess_image: bad argument");
+        return S3E_ERR_INVALID;
+    }
+    HIP_TRY(hipSetDevice(ctx->device));
+    HIP_TRY(launch_preprocess(hwc_device, width, height, img_size, norm, chw_device, ctx->stream));
+    return S3E_OK;
+}
+
+// sam3_encode_image's preprocessing (sam3_resize_bilinear +
+// sam3_preprocess_image, sam3.cpp:3441-3514, or sam2_preprocess_image,
+// :3518-3544, for SAM 2 models) on the device, then the encode.
 extern "C" int s3e_encode_image_u8(s3e_state *st, const uint8_t *hwc, int width, int height) {
     if (!st || !hwc || width <= 0 || height <= 0) { set_error("s3e_encode_image_u8: bad argument"); return S3E_ERR_INVALID; }
-    const int S = st->m->img;
-    std::vector<uint8_t> resized;
-    const uint8_t *px = hwc;
-    if (width != S || height != S) {
-        resized.resize((size_t)S * S * 3);
-        const double sx = (double)width / S, sy = (double)height / S;
-        for (int y = 0; y < S; ++y) {
-            double fy = (y + 0.5) * sy - 0.5;
-            if (fy < 0.0) fy = 0.0;
-            const int y0 = (int)fy, y1 = (y0 < height - 1) ? y0 + 1 : y0;
-            const double wy = fy - y0, wy0 = 1.0 - wy;
-            for (int x = 0; x < S; ++x) {
-                double fx = (x + 0.5) * sx - 0.5;
-                if (fx < 0.0) fx = 0.0;
-                const int x0 = (int)fx, x1 = (x0 < width - 1) ? x0 + 1 : x0;
-                const double wx = fx - x0, wx0 = 1.0 - wx;
-                for (int c = 0; c < 3; ++c) {
-                    const double p00 = hwc[(y0 * width + x0) * 3 + c], p01 = hwc[(y0 * width + x1) * 3 + c];
-                    const double p10 = hwc[(y1 * width + x0) * 3 + c], p11 = hwc[(y1 * width + x1) * 3 + c];
-                    const double v = wy0 * (wx0 * p00 + wx * p01) + wy * (wx0 * p10 + wx * p11);
-                    int iv = (int)(v + 0.5);
-                    iv = iv < 0 ? 0 : (iv > 255 ? 255 : iv);
-                    resized[((size_t)y * S + x) * 3 + c] = (uint8_t)iv;
-                }
-            }
-        }
-        px = resized.data();
+    HIP_TRY(hipSetDevice(st->ctx->device));
+    const size_t bytes = (size_t)width * height * 3;
+    if (bytes > st->img8_cap) {
+        HIP_TRY(hipStreamSynchronize(st->ctx->stream));
+        if (st->img8) (void)hipFree(st->img8);
+        st->img8 = nullptr;
+        st->img8_cap = 0;
+        HIP_TRY(hipMalloc(&st->img8, bytes));
+        st->img8_cap = bytes;
     }
-    std::vector<float> chw((size_t)3 * S * S);
-    static const float mean2[3] = {0.485f, 0.456f, 0.406f}, std2[3] = {0.229f, 0.224f, 0.225f};
-    const bool sam2 = st->m->hiera != nullptr;
-    for (int c = 0; c < 3; ++c)
-        for (int y = 0; y < S; ++y)
-            for (int x = 0; x < S; ++x) {
-                const float v = px[((size_t)y * S + x) * 3 + c] / 255.0f;
-                chw[(size_t)c * S * S + (size_t)y * S + x] = sam2 ? (v - mean2[c]) / std2[c] : (v - 0.5f) / 0.5f;
-            }
-    const int rc = s3e_encode_chw_host(st, chw.data());
+    HIP_TRY(hipMemcpyAsync(st->img8, hwc, bytes, hipMemcpyHostToDevice, st->ctx->stream));
+    const int norm = st->m->hiera ? S3E_NORM_IMAGENET : S3E_NORM_SAM3;
+    int rc = s3e_preprocess_image(st->ctx, st->img8, width, height, st->m->img, norm, st->chw);
+    if (rc == S3E_OK) rc = s3e_encode_chw(st, st->chw);
     if (rc != S3E_OK) return rc;
     return s3e_ctx_sync(st->ctx);
 }

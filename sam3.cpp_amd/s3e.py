@@ -22,6 +22,10 @@ PREC_DEFAULT, PREC_F32 = 0, 1
 FTYPE_BY_NAME = {"f32": 0, "f16": 1, "q4_0": 2, "q4_1": 3, "q8_0": 8}
 
 
+NORM_SAM3 = 0      # (v/255 - 0.5)/0.5
+NORM_IMAGENET = 1  # (v/255 - mean)/std, SAM 2
+
+
 class S3EError(RuntimeError):
     pass
 
@@ -95,6 +99,7 @@ def _load() -> ctypes.CDLL:
         "s3e_encode_chw": (c_int, [c_void_p, c_void_p]),
         "s3e_encode_chw_host": (c_int, [c_void_p, c_void_p]),
         "s3e_encode_image_u8": (c_int, [c_void_p, c_void_p, c_int, c_int]),
+        "s3e_preprocess_image": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p]),
         "s3e_vit_prefix": (c_int, [c_void_p, c_void_p, c_void_p]),
         "s3e_vit_block": (c_int, [c_void_p, c_int, c_void_p]),
         "s3e_run_neck": (c_int, [c_void_p, c_void_p]),
@@ -123,7 +128,7 @@ DECLARED = [
     "s3e_weight_info", "s3e_mul_mat", "s3e_mul_mat_q", "s3e_mul_mat_q_batch", "s3e_quantize_rows", "s3e_layer_norm", "s3e_copy",
     "s3e_flash_attn_ext", "s3e_model_load",
     "s3e_model_free", "s3e_model_hparams", "s3e_state_create", "s3e_state_free", "s3e_encode_chw",
-    "s3e_encode_chw_host", "s3e_encode_image_u8", "s3e_vit_prefix", "s3e_vit_block", "s3e_run_neck", "s3e_hiera_block", "s3e_model_type", "s3e_mem_attn_dims", "s3e_mem_attn",
+    "s3e_encode_chw_host", "s3e_encode_image_u8", "s3e_preprocess_image", "s3e_vit_prefix", "s3e_vit_block", "s3e_run_neck", "s3e_hiera_block", "s3e_model_type", "s3e_mem_attn_dims", "s3e_mem_attn",
     "s3e_state_tensor_info",
     "s3e_state_tensor_get", "s3e_state_tensor_device", "s3e_synth_write", "s3e_synth_write_sam2",
 ]
@@ -291,6 +296,13 @@ class Context:
     def to_device(self, arr: np.ndarray) -> DeviceBuffer:
         arr = np.ascontiguousarray(arr)
         return DeviceBuffer(self, arr.nbytes).upload(arr)
+
+    def preprocess_image(self, hwc: DeviceBuffer, width: int, height: int, img_size: int, norm: int,
+                         chw: DeviceBuffer):
+        """Resize + normalise a device-resident HWC uint8 image into CHW f32
+        (norm: NORM_SAM3 or NORM_IMAGENET)."""
+        check(LIB.s3e_preprocess_image(self.handle, hwc.ptr, width, height, img_size, norm, chw.ptr),
+              "s3e_preprocess_image")
 
     def weight(self, ggml_type: int, K: int, N: int, data: np.ndarray) -> Weight:
         return Weight(self, ggml_type, K, N, data)

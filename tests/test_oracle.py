@@ -299,6 +299,46 @@ def test_preprocess_identity_and_constant():
     assert np.all(out == np.float32((np.float32(77) / np.float32(255) - np.float32(0.5)) / np.float32(0.5)))
 
 
+def _resize_u8(img, ow, oh):
+    h, w, _ = img.shape
+    out = np.empty((oh, ow, 3), np.uint8)
+    orc.LIB.orc_resize_bilinear_u8(orc.ptr(np.ascontiguousarray(img)), w, h, orc.ptr(out), ow, oh)
+    return out
+
+
+def test_resize_exact_2x_downscale():
+    """Halving: every output pixel sits at the centre of a 2×2 source block
+    (half-pixel centres), so the result is the block mean rounded half up."""
+    img = np.random.default_rng(8).integers(0, 256, (64, 96, 3), dtype=np.uint8)
+    got = _resize_u8(img, 48, 32)
+    s = img.astype(np.int64).reshape(32, 2, 48, 2, 3).sum(axis=(1, 3))
+    assert np.array_equal(got, ((s * 2 + 4) // 8).astype(np.uint8))  # floor(s/4 + 0.5)
+
+
+@pytest.mark.parametrize("w,h,ow,oh", [(1920, 1080, 1008, 1008), (640, 480, 336, 336), (100, 50, 336, 336),
+                                       (7, 3, 64, 64), (1, 1, 16, 16), (1007, 1009, 1008, 1008),
+                                       (333, 777, 1024, 1024)])
+def test_resize_matches_torch_bilinear(w, h, ow, oh):
+    """sam3_resize_bilinear against torch's bilinear interpolation
+    (align_corners=False: half-pixel centres, source clamped at 0, edge
+    replication) in float64, rounded half up.  The two evaluation orders may
+    differ in the last bit of a value that is exactly half-way (an integer
+    + 0.5 in exact arithmetic), so those ties — and only those — may round
+    apart, by 1."""
+    import torch
+    import torch.nn.functional as F
+
+    img = np.random.default_rng(w + h).integers(0, 256, (h, w, 3), dtype=np.uint8)
+    got = _resize_u8(img, ow, oh)
+    t = torch.from_numpy(img.astype(np.float64)).permute(2, 0, 1)[None]
+    r = F.interpolate(t, size=(oh, ow), mode="bilinear", align_corners=False)[0].permute(1, 2, 0).numpy()
+    ref = np.clip(np.floor(r + 0.5), 0, 255).astype(np.uint8)
+    bad = got != ref
+    assert np.abs(got.astype(int) - ref.astype(int)).max() <= 1
+    assert bad.sum() <= 1e-4 * got.size
+    assert np.all(np.abs(r[bad] - np.floor(r[bad]) - 0.5) < 1e-9)
+
+
 @pytest.fixture(scope="module")
 def s3e_mod():
     import s3e
