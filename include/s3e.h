@@ -151,7 +151,12 @@ int s3e_layer_norm(s3e_ctx *ctx, const float *x, int64_t rows, int64_t n, float 
  * Q(b,h,i,d) = q[b*q_nb[3] + h*q_nb[2] + i*q_nb[1] + d] (d contiguous), K and
  * V likewise (V may be the strided view of sam3.cpp:3762-3763).  O follows
  * ggml's output layout [D, nh, Nq, B]: o[((b*Nq + i)*nh + h)*D + d].
- * D must be 64.  `prec` mirrors ggml_flash_attn_ext_set_prec:
+ * D: any multiple of 4 up to 128 (the ViT's 64; Hiera's 96, 56, 72, 32 —
+ * run zero-padded to 64 or 128 channels, sam3.cpp:4395), or 256 (the
+ * memory attention, sam3.cpp:9267, :9312; S3E_PREC_DEFAULT only).  Nq and
+ * Nkv may differ (Hiera's pooled queries).  When the query tiles alone
+ * would leave the GPU idle the keys are split into ranges whose partial
+ * results a second pass combines.  `prec` mirrors ggml_flash_attn_ext_set_prec:
  * S3E_PREC_DEFAULT computes on fp16 MFMA with Q, K, V and the
  * probabilities rounded to fp16 (fp32 accumulation); S3E_PREC_F32 carries
  * each operand as an fp16 pair (hi + lo) and reproduces f32 attention,

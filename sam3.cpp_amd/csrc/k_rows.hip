@@ -181,23 +181,23 @@ __global__ void k_im2col(const float *__restrict__ chw, int img, int P, int64_t 
     else ((float *)out)[idx] = val;
 }
 
-// f32 strided Q/K/V → fp16 [BH][N][64] for Q and K, [BH][64][ldt] for V
-// (keys in vt_slot order).
+// f32 strided Q/K/V (head dim D) → fp16 [BH][N][hdp] for Q and K,
+// [BH][hdp][ldt] for V (keys in vt_slot order), channels D..hdp−1 zero.
 // With lo != null the value is stored as the pair hi = fp16(v),
 // lo = fp16(v − hi) for split-precision attention.
 __global__ void k_attn_prep(const float *__restrict__ src, int64_t s1, int64_t s2, int64_t s3,
-                            int64_t N, int64_t nh, int64_t B, _Float16 *__restrict__ dst,
+                            int64_t N, int64_t nh, int64_t B, int D, int hdp, _Float16 *__restrict__ dst,
                             _Float16 *__restrict__ lo, int64_t ldt, int transpose) {
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t total = B * nh * N * 64;
+    const int64_t total = B * nh * N * hdp;
     if (idx >= total) return;
-    const int64_t d = idx % 64;
-    const int64_t i = (idx / 64) % N;
-    const int64_t h = (idx / (64 * N)) % nh;
-    const int64_t b = idx / (64 * N * nh);
-    const float v = src[b * s3 + h * s2 + i * s1 + d];
+    const int64_t d = idx % hdp;
+    const int64_t i = (idx / hdp) % N;
+    const int64_t h = (idx / (hdp * N)) % nh;
+    const int64_t b = idx / (hdp * N * nh);
+    const float v = d < D ? src[b * s3 + h * s2 + i * s1 + d] : 0.f;
     const int64_t bh = b * nh + h;
-    const int64_t o = transpose ? (bh * 64 + d) * ldt + vt_slot(i) : (bh * N + i) * 64 + d;
+    const int64_t o = transpose ? (bh * hdp + d) * ldt + vt_slot(i) : (bh * N + i) * hdp + d;
     const _Float16 hv = to_half(v);
     dst[o] = hv;
     if (lo) lo[o] = (_Float16)(v - (float)hv);
@@ -279,16 +279,17 @@ hipError_t launch_im2col(const float *chw, int img, int P, int64_t ldk, AKind ki
 
 hipError_t launch_attn_prep(const float *q, const int64_t q_nb[4], const float *k,
                             const int64_t k_nb[4], const float *v, const int64_t v_nb[4],
-                            int64_t Nq, int64_t Nkv, int64_t nh, int64_t B, _Float16 *q16,
+                            int64_t Nq, int64_t Nkv, int64_t nh, int64_t B, int D, int hdp, _Float16 *q16,
                             _Float16 *k16, _Float16 *vt16, _Float16 *q_lo, _Float16 *k_lo,
                             _Float16 *vt_lo, int64_t ldv, hipStream_t st) {
-    const int64_t tq = B * nh * Nq * 64, tk = B * nh * Nkv * 64;
+    if (D <= 0 || D > hdp) return hipErrorInvalidValue;
+    const int64_t tq = B * nh * Nq * hdp, tk = B * nh * Nkv * hdp;
     hipLaunchKernelGGL(k_attn_prep, dim3((unsigned)((tq + 255) / 256)), dim3(256), 0, st, q, q_nb[1],
-                       q_nb[2], q_nb[3], Nq, nh, B, q16, q_lo, (int64_t)0, 0);
+                       q_nb[2], q_nb[3], Nq, nh, B, D, hdp, q16, q_lo, (int64_t)0, 0);
     hipLaunchKernelGGL(k_attn_prep, dim3((unsigned)((tk + 255) / 256)), dim3(256), 0, st, k, k_nb[1],
-                       k_nb[2], k_nb[3], Nkv, nh, B, k16, k_lo, (int64_t)0, 0);
+                       k_nb[2], k_nb[3], Nkv, nh, B, D, hdp, k16, k_lo, (int64_t)0, 0);
     hipLaunchKernelGGL(k_attn_prep, dim3((unsigned)((tk + 255) / 256)), dim3(256), 0, st, v, v_nb[1],
-                       v_nb[2], v_nb[3], Nkv, nh, B, vt16, vt_lo, ldv, 1);
+                       v_nb[2], v_nb[3], Nkv, nh, B, D, hdp, vt16, vt_lo, ldv, 1);
     return hipGetLastError();
 }
 

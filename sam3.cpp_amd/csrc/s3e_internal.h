@@ -234,7 +234,7 @@ hipError_t launch_layernorm(const float *x, int64_t M, int64_t E, float eps, con
 hipError_t launch_attn(const AttnArgs &a, hipStream_t st);
 hipError_t launch_attn_prep(const float *q, const int64_t q_nb[4], const float *k,
                             const int64_t k_nb[4], const float *v, const int64_t v_nb[4],
-                            int64_t Nq, int64_t Nkv, int64_t nh, int64_t B, _Float16 *q16,
+                            int64_t Nq, int64_t Nkv, int64_t nh, int64_t B, int D, int hdp, _Float16 *q16,
                             _Float16 *k16, _Float16 *vt16, _Float16 *q_lo, _Float16 *k_lo,
                             _Float16 *vt_lo, int64_t ldv, hipStream_t st);
 hipError_t launch_im2col(const float *chw, int img, int P, int64_t ldk, AKind kind, void *out,

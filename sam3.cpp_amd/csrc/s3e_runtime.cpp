@@ -624,18 +624,40 @@ extern "C" int s3e_flash_attn_ext(s3e_ctx *ctx, const float *q, const int64_t q_
         set_error("s3e_flash_attn_ext: NULL argument");
         return S3E_ERR_INVALID;
     }
-    if (D != 64) { set_error("s3e_flash_attn_ext: head dim %lld not supported (64 only)", (long long)D); return S3E_ERR_UNSUPPORTED; }
-    if (Nq <= 0 || Nkv <= 0 || nh <= 0 || B <= 0) { set_error("s3e_flash_attn_ext: empty shape"); return S3E_ERR_INVALID; }
+    if (Nq <= 0 || Nkv <= 0 || nh <= 0 || B <= 0 || D <= 0) { set_error("s3e_flash_attn_ext: empty shape"); return S3E_ERR_INVALID; }
     if (prec != S3E_PREC_DEFAULT && prec != S3E_PREC_F32) { set_error("s3e_flash_attn_ext: unknown precision %d", prec); return S3E_ERR_INVALID; }
+    // head dims up to 128 run zero-padded to 64 or 128 channels (ViT 64; Hiera 96, 56, 32, 72); 256 (memory
+    // attention) runs as is, on fp16 operands only
+    const int hdp = D <= 64 ? 64 : (D <= 128 ? 128 : 256);
+    if (D % 4 != 0 || (D > 128 && D != 256)) {
+        set_error("s3e_flash_attn_ext: head dim %lld not supported (multiples of 4 up to 128, or 256)", (long long)D);
+        return S3E_ERR_UNSUPPORTED;
+    }
+    if (D == 256 && prec == S3E_PREC_F32) {
+        set_error("s3e_flash_attn_ext: head dim 256 runs on fp16 operands only (S3E_PREC_DEFAULT)");
+        return S3E_ERR_UNSUPPORTED;
+    }
+    if (B * nh > 65535 || Nq > (1 << 24) || Nkv > (1 << 24)) { set_error("s3e_flash_attn_ext: shape too large"); return S3E_ERR_INVALID; }
     HIP_TRY(hipSetDevice(ctx->device));
     const int64_t ldv = vt_ld_for(Nkv);
     const int np = (prec == S3E_PREC_F32) ? 2 : 1;  // hi (+ lo) planes
-    const size_t qn = (size_t)(B * nh * Nq * 64), kn = (size_t)(B * nh * Nkv * 64), vn = (size_t)(B * nh * ldv * 64);
+    const size_t qn = (size_t)(B * nh * Nq * hdp), kn = (size_t)(B * nh * Nkv * hdp), vn = (size_t)(B * nh * ldv * hdp);
+    // split the keys when the query tiles alone leave the chip idle (plain layouts only)
+    const int64_t BH = B * nh, qtiles = (Nq + 127) / 128, ktiles = (Nkv + 31) / 32;
+    int nsplit = 1;
+    if (D == hdp && qtiles * BH < 512) {
+        int64_t ns = std::min<int64_t>((512 + qtiles * BH - 1) / (qtiles * BH), std::max<int64_t>(1, ktiles / 4));
+        const int64_t per = (ktiles + ns - 1) / ns;
+        nsplit = (int)((ktiles + per - 1) / per);
+    }
     _Float16 *q16 = nullptr, *k16 = nullptr, *vt16 = nullptr;
+    float *part = nullptr;
     hipError_t e = hipMalloc(&q16, qn * 2 * np);
     if (e == hipSuccess) e = hipMalloc(&k16, kn * 2 * np);
     if (e == hipSuccess) e = hipMalloc(&vt16, vn * 2 * np);
     if (e == hipSuccess) e = hipMemsetAsync(vt16, 0, vn * 2 * np, ctx->stream);
+    const size_t po = (size_t)nsplit * BH * Nq * hdp, pml = (size_t)nsplit * BH * Nq * 2;
+    if (e == hipSuccess && nsplit > 1) e = hipMalloc(&part, (po + pml) * 4);
     AttnArgs a;
     a.q = q16;
     a.k = k16;
@@ -646,24 +668,32 @@ extern "C" int s3e_flash_attn_ext(s3e_ctx *ctx, const float *q, const int64_t q_
         a.vt_lo = vt16 + vn;
     }
     if (e == hipSuccess)
-        e = launch_attn_prep(q, q_nb, k, k_nb, v, v_nb, Nq, Nkv, nh, B, q16, k16, vt16, (_Float16 *)a.q_lo,
-                             (_Float16 *)a.k_lo, (_Float16 *)a.vt_lo, ldv, ctx->stream);
+        e = launch_attn_prep(q, q_nb, k, k_nb, v, v_nb, Nq, Nkv, nh, B, (int)D, hdp, q16, k16, vt16,
+                             (_Float16 *)a.q_lo, (_Float16 *)a.k_lo, (_Float16 *)a.vt_lo, ldv, ctx->stream);
     if (e == hipSuccess) {
         a.Nq = (int)Nq;
         a.Nkv = (int)Nkv;
         a.NH = (int)nh;
-        a.BH = (int)(B * nh);
+        a.BH = (int)BH;
+        a.hd = hdp;
+        a.hd_out = D == hdp ? 0 : (int)D;
         a.scale = scale;
         a.grid = 0;
+        a.nsplit = nsplit;
+        if (nsplit > 1) {
+            a.part_o = part;
+            a.part_ml = part + po;
+        }
         a.out.kind = A_F32;
         a.out.x = o;
-        a.out.ld = nh * 64;
+        a.out.ld = nh * D;
         e = launch_attn(a, ctx->stream);
     }
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (q16) (void)hipFree(q16);
     if (k16) (void)hipFree(k16);
     if (vt16) (void)hipFree(vt16);
+    if (part) (void)hipFree(part);
     if (e != hipSuccess) { set_error("s3e_flash_attn_ext: %s", hipGetErrorString(e)); return S3E_ERR_HIP; }
     return S3E_OK;
 }

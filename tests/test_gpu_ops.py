@@ -245,3 +245,40 @@ def test_flash_attn(ctx, B, nh, N, prec):
     # fp16 operands: the F16 tolerance; split fp16 pairs: f32 attention up to
     # accumulation order and exp2 vs expf rounding
     assert err <= (2e-3 if prec == 0 else 1e-5)
+
+
+@pytest.mark.parametrize("D,B,nh,Nq,Nkv,prec", [
+    (96, 2, 2, 64, 64, 1), (96, 1, 4, 49, 196, 1), (56, 3, 2, 16, 64, 1), (32, 1, 2, 200, 200, 1),
+    (72, 1, 3, 100, 130, 0), (128, 1, 2, 300, 300, 1), (64, 1, 1, 256, 4096, 1), (64, 1, 2, 100, 2000, 0),
+    (256, 1, 1, 512, 4096, 0), (256, 1, 1, 100, 1100, 0)],
+    ids=lambda x: str(x))
+def test_flash_attn_head_dims(ctx, D, B, nh, Nq, Nkv, prec):
+    """Hiera head dims (96, 56, 72, 32: zero-padded to 64 / 128 internally),
+    pooled queries (Nq ≠ Nkv), 128, the memory attention's 256 (fp16
+    operands), and single-head shapes long enough in keys to take the
+    key-split path; V through strides as in the ViT test."""
+    rng = np.random.default_rng(D * 7 + Nq + Nkv)
+    q = rng.standard_normal((B, nh, Nq, D)).astype(np.float32)
+    k = rng.standard_normal((B, nh, Nkv, D)).astype(np.float32)
+    v_tok = rng.standard_normal((B, Nkv, nh, D)).astype(np.float32)
+    v = np.ascontiguousarray(v_tok.transpose(0, 2, 1, 3))
+    scale = 1.0 / np.sqrt(D)
+    ref = orc.flash_attn(q, k, v, scale)
+    qd, kd, vd = ctx.to_device(q), ctx.to_device(k), ctx.to_device(v_tok)
+    od = ctx.buffer(B * Nq * nh * D * 4)
+    print(f"flash_attn D={D} B={B} nh={nh} Nq={Nq} Nkv={Nkv} prec={prec}", flush=True)
+    ctx.flash_attn_ext(qd, (1, D, Nq * D, nh * Nq * D), kd, (1, D, Nkv * D, nh * Nkv * D), vd,
+                       (1, nh * D, D, Nkv * nh * D), D, Nq, Nkv, nh, B, scale, od, prec=prec)
+    ctx.sync()
+    out = od.download(np.float32, (B, Nq, nh, D))
+    err = orc.rel_l2(out, ref)
+    print(f"  rel_l2={err:.3e} max_abs={orc.max_abs(out, ref):.3e}", flush=True)
+    assert err <= (2e-3 if prec == 0 else 1e-5)
+
+
+def test_flash_attn_rejects(ctx):
+    buf = ctx.buffer(1 << 20)
+    nb = (1, 64, 64 * 64, 64 * 64)
+    for D, prec in [(130, 1), (6, 1), (256, 1), (192, 0), (0, 1)]:
+        with pytest.raises(s3e.S3EError):
+            ctx.flash_attn_ext(buf, nb, buf, nb, buf, nb, D, 8, 8, 1, 1, 0.125, buf, prec=prec)
