@@ -91,6 +91,7 @@ struct GemmParams {
     const uint8_t *a;             // activation values, rows of a_ld bytes
     const uint8_t *a_d, *a_s;     // stage-major fp16 planes, a_mp rows per group
     int64_t a_ld, a_kbytes, a_mp;
+    int a_rec, b_rec;             // bytes the operand buffer loads may address
     const uint8_t *b;             // weight values, rows of b_ld bytes
     const uint8_t *b_d, *b_m;     // stage-major fp16 planes, b_np rows per group
     int64_t b_ld, b_np;
@@ -143,6 +144,15 @@ __device__ __forceinline__ void quant_block32(const float *v, int8_t *qdst, uint
 #define S3E_SWZ_SHIFT 1
 #endif
 __device__ __forceinline__ int swz(int r) { return (r >> S3E_SWZ_SHIFT) & 7; }
+
+// 16 bytes per lane from base + voff + soff (a raw buffer of nrec bytes) into
+// LDS at lds + 16·lane.  base, nrec and soff are wave-uniform, so the buffer
+// descriptor lives in scalar registers and the uniform part of the address
+// costs no vector instruction.
+__device__ __forceinline__ void dma16_buf(const void *base, int nrec, void *lds, int voff, int soff) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, nrec, 0x00020000);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, LDS_PTR(lds), 16, voff, soff, 0, 0);
+}
 
 // Epilogue from the fp32 tile Ct [BM][CLD] in LDS (scaled, complete), run by
 // the NT_ threads of the work-group.
@@ -487,22 +497,24 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 3 : 256 / BM) void k_gemm(
     // ---- per-lane DMA sources: lane writes LDS bytes [16·lane, 16·lane+16) of
     // a 1 KB run = 8 rows, i.e. slot lane & 7 of row lane >> 3 of the run; it
     // fetches the chunk that belongs there
+    // Sources are byte offsets into buffer resources (A: M rows of a_ld
+    // bytes, B: Np columns of b_ld bytes; the launcher keeps both under 2^31):
+    // the stage lives in the uniform soffset, so the DMA of a stage costs no
+    // vector ALU work.
     const int dma_row = lane >> 3;
-    const uint8_t *a_src[C::NA];
-    int a_cofs[C::NA];
+    int a_vo[C::NA], a_cofs[C::NA], b_vo[C::NB];
 #pragma unroll
     for (int j = 0; j < C::NA; j++) {
         const int row = 8 * (wave * C::NA + j) + dma_row;
         const int gm = min(m0 + row, p.M - 1);
-        a_src[j] = p.a + (int64_t)gm * p.a_ld;
         a_cofs[j] = ((lane & 7) ^ swz(row)) << 4;
+        a_vo[j] = gm * (int)p.a_ld + a_cofs[j];
     }
-    const int64_t a_last = p.a_kbytes - 16;
-    const uint8_t *b_src[C::NB];
+    const int a_kb = (int)p.a_kbytes, a_last = a_kb - 16;
 #pragma unroll
     for (int j = 0; j < C::NB; j++) {
         const int col = 8 * (wave * C::NB + j) + dma_row;
-        b_src[j] = p.b + (int64_t)(n0 + col) * p.b_ld + (((lane & 7) ^ swz(col)) << 4);
+        b_vo[j] = (n0 + col) * (int)p.b_ld + (((lane & 7) ^ swz(col)) << 4);
     }
     const uint8_t *s_src[C::NS > 0 ? C::NS : 1];
     int64_t s_step[C::NS > 0 ? C::NS : 1];
@@ -533,18 +545,24 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 3 : 256 / BM) void k_gemm(
         }
     }
 
-    auto issue = [&](int s) {
-        uint8_t *L = lds + (s % NBUF) * C::STAGE;
+    // stage s into ring buffer `buf`
+    auto issue = [&](int s, int buf) {
+        uint8_t *L = lds + buf * C::STAGE;
+        if ((s + 1) * ROWB <= a_kb) {
 #pragma unroll
-        for (int j = 0; j < C::NA; j++) {
-            const int64_t off = min((int64_t)s * ROWB + a_cofs[j], a_last);
-            __builtin_amdgcn_global_load_lds((const void *)(a_src[j] + off),
-                                             LDS_PTR(L + C::OFF_A + (wave * C::NA + j) * 1024), 16, 0, 0);
+            for (int j = 0; j < C::NA; j++)
+                dma16_buf(p.a, p.a_rec, L + C::OFF_A + (wave * C::NA + j) * 1024, a_vo[j], s * ROWB);
+        } else {
+            // the stage that reaches past K re-reads the row's last chunk
+            // (finite data against zero weight columns)
+#pragma unroll
+            for (int j = 0; j < C::NA; j++)
+                dma16_buf(p.a, p.a_rec, L + C::OFF_A + (wave * C::NA + j) * 1024,
+                          min(a_vo[j] + s * ROWB, a_vo[j] - a_cofs[j] + a_last), 0);
         }
 #pragma unroll
         for (int j = 0; j < C::NB; j++)
-            __builtin_amdgcn_global_load_lds((const void *)(b_src[j] + (int64_t)s * ROWB),
-                                             LDS_PTR(L + C::OFF_B + (wave * C::NB + j) * 1024), 16, 0, 0);
+            dma16_buf(p.b, p.b_rec, L + C::OFF_B + (wave * C::NB + j) * 1024, b_vo[j], s * ROWB);
         if constexpr (C::quant) {
 #pragma unroll
             for (int j = 0; j < C::NS; j++)
@@ -623,8 +641,8 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 3 : 256 / BM) void k_gemm(
                     acc[i][n][r] = __builtin_fmaf((float)S[i][n][r], Cs[i][n][r], acc[i][n][r]);
     };
 
-    auto compute = [&](int s) {
-        const uint8_t *L = lds + (s % NBUF) * C::STAGE;
+    auto compute = [&](int buf) {
+        const uint8_t *L = lds + buf * C::STAGE;
         if constexpr (C::quant) {
             if constexpr (C::PIPE) {
                 QFrag f0, f1;
@@ -704,20 +722,20 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 3 : 256 / BM) void k_gemm(
     // ---- main loop: stage s+NBUF−1 in flight while stage s is consumed ----
     const int ns = p.nstages;
     if constexpr (NBUF == 3) {
-        issue(0);
-        if (ns > 1) issue(1);
+        issue(0, 0);
+        if (ns > 1) issue(1, 1);
         for (int s = 0; s < ns; s++) {
             if (s + 1 < ns) wait_and_barrier<C::NLOAD>();
             else wait_and_barrier<0>();
-            if (s + 2 < ns) issue(s + 2);
-            compute(s);
+            if (s + 2 < ns) issue(s + 2, (s + 2) % NBUF);
+            compute(s % NBUF);
         }
     } else {
-        issue(0);
+        issue(0, 0);
         for (int s = 0; s < ns; s++) {
             wait_and_barrier<0>();  // stage s landed; every wave is done with stage s−1
-            if (s + 1 < ns) issue(s + 1);
-            compute(s);
+            if (s + 1 < ns) issue(s + 1, (s + 1) & 1);
+            compute(s & 1);
         }
     }
     wait_and_barrier<0>();
@@ -792,6 +810,10 @@ hipError_t launch_gemm(const Weight &w, const Act &a, int64_t M, Epi epi, const 
     p.b_m = (const uint8_t *)w.m;
     p.b_ld = w.Kp * esize;
     p.b_np = w.Np;
+    // buffer-load reach: A rows [0, M), B columns [0, Np), byte offsets below 2^31
+    if ((int64_t)M * p.a_ld > INT32_MAX || (int64_t)w.Np * p.b_ld > INT32_MAX) return hipErrorInvalidValue;
+    p.a_rec = (int)(M * p.a_ld);
+    p.b_rec = (int)(w.Np * p.b_ld);
     p.M = (int)M;
     p.N = (int)w.N;
     p.nstages = (int)(w.Kp / stage_k(w.kind));
