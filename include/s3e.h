@@ -97,7 +97,9 @@ int s3e_weight_info(const s3e_weight *w, int64_t out[4]);
  * converted to W's vec_dot type exactly as ggml's CPU path converts src1
  * (Q8_0 for Q4_0/Q8_0, Q8_1 for Q4_1, F16 for F16, none for F32).
  * Replaces ggml_mul_mat + ggml_add at sam3.cpp:3738-3739, 3779-3780,
- * 3792-3796. */
+ * 3792-3796.  Above 64 rows the converted X (M rows of K bytes for Q8, 2·K
+ * for F16, 4·K for F32, padded to 128-byte stages) and the repacked W must
+ * each stay below 2 GiB; larger products return S3E_ERR_HIP. */
 int s3e_mul_mat(s3e_ctx *ctx, const s3e_weight *w, const float *X, int64_t M,
                 const float *bias, float *Y);
 
