@@ -41,7 +41,6 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
 #define LDS_PTR(p) ((__attribute__((address_space(3))) void *)(p))
@@ -600,45 +599,35 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 3 : 256 / BM) void k_gemm(
 #pragma unroll
             for (int r = 0; r < 16; r++) { acc[i][n][r] = 0.f; accm[i][n][r] = 0.f; }
 
-    // One quant block step: integer sums and scale products of MT × NT tiles.
-    // The scale product 2·d_x[r]·d_w[c] of block blk is a K = 8 fp16 MFMA:
-    // the activation side passes row r's four block scales as they lie in LDS
-    // (K slots 0-3, and again 4-7 in the upper lane half), read once per stage;
-    // the weight side is one-hot, column c's scale of block blk in slot blk
-    // (and blk + 4) with zeros elsewhere — one mask per block and column tile.
+    // one quant block step: integer sums and scale products of MT × NT tiles
     struct QFrag {
         v4i a[MT], b[NT];
-        uint32_t mb[NT];
-    };
-    uint2 sa[MT];  // activation-side scale operands of the stage
-    uint2 sb[NT];  // column scales of the stage: blocks 0|1, 2|3
-    auto sread = [&](const uint8_t *L) {
-#pragma unroll
-        for (int i = 0; i < MT; i++) sa[i] = *(const uint2 *)(L + C::OFF_AD + ad_off[i]);
-#pragma unroll
-        for (int n = 0; n < NT; n++) sb[n] = *(const uint2 *)(L + C::OFF_BD + bd_off[n]);
+        uint32_t da[MT], db[NT];
     };
     auto qread = [&](const uint8_t *L, int blk, QFrag &f) {
 #pragma unroll
-        for (int i = 0; i < MT; i++) f.a[i] = *(const v4i *)(L + a_off[i] + cofs[blk]);
+        for (int i = 0; i < MT; i++) {
+            f.a[i] = *(const v4i *)(L + a_off[i] + cofs[blk]);
+            f.da[i] = *(const uint16_t *)(L + C::OFF_AD + ad_off[i] + 2 * blk);
+        }
 #pragma unroll
         for (int n = 0; n < NT; n++) {
             f.b[n] = *(const v4i *)(L + b_off[n] + cofs[blk]);
-            const uint32_t w = blk < 2 ? sb[n].x : sb[n].y;
-            f.mb[n] = w & ((blk & 1) ? 0xFFFF0000u : 0x0000FFFFu);
+            f.db[n] = *(const uint16_t *)(L + C::OFF_BD + bd_off[n] + 2 * blk);
         }
     };
-    auto qmma = [&](const QFrag &f, int blk, v16i (&S)[MT][NT], v16f (&Cs)[MT][NT]) {
+    auto qmma = [&](const QFrag &f, v16i (&S)[MT][NT], v16f (&Cs)[MT][NT]) {
         const v16i zi = {};
         const v16f zf = {};
 #pragma unroll
         for (int n = 0; n < NT; n++) {
-            const uint2 hb = blk < 2 ? make_uint2(f.mb[n], 0u) : make_uint2(0u, f.mb[n]);
+            const v4u hb = {f.db[n], 0u, 0u, 0u};
 #pragma unroll
             for (int i = 0; i < MT; i++) {
+                const v4u ha = {f.da[i], 0u, 0u, 0u};
                 S[i][n] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[i], f.b[n], zi, 0, 0, 0);
-                Cs[i][n] = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, sa[i]),
-                                                                __builtin_bit_cast(v4h, hb), zf, 0, 0, 0);
+                Cs[i][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, ha),
+                                                                  __builtin_bit_cast(v8h, hb), zf, 0, 0, 0);
             }
         }
     };
@@ -659,28 +648,26 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 3 : 256 / BM) void k_gemm(
                 QFrag f0, f1;
                 v16i S0[MT][NT], S1[MT][NT];
                 v16f C0[MT][NT], C1[MT][NT];
-                sread(L);
                 qread(L, 0, f0);
                 qread(L, 1, f1);
-                qmma(f0, 0, S0, C0);
+                qmma(f0, S0, C0);
                 qread(L, 2, f0);
-                qmma(f1, 1, S1, C1);
+                qmma(f1, S1, C1);
                 qvalu(S0, C0);
                 qread(L, 3, f1);
-                qmma(f0, 2, S0, C0);
+                qmma(f0, S0, C0);
                 qvalu(S1, C1);
-                qmma(f1, 3, S1, C1);
+                qmma(f1, S1, C1);
                 qvalu(S0, C0);
                 qvalu(S1, C1);
             } else {
-                sread(L);
 #pragma unroll
                 for (int blk = 0; blk < 4; blk++) {
                     QFrag f;
                     v16i S[MT][NT];
                     v16f Cs[MT][NT];
                     qread(L, blk, f);
-                    qmma(f, blk, S, Cs);
+                    qmma(f, S, Cs);
                     qvalu(S, Cs);
                 }
             }

@@ -14,14 +14,15 @@ namespace {
 // and columns K..ldk are zero.
 __global__ void k_im2col_conv(const float *__restrict__ chw, int S, int k, int stride, int pad, int OW, int64_t T,
                               int64_t ldk, int kind, void *out) {
-    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= T * ldk) return;
-    const int64_t t = idx / ldk;
-    const int kk = (int)(idx % ldk);
+    // 32-bit index arithmetic (the launcher keeps T·ldk below 2^31)
+    const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (uint32_t)(T * ldk)) return;
+    const uint32_t t = idx / (uint32_t)ldk;
+    const int kk = (int)(idx - t * (uint32_t)ldk);
     float val = 0.f;
     if (kk < 3 * k * k) {
         const int c = kk / (k * k), r = kk % (k * k), ky = r / k, kx = r % k;
-        const int oy = (int)(t / OW), ox = (int)(t % OW);
+        const int oy = (int)(t / (uint32_t)OW), ox = (int)(t - (uint32_t)oy * OW);
         const int iy = oy * stride + ky - pad, ix = ox * stride + kx - pad;
         if (iy >= 0 && iy < S && ix >= 0 && ix < S) val = chw[(int64_t)c * S * S + (int64_t)iy * S + ix];
     }
@@ -61,14 +62,16 @@ __device__ __forceinline__ void put(_Float16 *hi, _Float16 *lo, int64_t i, float
 
 // mode 0: Q (one thread per (b, h, query, d)); 1: K; 2: Vᵀ (keys up to ldv)
 __global__ void k_hiera_prep(Prep p, int mode, int64_t total) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= total) return;
-    const int d = (int)(i % p.HDp);
-    const int64_t r = i / p.HDp;
-    const int npos = mode == 0 ? p.Nq : (mode == 1 ? p.Nkv : p.ldv);
-    const int pos = (int)(r % npos);
-    const int64_t bh = r / npos;
-    const int b = (int)(bh / p.NH), h = (int)(bh % p.NH);
+    // 32-bit index arithmetic (the launcher keeps totals below 2^31)
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (uint32_t)total) return;
+    const uint32_t r = i / (uint32_t)p.HDp;
+    const int d = (int)(i - r * (uint32_t)p.HDp);
+    const uint32_t npos = mode == 0 ? p.Nq : (mode == 1 ? p.Nkv : p.ldv);
+    const uint32_t bh32 = r / npos;
+    const int pos = (int)(r - bh32 * npos);
+    const int64_t bh = bh32;
+    const int b = (int)(bh32 / (uint32_t)p.NH), h = (int)(bh32 - (uint32_t)b * p.NH);
     float v = 0.f;
     if (d < p.HD && pos < (mode == 0 ? p.Nq : p.Nkv)) {
         const int col = (p.ld == 3LL * p.C ? mode * p.C : 0) + h * p.HD + d;
@@ -92,14 +95,16 @@ __global__ void k_hiera_prep(Prep p, int mode, int64_t total) {
 // per (window·head, position < ldv, 8 channels); positions inside the grid
 // return at once.
 __global__ void k_hiera_pad(Prep p, int with_q, int64_t total) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= total) return;
-    const int nch = p.HDp / 8;
-    const int d0 = (int)(i % nch) * 8;
-    const int64_t r = i / nch;
-    const int pos = (int)(r % p.ldv);
-    const int64_t bh = r / p.ldv;
-    const int b = (int)(bh / p.NH), h = (int)(bh % p.NH);
+    // 32-bit index arithmetic (the launcher keeps totals below 2^31)
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (uint32_t)total) return;
+    const uint32_t nch = p.HDp / 8;
+    const uint32_t r = i / nch;
+    const int d0 = (int)(i - r * nch) * 8;
+    const uint32_t bh32 = r / (uint32_t)p.ldv;
+    const int pos = (int)(r - bh32 * (uint32_t)p.ldv);
+    const int64_t bh = bh32;
+    const int b = (int)(bh32 / (uint32_t)p.NH), h = (int)(bh32 - (uint32_t)b * p.NH);
     const int64_t vrow = bh * p.HDp;
     const int64_t slot = vt_slot(pos);
     if (pos >= p.Nkv) {
@@ -125,12 +130,14 @@ __global__ void k_hiera_pad(Prep p, int with_q, int64_t total) {
 // (ggml_upscale NEAREST, then ggml_add; sam3.cpp:4575-4580)
 __global__ void k_upsample_add(float *__restrict__ dst, const float *__restrict__ src, int side, int D,
                                int64_t n4) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n4) return;
-    const int d4 = D / 4;
-    const int64_t pix = i / d4;
-    const int c = (int)(i % d4) * 4;
-    const int y = (int)(pix / side), x = (int)(pix % side);
+    // 32-bit index arithmetic (the launcher keeps n4 below 2^31)
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (uint32_t)n4) return;
+    const uint32_t d4 = D / 4;
+    const uint32_t pix32 = i / d4;
+    const int64_t pix = pix32;
+    const int c = (int)(i - pix32 * d4) * 4;
+    const int y = (int)(pix32 / (uint32_t)side), x = (int)(pix32 - (uint32_t)y * side);
     const float4 u = *(const float4 *)(src + ((int64_t)(y / 2) * (side / 2) + x / 2) * D + c);
     float4 *o = (float4 *)(dst + pix * D + c);
     const float4 a = *o;
@@ -144,6 +151,7 @@ hipError_t launch_im2col_conv(const float *chw, int S, int k, int stride, int pa
     const int O = (S + 2 * pad - k) / stride + 1;
     if ((kind != A_F16 && kind != A_F32) || ldk < 3LL * k * k) return hipErrorInvalidValue;
     const int64_t T = (int64_t)O * O, total = T * ldk;
+    if (total >= INT32_MAX) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_im2col_conv, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, chw, S, k, stride,
                        pad, O, T, ldk, (int)kind, out);
     return hipGetLastError();
@@ -184,6 +192,7 @@ hipError_t launch_hiera_prep(const HieraPrepArgs &a, hipStream_t st) {
     if (p.HD > p.HDp || p.HDp % 8 != 0 || (p.ld != 3LL * p.C && p.ld != p.C)) return hipErrorInvalidValue;
     const int64_t bh = (int64_t)p.NW * p.NH;
     const int64_t tq = bh * p.Nq * p.HDp, tk = bh * p.Nkv * p.HDp, tv = bh * p.ldv * p.HDp;
+    if (tv >= INT32_MAX || tk >= INT32_MAX || tq >= INT32_MAX) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_hiera_prep, dim3((unsigned)((tq + 255) / 256)), dim3(256), 0, st, p, 0, tq);
     if (p.ld == 3LL * p.C) {
         hipLaunchKernelGGL(k_hiera_prep, dim3((unsigned)((tk + 255) / 256)), dim3(256), 0, st, p, 1, tk);
@@ -198,6 +207,7 @@ hipError_t launch_hiera_pad(const HieraPrepArgs &a, hipStream_t st) {
     // nothing to fill when the windows tile the grid and hold whole 16-key groups
     if ((int64_t)p.nwx * p.ww == p.W && (int64_t)(p.NW / p.nwx) * p.wh == p.H && p.ldv == p.Nkv) return hipSuccess;
     const int64_t total = (int64_t)p.NW * p.NH * p.ldv * (p.HDp / 8);
+    if (total >= INT32_MAX) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_hiera_pad, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, p, a.q_stride ? 0 : 1,
                        total);
     return hipGetLastError();
@@ -206,6 +216,7 @@ hipError_t launch_hiera_pad(const HieraPrepArgs &a, hipStream_t st) {
 hipError_t launch_upsample_add(float *dst, const float *src, int side, int D, hipStream_t st) {
     if (D % 4 != 0 || side % 2 != 0) return hipErrorInvalidValue;
     const int64_t n4 = (int64_t)side * side * (D / 4);
+    if (n4 >= INT32_MAX) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_upsample_add, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, dst, src, side, D, n4);
     return hipGetLastError();
 }

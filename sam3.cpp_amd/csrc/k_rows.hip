@@ -165,16 +165,17 @@ __global__ __launch_bounds__(256) void k_rows_quant(const float *__restrict__ x,
 // row t = py*G + px, column k = (c*P + ky)*P + kx, zero for k >= 3·P².
 __global__ void k_im2col(const float *__restrict__ chw, int img, int P, int64_t ldk, int kind,
                          void *out) {
+    // 32-bit index arithmetic (the launcher keeps G²·ldk below 2^31)
     const int G = img / P;
-    const int64_t T = (int64_t)G * G;
-    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= T * ldk) return;
-    const int64_t t = idx / ldk;
-    const int k = (int)(idx % ldk);
+    const uint32_t T = (uint32_t)(G * G);
+    const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= T * (uint32_t)ldk) return;
+    const uint32_t t = idx / (uint32_t)ldk;
+    const int k = (int)(idx - t * (uint32_t)ldk);
     float val = 0.f;
     if (k < 3 * P * P) {
         const int c = k / (P * P), r = k % (P * P), ky = r / P, kx = r % P;
-        const int py = (int)(t / G), px = (int)(t % G);
+        const int py = (int)(t / (uint32_t)G), px = (int)(t - (uint32_t)py * G);
         val = chw[(int64_t)c * img * img + (int64_t)(py * P + ky) * img + px * P + kx];
     }
     if (kind == A_F16) ((_Float16 *)out)[idx] = to_half(val);
@@ -208,16 +209,18 @@ __global__ void k_attn_prep(const float *__restrict__ src, int64_t s1, int64_t s
 // 4 channels of an output pixel.
 __global__ __launch_bounds__(256) void k_pool_act(const float *__restrict__ x, int w, int c, int pool, int ow,
                                                   int64_t n4, Act o) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= n4) return;
-    const int c4 = c / 4;
-    const int64_t pix = i / c4;
-    const int cc = (int)(i - pix * c4) * 4;
+    // 32-bit index arithmetic (the launcher keeps n4 below 2^31)
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= (uint32_t)n4) return;
+    const uint32_t c4 = c / 4;
+    const uint32_t pix32 = i / c4;
+    const int64_t pix = pix32;
+    const int cc = (int)(i - pix32 * c4) * 4;
     float4 v;
     if (pool == 1) {
         v = *(const float4 *)(x + pix * c + cc);
     } else {
-        const int64_t oy = pix / ow, ox = pix - oy * ow;
+        const int64_t oy = pix32 / (uint32_t)ow, ox = pix - oy * ow;
         const float *p0 = x + ((2 * oy) * w + 2 * ox) * c + cc;
         const float4 a = *(const float4 *)p0, b = *(const float4 *)(p0 + c);
         const float4 d = *(const float4 *)(p0 + (int64_t)w * c), e = *(const float4 *)(p0 + (int64_t)w * c + c);
@@ -238,6 +241,7 @@ hipError_t launch_pool_act(const float *x, int h, int w, int c, int pool, const 
         return hipErrorInvalidValue;
     const int oh = pool == 1 ? h : (h - 2) / 2 + 1, ow = pool == 1 ? w : (w - 2) / 2 + 1;
     const int64_t n4 = (int64_t)oh * ow * (c / 4);
+    if (n4 >= INT32_MAX) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_pool_act, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, x, w, c, pool, ow, n4, out);
     return hipGetLastError();
 }
@@ -272,6 +276,7 @@ hipError_t launch_im2col(const float *chw, int img, int P, int64_t ldk, AKind ki
                          hipStream_t st) {
     const int G = img / P;
     const int64_t total = (int64_t)G * G * ldk;
+    if (total >= INT32_MAX) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_im2col, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, chw, img, P,
                        ldk, (int)kind, out);
     return hipGetLastError();
