@@ -91,38 +91,53 @@ __global__ void k_hiera_prep(Prep p, int mode, int64_t total) {
 
 // Window positions outside the grid (ggml pads the normed input with zeros, so
 // after the projection they hold the QKV bias; zeros past HD) for Q (without
-// Q stride), K and Vᵀ, and the Vᵀ slots from Nkv to ldv (zeros).  One thread
-// per (window·head, position < ldv, 8 channels); positions inside the grid
-// return at once.
-__global__ void k_hiera_pad(Prep p, int with_q, int64_t total) {
-    // 32-bit index arithmetic (the launcher keeps totals below 2^31)
+// Q stride), K and Vᵀ, and the Vᵀ slots from Nkv to ldv (zeros).  Threads
+// cover only those places: first (padded grid position, head, 8 channels) —
+// the padded positions are the rows H..Hp−1 of the padded Hp × Wp grid, then
+// columns W..Wp−1 of rows 0..H−1 — then (window·head, tail slot, 8 channels).
+// 32-bit index arithmetic (the launcher keeps the counts below 2^31).
+__global__ void k_hiera_pad(Prep p, int with_q, uint32_t n_pad, uint32_t n_tail) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (uint32_t)total) return;
     const uint32_t nch = p.HDp / 8;
-    const uint32_t r = i / nch;
-    const int d0 = (int)(i - r * nch) * 8;
-    const uint32_t bh32 = r / (uint32_t)p.ldv;
-    const int pos = (int)(r - bh32 * (uint32_t)p.ldv);
-    const int64_t bh = bh32;
-    const int b = (int)(bh32 / (uint32_t)p.NH), h = (int)(bh32 - (uint32_t)b * p.NH);
-    const int64_t vrow = bh * p.HDp;
-    const int64_t slot = vt_slot(pos);
-    if (pos >= p.Nkv) {
+    if (i < n_pad) {
+        const uint32_t r = i / nch, q = r / (uint32_t)p.NH;
+        const int d0 = (int)(i - r * nch) * 8, h = (int)(r - q * p.NH);
+        const uint32_t Wp = (uint32_t)p.nwx * p.ww, Hp = (uint32_t)(p.NW / p.nwx) * p.wh;
+        const uint32_t below = (Hp - p.H) * Wp;  // positions in the rows past the grid
+        uint32_t y, x;
+        if (q < below) {
+            y = p.H + q / Wp;
+            x = q - (y - p.H) * Wp;
+        } else {
+            const uint32_t q2 = q - below, wr = Wp - p.W;
+            y = q2 / wr;
+            x = p.W + (q2 - y * wr);
+        }
+        const uint32_t wy = y / p.wh, wx = x / p.ww;
+        const int b = (int)(wy * p.nwx + wx);
+        const int pos = (int)((y - wy * p.wh) * p.ww + (x - wx * p.ww));
+        const int64_t bh = (int64_t)b * p.NH + h;
+        const int64_t vrow = bh * p.HDp;
+        const int64_t slot = vt_slot(pos);
         for (int d = d0; d < d0 + 8; d++) {
-            p.vt[(vrow + d) * p.ldv + slot] = (_Float16)0.f;
-            if (p.vt_lo) p.vt_lo[(vrow + d) * p.ldv + slot] = (_Float16)0.f;
+            const bool real = d < p.HD;
+            const float bk = real ? p.bias[p.C + h * p.HD + d] : 0.f;
+            put(p.k, p.k_lo, (bh * p.Nkv + pos) * p.HDp + d, bk);
+            if (real) put(p.vt, p.vt_lo, (vrow + d) * p.ldv + slot, p.bias[2 * p.C + h * p.HD + d]);
+            if (with_q) put(p.q, p.q_lo, (bh * p.Nkv + pos) * p.HDp + d, real ? p.bias[h * p.HD + d] : 0.f);
         }
         return;
     }
-    const int wy = b / p.nwx, wx = b % p.nwx;
-    const int y = wy * p.wh + pos / p.ww, x = wx * p.ww + pos % p.ww;
-    if (y < p.H && x < p.W) return;
+    const uint32_t j = i - n_pad;
+    if (j >= n_tail) return;
+    const uint32_t tails = (uint32_t)(p.ldv - p.Nkv);
+    const uint32_t r = j / nch, bh = r / tails;
+    const int d0 = (int)(j - r * nch) * 8;
+    const int64_t slot = vt_slot(p.Nkv + (int)(r - bh * tails));
+    const int64_t vrow = (int64_t)bh * p.HDp;
     for (int d = d0; d < d0 + 8; d++) {
-        const bool real = d < p.HD;
-        const float bk = real ? p.bias[p.C + h * p.HD + d] : 0.f;
-        put(p.k, p.k_lo, (bh * p.Nkv + pos) * p.HDp + d, bk);
-        if (real) put(p.vt, p.vt_lo, (vrow + d) * p.ldv + slot, p.bias[2 * p.C + h * p.HD + d]);
-        if (with_q) put(p.q, p.q_lo, (bh * p.Nkv + pos) * p.HDp + d, real ? p.bias[h * p.HD + d] : 0.f);
+        p.vt[(vrow + d) * p.ldv + slot] = (_Float16)0.f;
+        if (p.vt_lo) p.vt_lo[(vrow + d) * p.ldv + slot] = (_Float16)0.f;
     }
 }
 
@@ -204,12 +219,16 @@ hipError_t launch_hiera_prep(const HieraPrepArgs &a, hipStream_t st) {
 hipError_t launch_hiera_pad(const HieraPrepArgs &a, hipStream_t st) {
     const Prep p = make_prep(a);
     if (p.HD > p.HDp || !p.k || !p.vt || !p.bias || (!a.q_stride && !p.q)) return hipErrorInvalidValue;
+    const int64_t Wp = (int64_t)p.nwx * p.ww, Hp = (int64_t)(p.NW / p.nwx) * p.wh;
+    if (Wp < p.W || Hp < p.H || (int64_t)(p.NW / p.nwx) * p.nwx != p.NW || p.ldv < p.Nkv) return hipErrorInvalidValue;
+    const int64_t n_pad = (Hp * Wp - (int64_t)p.H * p.W) * p.NH * (p.HDp / 8);
+    const int64_t n_tail = (int64_t)p.NW * p.NH * (p.ldv - p.Nkv) * (p.HDp / 8);
     // nothing to fill when the windows tile the grid and hold whole 16-key groups
-    if ((int64_t)p.nwx * p.ww == p.W && (int64_t)(p.NW / p.nwx) * p.wh == p.H && p.ldv == p.Nkv) return hipSuccess;
-    const int64_t total = (int64_t)p.NW * p.NH * p.ldv * (p.HDp / 8);
-    if (total >= INT32_MAX) return hipErrorInvalidValue;
+    if (n_pad + n_tail == 0) return hipSuccess;
+    if (n_pad + n_tail >= INT32_MAX) return hipErrorInvalidValue;
+    const int64_t total = n_pad + n_tail;
     hipLaunchKernelGGL(k_hiera_pad, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, p, a.q_stride ? 0 : 1,
-                       total);
+                       (uint32_t)n_pad, (uint32_t)n_tail);
     return hipGetLastError();
 }
 
