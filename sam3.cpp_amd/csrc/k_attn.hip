@@ -448,11 +448,15 @@ __global__ __launch_bounds__(NTHR, HD == 64 ? 3 : (HD == 128 ? 2 : 1)) void k_at
 }
 
 // Combine the key-range partials: O = Σ_s 2^(m_s − M)·O_s / Σ_s 2^(m_s − M)·l_s.
-// One thread per (batch·head, query, 4 channels).
+// One thread per (batch·head, query, 4 channels); channels past the real
+// head dim (zero-padded heads) are not stored.  f32 or fp16 output, row
+// b·Nq + q, column h·hd_out + d.
 __global__ void k_attn_combine(AttnArgs a, int hd, int64_t total) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= total) return;
     const int d = (int)(i % (hd / 4)) * 4;
+    const int hdo = a.hd_out > 0 ? a.hd_out : hd;
+    if (d >= hdo) return;
     const int64_t r = i / (hd / 4);  // bh·Nq + q
     const int64_t plane = (int64_t)a.BH * a.Nq;
     float M = -INFINITY;
@@ -472,8 +476,14 @@ __global__ void k_attn_combine(AttnArgs a, int hd, int64_t total) {
     const float inv = den == 0.f ? 0.f : 1.0f / den;
     const int64_t bh = r / a.Nq, q = r % a.Nq;
     const int64_t b = bh / a.NH, h = bh % a.NH;
-    float *dst = (float *)a.out.x + (b * a.Nq + q) * a.out.ld + h * hd + d;
-    *(float4 *)dst = make_float4(num.x * inv, num.y * inv, num.z * inv, num.w * inv);
+    const int64_t off = (b * a.Nq + q) * a.out.ld + h * hdo + d;
+    if (a.out.kind == A_F16) {
+        const uint32_t w0 = (uint32_t)f2h_bits(num.x * inv) | ((uint32_t)f2h_bits(num.y * inv) << 16);
+        const uint32_t w1 = (uint32_t)f2h_bits(num.z * inv) | ((uint32_t)f2h_bits(num.w * inv) << 16);
+        *(uint2 *)((_Float16 *)a.out.x + off) = make_uint2(w0, w1);
+    } else {
+        *(float4 *)((float *)a.out.x + off) = make_float4(num.x * inv, num.y * inv, num.z * inv, num.w * inv);
+    }
 }
 
 }  // namespace
@@ -487,10 +497,12 @@ hipError_t launch_attn(const AttnArgs &a, hipStream_t st) {
     const int ntiles = (a.Nkv + 31) / 32;
     if (a.nsplit < 1 || a.nsplit > ntiles) return hipErrorInvalidValue;
     if (a.nsplit > 1) {
-        // every range must hold a tile; plain layouts, f32 output
+        // every range must hold a tile; plain layouts (narrower heads allowed),
+        // f32 or fp16 output
         const int per = (ntiles + a.nsplit - 1) / a.nsplit;
-        if ((int64_t)per * (a.nsplit - 1) >= ntiles || !a.part_o || !a.part_ml || a.out.kind != A_F32 ||
-            a.wo > 0 || a.grid > 0 || (a.hd_out > 0 && a.hd_out != hd))
+        if ((int64_t)per * (a.nsplit - 1) >= ntiles || !a.part_o || !a.part_ml ||
+            (a.out.kind != A_F32 && a.out.kind != A_F16) || a.wo > 0 || a.grid > 0 ||
+            (a.hd_out > 0 && (a.hd_out > hd || a.hd_out % 4 != 0)))
             return hipErrorInvalidValue;
     }
     // head dim 256: fp16 operands only

@@ -81,6 +81,8 @@ struct HieraState {
     int64_t q_cap = 0, k_cap = 0, v_cap = 0;
     _Float16 *fin = nullptr;        // FPN inputs as fp16 planes [hi | lo]
     int64_t fin_cap = 0;
+    float *part = nullptr;          // key-split partials of global attention: outputs | (m, l)
+    int64_t part_cap = 0;
     float *lat[4] = {};             // FPN levels, f32 [side²][D]
     float *pe[4] = {};              // sinusoidal PEs of the output levels
     ~HieraState() {
@@ -88,7 +90,7 @@ struct HieraState {
         a1.release();
         a2.release();
         for (void *p : {(void *)qkv, (void *)dp, (void *)attn_f32, (void *)q16, (void *)k16, (void *)vt16,
-                        (void *)fin})
+                        (void *)fin, (void *)part})
             if (p) (void)hipFree(p);
         for (int i = 0; i < 4; i++)
             for (void *p : {(void *)xs[i], (void *)lat[i], (void *)pe[i]})
@@ -97,6 +99,17 @@ struct HieraState {
 };
 
 namespace {
+
+// Key ranges for a global block's attention: enough work-groups (about 512)
+// when the query tiles alone would leave CUs idle, each range at least four
+// 32-key tiles.
+int attn_splits(int64_t nq, int64_t nkv, int64_t bh) {
+    const int64_t groups = (nq + 127) / 128 * bh, ktiles = (nkv + 31) / 32;
+    if (groups >= 512) return 1;
+    int64_t ns = std::min<int64_t>((512 + groups - 1) / groups, std::max<int64_t>(1, ktiles / 4));
+    const int64_t per = (ktiles + ns - 1) / ns;
+    return (int)((ktiles + per - 1) / per);
+}
 
 int upload_f32(HieraModel *m, const RawTensor &t, int64_t expect, float **dst) {
     const int64_t n = t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3];
@@ -436,7 +449,7 @@ int hiera_state_create(const HieraModel *m, hipStream_t st, HieraState **out) {
     std::unique_ptr<HieraState> s(new HieraState);
     const int64_t G = m->G, T0 = G * G;
     hipError_t e = s->col.alloc(T0, m->patch_k, st);
-    int64_t emax = 0, qkv_cap = 0, dp_cap = 0, q_cap = 0, k_cap = 0, v_cap = 0, attn_cap = 0;
+    int64_t emax = 0, qkv_cap = 0, dp_cap = 0, q_cap = 0, k_cap = 0, v_cap = 0, attn_cap = 0, part_cap = 0;
     {
         int H = (int)G, W = (int)G;
         for (const HBlock &b : m->blocks) {
@@ -451,6 +464,10 @@ int hiera_state_create(const HieraModel *m, hipStream_t st, HieraState **out) {
             const int64_t nkv = (int64_t)wh * ww, nq = b.qs ? (int64_t)(wh / 2) * (ww / 2) : nkv;
             const int64_t hdp = hd_pad(b.dout / b.heads);
             q_cap = std::max(q_cap, NW * b.heads * nq * hdp);
+            if (b.ws == 0 && !b.qs) {
+                const int ns = attn_splits(nq, nkv, b.heads);
+                if (ns > 1) part_cap = std::max(part_cap, (int64_t)ns * b.heads * nq * (hdp + 2));
+            }
             k_cap = std::max(k_cap, NW * b.heads * nkv * hdp);
             v_cap = std::max(v_cap, NW * b.heads * vt_ld_for(nkv) * hdp);
             H = Ht;
@@ -464,6 +481,8 @@ int hiera_state_create(const HieraModel *m, hipStream_t st, HieraState **out) {
     if (e == hipSuccess) e = hipMalloc(&s->qkv, (size_t)std::max<int64_t>(qkv_cap, 1) * 4);
     if (e == hipSuccess) e = hipMalloc(&s->dp, (size_t)dp_cap * 4);
     if (e == hipSuccess) e = hipMalloc(&s->attn_f32, (size_t)attn_cap * 4);
+    if (e == hipSuccess && part_cap > 0) e = hipMalloc(&s->part, (size_t)part_cap * 4);
+    s->part_cap = part_cap;
     s->q_cap = q_cap;
     s->k_cap = k_cap;
     s->v_cap = v_cap;
@@ -576,8 +595,21 @@ hipError_t hiera_block(const HieraModel *m, HieraState *s, int bi, const float *
     aa.out_w = Wt;
     const AKind kp = act_kind_for(b.proj.kind);
     const bool q8 = kp == A_Q8_0 || kp == A_Q8_1;
-    // a Q8 block must lie inside one head; split pairs go through f32
-    const bool direct = kp != A_F16X2 && (!q8 || HD % 32 == 0);
+    // A global block whose query tiles leave CUs idle splits its keys into
+    // ranges (partials merged by a second pass, f32 or fp16 output); its
+    // single window is the grid, so the output rows need no mapping.
+    const int ns = (b.ws == 0 && !b.qs) ? attn_splits(aa.Nq, aa.Nkv, aa.BH) : 1;
+    if (ns > 1) {
+        const int64_t po = (int64_t)ns * aa.BH * aa.Nq * HDp;
+        if (!s->part || po + (int64_t)ns * aa.BH * aa.Nq * 2 > s->part_cap) return hipErrorInvalidValue;
+        aa.wo = 0;
+        aa.nsplit = ns;
+        aa.part_o = s->part;
+        aa.part_ml = s->part + po;
+    }
+    // a Q8 block must lie inside one head; split pairs go through f32, as
+    // does a key-split attention into a Q8 format
+    const bool direct = kp != A_F16X2 && (!q8 || HD % 32 == 0) && (ns == 1 || kp == A_F16);
     const Act a_proj = s->a1.as(kp, C);
     aa.out = direct ? a_proj : f32_act(s->attn_f32, C);
     if ((e = launch_attn(aa, st)) != hipSuccess) return e;
