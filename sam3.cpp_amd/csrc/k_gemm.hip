@@ -34,6 +34,8 @@
 // inside one thread, float4 columns per lane for plain f32 stores.
 #include "s3e_internal.h"
 
+#include <algorithm>
+
 namespace s3e {
 namespace {
 
@@ -92,6 +94,8 @@ struct GemmParams {
     const uint8_t *a_d, *a_s;     // stage-major fp16 planes, a_mp rows per group
     int64_t a_ld, a_kbytes, a_mp;
     int a_rec, b_rec;             // bytes the operand buffer loads may address
+    int ksplit;                   // > 1: K split into ranges, raw partial tiles to part [ksplit][M][N]
+    float *part;
     const uint8_t *b;             // weight values, rows of b_ld bytes
     const uint8_t *b_d, *b_m;     // stage-major fp16 planes, b_np rows per group
     int64_t b_ld, b_np;
@@ -476,10 +480,11 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 3 : 256 / BM) void k_gemm(
     constexpr int MT = C::MT, NT = C::NT, NBUF = C::NBUF;
     __shared__ __attribute__((aligned(1024))) uint8_t lds[C::LDS];
 
-    // ---- tile of this work-group ----
+    // ---- tile of this work-group (and its K range when split) ----
     const int per = gridDim.x >> 3;
-    const int logical = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
-    if (logical >= p.ntiles) return;
+    const int logical0 = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    if (logical0 >= p.ntiles * p.ksplit) return;
+    const int kpart = logical0 % p.ksplit, logical = logical0 / p.ksplit;
     constexpr int GROUP = 8;
     const int group = logical / (GROUP * p.tiles_n);
     const int first_m = group * GROUP;
@@ -719,23 +724,25 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 3 : 256 / BM) void k_gemm(
         }
     };
 
-    // ---- main loop: stage s+NBUF−1 in flight while stage s is consumed ----
-    const int ns = p.nstages;
+    // ---- main loop over stages s0 .. s1−1: stage s+NBUF−1 in flight while
+    // stage s is consumed ----
+    const int kper = (p.nstages + p.ksplit - 1) / p.ksplit;
+    const int s0 = kpart * kper, s1 = min(p.nstages, s0 + kper);
     if constexpr (NBUF == 3) {
-        issue(0, 0);
-        if (ns > 1) issue(1, 1);
-        for (int s = 0; s < ns; s++) {
-            if (s + 1 < ns) wait_and_barrier<C::NLOAD>();
+        issue(s0, 0);
+        if (s0 + 1 < s1) issue(s0 + 1, 1);
+        for (int s = s0; s < s1; s++) {
+            if (s + 1 < s1) wait_and_barrier<C::NLOAD>();
             else wait_and_barrier<0>();
-            if (s + 2 < ns) issue(s + 2, (s + 2) % NBUF);
-            compute(s % NBUF);
+            if (s + 2 < s1) issue(s + 2, (s + 2 - s0) % NBUF);
+            compute((s - s0) % NBUF);
         }
     } else {
-        issue(0, 0);
-        for (int s = 0; s < ns; s++) {
+        issue(s0, 0);
+        for (int s = s0; s < s1; s++) {
             wait_and_barrier<0>();  // stage s landed; every wave is done with stage s−1
-            if (s + 1 < ns) issue(s + 1, (s + 1) & 1);
-            compute(s & 1);
+            if (s + 1 < s1) issue(s + 1, (s + 1 - s0) & 1);
+            compute((s - s0) & 1);
         }
     }
     wait_and_barrier<0>();
@@ -756,12 +763,57 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 3 : 256 / BM) void k_gemm(
             }
     __syncthreads();
 
+    if constexpr (EPI == EPI_F32 || EPI == EPI_RESID) {
+        if (p.ksplit > 1) {
+            // raw partial tile of this K range; the reduction adds bias / residual
+            GemmParams q = p;
+            q.e.y = p.part + (int64_t)kpart * p.M * p.N;
+            q.e.ldy = p.N;
+            q.e.bias = nullptr;
+            epilogue<EPI_F32, BM, C::NTH>(q, Ct, m0, n0, t);
+            return;
+        }
+    }
     epilogue<EPI, BM, C::NTH>(p, Ct, m0, n0, t);
+}
+
+// y = Σ_k part[k] (+ bias) for EPI_F32, y += Σ_k part[k] (+ bias) for
+// EPI_RESID, the ranges summed in order (the result does not depend on the
+// schedule).  One thread per 4 consecutive outputs of a row.
+__global__ __launch_bounds__(256) void k_gemm_reduce(const float *__restrict__ part, int ks, int M, int N,
+                                                     const float *__restrict__ bias, float *y, int64_t ldy,
+                                                     int resid) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t n4 = (uint32_t)N / 4;
+    if (i >= (uint32_t)M * n4) return;
+    const uint32_t r = i / n4;
+    const int c = (int)(i - r * n4) * 4;
+    const int64_t plane = (int64_t)M * N;
+    float4 v = *(const float4 *)(part + (int64_t)r * N + c);
+    for (int k = 1; k < ks; k++) {
+        const float4 w = *(const float4 *)(part + k * plane + (int64_t)r * N + c);
+        v.x = __fadd_rn(v.x, w.x);
+        v.y = __fadd_rn(v.y, w.y);
+        v.z = __fadd_rn(v.z, w.z);
+        v.w = __fadd_rn(v.w, w.w);
+    }
+    if (bias) {
+        v.x = __fadd_rn(v.x, bias[c]);
+        v.y = __fadd_rn(v.y, bias[c + 1]);
+        v.z = __fadd_rn(v.z, bias[c + 2]);
+        v.w = __fadd_rn(v.w, bias[c + 3]);
+    }
+    float4 *o = (float4 *)(y + (int64_t)r * ldy + c);
+    if (resid) {
+        const float4 x = *o;
+        v = make_float4(__fadd_rn(x.x, v.x), __fadd_rn(x.y, v.y), __fadd_rn(x.z, v.z), __fadd_rn(x.w, v.w));
+    }
+    *o = v;
 }
 
 template <int WK, int EPI, int BM, int WAVES>
 hipError_t launch_one(const GemmParams &p, hipStream_t st) {
-    const int grid = ((p.ntiles + 7) / 8) * 8;
+    const int grid = ((p.ntiles * p.ksplit + 7) / 8) * 8;
     hipLaunchKernelGGL((k_gemm<WK, EPI, BM, WAVES>), dim3(grid), dim3(64 * WAVES), 0, st, p);
     return hipGetLastError();
 }
@@ -792,7 +844,24 @@ hipError_t dispatch_waves(Epi epi, GemmParams &p, hipStream_t st) {
     return waves == 4 ? dispatch_epi<WK, 4>(epi, p, st) : dispatch_epi<WK, 8>(epi, p, st);
 }
 
+// K ranges for a product that leaves CUs idle: fewer 64 × 128 tiles than CUs
+// and at least 8 stages of K; about 512 work-groups, each range at least four
+// stages.
+int splitk_of(const Weight &w, int64_t M) {
+    const int esize = (w.kind == WK_F16) ? 2 : (w.kind == WK_F32 ? 4 : 1);
+    const int64_t ns = w.Kp * esize / 128, tiles = (M + 63) / 64 * (w.Np / BN);
+    if (tiles >= 256 || ns < 8 || w.N % 4 != 0) return 1;
+    int64_t ks = std::min<int64_t>((512 + tiles - 1) / tiles, ns / 4);
+    const int64_t per = (ns + ks - 1) / ks;
+    return (int)((ns + per - 1) / per);
+}
+
 }  // namespace
+
+int64_t gemm_splitk_floats(const Weight &w, int64_t M) {
+    const int ks = splitk_of(w, M);
+    return ks > 1 ? (int64_t)ks * M * w.N : 0;
+}
 
 hipError_t launch_gemm(const Weight &w, const Act &a, int64_t M, Epi epi, const EpiArgs &ea,
                        hipStream_t st) {
@@ -816,6 +885,14 @@ hipError_t launch_gemm(const Weight &w, const Act &a, int64_t M, Epi epi, const 
     p.b_rec = (int)(w.Np * p.b_ld);
     p.M = (int)M;
     p.N = (int)w.N;
+    p.ksplit = 1;
+    if ((epi == EPI_F32 || epi == EPI_RESID) && ea.ws && ea.ldy % 4 == 0) {
+        const int ks = splitk_of(w, M);
+        if (ks > 1 && (int64_t)ks * M * w.N <= ea.ws_cap) {
+            p.ksplit = ks;
+            p.part = ea.ws;
+        }
+    }
     p.nstages = (int)(w.Kp / stage_k(w.kind));
     p.tiles_n = (int)(w.Np / BN);
     p.e = ea;
@@ -830,14 +907,22 @@ hipError_t launch_gemm(const Weight &w, const Act &a, int64_t M, Epi epi, const 
     // 64-row tiles: two or three work-groups share a CU, so one work-group's
     // epilogue overlaps another's main loop; with 128-row tiles (one per CU)
     // every CU alternates between the two phases.
+    hipError_t e;
     switch (w.kind) {
-        case WK_Q4_0: return dispatch_waves<WK_Q4_0>(epi, p, st);
-        case WK_Q4_1: return dispatch_waves<WK_Q4_1>(epi, p, st);
-        case WK_Q8_0: return dispatch_waves<WK_Q8_0>(epi, p, st);
-        case WK_F16: return dispatch_waves<WK_F16>(epi, p, st);
-        case WK_F32: return dispatch_waves<WK_F32>(epi, p, st);
+        case WK_Q4_0: e = dispatch_waves<WK_Q4_0>(epi, p, st); break;
+        case WK_Q4_1: e = dispatch_waves<WK_Q4_1>(epi, p, st); break;
+        case WK_Q8_0: e = dispatch_waves<WK_Q8_0>(epi, p, st); break;
+        case WK_F16: e = dispatch_waves<WK_F16>(epi, p, st); break;
+        case WK_F32: e = dispatch_waves<WK_F32>(epi, p, st); break;
         default: return hipErrorInvalidValue;
     }
+    if (e == hipSuccess && p.ksplit > 1) {
+        const int64_t n = M * (w.N / 4);
+        hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p.part, p.ksplit,
+                           (int)M, (int)w.N, ea.bias, ea.y, ea.ldy, epi == EPI_RESID ? 1 : 0);
+        e = hipGetLastError();
+    }
+    return e;
 }
 
 }  // namespace s3e

@@ -83,6 +83,8 @@ struct HieraState {
     int64_t fin_cap = 0;
     float *part = nullptr;          // key-split partials of global attention: outputs | (m, l)
     int64_t part_cap = 0;
+    float *gws = nullptr;           // K-split partials of the small-grid residual GEMMs
+    int64_t gws_cap = 0;
     float *lat[4] = {};             // FPN levels, f32 [side²][D]
     float *pe[4] = {};              // sinusoidal PEs of the output levels
     ~HieraState() {
@@ -90,7 +92,7 @@ struct HieraState {
         a1.release();
         a2.release();
         for (void *p : {(void *)qkv, (void *)dp, (void *)attn_f32, (void *)q16, (void *)k16, (void *)vt16,
-                        (void *)fin, (void *)part})
+                        (void *)fin, (void *)part, (void *)gws})
             if (p) (void)hipFree(p);
         for (int i = 0; i < 4; i++)
             for (void *p : {(void *)xs[i], (void *)lat[i], (void *)pe[i]})
@@ -450,6 +452,7 @@ int hiera_state_create(const HieraModel *m, hipStream_t st, HieraState **out) {
     const int64_t G = m->G, T0 = G * G;
     hipError_t e = s->col.alloc(T0, m->patch_k, st);
     int64_t emax = 0, qkv_cap = 0, dp_cap = 0, q_cap = 0, k_cap = 0, v_cap = 0, attn_cap = 0, part_cap = 0;
+    int64_t gws_cap = 0;
     {
         int H = (int)G, W = (int)G;
         for (const HBlock &b : m->blocks) {
@@ -459,6 +462,8 @@ int hiera_state_create(const HieraModel *m, hipStream_t st, HieraState **out) {
             if (b.qs) qkv_cap = std::max(qkv_cap, T * b.dout);  // Q rows before pooling
             dp_cap = std::max(dp_cap, T * b.dout);
             attn_cap = std::max(attn_cap, (int64_t)Ht * Wt * b.dout);
+            gws_cap = std::max({gws_cap, gemm_splitk_floats(b.proj, (int64_t)Ht * Wt),
+                                gemm_splitk_floats(b.fc2, (int64_t)Ht * Wt)});
             int wh = b.ws > 0 ? b.ws : H, ww = b.ws > 0 ? b.ws : W;
             const int64_t NW = b.ws > 0 ? (int64_t)((H + b.ws - 1) / b.ws) * ((W + b.ws - 1) / b.ws) : 1;
             const int64_t nkv = (int64_t)wh * ww, nq = b.qs ? (int64_t)(wh / 2) * (ww / 2) : nkv;
@@ -483,6 +488,8 @@ int hiera_state_create(const HieraModel *m, hipStream_t st, HieraState **out) {
     if (e == hipSuccess) e = hipMalloc(&s->attn_f32, (size_t)attn_cap * 4);
     if (e == hipSuccess && part_cap > 0) e = hipMalloc(&s->part, (size_t)part_cap * 4);
     s->part_cap = part_cap;
+    if (e == hipSuccess && gws_cap > 0) e = hipMalloc(&s->gws, (size_t)gws_cap * 4);
+    s->gws_cap = gws_cap;
     s->q_cap = q_cap;
     s->k_cap = k_cap;
     s->v_cap = v_cap;
@@ -619,6 +626,8 @@ hipError_t hiera_block(const HieraModel *m, HieraState *s, int bi, const float *
     ep.bias = b.proj_b;
     ep.y = y;
     ep.ldy = C;
+    ep.ws = s->gws;
+    ep.ws_cap = s->gws_cap;
     if ((e = launch_gemm(b.proj, a_proj, Tt, EPI_RESID, ep, st)) != hipSuccess) return e;
     // 6. MLP: norm2 → fc1 + bias + ggml_gelu → fc2 + bias + residual
     const Act a_fc1 = s->a1.as(act_kind_for(b.fc1.kind), C);
@@ -632,6 +641,8 @@ hipError_t hiera_block(const HieraModel *m, HieraState *s, int bi, const float *
     e2.bias = b.fc2_b;
     e2.y = y;
     e2.ldy = C;
+    e2.ws = s->gws;
+    e2.ws_cap = s->gws_cap;
     return launch_gemm(b.fc2, e1.out, Tt, EPI_RESID, e2, st);
 }
 

@@ -104,6 +104,10 @@ struct EpiArgs {
     const float *bias = nullptr;
     float *y = nullptr;          // EPI_F32 / EPI_RESID / EPI_POS
     int64_t ldy = 0;
+    // EPI_F32 / EPI_RESID: workspace for a split over K (gemm_splitk_floats
+    // floats); null: never split
+    float *ws = nullptr;
+    int64_t ws_cap = 0;
     Act out;                     // EPI_GELU
     // EPI_POS
     const float *pos = nullptr;  // [pg][pg][E]
@@ -207,6 +211,9 @@ struct SmArgs {
 };
 
 // ---- kernel launchers (k_*.hip) ----
+// Floats of workspace a product of M rows against w would use when split over
+// K (0: it runs unsplit): products with fewer tiles than CUs and a long K.
+int64_t gemm_splitk_floats(const Weight &w, int64_t M);
 hipError_t launch_gemm(const Weight &w, const Act &a, int64_t M, Epi epi, const EpiArgs &ea,
                        hipStream_t st);
 // Small-M products (k_gemm_sm.hip): Q4_0 / Q4_1 / Q8_0 / F16 weights, M ≤ 64.
