@@ -54,7 +54,8 @@ struct MemAttnState {
     int64_t capN = 0, capM = 0;
     int D = 0, MD = 0, FFN = 0;
     float *x = nullptr, *att = nullptr, *kvp = nullptr, *part_o = nullptr, *part_ml = nullptr;
-    int64_t part_cap = 0;
+    int64_t part_cap = 0;           // rows of part_ml (and of part_o at D floats each)
+    int64_t part_o_floats = 0;      // part_o also serves the K-split residual GEMMs
     ActBuf an, ah, am1, am2;
     _Float16 *q16 = nullptr, *k16 = nullptr, *vt16 = nullptr;
     void release() {
@@ -67,7 +68,7 @@ struct MemAttnState {
             if (p) (void)hipFree(p);
         x = att = kvp = part_o = part_ml = nullptr;
         q16 = k16 = vt16 = nullptr;
-        capN = capM = part_cap = 0;
+        capN = capM = part_cap = part_o_floats = 0;
     }
     ~MemAttnState() { release(); }
 };
@@ -256,14 +257,24 @@ int memattn_run(const MemAttnModel *m, MemAttnState **sp, const float *curr, con
     hipError_t e = grow(m, s, N, M, st);
     const int nsS = pick_splits(N, N), nsC = pick_splits(N, M);
     const int64_t part = (int64_t)std::max(nsS, nsC) * N;
-    if (e == hipSuccess && part > s->part_cap) {
+    // the residual GEMMs (N rows, D outputs) may split K through part_o: the
+    // attention partials are merged before each of them on the same stream
+    int64_t gws = 0;
+    for (const MemAttnLayer &ly : m->layers)
+        gws = std::max({gws, gemm_splitk_floats(ly.sa_out, N), gemm_splitk_floats(ly.ca_out, N),
+                        gemm_splitk_floats(ly.fc2, N)});
+    const int64_t need_o = std::max(part * D, gws);
+    if (e == hipSuccess && (part > s->part_cap || need_o > s->part_o_floats)) {
         if (s->part_o) (void)hipFree(s->part_o);
         if (s->part_ml) (void)hipFree(s->part_ml);
         s->part_o = s->part_ml = nullptr;
-        s->part_cap = 0;
-        e = hipMalloc(&s->part_o, (size_t)(part * D * 4));
+        s->part_cap = s->part_o_floats = 0;
+        e = hipMalloc(&s->part_o, (size_t)(need_o * 4));
         if (e == hipSuccess) e = hipMalloc(&s->part_ml, (size_t)(part * 2 * 4));
-        if (e == hipSuccess) s->part_cap = part;
+        if (e == hipSuccess) {
+            s->part_cap = part;
+            s->part_o_floats = need_o;
+        }
     }
     if (e != hipSuccess) { set_error("s3e_mem_attn: %s", hipGetErrorString(e)); return S3E_ERR_NOMEM; }
 #define MA_TRY(x)                                                                  \
@@ -335,6 +346,8 @@ int memattn_run(const MemAttnModel *m, MemAttnState **sp, const float *curr, con
         er.bias = ly.sa_out_b;
         er.y = s->x;
         er.ldy = D;
+        er.ws = s->part_o;
+        er.ws_cap = s->part_o_floats;
         MA_TRY(launch_gemm(ly.sa_out, ao, N, EPI_RESID, er, st));
         // cross-attention: keys from memory + positions, RoPE on the spatial ones
         const Act ac = s->an.as(act_kind_for(ly.ca_q.kind), D);
