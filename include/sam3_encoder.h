@@ -81,7 +81,7 @@ sam3_state_ptr sam3_create_state(const sam3_model & model, const sam3_params & p
 /* sam3.h:205 */
 void sam3_free_state(sam3_state & state);
 
-/* sam3.h:216: resize + normalise on the host (sam3.cpp:3441-3514), then the
+/* sam3.h:216: resize + normalise as sam3.cpp:3441-3514 does (on the device), then the
  * ViT backbone and every FPN neck of the model on the GPU */
 bool sam3_encode_image(sam3_state & state, const sam3_model & model, const sam3_image & image);
 /* sam3.h:432: CHW f32 already resized and normalised; img_size must equal

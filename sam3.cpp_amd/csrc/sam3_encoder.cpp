@@ -4,9 +4,10 @@
 // Each function keeps the reference's contract: sam3_load_model returns
 // nullptr and sam3_encode_image false on failure with a message on stderr
 // (sam3.cpp:3200-3344, :6024-6212, :6997-7008); no exception leaves the
-// library.  The host-side preprocessing is the engine's
+// library.  The preprocessing is the engine's, on the device
 // (s3e_encode_image_u8: sam3_resize_bilinear + sam3_preprocess_image,
-// sam3.cpp:3441-3514, or sam2_preprocess_image, :3518-3544, for SAM 2 files).
+// sam3.cpp:3441-3514, or sam2_preprocess_image, :3518-3544, for SAM 2 files,
+// with the same resized bytes).
 #include <cstdio>
 #include <cstring>
 #include <fstream>

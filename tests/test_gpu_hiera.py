@@ -209,7 +209,7 @@ def _encode_and_compare(tag, ft, om, st, img_hwc):
 
 
 def test_encode_image(hiera):
-    """End to end from a non-square image (host resize + ImageNet
+    """End to end from a non-square image (device resize + ImageNet
     normalisation) to the stage outputs and FPN levels."""
     tag, ft, om, gm, st = hiera
     rng = np.random.default_rng(4)

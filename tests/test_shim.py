@@ -85,7 +85,7 @@ def test_example_encode_matches_oracle(tmp_path, s3e_lib):
     s3e_lib.synth_write(path, img_size=336, patch=14, embed_dim=1024, depth=2, heads=16, window=8,
                         global_idx=(1,), ftype="q8_0", seed=21, std=0.02, random_affine=True, neck=1)
     rng = np.random.default_rng(9)
-    img = rng.integers(0, 256, (400, 300, 3), dtype=np.uint8)  # resized to 336² on the host
+    img = rng.integers(0, 256, (400, 300, 3), dtype=np.uint8)  # resized to 336² by the engine
     _write_ppm(str(tmp_path / "img.ppm"), img)
     out = str(tmp_path / "a_")
     print("sam3_encode on a 300x400 PPM", flush=True)
