@@ -230,10 +230,11 @@ hipError_t grow(const MemAttnModel *m, MemAttnState *s, int64_t N, int64_t M, hi
     return hipSuccess;
 }
 
-// split the keys so that the query tiles × splits fill the GPU twice
+// split the keys so that query tiles × splits give each CU one work-group
+// (head dim 256 holds one work-group per CU)
 int pick_splits(int64_t Nq, int64_t Nkv) {
     const int64_t qtiles = (Nq + 127) / 128, ktiles = (Nkv + 31) / 32;
-    int64_t ns = std::max<int64_t>(1, (512 + qtiles - 1) / qtiles);
+    int64_t ns = std::max<int64_t>(1, (256 + qtiles - 1) / qtiles);
     ns = std::min(ns, std::max<int64_t>(1, ktiles / 4));  // at least 4 tiles per range
     const int64_t per = (ktiles + ns - 1) / ns;
     return (int)((ktiles + per - 1) / per);
