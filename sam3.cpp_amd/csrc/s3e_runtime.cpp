@@ -645,8 +645,10 @@ extern "C" int s3e_flash_attn_ext(s3e_ctx *ctx, const float *q, const int64_t q_
     // split the keys when the query tiles alone leave the chip idle (plain layouts only)
     const int64_t BH = B * nh, qtiles = (Nq + 127) / 128, ktiles = (Nkv + 31) / 32;
     int nsplit = 1;
-    if (D == hdp && qtiles * BH < 512) {
-        int64_t ns = std::min<int64_t>((512 + qtiles * BH - 1) / (qtiles * BH), std::max<int64_t>(1, ktiles / 4));
+    // about one round of work-groups: 512 (two or three fit a CU), 256 at head dim 256 (one fits)
+    const int64_t target = hdp == 256 ? 256 : 512;
+    if (D == hdp && qtiles * BH < target) {
+        int64_t ns = std::min<int64_t>((target + qtiles * BH - 1) / (qtiles * BH), std::max<int64_t>(1, ktiles / 4));
         const int64_t per = (ktiles + ns - 1) / ns;
         nsplit = (int)((ktiles + per - 1) / per);
     }
