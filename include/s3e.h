@@ -231,6 +231,62 @@ int s3e_preprocess_image(s3e_ctx *ctx, const uint8_t *hwc_device, int width, int
  * runs ViT block idx in place on x. */
 int s3e_vit_prefix(s3e_state *st, const float *chw_device, float *x_device);
 int s3e_vit_block(s3e_state *st, int idx, float *x_device);
+/* Sub-stage hooks, replacing sam3_test_run_vit_block_stage and
+ * sam3_test_run_vit_prefix_stage (sam3.h:441-496, sam3.cpp:6390-6520 and
+ * :6874-6993; stage builders :6716-6872): one operator group of the graph
+ * on an f32 input in ggml 4D layout (in_ne; entries ≤ 0 count as 1), on the
+ * device.  out_ne receives the output shape; with out_device NULL only the
+ * shape is computed (in_device may then be NULL too).  Stage numbers are
+ * the reference's enums (sam3.h:112-134), reproduced below.  Block stages:
+ * NORM1 / NORM2 [E,..] → [E,..]; WINDOW_PART [E,W,H,1] → [E,WS,WS,n]
+ * (zero-padded); QKV_PROJ [E,..] → [3E,..]; ATTN_CORE [3E,W,H,B] → [E,W,H,B]
+ * (q|k|v split, heads, RoPE from the block's table, which must have W·H
+ * positions, attention); ATTN_PROJ [E,..]; WINDOW_UNPART [E,WS,WS,n] →
+ * [E,G,G,1]; MLP_FC1 [E,..] → [MLP,..]; MLP_GELU; MLP_FC2 [MLP,..] → [E,..];
+ * MLP = fc1 + GELU + fc2.  Prefix stages: PATCH_EMBED [img,img,3,1] →
+ * [E,G,G,1]; PATCH_IM2COL → [3P²,G,G,1] (in the kernel's type, as f32);
+ * PATCH_MULMAT_RAW [3P²,G,G,1] → [G²,E,1,1] and PATCH_MULMAT → [G,G,E,1]
+ * (input and kernel rounded to F16, as the reference's F16 input tensor
+ * makes ggml do); POS_ADD; LN_PRE_NORM (ggml_norm); LN_PRE.  Inputs and
+ * outputs of at most G² rows (the state's buffers).  Asynchronous on the
+ * context's stream. */
+enum s3e_vit_block_stage {
+    S3E_VIT_BLOCK_STAGE_NORM1 = 0,
+    S3E_VIT_BLOCK_STAGE_WINDOW_PART,
+    S3E_VIT_BLOCK_STAGE_QKV_PROJ,
+    S3E_VIT_BLOCK_STAGE_ATTN_CORE,
+    S3E_VIT_BLOCK_STAGE_ATTN_PROJ,
+    S3E_VIT_BLOCK_STAGE_WINDOW_UNPART,
+    S3E_VIT_BLOCK_STAGE_NORM2,
+    S3E_VIT_BLOCK_STAGE_MLP_FC1,
+    S3E_VIT_BLOCK_STAGE_MLP_GELU,
+    S3E_VIT_BLOCK_STAGE_MLP_FC2,
+    S3E_VIT_BLOCK_STAGE_MLP
+};
+enum s3e_vit_prefix_stage {
+    S3E_VIT_PREFIX_STAGE_PATCH_EMBED = 0,
+    S3E_VIT_PREFIX_STAGE_PATCH_IM2COL,
+    S3E_VIT_PREFIX_STAGE_PATCH_MULMAT_RAW,
+    S3E_VIT_PREFIX_STAGE_PATCH_MULMAT,
+    S3E_VIT_PREFIX_STAGE_POS_ADD,
+    S3E_VIT_PREFIX_STAGE_LN_PRE_NORM,
+    S3E_VIT_PREFIX_STAGE_LN_PRE
+};
+int s3e_vit_block_stage(s3e_state *st, int idx, int stage, const float *in_device, const int64_t in_ne[4],
+                        float *out_device, int64_t out_ne[4]);
+int s3e_vit_prefix_stage(s3e_state *st, int stage, const float *in_device, const int64_t in_ne[4],
+                         float *out_device, int64_t out_ne[4]);
+/* The backbone alone (prefix + blocks, no neck) into "vit_output": the graph
+ * of sam3_encode_vit_from_preprocessed_selective (sam3.cpp:6237-6327). */
+int s3e_encode_vit_chw(s3e_state *st, const float *chw_device);
+/* A model tensor in its registered type, copied to host memory (the
+ * ggml_backend_tensor_get of sam3.cpp:6540, :6637-6641 in the host
+ * references): "vit.patch_embed.proj.weight" and the block linears
+ * "vit.blocks.<i>.{attn.qkv,attn.proj,mlp.lin1,mlp.lin2}.{weight,bias}".
+ * Weights come back only when stored F16 or F32 (quantized ones are
+ * repacked on the device: S3E_ERR_UNSUPPORTED).  type and ne (ggml order)
+ * are always written; host may be NULL to query them. */
+int s3e_model_tensor_get(const s3e_model *m, const char *name, int *type, int64_t ne[4], void *host, size_t bytes);
 /* Neck stage hook: run the model's necks on a backbone output given on the
  * device (W*H rows of E f32), filling the state's neck_* tensors exactly as
  * s3e_encode_chw does after the backbone (the neck part of the encode graph,

@@ -14,7 +14,10 @@
  *   - params.use_gpu == false is refused (the engine encodes on the GPU);
  *   - params.encode_img_size must be 0 or the model's img_size (the RoPE
  *     tables and positional embedding in the file fix the token grid);
- *   - SAM 2 / EdgeTAM files are refused (magic "sam2" / "edgetam").
+ *   - SAM 2 (Hiera) files are accepted and encoded; EdgeTAM files are
+ *     refused;
+ *   - the test-only stage hooks take inputs of at most the model's token
+ *     count (G² rows), and n_threads is ignored (the work runs on the GPU).
  * The segmentation, tracking and text entry points of sam3.h are not part
  * of the encoder and are not declared here.
  */
@@ -57,6 +60,32 @@ struct sam3_params {
     int         encode_img_size = 0;
 };
 
+/* sam3.h:112-124 */
+enum sam3_vit_block_stage {
+    SAM3_VIT_BLOCK_STAGE_NORM1 = 0,
+    SAM3_VIT_BLOCK_STAGE_WINDOW_PART,
+    SAM3_VIT_BLOCK_STAGE_QKV_PROJ,
+    SAM3_VIT_BLOCK_STAGE_ATTN_CORE,
+    SAM3_VIT_BLOCK_STAGE_ATTN_PROJ,
+    SAM3_VIT_BLOCK_STAGE_WINDOW_UNPART,
+    SAM3_VIT_BLOCK_STAGE_NORM2,
+    SAM3_VIT_BLOCK_STAGE_MLP_FC1,
+    SAM3_VIT_BLOCK_STAGE_MLP_GELU,
+    SAM3_VIT_BLOCK_STAGE_MLP_FC2,
+    SAM3_VIT_BLOCK_STAGE_MLP,
+};
+
+/* sam3.h:126-134 */
+enum sam3_vit_prefix_stage {
+    SAM3_VIT_PREFIX_STAGE_PATCH_EMBED = 0,
+    SAM3_VIT_PREFIX_STAGE_PATCH_IM2COL,
+    SAM3_VIT_PREFIX_STAGE_PATCH_MULMAT_RAW,
+    SAM3_VIT_PREFIX_STAGE_PATCH_MULMAT,
+    SAM3_VIT_PREFIX_STAGE_POS_ADD,
+    SAM3_VIT_PREFIX_STAGE_LN_PRE_NORM,
+    SAM3_VIT_PREFIX_STAGE_LN_PRE,
+};
+
 /* sam3.h:104-110: ne/nb in ggml order; the engine's state tensors are
  * contiguous f32 (type 0) */
 struct sam3_tensor_info {
@@ -97,3 +126,32 @@ bool sam3_dump_state_tensor(const sam3_state & state, const std::string & tensor
                             const std::string & output_path);
 bool sam3_get_state_tensor_info(const sam3_state & state, const std::string & tensor_name,
                                 sam3_tensor_info & info);
+
+/* ---- test-only entry points (sam3.h:436-496) ---- */
+
+/* sam3.h:441: the ViT backbone alone (no neck); output_tensors may name
+ * "vit_output" (the only named tensor of the reference's ViT graph,
+ * sam3.cpp:6237-6327); afterwards the state holds vit_output only. */
+bool sam3_encode_vit_from_preprocessed_selective(sam3_state & state, const sam3_model & model,
+                                                 const float * chw_data, int img_size,
+                                                 const std::vector<std::string> & output_tensors);
+/* sam3.h:451: the prefix (patch embed + pos embed + ln_pre) */
+bool sam3_test_run_vit_block0_input(const sam3_model & model, const float * chw_data, int img_size,
+                                    std::vector<float> & output_data, int64_t output_ne[4], int n_threads = 4);
+/* sam3.h:463: one prefix sub-stage on the GPU */
+bool sam3_test_run_vit_prefix_stage(const sam3_model & model, sam3_vit_prefix_stage stage,
+                                    const float * input_data, const int64_t input_ne[4],
+                                    std::vector<float> & output_data, int64_t output_ne[4], int n_threads = 4);
+/* sam3.h:470, :476: host (CPU) references of the patch mul_mat and the
+ * block linears for F16 weights: fp16 operands, f32 (or double) sums */
+bool sam3_test_run_patch_mulmat_host_ref(const sam3_model & model, const float * input_data,
+                                         const int64_t input_ne[4], bool use_double_accum,
+                                         std::vector<float> & output_data, int64_t output_ne[4]);
+bool sam3_test_run_vit_block_linear_host_ref(const sam3_model & model, int block_idx, sam3_vit_block_stage stage,
+                                             const float * input_data, const int64_t input_ne[4],
+                                             bool use_double_accum, std::vector<float> & output_data,
+                                             int64_t output_ne[4]);
+/* sam3.h:489: one block sub-stage on the GPU */
+bool sam3_test_run_vit_block_stage(const sam3_model & model, int block_idx, sam3_vit_block_stage stage,
+                                   const float * input_data, const int64_t input_ne[4],
+                                   std::vector<float> & output_data, int64_t output_ne[4], int n_threads = 4);

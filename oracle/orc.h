@@ -139,6 +139,13 @@ int  orc_vit_prefix(const orc_model *m, const float *chw, float *x, int nthreads
 int  orc_vit_block(const orc_model *m, int idx, float *x, int nthreads);
 /* Whole backbone: chw → vit_output [T][E]. */
 int  orc_vit_encode(const orc_model *m, const float *chw, float *out, int nthreads);
+/* Sub-stage hooks (sam3_test_run_vit_block_stage / _prefix_stage, stage
+ * numbers of sam3.h:112-134) on an f32 input in ggml 4D layout; out_ne gets
+ * the output shape, out may be NULL (shape only). */
+int  orc_vit_block_stage(const orc_model *m, int idx, int stage, const float *in, const int64_t in_ne[4],
+                         float *out, int64_t out_ne[4], int nthreads);
+int  orc_vit_prefix_stage(const orc_model *m, int stage, const float *in, const int64_t in_ne[4], float *out,
+                          int64_t out_ne[4], int nthreads);
 
 /* ---- SimpleFPN neck (sam3.cpp:3863-3921), NHWC activations --------------- */
 /* ggml_conv_transpose_2d_p0 with a 2×2 fp16 kernel ggml [2, 2, Cout, Cin]:

@@ -396,3 +396,253 @@ int orc_vit_encode(const orc_model *m, const float *chw, float *out, int nthread
     }
     return 0;
 }
+
+/* ------------------------------------------------------------------------ */
+/* Sub-stage hooks: sam3_test_run_vit_block_stage and
+ * sam3_test_run_vit_prefix_stage (sam3.cpp:6390-6520, :6874-6993), one
+ * ggml operator group of the graph at a time on an f32 input in ggml 4D
+ * layout; the stage builders are sam3.cpp:6716-6872.  Stage numbers follow
+ * the enums of sam3.h:112-134.  out may be NULL: only out_ne is produced. */
+enum {
+    BS_NORM1 = 0, BS_WINDOW_PART, BS_QKV_PROJ, BS_ATTN_CORE, BS_ATTN_PROJ, BS_WINDOW_UNPART, BS_NORM2,
+    BS_MLP_FC1, BS_MLP_GELU, BS_MLP_FC2, BS_MLP
+};
+enum { PS_PATCH_EMBED = 0, PS_PATCH_IM2COL, PS_PATCH_MULMAT_RAW, PS_PATCH_MULMAT, PS_POS_ADD, PS_LN_PRE_NORM, PS_LN_PRE };
+
+static void norm_ne(const int64_t in[4], int64_t ne[4]) {
+    for (int i = 0; i < 4; i++) ne[i] = (in && in[i] > 0) ? in[i] : 1;
+}
+
+/* y = W·x + bias over rows of K (ggml_add(ggml_mul_mat(w, x), b)). */
+static void linear_bias(const orc_tensor *w, const orc_tensor *b, const float *x, int64_t M, float *y,
+                        int nthreads) {
+    const int64_t K = w->ne[0], N = w->ne[1];
+    orc_mul_mat(w->type, w->data, N, K, x, M, y, nthreads);
+    const float *bb = (const float *)b->data;
+    for (int64_t r = 0; r < M; r++)
+        for (int64_t c = 0; c < N; c++) y[r * N + c] = y[r * N + c] + bb[c];
+}
+
+int orc_vit_block_stage(const orc_model *m, int bi, int stage, const float *in, const int64_t in_ne[4],
+                        float *out, int64_t out_ne[4], int nthreads) {
+    const orc_hp *hp = &m->hp;
+    if (m->is_sam2) { snprintf(g_err, sizeof g_err, "not a SAM 3 model"); return -1; }
+    if (bi < 0 || bi >= hp->depth) { snprintf(g_err, sizeof g_err, "invalid block_idx=%d", bi); return -1; }
+    if (stage < BS_NORM1 || stage > BS_MLP) { snprintf(g_err, sizeof g_err, "unknown block stage %d", stage); return -1; }
+    const int E = hp->E, G = hp->img_size / hp->patch, NH = hp->heads, HD = E / NH, WS = hp->window;
+    const orc_tensor *f1w = findf(m, "vit.blocks.%d.mlp.lin1.weight", bi);
+    if (!f1w) { snprintf(g_err, sizeof g_err, "block %d: missing tensors", bi); return -1; }
+    const int MLP = (int)f1w->ne[1];
+    int64_t ne[4];
+    norm_ne(in_ne, ne);
+    const int64_t want0 = stage == BS_ATTN_CORE ? 3 * E : ((stage == BS_MLP_GELU || stage == BS_MLP_FC2) ? MLP : E);
+    if (ne[0] != want0) {
+        snprintf(g_err, sizeof g_err, "stage %d input ne0=%lld expected %lld", stage, (long long)ne[0], (long long)want0);
+        return -1;
+    }
+    const int64_t rows = ne[1] * ne[2] * ne[3];
+    int64_t o[4] = {ne[0], ne[1], ne[2], ne[3]};
+    switch (stage) {
+        case BS_WINDOW_PART: {
+            if (ne[3] != 1) { snprintf(g_err, sizeof g_err, "window partition needs ne3 = 1"); return -1; }
+            const int64_t npx = (ne[1] + WS - 1) / WS, npy = (ne[2] + WS - 1) / WS;
+            o[1] = WS; o[2] = WS; o[3] = npx * npy;
+        } break;
+        case BS_WINDOW_UNPART:
+            if (ne[1] != WS || ne[2] != WS) { snprintf(g_err, sizeof g_err, "window unpartition needs [E, %d, %d, n]", WS, WS); return -1; }
+            if (ne[3] != (int64_t)((G + WS - 1) / WS) * ((G + WS - 1) / WS)) { snprintf(g_err, sizeof g_err, "window count %lld does not tile the %dx%d grid", (long long)ne[3], G, G); return -1; }
+            o[1] = G; o[2] = G; o[3] = 1;
+            break;
+        case BS_QKV_PROJ: o[0] = 3 * E; break;
+        case BS_ATTN_CORE: o[0] = E; break;
+        case BS_MLP_FC1: o[0] = MLP; break;
+        case BS_MLP_FC2: o[0] = E; break;
+        default: break;
+    }
+    for (int i = 0; i < 4; i++) out_ne[i] = o[i];
+    if (!out) return 0;
+    if (nthreads <= 0) nthreads = omp_get_max_threads();
+#define T_(s) findf(m, "vit.blocks.%d." s, bi)
+    switch (stage) {
+        case BS_NORM1:
+        case BS_NORM2: {
+            const orc_tensor *w = stage == BS_NORM1 ? T_("norm1.weight") : T_("norm2.weight");
+            const orc_tensor *b = stage == BS_NORM1 ? T_("norm1.bias") : T_("norm2.bias");
+            orc_layer_norm(in, out, rows, E, 1e-5f, (const float *)w->data, (const float *)b->data, nthreads);
+        } break;
+        case BS_WINDOW_PART: /* ggml_win_part: window py*npx + px, zero padding */
+        case BS_WINDOW_UNPART: {
+            const int part = stage == BS_WINDOW_PART;
+            const int64_t W0 = part ? ne[1] : G, H0 = part ? ne[2] : G;
+            const int64_t npx = (W0 + WS - 1) / WS, npy = (H0 + WS - 1) / WS;
+            for (int64_t w = 0; w < npx * npy; w++)
+                for (int64_t p = 0; p < (int64_t)WS * WS; p++) {
+                    const int64_t x = (w % npx) * WS + p % WS, y = (w / npx) * WS + p / WS;
+                    const int64_t wr = w * WS * WS + p, tr = y * W0 + x;
+                    const int inside = x < W0 && y < H0;
+                    if (part) {
+                        if (inside) memcpy(out + wr * E, in + tr * E, sizeof(float) * E);
+                        else memset(out + wr * E, 0, sizeof(float) * E);
+                    } else if (inside) {
+                        memcpy(out + tr * E, in + wr * E, sizeof(float) * E);
+                    }
+                }
+        } break;
+        case BS_QKV_PROJ: linear_bias(T_("attn.qkv.weight"), T_("attn.qkv.bias"), in, rows, out, nthreads); break;
+        case BS_ATTN_PROJ: linear_bias(T_("attn.proj.weight"), T_("attn.proj.bias"), in, rows, out, nthreads); break;
+        case BS_MLP_FC1: linear_bias(f1w, T_("mlp.lin1.bias"), in, rows, out, nthreads); break;
+        case BS_MLP_FC2: linear_bias(T_("mlp.lin2.weight"), T_("mlp.lin2.bias"), in, rows, out, nthreads); break;
+        case BS_MLP_GELU:
+            memcpy(out, in, sizeof(float) * (size_t)(rows * MLP));
+            orc_gelu_erf(out, rows * MLP);
+            break;
+        case BS_MLP: {
+            float *h = (float *)malloc(sizeof(float) * (size_t)(rows * MLP));
+            linear_bias(f1w, T_("mlp.lin1.bias"), in, rows, h, nthreads);
+            orc_gelu_erf(h, rows * MLP);
+            linear_bias(T_("mlp.lin2.weight"), T_("mlp.lin2.bias"), h, rows, out, nthreads);
+            free(h);
+        } break;
+        case BS_ATTN_CORE: {
+            /* sam3_build_vit_attn_core_from_qkv (sam3.cpp:6778-6823): q|k|v
+             * column thirds, heads of HD, RoPE on Q and K, flash attention,
+             * output [E, W, H, B] with heads adjacent. */
+            const int64_t N = ne[1] * ne[2], B = ne[3];
+            const orc_tensor *fc = T_("attn.freqs_cis");
+            if (fc && fc->ne[2] != N) {
+                snprintf(g_err, sizeof g_err, "freqs_cis has %lld positions, attention has %lld", (long long)fc->ne[2], (long long)N);
+                return -1;
+            }
+            float *Q = (float *)malloc(sizeof(float) * (size_t)(B * N * E));
+            float *K = (float *)malloc(sizeof(float) * (size_t)(B * N * E));
+            for (int64_t b = 0; b < B; b++)
+                for (int h = 0; h < NH; h++)
+                    for (int64_t p = 0; p < N; p++) {
+                        const float *src = in + (b * N + p) * 3 * E;
+                        memcpy(Q + ((b * NH + h) * N + p) * HD, src + h * HD, sizeof(float) * HD);
+                        memcpy(K + ((b * NH + h) * N + p) * HD, src + E + h * HD, sizeof(float) * HD);
+                    }
+            if (fc) {
+                orc_rope(Q, HD, N, (int64_t)NH * B, (const float *)fc->data);
+                orc_rope(K, HD, N, (int64_t)NH * B, (const float *)fc->data);
+            }
+            orc_flash_attn_ext(Q, HD, N * HD, (int64_t)NH * N * HD, K, HD, N * HD, (int64_t)NH * N * HD,
+                               in + 2 * E, 3 * E, HD, N * 3 * E, HD, N, N, NH, B, 1.0f / sqrtf((float)HD), out,
+                               nthreads);
+            free(Q);
+            free(K);
+        } break;
+        default: break;
+    }
+#undef T_
+    return 0;
+}
+
+int orc_vit_prefix_stage(const orc_model *m, int stage, const float *in, const int64_t in_ne[4], float *out,
+                         int64_t out_ne[4], int nthreads) {
+    const orc_hp *hp = &m->hp;
+    if (m->is_sam2) { snprintf(g_err, sizeof g_err, "not a SAM 3 model"); return -1; }
+    if (stage < PS_PATCH_EMBED || stage > PS_LN_PRE) { snprintf(g_err, sizeof g_err, "unknown prefix stage %d", stage); return -1; }
+    const int P = hp->patch, G = hp->img_size / P, E = hp->E, T = G * G;
+    const int64_t Kp = (int64_t)P * P * 3;
+    const orc_tensor *pw = find(m, "vit.patch_embed.proj.weight");
+    const orc_tensor *pos = find(m, "vit.pos_embed");
+    const orc_tensor *lw = find(m, "vit.ln_pre.weight"), *lb = find(m, "vit.ln_pre.bias");
+    if (!pw || !pos || !lw || !lb) { snprintf(g_err, sizeof g_err, "missing prefix tensors"); return -1; }
+    int64_t ne[4];
+    norm_ne(in_ne, ne);
+    int64_t o[4] = {ne[0], ne[1], ne[2], ne[3]};
+    switch (stage) {
+        case PS_PATCH_EMBED:
+        case PS_PATCH_IM2COL:
+            if (ne[0] != hp->img_size || ne[1] != hp->img_size || ne[2] != 3 || ne[3] != 1) {
+                snprintf(g_err, sizeof g_err, "patch_embed input shape mismatch");
+                return -1;
+            }
+            o[0] = stage == PS_PATCH_EMBED ? E : Kp; o[1] = G; o[2] = G; o[3] = 1;
+            break;
+        case PS_PATCH_MULMAT_RAW:
+        case PS_PATCH_MULMAT:
+            if (ne[0] != Kp || ne[1] != G || ne[2] != G || ne[3] != 1) {
+                snprintf(g_err, sizeof g_err, "patch_mulmat input shape mismatch");
+                return -1;
+            }
+            if (stage == PS_PATCH_MULMAT_RAW) { o[0] = T; o[1] = E; o[2] = 1; o[3] = 1; }
+            else { o[0] = G; o[1] = G; o[2] = E; o[3] = 1; }
+            break;
+        default:
+            if (ne[0] != E || ne[1] != G || ne[2] != G) {
+                snprintf(g_err, sizeof g_err, "prefix feature input shape mismatch");
+                return -1;
+            }
+            break;
+    }
+    for (int i = 0; i < 4; i++) out_ne[i] = o[i];
+    if (!out) return 0;
+    if (nthreads <= 0) nthreads = omp_get_max_threads();
+    const int64_t rows = ne[1] * ne[2] * ne[3];
+    switch (stage) {
+        case PS_PATCH_EMBED:
+            /* the conv without position embedding and norm: the prefix on a
+             * zero position table would add zeros, so compute it directly */
+        case PS_PATCH_IM2COL: {
+            const int ptype = pw->type;
+            const size_t rs = orc_row_size(ptype, Kp);
+            char *cols = (char *)malloc(rs * (size_t)T);
+            const size_t plane = (size_t)hp->img_size * hp->img_size;
+#pragma omp parallel for num_threads(nthreads)
+            for (int t = 0; t < T; t++) {
+                const int py = t / G, px = t % G;
+                float tmp[3 * 64 * 64];
+                int64_t k = 0;
+                for (int c = 0; c < 3; c++)
+                    for (int ky = 0; ky < P; ky++)
+                        for (int kx = 0; kx < P; kx++)
+                            tmp[k++] = in[c * plane + (size_t)(py * P + ky) * hp->img_size + px * P + kx];
+                orc_from_float(ptype, tmp, cols + (size_t)t * rs, Kp);
+            }
+            if (stage == PS_PATCH_IM2COL) {
+                for (int t = 0; t < T; t++) {
+                    if (ptype == ORC_TYPE_F16) orc_fp16_to_fp32_row((const uint16_t *)(cols + (size_t)t * rs), out + (size_t)t * Kp, Kp);
+                    else memcpy(out + (size_t)t * Kp, cols + (size_t)t * rs, sizeof(float) * Kp);
+                }
+            } else {
+#pragma omp parallel for num_threads(nthreads)
+                for (int t = 0; t < T; t++)
+                    for (int e = 0; e < E; e++)
+                        out[(size_t)t * E + e] = orc_vec_dot(ptype, Kp, cols + (size_t)t * rs, (const char *)pw->data + (size_t)e * rs);
+            }
+            free(cols);
+        } break;
+        case PS_PATCH_MULMAT_RAW:
+        case PS_PATCH_MULMAT: {
+            /* the stage's input tensor is F16 (sam3.cpp:6463-6464); mul_mat(im2col,
+             * kernel) converts the kernel to F16 too; result[e][t] */
+            uint16_t *a = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)(T * Kp));
+            uint16_t *kw = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)(E * Kp));
+            orc_fp32_to_fp16_row(in, a, T * Kp);
+            if (pw->type == ORC_TYPE_F16) memcpy(kw, pw->data, sizeof(uint16_t) * (size_t)(E * Kp));
+            else orc_fp32_to_fp16_row((const float *)pw->data, kw, E * Kp);
+#pragma omp parallel for num_threads(nthreads)
+            for (int e = 0; e < E; e++)
+                for (int t = 0; t < T; t++)
+                    out[(size_t)e * T + t] = orc_vec_dot(ORC_TYPE_F16, Kp, a + (size_t)t * Kp, kw + (size_t)e * Kp);
+            free(a);
+            free(kw);
+        } break;
+        case PS_POS_ADD: {
+            const int pg = (int)pos->ne[1];
+            for (int64_t r = 0; r < rows; r++) {
+                const int64_t t = r % T, py = t / G, px = t % G;
+                const float *pr = (const float *)pos->data + ((size_t)(py % pg) * pg + (px % pg)) * E;
+                for (int e = 0; e < E; e++) out[r * E + e] = in[r * E + e] + pr[e];
+            }
+        } break;
+        case PS_LN_PRE_NORM: orc_layer_norm(in, out, rows, E, 1e-5f, NULL, NULL, nthreads); break;
+        case PS_LN_PRE:
+            orc_layer_norm(in, out, rows, E, 1e-5f, (const float *)lw->data, (const float *)lb->data, nthreads);
+            break;
+        default: break;
+    }
+    return 0;
+}

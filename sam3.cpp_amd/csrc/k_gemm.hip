@@ -840,8 +840,8 @@ hipError_t dispatch_waves(Epi epi, GemmParams &p, hipStream_t st) {
     // 4-wave work-groups (three per CU, 4-12% faster on the SAM 3 shapes)
     // except for Q4_1, whose extra minimum term needs more registers than
     // three work-groups per CU leave
-    const int waves = (WK == WK_Q4_1) ? 8 : 4;
-    return waves == 4 ? dispatch_epi<WK, 4>(epi, p, st) : dispatch_epi<WK, 8>(epi, p, st);
+    if constexpr (WK == WK_Q4_1) return dispatch_epi<WK, 8>(epi, p, st);
+    else return dispatch_epi<WK, 4>(epi, p, st);
 }
 
 // K ranges for a product that leaves CUs idle: fewer 64 × 128 tiles than CUs

@@ -332,3 +332,147 @@ hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t st)
 }
 
 }  // namespace s3e
+
+// ---- sub-stage hooks (sam3_test_run_vit_block_stage / _prefix_stage) ----------
+// The fused encoder never materialises these intermediates; the hooks do,
+// with the same device arithmetic the fused epilogues use.
+namespace s3e {
+namespace {
+
+// ggml_gelu_erf on f32, the device gelu_erf of the fc1 epilogue.
+__global__ __launch_bounds__(256) void k_gelu_rows(const float *__restrict__ x, float *__restrict__ y, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = gelu_erf(x[i]);
+}
+
+// ggml_win_part / ggml_win_unpart on rows of E (E % 4 == 0): window
+// w = wy·npx + wx of WS×WS positions, zero rows where a window leaves the
+// W0×H0 grid (partition only).  One thread per float4.
+__global__ __launch_bounds__(256) void k_win_perm(const float4 *__restrict__ x, float4 *__restrict__ y, int W0,
+                                                  int H0, int WS, int64_t e4, int64_t n, int part) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int64_t r = i / e4, c = i - r * e4;  // window row r = w·WS² + p
+    const int64_t npx = (W0 + WS - 1) / WS;
+    const int64_t w = r / ((int64_t)WS * WS), p = r - w * WS * WS;
+    const int64_t gx = (w % npx) * WS + p % WS, gy = (w / npx) * WS + p / WS;
+    const bool inside = gx < W0 && gy < H0;
+    const int64_t t = gy * W0 + gx;
+    if (part) y[i] = inside ? x[t * e4 + c] : make_float4(0.f, 0.f, 0.f, 0.f);
+    else if (inside) y[t * e4 + c] = x[i];
+}
+
+// Q and K of the ViT attention core from qkv rows [B·N][3E] (bias added):
+// q|k column thirds, heads of HD; RoPE as sam3_apply_rope (each product
+// rounded, then the difference / sum, as the EPI_QKV epilogue computes it);
+// out [2][B][NH][N][HD] f32.  One thread per (re, im) pair.
+__global__ __launch_bounds__(256) void k_vit_rope_split(const float *__restrict__ qkv, const float *__restrict__ freqs,
+                                                        float *__restrict__ out, int64_t B, int64_t N, int NH, int HD,
+                                                        int64_t npairs) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= npairs) return;
+    const int half = HD / 2;
+    const int64_t E = (int64_t)NH * HD;
+    const int j = (int)(i % half);
+    const int64_t p = (i / half) % N, h = (i / ((int64_t)half * N)) % NH;
+    const int64_t b = (i / ((int64_t)half * N * NH)) % B, sel = i / ((int64_t)half * N * NH * B);
+    const float *src = qkv + (b * N + p) * 3 * E + sel * E + h * HD + 2 * j;
+    float re = src[0], im = src[1];
+    if (freqs) {
+        const float c = freqs[(p * half + j) * 2], s = freqs[(p * half + j) * 2 + 1];
+        const float r2 = __fsub_rn(__fmul_rn(re, c), __fmul_rn(im, s));
+        const float i2 = __fadd_rn(__fmul_rn(re, s), __fmul_rn(im, c));
+        re = r2;
+        im = i2;
+    }
+    float *dst = out + (((sel * B + b) * NH + h) * N + p) * HD + 2 * j;
+    dst[0] = re;
+    dst[1] = im;
+}
+
+// Activation rows (A_F16 or A_F32, row stride ld) → f32 [M][K].
+__global__ __launch_bounds__(256) void k_act_f32(const void *__restrict__ x, int kind, int64_t ld, int64_t K,
+                                                 int64_t n, float *__restrict__ y) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int64_t r = i / K, c = i - r * K;
+    y[i] = kind == A_F16 ? (float)((const _Float16 *)x)[r * ld + c] : ((const float *)x)[r * ld + c];
+}
+
+// [R][C] → [C][R] through a 32×33 LDS tile.
+__global__ __launch_bounds__(256) void k_transpose(const float *__restrict__ x, float *__restrict__ y, int64_t R,
+                                                   int64_t C) {
+    __shared__ float tile[32][33];
+    const int64_t r0 = (int64_t)blockIdx.y * 32, c0 = (int64_t)blockIdx.x * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+    for (int k = ty; k < 32; k += 8) {
+        const int64_t r = r0 + k, c = c0 + tx;
+        if (r < R && c < C) tile[k][tx] = x[r * C + c];
+    }
+    __syncthreads();
+    for (int k = ty; k < 32; k += 8) {
+        const int64_t c = c0 + k, r = r0 + tx;
+        if (r < R && c < C) y[c * R + r] = tile[tx][k];
+    }
+}
+
+// ggml_add(x, ggml_repeat(pos [pg][pg][E], [E, G, G])): rows of E, token
+// t = row % G² at (t / G, t % G).
+__global__ __launch_bounds__(256) void k_add_pos(const float *__restrict__ x, const float *__restrict__ pos,
+                                                 float *__restrict__ y, int G, int pg, int64_t E, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int64_t r = i / E, e = i - r * E, t = r % ((int64_t)G * G);
+    const int64_t py = t / G, px = t % G;
+    y[i] = __fadd_rn(x[i], pos[((py % pg) * pg + px % pg) * E + e]);
+}
+
+inline dim3 blocks_for(int64_t n) { return dim3((unsigned)((n + 255) / 256)); }
+
+}  // namespace
+
+hipError_t launch_gelu_rows(const float *x, float *y, int64_t n, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_gelu_rows, blocks_for(n), dim3(256), 0, st, x, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_win_perm(const float *x, float *y, int W0, int H0, int WS, int64_t E, int part, hipStream_t st) {
+    if (E % 4 != 0 || WS <= 0 || W0 <= 0 || H0 <= 0) return hipErrorInvalidValue;
+    const int64_t nw = (int64_t)((W0 + WS - 1) / WS) * ((H0 + WS - 1) / WS);
+    const int64_t n = nw * WS * WS * (E / 4);
+    hipLaunchKernelGGL(k_win_perm, blocks_for(n), dim3(256), 0, st, (const float4 *)x, (float4 *)y, W0, H0, WS,
+                       E / 4, n, part);
+    return hipGetLastError();
+}
+
+hipError_t launch_vit_rope_split(const float *qkv, const float *freqs, float *out, int64_t B, int64_t N, int NH,
+                                 int HD, hipStream_t st) {
+    if (HD % 2 != 0 || B <= 0 || N <= 0) return hipErrorInvalidValue;
+    const int64_t np = 2 * B * NH * N * (HD / 2);
+    hipLaunchKernelGGL(k_vit_rope_split, blocks_for(np), dim3(256), 0, st, qkv, freqs, out, B, N, NH, HD, np);
+    return hipGetLastError();
+}
+
+hipError_t launch_act_f32(const Act &a, int64_t M, int64_t K, float *y, hipStream_t st) {
+    if (a.kind != A_F16 && a.kind != A_F32) return hipErrorInvalidValue;
+    const int64_t n = M * K;
+    hipLaunchKernelGGL(k_act_f32, blocks_for(n), dim3(256), 0, st, (const void *)a.x, (int)a.kind, a.ld, K, n, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_transpose(const float *x, float *y, int64_t R, int64_t C, hipStream_t st) {
+    const dim3 grid((unsigned)((C + 31) / 32), (unsigned)((R + 31) / 32));
+    hipLaunchKernelGGL(k_transpose, grid, dim3(256), 0, st, x, y, R, C);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_pos(const float *x, const float *pos, float *y, int G, int pg, int64_t E, int64_t rows,
+                          hipStream_t st) {
+    const int64_t n = rows * E;
+    hipLaunchKernelGGL(k_add_pos, blocks_for(n), dim3(256), 0, st, x, pos, y, G, pg, E, n);
+    return hipGetLastError();
+}
+
+
+}  // namespace s3e

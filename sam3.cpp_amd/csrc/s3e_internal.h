@@ -253,6 +253,21 @@ hipError_t launch_add_scaled(float *y, const float *a, const float *b, float s, 
 // w = h = S) and normalisation (norm 0: (v − 0.5)/0.5, 1: ImageNet mean/std).
 hipError_t launch_preprocess(const uint8_t *hwc, int w, int h, int S, int norm, float *chw, hipStream_t st);
 
+// ---- sub-stage hooks (k_rows.hip) ----
+hipError_t launch_gelu_rows(const float *x, float *y, int64_t n, hipStream_t st);
+// ggml_win_part (part = 1: grid rows → window rows, zero-padded) or
+// ggml_win_unpart (part = 0) on rows of E floats over a W0 × H0 grid
+hipError_t launch_win_perm(const float *x, float *y, int W0, int H0, int WS, int64_t E, int part, hipStream_t st);
+// qkv [B·N][3·NH·HD] → RoPE'd Q and K, f32 [2][B][NH][N][HD] (freqs may be null)
+hipError_t launch_vit_rope_split(const float *qkv, const float *freqs, float *out, int64_t B, int64_t N, int NH,
+                                 int HD, hipStream_t st);
+// A_F16 / A_F32 activation rows → f32 [M][K]
+hipError_t launch_act_f32(const Act &a, int64_t M, int64_t K, float *y, hipStream_t st);
+hipError_t launch_transpose(const float *x, float *y, int64_t R, int64_t C, hipStream_t st);
+// y = x + pos tiled over the G × G grid (pos [pg][pg][E]); rows of E
+hipError_t launch_add_pos(const float *x, const float *pos, float *y, int G, int pg, int64_t E, int64_t rows,
+                          hipStream_t st);
+
 // ---- Hiera (k_hiera.hip) ----
 // Patch-embedding im2col: CHW f32 [3][S][S], k×k / stride / pad → rows of ldk.
 hipError_t launch_im2col_conv(const float *chw, int S, int k, int stride, int pad, int64_t ldk, AKind kind,

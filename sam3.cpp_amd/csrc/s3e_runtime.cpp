@@ -1127,6 +1127,11 @@ struct s3e_state {
     hipStream_t aux[2] = {nullptr, nullptr};
     hipEvent_t ev_fork = nullptr, ev_join[2] = {nullptr, nullptr};
     HieraState *hst = nullptr;  // SAM 2.x models
+    // sub-stage hooks: f32 scratch grown on demand, and an F16 copy of an
+    // F32 patch kernel (the mul_mat stages convert the kernel to F16)
+    float *stg = nullptr;
+    int64_t stg_cap = 0;
+    Weight patch16;
 };
 
 extern "C" void s3e_state_free(s3e_state *st) {
@@ -1160,6 +1165,8 @@ extern "C" void s3e_state_free(s3e_state *st) {
     }
     if (st->ev_fork) (void)hipEventDestroy(st->ev_fork);
     if (st->hst) hiera_state_free(st->hst);
+    if (st->stg) (void)hipFree(st->stg);
+    free_weight(st->patch16);
     delete st;
 }
 
@@ -1480,6 +1487,350 @@ extern "C" int s3e_vit_block(s3e_state *st, int idx, float *x_device) {
     if (idx < 0 || idx >= st->m->depth) { set_error("s3e_vit_block: block %d out of range", idx); return S3E_ERR_INVALID; }
     HIP_TRY(hipSetDevice(st->ctx->device));
     HIP_TRY(run_block(st, idx, x_device));
+    return S3E_OK;
+}
+
+// ---- sub-stage hooks --------------------------------------------------------
+// sam3_test_run_vit_block_stage / sam3_test_run_vit_prefix_stage
+// (sam3.cpp:6390-6520, :6874-6993; stage builders :6716-6872): one operator
+// group of the graph on an f32 input in ggml 4D layout, through the kernels
+// the encoder uses for it.  Where the encoder fuses a stage into a
+// neighbour's epilogue (window partition into the QKV store, RoPE into the
+// QKV epilogue, GELU into fc1's, the position table into the patch GEMM's),
+// the hook runs the same device arithmetic as a stand-alone pass.
+namespace {
+
+enum : int {
+    BS_NORM1 = 0, BS_WINDOW_PART, BS_QKV_PROJ, BS_ATTN_CORE, BS_ATTN_PROJ, BS_WINDOW_UNPART, BS_NORM2,
+    BS_MLP_FC1, BS_MLP_GELU, BS_MLP_FC2, BS_MLP
+};
+enum : int { PS_PATCH_EMBED = 0, PS_PATCH_IM2COL, PS_PATCH_MULMAT_RAW, PS_PATCH_MULMAT, PS_POS_ADD, PS_LN_PRE_NORM, PS_LN_PRE };
+
+void norm_ne4(const int64_t *in, int64_t ne[4]) {
+    for (int i = 0; i < 4; i++) ne[i] = (in && in[i] > 0) ? in[i] : 1;
+}
+
+hipError_t stage_scratch(s3e_state *st, int64_t floats) {
+    if (floats <= st->stg_cap) return hipSuccess;
+    if (st->stg) {
+        hipError_t e = hipStreamSynchronize(st->ctx->stream);
+        if (e != hipSuccess) return e;
+        (void)hipFree(st->stg);
+        st->stg = nullptr;
+        st->stg_cap = 0;
+    }
+    hipError_t e = hipMalloc(&st->stg, (size_t)floats * 4);
+    if (e == hipSuccess) st->stg_cap = floats;
+    return e;
+}
+
+// y = W·x + b on M rows: x converted to W's activation format in buf, then
+// the encoder's GEMM with an f32 output.
+hipError_t stage_linear(s3e_state *st, const Weight &w, const float *bias, const ActBuf &buf, const float *x,
+                        int64_t M, float *y) {
+    hipStream_t s = st->ctx->stream;
+    const Act a = buf.as(act_kind_for(w.kind), w.K);
+    hipError_t e = launch_rows_quant(a.kind, x, M, w.K, a, s);
+    if (e != hipSuccess) return e;
+    EpiArgs ea;
+    ea.bias = bias;
+    ea.y = y;
+    ea.ldy = w.N;
+    return launch_gemm(w, a, M, EPI_F32, ea, s);
+}
+
+// The F16 patch kernel the mul_mat stages multiply by.
+int patch_f16(s3e_state *st, const Weight **out) {
+    const s3e_model *m = st->m;
+    if (m->patch_w.kind == WK_F16) { *out = &m->patch_w; return S3E_OK; }
+    if (!st->patch16.q) {
+        const Weight &w = m->patch_w;  // WK_F32 [Np][Kp]
+        std::vector<float> f((size_t)(w.Np * w.Kp));
+        HIP_TRY(hipMemcpy(f.data(), w.q, f.size() * 4, hipMemcpyDeviceToHost));
+        std::vector<uint16_t> h((size_t)(w.N * w.K));
+        for (int64_t n = 0; n < w.N; n++)
+            for (int64_t k = 0; k < w.K; k++) h[(size_t)(n * w.K + k)] = host_f2h(f[(size_t)(n * w.Kp + k)]);
+        const int rc = upload_weight(st->ctx->device, S3E_TYPE_F16, w.K, w.N, (const uint8_t *)h.data(),
+                                     h.size() * 2, st->patch16);
+        if (rc != S3E_OK) return rc;
+    }
+    *out = &st->patch16;
+    return S3E_OK;
+}
+
+}  // namespace
+
+extern "C" int s3e_vit_block_stage(s3e_state *st, int idx, int stage, const float *in_device, const int64_t in_ne[4],
+                                   float *out_device, int64_t out_ne[4]) {
+    if (!st || !in_ne || !out_ne) { set_error("s3e_vit_block_stage: NULL argument"); return S3E_ERR_INVALID; }
+    const s3e_model *m = st->m;
+    if (m->hiera) { set_error("s3e_vit_block_stage: the model is a SAM 2 (Hiera) encoder"); return S3E_ERR_INVALID; }
+    if (idx < 0 || idx >= m->depth) { set_error("s3e_vit_block_stage: invalid block_idx=%d", idx); return S3E_ERR_INVALID; }
+    if (stage < BS_NORM1 || stage > BS_MLP) { set_error("s3e_vit_block_stage: unknown stage %d", stage); return S3E_ERR_INVALID; }
+    const Block &b = m->blocks[(size_t)idx];
+    const int64_t E = m->E, MLP = m->mlp, G = m->grid, WS = m->window, NH = m->heads, HD = E / NH;
+    int64_t ne[4];
+    norm_ne4(in_ne, ne);
+    const int64_t want0 = stage == BS_ATTN_CORE ? 3 * E : ((stage == BS_MLP_GELU || stage == BS_MLP_FC2) ? MLP : E);
+    if (ne[0] != want0) {
+        set_error("s3e_vit_block_stage: stage %d input ne0=%lld expected %lld", stage, (long long)ne[0], (long long)want0);
+        return S3E_ERR_INVALID;
+    }
+    int64_t o[4] = {ne[0], ne[1], ne[2], ne[3]};
+    const int64_t npx = (ne[1] + WS - 1) / WS, npy = (ne[2] + WS - 1) / WS;
+    switch (stage) {
+        case BS_WINDOW_PART:
+            if (ne[3] != 1) { set_error("s3e_vit_block_stage: window partition needs ne3 = 1"); return S3E_ERR_INVALID; }
+            o[1] = WS; o[2] = WS; o[3] = npx * npy;
+            break;
+        case BS_WINDOW_UNPART: {
+            const int64_t nw = ((G + WS - 1) / WS) * ((G + WS - 1) / WS);
+            if (ne[1] != WS || ne[2] != WS || ne[3] != nw) {
+                set_error("s3e_vit_block_stage: window unpartition needs [E, %lld, %lld, %lld]", (long long)WS, (long long)WS, (long long)nw);
+                return S3E_ERR_INVALID;
+            }
+            o[1] = G; o[2] = G; o[3] = 1;
+        } break;
+        case BS_QKV_PROJ: o[0] = 3 * E; break;
+        case BS_ATTN_CORE: o[0] = E; break;
+        case BS_MLP_FC1: o[0] = MLP; break;
+        case BS_MLP_FC2: o[0] = E; break;
+        default: break;
+    }
+    for (int i = 0; i < 4; i++) out_ne[i] = o[i];
+    if (!out_device) return S3E_OK;
+    if (!in_device) { set_error("s3e_vit_block_stage: NULL input"); return S3E_ERR_INVALID; }
+    const int64_t rows = ne[1] * ne[2] * ne[3];
+    const int64_t orows = o[1] * o[2] * o[3];
+    // the state's activation buffers hold T rows
+    if (rows > st->T || orows > st->T) {
+        set_error("s3e_vit_block_stage: %lld rows exceed the state's %lld", (long long)std::max(rows, orows), (long long)st->T);
+        return S3E_ERR_INVALID;
+    }
+    HIP_TRY(hipSetDevice(st->ctx->device));
+    hipStream_t s = st->ctx->stream;
+    Act none;
+    switch (stage) {
+        case BS_NORM1:
+        case BS_NORM2:
+            HIP_TRY(launch_layernorm(in_device, rows, E, 1e-5f, stage == BS_NORM1 ? b.n1w : b.n2w,
+                                     stage == BS_NORM1 ? b.n1b : b.n2b, none, out_device, s));
+            break;
+        case BS_WINDOW_PART:
+            HIP_TRY(launch_win_perm(in_device, out_device, (int)ne[1], (int)ne[2], (int)WS, E, 1, s));
+            break;
+        case BS_WINDOW_UNPART:
+            HIP_TRY(launch_win_perm(in_device, out_device, (int)G, (int)G, (int)WS, E, 0, s));
+            break;
+        case BS_QKV_PROJ: HIP_TRY(stage_linear(st, b.qkv, b.qkv_b, st->a1, in_device, rows, out_device)); break;
+        case BS_ATTN_PROJ: HIP_TRY(stage_linear(st, b.proj, b.proj_b, st->a1, in_device, rows, out_device)); break;
+        case BS_MLP_FC1: HIP_TRY(stage_linear(st, b.fc1, b.fc1_b, st->a1, in_device, rows, out_device)); break;
+        case BS_MLP_FC2: HIP_TRY(stage_linear(st, b.fc2, b.fc2_b, st->a2, in_device, rows, out_device)); break;
+        case BS_MLP_GELU: HIP_TRY(launch_gelu_rows(in_device, out_device, rows * MLP, s)); break;
+        case BS_MLP: {
+            // fc1 with the encoder's fused bias + GELU + conversion epilogue, then fc2
+            const Act a1 = st->a1.as(act_kind_for(b.fc1.kind), E);
+            HIP_TRY(launch_rows_quant(a1.kind, in_device, rows, E, a1, s));
+            EpiArgs e1;
+            e1.bias = b.fc1_b;
+            e1.out = st->a2.as(act_kind_for(b.fc2.kind), MLP);
+            HIP_TRY(launch_gemm(b.fc1, a1, rows, EPI_GELU, e1, s));
+            EpiArgs e2;
+            e2.bias = b.fc2_b;
+            e2.y = out_device;
+            e2.ldy = E;
+            HIP_TRY(launch_gemm(b.fc2, e1.out, rows, EPI_F32, e2, s));
+        } break;
+        case BS_ATTN_CORE: {
+            const int64_t N = ne[1] * ne[2], B = ne[3];
+            if (b.freqs && b.freqs_n != N) {
+                set_error("s3e_vit_block_stage: freqs_cis has %lld positions, attention has %lld", (long long)b.freqs_n, (long long)N);
+                return S3E_ERR_INVALID;
+            }
+            const int64_t ldv = vt_ld_for(N);
+            if (HD != 64 || B * NH * HD * ldv > st->vt_elems || B * NH > 65535) {
+                set_error("s3e_vit_block_stage: attention shape [%lld tokens x %lld windows] not supported", (long long)N, (long long)B);
+                return S3E_ERR_UNSUPPORTED;
+            }
+            HIP_TRY(stage_scratch(st, 2 * rows * E));
+            float *rq = st->stg, *rk = st->stg + rows * E;
+            HIP_TRY(launch_vit_rope_split(in_device, b.freqs, st->stg, B, N, (int)NH, (int)HD, s));
+            // the encoder's rule: split fp16 pairs unless the projection is F16
+            const bool split = b.proj.kind != WK_F16;
+            _Float16 *q_lo = split ? st->q16 + st->T * E : nullptr;
+            _Float16 *k_lo = split ? st->k16 + st->T * E : nullptr;
+            _Float16 *vt_lo = split ? st->vt16 + st->vt_elems : nullptr;
+            HIP_TRY(hipMemsetAsync(st->vt16, 0, (size_t)(B * NH * HD * ldv) * 2, s));
+            if (split) HIP_TRY(hipMemsetAsync(vt_lo, 0, (size_t)(B * NH * HD * ldv) * 2, s));
+            const int64_t qk_nb[4] = {1, HD, N * HD, NH * N * HD};
+            const int64_t v_nb[4] = {1, 3 * E, HD, N * 3 * E};
+            HIP_TRY(launch_attn_prep(rq, qk_nb, rk, qk_nb, in_device + 2 * E, v_nb, N, N, NH, B, (int)HD, 64,
+                                     st->q16, st->k16, st->vt16, q_lo, k_lo, vt_lo, ldv, s));
+            AttnArgs a;
+            a.q = st->q16;
+            a.k = st->k16;
+            a.vt = st->vt16;
+            a.q_lo = q_lo;
+            a.k_lo = k_lo;
+            a.vt_lo = vt_lo;
+            a.Nq = (int)N;
+            a.Nkv = (int)N;
+            a.NH = (int)NH;
+            a.BH = (int)(B * NH);
+            a.scale = 1.0f / std::sqrt((float)HD);
+            a.out.kind = A_F32;
+            a.out.x = out_device;
+            a.out.ld = E;
+            HIP_TRY(launch_attn(a, s));
+        } break;
+        default: break;
+    }
+    return S3E_OK;
+}
+
+extern "C" int s3e_vit_prefix_stage(s3e_state *st, int stage, const float *in_device, const int64_t in_ne[4],
+                                    float *out_device, int64_t out_ne[4]) {
+    if (!st || !in_ne || !out_ne) { set_error("s3e_vit_prefix_stage: NULL argument"); return S3E_ERR_INVALID; }
+    const s3e_model *m = st->m;
+    if (m->hiera) { set_error("s3e_vit_prefix_stage: the model is a SAM 2 (Hiera) encoder"); return S3E_ERR_INVALID; }
+    if (stage < PS_PATCH_EMBED || stage > PS_LN_PRE) { set_error("s3e_vit_prefix_stage: unknown stage %d", stage); return S3E_ERR_INVALID; }
+    const int64_t P = m->patch, G = m->grid, E = m->E, T = st->T, K = 3 * P * P;
+    int64_t ne[4];
+    norm_ne4(in_ne, ne);
+    int64_t o[4] = {ne[0], ne[1], ne[2], ne[3]};
+    switch (stage) {
+        case PS_PATCH_EMBED:
+        case PS_PATCH_IM2COL:
+            if (ne[0] != m->img || ne[1] != m->img || ne[2] != 3 || ne[3] != 1) {
+                set_error("s3e_vit_prefix_stage: patch_embed input shape mismatch");
+                return S3E_ERR_INVALID;
+            }
+            o[0] = stage == PS_PATCH_EMBED ? E : K; o[1] = G; o[2] = G; o[3] = 1;
+            break;
+        case PS_PATCH_MULMAT_RAW:
+        case PS_PATCH_MULMAT:
+            if (ne[0] != K || ne[1] != G || ne[2] != G || ne[3] != 1) {
+                set_error("s3e_vit_prefix_stage: patch_mulmat input shape mismatch");
+                return S3E_ERR_INVALID;
+            }
+            if (stage == PS_PATCH_MULMAT_RAW) { o[0] = T; o[1] = E; o[2] = 1; o[3] = 1; }
+            else { o[0] = G; o[1] = G; o[2] = E; o[3] = 1; }
+            break;
+        default:
+            if (ne[0] != E || ne[1] != G || ne[2] != G) {
+                set_error("s3e_vit_prefix_stage: prefix feature input shape mismatch");
+                return S3E_ERR_INVALID;
+            }
+            break;
+    }
+    for (int i = 0; i < 4; i++) out_ne[i] = o[i];
+    if (!out_device) return S3E_OK;
+    if (!in_device) { set_error("s3e_vit_prefix_stage: NULL input"); return S3E_ERR_INVALID; }
+    const int64_t rows = ne[1] * ne[2] * ne[3];
+    HIP_TRY(hipSetDevice(st->ctx->device));
+    hipStream_t s = st->ctx->stream;
+    const AKind pk = (m->patch_w.kind == WK_F16) ? A_F16 : A_F32;
+    const int64_t ldk = m->patch_w.K;  // 3·P² padded to 32
+    switch (stage) {
+        case PS_PATCH_EMBED: {
+            HIP_TRY(launch_im2col(in_device, m->img, m->patch, ldk, pk, st->col.x, s));
+            EpiArgs ea;
+            ea.y = out_device;
+            ea.ldy = E;
+            HIP_TRY(launch_gemm(m->patch_w, st->col.as(pk, ldk), T, EPI_F32, ea, s));
+        } break;
+        case PS_PATCH_IM2COL:
+            HIP_TRY(launch_im2col(in_device, m->img, m->patch, ldk, pk, st->col.x, s));
+            HIP_TRY(launch_act_f32(st->col.as(pk, ldk), T, K, out_device, s));
+            break;
+        case PS_PATCH_MULMAT_RAW:
+        case PS_PATCH_MULMAT: {
+            // the stage's input is F16 (sam3.cpp:6463-6464) and mul_mat converts
+            // the kernel to F16: fp16 × fp16 products, f32 sums, result [E][T]
+            const Weight *w16 = nullptr;
+            const int rc = patch_f16(st, &w16);
+            if (rc != S3E_OK) return rc;
+            const Act a = st->col.as(A_F16, ldk);
+            HIP_TRY(hipMemsetAsync(a.x, 0, (size_t)(T * ldk) * 2, s));  // zero columns past K
+            HIP_TRY(launch_rows_quant(A_F16, in_device, T, K, a, s));
+            HIP_TRY(stage_scratch(st, T * E));
+            EpiArgs ea;
+            ea.y = st->stg;
+            ea.ldy = E;
+            HIP_TRY(launch_gemm(*w16, a, T, EPI_F32, ea, s));
+            HIP_TRY(launch_transpose(st->stg, out_device, T, E, s));
+        } break;
+        case PS_POS_ADD:
+            HIP_TRY(launch_add_pos(in_device, m->pos, out_device, (int)G, m->pos_grid, E, rows, s));
+            break;
+        case PS_LN_PRE_NORM:
+        case PS_LN_PRE: {
+            Act none;
+            const bool aff = stage == PS_LN_PRE;
+            HIP_TRY(launch_layernorm(in_device, rows, E, 1e-5f, aff ? m->ln_pre_w : nullptr, aff ? m->ln_pre_b : nullptr,
+                                     none, out_device, s));
+        } break;
+        default: break;
+    }
+    return S3E_OK;
+}
+
+extern "C" int s3e_encode_vit_chw(s3e_state *st, const float *chw_device) {
+    if (!st || !chw_device) { set_error("s3e_encode_vit_chw: NULL argument"); return S3E_ERR_INVALID; }
+    if (st->m->hiera) { set_error("s3e_encode_vit_chw: the model is a SAM 2 (Hiera) encoder"); return S3E_ERR_INVALID; }
+    HIP_TRY(hipSetDevice(st->ctx->device));
+    HIP_TRY(run_prefix(st, chw_device, st->x));
+    for (int i = 0; i < st->m->depth; i++) HIP_TRY(run_block(st, i, st->x));
+    return S3E_OK;
+}
+
+extern "C" int s3e_model_tensor_get(const s3e_model *m, const char *name, int *type, int64_t ne[4], void *host,
+                                    size_t bytes) {
+    if (!m || !name || !type || !ne) { set_error("s3e_model_tensor_get: NULL argument"); return S3E_ERR_INVALID; }
+    if (m->hiera) { set_error("s3e_model_tensor_get: the model is a SAM 2 (Hiera) encoder"); return S3E_ERR_UNSUPPORTED; }
+    const std::string n(name);
+    const Weight *w = nullptr;
+    const float *vec = nullptr;
+    int64_t vlen = 0;
+    int64_t K = 0;
+    for (int i = 0; i < 4; i++) ne[i] = 1;
+    if (n == "vit.patch_embed.proj.weight") {
+        w = &m->patch_w;
+        K = 3LL * m->patch * m->patch;
+        ne[0] = m->patch; ne[1] = m->patch; ne[2] = 3; ne[3] = m->E;
+    } else if (n.compare(0, 11, "vit.blocks.") == 0) {
+        const size_t dot = n.find('.', 11);
+        const int bi = dot == std::string::npos ? -1 : std::atoi(n.substr(11, dot - 11).c_str());
+        if (bi < 0 || bi >= m->depth) { set_error("s3e_model_tensor_get: no tensor '%s'", name); return S3E_ERR_INVALID; }
+        const Block &b = m->blocks[(size_t)bi];
+        const std::string rest = n.substr(dot + 1);
+        const struct { const char *w, *b; const Weight *wt; const float *bias; } lin[4] = {
+            {"attn.qkv.weight", "attn.qkv.bias", &b.qkv, b.qkv_b}, {"attn.proj.weight", "attn.proj.bias", &b.proj, b.proj_b},
+            {"mlp.lin1.weight", "mlp.lin1.bias", &b.fc1, b.fc1_b}, {"mlp.lin2.weight", "mlp.lin2.bias", &b.fc2, b.fc2_b}};
+        for (const auto &l : lin) {
+            if (rest == l.w) { w = l.wt; K = w->K; ne[0] = w->K; ne[1] = w->N; }
+            if (rest == l.b) { vec = l.bias; vlen = l.wt->N; ne[0] = vlen; }
+        }
+    }
+    if (!w && !vec) { set_error("s3e_model_tensor_get: no tensor '%s' (linear and patch weights and biases only)", name); return S3E_ERR_INVALID; }
+    if (vec) {
+        *type = S3E_TYPE_F32;
+        if (!host) return S3E_OK;
+        if (bytes < (size_t)vlen * 4) { set_error("s3e_model_tensor_get: buffer too small"); return S3E_ERR_INVALID; }
+        HIP_TRY(hipSetDevice(m->ctx->device));
+        HIP_TRY(hipMemcpy(host, vec, (size_t)vlen * 4, hipMemcpyDeviceToHost));
+        return S3E_OK;
+    }
+    if (w->kind != WK_F16 && w->kind != WK_F32) {
+        set_error("s3e_model_tensor_get: '%s' is quantized; only F16 and F32 weights are returned", name);
+        return S3E_ERR_UNSUPPORTED;
+    }
+    *type = w->kind == WK_F16 ? S3E_TYPE_F16 : S3E_TYPE_F32;
+    if (!host) return S3E_OK;
+    const size_t es = w->kind == WK_F16 ? 2 : 4;
+    if (bytes < (size_t)(K * w->N) * es) { set_error("s3e_model_tensor_get: buffer too small"); return S3E_ERR_INVALID; }
+    HIP_TRY(hipSetDevice(m->ctx->device));
+    HIP_TRY(hipMemcpy2D(host, (size_t)K * es, w->q, (size_t)w->Kp * es, (size_t)K * es, (size_t)w->N, hipMemcpyDeviceToHost));
     return S3E_OK;
 }
 

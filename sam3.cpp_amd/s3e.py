@@ -103,6 +103,10 @@ def _load() -> ctypes.CDLL:
         "s3e_vit_prefix": (c_int, [c_void_p, c_void_p, c_void_p]),
         "s3e_vit_block": (c_int, [c_void_p, c_int, c_void_p]),
         "s3e_run_neck": (c_int, [c_void_p, c_void_p]),
+        "s3e_vit_block_stage": (c_int, [c_void_p, c_int, c_int, c_void_p, P64, c_void_p, P64]),
+        "s3e_encode_vit_chw": (c_int, [c_void_p, c_void_p]),
+        "s3e_model_tensor_get": (c_int, [c_void_p, c_char_p, POINTER(c_int), P64, c_void_p, c_size_t]),
+        "s3e_vit_prefix_stage": (c_int, [c_void_p, c_int, c_void_p, P64, c_void_p, P64]),
         "s3e_hiera_block": (c_int, [c_void_p, c_int, c_void_p, c_int, c_int, c_void_p]),
         "s3e_mem_attn_dims": (c_int, [c_void_p, POINTER(c_int32)]),
         "s3e_mem_attn": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64,
@@ -128,7 +132,7 @@ DECLARED = [
     "s3e_weight_info", "s3e_mul_mat", "s3e_mul_mat_q", "s3e_mul_mat_q_batch", "s3e_quantize_rows", "s3e_layer_norm", "s3e_copy",
     "s3e_flash_attn_ext", "s3e_model_load",
     "s3e_model_free", "s3e_model_hparams", "s3e_state_create", "s3e_state_free", "s3e_encode_chw",
-    "s3e_encode_chw_host", "s3e_encode_image_u8", "s3e_preprocess_image", "s3e_vit_prefix", "s3e_vit_block", "s3e_run_neck", "s3e_hiera_block", "s3e_model_type", "s3e_mem_attn_dims", "s3e_mem_attn",
+    "s3e_encode_chw_host", "s3e_encode_image_u8", "s3e_preprocess_image", "s3e_vit_prefix", "s3e_vit_block", "s3e_vit_block_stage", "s3e_vit_prefix_stage", "s3e_encode_vit_chw", "s3e_model_tensor_get", "s3e_run_neck", "s3e_hiera_block", "s3e_model_type", "s3e_mem_attn_dims", "s3e_mem_attn",
     "s3e_state_tensor_info",
     "s3e_state_tensor_get", "s3e_state_tensor_device", "s3e_synth_write", "s3e_synth_write_sam2",
 ]
@@ -410,6 +414,26 @@ class State:
 
     def run_neck(self, x: DeviceBuffer):
         check(LIB.s3e_run_neck(self.handle, x.ptr), "s3e_run_neck")
+
+    def block_stage(self, idx: int, stage: int, x: np.ndarray, ne) -> tuple:
+        """Block sub-stage hook on host data x of ggml shape ne → (output, out_ne);
+        the input is uploaded and the output downloaded around the device call."""
+        return self._stage(lambda *a: LIB.s3e_vit_block_stage(self.handle, idx, stage, *a), x, ne,
+                           "s3e_vit_block_stage")
+
+    def prefix_stage(self, stage: int, x: np.ndarray, ne) -> tuple:
+        return self._stage(lambda *a: LIB.s3e_vit_prefix_stage(self.handle, stage, *a), x, ne,
+                           "s3e_vit_prefix_stage")
+
+    def _stage(self, fn, x, ne, what):
+        ine, one = (c_int64 * 4)(*ne), (c_int64 * 4)()
+        check(fn(None, ine, None, one), what)
+        n = one[0] * one[1] * one[2] * one[3]
+        xd = self.ctx.to_device(np.ascontiguousarray(x, dtype=np.float32))
+        yd = self.ctx.buffer(4 * n)
+        check(fn(xd.ptr, ine, yd.ptr, one), what)
+        self.ctx.sync()
+        return yd.download(np.float32, (n,)), tuple(int(v) for v in one)
 
     def mem_attn(self, curr, src_pos, N: int, prompt, prompt_pos, M_total: int, n_ptr: int, rope_q, rope_k, out):
         """Memory attention on device buffers (s3e_mem_attn)."""

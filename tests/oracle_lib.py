@@ -66,6 +66,8 @@ def _load():
         "orc_vit_prefix": (c_int, [P, P, P, c_int]),
         "orc_vit_block": (c_int, [P, c_int, P, c_int]),
         "orc_vit_encode": (c_int, [P, P, P, c_int]),
+        "orc_vit_block_stage": (c_int, [P, c_int, c_int, P, P, P, P, c_int]),
+        "orc_vit_prefix_stage": (c_int, [P, c_int, P, P, P, P, c_int]),
         "orc_conv_transpose_2x2": (None, [P, c_int64, c_int64, P, c_int64, c_int64, P, c_int]),
         "orc_conv2d": (None, [c_int, P, c_int64, c_int64, c_int64, c_int64, c_int64, P, c_int64, c_int64, P,
                               c_int]),
@@ -220,6 +222,28 @@ class OracleModel:
         assert LIB.orc_vit_encode(self.h, ptr(chw), ptr(x), nthreads) == 0, LIB.orc_last_error()
         return x
 
+    def block_stage(self, i: int, stage: int, x: np.ndarray, ne, nthreads: int = 0) -> tuple:
+        """sam3_test_run_vit_block_stage on x (ggml shape ne) → (output, out_ne)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        ine, one = np.array(ne, np.int64), np.zeros(4, np.int64)
+        assert LIB.orc_vit_block_stage(self.h, i, stage, ptr(x), ptr(ine), None, ptr(one), nthreads) == 0, \
+            LIB.orc_last_error()
+        out = np.empty(int(np.prod(one)), np.float32)
+        assert LIB.orc_vit_block_stage(self.h, i, stage, ptr(x), ptr(ine), ptr(out), ptr(one), nthreads) == 0, \
+            LIB.orc_last_error()
+        return out, tuple(int(v) for v in one)
+
+    def prefix_stage(self, stage: int, x: np.ndarray, ne, nthreads: int = 0) -> tuple:
+        """sam3_test_run_vit_prefix_stage on x (ggml shape ne) → (output, out_ne)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        ine, one = np.array(ne, np.int64), np.zeros(4, np.int64)
+        assert LIB.orc_vit_prefix_stage(self.h, stage, ptr(x), ptr(ine), None, ptr(one), nthreads) == 0, \
+            LIB.orc_last_error()
+        out = np.empty(int(np.prod(one)), np.float32)
+        assert LIB.orc_vit_prefix_stage(self.h, stage, ptr(x), ptr(ine), ptr(out), ptr(one), nthreads) == 0, \
+            LIB.orc_last_error()
+        return out, tuple(int(v) for v in one)
+
     def neck_dims(self, which: str = "trk"):
         side = np.zeros(4, np.int64)
         D = np.zeros(1, np.int64)
@@ -237,9 +261,16 @@ class OracleModel:
         return outs
 
     def __del__(self):
-        if getattr(self, "h", None):
+        if getattr(self, "h", None) and LIB is not None:
             LIB.orc_model_free(self.h)
             self.h = None
+
+
+# sam3.h:112-134
+BLOCK_STAGES = ["NORM1", "WINDOW_PART", "QKV_PROJ", "ATTN_CORE", "ATTN_PROJ", "WINDOW_UNPART", "NORM2",
+                "MLP_FC1", "MLP_GELU", "MLP_FC2", "MLP"]
+PREFIX_STAGES = ["PATCH_EMBED", "PATCH_IM2COL", "PATCH_MULMAT_RAW", "PATCH_MULMAT", "POS_ADD", "LN_PRE_NORM",
+                 "LN_PRE"]
 
 
 class HieraHp(ctypes.Structure):

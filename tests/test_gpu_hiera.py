@@ -16,7 +16,7 @@ Models are random-init files in sam3.cpp's SAM 2 format:
 Each block runs on the same input as the oracle's block (s3e_hiera_block),
 and the encoder runs end to end from the same image.  Tolerances follow the
 SAM 3 backbone tests: F16 files to the F16 specification (relative L2 ≤
-2e-3); F32 and quantized files within 3× the reference's own noise floor,
+2e-3); F32 and quantized files within 2× the reference's own noise floor,
 with the specification as the lower bound (F32: relative L2 ≤ 2e-4;
 quantized: relative L2 ≤ 1e-3 and max-abs ≤ 5e-3).
 
@@ -42,7 +42,8 @@ import oracle_lib as orc
 pytestmark = pytest.mark.gpu
 
 orc.LIB.orc_set_variant.argtypes = [ctypes.c_int]
-FLOOR_FACTOR = 3.0
+# measured: quantized outputs at 1.0-1.8x the noise floor where the floor exceeds the specification
+FLOOR_FACTOR = 2.0
 SMALL = dict(embed_dim=32, num_heads=1, stages=(1, 2, 3, 2), global_idx=(4,), window_spec=(8, 6, 4, 4), bkg=(5, 5))
 
 CASES = [
@@ -227,7 +228,8 @@ def test_encode_is_repeatable(hiera):
         assert np.array_equal(st.tensor(f"neck_trk_{i}"), a[i])
 
 
-@pytest.mark.parametrize("variant,ft", [("hiera_t", "q4_0"), ("hiera_b+", "q4_0"), ("hiera_t", "f16")])
+@pytest.mark.parametrize("variant,ft", [("hiera_t", "q4_0"), ("hiera_b+", "q4_0"), ("hiera_b+", "q8_0"),
+                                        ("hiera_t", "f16")])
 def test_encode_full_size(variant, ft, tmpdir_session, ctx):
     """The SAM 2.1 encoders at their real 1024 px size."""
     import s3e

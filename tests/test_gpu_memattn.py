@@ -11,7 +11,7 @@ without RoPE), axial RoPE tables for the queries and the spatial keys.
 The engine runs the attention on fp16 operands (head dim 256) with fp32
 accumulation and the GEMMs on the weight type as ggml does; tolerances:
 F32 and F16 files relative L2 ≤ 2e-3 (the F16 specification: fp16
-attention operands are the intended difference); quantized files within 3×
+attention operands are the intended difference); quantized files within 2×
 the reference's noise floor — ggml's two dot-product orders and the
 oracle's own response to a one- to two-ulp perturbation of its inputs, as
 in the encoder tests — with the 1e-3 / 5e-3 specification as the floor.
@@ -29,7 +29,8 @@ import oracle_lib as orc
 pytestmark = pytest.mark.gpu
 
 orc.LIB.orc_set_variant.argtypes = [ctypes.c_int]
-FLOOR = 3.0
+# measured: 1.1-1.8x (C5 size 1.78x in relative L2, max-abs at most 1.3x)
+FLOOR = 2.0
 
 
 def _inputs(D, MD, h, frames, n_ptr, seed):

@@ -222,7 +222,7 @@ def test_mul_mat_q_batch_rejects(ctx):
 
 
 @pytest.mark.parametrize("prec", [0, 1], ids=["fp16", "f32"])
-@pytest.mark.parametrize("B,nh,N", [(1, 2, 64), (2, 3, 100), (9, 16, 576), (1, 2, 5184)])
+@pytest.mark.parametrize("B,nh,N", [(1, 2, 64), (2, 3, 100), (9, 16, 576), (1, 2, 5184), (1, 16, 5184)])
 def test_flash_attn(ctx, B, nh, N, prec):
     rng = np.random.default_rng(B * 100 + nh * 10 + N)
     q = rng.standard_normal((B, nh, N, 64)).astype(np.float32)

@@ -15,7 +15,7 @@ up apart by about the quantization noise.  The reference is no exception:
 ggml's own AVX2 and generic-C dot-product orders (both restated in the
 oracle, orc_set_variant) disagree by more than the nominal 1e-3 / 5e-3 after
 a single block.  Quantized blocks therefore must meet relative L2 ≤ 1e-3,
-and quantized outputs must stay within 3× the distance between those two
+and quantized outputs must stay within 2× the distance between those two
 ggml evaluation orders, measured here on the same model and image.
 """
 import ctypes
@@ -30,7 +30,13 @@ pytestmark = pytest.mark.gpu
 
 FTYPES = ["q4_0", "q8_0", "q4_1", "f16"]
 orc.LIB.orc_set_variant.argtypes = [ctypes.c_int]
-FLOOR_FACTOR = 3.0
+# Measured: the engine's quantized outputs sit at 0.9-1.9x ggml's own
+# AVX2-vs-generic distance (1.0x for the 32-block encoder at 1008 px, where
+# both saturate at the quantization noise).  The two ggml orders share
+# ggml's f32 attention; the engine's split-fp16 attention is one more
+# independent source of last-bit differences (it flips 1e-5-3e-5 of the proj
+# input's Q8 codes per block), so small models sit above 1x.
+FLOOR_FACTOR = 2.0
 
 
 def _variant_gap(fn):

@@ -231,3 +231,111 @@ def test_planted_mistakes_are_detected(f32_model, mutation):
     got = om.block(0, x)
     bad = _tok(torch_block(tensors, 0, _grid(x), False, mutate=mutation))
     assert orc.rel_l2(got, bad) > 1e-5, (mutation, orc.rel_l2(got, bad))
+
+
+# ---- sub-stage hooks (sam3_test_run_vit_block_stage / _prefix_stage) ---------------
+BS = {n: i for i, n in enumerate(orc.BLOCK_STAGES)}
+PS = {n: i for i, n in enumerate(orc.PREFIX_STAGES)}
+
+
+def _stages_block(om, bi, x, glob):
+    """The block as the reference's stage sequence: each stage fed the previous
+    stage's output, residual adds in float32 as ggml_add does."""
+    nw = (G // WS) ** 2
+    h, ne = om.block_stage(bi, BS["NORM1"], x, (E, G, G, 1))
+    if not glob:
+        h, ne = om.block_stage(bi, BS["WINDOW_PART"], h, ne)
+        assert ne == (E, WS, WS, nw)
+    h, ne = om.block_stage(bi, BS["QKV_PROJ"], h, ne)
+    assert ne[0] == 3 * E
+    h, ne = om.block_stage(bi, BS["ATTN_CORE"], h, ne)
+    assert ne[0] == E
+    h, ne = om.block_stage(bi, BS["ATTN_PROJ"], h, ne)
+    if not glob:
+        h, ne = om.block_stage(bi, BS["WINDOW_UNPART"], h, ne)
+    assert ne == (E, G, G, 1)
+    x1 = (x.ravel() + h).astype(np.float32)
+    h, _ = om.block_stage(bi, BS["NORM2"], x1, ne)
+    y, _ = om.block_stage(bi, BS["MLP"], h, ne)
+    return (x1 + y).astype(np.float32)
+
+
+@pytest.mark.parametrize("bi,glob", [(0, False), (1, True)])
+def test_block_stages_compose_to_block(f32_model, f16_model, bi, glob):
+    """Chaining the stage hooks reproduces the block bit for bit, and MLP is
+    MLP_FC1 → MLP_GELU → MLP_FC2."""
+    for path, _ in (f32_model, f16_model):
+        om = orc.OracleModel(path)
+        x = np.random.default_rng(30 + bi).standard_normal((G * G, E)).astype(np.float32)
+        assert np.array_equal(_stages_block(om, bi, x, glob), om.block(bi, x).ravel())
+        h, ne = om.block_stage(bi, BS["NORM2"], x, (E, G, G, 1))
+        a, ne1 = om.block_stage(bi, BS["MLP_FC1"], h, ne)
+        a, _ = om.block_stage(bi, BS["MLP_GELU"], a, ne1)
+        a, ne2 = om.block_stage(bi, BS["MLP_FC2"], a, ne1)
+        assert ne2 == ne and np.array_equal(a, om.block_stage(bi, BS["MLP"], h, ne)[0])
+
+
+def test_stages_vs_torch(f32_model):
+    """Each stage against its torch restatement: the window operators against
+    window_partition / window_unpartition, the attention core against RoPE +
+    softmax attention, GELU against erf-GELU."""
+    path, tensors = f32_model
+    om = orc.OracleModel(path)
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((G * G, E)).astype(np.float32)
+    w, ne = om.block_stage(0, BS["WINDOW_PART"], x, (E, G, G, 1))
+    ref = window_partition(_grid(x), WS).numpy()
+    assert np.array_equal(w, ref.ravel().astype(np.float32))
+    back, ne2 = om.block_stage(0, BS["WINDOW_UNPART"], w, ne)
+    assert ne2 == (E, G, G, 1) and np.array_equal(back, x.ravel())
+    nw = (G // WS) ** 2
+    qkv = rng.standard_normal((nw, WS * WS, 3 * E)).astype(np.float32)
+    got, one = om.block_stage(0, BS["ATTN_CORE"], qkv, (3 * E, WS, WS, nw))
+    assert one == (E, WS, WS, nw)
+    t = torch.from_numpy(qkv.astype(np.float64)).reshape(nw, WS * WS, 3, NH, HD)
+    q, k, v = t.permute(2, 0, 3, 1, 4).unbind(0)
+    fc = _t(tensors, "vit.blocks.0.attn.freqs_cis")
+    freqs = torch.complex(fc[..., 0], fc[..., 1])
+    q, k = apply_rotary(q, freqs), apply_rotary(k, freqs)
+    o = torch.matmul(torch.softmax(torch.matmul(q, k.transpose(-1, -2)) / math.sqrt(HD), dim=-1), v)
+    ref = o.permute(0, 2, 1, 3).reshape(-1).numpy()  # [B][N][NH][HD]
+    assert orc.rel_l2(got, ref) < 1e-6
+    a = rng.standard_normal((16, 592)).astype(np.float32) * 3
+    g, _ = om.block_stage(0, BS["MLP_GELU"], a, (592, 16, 1, 1))
+    ref = torch.nn.functional.gelu(torch.from_numpy(a.astype(np.float64))).numpy()
+    assert np.max(np.abs(g - ref.ravel())) < 1e-6
+
+
+def test_prefix_stages_compose(f32_model, f16_model):
+    for path, tensors in (f32_model, f16_model):
+        om = orc.OracleModel(path)
+        chw = _image(13)
+        p, ne = om.prefix_stage(PS["PATCH_EMBED"], chw, (IMG, IMG, 3, 1))
+        assert ne == (E, G, G, 1)
+        p, ne = om.prefix_stage(PS["POS_ADD"], p, ne)
+        p, ne = om.prefix_stage(PS["LN_PRE"], p, ne)
+        assert np.array_equal(p, om.prefix(chw).ravel())
+        # ln_pre = ggml_norm, then ·w + b
+        n, _ = om.prefix_stage(PS["LN_PRE_NORM"], p, ne)
+        ref = F.layer_norm(torch.from_numpy(p.astype(np.float64)).reshape(-1, E), [E], eps=1e-5).numpy()
+        assert orc.rel_l2(n, ref.ravel()) < 1e-6
+        # im2col rows are the image patches in (c, ky, kx) order, in the kernel's type
+        cols, cne = om.prefix_stage(PS["PATCH_IM2COL"], chw, (IMG, IMG, 3, 1))
+        assert cne == (3 * P * P, G, G, 1)
+        ref = chw.reshape(3, G, P, G, P).transpose(1, 3, 0, 2, 4).reshape(G * G, 3 * P * P)
+        f16 = tensors["vit.patch_embed.proj.weight"][0] == orc.F16 or path.endswith("f16.ggml")
+        if f16:
+            ref = ref.astype(np.float16).astype(np.float32)
+        assert np.array_equal(cols, ref.ravel())
+        # the mul_mat stages take an F16 input and convert the kernel to F16
+        raw, rne = om.prefix_stage(PS["PATCH_MULMAT_RAW"], cols, cne)
+        assert rne == (G * G, E, 1, 1)
+        mm, mne = om.prefix_stage(PS["PATCH_MULMAT"], cols, cne)
+        assert mne == (G, G, E, 1) and np.array_equal(mm, raw)
+        w16 = np.asarray(tensors["vit.patch_embed.proj.weight"][2], np.float32).reshape(E, -1)
+        w16 = w16.astype(np.float16).astype(np.float64)
+        a16 = cols.reshape(G * G, -1).astype(np.float16).astype(np.float64)
+        assert orc.rel_l2(raw, (w16 @ a16.T).ravel()) < 1e-6
+        if f16:  # the same products as the conv itself: equal up to the transpose
+            conv, _ = om.prefix_stage(PS["PATCH_EMBED"], chw, (IMG, IMG, 3, 1))
+            assert np.array_equal(raw.reshape(E, G * G).T.ravel(), conv)

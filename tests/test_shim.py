@@ -34,7 +34,7 @@ def declared():
 def test_header_functions_are_exported():
     out = subprocess.run(["nm", "-DC", "--defined-only", LIB], capture_output=True, text=True, check=True).stdout
     names = declared()
-    assert len(names) == 10, names
+    assert len(names) == 16, names
     for n in names:
         assert re.search(rf"\b{n}\(", out), n
     # the C++ signatures of sam3.h (demangled)
@@ -42,6 +42,10 @@ def test_header_functions_are_exported():
     assert "sam3_encode_image(sam3_state&, sam3_model const&, sam3_image const&)" in out
     assert "sam3_dump_state_tensor(sam3_state const&, std::__cxx11::basic_string" in out
     assert "sam3_state_deleter::operator()(sam3_state*) const" in out
+    assert ("sam3_test_run_vit_block_stage(sam3_model const&, int, sam3_vit_block_stage, float const*, "
+            "long const*, std::vector<float, std::allocator<float> >&, long*, int)") in out
+    assert ("sam3_test_run_vit_prefix_stage(sam3_model const&, sam3_vit_prefix_stage, float const*, "
+            "long const*, std::vector<float, std::allocator<float> >&, long*, int)") in out
 
 
 def test_example_fails_like_sam3_load_model(tmp_path):
@@ -115,7 +119,7 @@ def test_example_encode_matches_oracle(tmp_path, s3e_lib):
         gma = orc.max_abs(refs[1][k], refs[0][k])
         rl, ma = orc.rel_l2(got, ref), orc.max_abs(got, ref)
         print(f"{name}: rel_l2={rl:.3e} max_abs={ma:.3e} (ggml order gap {gap:.2e}/{gma:.2e})", flush=True)
-        assert rl <= max(1e-3, 3.0 * gap) and ma <= max(5e-3, 3.0 * gma), name
+        assert rl <= max(1e-3, 2.0 * gap) and ma <= max(5e-3, 2.0 * gma), name
 
     # preprocessed input of the same image: identical dumps
     chw.astype(np.float32).tofile(str(tmp_path / "img.chw.f32"))
@@ -170,4 +174,80 @@ def test_example_encode_sam2_matches_oracle(tmp_path, s3e_lib):
         gma = orc.max_abs(refs[1][k], refs[0][k])
         rl, ma = orc.rel_l2(got, ref), orc.max_abs(got, ref)
         print(f"{name}: rel_l2={rl:.3e} max_abs={ma:.3e} (ggml order gap {gap:.2e}/{gma:.2e})", flush=True)
-        assert rl <= max(1e-3, 3.0 * gap) and ma <= max(5e-3, 3.0 * gma), name
+        assert rl <= max(1e-3, 2.0 * gap) and ma <= max(5e-3, 2.0 * gma), name
+
+
+@pytest.mark.gpu
+def test_example_stage_hooks_match_oracle(tmp_path, s3e_lib):
+    """The test-only entry points of sam3.h through the shim: the prefix, the
+    prefix and block sub-stages (each fed the previous stage's output), the
+    host references of the F16 linears and the backbone-only encode, each
+    compared with the oracle on the same input."""
+    path = str(tmp_path / "f.ggml")
+    s3e_lib.synth_write(path, img_size=336, patch=14, embed_dim=1024, depth=2, heads=16, window=8,
+                        global_idx=(1,), ftype="f16", seed=31, std=0.02, random_affine=True, neck=1)
+    chw = orc.preprocess_sam3(np.random.default_rng(12).integers(0, 256, (336, 336, 3), dtype=np.uint8), 336)
+    chw.astype(np.float32).tofile(str(tmp_path / "img.chw.f32"))
+    om = orc.OracleModel(path)
+    for bi in (0, 1):
+        out = str(tmp_path / f"s{bi}_")
+        print(f"sam3_encode stage hooks, block {bi}", flush=True)
+        r = subprocess.run([EXE, "-m", path, "-p", str(tmp_path / "img.chw.f32"), "-s", "336", "-o", out,
+                            "-B" if bi == 1 else "-b", str(bi)], capture_output=True, text=True, timeout=120)
+        print(r.stdout, r.stderr[-2000:], flush=True)
+        assert r.returncode == 0
+
+        def dump(name):
+            shape, data = _read_dump(out + name)
+            return data, tuple(shape)
+
+        x0, ne0 = dump("block0_input")
+        assert ne0 == (1024, 24, 24, 1) and orc.rel_l2(x0, om.prefix(chw).ravel()) <= 1e-5
+        img_ne = (336, 336, 3, 1)
+        got, ne = dump("stage_PATCH_EMBED")
+        ref, one = om.prefix_stage(0, chw, img_ne)
+        assert ne == one and orc.rel_l2(got, ref) <= 1e-6
+        cols, cne = dump("stage_PATCH_IM2COL")
+        assert np.array_equal(cols, om.prefix_stage(1, chw, img_ne)[0])
+        got, ne = dump("stage_PATCH_MULMAT")
+        ref, one = om.prefix_stage(3, cols, cne)
+        assert ne == one and orc.rel_l2(got, ref) <= 1e-6
+        # block stages, each on the shim's own previous output
+        names = orc.BLOCK_STAGES
+        chain = ["NORM1", "WINDOW_PART", "QKV_PROJ", "ATTN_CORE", "ATTN_PROJ", "WINDOW_UNPART"]
+        if bi == 1:  # global block: no window stages
+            chain = [c for c in chain if not c.startswith("WINDOW")]
+        x, xne = x0, ne0
+        ins = {}
+        for nm in chain:
+            got, ne = dump("stage_" + nm)
+            ref, one = om.block_stage(bi, names.index(nm), x, xne)
+            ins[nm] = (x, xne)
+            assert ne == one, nm
+            rl = orc.rel_l2(got, ref)
+            print(f"shim block {bi} {nm}: rel_l2={rl:.3e}", flush=True)
+            assert rl <= (2e-3 if nm == "ATTN_CORE" else 1e-6), nm
+            x, xne = got, ne
+        x1 = (x0 + x).astype(np.float32)
+        n2, _ = dump("stage_NORM2")
+        assert np.array_equal(n2, om.block_stage(bi, names.index("NORM2"), x1, ne0)[0])
+        x, xne = n2, ne0
+        for nm in ("MLP_FC1", "MLP_GELU", "MLP_FC2"):
+            got, ne = dump("stage_" + nm)
+            ref, one = om.block_stage(bi, names.index(nm), x, xne)
+            ins[nm] = (x, xne)
+            assert ne == one and orc.rel_l2(got, ref) <= 1e-6, nm
+            x, xne = got, ne
+        # fc1 → GELU → fp16 rounding of fc2's input: last-bit differences of
+        # fc1 flip a few fp16 roundings (ggml's own two evaluation orders are
+        # 7.7e-6 apart on such a stage)
+        got, _ = dump("stage_MLP")
+        assert orc.rel_l2(got, om.block_stage(bi, names.index("MLP"), n2, ne0)[0]) <= 5e-5
+        # host references (fp16 operands, one sequential f32 sum per output:
+        # its rounding grows with K, 1.2e-6 at K = 4736) = the same linears
+        for nm in ("QKV_PROJ", "ATTN_PROJ", "MLP_FC1", "MLP_FC2"):
+            got, ne = dump("host_" + nm)
+            ref, one = om.block_stage(bi, names.index(nm), *ins[nm])
+            assert ne == one and orc.rel_l2(got, ref) <= 1e-5, nm
+        got, ne = dump("vit_output")
+        assert orc.rel_l2(got, om.encode(chw).ravel()) <= 2e-3
