@@ -103,6 +103,21 @@ int s3e_weight_info(const s3e_weight *w, int64_t out[4]);
 int s3e_mul_mat(s3e_ctx *ctx, const s3e_weight *w, const float *X, int64_t M,
                 const float *bias, float *Y);
 
+/* No counterpart in the reference: s3e_mul_mat for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops that
+ * forbid hipMalloc).  Same arguments and results; X is converted into a
+ * file-scope device array of S3E_NOALLOC_SCRATCH_BYTES per GPU (64 MiB:
+ * every C4 linear at 5184 rows fits, in every weight type) instead of a
+ * per-call allocation, and every product runs on the large-M kernel (at 64
+ * rows or fewer s3e_mul_mat streams the weight on another kernel: equal up
+ * to fp32 summation order).  Calls no hipMalloc / hipFree and does not
+ * synchronise.  A product whose conversion exceeds the array returns
+ * S3E_ERR_INVALID.  All calls on one GPU share its array and leave their
+ * contents in it: calls that overlap on one GPU race. */
+#define S3E_NOALLOC_SCRATCH_BYTES (64ull << 20)
+int s3e_mul_mat_noalloc(s3e_ctx *ctx, const s3e_weight *w, const float *X, int64_t M, const float *bias,
+                        float *Y);
+
 /* Same GEMM with X already in W's vec_dot type (ggml_mul_mat with src1 of
  * that type; ggml skips the conversion then): `xq`, `d`, `s` as written by
  * s3e_quantize_rows for K = W's ne0 (layout there).  Launches the GEMM kernel

@@ -6,12 +6,38 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <mutex>
 #include <vector>
 
 #include "s3e_host.h"
 #include "s3e_internal.h"
 
+// A context: one device and one stream of work (s3e.h).
+struct s3e_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    // descriptors of the last batched small-M launch (device copy + host copy,
+    // reused while a caller repeats the same batch)
+    void *sm_dev = nullptr;
+    size_t sm_cap = 0;
+    std::vector<uint8_t> sm_last;
+    // this device's copy of the allocation-free entry points' scratch array
+    void *scratch = nullptr;
+};
+
+struct s3e_weight {
+    s3e_ctx *ctx = nullptr;
+    s3e::Weight w;
+    // the small-M kernel's block-interleaved copy, made at first use
+    mutable std::mutex mu;
+    mutable void *sm = nullptr;
+};
+
 namespace s3e {
+
+// Address of the allocation-free entry points' scratch array on `device`
+// (which must be current), looked up once per device (s3e_noalloc.cpp).
+int noalloc_init(int device, void **scratch);
 
 int64_t round_up(int64_t x, int64_t m);
 WKind wkind_of(int type);

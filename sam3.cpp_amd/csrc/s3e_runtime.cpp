@@ -49,24 +49,6 @@ using namespace s3e;
         }                                                                               \
     } while (0)
 
-struct s3e_ctx {
-    int device = 0;
-    hipStream_t stream = nullptr;
-    // descriptors of the last batched small-M launch (device copy + host copy,
-    // reused while a caller repeats the same batch)
-    void *sm_dev = nullptr;
-    size_t sm_cap = 0;
-    std::vector<uint8_t> sm_last;
-};
-
-struct s3e_weight {
-    s3e_ctx *ctx = nullptr;
-    Weight w;
-    // the small-M kernel's block-interleaved copy, made at first use
-    mutable std::mutex mu;
-    mutable void *sm = nullptr;
-};
-
 // ---- host helpers shared with s3e_hiera.cpp (declared in s3e_rt.h) ----
 namespace s3e {
 
@@ -285,8 +267,13 @@ extern "C" int s3e_ctx_create(int device, s3e_ctx **out) {
         return S3E_ERR_INVALID;
     }
     HIP_TRY(hipSetDevice(device));
+    // the allocation-free entry points' scratch address on this device
+    void *scratch = nullptr;
+    const int rc = noalloc_init(device, &scratch);
+    if (rc != S3E_OK) return rc;
     auto *c = new s3e_ctx;
     c->device = device;
+    c->scratch = scratch;
     hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
         delete c;

@@ -83,6 +83,7 @@ def _load() -> ctypes.CDLL:
         "s3e_weight_free": (None, [c_void_p]),
         "s3e_weight_info": (c_int, [c_void_p, P64]),
         "s3e_mul_mat": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
+        "s3e_mul_mat_noalloc": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
         "s3e_quantize_rows": (c_int, [c_void_p, c_int, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
         "s3e_layer_norm": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_float, c_void_p, c_void_p, c_void_p]),
         "s3e_mul_mat_q": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
@@ -129,7 +130,7 @@ LIB = _load()
 DECLARED = [
     "s3e_last_error", "s3e_abi_version", "s3e_ctx_create", "s3e_ctx_destroy", "s3e_ctx_sync", "s3e_ctx_stream",
     "s3e_malloc", "s3e_free", "s3e_memcpy_h2d", "s3e_memcpy_d2h", "s3e_weight_upload", "s3e_weight_free",
-    "s3e_weight_info", "s3e_mul_mat", "s3e_mul_mat_q", "s3e_mul_mat_q_batch", "s3e_quantize_rows", "s3e_layer_norm", "s3e_copy",
+    "s3e_weight_info", "s3e_mul_mat", "s3e_mul_mat_noalloc", "s3e_mul_mat_q", "s3e_mul_mat_q_batch", "s3e_quantize_rows", "s3e_layer_norm", "s3e_copy",
     "s3e_flash_attn_ext", "s3e_model_load",
     "s3e_model_free", "s3e_model_hparams", "s3e_state_create", "s3e_state_free", "s3e_encode_chw",
     "s3e_encode_chw_host", "s3e_encode_image_u8", "s3e_preprocess_image", "s3e_vit_prefix", "s3e_vit_block", "s3e_vit_block_stage", "s3e_vit_prefix_stage", "s3e_encode_vit_chw", "s3e_model_tensor_get", "s3e_run_neck", "s3e_hiera_block", "s3e_model_type", "s3e_mem_attn_dims", "s3e_mem_attn",
@@ -310,6 +311,10 @@ class Context:
 
     def weight(self, ggml_type: int, K: int, N: int, data: np.ndarray) -> Weight:
         return Weight(self, ggml_type, K, N, data)
+
+    def mul_mat_noalloc(self, w: Weight, X: DeviceBuffer, M: int, Y: DeviceBuffer, bias: DeviceBuffer | None = None):
+        check(LIB.s3e_mul_mat_noalloc(self.handle, w.handle, X.ptr, M, bias.ptr if bias else None, Y.ptr),
+              "s3e_mul_mat_noalloc")
 
     def mul_mat(self, w: Weight, X: DeviceBuffer, M: int, Y: DeviceBuffer, bias: DeviceBuffer | None = None):
         check(LIB.s3e_mul_mat(self.handle, w.handle, X.ptr, M, bias.ptr if bias else None, Y.ptr), "s3e_mul_mat")
