@@ -103,11 +103,6 @@ __device__ __forceinline__ float sub_hi_half(float p, uint32_t h2) {
     return r;
 }
 
-template <int N>
-__device__ __forceinline__ void wait_and_barrier() {
-    __asm__ volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
-}
-
 // CROP: the windowed, cropped output mapping and narrower real heads
 // (a.wo, a.hd_out; the Hiera layouts), kept out of the plain variants.
 template <bool SPLIT, int HD, bool CROP>
@@ -396,7 +391,48 @@ __global__ __launch_bounds__(NTHR, HD == 64 ? 3 : (HD == 128 ? 2 : 1)) void k_at
 #pragma unroll
     for (int dt = 0; dt < G::DT; dt++) {
         if (CROP && dt * 32 >= hdo) break;
-        if (out.kind == A_Q8_0 || out.kind == A_Q8_1) {
+        if (out.kind == A_F6) {
+            // the same Q8_0 codes in the A_F6 layout: this lane holds block
+            // positions 8g + 4·lh + i; each lane builds its fields of both
+            // parts, sends the partner the part it stores (h: lh = 0, l: lh = 1)
+            float amax = 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; r++) amax = fmaxf(amax, fabsf(o[dt][r]));
+            amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+            const float d = amax / 127.f;
+            const float id = (amax != 0.f) ? 127.f / amax : 0.f;
+            uint32_t bh[6] = {0, 0, 0, 0, 0, 0}, bl[6] = {0, 0, 0, 0, 0, 0};
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int q = (int)__builtin_rintf(o[dt][4 * g + i] * id);
+                    const int hq = f6_hi(q);
+                    const uint32_t ch = f6_code(hq), cl = f6_code(q - 16 * hq);
+                    const int at = 6 * (8 * g + 4 * lh + i);
+                    bh[at / 32] |= ch << (at % 32);
+                    bl[at / 32] |= cl << (at % 32);
+                    if (at % 32 > 26) {
+                        bh[at / 32 + 1] |= ch >> (32 - at % 32);
+                        bl[at / 32 + 1] |= cl >> (32 - at % 32);
+                    }
+                }
+            uint32_t mine[6];
+#pragma unroll
+            for (int j = 0; j < 6; j++) {
+                const uint32_t other = __shfl_xor(lh ? bh[j] : bl[j], 32, 64);
+                mine[j] = (lh ? bl[j] : bh[j]) | other;
+            }
+            if (ovalid) {
+                const int64_t blk = (colbase + dt * 32) / QK;
+                uint64_t *base = (uint64_t *)out.x;
+#pragma unroll
+                for (int tw = 0; tw < 3; tw++)
+                    base[f6_act_word(out.ld / 128, orow, blk, lh, tw)] =
+                        (uint64_t)mine[2 * tw] | ((uint64_t)mine[2 * tw + 1] << 32);
+                if (lh == 0) out.d[scale_index(out.mp, orow, blk)] = f2h_bits(d);
+            }
+        } else if (out.kind == A_Q8_0 || out.kind == A_Q8_1) {
             // ggml quantize_row_q8_0/q8_1 of the 32 values d = dt*32 .. dt*32+31,
             // split 16/16 between lanes l and l^32
             float amax = 0.f;
@@ -508,6 +544,8 @@ hipError_t launch_attn(const AttnArgs &a, hipStream_t st) {
     // head dim 256: fp16 operands only
     if (hd == 256 && (a.q_lo || a.wo > 0 || (a.hd_out > 0 && a.hd_out != hd))) return hipErrorInvalidValue;
     // a Q8 output block must lie inside one head
+    if (a.out.kind == A_F6 && (a.out.ld % 128 != 0 || (a.hd_out > 0 && a.hd_out % 32 != 0)))
+        return hipErrorInvalidValue;
     if ((a.out.kind == A_Q8_0 || a.out.kind == A_Q8_1) && a.hd_out > 0 && a.hd_out % 32 != 0)
         return hipErrorInvalidValue;
     const dim3 grid((unsigned)((a.Nq + QT - 1) / QT), (unsigned)a.BH, (unsigned)a.nsplit);

@@ -40,6 +40,8 @@ namespace s3e {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef uint64_t v4u64 __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
@@ -138,6 +140,38 @@ __device__ __forceinline__ void quant_block32(const float *v, int8_t *qdst, uint
     *ddst = f2h_bits(d);
     // s = fp16(fp32(d·Σq)): f2h_bits keeps the fp32 rounding of the product
     if (sdst) *sdst = f2h_bits(d * (float)sum);
+}
+
+// The same quantization into the A_F6 layout (row `row`, block `blk` of an
+// activation with nst stages of 128): the codes split q = 16·h + l, each part
+// as three 8-byte words of fp6 E3M2 codes.
+__device__ __forceinline__ void quant_block32_f6(const float *v, uint64_t *base, int64_t nst, int64_t row,
+                                                 int64_t blk, uint16_t *ddst) {
+    float amax = 0.f;
+#pragma unroll
+    for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(v[j]));
+    const float d = amax / 127.f;
+    const float id = (amax != 0.f) ? 127.f / amax : 0.f;
+    uint64_t wh[3] = {0, 0, 0}, wl[3] = {0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+        const int q = (int)(__builtin_bit_cast(uint32_t, __fadd_rn(__fmul_rn(v[j], id), 12582912.0f)) - 0x4B400000u);
+        const int h = f6_hi(q);
+        const uint64_t ch = f6_code(h), cl = f6_code(q - 16 * h);
+        const int at = 6 * j;
+        wh[at / 64] |= ch << (at % 64);
+        wl[at / 64] |= cl << (at % 64);
+        if (at % 64 > 58) {
+            wh[at / 64 + 1] |= ch >> (64 - at % 64);
+            wl[at / 64 + 1] |= cl >> (64 - at % 64);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < 3; t++) {
+        base[f6_act_word(nst, row, blk, 0, t)] = wh[t];
+        base[f6_act_word(nst, row, blk, 1, t)] = wl[t];
+    }
+    *ddst = f2h_bits(d);
 }
 
 // XOR swizzle of the 16-byte chunks of LDS row r: chunk c lives at slot
@@ -422,6 +456,8 @@ __device__ __forceinline__ void epilogue(const GemmParams &p, const float *Ct, i
                 float4 *dst = (float4 *)((float *)o.x + (int64_t)gm * o.ld + gn0);
 #pragma unroll
                 for (int j = 0; j < 8; j++) dst[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+            } else if (o.kind == A_F6) {
+                quant_block32_f6(v, (uint64_t *)o.x, o.ld / 128, gm, gn0 / QK, o.d + scale_index(o.mp, gm, gn0 / QK));
             } else {
                 const int64_t blk = scale_index(o.mp, gm, gn0 / QK);
                 quant_block32(v, (int8_t *)o.x + (int64_t)gm * o.ld + gn0, o.d + blk,
@@ -681,11 +717,11 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 3 : 256 / BM) void k_gemm(
                 // the scale products (both lane halves carry the values)
 #pragma unroll
                 for (int n = 0; n < NT; n++) {
-                    const uint2 mb = *(const uint2 *)(L + C::OFF_BMIN + bd_off[n]);
+                    const uint2 mb = lds_u2(L + C::OFF_BMIN + bd_off[n]);
                     const v4u hb = {mb.x, mb.y, 0u, 0u};
 #pragma unroll
                     for (int i = 0; i < MT; i++) {
-                        const uint2 sa = *(const uint2 *)(L + C::OFF_AS + ad_off[i]);
+                        const uint2 sa = lds_u2(L + C::OFF_AS + ad_off[i]);
                         const v4u ha = {sa.x, sa.y, 0u, 0u};
                         accm[i][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
                             __builtin_bit_cast(v8h, ha), __builtin_bit_cast(v8h, hb), accm[i][n], 0, 0, 0);
@@ -775,6 +811,200 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 3 : 256 / BM) void k_gemm(
         }
     }
     epilogue<EPI, BM, C::NTH>(p, Ct, m0, n0, t);
+}
+
+// ---- Q4_0 weights × A_F6 activations --------------------------------------
+// The same tile, epilogues and scale products as k_gemm, with the integer
+// block sums formed on the fp6 MFMA instead of the int8 one:
+// v_mfma_scale_f32_32x32x64_f8f6f4 with E3M2 operands takes K = 64 as two
+// halves of 32 (lanes 0-31 and 32-63), each with its own power-of-two scale.
+// The activation half carries h (scale 16) and l (scale 1) of q = 16·h + l,
+// the weight half carries the Q4_0 code twice, so one instruction returns
+//     16·Σ h·qw + Σ l·qw = Σ_{k∈b} qx·qw = S_b
+// exactly (integers below 2^24) and already in fp32: the per-block rescale is
+// one FMA per element instead of a convert and an FMA, and the fp6 MFMA
+// issues at about the int8 one's rate (gfx950 runs fp6 at twice the fp8 /
+// int8 rate, so K = 64 of fp6 costs what K = 32 of int8 does).
+// Operands stream as they lie in memory: a tile row's stage of A_F6 (12 KB)
+// and a tile column's stage of the fp6 weight copy (12 KB) are contiguous,
+// laid out so that the 32 rows (columns) of one operand read are 256
+// contiguous bytes of LDS.
+template <int EPI>
+__global__ __launch_bounds__(256, 3) void k_gemm_f6(GemmParams p) {
+    constexpr int BM = 64, NTH = 256, WN = 2, NT = 2;
+    constexpr int OFF_A = 0, OFF_B = 12288, OFF_AD = 24576, OFF_BD = OFF_AD + BM * 8;
+    constexpr int STAGE = OFF_BD + BN * 8;  // 26112
+    constexpr int LDSZ = 2 * STAGE > BM * CLD * 4 ? 2 * STAGE : BM * CLD * 4;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[LDSZ];
+
+    const int per = gridDim.x >> 3;
+    const int logical0 = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    if (logical0 >= p.ntiles * p.ksplit) return;
+    const int kpart = logical0 % p.ksplit, logical = logical0 / p.ksplit;
+    constexpr int GROUP = 8;
+    const int group = logical / (GROUP * p.tiles_n);
+    const int first_m = group * GROUP;
+    const int gsz = min(p.tiles_m - first_m, GROUP);
+    const int rem = logical - group * GROUP * p.tiles_n;
+    const int tm = first_m + rem % gsz, tn = rem / gsz;
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    const int t = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int lane = t & 63;
+    const int wm = wave / WN, wn = wave % WN;
+    const int lr = lane & 31, lh = lane >> 5;
+
+    // DMA: wave w copies 1 KB runs 3w .. 3w+2 of the stage's A and of its B,
+    // and 256-byte scale runs w and w + 4 (A: runs 0-1, B: runs 2-5)
+    const int a_tile = tm * p.nstages * 12288, b_tile = tn * p.nstages * 12288;
+    int s_n = 0;
+    const uint8_t *s_src[2];
+    int64_t s_step[2];
+    int s_dst[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int k = wave + 4 * j;
+        if (k >= 6) break;
+        s_n++;
+        if (k < 2) {
+            s_src[j] = p.a_d + ((int64_t)m0 * 4) * 2 + k * 256 + lane * 4;
+            s_step[j] = p.a_mp * 8;
+            s_dst[j] = OFF_AD + k * 256;
+        } else {
+            s_src[j] = p.b_d + ((int64_t)n0 * 4) * 2 + (k - 2) * 256 + lane * 4;
+            s_step[j] = p.b_np * 8;
+            s_dst[j] = OFF_BD + (k - 2) * 256;
+        }
+    }
+    auto issue = [&](int s, int buf) {
+        uint8_t *L = lds + buf * STAGE;
+#pragma unroll
+        for (int j = 0; j < 3; j++) {
+            const int run = 3 * wave + j;
+            dma16_buf(p.a, p.a_rec, L + OFF_A + run * 1024, a_tile + run * 1024 + lane * 16, s * 12288);
+            dma16_buf(p.b, p.b_rec, L + OFF_B + run * 1024, b_tile + run * 1024 + lane * 16, s * 12288);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            if (j < s_n)
+                __builtin_amdgcn_global_load_lds((const void *)(s_src[j] + s * s_step[j]), LDS_PTR(L + s_dst[j]), 4,
+                                                 0, 0);
+    };
+
+    // per-lane LDS operand offsets: A row wm·32 + lr, part lh; B column
+    // wn·64 + 32n + lr (both lane halves read the same B words)
+    const int a_row = wm * 32 + lr;
+    const int a_off = OFF_A + lh * 3 * 512 + a_row * 8;
+    const int ad_off = OFF_AD + a_row * 8;
+    int b_off[NT], bd_off[NT];
+#pragma unroll
+    for (int n = 0; n < NT; n++) {
+        const int col = wn * 64 + 32 * n + lr;
+        b_off[n] = OFF_B + col * 8;
+        bd_off[n] = OFF_BD + col * 8;
+    }
+    const int a_scale = lh ? 127 : 131;  // E8M0: 2^0 for l, 2^4 for h
+
+    v16f acc[NT];
+#pragma unroll
+    for (int n = 0; n < NT; n++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[n][r] = 0.f;
+
+    // scale products: the A operand carries the stage's four row scales in
+    // K slots 0-3 (one 8-byte read per stage), the B operand of block b only
+    // its column scale in slot b, so the product is dx[b]·dw[b]; the unused
+    // slots stay zero in registers kept across blocks (slots 0-1 and 2-3 are
+    // separate operands)
+    v4u ha = {0u, 0u, 0u, 0u};
+    v4u hb01[NT], hb23[NT];
+#pragma unroll
+    for (int n = 0; n < NT; n++) {
+        hb01[n] = v4u{0u, 0u, 0u, 0u};
+        hb23[n] = v4u{0u, 0u, 0u, 0u};
+    }
+    struct Ops {
+        v8i a, b[NT];
+    };
+    auto load_ops = [&](const uint8_t *L, int blk, Ops &o) {
+        {
+            const uint64_t *q = (const uint64_t *)(L + a_off + blk * 6 * 512);
+            const v4u64 w = {q[0], q[64], q[128], 0ull};
+            o.a = __builtin_bit_cast(v8i, w);
+        }
+#pragma unroll
+        for (int n = 0; n < NT; n++) {
+            __asm__ volatile("" ::: "memory");
+            const uint64_t *q = (const uint64_t *)(L + b_off[n] + blk * 3 * 1024);
+            const v4u64 w = {q[0], q[128], q[256], 0ull};
+            o.b[n] = __builtin_bit_cast(v8i, w);
+        }
+    };
+    auto compute = [&](int buf) {
+        const uint8_t *L = lds + buf * STAGE;
+        {
+            const uint2 sa = lds_u2(L + ad_off);
+            ha[0] = sa.x;
+            ha[1] = sa.y;
+        }
+        uint2 sb[NT];
+#pragma unroll
+        for (int n = 0; n < NT; n++) sb[n] = lds_u2(L + bd_off[n]);
+#pragma unroll
+        for (int blk = 0; blk < 4; blk++) {
+            Ops cur;
+            load_ops(L, blk, cur);
+            const v16f zf = {};
+            v16f S[NT], Cs[NT];
+#pragma unroll
+            for (int n = 0; n < NT; n++) {
+                const uint32_t w = blk < 2 ? sb[n].x : sb[n].y;
+                const uint32_t m = (blk & 1) ? (w & 0xFFFF0000u) : (w & 0xFFFFu);
+                if (blk < 2) hb01[n][0] = m;
+                else hb23[n][1] = m;
+                S[n] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(cur.a, cur.b[n], zf, 3, 3, 0, a_scale, 0, 127);
+                Cs[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, ha),
+                                                              __builtin_bit_cast(v8h, blk < 2 ? hb01[n] : hb23[n]),
+                                                              zf, 0, 0, 0);
+            }
+#pragma unroll
+            for (int n = 0; n < NT; n++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[n][r] = __builtin_fmaf(S[n][r], Cs[n][r], acc[n][r]);
+        }
+    };
+
+    const int kper = (p.nstages + p.ksplit - 1) / p.ksplit;
+    const int s0 = kpart * kper, s1 = min(p.nstages, s0 + kper);
+    issue(s0, 0);
+    for (int s = s0; s < s1; s++) {
+        wait_and_barrier<0>();
+        if (s + 1 < s1) issue(s + 1, (s + 1 - s0) & 1);
+        compute((s - s0) & 1);
+    }
+    wait_and_barrier<0>();
+
+    float *Ct = (float *)lds;
+#pragma unroll
+    for (int n = 0; n < NT; n++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int row = wm * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+            Ct[row * CLD + wn * 64 + 32 * n + lr] = acc[n][r] * 0.5f;  // the doubled scale products
+        }
+    __syncthreads();
+    if constexpr (EPI == EPI_F32 || EPI == EPI_RESID) {
+        if (p.ksplit > 1) {
+            GemmParams q = p;
+            q.e.y = p.part + (int64_t)kpart * p.M * p.N;
+            q.e.ldy = p.N;
+            q.e.bias = nullptr;
+            epilogue<EPI_F32, BM, NTH>(q, Ct, m0, n0, t);
+            return;
+        }
+    }
+    epilogue<EPI, BM, NTH>(p, Ct, m0, n0, t);
 }
 
 // y = Σ_k part[k] (+ bias) for EPI_F32, y += Σ_k part[k] (+ bias) for
@@ -903,6 +1133,34 @@ hipError_t launch_gemm(const Weight &w, const Act &a, int64_t M, Epi epi, const 
             (int64_t)ea.grid * ea.grid_h != M || ea.window < 0 || !ea.bias || !ea.k || !ea.vt || ea.vt_ld <= 0 ||
             (ea.qpool ? (!ea.y || ea.ldy < ea.E) : !ea.q))
             return hipErrorInvalidValue;
+    }
+    if (a.kind == A_F6) {
+        // Q4_0 weights against fp6 activations (k_gemm_f6)
+        if (w.kind != WK_Q4_0 || !w.f6 || w.Kp % 128 != 0 || a.ld != w.Kp || !a.d) return hipErrorInvalidValue;
+        p.b = (const uint8_t *)w.f6;
+        p.nstages = (int)(w.Kp / 128);
+        p.tiles_m = (int)((M + 63) / 64);
+        p.ntiles = p.tiles_m * p.tiles_n;
+        const int64_t arec = (int64_t)p.tiles_m * p.nstages * 12288, brec = (int64_t)p.tiles_n * p.nstages * 12288;
+        if (arec > INT32_MAX || brec > INT32_MAX) return hipErrorInvalidValue;
+        p.a_rec = (int)arec;
+        p.b_rec = (int)brec;
+        const int grid = ((p.ntiles * p.ksplit + 7) / 8) * 8;
+        switch (epi) {
+            case EPI_F32: hipLaunchKernelGGL(k_gemm_f6<EPI_F32>, dim3(grid), dim3(256), 0, st, p); break;
+            case EPI_RESID: hipLaunchKernelGGL(k_gemm_f6<EPI_RESID>, dim3(grid), dim3(256), 0, st, p); break;
+            case EPI_GELU: hipLaunchKernelGGL(k_gemm_f6<EPI_GELU>, dim3(grid), dim3(256), 0, st, p); break;
+            case EPI_QKV: hipLaunchKernelGGL(k_gemm_f6<EPI_QKV>, dim3(grid), dim3(256), 0, st, p); break;
+            default: return hipErrorInvalidValue;
+        }
+        hipError_t e = hipGetLastError();
+        if (e == hipSuccess && p.ksplit > 1) {
+            const int64_t n = M * (w.N / 4);
+            hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p.part, p.ksplit,
+                               (int)M, (int)w.N, ea.bias, ea.y, ea.ldy, epi == EPI_RESID ? 1 : 0);
+            e = hipGetLastError();
+        }
+        return e;
     }
     // 64-row tiles: two or three work-groups share a CU, so one work-group's
     // epilogue overlaps another's main loop; with 128-row tiles (one per CU)

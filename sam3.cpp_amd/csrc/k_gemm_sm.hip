@@ -305,11 +305,11 @@ __global__ __launch_bounds__(64 * SM_WAVES, 2) void k_gemm_smb(SmArgs p) {
         for (int j = 0; j < C::WL; j++) {
             const int blk = C::q4 ? b0 + j : (WK == WK_Q8_0 ? b0 + j : b0 + j / 2);
             const int sub = C::q4 ? 0 : (WK == WK_Q8_0 ? lh : 2 * (j & 1) + lh);
-            f.w[j] = *(const uint4 *)(G.w + ((int64_t)blk * G.np + n) * C::BB + sub * 16);
+            f.w[j] = gload16(G.w + ((int64_t)blk * G.np + n) * C::BB + sub * 16);
         }
         if constexpr (C::quant) {
-            f.wd = *(const uint2 *)(G.wd + ((int64_t)s * G.np + n) * 4);
-            if constexpr (C::q41) f.wm = *(const uint2 *)(G.wm + ((int64_t)s * G.np + n) * 4);
+            f.wd = gload8(G.wd + ((int64_t)s * G.np + n) * 4);
+            if constexpr (C::q41) f.wm = gload8(G.wm + ((int64_t)s * G.np + n) * 4);
         }
     };
 
@@ -328,8 +328,8 @@ __global__ __launch_bounds__(64 * SM_WAVES, 2) void k_gemm_smb(SmArgs p) {
             uint2 ad[MT], as[MT];
 #pragma unroll
             for (int i = 0; i < MT; i++) {
-                ad[i] = *(const uint2 *)(L + B::A_BYTES + (32 * i + lr) * 8);
-                if constexpr (C::q41) as[i] = *(const uint2 *)(L + B::A_BYTES + B::SC_BYTES + (32 * i + lr) * 8);
+                ad[i] = lds_u2(L + B::A_BYTES + (32 * i + lr) * 8);
+                if constexpr (C::q41) as[i] = lds_u2(L + B::A_BYTES + B::SC_BYTES + (32 * i + lr) * 8);
             }
             const uint32_t wdw[2] = {f.wd.x, f.wd.y};
 #pragma unroll

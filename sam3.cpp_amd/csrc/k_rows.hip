@@ -48,6 +48,36 @@ __device__ __forceinline__ void emit4(const float *v, const Act &o, int64_t row,
     amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
     const float d = amax / 127.f;
     const float id = (amax != 0.f) ? 127.f / amax : 0.f;
+    if (o.kind == A_F6) {
+        // the same codes, split q = 16·h + l; lane k of the block's 8 holds
+        // bits [24k, 24k + 24) of each part's 192-bit operand string, and
+        // lanes 0-5 of the 8 each assemble and store one 8-byte word
+        uint32_t ph = 0, pl = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int q = (int)__builtin_rintf(v[i] * id);
+            const int h = f6_hi(q);
+            ph |= f6_code(h) << (6 * i);
+            pl |= f6_code(q - 16 * h) << (6 * i);
+        }
+        const int g = lane & ~7, k = lane & 7;
+        uint32_t x[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t a = __shfl(ph, g + j, 64), b = __shfl(pl, g + j, 64);
+            x[j] = k < 3 ? a : b;
+        }
+        if (k < 6) {
+            const int t = k % 3;
+            uint64_t w;
+            if (t == 0) w = (uint64_t)x[0] | ((uint64_t)x[1] << 24) | ((uint64_t)(x[2] & 0xFFFFu) << 48);
+            else if (t == 1) w = (uint64_t)(x[2] >> 16) | ((uint64_t)x[3] << 8) | ((uint64_t)x[4] << 32) | ((uint64_t)(x[5] & 0xFFu) << 56);
+            else w = (uint64_t)(x[5] >> 8) | ((uint64_t)x[6] << 16) | ((uint64_t)x[7] << 40);
+            ((uint64_t *)o.x)[f6_act_word(o.ld / 128, row, col / QK, k / 3, t)] = w;
+        }
+        if (k == 0) o.d[scale_index(o.mp, row, col / QK)] = f2h_bits(d);
+        return;
+    }
     int sum = 0;
     uint32_t packed = 0;
 #pragma unroll
@@ -250,7 +280,8 @@ hipError_t launch_layernorm(const float *x, int64_t M, int64_t E, float eps, con
                             const float *b, const Act &out, float *y_f32, hipStream_t st) {
     // float4 lanes; a Q8 block must be whole inside the row
     const bool q8 = !y_f32 && (out.kind == A_Q8_0 || out.kind == A_Q8_1);
-    if (E % 4 != 0 || E > 4096 || (q8 && E % 32 != 0)) return hipErrorInvalidValue;
+    const bool f6 = !y_f32 && out.kind == A_F6;
+    if (E % 4 != 0 || E > 4096 || (q8 && E % 32 != 0) || (f6 && (E % 128 != 0 || out.ld != E))) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((M + 3) / 4));
     if (E <= 256) hipLaunchKernelGGL(k_layernorm<1>, grid, dim3(256), 0, st, x, M, E, eps, w, b, out, y_f32);
     else if (E <= 512) hipLaunchKernelGGL(k_layernorm<2>, grid, dim3(256), 0, st, x, M, E, eps, w, b, out, y_f32);
@@ -265,7 +296,8 @@ hipError_t launch_rows_quant(AKind kind, const float *x, int64_t M, int64_t K, c
     (void)kind;
     // a Q8 block must be whole inside the row; other formats go by float4
     const bool q8 = out.kind == A_Q8_0 || out.kind == A_Q8_1;
-    if ((q8 && K % 32 != 0) || K % 4 != 0) return hipErrorInvalidValue;
+    if ((q8 && K % 32 != 0) || K % 4 != 0 || (out.kind == A_F6 && (K % 128 != 0 || out.ld != K)))
+        return hipErrorInvalidValue;
     const int64_t nf4 = (K + 127) / 128 * 32;  // float4 up to the 128-element group
     const dim3 grid((unsigned)((nf4 + 63) / 64), (unsigned)((M + 3) / 4));
     hipLaunchKernelGGL(k_rows_quant, grid, dim3(256), 0, st, x, M, K, out);

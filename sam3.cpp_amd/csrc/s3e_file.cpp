@@ -324,7 +324,7 @@ void add_mem_attn(std::vector<SynthTensor> &ts, int layers, int D) {
 
 }  // namespace
 
-extern "C" int s3e_synth_write(const char *path, const s3e_synth_cfg *cfg) {
+extern "C" int s3e_synth_write(const char *path, const s3e_synth_cfg *cfg) try {
     if (!path || !cfg) { set_error("s3e_synth_write: null argument"); return S3E_ERR_INVALID; }
     const int ftype = cfg->ftype;
     int wtype;
@@ -426,13 +426,13 @@ extern "C" int s3e_synth_write(const char *path, const s3e_synth_cfg *cfg) {
                                      256, 2, 3, 3, 64, cfg->mem_attn_layers > 0 ? cfg->mem_attn_layers : 4, 7, 16, 2,
                                      cfg->neck == 2 ? 0 : 1};       // visual_only
     return write_model(path, 0x73616D33u, 3, ftype, wtype, hp, ts, cfg->seed, sd, rnd_affine, HD);
-}
+} S3E_CATCH("s3e_synth_write")
 
 // SAM 2.x (Hiera) encoder file: convert_sam2_to_ggml.py:205-277 header (magic
 // "sam2", version 1, 57 hparams), the Hiera and FPN tensors of
 // sam2_register_tensors (sam3.cpp:1745-1847), block dimensions from
 // sam2_precompute_hiera_metadata (sam3.cpp:1676-1742).
-extern "C" int s3e_synth_write_sam2(const char *path, const s3e_synth_sam2_cfg *cfg) {
+extern "C" int s3e_synth_write_sam2(const char *path, const s3e_synth_sam2_cfg *cfg) try {
     if (!path || !cfg) { set_error("s3e_synth_write_sam2: null argument"); return S3E_ERR_INVALID; }
     const int ftype = cfg->ftype;
     if (ftype != 0 && ftype != 1 && ftype != 2 && ftype != 3 && ftype != 8) {
@@ -514,4 +514,4 @@ extern "C" int s3e_synth_write_sam2(const char *path, const s3e_synth_sam2_cfg *
     if (hp.size() != 57) { set_error("s3e_synth_write_sam2: internal hparams count"); return S3E_ERR_INVALID; }
     const int wtype = ftype;  // ggml type ids equal the ftype codes used here
     return write_model(path, 0x73616D32u, 1, ftype, wtype, hp, ts, cfg->seed, sd, rnd_affine, 0);
-}
+} S3E_CATCH("s3e_synth_write_sam2")

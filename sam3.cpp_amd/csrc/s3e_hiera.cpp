@@ -290,9 +290,13 @@ int hiera_load(int device, std::ifstream &fin, int ftype, int32_t n_tensors, Hie
         if (!fin.read(&name[0], name_len)) { set_error("s3e_model_load: truncated name"); return S3E_ERR_IO; }
         const std::streamoff pos = fin.tellg();
         fin.seekg((32 - pos % 32) % 32, std::ios::cur);
-        const int64_t n_el = t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3];
         if (t.ne[0] % ggml_blck(t.type) != 0) { set_error("s3e_model_load: '%s' ne0 not a block multiple", name.c_str()); return S3E_ERR_IO; }
-        const size_t bytes = ggml_rowsize(t.type, t.ne[0]) * (size_t)(n_el / t.ne[0]);
+        size_t bytes = 0;
+        if (!fin || !record_bytes(t.type, t.ne, stream_left(fin), &bytes)) {
+            set_error("s3e_model_load: data of '%s' oversized or past the end of the file", name.c_str());
+            return S3E_ERR_IO;
+        }
+        const int64_t n_el = t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3];
         if (memattn_wants(name)) {
             t.data.resize(bytes);
             if (!fin.read((char *)t.data.data(), (std::streamsize)bytes)) { set_error("s3e_model_load: truncated data of '%s'", name.c_str()); return S3E_ERR_IO; }

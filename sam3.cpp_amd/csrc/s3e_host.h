@@ -2,9 +2,10 @@
 // code: fp16 conversion, ggml block formats and the reference quantizers.
 #pragma once
 
+#include <cmath>
 #include <cstdint>
 #include <cstring>
-#include <cmath>
+#include <istream>
 
 namespace s3e {
 
@@ -63,6 +64,35 @@ inline size_t ggml_tsize(int type) {
     }
 }
 inline size_t ggml_rowsize(int type, int64_t ne0) { return ggml_tsize(type) * (size_t)(ne0 / ggml_blck(type)); }
+
+// Data bytes of a tensor record with dims ne[0..3] (positive, unused ones 1)
+// of ggml type `type`, if that size is representable and at most `left`
+// (the bytes remaining in the file): a malformed or truncated record is
+// refused before anything is allocated for it.
+inline bool record_bytes(int type, const int64_t ne[4], int64_t left, size_t *bytes) {
+    const int64_t lim = (int64_t)1 << 62;
+    int64_t rows = 1;
+    for (int i = 1; i < 4; i++) {
+        if (ne[i] <= 0 || rows > lim / ne[i]) return false;
+        rows *= ne[i];
+    }
+    if (ne[0] <= 0 || ggml_tsize(type) == 0 || ne[0] % ggml_blck(type) != 0) return false;
+    const int64_t rb = (int64_t)ggml_rowsize(type, ne[0]);
+    if (rb > lim / rows) return false;
+    const int64_t b = rb * rows;
+    if (b > left) return false;
+    *bytes = (size_t)b;
+    return true;
+}
+
+// Bytes between the read position of `f` and its end.
+inline int64_t stream_left(std::istream &f) {
+    const std::streamoff cur = f.tellg();
+    f.seekg(0, std::ios::end);
+    const std::streamoff end = f.tellg();
+    f.seekg(cur, std::ios::beg);
+    return cur < 0 || end < cur ? 0 : (int64_t)(end - cur);
+}
 
 // ggml reference quantizers (ggml_quantize_chunk with no importance matrix),
 // the ones examples/quantize.cpp:244-245 runs on model weights.

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <cstddef>
 #include <cstdint>
+#include <exception>
+#include <new>
 #include <string>
 
 #include "../../include/s3e.h"
@@ -25,7 +27,12 @@ enum WKind : int { WK_Q4_0 = 0, WK_Q4_1 = 1, WK_Q8_0 = 2, WK_F16 = 3, WK_F32 = 4
 //   A_F16  : fp16 [M][ld]                                 (vec_dot type of F16)
 //   A_F32  : f32  [M][ld]                                 (vec_dot type of F32)
 //   A_F16X2: fp16 hi [M][ld] + fp16 lo [M][ld], x = hi + lo  (f32 input of WK_F16X3)
-enum AKind : int { A_Q8_0 = 0, A_Q8_1 = 1, A_F16 = 2, A_F32 = 3, A_F16X2 = 4 };
+//   A_F6   : the Q8_0 codes q of each 32-element block split as q = 16·h + l
+//            (h ∈ [−8, 8], l ∈ [−8, 7], both exact in fp6 E3M2), in the
+//            operand order of the fp6 MFMA (f6_word below); fp16 scales d as
+//            for A_Q8_0.  Input of Q4_0 weights in the large-M GEMM (ld a
+//            multiple of 128).
+enum AKind : int { A_Q8_0 = 0, A_Q8_1 = 1, A_F16 = 2, A_F32 = 3, A_F16X2 = 4, A_F6 = 5 };
 
 inline AKind act_kind_for(WKind w) {
     switch (w) {
@@ -62,6 +69,36 @@ __host__ __device__ inline int64_t scale_index(int64_t mp, int64_t row, int64_t 
     return ((blk >> 2) * mp + row) * 4 + (blk & 3);
 }
 
+// fp6 E3M2 (sign, 3 exponent bits with bias 3, 2 mantissa bits): the code of
+// an integer v ∈ [−8, 8] (0, ±1, ±2, ±3 = 1.5·2, ±4, ±5 = 1.25·4, ±6, ±7 =
+// 1.75·4, ±8).  The magnitudes' 5-bit codes 0, 12, 16, 18, 20, 21, 22, 23, 24
+// sit in 6-bit fields of one 64-bit constant.
+__host__ __device__ inline uint32_t f6_code(int v) {
+    constexpr uint64_t T = (0ull) | (12ull << 6) | (16ull << 12) | (18ull << 18) | (20ull << 24) | (21ull << 30) |
+                           (22ull << 36) | (23ull << 42) | (24ull << 48);
+    const uint32_t a = (uint32_t)(v < 0 ? -v : v);
+    return ((uint32_t)(T >> (6 * a)) & 31u) | (v < 0 ? 32u : 0u);
+}
+// q = 16·h + l with h = ⌊(q + 8)/16⌋ ∈ [−8, 8] and l ∈ [−8, 7], for |q| ≤ 127.
+__host__ __device__ inline int f6_hi(int q) { return (q + 8) >> 4; }
+
+// A fp6 operand is 32 codes of one 32-element block (block order, code j in
+// bits [6j, 6j + 6) of a 192-bit string, little endian), stored as three
+// 8-byte words t = 0, 1, 2.  Activations (A_F6), in units of 8 bytes: for
+// 64-row tile rt, stage s of 4 blocks (K/128 stages), block b of the stage,
+// part p (0: h, 1: l), word t, row r % 64:
+//     (((rt · nst + s) · 4 + b) · 2 + p) · 3 + t) · 64 + r % 64
+// so one tile row's stage is 12 KB of contiguous memory (what the GEMM's DMA
+// copies to LDS as it is), and the 32 rows one MFMA operand read touches are
+// 256 contiguous bytes.  Weights (Weight::f6), likewise per 128-column tile
+// ct:  (((ct · nst + s) · 4 + b) · 3 + t) · 128 + n % 128.
+__host__ __device__ inline int64_t f6_act_word(int64_t nst, int64_t r, int64_t blk, int p, int t) {
+    return (((((r >> 6) * nst + (blk >> 2)) * 4 + (blk & 3)) * 2 + p) * 3 + t) * 64 + (r & 63);
+}
+__host__ __device__ inline int64_t f6_weight_word(int64_t nst, int64_t n, int64_t blk, int t) {
+    return ((((n >> 7) * nst + (blk >> 2)) * 4 + (blk & 3)) * 3 + t) * 128 + (n & 127);
+}
+
 // A weight matrix repacked for the GEMM kernels.  N rows of K, stored as
 // column-blocks of the output: row n of the ggml matrix is "column" n here.
 //   Q4_0/Q4_1/Q8_0: q8 [Np][Kp] int8 block codes — the file's integers
@@ -85,7 +122,14 @@ struct Weight {
     void *lo = nullptr;
     float alpha = 1.0f;
     size_t bytes = 0;
+    // Q4_0: the codes again as fp6 E3M2 words (f6_weight_word) for the GEMM
+    // against A_F6 activations
+    void *f6 = nullptr;
 };
+
+// The activation format the large-M GEMM takes for w: Q4_0 weights with an
+// fp6 copy run on the fp6 MFMA (A_F6), everything else as act_kind_for.
+inline AKind act_kind_gemm(const Weight &w) { return (w.kind == WK_Q4_0 && w.f6) ? A_F6 : act_kind_for(w.kind); }
 
 // GEMM epilogues.
 enum Epi : int {
@@ -327,12 +371,45 @@ __device__ __forceinline__ float gelu_erf(float x) {
     return 0.5f * x * w;
 }
 
+// 16 / 8 bytes loaded through a global-address-space pointer.  A pointer the
+// compiler cannot place (one read from memory rather than a kernel argument)
+// makes a flat load, which may address LDS, so behind LDS DMA the compiler
+// first waits for every DMA in flight.  The loads go through vector types:
+// HIP's uint4 / uint2 copy through a generic reference and stay flat.
+__device__ __forceinline__ uint4 gload16(const void *p) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(1))) const u32x4 g_u32x4;
+    const u32x4 v = *(g_u32x4 *)p;
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint2 gload8(const void *p) {
+    typedef __attribute__((address_space(1))) const uint64_t g_u64;
+    const uint64_t v = *(g_u64 *)p;
+    return make_uint2((uint32_t)v, (uint32_t)(v >> 32));
+}
+
+// An 8-byte LDS word as two 32-bit halves.  Read as uint2, the load makes
+// the compiler wait for every LDS DMA in flight (the next stage's included)
+// before it; a 64-bit read does not.
+__device__ __forceinline__ uint2 lds_u2(const void *p) {
+    const uint64_t v = *(const uint64_t *)p;
+    return make_uint2((uint32_t)v, (uint32_t)(v >> 32));
+}
+
 // Wait until at most N of this wave's vector-memory operations are
 // outstanding and all its LDS reads have returned, then join the work-group.
-// The memory clobber keeps the compiler from moving LDS accesses across it.
+// The wait is the builtin (gfx9 s_waitcnt fields: vmcnt [3:0] and [15:14],
+// expcnt [6:4] left at 7, lgkmcnt [11:8] at 0) so that the compiler's own
+// wait tracking knows those loads completed: behind an opaque asm wait it
+// would still treat earlier loads (e.g. fragments loaded before a loop) as
+// outstanding and put a vmcnt(0) inside the loop, which also drains the LDS
+// DMA of the next stage.  The barrier is asm with a memory clobber, which
+// keeps the compiler from moving LDS accesses across it.
 template <int N>
 __device__ __forceinline__ void wait_and_barrier() {
-    __asm__ volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+    __asm__ volatile("s_barrier" ::: "memory");
 }
 
 // Stage widths (elements of K per pipeline stage) by weight kind.
@@ -350,3 +427,21 @@ constexpr int CONV_BN = 256;
 void set_error(const char *fmt, ...);
 
 }  // namespace s3e
+
+// Handlers of the function-try-blocks around the extern "C" entry points
+// (`extern "C" int s3e_x(...) try { ... } S3E_CATCH("s3e_x")`): no exception
+// leaves the library; a failed host allocation returns S3E_ERR_NOMEM,
+// anything else S3E_ERR_IO, with the message set.
+#define S3E_CATCH(fn)                                                 \
+    catch (const std::bad_alloc &) {                                  \
+        s3e::set_error("%s: out of host memory", fn);                 \
+        return S3E_ERR_NOMEM;                                         \
+    }                                                                 \
+    catch (const std::exception &ex_) {                               \
+        s3e::set_error("%s: %s", fn, ex_.what());                     \
+        return S3E_ERR_IO;                                            \
+    }                                                                 \
+    catch (...) {                                                     \
+        s3e::set_error("%s: unexpected exception", fn);               \
+        return S3E_ERR_IO;                                            \
+    }

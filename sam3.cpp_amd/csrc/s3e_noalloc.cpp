@@ -58,7 +58,7 @@ int noalloc_init(int device, void **out) {
 }  // namespace s3e
 
 extern "C" int s3e_mul_mat_noalloc(s3e_ctx *ctx, const s3e_weight *w, const float *X, int64_t M, const float *bias,
-                                   float *Y) {
+                                   float *Y) try {
     if (!ctx || !w || !X || !Y) { set_error("s3e_mul_mat_noalloc: NULL argument"); return S3E_ERR_INVALID; }
     if (M < 0) { set_error("s3e_mul_mat_noalloc: negative M"); return S3E_ERR_INVALID; }
     const Weight &W = w->w;
@@ -111,4 +111,4 @@ extern "C" int s3e_mul_mat_noalloc(s3e_ctx *ctx, const s3e_weight *w, const floa
     }
     if (e != hipSuccess) { set_error("s3e_mul_mat_noalloc: %s", hipGetErrorString(e)); return S3E_ERR_HIP; }
     return S3E_OK;
-}
+} S3E_CATCH("s3e_mul_mat_noalloc")

@@ -69,9 +69,11 @@ void free_weight(Weight &w) {
     if (w.d) (void)hipFree(w.d);
     if (w.m) (void)hipFree(w.m);
     if (w.lo) (void)hipFree(w.lo);
+    if (w.f6) (void)hipFree(w.f6);
     w.q = nullptr;
     w.d = w.m = nullptr;
     w.lo = nullptr;
+    w.f6 = nullptr;
 }
 
 // f32 weights (N rows of K) as two fp16 planes for the split-precision GEMM:
@@ -183,8 +185,30 @@ int upload_weight(int device, int type, int64_t K, int64_t N, const uint8_t *src
         } break;
         default: break;  // WK_F16X3 comes from upload_weight_split
     }
+    // Q4_0 with K a multiple of 128: the codes also as fp6 E3M2 operand words
+    std::vector<uint64_t> f6;
+    if (w.kind == WK_Q4_0 && K % 128 == 0) {
+        const int64_t nst = w.Kp / 128;
+        f6.assign((size_t)(w.Np * (w.Kp / 32) * 3), 0);
+        for (int64_t n = 0; n < N; n++)
+            for (int64_t b = 0; b < Kb; b++) {
+                const int8_t *c = (const int8_t *)&q[(size_t)(n * w.Kp + b * 32)];
+                uint64_t bits[3] = {0, 0, 0};
+                for (int j = 0; j < 32; j++) {
+                    const uint64_t v = f6_code(c[j]);
+                    const int at = 6 * j;
+                    bits[at / 64] |= v << (at % 64);
+                    if (at % 64 > 58) bits[at / 64 + 1] |= v >> (64 - at % 64);
+                }
+                for (int t = 0; t < 3; t++) f6[(size_t)f6_weight_word(nst, n, b, t)] = bits[t];
+            }
+    }
     hipError_t e = hipMalloc(&w.q, q.size());
     if (e == hipSuccess) e = hipMemcpy(w.q, q.data(), q.size(), hipMemcpyHostToDevice);
+    if (e == hipSuccess && !f6.empty()) {
+        e = hipMalloc(&w.f6, f6.size() * 8);
+        if (e == hipSuccess) e = hipMemcpy(w.f6, f6.data(), f6.size() * 8, hipMemcpyHostToDevice);
+    }
     if (e == hipSuccess && !d.empty()) {
         e = hipMalloc(&w.d, d.size() * 2);
         if (e == hipSuccess) e = hipMemcpy(w.d, d.data(), d.size() * 2, hipMemcpyHostToDevice);
@@ -198,7 +222,7 @@ int upload_weight(int device, int type, int64_t K, int64_t N, const uint8_t *src
         set_error("weight upload: %s", hipGetErrorString(e));
         return S3E_ERR_HIP;
     }
-    w.bytes = q.size() + d.size() * 2 + m.size() * 2;
+    w.bytes = q.size() + d.size() * 2 + m.size() * 2 + f6.size() * 8;
     return S3E_OK;
 }
 
@@ -257,7 +281,7 @@ std::vector<float> sinusoidal_pe_2d(int H, int W, int d) {
 extern "C" const char *s3e_last_error(void) { return g_err.c_str(); }
 extern "C" int s3e_abi_version(void) { return S3E_ABI_VERSION; }
 
-extern "C" int s3e_ctx_create(int device, s3e_ctx **out) {
+extern "C" int s3e_ctx_create(int device, s3e_ctx **out) try {
     if (!out) { set_error("s3e_ctx_create: out is NULL"); return S3E_ERR_INVALID; }
     *out = nullptr;
     int n = 0;
@@ -282,7 +306,7 @@ extern "C" int s3e_ctx_create(int device, s3e_ctx **out) {
     }
     *out = c;
     return S3E_OK;
-}
+} S3E_CATCH("s3e_ctx_create")
 
 extern "C" void s3e_ctx_destroy(s3e_ctx *ctx) {
     if (!ctx) return;
@@ -293,15 +317,15 @@ extern "C" void s3e_ctx_destroy(s3e_ctx *ctx) {
     delete ctx;
 }
 
-extern "C" int s3e_ctx_sync(s3e_ctx *ctx) {
+extern "C" int s3e_ctx_sync(s3e_ctx *ctx) try {
     if (!ctx) { set_error("s3e_ctx_sync: NULL context"); return S3E_ERR_INVALID; }
     HIP_TRY(hipStreamSynchronize(ctx->stream));
     return S3E_OK;
-}
+} S3E_CATCH("s3e_ctx_sync")
 
 extern "C" void *s3e_ctx_stream(s3e_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
 
-extern "C" int s3e_malloc(s3e_ctx *ctx, size_t bytes, void **out) {
+extern "C" int s3e_malloc(s3e_ctx *ctx, size_t bytes, void **out) try {
     if (!ctx || !out) { set_error("s3e_malloc: NULL argument"); return S3E_ERR_INVALID; }
     HIP_TRY(hipSetDevice(ctx->device));
     if (hipMalloc(out, bytes) != hipSuccess) {
@@ -309,22 +333,22 @@ extern "C" int s3e_malloc(s3e_ctx *ctx, size_t bytes, void **out) {
         return S3E_ERR_NOMEM;
     }
     return S3E_OK;
-}
+} S3E_CATCH("s3e_malloc")
 
-extern "C" int s3e_free(s3e_ctx *ctx, void *ptr) {
+extern "C" int s3e_free(s3e_ctx *ctx, void *ptr) try {
     if (!ctx) { set_error("s3e_free: NULL context"); return S3E_ERR_INVALID; }
     if (ptr) HIP_TRY(hipFree(ptr));
     return S3E_OK;
-}
+} S3E_CATCH("s3e_free")
 
-extern "C" int s3e_memcpy_h2d(s3e_ctx *ctx, void *dst, const void *src, size_t bytes) {
+extern "C" int s3e_memcpy_h2d(s3e_ctx *ctx, void *dst, const void *src, size_t bytes) try {
     if (!ctx) { set_error("s3e_memcpy_h2d: NULL context"); return S3E_ERR_INVALID; }
     HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
     HIP_TRY(hipStreamSynchronize(ctx->stream));
     return S3E_OK;
-}
+} S3E_CATCH("s3e_memcpy_h2d")
 
-extern "C" int s3e_copy(s3e_ctx *ctx, void *dst, const void *src, size_t bytes) {
+extern "C" int s3e_copy(s3e_ctx *ctx, void *dst, const void *src, size_t bytes) try {
     if (!ctx || !dst || !src) { set_error("s3e_copy: NULL argument"); return S3E_ERR_INVALID; }
     if (bytes % 16 != 0 || ((uintptr_t)dst | (uintptr_t)src) % 16 != 0) {
         set_error("s3e_copy: size and pointers must be 16-byte multiples");
@@ -333,18 +357,18 @@ extern "C" int s3e_copy(s3e_ctx *ctx, void *dst, const void *src, size_t bytes) 
     HIP_TRY(hipSetDevice(ctx->device));
     HIP_TRY(launch_copy(dst, src, bytes, ctx->stream));
     return S3E_OK;
-}
+} S3E_CATCH("s3e_copy")
 
-extern "C" int s3e_memcpy_d2h(s3e_ctx *ctx, void *dst, const void *src, size_t bytes) {
+extern "C" int s3e_memcpy_d2h(s3e_ctx *ctx, void *dst, const void *src, size_t bytes) try {
     if (!ctx) { set_error("s3e_memcpy_d2h: NULL context"); return S3E_ERR_INVALID; }
     HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
     HIP_TRY(hipStreamSynchronize(ctx->stream));
     return S3E_OK;
-}
+} S3E_CATCH("s3e_memcpy_d2h")
 
 // ---- ggml_mul_mat ---------------------------------------------------------
 extern "C" int s3e_weight_upload(s3e_ctx *ctx, int type, int64_t ne0, int64_t ne1, const void *host_data,
-                                 size_t nbytes, s3e_weight **out) {
+                                 size_t nbytes, s3e_weight **out) try {
     if (!ctx || !host_data || !out) { set_error("s3e_weight_upload: NULL argument"); return S3E_ERR_INVALID; }
     *out = nullptr;
     HIP_TRY(hipSetDevice(ctx->device));
@@ -357,7 +381,7 @@ extern "C" int s3e_weight_upload(s3e_ctx *ctx, int type, int64_t ne0, int64_t ne
     }
     *out = w;
     return S3E_OK;
-}
+} S3E_CATCH("s3e_weight_upload")
 
 extern "C" void s3e_weight_free(s3e_weight *w) {
     if (!w) return;
@@ -432,17 +456,17 @@ hipError_t run_mul_mat(const s3e_weight *w, const Act &a, int64_t M, const EpiAr
 
 }  // namespace
 
-extern "C" int s3e_weight_info(const s3e_weight *w, int64_t out[4]) {
+extern "C" int s3e_weight_info(const s3e_weight *w, int64_t out[4]) try {
     if (!w || !out) { set_error("s3e_weight_info: NULL argument"); return S3E_ERR_INVALID; }
     out[0] = w->w.ggml_type;
     out[1] = w->w.K;
     out[2] = w->w.N;
     out[3] = (int64_t)w->w.bytes;
     return S3E_OK;
-}
+} S3E_CATCH("s3e_weight_info")
 
 extern "C" int s3e_quantize_rows(s3e_ctx *ctx, int type, const float *X, int64_t M, int64_t K, void *qs,
-                                 uint16_t *d, uint16_t *s) {
+                                 uint16_t *d, uint16_t *s) try {
     if (!ctx || !X || !qs) { set_error("s3e_quantize_rows: NULL argument"); return S3E_ERR_INVALID; }
     if (K % 32 != 0 || M < 0) { set_error("s3e_quantize_rows: K=%lld must be a multiple of 32", (long long)K); return S3E_ERR_INVALID; }
     Act a;
@@ -459,10 +483,10 @@ extern "C" int s3e_quantize_rows(s3e_ctx *ctx, int type, const float *X, int64_t
     HIP_TRY(hipSetDevice(ctx->device));
     HIP_TRY(launch_rows_quant(a.kind, X, M, K, a, ctx->stream));
     return S3E_OK;
-}
+} S3E_CATCH("s3e_quantize_rows")
 
 extern "C" int s3e_mul_mat(s3e_ctx *ctx, const s3e_weight *w, const float *X, int64_t M, const float *bias,
-                           float *Y) {
+                           float *Y) try {
     if (!ctx || !w || !X || !Y) { set_error("s3e_mul_mat: NULL argument"); return S3E_ERR_INVALID; }
     if (M < 0) { set_error("s3e_mul_mat: negative M"); return S3E_ERR_INVALID; }
     const Weight &W = w->w;
@@ -486,18 +510,18 @@ extern "C" int s3e_mul_mat(s3e_ctx *ctx, const s3e_weight *w, const float *X, in
         return S3E_OK;
     }
     ActBuf buf;
-    HIP_TRY(buf.alloc(M, W.K, ctx->stream));
-    const Act a = buf.as(ak, W.K);
-    hipError_t e = launch_rows_quant(ak, X, M, W.K, a, ctx->stream);
+    HIP_TRY(buf.alloc(std::max<int64_t>(M, 64), W.K, ctx->stream));
+    const Act a = buf.as(sm_eligible(W, M) ? ak : act_kind_gemm(W), W.K);
+    hipError_t e = launch_rows_quant(a.kind, X, M, W.K, a, ctx->stream);
     if (e == hipSuccess) e = run_mul_mat(w, a, M, ea, ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     buf.release();
     if (e != hipSuccess) { set_error("s3e_mul_mat: %s", hipGetErrorString(e)); return S3E_ERR_HIP; }
     return S3E_OK;
-}
+} S3E_CATCH("s3e_mul_mat")
 
 extern "C" int s3e_mul_mat_q(s3e_ctx *ctx, const s3e_weight *w, const void *xq, const uint16_t *d,
-                             const uint16_t *s, int64_t M, const float *bias, float *Y) {
+                             const uint16_t *s, int64_t M, const float *bias, float *Y) try {
     if (!ctx || !w || !xq || !Y) { set_error("s3e_mul_mat_q: NULL argument"); return S3E_ERR_INVALID; }
     const Weight &W = w->w;
     const AKind ak = act_kind_for(W.kind);
@@ -519,11 +543,11 @@ extern "C" int s3e_mul_mat_q(s3e_ctx *ctx, const s3e_weight *w, const void *xq, 
     ea.ldy = W.N;
     HIP_TRY(run_mul_mat(w, a, M, ea, ctx->stream));
     return S3E_OK;
-}
+} S3E_CATCH("s3e_mul_mat_q")
 
 extern "C" int s3e_mul_mat_q_batch(s3e_ctx *ctx, int n, const s3e_weight *const *w, const void *const *xq,
                                    const uint16_t *const *d, const uint16_t *const *s, int64_t M,
-                                   const float *const *bias, float *const *Y) {
+                                   const float *const *bias, float *const *Y) try {
     if (!ctx || n <= 0 || !w || !xq || !Y) { set_error("s3e_mul_mat_q_batch: NULL argument or n <= 0"); return S3E_ERR_INVALID; }
     if (M < 1 || M > 64) { set_error("s3e_mul_mat_q_batch: M=%lld is outside 1..64", (long long)M); return S3E_ERR_UNSUPPORTED; }
     const WKind kind = w[0] ? w[0]->w.kind : WK_F32;
@@ -586,10 +610,10 @@ extern "C" int s3e_mul_mat_q_batch(s3e_ctx *ctx, int n, const s3e_weight *const 
     sa.M = (int)M;
     HIP_TRY(launch_gemm_smb(kind, sa, wgs, ctx->stream));
     return S3E_OK;
-}
+} S3E_CATCH("s3e_mul_mat_q_batch")
 
 extern "C" int s3e_layer_norm(s3e_ctx *ctx, const float *x, int64_t rows, int64_t n, float eps, const float *w,
-                              const float *b, float *y) {
+                              const float *b, float *y) try {
     if (!ctx || !x || !y) { set_error("s3e_layer_norm: NULL argument"); return S3E_ERR_INVALID; }
     if (rows < 0 || n <= 0 || n % 32 != 0 || n > 4096) {
         set_error("s3e_layer_norm: row length %lld must be a positive multiple of 32 up to 4096", (long long)n);
@@ -600,13 +624,13 @@ extern "C" int s3e_layer_norm(s3e_ctx *ctx, const float *x, int64_t rows, int64_
     Act none;
     HIP_TRY(launch_layernorm(x, rows, n, eps, w, b, none, y, ctx->stream));
     return S3E_OK;
-}
+} S3E_CATCH("s3e_layer_norm")
 
 // ---- ggml_flash_attn_ext --------------------------------------------------
 extern "C" int s3e_flash_attn_ext(s3e_ctx *ctx, const float *q, const int64_t q_nb[4], const float *k,
                                   const int64_t k_nb[4], const float *v, const int64_t v_nb[4], int64_t D,
                                   int64_t Nq, int64_t Nkv, int64_t nh, int64_t B, float scale, int prec,
-                                  float *o) {
+                                  float *o) try {
     if (!ctx || !q || !k || !v || !o || !q_nb || !k_nb || !v_nb) {
         set_error("s3e_flash_attn_ext: NULL argument");
         return S3E_ERR_INVALID;
@@ -685,7 +709,7 @@ extern "C" int s3e_flash_attn_ext(s3e_ctx *ctx, const float *q, const int64_t q_
     if (part) (void)hipFree(part);
     if (e != hipSuccess) { set_error("s3e_flash_attn_ext: %s", hipGetErrorString(e)); return S3E_ERR_HIP; }
     return S3E_OK;
-}
+} S3E_CATCH("s3e_flash_attn_ext")
 
 // ---- SAM 3 ViT model -------------------------------------------------------
 namespace {
@@ -880,7 +904,7 @@ extern "C" void s3e_model_free(s3e_model *m) {
     delete m;
 }
 
-extern "C" int s3e_model_load(s3e_ctx *ctx, const char *path, s3e_model **out) {
+extern "C" int s3e_model_load(s3e_ctx *ctx, const char *path, s3e_model **out) try {
     if (!ctx || !path || !out) { set_error("s3e_model_load: NULL argument"); return S3E_ERR_INVALID; }
     *out = nullptr;
     HIP_TRY(hipSetDevice(ctx->device));
@@ -965,9 +989,12 @@ extern "C" int s3e_model_load(s3e_ctx *ctx, const char *path, s3e_model **out) {
         if (!rd(&name[0], (size_t)name_len)) { set_error("s3e_model_load: truncated name"); return S3E_ERR_IO; }
         const std::streamoff pos = fin.tellg();
         fin.seekg((32 - pos % 32) % 32, std::ios::cur);
-        const int64_t n_el = t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3];
         if (t.ne[0] % ggml_blck(t.type) != 0) { set_error("s3e_model_load: '%s' ne0 not a block multiple", name.c_str()); return S3E_ERR_IO; }
-        const size_t bytes = ggml_rowsize(t.type, t.ne[0]) * (size_t)(n_el / t.ne[0]);
+        size_t bytes = 0;
+        if (!fin || !record_bytes(t.type, t.ne, stream_left(fin), &bytes)) {
+            set_error("s3e_model_load: data of '%s' oversized or past the end of the file", name.c_str());
+            return S3E_ERR_IO;
+        }
         const bool is_neck = name.compare(0, 9, "neck.det.") == 0 || name.compare(0, 9, "neck.trk.") == 0;
         if (memattn_wants(name)) {
             t.data.resize(bytes);
@@ -1059,16 +1086,16 @@ extern "C" int s3e_model_load(s3e_ctx *ctx, const char *path, s3e_model **out) {
     }
     *out = m.release();
     return S3E_OK;
-}
+} S3E_CATCH("s3e_model_load")
 
-extern "C" int s3e_model_type(const s3e_model *m) {
+extern "C" int s3e_model_type(const s3e_model *m) try {
     if (!m) return -1;
     if (m->hiera) return 2;           // SAM3_MODEL_SAM2
     return m->necks_present & 2 ? 0   // SAM3_MODEL_SAM3
                                 : 1;  // SAM3_MODEL_SAM3_VISUAL
-}
+} S3E_CATCH("s3e_model_type")
 
-extern "C" int s3e_model_hparams(const s3e_model *m, int32_t out[16]) {
+extern "C" int s3e_model_hparams(const s3e_model *m, int32_t out[16]) try {
     if (!m || !out) { set_error("s3e_model_hparams: NULL argument"); return S3E_ERR_INVALID; }
     if (m->hiera) {
         hiera_hparams(m->hiera, out);
@@ -1083,7 +1110,7 @@ extern "C" int s3e_model_hparams(const s3e_model *m, int32_t out[16]) {
     out[14] = m->neck_dim;
     out[15] = m->necks_present;
     return S3E_OK;
-}
+} S3E_CATCH("s3e_model_hparams")
 
 // ---- state + encoder --------------------------------------------------------
 struct s3e_state {
@@ -1207,7 +1234,7 @@ hipError_t alloc_neck(s3e_state *st) {
 
 }  // namespace
 
-extern "C" int s3e_state_create(s3e_ctx *ctx, const s3e_model *m, s3e_state **out) {
+extern "C" int s3e_state_create(s3e_ctx *ctx, const s3e_model *m, s3e_state **out) try {
     if (!ctx || !m || !out) { set_error("s3e_state_create: NULL argument"); return S3E_ERR_INVALID; }
     *out = nullptr;
     HIP_TRY(hipSetDevice(ctx->device));
@@ -1252,7 +1279,7 @@ extern "C" int s3e_state_create(s3e_ctx *ctx, const s3e_model *m, s3e_state **ou
     }
     *out = st;
     return S3E_OK;
-}
+} S3E_CATCH("s3e_state_create")
 
 namespace {
 
@@ -1284,7 +1311,7 @@ hipError_t run_block(s3e_state *st, int bi, float *x) {
     const int WS = b.global ? m->grid : m->window;
     const int Nw = WS * WS, NW = (m->grid / WS) * (m->grid / WS);
     // LN1 → activation for the QKV weight
-    const Act a_qkv = st->a1.as(act_kind_for(b.qkv.kind), E);
+    const Act a_qkv = st->a1.as(act_kind_gemm(b.qkv), E);
     hipError_t e = launch_layernorm(x, T, E, 1e-5f, b.n1w, b.n1b, a_qkv, nullptr, s);
     if (e != hipSuccess) return e;
     // QKV GEMM + bias + RoPE → fp16 Q, K, Vᵀ in window layout
@@ -1325,7 +1352,7 @@ hipError_t run_block(s3e_state *st, int bi, float *x) {
     aa.scale = 1.0f / std::sqrt(64.0f);
     aa.grid = m->grid;
     aa.window = WS;
-    aa.out = st->a1.as(act_kind_for(b.proj.kind), E);
+    aa.out = st->a1.as(act_kind_gemm(b.proj), E);
     e = launch_attn(aa, s);
     if (e != hipSuccess) return e;
     // proj + bias + residual
@@ -1336,12 +1363,12 @@ hipError_t run_block(s3e_state *st, int bi, float *x) {
     e = launch_gemm(b.proj, aa.out, T, EPI_RESID, ep, s);
     if (e != hipSuccess) return e;
     // LN2 → fc1 + bias + GELU(erf) → activation for fc2 → fc2 + bias + residual
-    const Act a_fc1 = st->a1.as(act_kind_for(b.fc1.kind), E);
+    const Act a_fc1 = st->a1.as(act_kind_gemm(b.fc1), E);
     e = launch_layernorm(x, T, E, 1e-5f, b.n2w, b.n2b, a_fc1, nullptr, s);
     if (e != hipSuccess) return e;
     EpiArgs e1;
     e1.bias = b.fc1_b;
-    e1.out = st->a2.as(act_kind_for(b.fc2.kind), m->mlp);
+    e1.out = st->a2.as(act_kind_gemm(b.fc2), m->mlp);
     e = launch_gemm(b.fc1, a_fc1, T, EPI_GELU, e1, s);
     if (e != hipSuccess) return e;
     EpiArgs e2;
@@ -1460,22 +1487,22 @@ hipError_t run_necks(s3e_state *st, const float *x) {
 
 }  // namespace
 
-extern "C" int s3e_vit_prefix(s3e_state *st, const float *chw_device, float *x_device) {
+extern "C" int s3e_vit_prefix(s3e_state *st, const float *chw_device, float *x_device) try {
     if (!st || !chw_device || !x_device) { set_error("s3e_vit_prefix: NULL argument"); return S3E_ERR_INVALID; }
     if (st->m->hiera) { set_error("s3e_vit_prefix: the model is a SAM 2 (Hiera) encoder"); return S3E_ERR_INVALID; }
     HIP_TRY(hipSetDevice(st->ctx->device));
     HIP_TRY(run_prefix(st, chw_device, x_device));
     return S3E_OK;
-}
+} S3E_CATCH("s3e_vit_prefix")
 
-extern "C" int s3e_vit_block(s3e_state *st, int idx, float *x_device) {
+extern "C" int s3e_vit_block(s3e_state *st, int idx, float *x_device) try {
     if (!st || !x_device) { set_error("s3e_vit_block: NULL argument"); return S3E_ERR_INVALID; }
     if (st->m->hiera) { set_error("s3e_vit_block: the model is a SAM 2 (Hiera) encoder"); return S3E_ERR_INVALID; }
     if (idx < 0 || idx >= st->m->depth) { set_error("s3e_vit_block: block %d out of range", idx); return S3E_ERR_INVALID; }
     HIP_TRY(hipSetDevice(st->ctx->device));
     HIP_TRY(run_block(st, idx, x_device));
     return S3E_OK;
-}
+} S3E_CATCH("s3e_vit_block")
 
 // ---- sub-stage hooks --------------------------------------------------------
 // sam3_test_run_vit_block_stage / sam3_test_run_vit_prefix_stage
@@ -1516,7 +1543,7 @@ hipError_t stage_scratch(s3e_state *st, int64_t floats) {
 hipError_t stage_linear(s3e_state *st, const Weight &w, const float *bias, const ActBuf &buf, const float *x,
                         int64_t M, float *y) {
     hipStream_t s = st->ctx->stream;
-    const Act a = buf.as(act_kind_for(w.kind), w.K);
+    const Act a = buf.as(act_kind_gemm(w), w.K);
     hipError_t e = launch_rows_quant(a.kind, x, M, w.K, a, s);
     if (e != hipSuccess) return e;
     EpiArgs ea;
@@ -1548,7 +1575,7 @@ int patch_f16(s3e_state *st, const Weight **out) {
 }  // namespace
 
 extern "C" int s3e_vit_block_stage(s3e_state *st, int idx, int stage, const float *in_device, const int64_t in_ne[4],
-                                   float *out_device, int64_t out_ne[4]) {
+                                   float *out_device, int64_t out_ne[4]) try {
     if (!st || !in_ne || !out_ne) { set_error("s3e_vit_block_stage: NULL argument"); return S3E_ERR_INVALID; }
     const s3e_model *m = st->m;
     if (m->hiera) { set_error("s3e_vit_block_stage: the model is a SAM 2 (Hiera) encoder"); return S3E_ERR_INVALID; }
@@ -1616,11 +1643,11 @@ extern "C" int s3e_vit_block_stage(s3e_state *st, int idx, int stage, const floa
         case BS_MLP_GELU: HIP_TRY(launch_gelu_rows(in_device, out_device, rows * MLP, s)); break;
         case BS_MLP: {
             // fc1 with the encoder's fused bias + GELU + conversion epilogue, then fc2
-            const Act a1 = st->a1.as(act_kind_for(b.fc1.kind), E);
+            const Act a1 = st->a1.as(act_kind_gemm(b.fc1), E);
             HIP_TRY(launch_rows_quant(a1.kind, in_device, rows, E, a1, s));
             EpiArgs e1;
             e1.bias = b.fc1_b;
-            e1.out = st->a2.as(act_kind_for(b.fc2.kind), MLP);
+            e1.out = st->a2.as(act_kind_gemm(b.fc2), MLP);
             HIP_TRY(launch_gemm(b.fc1, a1, rows, EPI_GELU, e1, s));
             EpiArgs e2;
             e2.bias = b.fc2_b;
@@ -1673,10 +1700,10 @@ extern "C" int s3e_vit_block_stage(s3e_state *st, int idx, int stage, const floa
         default: break;
     }
     return S3E_OK;
-}
+} S3E_CATCH("s3e_vit_block_stage")
 
 extern "C" int s3e_vit_prefix_stage(s3e_state *st, int stage, const float *in_device, const int64_t in_ne[4],
-                                    float *out_device, int64_t out_ne[4]) {
+                                    float *out_device, int64_t out_ne[4]) try {
     if (!st || !in_ne || !out_ne) { set_error("s3e_vit_prefix_stage: NULL argument"); return S3E_ERR_INVALID; }
     const s3e_model *m = st->m;
     if (m->hiera) { set_error("s3e_vit_prefix_stage: the model is a SAM 2 (Hiera) encoder"); return S3E_ERR_INVALID; }
@@ -1760,19 +1787,19 @@ extern "C" int s3e_vit_prefix_stage(s3e_state *st, int stage, const float *in_de
         default: break;
     }
     return S3E_OK;
-}
+} S3E_CATCH("s3e_vit_prefix_stage")
 
-extern "C" int s3e_encode_vit_chw(s3e_state *st, const float *chw_device) {
+extern "C" int s3e_encode_vit_chw(s3e_state *st, const float *chw_device) try {
     if (!st || !chw_device) { set_error("s3e_encode_vit_chw: NULL argument"); return S3E_ERR_INVALID; }
     if (st->m->hiera) { set_error("s3e_encode_vit_chw: the model is a SAM 2 (Hiera) encoder"); return S3E_ERR_INVALID; }
     HIP_TRY(hipSetDevice(st->ctx->device));
     HIP_TRY(run_prefix(st, chw_device, st->x));
     for (int i = 0; i < st->m->depth; i++) HIP_TRY(run_block(st, i, st->x));
     return S3E_OK;
-}
+} S3E_CATCH("s3e_encode_vit_chw")
 
 extern "C" int s3e_model_tensor_get(const s3e_model *m, const char *name, int *type, int64_t ne[4], void *host,
-                                    size_t bytes) {
+                                    size_t bytes) try {
     if (!m || !name || !type || !ne) { set_error("s3e_model_tensor_get: NULL argument"); return S3E_ERR_INVALID; }
     if (m->hiera) { set_error("s3e_model_tensor_get: the model is a SAM 2 (Hiera) encoder"); return S3E_ERR_UNSUPPORTED; }
     const std::string n(name);
@@ -1819,9 +1846,9 @@ extern "C" int s3e_model_tensor_get(const s3e_model *m, const char *name, int *t
     HIP_TRY(hipSetDevice(m->ctx->device));
     HIP_TRY(hipMemcpy2D(host, (size_t)K * es, w->q, (size_t)w->Kp * es, (size_t)K * es, (size_t)w->N, hipMemcpyDeviceToHost));
     return S3E_OK;
-}
+} S3E_CATCH("s3e_model_tensor_get")
 
-extern "C" int s3e_encode_chw(s3e_state *st, const float *chw_device) {
+extern "C" int s3e_encode_chw(s3e_state *st, const float *chw_device) try {
     if (!st || !chw_device) { set_error("s3e_encode_chw: NULL argument"); return S3E_ERR_INVALID; }
     HIP_TRY(hipSetDevice(st->ctx->device));
     if (st->m->hiera) {
@@ -1832,34 +1859,34 @@ extern "C" int s3e_encode_chw(s3e_state *st, const float *chw_device) {
     for (int i = 0; i < st->m->depth; i++) HIP_TRY(run_block(st, i, st->x));
     HIP_TRY(run_necks(st, st->x));
     return S3E_OK;
-}
+} S3E_CATCH("s3e_encode_chw")
 
-extern "C" int s3e_run_neck(s3e_state *st, const float *x_device) {
+extern "C" int s3e_run_neck(s3e_state *st, const float *x_device) try {
     if (!st || !x_device) { set_error("s3e_run_neck: NULL argument"); return S3E_ERR_INVALID; }
     if (!st->m->necks_present || st->m->hiera) { set_error("s3e_run_neck: the model has no SimpleFPN neck"); return S3E_ERR_INVALID; }
     HIP_TRY(hipSetDevice(st->ctx->device));
     HIP_TRY(run_necks(st, x_device));
     return S3E_OK;
-}
+} S3E_CATCH("s3e_run_neck")
 
-extern "C" int s3e_mem_attn_dims(const s3e_model *m, int32_t out[4]) {
+extern "C" int s3e_mem_attn_dims(const s3e_model *m, int32_t out[4]) try {
     if (!m || !out) { set_error("s3e_mem_attn_dims: NULL argument"); return S3E_ERR_INVALID; }
     if (!m->ma) { set_error("s3e_mem_attn_dims: the model file has no memory attention"); return S3E_ERR_UNSUPPORTED; }
     memattn_dims(m->ma, out);
     return S3E_OK;
-}
+} S3E_CATCH("s3e_mem_attn_dims")
 
 extern "C" int s3e_mem_attn(s3e_state *st, const float *curr, const float *src_pos, int64_t N, const float *prompt,
                             const float *prompt_pos, int64_t M_total, int64_t num_obj_ptr_tokens, const float *rope_q,
-                            const float *rope_k, float *out) {
+                            const float *rope_k, float *out) try {
     if (!st) { set_error("s3e_mem_attn: NULL state"); return S3E_ERR_INVALID; }
     if (!st->m->ma) { set_error("s3e_mem_attn: the model file has no memory attention"); return S3E_ERR_UNSUPPORTED; }
     HIP_TRY(hipSetDevice(st->ctx->device));
     return memattn_run(st->m->ma, &st->mas, curr, src_pos, N, prompt, prompt_pos, M_total, num_obj_ptr_tokens, rope_q,
                        rope_k, out, st->ctx->stream);
-}
+} S3E_CATCH("s3e_mem_attn")
 
-extern "C" int s3e_hiera_block(s3e_state *st, int idx, const float *x_device, int H, int W, float *y_device) {
+extern "C" int s3e_hiera_block(s3e_state *st, int idx, const float *x_device, int H, int W, float *y_device) try {
     if (!st || !x_device || !y_device) { set_error("s3e_hiera_block: NULL argument"); return S3E_ERR_INVALID; }
     if (!st->m->hiera) { set_error("s3e_hiera_block: the model is not a SAM 2 (Hiera) encoder"); return S3E_ERR_INVALID; }
     int32_t hp[16];
@@ -1877,18 +1904,18 @@ extern "C" int s3e_hiera_block(s3e_state *st, int idx, const float *x_device, in
     }
     HIP_TRY(e);
     return S3E_OK;
-}
+} S3E_CATCH("s3e_hiera_block")
 
-extern "C" int s3e_encode_chw_host(s3e_state *st, const float *chw_host) {
+extern "C" int s3e_encode_chw_host(s3e_state *st, const float *chw_host) try {
     if (!st || !chw_host) { set_error("s3e_encode_chw_host: NULL argument"); return S3E_ERR_INVALID; }
     HIP_TRY(hipSetDevice(st->ctx->device));
     HIP_TRY(hipMemcpyAsync(st->chw, chw_host, (size_t)3 * st->m->img * st->m->img * 4, hipMemcpyHostToDevice,
                            st->ctx->stream));
     return s3e_encode_chw(st, st->chw);
-}
+} S3E_CATCH("s3e_encode_chw_host")
 
 extern "C" int s3e_preprocess_image(s3e_ctx *ctx, const uint8_t *hwc_device, int width, int height, int img_size,
-                                    int norm, float *chw_device) {
+                                    int norm, float *chw_device) try {
     if (!ctx || !hwc_device || !chw_device || width <= 0 || height <= 0 || img_size <= 0 ||
         (norm != S3E_NORM_SAM3 && norm != S3E_NORM_IMAGENET)) {
         set_error("s3e_preprocess_image: bad argument");
@@ -1897,12 +1924,12 @@ extern "C" int s3e_preprocess_image(s3e_ctx *ctx, const uint8_t *hwc_device, int
     HIP_TRY(hipSetDevice(ctx->device));
     HIP_TRY(launch_preprocess(hwc_device, width, height, img_size, norm, chw_device, ctx->stream));
     return S3E_OK;
-}
+} S3E_CATCH("s3e_preprocess_image")
 
 // sam3_encode_image's preprocessing (sam3_resize_bilinear +
 // sam3_preprocess_image, sam3.cpp:3441-3514, or sam2_preprocess_image,
 // :3518-3544, for SAM 2 models) on the device, then the encode.
-extern "C" int s3e_encode_image_u8(s3e_state *st, const uint8_t *hwc, int width, int height) {
+extern "C" int s3e_encode_image_u8(s3e_state *st, const uint8_t *hwc, int width, int height) try {
     if (!st || !hwc || width <= 0 || height <= 0) { set_error("s3e_encode_image_u8: bad argument"); return S3E_ERR_INVALID; }
     HIP_TRY(hipSetDevice(st->ctx->device));
     const size_t bytes = (size_t)width * height * 3;
@@ -1920,7 +1947,7 @@ extern "C" int s3e_encode_image_u8(s3e_state *st, const uint8_t *hwc, int width,
     if (rc == S3E_OK) rc = s3e_encode_chw(st, st->chw);
     if (rc != S3E_OK) return rc;
     return s3e_ctx_sync(st->ctx);
-}
+} S3E_CATCH("s3e_encode_image_u8")
 
 namespace {
 
@@ -1955,11 +1982,11 @@ const float *find_tensor(const s3e_state *st, const char *name, int64_t ne[4]) {
 
 }  // namespace
 
-extern "C" int s3e_state_tensor_info(const s3e_state *st, const char *name, int64_t ne[4]) {
+extern "C" int s3e_state_tensor_info(const s3e_state *st, const char *name, int64_t ne[4]) try {
     if (!st || !name || !ne) { set_error("s3e_state_tensor_info: NULL argument"); return S3E_ERR_INVALID; }
     if (!find_tensor(st, name, ne)) { set_error("s3e_state_tensor_info: unknown tensor '%s'", name); return S3E_ERR_INVALID; }
     return S3E_OK;
-}
+} S3E_CATCH("s3e_state_tensor_info")
 
 extern "C" const float *s3e_state_tensor_device(const s3e_state *st, const char *name) {
     int64_t ne[4];
@@ -1967,7 +1994,7 @@ extern "C" const float *s3e_state_tensor_device(const s3e_state *st, const char 
     return find_tensor(st, name, ne);
 }
 
-extern "C" int s3e_state_tensor_get(const s3e_state *st, const char *name, float *host, size_t n) {
+extern "C" int s3e_state_tensor_get(const s3e_state *st, const char *name, float *host, size_t n) try {
     int64_t ne[4];
     if (!st || !name) { set_error("s3e_state_tensor_get: NULL argument"); return S3E_ERR_INVALID; }
     const float *src = find_tensor(st, name, ne);
@@ -1978,4 +2005,4 @@ extern "C" int s3e_state_tensor_get(const s3e_state *st, const char *name, float
     HIP_TRY(hipMemcpyAsync(host, src, need * 4, hipMemcpyDeviceToHost, st->ctx->stream));
     HIP_TRY(hipStreamSynchronize(st->ctx->stream));
     return S3E_OK;
-}
+} S3E_CATCH("s3e_state_tensor_get")

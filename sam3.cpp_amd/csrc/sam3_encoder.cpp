@@ -10,6 +10,7 @@
 // with the same resized bytes).
 #include <cstdio>
 #include <cstring>
+#include <exception>
 #include <fstream>
 #include <new>
 
@@ -34,6 +35,18 @@ struct sam3_state {
     ~sam3_state() { sam3_free_state(*this); }
 };
 
+// Handlers of the function-try-blocks around the sam3.h entry points: no
+// exception (a failed host allocation, a stream error) leaves the library.
+#define SAM3_CATCH(ret)                                                   \
+    catch (const std::exception &ex_) {                                   \
+        fprintf(stderr, "%s: %s\n", __func__, ex_.what());                \
+        return ret;                                                       \
+    }                                                                     \
+    catch (...) {                                                         \
+        fprintf(stderr, "%s: unexpected exception\n", __func__);          \
+        return ret;                                                       \
+    }
+
 namespace {
 
 // hparams slots of s3e_model_hparams
@@ -46,7 +59,7 @@ bool read_magic(const std::string &path, uint32_t *magic) {
 
 }  // namespace
 
-std::shared_ptr<sam3_model> sam3_load_model(const sam3_params &params) {
+std::shared_ptr<sam3_model> sam3_load_model(const sam3_params &params) try {
     if (!params.use_gpu) {
         fprintf(stderr, "%s: this build encodes on the MI355X only (use_gpu = false)\n", __func__);
         return nullptr;
@@ -69,7 +82,7 @@ std::shared_ptr<sam3_model> sam3_load_model(const sam3_params &params) {
         return nullptr;
     }
     return m;
-}
+} SAM3_CATCH(nullptr)
 
 void sam3_free_model(sam3_model &model) {
     if (model.hook) s3e_state_free(model.hook);
@@ -91,7 +104,7 @@ sam3_model_type sam3_get_model_type(const sam3_model &model) {
 
 void sam3_state_deleter::operator()(sam3_state *p) const { delete p; }
 
-sam3_state_ptr sam3_create_state(const sam3_model &model, const sam3_params &params) {
+sam3_state_ptr sam3_create_state(const sam3_model &model, const sam3_params &params) try {
     if (!model.enc) {
         fprintf(stderr, "%s: model is not loaded\n", __func__);
         return nullptr;
@@ -109,14 +122,14 @@ sam3_state_ptr sam3_create_state(const sam3_model &model, const sam3_params &par
         return nullptr;
     }
     return st;
-}
+} SAM3_CATCH(nullptr)
 
 void sam3_free_state(sam3_state &state) {
     if (state.st) s3e_state_free(state.st);
     state.st = nullptr;
 }
 
-bool sam3_encode_image(sam3_state &state, const sam3_model &model, const sam3_image &image) {
+bool sam3_encode_image(sam3_state &state, const sam3_model &model, const sam3_image &image) try {
     if (!state.st || state.model != &model) {
         fprintf(stderr, "%s: state was not created for this model\n", __func__);
         return false;
@@ -133,10 +146,10 @@ bool sam3_encode_image(sam3_state &state, const sam3_model &model, const sam3_im
     }
     state.vit_only = false;
     return true;
-}
+} SAM3_CATCH(false)
 
 bool sam3_encode_image_from_preprocessed(sam3_state &state, const sam3_model &model, const float *chw_data,
-                                         int img_size) {
+                                         int img_size) try {
     if (!state.st || state.model != &model || !chw_data) {
         fprintf(stderr, "%s: bad argument\n", __func__);
         return false;
@@ -151,9 +164,9 @@ bool sam3_encode_image_from_preprocessed(sam3_state &state, const sam3_model &mo
     }
     state.vit_only = false;
     return true;
-}
+} SAM3_CATCH(false)
 
-bool sam3_get_state_tensor_info(const sam3_state &state, const std::string &tensor_name, sam3_tensor_info &info) {
+bool sam3_get_state_tensor_info(const sam3_state &state, const std::string &tensor_name, sam3_tensor_info &info) try {
     int64_t ne[4];
     if (!state.st || (state.vit_only && tensor_name != "vit_output") ||
         s3e_state_tensor_info(state.st, tensor_name.c_str(), ne) != S3E_OK) {
@@ -170,9 +183,9 @@ bool sam3_get_state_tensor_info(const sam3_state &state, const std::string &tens
     info.op = 0;
     info.is_contiguous = true;
     return true;
-}
+} SAM3_CATCH(false)
 
-bool sam3_dump_state_tensor(const sam3_state &state, const std::string &tensor_name, const std::string &output_path) {
+bool sam3_dump_state_tensor(const sam3_state &state, const std::string &tensor_name, const std::string &output_path) try {
     sam3_tensor_info info;
     if (!sam3_get_state_tensor_info(state, tensor_name, info)) return false;
     const size_t n = (size_t)(info.ne[0] * info.ne[1] * info.ne[2] * info.ne[3]);
@@ -205,7 +218,7 @@ bool sam3_dump_state_tensor(const sam3_state &state, const std::string &tensor_n
             (long long)info.ne[0], (long long)info.ne[1], (long long)info.ne[2], (long long)info.ne[3],
             output_path.c_str());
     return true;
-}
+} SAM3_CATCH(false)
 
 // ---- test-only entry points (sam3.h:436-496) --------------------------------
 namespace {
@@ -279,7 +292,7 @@ bool model_tensor(const sam3_model &model, const std::string &name, int want, st
 }  // namespace
 
 bool sam3_encode_vit_from_preprocessed_selective(sam3_state &state, const sam3_model &model, const float *chw_data,
-                                                 int img_size, const std::vector<std::string> &output_tensors) {
+                                                 int img_size, const std::vector<std::string> &output_tensors) try {
     if (!state.st || state.model != &model || !chw_data) {
         fprintf(stderr, "%s: bad argument\n", __func__);
         return false;
@@ -302,10 +315,10 @@ bool sam3_encode_vit_from_preprocessed_selective(sam3_state &state, const sam3_m
     if (d) (void)s3e_free(model.ctx, d);
     if (ok) state.vit_only = true;
     return ok;
-}
+} SAM3_CATCH(false)
 
 bool sam3_test_run_vit_block0_input(const sam3_model &model, const float *chw_data, int img_size,
-                                    std::vector<float> &output_data, int64_t output_ne[4], int n_threads) {
+                                    std::vector<float> &output_data, int64_t output_ne[4], int n_threads) try {
     (void)n_threads;
     if (!chw_data) {
         fprintf(stderr, "%s: chw_data is null\n", __func__);
@@ -335,11 +348,11 @@ bool sam3_test_run_vit_block0_input(const sam3_model &model, const float *chw_da
     if (din) (void)s3e_free(model.ctx, din);
     if (dout) (void)s3e_free(model.ctx, dout);
     return ok;
-}
+} SAM3_CATCH(false)
 
 bool sam3_test_run_vit_prefix_stage(const sam3_model &model, sam3_vit_prefix_stage stage, const float *input_data,
                                     const int64_t input_ne[4], std::vector<float> &output_data, int64_t output_ne[4],
-                                    int n_threads) {
+                                    int n_threads) try {
     (void)n_threads;
     s3e_state *st = hook_state(model, __func__);
     if (!st) return false;
@@ -347,11 +360,11 @@ bool sam3_test_run_vit_prefix_stage(const sam3_model &model, sam3_vit_prefix_sta
                      [&](const float *in, const int64_t *ne, float *out, int64_t *one) {
                          return s3e_vit_prefix_stage(st, (int)stage, in, ne, out, one);
                      });
-}
+} SAM3_CATCH(false)
 
 bool sam3_test_run_vit_block_stage(const sam3_model &model, int block_idx, sam3_vit_block_stage stage,
                                    const float *input_data, const int64_t input_ne[4], std::vector<float> &output_data,
-                                   int64_t output_ne[4], int n_threads) {
+                                   int64_t output_ne[4], int n_threads) try {
     (void)n_threads;
     s3e_state *st = hook_state(model, __func__);
     if (!st) return false;
@@ -359,12 +372,12 @@ bool sam3_test_run_vit_block_stage(const sam3_model &model, int block_idx, sam3_
                      [&](const float *in, const int64_t *ne, float *out, int64_t *one) {
                          return s3e_vit_block_stage(st, block_idx, (int)stage, in, ne, out, one);
                      });
-}
+} SAM3_CATCH(false)
 
 // sam3.cpp:6512-6574: fp16 input and kernel, one f32 (or double) sum per output
 bool sam3_test_run_patch_mulmat_host_ref(const sam3_model &model, const float *input_data, const int64_t input_ne[4],
                                          bool use_double_accum, std::vector<float> &output_data,
-                                         int64_t output_ne[4]) {
+                                         int64_t output_ne[4]) try {
     if (!input_data || !model.enc) return false;
     int64_t ne[4];
     for (int i = 0; i < 4; i++) ne[i] = (input_ne && input_ne[i] > 0) ? input_ne[i] : 1;
@@ -403,12 +416,12 @@ bool sam3_test_run_patch_mulmat_host_ref(const sam3_model &model, const float *i
         }
     }
     return true;
-}
+} SAM3_CATCH(false)
 
 // sam3.cpp:6576-6674: bias + Σ fp16(w)·fp16(x), f32 (or double) accumulation
 bool sam3_test_run_vit_block_linear_host_ref(const sam3_model &model, int block_idx, sam3_vit_block_stage stage,
                                              const float *input_data, const int64_t input_ne[4], bool use_double_accum,
-                                             std::vector<float> &output_data, int64_t output_ne[4]) {
+                                             std::vector<float> &output_data, int64_t output_ne[4]) try {
     if (!input_data || !model.enc || block_idx < 0 || block_idx >= model.hp[3]) return false;
     const char *lin = nullptr;
     switch (stage) {
@@ -460,4 +473,4 @@ bool sam3_test_run_vit_block_linear_host_ref(const sam3_model &model, int block_
         }
     }
     return true;
-}
+} SAM3_CATCH(false)
