@@ -152,24 +152,22 @@ __device__ __forceinline__ void quant_block32_f6(const float *v, uint64_t *base,
     for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(v[j]));
     const float d = amax / 127.f;
     const float id = (amax != 0.f) ? 127.f / amax : 0.f;
-    uint64_t wh[3] = {0, 0, 0}, wl[3] = {0, 0, 0};
+    f32x16 he, ho, le, lo;
 #pragma unroll
-    for (int j = 0; j < 32; j++) {
-        const int q = (int)(__builtin_bit_cast(uint32_t, __fadd_rn(__fmul_rn(v[j], id), 12582912.0f)) - 0x4B400000u);
-        const int h = f6_hi(q);
-        const uint64_t ch = f6_code(h), cl = f6_code(q - 16 * h);
-        const int at = 6 * j;
-        wh[at / 64] |= ch << (at % 64);
-        wl[at / 64] |= cl << (at % 64);
-        if (at % 64 > 58) {
-            wh[at / 64 + 1] |= ch >> (64 - at % 64);
-            wl[at / 64 + 1] |= cl >> (64 - at % 64);
-        }
+    for (int i = 0; i < 16; i++) {
+        float a, b, c, e;
+        f6_split(v[2 * i], id, a, b);
+        f6_split(v[2 * i + 1], id, c, e);
+        he[i] = a;
+        le[i] = b;
+        ho[i] = c;
+        lo[i] = e;
     }
+    const u32x6 ph = pack_bf6(he, ho), pl = pack_bf6(le, lo);
 #pragma unroll
     for (int t = 0; t < 3; t++) {
-        base[f6_act_word(nst, row, blk, 0, t)] = wh[t];
-        base[f6_act_word(nst, row, blk, 1, t)] = wl[t];
+        base[f6_act_word(nst, row, blk, 0, t)] = (uint64_t)ph[2 * t] | ((uint64_t)ph[2 * t + 1] << 32);
+        base[f6_act_word(nst, row, blk, 1, t)] = (uint64_t)pl[2 * t] | ((uint64_t)pl[2 * t + 1] << 32);
     }
     *ddst = f2h_bits(d);
 }

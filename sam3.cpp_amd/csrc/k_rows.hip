@@ -167,6 +167,112 @@ __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ x, 
     }
 }
 
+// LayerNorm straight into A_F6 (E % 128 == 0): one wave per row, lane L
+// holding the 16 consecutive values [16·(L + 64·it), +16), i.e. half L & 1 of
+// one 32-element block.  Each lane converts its half with the fp6 pack
+// instruction (its 16 codes are 96 contiguous bits of the block's 192-bit
+// string) and stores it; only the block maximum crosses lanes.  The same
+// statistics and per-element operations as k_layernorm, so the same codes.
+template <int NIT>
+__global__ __launch_bounds__(256) void k_layernorm_f6(const float *__restrict__ x, int64_t M, int64_t E,
+                                                      float eps, const float *__restrict__ w,
+                                                      const float *__restrict__ b, Act o) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M) return;
+    const int nseg = (int)(E / 16);
+    const float4 *xr = (const float4 *)(x + row * E);
+    float v[NIT][16];
+#pragma unroll
+    for (int it = 0; it < NIT; it++) {
+        const int seg = lane + 64 * it;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float4 q = (seg < nseg) ? xr[4 * seg + j] : make_float4(0.f, 0.f, 0.f, 0.f);
+            v[it][4 * j] = q.x; v[it][4 * j + 1] = q.y; v[it][4 * j + 2] = q.z; v[it][4 * j + 3] = q.w;
+        }
+    }
+    double s = 0.0;
+#pragma unroll
+    for (int it = 0; it < NIT; it++)
+#pragma unroll
+        for (int j = 0; j < 16; j++) s += (double)v[it][j];
+    s = wave_sum_d(s);
+    const float mean = (float)(s / (double)E);
+    double s2 = 0.0;
+#pragma unroll
+    for (int it = 0; it < NIT; it++) {
+        const bool ok = lane + 64 * it < nseg;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const float c = __fsub_rn(v[it][j], mean);
+            v[it][j] = c;
+            if (ok) s2 += (double)__fmul_rn(c, c);
+        }
+    }
+    s2 = wave_sum_d(s2);
+    const float var = (float)(s2 / (double)E);
+    const float scale = 1.0f / sqrtf(var + eps);
+    uint64_t *o64 = (uint64_t *)o.x;
+    uint32_t *o32 = (uint32_t *)o.x;
+    const int64_t nst = o.ld / 128;
+#pragma unroll
+    for (int it = 0; it < NIT; it++) {
+        const int seg = lane + 64 * it;
+        if (64 * it >= nseg) break;  // whole wave past the row
+        // both lanes of a block are inside the row or both past it (nseg is even)
+        if (seg >= nseg) continue;
+        float amax = 0.f;
+#pragma unroll
+        for (int j4 = 0; j4 < 4; j4++) {
+            const float4 wf = w ? ((const float4 *)w)[4 * seg + j4] : make_float4(1.f, 1.f, 1.f, 1.f);
+            const float4 bf = b ? ((const float4 *)b)[4 * seg + j4] : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float wv[4] = {wf.x, wf.y, wf.z, wf.w}, bv[4] = {bf.x, bf.y, bf.z, bf.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                float t = __fmul_rn(v[it][4 * j4 + j], scale);
+                if (w) t = __fmul_rn(t, wv[j]);
+                if (b) t = __fadd_rn(t, bv[j]);
+                v[it][4 * j4 + j] = t;
+                amax = fmaxf(amax, fabsf(t));
+            }
+        }
+        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+        const float id = (amax != 0.f) ? 127.f / amax : 0.f;
+        f32x16 he = {}, ho = {}, le = {}, lo = {};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float a, c, e, g;
+            f6_split(v[it][2 * i], id, a, c);
+            f6_split(v[it][2 * i + 1], id, e, g);
+            he[i] = a;
+            le[i] = c;
+            ho[i] = e;
+            lo[i] = g;
+        }
+        const u32x6 ph = pack_bf6(he, ho), pl = pack_bf6(le, lo);
+        const int64_t blk = seg >> 1;
+        const int64_t h0 = f6_act_word(nst, row, blk, 0, 0), h1 = f6_act_word(nst, row, blk, 0, 1),
+                      h2 = f6_act_word(nst, row, blk, 0, 2);
+        const int64_t l0 = f6_act_word(nst, row, blk, 1, 0), l1 = f6_act_word(nst, row, blk, 1, 1),
+                      l2 = f6_act_word(nst, row, blk, 1, 2);
+        if ((seg & 1) == 0) {
+            // bits [0, 96) of the block string: word 0 and the low half of word 1
+            o64[h0] = (uint64_t)ph[0] | ((uint64_t)ph[1] << 32);
+            o32[2 * h1] = ph[2];
+            o64[l0] = (uint64_t)pl[0] | ((uint64_t)pl[1] << 32);
+            o32[2 * l1] = pl[2];
+            o.d[scale_index(o.mp, row, blk)] = f2h_bits(amax / 127.f);
+        } else {
+            // bits [96, 192): the high half of word 1 and word 2
+            o32[2 * h1 + 1] = ph[0];
+            o64[h2] = (uint64_t)ph[1] | ((uint64_t)ph[2] << 32);
+            o32[2 * l1 + 1] = pl[0];
+            o64[l2] = (uint64_t)pl[1] | ((uint64_t)pl[2] << 32);
+        }
+    }
+}
+
 // Plain conversion of f32 rows into an activation format (ggml from_float):
 // lane L of a wave converts float4 number 64·blockIdx.x + L of its row.
 __global__ __launch_bounds__(256) void k_rows_quant(const float *__restrict__ x, int64_t M, int64_t K, Act o) {
@@ -283,6 +389,12 @@ hipError_t launch_layernorm(const float *x, int64_t M, int64_t E, float eps, con
     const bool f6 = !y_f32 && out.kind == A_F6;
     if (E % 4 != 0 || E > 4096 || (q8 && E % 32 != 0) || (f6 && (E % 128 != 0 || out.ld != E))) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((M + 3) / 4));
+    if (f6) {
+        if (E <= 1024) hipLaunchKernelGGL(k_layernorm_f6<1>, grid, dim3(256), 0, st, x, M, E, eps, w, b, out);
+        else if (E <= 2048) hipLaunchKernelGGL(k_layernorm_f6<2>, grid, dim3(256), 0, st, x, M, E, eps, w, b, out);
+        else hipLaunchKernelGGL(k_layernorm_f6<4>, grid, dim3(256), 0, st, x, M, E, eps, w, b, out);
+        return hipGetLastError();
+    }
     if (E <= 256) hipLaunchKernelGGL(k_layernorm<1>, grid, dim3(256), 0, st, x, M, E, eps, w, b, out, y_f32);
     else if (E <= 512) hipLaunchKernelGGL(k_layernorm<2>, grid, dim3(256), 0, st, x, M, E, eps, w, b, out, y_f32);
     else if (E <= 1024) hipLaunchKernelGGL(k_layernorm<4>, grid, dim3(256), 0, st, x, M, E, eps, w, b, out, y_f32);

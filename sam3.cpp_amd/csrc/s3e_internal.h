@@ -371,6 +371,31 @@ __device__ __forceinline__ float gelu_erf(float x) {
     return 0.5f * x * w;
 }
 
+// ---- fp6 (E3M2) operand strings on the device ----
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x6 __attribute__((ext_vector_type(6)));
+
+// The E3M2 codes of 32 small integers (|v| ≤ 8, exact in E3M2) as the 192-bit
+// operand string, code j in bits [6j, 6j + 6): v_cvt_scalef32_2xpk16_bf6_f32
+// fills slot 2i from even[i] and slot 2i + 1 from odd[i] (so even / odd are
+// the block's even- and odd-indexed values), dividing by the scale (1 here).
+// Written as asm with an early-clobber result: through the builtin the
+// compiler may give the result registers that overlap the inputs, and the
+// instruction then reads inputs it has already overwritten.
+__device__ __forceinline__ u32x6 pack_bf6(const f32x16 &even, const f32x16 &odd) {
+    u32x6 r;
+    __asm__("v_cvt_scalef32_2xpk16_bf6_f32 %0, %1, %2, %3" : "=&v"(r) : "v"(even), "v"(odd), "v"(1.0f));
+    return r;
+}
+
+// q = round-half-even(v·id) as a float, split q = 16·h + l with
+// h = ⌊(q + 8) / 16⌋, l = q − 16·h (f6_hi); every step is exact.
+__device__ __forceinline__ void f6_split(float v, float id, float &h, float &l) {
+    const float q = __builtin_rintf(v * id);
+    h = __builtin_floorf((q + 8.f) * 0.0625f);
+    l = __builtin_fmaf(-16.f, h, q);
+}
+
 // 16 / 8 bytes loaded through a global-address-space pointer.  A pointer the
 // compiler cannot place (one read from memory rather than a kernel argument)
 // makes a flat load, which may address LDS, so behind LDS DMA the compiler
