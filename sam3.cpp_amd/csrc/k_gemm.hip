@@ -6,13 +6,16 @@
 // each 32-element block b the kernel forms the exact integer sum
 //     S_b[m][n] = Σ_{k∈b} qx[m][k]·qw[n][k]
 // with one v_mfma_i32_32x32x32_i8 (K = 32 = one ggml block), the exact fp32
-// block scale 2·dx[m][b]·dw[n][b] with one v_mfma_f32_32x32x16_f16 whose
+// block scale 2·dx[m][b]·dw[n][b] with one v_mfma_f32_32x32x8_f16 whose
 // operands hold each lane's own scale in its first K slot and zeros elsewhere
 // (both lane halves carry the scale, hence the exact factor 2, removed at the
-// end), and accumulates acc += float(S_b)·c_b in fp32 on the VALU.  Q4_1 adds
-// Σ_b m_w[n][b]·s_x[m][b] with one more fp16 MFMA per 4 blocks into its own
-// accumulator.  F16 weights run on fp16 MFMA against activations rounded to
-// fp16; F32 weights run on fp32 MFMA.
+// end; the K = 8 form issues faster than K = 16 and the product needs one
+// slot), and accumulates acc += float(S_b)·c_b in fp32 on the VALU.  Q4_1
+// adds Σ_b m_w[n][b]·s_x[m][b] with one more fp16 MFMA per 4 blocks into its
+// own accumulator.  Q4_0 weights with an fp6 copy run in k_gemm_f6 (below),
+// where the block sum comes out of the fp6 MFMA already in fp32.  F16
+// weights run on fp16 MFMA against activations rounded to fp16; F32 weights
+// run on fp32 MFMA.
 //
 // Per work-group: a 64×128 output tile and 4 waves (2 along M × 2 along N,
 // each 32×64; three work-groups per CU) or, for Q4_1, 8 waves (2 × 4, each
@@ -45,6 +48,8 @@ typedef uint64_t v4u64 __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
 #define LDS_PTR(p) ((__attribute__((address_space(3))) void *)(p))
@@ -660,13 +665,13 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 3 : 256 / BM) void k_gemm(
         const v16f zf = {};
 #pragma unroll
         for (int n = 0; n < NT; n++) {
-            const v4u hb = {f.db[n], 0u, 0u, 0u};
+            const v2u hb = {f.db[n], 0u};
 #pragma unroll
             for (int i = 0; i < MT; i++) {
-                const v4u ha = {f.da[i], 0u, 0u, 0u};
+                const v2u ha = {f.da[i], 0u};
                 S[i][n] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[i], f.b[n], zi, 0, 0, 0);
-                Cs[i][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, ha),
-                                                                  __builtin_bit_cast(v8h, hb), zf, 0, 0, 0);
+                Cs[i][n] = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, ha), __builtin_bit_cast(v4h, hb),
+                                                                zf, 0, 0, 0);
             }
         }
     };
@@ -716,13 +721,13 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 3 : 256 / BM) void k_gemm(
 #pragma unroll
                 for (int n = 0; n < NT; n++) {
                     const uint2 mb = lds_u2(L + C::OFF_BMIN + bd_off[n]);
-                    const v4u hb = {mb.x, mb.y, 0u, 0u};
+                    const v2u hb = {mb.x, mb.y};
 #pragma unroll
                     for (int i = 0; i < MT; i++) {
                         const uint2 sa = lds_u2(L + C::OFF_AS + ad_off[i]);
-                        const v4u ha = {sa.x, sa.y, 0u, 0u};
-                        accm[i][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                            __builtin_bit_cast(v8h, ha), __builtin_bit_cast(v8h, hb), accm[i][n], 0, 0, 0);
+                        const v2u ha = {sa.x, sa.y};
+                        accm[i][n] = __builtin_amdgcn_mfma_f32_32x32x8f16(
+                            __builtin_bit_cast(v4h, ha), __builtin_bit_cast(v4h, hb), accm[i][n], 0, 0, 0);
                     }
                 }
             }
@@ -910,18 +915,12 @@ __global__ __launch_bounds__(256, 3) void k_gemm_f6(GemmParams p) {
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[n][r] = 0.f;
 
-    // scale products: the A operand carries the stage's four row scales in
-    // K slots 0-3 (one 8-byte read per stage), the B operand of block b only
-    // its column scale in slot b, so the product is dx[b]·dw[b]; the unused
-    // slots stay zero in registers kept across blocks (slots 0-1 and 2-3 are
-    // separate operands)
-    v4u ha = {0u, 0u, 0u, 0u};
-    v4u hb01[NT], hb23[NT];
-#pragma unroll
-    for (int n = 0; n < NT; n++) {
-        hb01[n] = v4u{0u, 0u, 0u, 0u};
-        hb23[n] = v4u{0u, 0u, 0u, 0u};
-    }
+    // scale products on the fp16 MFMA (32×32×8): the A operand carries the
+    // stage's four row scales in K slots 0-3 (one 8-byte read per stage; the
+    // other lane half holds slots 4-7, the same values), the B operand of
+    // block b only its column scale in slots b and 4 + b, so the product is
+    // 2·dx[b]·dw[b]
+    v2u ha = {0u, 0u};
     struct Ops {
         v8i a, b[NT];
     };
@@ -959,12 +958,10 @@ __global__ __launch_bounds__(256, 3) void k_gemm_f6(GemmParams p) {
             for (int n = 0; n < NT; n++) {
                 const uint32_t w = blk < 2 ? sb[n].x : sb[n].y;
                 const uint32_t m = (blk & 1) ? (w & 0xFFFF0000u) : (w & 0xFFFFu);
-                if (blk < 2) hb01[n][0] = m;
-                else hb23[n][1] = m;
+                const v2u hb = blk < 2 ? v2u{m, 0u} : v2u{0u, m};
                 S[n] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(cur.a, cur.b[n], zf, 3, 3, 0, a_scale, 0, 127);
-                Cs[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, ha),
-                                                              __builtin_bit_cast(v8h, blk < 2 ? hb01[n] : hb23[n]),
-                                                              zf, 0, 0, 0);
+                Cs[n] = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, ha), __builtin_bit_cast(v4h, hb),
+                                                             zf, 0, 0, 0);
             }
 #pragma unroll
             for (int n = 0; n < NT; n++)
