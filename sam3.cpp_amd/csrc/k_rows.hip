@@ -9,9 +9,31 @@ namespace {
 
 __device__ __forceinline__ uint16_t f2h_bits(float v) { return half_bits(v); }
 
+// A double moved by a DPP pattern within 16-lane rows (both 32-bit halves).
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xF, 0xF, false);
+    return __builtin_bit_cast(double, (uint64_t)lo | ((uint64_t)hi << 32));
+}
+__device__ __forceinline__ double swz16_d(double v) {  // lane ^ 16 within each 32-lane half
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_swizzle((int)(uint32_t)u, 0x401F);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_swizzle((int)(uint32_t)(u >> 32), 0x401F);
+    return __builtin_bit_cast(double, (uint64_t)lo | ((uint64_t)hi << 32));
+}
+
+// Sum over the wave's 64 lanes, in every lane: DPP within rows of 16 (quad
+// xor 1, quad xor 2, half-row mirror, row mirror), a swizzle across the rows
+// of each half, a permute across the halves.  Only the last two wait on LDS.
 __device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    v += dpp_d<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_d<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_d<0x141>(v);  // row_half_mirror
+    v += dpp_d<0x140>(v);  // row_mirror
+    v += swz16_d(v);
+    v += __shfl_xor(v, 32, 64);
     return v;
 }
 
@@ -167,109 +189,168 @@ __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ x, 
     }
 }
 
-// LayerNorm straight into A_F6 (E % 128 == 0): one wave per row, lane L
-// holding the 16 consecutive values [16·(L + 64·it), +16), i.e. half L & 1 of
-// one 32-element block.  Each lane converts its half with the fp6 pack
-// instruction (its 16 codes are 96 contiguous bits of the block's 192-bit
-// string) and stores it; only the block maximum crosses lanes.  The same
-// statistics and per-element operations as k_layernorm, so the same codes.
-template <int NIT>
+// LayerNorm straight into A_F6 (E % 128 == 0, E ≤ 1024·NIT): a work-group
+// normalizes 16 consecutive rows (each wave 4 of them, the next row's values
+// loaded while one is converted), lane L of a wave holding the 16 consecutive
+// values [16·(L + 64·it), +16), half L & 1 of one 32-element block.  Each
+// lane converts its half with one fp6 pack instruction (h codes in slots
+// 0-15, l codes in 16-31) and leaves its bits in LDS in the output's order;
+// the work-group then writes every (block, part, word) run of its 16 rows
+// (128 contiguous bytes in A_F6) and every stage's 16 rows of block scales
+// as whole lines.  The same statistics and per-element operations as
+// k_layernorm, so the same codes.
+constexpr int LNF6_ROWS = 16;
+constexpr int LNF6_BSTRIDE = 98;  // 8-byte LDS words per block: 6 runs of 16 rows, padded (bank spread, 16 B aligned)
+
+template <int NIT, bool WB>
 __global__ __launch_bounds__(256) void k_layernorm_f6(const float *__restrict__ x, int64_t M, int64_t E,
                                                       float eps, const float *__restrict__ w,
                                                       const float *__restrict__ b, Act o) {
-    const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= M) return;
-    const int nseg = (int)(E / 16);
-    const float4 *xr = (const float4 *)(x + row * E);
-    float v[NIT][16];
+    __shared__ __attribute__((aligned(16))) uint64_t stg[32 * NIT * LNF6_BSTRIDE];
+    __shared__ __attribute__((aligned(16))) uint16_t stgd[8 * NIT][LNF6_ROWS][4];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nseg = (int)(E / 16), nblk = (int)(E / 32);
+    const int64_t r0 = (int64_t)blockIdx.x * LNF6_ROWS;
+    uint32_t *stg32 = (uint32_t *)stg;
+    // pairwise sums in double (exact enough that the order never shows in
+    // the float results)
+    auto dsum16 = [](const float *a) {
+        double t[8];
 #pragma unroll
-    for (int it = 0; it < NIT; it++) {
-        const int seg = lane + 64 * it;
+        for (int j = 0; j < 8; j++) t[j] = (double)a[2 * j] + (double)a[2 * j + 1];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const float4 q = (seg < nseg) ? xr[4 * seg + j] : make_float4(0.f, 0.f, 0.f, 0.f);
-            v[it][4 * j] = q.x; v[it][4 * j + 1] = q.y; v[it][4 * j + 2] = q.z; v[it][4 * j + 3] = q.w;
-        }
-    }
-    double s = 0.0;
+        for (int j = 0; j < 4; j++) t[j] += t[j + 4];
+        return (t[0] + t[2]) + (t[1] + t[3]);
+    };
+    float nx[NIT][16];
+    auto load_row = [&](int64_t r) {
+        const float4 *xr = (const float4 *)(x + r * E);
 #pragma unroll
-    for (int it = 0; it < NIT; it++)
+        for (int it = 0; it < NIT; it++) {
+            const int seg = lane + 64 * it;
+            if (seg < nseg) {
 #pragma unroll
-        for (int j = 0; j < 16; j++) s += (double)v[it][j];
-    s = wave_sum_d(s);
-    const float mean = (float)(s / (double)E);
-    double s2 = 0.0;
+                for (int j = 0; j < 4; j++) {
+                    const float4 q = xr[4 * seg + j];
+                    nx[it][4 * j] = q.x; nx[it][4 * j + 1] = q.y; nx[it][4 * j + 2] = q.z; nx[it][4 * j + 3] = q.w;
+                }
+            } else {
 #pragma unroll
-    for (int it = 0; it < NIT; it++) {
-        const bool ok = lane + 64 * it < nseg;
-#pragma unroll
-        for (int j = 0; j < 16; j++) {
-            const float c = __fsub_rn(v[it][j], mean);
-            v[it][j] = c;
-            if (ok) s2 += (double)__fmul_rn(c, c);
-        }
-    }
-    s2 = wave_sum_d(s2);
-    const float var = (float)(s2 / (double)E);
-    const float scale = 1.0f / sqrtf(var + eps);
-    uint64_t *o64 = (uint64_t *)o.x;
-    uint32_t *o32 = (uint32_t *)o.x;
-    const int64_t nst = o.ld / 128;
-#pragma unroll
-    for (int it = 0; it < NIT; it++) {
-        const int seg = lane + 64 * it;
-        if (64 * it >= nseg) break;  // whole wave past the row
-        // both lanes of a block are inside the row or both past it (nseg is even)
-        if (seg >= nseg) continue;
-        float amax = 0.f;
-#pragma unroll
-        for (int j4 = 0; j4 < 4; j4++) {
-            const float4 wf = w ? ((const float4 *)w)[4 * seg + j4] : make_float4(1.f, 1.f, 1.f, 1.f);
-            const float4 bf = b ? ((const float4 *)b)[4 * seg + j4] : make_float4(0.f, 0.f, 0.f, 0.f);
-            const float wv[4] = {wf.x, wf.y, wf.z, wf.w}, bv[4] = {bf.x, bf.y, bf.z, bf.w};
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                float t = __fmul_rn(v[it][4 * j4 + j], scale);
-                if (w) t = __fmul_rn(t, wv[j]);
-                if (b) t = __fadd_rn(t, bv[j]);
-                v[it][4 * j4 + j] = t;
-                amax = fmaxf(amax, fabsf(t));
+                for (int j = 0; j < 16; j++) nx[it][j] = 0.f;
             }
         }
-        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-        const float id = (amax != 0.f) ? 127.f / amax : 0.f;
-        f32x16 he = {}, ho = {}, le = {}, lo = {};
+    };
+    constexpr int RPW = LNF6_ROWS / 4;  // rows per wave
+    if (r0 + wave * RPW < M) load_row(r0 + wave * RPW);
+    for (int k = 0; k < RPW; k++) {
+        const int rr = wave * RPW + k;  // row within the group
+        const int64_t row = r0 + rr;
+        if (row >= M) break;
+        float v[NIT][16];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            float a, c, e, g;
-            f6_split(v[it][2 * i], id, a, c);
-            f6_split(v[it][2 * i + 1], id, e, g);
-            he[i] = a;
-            le[i] = c;
-            ho[i] = e;
-            lo[i] = g;
+        for (int it = 0; it < NIT; it++)
+#pragma unroll
+            for (int j = 0; j < 16; j++) v[it][j] = nx[it][j];
+        if (k + 1 < RPW && row + 1 < M) load_row(row + 1);
+        double s = 0.0;
+#pragma unroll
+        for (int it = 0; it < NIT; it++) s += dsum16(v[it]);
+        s = wave_sum_d(s);
+        const float mean = (float)(s / (double)E);
+        double s2 = 0.0;
+#pragma unroll
+        for (int it = 0; it < NIT; it++) {
+            float sq[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const float c = __fsub_rn(v[it][j], mean);
+                v[it][j] = c;
+                sq[j] = __fmul_rn(c, c);
+            }
+            if (lane + 64 * it < nseg) s2 += dsum16(sq);
         }
-        const u32x6 ph = pack_bf6(he, ho), pl = pack_bf6(le, lo);
-        const int64_t blk = seg >> 1;
-        const int64_t h0 = f6_act_word(nst, row, blk, 0, 0), h1 = f6_act_word(nst, row, blk, 0, 1),
-                      h2 = f6_act_word(nst, row, blk, 0, 2);
-        const int64_t l0 = f6_act_word(nst, row, blk, 1, 0), l1 = f6_act_word(nst, row, blk, 1, 1),
-                      l2 = f6_act_word(nst, row, blk, 1, 2);
-        if ((seg & 1) == 0) {
-            // bits [0, 96) of the block string: word 0 and the low half of word 1
-            o64[h0] = (uint64_t)ph[0] | ((uint64_t)ph[1] << 32);
-            o32[2 * h1] = ph[2];
-            o64[l0] = (uint64_t)pl[0] | ((uint64_t)pl[1] << 32);
-            o32[2 * l1] = pl[2];
-            o.d[scale_index(o.mp, row, blk)] = f2h_bits(amax / 127.f);
-        } else {
-            // bits [96, 192): the high half of word 1 and word 2
-            o32[2 * h1 + 1] = ph[0];
-            o64[h2] = (uint64_t)ph[1] | ((uint64_t)ph[2] << 32);
-            o32[2 * l1 + 1] = pl[0];
-            o64[l2] = (uint64_t)pl[1] | ((uint64_t)pl[2] << 32);
+        s2 = wave_sum_d(s2);
+        const float var = (float)(s2 / (double)E);
+        const float scale = 1.0f / sqrtf(var + eps);
+#pragma unroll
+        for (int it = 0; it < NIT; it++) {
+            const int seg = lane + 64 * it;
+            if (64 * it >= nseg) break;  // whole wave past the row
+            // both lanes of a block are inside the row or both past it (nseg is even)
+            if (seg >= nseg) continue;
+            float amax = 0.f;
+#pragma unroll
+            for (int j4 = 0; j4 < 4; j4++) {
+                float wv[4] = {1.f, 1.f, 1.f, 1.f}, bv[4] = {0.f, 0.f, 0.f, 0.f};
+                if constexpr (WB) {
+                    const float4 wf = ((const float4 *)w)[4 * seg + j4];
+                    const float4 bf = ((const float4 *)b)[4 * seg + j4];
+                    wv[0] = wf.x; wv[1] = wf.y; wv[2] = wf.z; wv[3] = wf.w;
+                    bv[0] = bf.x; bv[1] = bf.y; bv[2] = bf.z; bv[3] = bf.w;
+                }
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    float t = __fmul_rn(v[it][4 * j4 + j], scale);
+                    if constexpr (WB) t = __fadd_rn(__fmul_rn(t, wv[j]), bv[j]);
+                    v[it][4 * j4 + j] = t;
+                    amax = fmaxf(amax, fabsf(t));
+                }
+            }
+            amax = fmaxf(amax, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                                              0, __builtin_bit_cast(int, amax), 0xB1, 0xF, 0xF, false)));
+            const float id = (amax != 0.f) ? 127.f / amax : 0.f;
+            // one conversion for both parts: slots 0-15 take this lane's h
+            // codes, slots 16-31 its l codes, so result dwords 0-2 are its 96
+            // bits of the h string and dwords 3-5 its 96 bits of the l string
+            f32x16 ev, od;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                float a, c, e, g;
+                f6_split(v[it][2 * i], id, a, c);
+                f6_split(v[it][2 * i + 1], id, e, g);
+                ev[i] = a;
+                od[i] = e;
+                ev[8 + i] = c;
+                od[8 + i] = g;
+            }
+            const u32x6 r6 = pack_bf6(ev, od);
+            const int blk = seg >> 1;
+            // LDS word of (block, part p, word t, row rr): blk·98 + (3p + t)·16 + rr
+            const int wb = blk * LNF6_BSTRIDE + rr;
+            if ((seg & 1) == 0) {
+                // bits [0, 96) of the block string: word 0 and the low half of word 1
+                stg[wb] = (uint64_t)r6[0] | ((uint64_t)r6[1] << 32);
+                stg32[2 * (wb + 16)] = r6[2];
+                stg[wb + 48] = (uint64_t)r6[3] | ((uint64_t)r6[4] << 32);
+                stg32[2 * (wb + 64)] = r6[5];
+                stgd[blk >> 2][rr][blk & 3] = f2h_bits(amax / 127.f);
+            } else {
+                // bits [96, 192): the high half of word 1 and word 2
+                stg32[2 * (wb + 16) + 1] = r6[0];
+                stg[wb + 32] = (uint64_t)r6[1] | ((uint64_t)r6[2] << 32);
+                stg32[2 * (wb + 64) + 1] = r6[3];
+                stg[wb + 80] = (uint64_t)r6[4] | ((uint64_t)r6[5] << 32);
+            }
         }
+    }
+    __syncthreads();
+    // (block, part, word) runs: 16 rows × 8 bytes at f6_act_word(.., r0, ..);
+    // 16-byte pieces of rows 2q, 2q + 1 (rows past M land in the padded rows
+    // of the 64-row tile, which no product stores)
+    const int64_t nst = o.ld / 128;
+    const int npieces = nblk * 6 * 8;
+    for (int pc = threadIdx.x; pc < npieces; pc += 256) {
+        const int run = pc >> 3, q = pc & 7;
+        const int blk = run / 6, pt = run % 6;
+        if (r0 + 2 * q >= M) continue;
+        const uint4 val = *(const uint4 *)(stg + blk * LNF6_BSTRIDE + pt * 16 + 2 * q);
+        *(uint4 *)((uint64_t *)o.x + f6_act_word(nst, r0, blk, pt / 3, pt % 3) + 2 * q) = val;
+    }
+    // block scales: per stage, 16 rows × 4 fp16 = 128 contiguous bytes
+    for (int pc = threadIdx.x; pc < (nblk / 4) * 8; pc += 256) {
+        const int sg = pc >> 3, q = pc & 7;
+        if (r0 + 2 * q >= M) continue;
+        *(uint4 *)(o.d + scale_index(o.mp, r0 + 2 * q, 4 * sg)) = *(const uint4 *)&stgd[sg][2 * q][0];
     }
 }
 
@@ -389,10 +470,12 @@ hipError_t launch_layernorm(const float *x, int64_t M, int64_t E, float eps, con
     const bool f6 = !y_f32 && out.kind == A_F6;
     if (E % 4 != 0 || E > 4096 || (q8 && E % 32 != 0) || (f6 && (E % 128 != 0 || out.ld != E))) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((M + 3) / 4));
-    if (f6) {
-        if (E <= 1024) hipLaunchKernelGGL(k_layernorm_f6<1>, grid, dim3(256), 0, st, x, M, E, eps, w, b, out);
-        else if (E <= 2048) hipLaunchKernelGGL(k_layernorm_f6<2>, grid, dim3(256), 0, st, x, M, E, eps, w, b, out);
-        else hipLaunchKernelGGL(k_layernorm_f6<4>, grid, dim3(256), 0, st, x, M, E, eps, w, b, out);
+    if (f6 && E <= 1024 && (w != nullptr) == (b != nullptr)) {
+        // rows of up to 1024 (the ViT's); the ViT's norms carry both gamma and
+        // beta (sam3_layer_norm, sam3.cpp:1037-1046)
+        const dim3 gf((unsigned)((M + LNF6_ROWS - 1) / LNF6_ROWS));
+        if (w) hipLaunchKernelGGL((k_layernorm_f6<1, true>), gf, dim3(256), 0, st, x, M, E, eps, w, b, out);
+        else hipLaunchKernelGGL((k_layernorm_f6<1, false>), gf, dim3(256), 0, st, x, M, E, eps, w, b, out);
         return hipGetLastError();
     }
     if (E <= 256) hipLaunchKernelGGL(k_layernorm<1>, grid, dim3(256), 0, st, x, M, E, eps, w, b, out, y_f32);
