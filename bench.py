@@ -14,12 +14,21 @@ breakdown.neck_ms.
 
 Also reported, on the same JSON line:
   roofline      — the dominant kernel (the fc1 GEMM, M=5184 N=4736 K=1024,
-                  the largest of the four per-block GEMMs) timed alone with
-                  HIP events on the engine's stream: algorithmic ops 2·M·N·K
-                  per launch ÷ average launch time, against the MI355X dense
-                  int8 MFMA peak (fp16 for F16 weights, fp32 for F32).
-                  `traffic` comes from the committed rocprofv3 FETCH_SIZE /
-                  WRITE_SIZE counter summary when present.
+                  the largest of the four per-block GEMMs, on the kernel the
+                  encoder runs for the weight type: the fp6 kernel for Q4_0)
+                  timed alone with HIP events on the engine's stream:
+                  algorithmic ops 2·M·N·K per launch ÷ average launch time,
+                  against the MI355X dense int8 MFMA peak (fp16 for F16
+                  weights, fp32 for F32).  `traffic` comes from the committed
+                  rocprofv3 FETCH_SIZE / WRITE_SIZE counter summary when
+                  present.
+  c4_other_weights — the same 1008 px encoder with Q8_0 and F16 linear
+                  weights (the other two weight types of the workload), ms
+                  per frame.
+  attention_fp16 — the ViT attention at F16 precision (fp16 operands, fp32
+                  accumulation): 16 heads of 64 over 9 windows of 576 tokens
+                  and over the 5184-token global grid, µs per call, TFLOP/s
+                  and the fraction of the fp16 dense peak.
   small_m       — weight streaming at M = 64 rows (the C2 small-M shapes):
                   fc1 and fc2 alone, and all four ViT linears of 64 distinct
                   layers in one batched launch, as algorithmic GB/s against
@@ -34,8 +43,10 @@ Also reported, on the same JSON line:
                   s3e_encode_image_u8 call against the resident encode.
   cpu_baseline  — the CPU oracle (a C restatement of ggml's CPU path, not
                   the upstream binary) on this host: one whole frame of the
-                  same model and image, backbone and neck (about 12 s on 16
-                  host threads).
+                  same model and image, backbone and neck, on every core the
+                  job may use (OMP_NUM_THREADS where the host sets the job's
+                  CPU share, else all cores the process can run on; about
+                  11 s on 16 threads).
 """
 from __future__ import annotations
 
@@ -56,7 +67,7 @@ METRIC = "image-encoder ms/frame (SAM3 ViT 1008², q4_0/q8_0/f16) + % MFMA/HBM p
 PEAK_TOPS = {"q4_0": 5000.0, "q4_1": 5000.0, "q8_0": 5000.0, "f16": 2500.0, "f32": 157.3}
 CFG = dict(img_size=1008, patch=14, embed_dim=1024, depth=32, heads=16, mlp_ratio_x1000=4625, window=24,
            global_idx=(7, 15, 23, 31))
-GEMM_KERNEL = "k_gemm"
+GEMM_KERNEL = {"q4_0": "k_gemm_f6", "q4_1": "k_gemm", "q8_0": "k_gemm", "f16": "k_gemm", "f32": "k_gemm"}
 SAM2_RUNS = [("hiera_t", "f16"), ("hiera_b+", "q8_0")]
 
 
@@ -91,7 +102,9 @@ def read_traffic(path: str):
 
 
 def gemm_roofline(s3e, ctx, ev, ftype: str, reps: int):
-    """Time the fc1 GEMM kernel alone (s3e_mul_mat_q on pre-converted activations)."""
+    """Time the fc1 GEMM kernel alone on pre-converted activations: for Q4_0
+    the fp6 kernel the encoder runs (s3e_mul_mat_q_f6 on S3E_TYPE_Q8_0_F6X2),
+    otherwise s3e_mul_mat_q."""
     M, N, K = 5184, 4736, 1024
     rng = np.random.default_rng(1)
     tmap = {"q4_0": s3e.TYPE_Q4_0, "q4_1": s3e.TYPE_Q4_1, "q8_0": s3e.TYPE_Q8_0, "f16": s3e.TYPE_F16,
@@ -101,7 +114,13 @@ def gemm_roofline(s3e, ctx, ev, ftype: str, reps: int):
     X = rng.standard_normal((M, K)).astype(np.float32)
     Xd = ctx.to_device(X)
     Y = ctx.buffer(M * N * 4)
-    if wt in (s3e.TYPE_Q4_0, s3e.TYPE_Q8_0, s3e.TYPE_Q4_1):
+    run = None
+    if wt == s3e.TYPE_Q4_0:
+        ns = s3e.act_scale_elems(M, K)
+        qs, d = ctx.buffer((M + 63) // 64 * 64 * K * 3 // 2), ctx.buffer(ns * 2)
+        ctx.quantize_rows(s3e.TYPE_Q8_0_F6X2, Xd, M, K, qs, d, None)
+        run = lambda: ctx.mul_mat_q_f6(w, qs, d, M, Y)
+    elif wt in (s3e.TYPE_Q8_0, s3e.TYPE_Q4_1):
         vdt = s3e.TYPE_Q8_1 if wt == s3e.TYPE_Q4_1 else s3e.TYPE_Q8_0
         ns = s3e.act_scale_elems(M, K)
         qs, d, s = ctx.buffer(M * K), ctx.buffer(ns * 2), ctx.buffer(ns * 2)
@@ -113,13 +132,15 @@ def gemm_roofline(s3e, ctx, ev, ftype: str, reps: int):
         args = (qs, None, None)
     else:
         args = (Xd, None, None)
+    if run is None:
+        run = lambda: ctx.mul_mat_q(w, *args, M, Y)
     for _ in range(3):
-        ctx.mul_mat_q(w, *args, M, Y)
+        run()
     ctx.sync()
     e0, e1 = ev.create(), ev.create()
     ev.record(e0, ctx.stream)
     for _ in range(reps):
-        ctx.mul_mat_q(w, *args, M, Y)
+        run()
     ev.record(e1, ctx.stream)
     ms = ev.elapsed_ms(e0, e1) / reps
     ctx.sync()
@@ -353,6 +374,76 @@ def preprocess_leg(s3e, ctx, ev, st, S: int, encode_ms: float, reps: int = 20) -
     return res
 
 
+def encode_ms(s3e, ctx, ev, ftype: str, steps: int, warmup: int) -> float:
+    """ms/frame of the full 1008 px encoder (backbone + tracker neck) with the
+    ViT's linear weights in `ftype`, input resident in HBM."""
+    tmpdir = os.environ.get("TMPDIR", tempfile.gettempdir())
+    path = os.path.join(tmpdir, f"s3e_bench_sam3_vit_{ftype}.ggml")
+    s3e.synth_write(path, ftype=ftype, seed=0, std=0.02, **CFG)
+    model = s3e.Model(ctx, path)
+    st = s3e.State(ctx, model)
+    chw_d = ctx.to_device(preprocess(synthetic_image(CFG["img_size"])))
+    for _ in range(warmup):
+        st.encode_chw(chw_d)
+    ctx.sync()
+    e0, e1 = ev.create(), ev.create()
+    ev.record(e0, ctx.stream)
+    for _ in range(steps):
+        st.encode_chw(chw_d)
+    ev.record(e1, ctx.stream)
+    ms = ev.elapsed_ms(e0, e1) / steps
+    ctx.sync()
+    st.free()
+    model.free()
+    try:
+        os.remove(path)
+    except OSError:
+        pass
+    log(f"encode {ftype}: {ms:.3f} ms/frame over {steps} steps")
+    return ms
+
+
+ATTN_SHAPES = [("windowed", 9, 576), ("global", 1, 5184)]  # (name, windows B, tokens N); 16 heads, head dim 64
+
+
+def attention_fp16(s3e, ctx, ev, reps: int = 20) -> dict:
+    """The ViT's attention at F16 precision (fp16 operands, fp32
+    accumulation: ggml_flash_attn_ext as the reference's F16-weight path
+    computes it, S3E_PREC_DEFAULT): 16 heads of 64 over 9 windows of 576
+    tokens and over the 5184-token global grid, through s3e_flash_attn_ext
+    (f32 Q, K, V in ggml's layout, converted to fp16 by the call).  FLOPs
+    4·B·heads·N²·64 (QKᵀ and PV), against the 2.5 PFLOP/s dense fp16 peak."""
+    res = {}
+    rng = np.random.default_rng(7)
+    nh, D = 16, 64
+    e0, e1 = ev.create(), ev.create()
+    for name, B, N in ATTN_SHAPES:
+        q = ctx.to_device(rng.standard_normal((B, nh, N, D)).astype(np.float32))
+        k = ctx.to_device(rng.standard_normal((B, nh, N, D)).astype(np.float32))
+        v = ctx.to_device(rng.standard_normal((B, N, nh, D)).astype(np.float32))
+        o = ctx.buffer(B * N * nh * D * 4)
+        qk_nb = (1, D, N * D, nh * N * D)
+        v_nb = (1, nh * D, D, N * nh * D)
+        run = lambda: ctx.flash_attn_ext(q, qk_nb, k, qk_nb, v, v_nb, D, N, N, nh, B, 0.125, o, prec=0)
+        for _ in range(3):
+            run()
+        ctx.sync()
+        ev.record(e0, ctx.stream)
+        for _ in range(reps):
+            run()
+        ev.record(e1, ctx.stream)
+        us = ev.elapsed_ms(e0, e1) / reps * 1e3
+        ctx.sync()
+        flops = 4.0 * B * nh * N * N * D
+        tf = flops / (us * 1e-6) / 1e12
+        res[name] = {"windows": B, "tokens": N, "heads": nh, "us": round(us, 1), "TFLOPs": round(tf, 1),
+                     "frac_fp16_peak": round(tf / 2500.0, 4)}
+        log(f"attention fp16 {name} {B}x{nh}x{N}: {us:.1f} us, {tf:.1f} TFLOP/s")
+        for b in (q, k, v, o):
+            b.free()
+    return res
+
+
 def cpu_preprocess_ms(S: int, reps: int = 3) -> float:
     """The oracle's single-threaded sam3_resize_bilinear + sam3_preprocess_image
     (the reference's host loop) on the same 1920×1080 frame."""
@@ -423,6 +514,56 @@ def summarize_trace(trace_csv: str, marker: str, first: int, last: int, frames: 
     return "\n".join(lines)
 
 
+def summarize_grids(trace_csv: str, frames: int) -> str:
+    """Per (kernel, grid) table from a rocprofv3 kernel_trace.csv: separates
+    launches of one kernel at different shapes (e.g. windowed and global
+    attention)."""
+    import collections
+    import csv
+
+    agg = collections.defaultdict(list)
+    for r in csv.DictReader(open(trace_csv)):
+        key = (_short_kernel(r["Kernel_Name"]), f"{r['Grid_Size_X']}x{r['Grid_Size_Y']}x{r['Grid_Size_Z']}")
+        agg[key].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    lines = [f"{'kernel':28s} {'grid (threads)':>18s} {'calls':>6s} {'avg_us':>9s} {'ms/frame':>9s}"]
+    for (k, g), v in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"{k:28s} {g:>18s} {len(v):6d} {sum(v) / len(v):9.1f} {sum(v) / 1e3 / frames:9.3f}")
+    return "\n".join(lines)
+
+
+def summarize_pmc(csvs: list, kernels: list) -> str:
+    """Per-kernel averages per dispatch of rocprofv3 --pmc counter CSVs, and
+    the derived utilisation: kernel cycles = GRBM_GUI_ACTIVE / 8 (the counter
+    sums the 8 XCDs); MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (kernel cycles ×
+    1024 SIMDs); VALU issue = SQ_INSTS_VALU × 4 cycles (a wave64 VALU
+    instruction occupies a SIMD 4 cycles) / (kernel cycles × 1024)."""
+    import collections
+    import csv
+
+    agg = collections.defaultdict(lambda: collections.defaultdict(float))
+    disp = collections.defaultdict(lambda: collections.defaultdict(set))
+    for path in csvs:
+        for r in csv.DictReader(open(path)):
+            k = _short_kernel(r["Kernel_Name"])
+            agg[k][r["Counter_Name"]] += float(r["Counter_Value"])
+            disp[k][r["Counter_Name"]].add(r["Dispatch_Id"])
+    out = []
+    for k in kernels:
+        if k not in agg:
+            continue
+        c = {n: v / len(disp[k][n]) for n, v in agg[k].items()}
+        out.append(f"{k}  ({max(len(x) for x in disp[k].values())} dispatches)")
+        for n in sorted(c):
+            out.append(f"    {n:34s} {c[n]:14.4g}")
+        cyc = c.get("GRBM_GUI_ACTIVE", 0) / 8
+        if cyc:
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in c:
+                out.append(f"    {'-> MFMA busy':34s} {c['SQ_VALU_MFMA_BUSY_CYCLES'] / (cyc * 1024):14.3f}")
+            if "SQ_INSTS_VALU" in c:
+                out.append(f"    {'-> VALU issue':34s} {4 * c['SQ_INSTS_VALU'] / (cyc * 1024):14.3f}")
+    return "\n".join(out)
+
+
 def summarize_counters(fetch_csv: str, write_csv: str, cfetch_csv: str, cwrite_csv: str, copy_bytes: int,
                        kernel: str) -> str:
     """HBM bytes per launch of `kernel` from FETCH_SIZE / WRITE_SIZE (KiB per
@@ -459,6 +600,15 @@ def main() -> int:
         a = sys.argv[2:]
         print(summarize_trace(a[0], a[1], int(a[2]), int(a[3]), int(a[4])))
         return 0
+    if len(sys.argv) > 1 and sys.argv[1] == "--summarize-grids":
+        print(summarize_grids(sys.argv[2], int(sys.argv[3])))
+        return 0
+    if len(sys.argv) > 1 and sys.argv[1] == "--summarize-pmc":
+        # --summarize-pmc a.csv [b.csv ...] -- kernel [kernel ...]
+        a = sys.argv[2:]
+        i = a.index("--")
+        print(summarize_pmc(a[:i], a[i + 1:]))
+        return 0
     if len(sys.argv) > 1 and sys.argv[1] == "--summarize-counters":
         a = sys.argv[2:]
         print(summarize_counters(a[0], a[1], a[2], a[3], int(a[4]), a[5]))
@@ -472,7 +622,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "gemm_fc1_q4_0_counters.txt"))
-    ap.add_argument("--only", choices=["encode", "gemm", "copy", "neck", "preprocess", "sam2", "small_m"], default=None,
+    ap.add_argument("--only", choices=["encode", "gemm", "copy", "neck", "preprocess", "sam2", "small_m", "c4",
+                                       "attn"], default=None,
                     help="run one leg only (for profiling runs)")
     ap.add_argument("--sam2-run", default=None, help="with --only sam2: one encoder, e.g. hiera_t:f16")
     args = ap.parse_args()
@@ -499,6 +650,15 @@ def main() -> int:
         ev.record(e1, ctx.stream)
         ms = ev.elapsed_ms(e0, e1) / 10
         log(f"copy 1 GiB: {ms:.3f} ms = {2 * nbytes / ms / 1e6:.1f} GB/s (read+write)")
+        return 0
+
+    if args.only == "attn":
+        attention_fp16(s3e, ctx, ev)
+        return 0
+
+    if args.only == "c4":
+        for ft in ("q8_0", "f16"):
+            encode_ms(s3e, ctx, ev, ft, args.steps, args.warmup)
         return 0
 
     if args.only == "small_m":
@@ -560,6 +720,9 @@ def main() -> int:
     pre = preprocess_leg(s3e, ctx, ev, st, CFG["img_size"], ms_frame)
     if args.only == "preprocess":
         return 0
+    c4 = {f"{ft}_ms": round(encode_ms(s3e, ctx, ev, ft, max(5, args.steps // 2), 2), 3)
+          for ft in ("q4_0", "q8_0", "f16") if ft != args.ftype}
+    attn = attention_fp16(s3e, ctx, ev)
     sam2 = sam2_encoders(s3e, ctx, ev, max(3, args.steps // 2), 2)
     sm = small_m(s3e, ctx, ev, args.ftype) if args.ftype in BPW else None
 
@@ -568,12 +731,16 @@ def main() -> int:
     traffic = read_traffic(args.traffic) if args.ftype == "q4_0" else None
     cpu = None
     if not args.no_cpu_baseline:
-        threads = args.cpu_threads or min(16, len(os.sched_getaffinity(0)))
+        # all the cores this job may use: OMP_NUM_THREADS where the job's
+        # host sets its CPU share, else every core the process can run on
+        host_cores = len(os.sched_getaffinity(0))
+        threads = args.cpu_threads or int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or host_cores
         cms = cpu_baseline(path, img, threads)
         log(f"cpu baseline: {cms / 1e3:.1f} s/frame, {threads} threads")
         pms = cpu_preprocess_ms(CFG["img_size"])
         log(f"cpu preprocessing of a {CAMERA[0]}x{CAMERA[1]} frame: {pms:.1f} ms, 1 thread")
-        cpu = {"value": round(cms, 1), "unit": "ms/frame", "cores": threads, "kind": "port",
+        cpu = {"value": round(cms, 1), "unit": "ms/frame", "cores": threads, "host_cores_visible": host_cores,
+               "kind": "port",
                "preprocess_ms": round(pms, 2),
                "sample": f"one full frame (prefix + 32 blocks + tracker neck) of the same {args.ftype.upper()} "
                          "model and image on the CPU oracle, a C restatement of ggml's CPU path (AVX2, "
@@ -602,10 +769,12 @@ def main() -> int:
                    "img_size": 1008, "weights": args.ftype, "blocks": 32, "window": 24,
                    "global_blocks": [7, 15, 23, 31], "neck_levels": [288, 144, 72, 36]},
         "breakdown": {"neck_ms": round(neck_ms, 3), "backbone_ms": round(ms_frame - neck_ms, 3)},
+        "c4_other_weights": c4,
+        "attention_fp16": attn,
         "sam2_encoders": sam2,
         "small_m": sm,
         "preprocess": pre,
-        "roofline": {"kernel": f"{GEMM_KERNEL} fc1 M=5184 N=4736 K=1024 ({args.ftype})", "bound": "mfma",
+        "roofline": {"kernel": f"{GEMM_KERNEL[args.ftype]} fc1 M=5184 N=4736 K=1024 ({args.ftype})", "bound": "mfma",
                      "achieved": round(gtops, 1), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(gtops / peak, 4), "traffic": traffic,
                      "us_per_launch": round(gms * 1e3, 2), "ops_per_launch": gops},

@@ -48,6 +48,11 @@ enum s3e_type {
     S3E_TYPE_Q4_1 = 3,
     S3E_TYPE_Q8_0 = 8,
     S3E_TYPE_Q8_1 = 9,
+    /* Not a ggml type: the Q8_0 codes of quantize_row_q8_0, each split
+     * q = 16·h + l (h = ⌊(q + 8)/16⌋) into two fp6 E3M2 values, in the tiled
+     * layout the engine's Q4_0 kernel streams (s3e_quantize_rows,
+     * s3e_mul_mat_q_f6). */
+    S3E_TYPE_Q8_0_F6X2 = 64,
 };
 
 typedef struct s3e_ctx s3e_ctx;       /* device + HIP stream */
@@ -128,6 +133,15 @@ int s3e_mul_mat_noalloc(s3e_ctx *ctx, const s3e_weight *w, const float *X, int64
  * call allocates nothing. */
 int s3e_mul_mat_q(s3e_ctx *ctx, const s3e_weight *w, const void *xq, const uint16_t *d,
                   const uint16_t *s, int64_t M, const float *bias, float *Y);
+/* No counterpart in the reference: s3e_mul_mat_q for Q4_0 weights with
+ * activations in S3E_TYPE_Q8_0_F6X2 (from s3e_quantize_rows), the kernel
+ * s3e_mul_mat and the encoder run for Q4_0: each 32-block sum comes from the
+ * fp6 MFMA, the same integers as the int8 path, so Y equals s3e_mul_mat_q's
+ * bit for bit.  K must be a multiple of 128; any M (no small-M kernel).
+ * Launches the GEMM kernel only. */
+int s3e_mul_mat_q_f6(s3e_ctx *ctx, const s3e_weight *w, const void *xq, const uint16_t *d, int64_t M,
+                     const float *bias, float *Y);
+
 /* Several independent products of one graph level in one launch: Y[i] =
  * ggml_add(ggml_mul_mat(W[i], X[i]), bias[i]) for i < n, each as in
  * s3e_mul_mat_q (activations already in the weight's vec_dot format, device
@@ -150,7 +164,13 @@ int s3e_mul_mat_q_batch(s3e_ctx *ctx, int n, const s3e_weight *const *w, const v
  * block b of row r is element ((b/4)·Mp + r)·4 + b%4 of a plane of G·Mp·4
  * fp16 values (blocks of one row come in groups of 4, and each group is laid
  * out for all rows before the next).  Blocks from K/32 to 4G−1 are written as
- * zero; rows from M to Mp−1 are not written.  All device pointers. */
+ * zero; rows from M to Mp−1 are not written.  All device pointers.
+ * S3E_TYPE_Q8_0_F6X2 (K a multiple of 128): the same codes and `d` as Q8_0;
+ * `qs` receives 3·Mt·K/2 bytes, Mt = M rounded up to 64: for each 64-row
+ * tile t, stage g (128 columns), block b < 4 of the stage, part p (0 h, 1 l)
+ * and word w < 3, the 64 rows' 8-byte words of the 192-bit E3M2 strings
+ * (code j of the block in bits [6j, 6j + 6)), as word
+ * ((((t·G + g)·4 + b)·2 + p)·3 + w)·64 + row % 64. */
 int s3e_quantize_rows(s3e_ctx *ctx, int type, const float *X, int64_t M, int64_t K,
                       void *qs, uint16_t *d, uint16_t *s);
 

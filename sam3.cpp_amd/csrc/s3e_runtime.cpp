@@ -478,7 +478,12 @@ extern "C" int s3e_quantize_rows(s3e_ctx *ctx, int type, const float *X, int64_t
     if (type == S3E_TYPE_Q8_0) a.kind = A_Q8_0;
     else if (type == S3E_TYPE_Q8_1) a.kind = A_Q8_1;
     else if (type == S3E_TYPE_F16) a.kind = A_F16;
+    else if (type == S3E_TYPE_Q8_0_F6X2) a.kind = A_F6;
     else { set_error("s3e_quantize_rows: type %d is not a vec_dot type", type); return S3E_ERR_UNSUPPORTED; }
+    if (a.kind == A_F6 && K % 128 != 0) {
+        set_error("s3e_quantize_rows: K=%lld must be a multiple of 128 for the fp6 split", (long long)K);
+        return S3E_ERR_INVALID;
+    }
     if ((a.kind != A_F16 && !d) || (a.kind == A_Q8_1 && !s)) { set_error("s3e_quantize_rows: missing scale buffer"); return S3E_ERR_INVALID; }
     HIP_TRY(hipSetDevice(ctx->device));
     HIP_TRY(launch_rows_quant(a.kind, X, M, K, a, ctx->stream));
@@ -519,6 +524,31 @@ extern "C" int s3e_mul_mat(s3e_ctx *ctx, const s3e_weight *w, const float *X, in
     if (e != hipSuccess) { set_error("s3e_mul_mat: %s", hipGetErrorString(e)); return S3E_ERR_HIP; }
     return S3E_OK;
 } S3E_CATCH("s3e_mul_mat")
+
+extern "C" int s3e_mul_mat_q_f6(s3e_ctx *ctx, const s3e_weight *w, const void *xq, const uint16_t *d, int64_t M,
+                                const float *bias, float *Y) try {
+    if (!ctx || !w || !xq || !d || !Y) { set_error("s3e_mul_mat_q_f6: NULL argument"); return S3E_ERR_INVALID; }
+    const Weight &W = w->w;
+    if (W.kind != WK_Q4_0 || !W.f6) {
+        set_error("s3e_mul_mat_q_f6: needs Q4_0 weights with K a multiple of 128");
+        return S3E_ERR_UNSUPPORTED;
+    }
+    if (M < 0) { set_error("s3e_mul_mat_q_f6: negative M"); return S3E_ERR_INVALID; }
+    if (M == 0) return S3E_OK;
+    HIP_TRY(hipSetDevice(ctx->device));
+    Act a;
+    a.kind = A_F6;
+    a.x = (void *)xq;
+    a.d = (uint16_t *)d;
+    a.ld = W.K;
+    a.mp = round_up(M, ROW_PAD);
+    EpiArgs ea;
+    ea.bias = bias;
+    ea.y = Y;
+    ea.ldy = W.N;
+    HIP_TRY(launch_gemm(W, a, M, EPI_F32, ea, ctx->stream));
+    return S3E_OK;
+} S3E_CATCH("s3e_mul_mat_q_f6")
 
 extern "C" int s3e_mul_mat_q(s3e_ctx *ctx, const s3e_weight *w, const void *xq, const uint16_t *d,
                              const uint16_t *s, int64_t M, const float *bias, float *Y) try {

@@ -18,6 +18,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("S3E_LIB_PATH", os.path.join(HERE, "libs3e.so"))
 
 TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_Q4_1, TYPE_Q8_0, TYPE_Q8_1 = 0, 1, 2, 3, 8, 9
+TYPE_Q8_0_F6X2 = 64  # the Q8_0 codes split into two fp6 halves (engine layout)
 PREC_DEFAULT, PREC_F32 = 0, 1
 FTYPE_BY_NAME = {"f32": 0, "f16": 1, "q4_0": 2, "q4_1": 3, "q8_0": 8}
 
@@ -87,6 +88,7 @@ def _load() -> ctypes.CDLL:
         "s3e_quantize_rows": (c_int, [c_void_p, c_int, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
         "s3e_layer_norm": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_float, c_void_p, c_void_p, c_void_p]),
         "s3e_mul_mat_q": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
+        "s3e_mul_mat_q_f6": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
         "s3e_mul_mat_q_batch": (c_int, [c_void_p, c_int, POINTER(c_void_p), POINTER(c_void_p), POINTER(c_void_p),
                                         POINTER(c_void_p), c_int64, POINTER(c_void_p), POINTER(c_void_p)]),
         "s3e_copy": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t]),
@@ -130,7 +132,7 @@ LIB = _load()
 DECLARED = [
     "s3e_last_error", "s3e_abi_version", "s3e_ctx_create", "s3e_ctx_destroy", "s3e_ctx_sync", "s3e_ctx_stream",
     "s3e_malloc", "s3e_free", "s3e_memcpy_h2d", "s3e_memcpy_d2h", "s3e_weight_upload", "s3e_weight_free",
-    "s3e_weight_info", "s3e_mul_mat", "s3e_mul_mat_noalloc", "s3e_mul_mat_q", "s3e_mul_mat_q_batch", "s3e_quantize_rows", "s3e_layer_norm", "s3e_copy",
+    "s3e_weight_info", "s3e_mul_mat", "s3e_mul_mat_noalloc", "s3e_mul_mat_q", "s3e_mul_mat_q_f6", "s3e_mul_mat_q_batch", "s3e_quantize_rows", "s3e_layer_norm", "s3e_copy",
     "s3e_flash_attn_ext", "s3e_model_load",
     "s3e_model_free", "s3e_model_hparams", "s3e_state_create", "s3e_state_free", "s3e_encode_chw",
     "s3e_encode_chw_host", "s3e_encode_image_u8", "s3e_preprocess_image", "s3e_vit_prefix", "s3e_vit_block", "s3e_vit_block_stage", "s3e_vit_prefix_stage", "s3e_encode_vit_chw", "s3e_model_tensor_get", "s3e_run_neck", "s3e_hiera_block", "s3e_model_type", "s3e_mem_attn_dims", "s3e_mem_attn",
@@ -328,6 +330,11 @@ class Context:
                   Y: DeviceBuffer, bias: DeviceBuffer | None = None):
         check(LIB.s3e_mul_mat_q(self.handle, w.handle, xq.ptr, d.ptr if d else None, s.ptr if s else None, M,
                                 bias.ptr if bias else None, Y.ptr), "s3e_mul_mat_q")
+
+    def mul_mat_q_f6(self, w: Weight, xq: DeviceBuffer, d: DeviceBuffer, M: int, Y: DeviceBuffer,
+                     bias: DeviceBuffer | None = None):
+        check(LIB.s3e_mul_mat_q_f6(self.handle, w.handle, xq.ptr, d.ptr, M, bias.ptr if bias else None, Y.ptr),
+              "s3e_mul_mat_q_f6")
 
     def mul_mat_q_batch(self, ws, xqs, ds, ss, M: int, biases, Ys):
         """Independent small-M products in one launch (lists of equal length;

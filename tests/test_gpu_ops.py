@@ -129,6 +129,52 @@ def test_mul_mat(ctx, wt, M, N, K):
     assert err <= 1e-5
 
 
+@pytest.mark.parametrize("M,N,K", [(100, 384, 1024), (777, 1024, 4736), (5184, 4736, 1024)])
+def test_mul_mat_q_f6(ctx, M, N, K):
+    """Q4_0 products on the fp6 kernel (activations as S3E_TYPE_Q8_0_F6X2)
+    equal the int8 kernel's bit for bit (the same exact block sums, the same
+    scale products and FMA order), and the oracle to fp32 order noise."""
+    import s3e
+
+    rng = np.random.default_rng(M + N + K)
+    W = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    bias = rng.normal(0, 0.1, N).astype(np.float32)
+    wb = orc.to_weight_bytes(orc.Q4_0, W)
+    w = ctx.weight(orc.Q4_0, K, N, wb)
+    Xd, bd = ctx.to_device(X), ctx.to_device(bias)
+    ns = s3e.act_scale_elems(M, K)
+    q8, d8 = ctx.buffer(M * K), ctx.buffer(ns * 2)
+    f6, d6 = ctx.buffer((M + 63) // 64 * 64 * K * 3 // 2), ctx.buffer(ns * 2)
+    ctx.quantize_rows(s3e.TYPE_Q8_0, Xd, M, K, q8, d8, None)
+    ctx.quantize_rows(s3e.TYPE_Q8_0_F6X2, Xd, M, K, f6, d6, None)
+    Y8, Y6 = ctx.buffer(M * N * 4), ctx.buffer(M * N * 4)
+    ctx.mul_mat_q(w, q8, d8, None, M, Y8, bd)
+    ctx.mul_mat_q_f6(w, f6, d6, M, Y6, bd)
+    ctx.sync()
+    y8, y6 = Y8.download(np.float32, (M, N)), Y6.download(np.float32, (M, N))
+    ref = orc.mul_mat(orc.Q4_0, wb, N, K, X) + bias
+    err = orc.rel_l2(y6, ref)
+    print(f"mul_mat_q_f6 M={M} N={N} K={K}: differing from int8 {np.count_nonzero(y6 != y8)}, rel_l2={err:.3e}")
+    assert np.array_equal(y6, y8)
+    assert err <= 1e-5
+    w.free()
+
+
+def test_mul_mat_q_f6_rejects(ctx):
+    import s3e
+
+    rng = np.random.default_rng(9)
+    W = rng.normal(0, 0.02, (64, 96)).astype(np.float32)
+    w = ctx.weight(orc.Q4_0, 96, 64, orc.to_weight_bytes(orc.Q4_0, W))  # K % 128 != 0: no fp6 copy
+    buf = ctx.buffer(1 << 16)
+    with pytest.raises(s3e.S3EError):
+        ctx.mul_mat_q_f6(w, buf, buf, 8, buf)
+    with pytest.raises(s3e.S3EError):
+        ctx.quantize_rows(s3e.TYPE_Q8_0_F6X2, buf, 8, 96, buf, buf, None)
+    w.free()
+
+
 SMALL_M = [1, 5, 32, 33, 64]
 
 
