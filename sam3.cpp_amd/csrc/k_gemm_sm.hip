@@ -18,7 +18,10 @@
 // K ranges (KS = 4 is built: four waves share one strip's K range, which
 // keeps each wave's dependent chain short; a whole strip per wave measured
 // no faster and needs more registers); split partial sums are added in LDS
-// in a fixed order (deterministic).  The next stage is loaded while one is
+// in a fixed order (deterministic).  A lone product with few strips (N =
+// 1024: 32 work-groups for 256 CUs) also splits K across kg work-groups per
+// strip: each writes its sum to a workspace and a second pass adds the kg
+// sums in index order.  The next stage is loaded while one is
 // consumed.  Per 32-element block and 32-row tile
 // the arithmetic is the large-M kernel's: the exact integer block sum on
 // v_mfma_i32_32x32x32_i8 (the Q4_0 offset −8 applied by a second MFMA against
@@ -35,6 +38,8 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int SM_WAVES = 4;
@@ -68,15 +73,20 @@ __global__ __launch_bounds__(64 * SM_WAVES, 2) void k_gemm_sm(SmArgs p) {
     const int t = threadIdx.x, lane = t & 63, lr = lane & 31, lh = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int ls = wave / KS, kr = wave % KS;
-    const int n0 = ((wg - G.wg0) * SPW + ls) * 32;
+    // kg work-groups share a column group, each over its own K range, and
+    // with p.rt = 2 each 32-row tile has work-groups of its own (MT = 1)
+    const int kgi = (wg - G.wg0) % p.kg, wr = (wg - G.wg0) / p.kg;
+    const int r0 = (wr % p.rt) * 32, cg = wr / p.rt;
+    const int n0 = (cg * SPW + ls) * 32;
     const int n = n0 + lr;  // < Np: weights are padded to whole 128-column groups
     const bool live = n0 < G.N;
-    const int s0 = G.nst * kr / KS, s1 = live ? G.nst * (kr + 1) / KS : s0;
+    const int ka = G.nst * kgi / p.kg, kn = G.nst * (kgi + 1) / p.kg - ka;
+    const int s0 = ka + kn * kr / KS, s1 = live ? ka + kn * (kr + 1) / KS : s0;
     const int M = p.M;
 
     int rows[MT];
 #pragma unroll
-    for (int i = 0; i < MT; i++) rows[i] = min(32 * i + lr, M - 1);
+    for (int i = 0; i < MT; i++) rows[i] = min(r0 + 32 * i + lr, M - 1);
 
     auto load = [&](int s, SmStage<WK, MT> &f) {
         const int b0 = 4 * s;
@@ -196,7 +206,7 @@ __global__ __launch_bounds__(64 * SM_WAVES, 2) void k_gemm_sm(SmArgs p) {
         for (int i = 0; i < MT; i++)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int row = 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
+                const int row = r0 + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
                 if (row < M && gn < G.N) G.y[(int64_t)row * G.ldy + gn] = acc[i][r] * kScale + bv;
             }
     } else {
@@ -207,18 +217,53 @@ __global__ __launch_bounds__(64 * SM_WAVES, 2) void k_gemm_sm(SmArgs p) {
             for (int r = 0; r < 16; r++)
                 red[wave][32 * i + 8 * (r >> 2) + 4 * lh + (r & 3)][lr] = acc[i][r];
         __syncthreads();
+        if (p.kg == 1) {
+            for (int o = t; o < SPW * MT * 32 * 32; o += 64 * SM_WAVES) {
+                const int st = o / (MT * 32 * 32), row = (o >> 5) % (MT * 32), col = o & 31;
+                const int gn = (cg * SPW + st) * 32 + col;
+                if (r0 + row >= M || gn >= G.N) continue;
+                float v = red[st * KS][row][col];
+#pragma unroll
+                for (int w = 1; w < KS; w++) v += red[st * KS + w][row][col];
+                v *= kScale;
+                if (G.bias) v += G.bias[gn];
+                G.y[(int64_t)(r0 + row) * G.ldy + gn] = v;
+            }
+            return;
+        }
+        // split over work-groups: each writes its K range's sum to part
+        // [kg][M][N] and k_sm_reduce adds the kg sums in index order
         for (int o = t; o < SPW * MT * 32 * 32; o += 64 * SM_WAVES) {
             const int st = o / (MT * 32 * 32), row = (o >> 5) % (MT * 32), col = o & 31;
-            const int gn = ((wg - G.wg0) * SPW + st) * 32 + col;
-            if (row >= M || gn >= G.N) continue;
+            const int gn = (cg * SPW + st) * 32 + col;
+            if (r0 + row >= M || gn >= G.N) continue;
             float v = red[st * KS][row][col];
 #pragma unroll
             for (int w = 1; w < KS; w++) v += red[st * KS + w][row][col];
-            v *= kScale;
-            if (G.bias) v += G.bias[gn];
-            G.y[(int64_t)row * G.ldy + gn] = v;
+            p.part[((int64_t)kgi * M + r0 + row) * G.N + gn] = v;
         }
     }
+}
+
+// Y = scale · Σ_k part[k] + bias over the kg ≤ SM_KG_MAX partial sums of a
+// split small-M product, added in index order (one thread per output; the kg
+// loads are all issued before the first add).
+__global__ __launch_bounds__(256) void k_sm_reduce(const float *__restrict__ part, int kg, int64_t mn, int N,
+                                                  float scale, const float *__restrict__ bias, float *__restrict__ y,
+                                                  int64_t ldy) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= mn) return;
+    float pv[SM_KG_MAX];
+#pragma unroll
+    for (int k = 0; k < SM_KG_MAX; k++) pv[k] = k < kg ? part[k * mn + i] : 0.f;
+    float v = 0.f;
+#pragma unroll
+    for (int k = 0; k < SM_KG_MAX; k++) v += pv[k];  // + 0 past kg leaves v unchanged
+    const int64_t row = i / N;
+    const int col = (int)(i - row * N);
+    v *= scale;
+    if (bias) v += bias[col];
+    y[row * ldy + col] = v;
 }
 
 #define LDS_PTR(p) ((__attribute__((address_space(3))) void *)(p))
@@ -226,23 +271,52 @@ __global__ __launch_bounds__(64 * SM_WAVES, 2) void k_gemm_sm(SmArgs p) {
 // Batched variant: a work-group owns 4 adjacent strips (128 columns), one
 // per wave, over the whole K range, so the activation stage (the same for
 // the four waves) is staged once in LDS by direct-to-LDS loads (rows of 128
-// bytes, 256 for F16, 16-byte chunks XOR-swizzled by row) while each wave
-// streams its own weights into registers one stage ahead.  One barrier per
-// stage releases the previous activation buffer.
+// bytes, 256 for F16, 16-byte chunks XOR-swizzled by row).  Quantized weights
+// and their scales go to LDS the same way, each wave its own strip's, so that
+// AHEAD stages are in flight while one is consumed with no registers held
+// for them; F16 weights (8 KB per wave and stage) stream into registers one
+// stage ahead instead.  One barrier per stage releases the buffers the stage
+// before read.
 template <int WK, int MT>
 struct SmbCfg {
     static constexpr bool quant = WK != WK_F16;
+    static constexpr bool q41 = WK == WK_Q4_1;
     static constexpr int ROWB = quant ? 128 : 256;
     static constexpr int A_BYTES = MT * 32 * ROWB;
     static constexpr int SC_BYTES = quant ? MT * 32 * 8 : 0;               // 4 block scales per row
-    static constexpr int SS_BYTES = (WK == WK_Q4_1) ? MT * 32 * 8 : 0;      // 4 block sums per row
-    static constexpr int STAGE = A_BYTES + SC_BYTES + SS_BYTES;
+    static constexpr int SS_BYTES = q41 ? MT * 32 * 8 : 0;                  // 4 block sums per row
     static constexpr int NA = A_BYTES / 4096;                               // 1 KB DMA runs per wave
-    static constexpr int NBUF = 2;                                           // stages s, s+1
+    // quantized weights in LDS: per wave [4 blocks][32 columns][BB bytes],
+    // then the columns' 4 scales (and Q4_1 minima), 8 bytes each
+    static constexpr int BB = SmCfg<WK>::BB;
+    static constexpr int WW = quant ? 128 * BB : 0;
+    static constexpr int NWI = WW / 1024;                                   // 1 KB DMA runs per wave
+    static constexpr int W_OFF = A_BYTES + SC_BYTES + SS_BYTES;
+    static constexpr int WD_OFF = W_OFF + SM_WAVES * WW;
+    static constexpr int WM_OFF = WD_OFF + (quant ? SM_WAVES * 256 : 0);
+    static constexpr int STAGE = WM_OFF + (q41 ? SM_WAVES * 256 : 0);
+    // two buffers: stage s + 1 lands while stage s is consumed.  The
+    // products are bound by overlapping one wave's MFMA with another's VALU,
+    // so small buffers that let three work-groups share a CU (Q4_0 at 64
+    // rows: 36 KB, 145 VGPRs) beat deeper rings (4 buffers: 2.37 TB/s
+    // against 2.77 over a 256-product sweep)
+    static constexpr int NBUF = 2;
+    static constexpr int AHEAD = NBUF - 1;                                  // stages issued ahead
+    // vector memory instructions a lane issues per stage (quantized path)
+    static constexpr int LOADS = NA + NWI + (quant ? 2 : 0) + (q41 ? 2 : 0);
 };
 
 template <int R>
 __device__ __forceinline__ int smb_swz(int r) { return R == 128 ? ((r >> 1) & 7) : (r & 15); }
+
+template <int LOADS, int AHEAD>
+__device__ __forceinline__ void smb_wait(int ahead) {
+    // stage s has landed when at most `ahead` later stages' loads are outstanding
+    static_assert(AHEAD >= 1 && AHEAD <= 3, "deeper rings need more cases");
+    if (AHEAD >= 3 && ahead >= 2) wait_and_barrier<(AHEAD >= 3 ? 2 * LOADS : 0)>();
+    else if (AHEAD >= 2 && ahead >= 1) wait_and_barrier<(AHEAD >= 2 ? LOADS : 0)>();
+    else wait_and_barrier<0>();
+}
 
 template <int WK, int MT>
 __global__ __launch_bounds__(64 * SM_WAVES, 2) void k_gemm_smb(SmArgs p) {
@@ -254,10 +328,10 @@ __global__ __launch_bounds__(64 * SM_WAVES, 2) void k_gemm_smb(SmArgs p) {
     const SmGemm G = p.many ? p.many[p.wg_gemm[wg]] : p.one;
     const int t = threadIdx.x, lane = t & 63, lr = lane & 31, lh = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const int n0 = ((wg - G.wg0) * SM_WAVES + wave) * 32;
+    const int n0 = __builtin_amdgcn_readfirstlane(((wg - G.wg0) * SM_WAVES + wave) * 32);
     const int n = n0 + lr;  // < Np (weights padded to 128-column groups)
-    const bool live = n0 < G.N;
-    const int nst = G.nst, M = p.M;
+    const bool live = n0 < __builtin_amdgcn_readfirstlane(G.N);
+    const int nst = __builtin_amdgcn_readfirstlane(G.nst), M = __builtin_amdgcn_readfirstlane(p.M);
     const int esize = B::quant ? 1 : 2;
     const int64_t kbytes = (int64_t)G.K * esize;
 
@@ -275,7 +349,16 @@ __global__ __launch_bounds__(64 * SM_WAVES, 2) void k_gemm_smb(SmArgs p) {
         a_ch[j] = (slot ^ smb_swz<B::ROWB>(row)) * 16;
         a_dst[j] = run * 1024;
     }
-    auto issue_a = [&](int s) {
+    // DMA sources of this wave's weight runs (quantized): lane fills bytes
+    // [16·lane, 16·lane + 16) of run i of the wave's [block][column][BB] area
+    int64_t w_src[B::NWI > 0 ? B::NWI : 1];
+#pragma unroll
+    for (int i = 0; i < B::NWI; i++) {
+        const int o = i * 1024 + lane * 16;
+        const int j = o / (32 * B::BB), c = (o % (32 * B::BB)) / B::BB, sub = o % B::BB;
+        w_src[i] = ((int64_t)j * G.np + n0 + c) * B::BB + sub;
+    }
+    auto issue = [&](int s) {
         uint8_t *L = lds + (s % B::NBUF) * B::STAGE;
 #pragma unroll
         for (int j = 0; j < B::NA; j++) {
@@ -290,26 +373,22 @@ __global__ __launch_bounds__(64 * SM_WAVES, 2) void k_gemm_smb(SmArgs p) {
             const int64_t src = ((int64_t)s * G.xmp) * 8 + run + lane * 4;
             __builtin_amdgcn_global_load_lds((const void *)((const uint8_t *)G.xd + src),
                                              LDS_PTR(L + B::A_BYTES + run), 4, 0, 0);
-            if constexpr (WK == WK_Q4_1)
+            if constexpr (B::q41)
                 __builtin_amdgcn_global_load_lds((const void *)((const uint8_t *)G.xs + src),
                                                  LDS_PTR(L + B::A_BYTES + B::SC_BYTES + run), 4, 0, 0);
-        }
-    };
-    struct WStage {
-        uint4 w[C::WL];
-        uint2 wd, wm;
-    };
-    auto load_w = [&](int s, WStage &f) {
-        const int b0 = 4 * s;
+            // this wave's weights (4 blocks = 4·np·BB bytes per stage) and the
+            // 8 scale bytes of each of its 32 columns
+            const int64_t wst = (int64_t)4 * s * G.np * B::BB;
 #pragma unroll
-        for (int j = 0; j < C::WL; j++) {
-            const int blk = C::q4 ? b0 + j : (WK == WK_Q8_0 ? b0 + j : b0 + j / 2);
-            const int sub = C::q4 ? 0 : (WK == WK_Q8_0 ? lh : 2 * (j & 1) + lh);
-            f.w[j] = gload16(G.w + ((int64_t)blk * G.np + n) * C::BB + sub * 16);
-        }
-        if constexpr (C::quant) {
-            f.wd = gload8(G.wd + ((int64_t)s * G.np + n) * 4);
-            if constexpr (C::q41) f.wm = gload8(G.wm + ((int64_t)s * G.np + n) * 4);
+            for (int i = 0; i < B::NWI; i++)
+                __builtin_amdgcn_global_load_lds((const void *)(G.w + wst + w_src[i]),
+                                                 LDS_PTR(L + B::W_OFF + wave * B::WW + i * 1024), 16, 0, 0);
+            const int64_t dsrc = ((int64_t)s * G.np + n0) * 8 + lane * 4;
+            __builtin_amdgcn_global_load_lds((const void *)((const uint8_t *)G.wd + dsrc),
+                                             LDS_PTR(L + B::WD_OFF + wave * 256), 4, 0, 0);
+            if constexpr (B::q41)
+                __builtin_amdgcn_global_load_lds((const void *)((const uint8_t *)G.wm + dsrc),
+                                                 LDS_PTR(L + B::WM_OFF + wave * 256), 4, 0, 0);
         }
     };
 
@@ -319,50 +398,52 @@ __global__ __launch_bounds__(64 * SM_WAVES, 2) void k_gemm_smb(SmArgs p) {
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[i][r] = 0.f;
 
-    auto compute = [&](int s, const WStage &f) {
-        const uint8_t *L = lds + (s % B::NBUF) * B::STAGE;
-        if constexpr (C::quant) {
+    if constexpr (B::quant) {
+        auto compute = [&](int s) {
+            const uint8_t *L = lds + (s % B::NBUF) * B::STAGE;
+            const uint8_t *Wl = L + B::W_OFF + wave * B::WW;
             const v16i zi = {};
             const v16f zf = {};
             const v4i minus8 = {(int)0xF8F8F8F8, (int)0xF8F8F8F8, (int)0xF8F8F8F8, (int)0xF8F8F8F8};
-            uint2 ad[MT], as[MT];
+            // the rows' 4 block scales are the raw K = 8 operand of the scale
+            // product; the weight side is one-hot at block j (both K halves)
+            v4h ha[MT];
+            uint2 as[MT];
 #pragma unroll
             for (int i = 0; i < MT; i++) {
-                ad[i] = lds_u2(L + B::A_BYTES + (32 * i + lr) * 8);
+                const uint2 ad = lds_u2(L + B::A_BYTES + (32 * i + lr) * 8);
+                ha[i] = __builtin_bit_cast(v4h, v2u{ad.x, ad.y});
                 if constexpr (C::q41) as[i] = lds_u2(L + B::A_BYTES + B::SC_BYTES + (32 * i + lr) * 8);
             }
-            const uint32_t wdw[2] = {f.wd.x, f.wd.y};
+            const uint2 wd = lds_u2(L + B::WD_OFF + wave * 256 + lr * 8);
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 v4i b;
                 if constexpr (C::q4) {
-                    const int sh = 4 * lh;
-                    b[0] = (int)((f.w[j].x >> sh) & 0x0F0F0F0Fu);
-                    b[1] = (int)((f.w[j].y >> sh) & 0x0F0F0F0Fu);
-                    b[2] = (int)((f.w[j].z >> sh) & 0x0F0F0F0Fu);
-                    b[3] = (int)((f.w[j].w >> sh) & 0x0F0F0F0Fu);
+                    const v4i wq = *(const v4i *)(Wl + (j * 32 + lr) * 16);
+                    const int sh = 4 * lh;  // low nibbles: elements 0..15, high: 16..31
+#pragma unroll
+                    for (int e = 0; e < 4; e++) b[e] = (int)(((uint32_t)wq[e] >> sh) & 0x0F0F0F0Fu);
                 } else {
-                    b = __builtin_bit_cast(v4i, f.w[j]);
+                    b = *(const v4i *)(Wl + (j * 32 + lr) * 32 + lh * 16);
                 }
-                const uint32_t hw = (wdw[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
-                const v4u hb = {hw, 0u, 0u, 0u};
+                const uint32_t w = j < 2 ? wd.x : wd.y;
+                const uint32_t m = (j & 1) ? (w & 0xFFFF0000u) : (w & 0xFFFFu);
+                const v4h hb = __builtin_bit_cast(v4h, j < 2 ? v2u{m, 0u} : v2u{0u, m});
 #pragma unroll
                 for (int i = 0; i < MT; i++) {
                     const int r = 32 * i + lr;
                     const v4i a = *(const v4i *)(L + r * B::ROWB + (((2 * j + lh) ^ smb_swz<B::ROWB>(r)) << 4));
                     v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, zi, 0, 0, 0);
                     if constexpr (WK == WK_Q4_0) S = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, minus8, S, 0, 0, 0);
-                    const uint32_t adw[2] = {ad[i].x, ad[i].y};
-                    const uint32_t ha_ = (adw[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
-                    const v4u ha = {ha_, 0u, 0u, 0u};
-                    const v16f Cs = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, ha),
-                                                                          __builtin_bit_cast(v8h, hb), zf, 0, 0, 0);
+                    const v16f Cs = __builtin_amdgcn_mfma_f32_32x32x8f16(ha[i], hb, zf, 0, 0, 0);
 #pragma unroll
                     for (int r2 = 0; r2 < 16; r2++) acc[i][r2] = __builtin_fmaf((float)S[r2], Cs[r2], acc[i][r2]);
                 }
             }
             if constexpr (C::q41) {
-                const v4u hb = {f.wm.x, f.wm.y, 0u, 0u};
+                const uint2 wm = lds_u2(L + B::WM_OFF + wave * 256 + lr * 8);
+                const v4u hb = {wm.x, wm.y, 0u, 0u};
 #pragma unroll
                 for (int i = 0; i < MT; i++) {
                     const v4u ha = {as[i].x, as[i].y, 0u, 0u};
@@ -370,7 +451,33 @@ __global__ __launch_bounds__(64 * SM_WAVES, 2) void k_gemm_smb(SmArgs p) {
                                                                     __builtin_bit_cast(v8h, hb), acc[i], 0, 0, 0);
                 }
             }
-        } else {
+        };
+        // stages s + 1 .. s + AHEAD − 1 are in flight while stage s is
+        // consumed; every wave issues B::LOADS instructions per stage (idle
+        // strips load the zero padding columns), so stage s has landed when
+        // at most the later issued stages' loads are outstanding.  The barrier
+        // at the top of step s also frees the buffer stage s + AHEAD
+        // overwrites (read by stage s − 1).
+        for (int i = 0; i < B::AHEAD && i < nst; i++) issue(i);
+        for (int s = 0; s < nst; s++) {
+            smb_wait<B::LOADS, B::AHEAD>(min(B::AHEAD - 1, nst - 1 - s));
+            if (s + B::AHEAD < nst) issue(s + B::AHEAD);
+            if (live) compute(s);
+        }
+    } else {
+        struct WStage {
+            uint4 w[C::WL];
+        };
+        auto load_w = [&](int s, WStage &f) {
+            const int b0 = 4 * s;
+#pragma unroll
+            for (int j = 0; j < C::WL; j++) {
+                // block j / 2, slab j % 2, half lh
+                f.w[j] = gload16(G.w + ((int64_t)(b0 + j / 2) * G.np + n) * C::BB + (2 * (j & 1) + lh) * 16);
+            }
+        };
+        auto compute = [&](int s, const WStage &f) {
+            const uint8_t *L = lds + (s % B::NBUF) * B::STAGE;
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 const v8h b = __builtin_bit_cast(v8h, f.w[j]);
@@ -381,22 +488,21 @@ __global__ __launch_bounds__(64 * SM_WAVES, 2) void k_gemm_smb(SmArgs p) {
                     acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[i], 0, 0, 0);
                 }
             }
+        };
+        // stage s + 1 (activations in LDS, weights in registers) is in flight
+        // while stage s is consumed; the barrier at the top of an iteration
+        // also frees the buffer stage s + 1 overwrites
+        WStage cur, nxt;
+        issue(0);
+        if (live) load_w(0, cur);
+        for (int s = 0; s < nst; s++) {
+            wait_and_barrier<0>();
+            const bool more = s + 1 < nst;
+            if (more) issue(s + 1);
+            if (more && live) load_w(s + 1, nxt);
+            if (live) compute(s, cur);
+            if (more && live) cur = nxt;
         }
-    };
-
-    // stage s + 1 (activations in LDS, weights in registers) is in flight while
-    // stage s is consumed; the barrier at the top of an iteration also frees
-    // the buffer stage s + 1 overwrites
-    WStage cur, nxt;
-    issue_a(0);
-    if (live) load_w(0, cur);
-    for (int s = 0; s < nst; s++) {
-        wait_and_barrier<0>();
-        const bool more = s + 1 < nst;
-        if (more) issue_a(s + 1);
-        if (more && live) load_w(s + 1, nxt);
-        if (live) compute(s, cur);
-        if (more && live) cur = nxt;
     }
 
     if (!live) return;
@@ -486,8 +592,11 @@ hipError_t launch_gemm_smb(WKind kind, const SmArgs &a, int wgs, hipStream_t st)
 
 hipError_t launch_gemm_sm(WKind kind, const SmArgs &a, int wgs, int ks, hipStream_t st) {
     if (a.M <= 0 || a.M > 64 || wgs <= 0 || ks != 4 || (a.many && !a.wg_gemm)) return hipErrorInvalidValue;
+    if (a.kg < 1 || a.kg > SM_KG_MAX || (a.kg > 1 && (a.many || !a.part || wgs % a.kg != 0)))
+        return hipErrorInvalidValue;
+    if (a.rt != 1 && (a.rt != 2 || a.M <= 32 || a.many || wgs % (2 * a.kg) != 0)) return hipErrorInvalidValue;
     const dim3 grid((unsigned)wgs), block(64 * SM_WAVES);
-    const bool two = a.M > 32;
+    const bool two = a.M > 32 && a.rt == 1;
 #define S3E_SM(WK)                                                                                       \
     do {                                                                                                 \
         if (two) hipLaunchKernelGGL((k_gemm_sm<WK, 2, 4>), grid, block, 0, st, a);                       \
@@ -501,6 +610,13 @@ hipError_t launch_gemm_sm(WKind kind, const SmArgs &a, int wgs, int ks, hipStrea
         default: return hipErrorInvalidValue;
     }
 #undef S3E_SM
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a.kg == 1) return e;
+    const SmGemm &g = a.one;
+    const int64_t mn = (int64_t)a.M * g.N;
+    const float scale = kind == WK_F16 ? 1.0f : 0.5f;  // the quantized scale products are doubled
+    hipLaunchKernelGGL(k_sm_reduce, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, st, (const float *)a.part, a.kg,
+                       mn, g.N, scale, g.bias, g.y, g.ldy);
     return hipGetLastError();
 }
 

@@ -252,6 +252,12 @@ struct SmArgs {
     const uint16_t *wg_gemm = nullptr;  // device: product index of each work-group (with many)
     int n = 1;
     int M = 0;                   // rows, 1..64, shared by the products
+    // one product split over K across kg work-groups per column group
+    // (k_gemm_sm only): part holds the kg·M·N partial sums
+    int kg = 1;
+    float *part = nullptr;
+    // k_gemm_sm with M > 32: 2 gives each 32-row tile work-groups of its own
+    int rt = 1;
 };
 
 // ---- kernel launchers (k_*.hip) ----
@@ -262,9 +268,10 @@ hipError_t launch_gemm(const Weight &w, const Act &a, int64_t M, Epi epi, const 
                        hipStream_t st);
 // Small-M products (k_gemm_sm.hip): Q4_0 / Q4_1 / Q8_0 / F16 weights, M ≤ 64.
 // ks = 4 (four waves split the K range of one 32-column strip); wgs = total
-// of sm_wgs(N, ks) over the products.
+// of sm_wgs(N, ks) over the products, times a.kg for a split product.
 int64_t sm_weight_bytes(const Weight &w);
 int sm_wgs(int64_t N, int ks);
+constexpr int SM_KG_MAX = 16;  // most work-groups one column group's K range splits over
 hipError_t launch_pack_sm(const Weight &w, void *out, hipStream_t st);
 hipError_t launch_gemm_sm(WKind kind, const SmArgs &a, int wgs, int ks, hipStream_t st);
 // Batched products (many): 4 strips per work-group, activations staged in

@@ -23,6 +23,9 @@ struct s3e_ctx {
     std::vector<uint8_t> sm_last;
     // this device's copy of the allocation-free entry points' scratch array
     void *scratch = nullptr;
+    // partial sums of small-M products split over K across work-groups
+    float *sk_part = nullptr;
+    int64_t sk_part_cap = 0;
 };
 
 struct s3e_weight {

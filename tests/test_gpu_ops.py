@@ -203,6 +203,38 @@ def test_mul_mat_small_m(ctx, wt, N, K):
         assert err <= 1e-5, M
 
 
+@pytest.mark.parametrize("wt", [orc.Q4_0, orc.Q8_0], ids=lambda t: {2: "q4_0", 8: "q8_0"}[t])
+def test_mul_mat_small_m_split_repeats(ctx, wt):
+    """Lone small-M products whose K range is split across work-groups (few
+    32-column strips, long K: the fc2 shape has 32 strips over 37 stages of
+    128) give the same bits on every call, also with products of other
+    widths in between (each launch leaves its arrival counters at zero for
+    the next), and match the oracle."""
+    rng = np.random.default_rng(wt + 11)
+    cases = []
+    for N, K, M in [(1024, 4736, 64), (4736, 1024, 7), (96, 2048, 33), (1024, 4736, 1)]:
+        W = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+        wb = orc.to_weight_bytes(wt, W)
+        X = rng.standard_normal((M, K)).astype(np.float32)
+        ref = orc.mul_mat(wt, wb, N, K, X)
+        cases.append((ctx.weight(wt, K, N, wb), ctx.to_device(X), ctx.buffer(M * N * 4), M, N, K, ref))
+    first = {}
+    for rep in range(3):
+        for i, (w, Xd, Yd, M, N, K, ref) in enumerate(cases):
+            ctx.mul_mat(w, Xd, M, Yd)
+            ctx.sync()
+            Y = Yd.download(np.float32, (M, N))
+            if rep == 0:
+                err = orc.rel_l2(Y, ref)
+                print(f"split small-M type={wt} M={M} N={N} K={K}: rel_l2={err:.3e}", flush=True)
+                assert err <= 1e-5, (M, N, K)
+                first[i] = Y
+            else:
+                assert np.array_equal(Y, first[i]), (rep, M, N, K)
+    for w, *_ in cases:
+        w.free()
+
+
 @pytest.mark.parametrize("wt", [orc.Q4_0, orc.Q4_1, orc.Q8_0, orc.F16],
                          ids=lambda t: {1: "f16", 2: "q4_0", 3: "q4_1", 8: "q8_0"}[t])
 def test_mul_mat_q_batch_matches_single(ctx, wt):
