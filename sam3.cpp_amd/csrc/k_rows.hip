@@ -190,8 +190,9 @@ __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ x, 
 }
 
 // LayerNorm straight into A_F6 (E % 128 == 0, E ≤ 1024·NIT): a work-group
-// normalizes 16 consecutive rows (each wave 4 of them, the next row's values
-// loaded while one is converted), lane L of a wave holding the 16 consecutive
+// normalizes 16 consecutive rows (each wave LNF6_ROWS / LNF6_WAVES of them, the
+// next row's values loaded while one is converted), lane L of a wave holding the
+// 16 consecutive
 // values [16·(L + 64·it), +16), half L & 1 of one 32-element block.  Each
 // lane converts its half with one fp6 pack instruction (h codes in slots
 // 0-15, l codes in 16-31) and leaves its bits in LDS in the output's order;
@@ -200,10 +201,14 @@ __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ x, 
 // as whole lines.  The same statistics and per-element operations as
 // k_layernorm, so the same codes.
 constexpr int LNF6_ROWS = 16;
+// waves per work-group, LNF6_ROWS / LNF6_WAVES rows each: one row per wave
+// (no chain of dependent row loads; 5184 rows: 11.42 → 11.33 ms per ViT frame
+// against four rows per wave)
+constexpr int LNF6_WAVES = 16;
 constexpr int LNF6_BSTRIDE = 98;  // 8-byte LDS words per block: 6 runs of 16 rows, padded (bank spread, 16 B aligned)
 
-template <int NIT, bool WB>
-__global__ __launch_bounds__(256) void k_layernorm_f6(const float *__restrict__ x, int64_t M, int64_t E,
+template <int NIT, bool WB, int LNW>
+__global__ __launch_bounds__(64 * LNW) void k_layernorm_f6(const float *__restrict__ x, int64_t M, int64_t E,
                                                       float eps, const float *__restrict__ w,
                                                       const float *__restrict__ b, Act o) {
     __shared__ __attribute__((aligned(16))) uint64_t stg[32 * NIT * LNF6_BSTRIDE];
@@ -240,7 +245,7 @@ __global__ __launch_bounds__(256) void k_layernorm_f6(const float *__restrict__ 
             }
         }
     };
-    constexpr int RPW = LNF6_ROWS / 4;  // rows per wave
+    constexpr int RPW = LNF6_ROWS / LNW;  // rows per wave
     if (r0 + wave * RPW < M) load_row(r0 + wave * RPW);
     for (int k = 0; k < RPW; k++) {
         const int rr = wave * RPW + k;  // row within the group
@@ -339,7 +344,7 @@ __global__ __launch_bounds__(256) void k_layernorm_f6(const float *__restrict__ 
     // of the 64-row tile, which no product stores)
     const int64_t nst = o.ld / 128;
     const int npieces = nblk * 6 * 8;
-    for (int pc = threadIdx.x; pc < npieces; pc += 256) {
+    for (int pc = threadIdx.x; pc < npieces; pc += 64 * LNW) {
         const int run = pc >> 3, q = pc & 7;
         const int blk = run / 6, pt = run % 6;
         if (r0 + 2 * q >= M) continue;
@@ -347,7 +352,7 @@ __global__ __launch_bounds__(256) void k_layernorm_f6(const float *__restrict__ 
         *(uint4 *)((uint64_t *)o.x + f6_act_word(nst, r0, blk, pt / 3, pt % 3) + 2 * q) = val;
     }
     // block scales: per stage, 16 rows × 4 fp16 = 128 contiguous bytes
-    for (int pc = threadIdx.x; pc < (nblk / 4) * 8; pc += 256) {
+    for (int pc = threadIdx.x; pc < (nblk / 4) * 8; pc += 64 * LNW) {
         const int sg = pc >> 3, q = pc & 7;
         if (r0 + 2 * q >= M) continue;
         *(uint4 *)(o.d + scale_index(o.mp, r0 + 2 * q, 4 * sg)) = *(const uint4 *)&stgd[sg][2 * q][0];
@@ -474,8 +479,9 @@ hipError_t launch_layernorm(const float *x, int64_t M, int64_t E, float eps, con
         // rows of up to 1024 (the ViT's); the ViT's norms carry both gamma and
         // beta (sam3_layer_norm, sam3.cpp:1037-1046)
         const dim3 gf((unsigned)((M + LNF6_ROWS - 1) / LNF6_ROWS));
-        if (w) hipLaunchKernelGGL((k_layernorm_f6<1, true>), gf, dim3(256), 0, st, x, M, E, eps, w, b, out);
-        else hipLaunchKernelGGL((k_layernorm_f6<1, false>), gf, dim3(256), 0, st, x, M, E, eps, w, b, out);
+        constexpr int W = LNF6_WAVES;
+        if (w) hipLaunchKernelGGL((k_layernorm_f6<1, true, W>), gf, dim3(64 * W), 0, st, x, M, E, eps, w, b, out);
+        else hipLaunchKernelGGL((k_layernorm_f6<1, false, W>), gf, dim3(64 * W), 0, st, x, M, E, eps, w, b, out);
         return hipGetLastError();
     }
     if (E <= 256) hipLaunchKernelGGL(k_layernorm<1>, grid, dim3(256), 0, st, x, M, E, eps, w, b, out, y_f32);
