@@ -256,7 +256,16 @@ __global__ __launch_bounds__(NTH, SPLIT ? 1 : 2) void k_conv(ConvParams p) {
             for (int r = 0; r < 16; r++) {
                 const int gm = m0 + wm * 64 + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
                 if (gm >= p.M) continue;
-                float v = __fadd_rn(acc[i][n][r] * alpha, bv);
+                float b = bv;
+                if constexpr (CONV == 1) {
+                    if (e.bias_cls) {
+                        const int py = gm / p.cw, px = gm - py * p.cw;
+                        const int cy = py == 0 ? 0 : (py == p.ch - 1 ? 2 : 1);
+                        const int cx = px == 0 ? 0 : (px == p.cw - 1 ? 2 : 1);
+                        b = e.bias[(3 * cy + cx) * p.N + co];
+                    }
+                }
+                float v = __fadd_rn(acc[i][n][r] * alpha, b);
                 if constexpr (EPI == EPI_F32) {
                     e.y[(int64_t)gm * e.ldy + gn] = v;
                 } else if constexpr (EPI == EPI_ACT) {

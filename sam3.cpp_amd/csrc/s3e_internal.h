@@ -177,6 +177,10 @@ struct EpiArgs {
     // channel n % cout, written to output pixel (2y + ky, 2x + kx)
     int dc_w = 0, dc_cout = 0;
     int gelu = 0;                  // EPI_DECONV: gelu_erf after the bias
+    // EPI_F32 of a 3×3 conv: bias holds 9 rows of N, row 3·cy + cx for an
+    // output pixel in image row class cy and column class cx (0: first, 2:
+    // last, 1: otherwise)
+    int bias_cls = 0;
     // EPI_GELU: ggml_gelu (tanh form) through this fp16 table (65536 entries,
     // ggml_vec_gelu_f32 with GGML_GELU_FP16) instead of gelu_erf
     const uint16_t *gelu_tab = nullptr;

@@ -802,6 +802,12 @@ struct NeckScale {
     Weight dc[2], c1, c3;
     float *dc_b[2] = {nullptr, nullptr}, *c1_b = nullptr, *c3_b = nullptr;
     int64_t dc_b_n[2] = {0, 0}, c1_b_n = 0, c3_b_n = 0;
+    // scale 0 of files with F32 convs: the 1×1 folded into the 3×3 (c3f,
+    // weights W3·W1 per tap; c3f_b: 9 bias rows by border class), and the
+    // host f32 records it is computed from until the neck is complete
+    Weight c3f;
+    float *c3f_b = nullptr;
+    std::vector<float> h_c1, h_c1_b, h_c3, h_c3_b;
 };
 
 struct Neck {
@@ -871,10 +877,17 @@ int load_neck_tensor(s3e_model *m, const std::string &name, const RawTensor &t) 
         *len = t.ne[0];
         return upload_f32(m, t, t.ne[0], dst);
     };
+    const bool scale0 = name[9] == '0';
+    auto keep = [&](std::vector<float> &h) {  // scale-0 f32 record for the 1×1 → 3×3 fold
+        if (scale0 && t.type == 0) {
+            const float *src = (const float *)t.data.data();
+            h.assign(src, src + n_el);
+        }
+    };
     if (f == "dconv_2x2_0.bias" || f == "dconv_2x2.bias") rc = bias(&sc.dc_b[0], &sc.dc_b_n[0]);
     else if (f == "dconv_2x2_1.bias") rc = bias(&sc.dc_b[1], &sc.dc_b_n[1]);
-    else if (f == "conv_1x1.bias") rc = bias(&sc.c1_b, &sc.c1_b_n);
-    else if (f == "conv_3x3.bias") rc = bias(&sc.c3_b, &sc.c3_b_n);
+    else if (f == "conv_1x1.bias") { rc = bias(&sc.c1_b, &sc.c1_b_n); keep(sc.h_c1_b); }
+    else if (f == "conv_3x3.bias") { rc = bias(&sc.c3_b, &sc.c3_b_n); keep(sc.h_c3_b); }
     else if (f == "dconv_2x2_0.weight" || f == "dconv_2x2.weight" || f == "dconv_2x2_1.weight") {
         // ggml [kW=2, kH=2, Cout, Cin]: element (kx, ky, co, ci) at ((ci·Cout + co)·2 + ky)·2 + kx;
         // cast to fp16 as sam3_conv_transpose_weight does (sam3.cpp:1083-1086)
@@ -916,6 +929,7 @@ int load_neck_tensor(s3e_model *m, const std::string &name, const RawTensor &t) 
                                CONV_BN);
         else
             rc = upload_weight_split(wf.data(), K, Cout, dst, CONV_BN);
+        if (rc == S3E_OK && scale0 && t.type == 0) (k == 1 ? sc.h_c1 : sc.h_c3) = std::move(wf);
     } else {
         return S3E_OK;
     }
@@ -950,6 +964,63 @@ int check_neck(const s3e_model *m, int which) {
     return S3E_OK;
 }
 
+// Scale 0 of a neck with F32 convs: its 1×1 (W1 [D][D], b1) feeds the 3×3
+// (W3 [D][9][D], b3) with nothing between them (sam3.cpp:3863-3921), so
+//     3×3(pad(1×1(y))) = Σ_taps y_shifted·(W3_tap·W1) + b3 + Σ_{taps inside} W3_tap·b1:
+// one 3×3 with weights W3_tap·W1 over the deconvolution's output, whose bias
+// depends only on which taps fall outside the image (zero padding), i.e. on
+// the pixel's border class (first / inner / last row × column).  Products
+// and sums in double, rounded once to f32 and split to fp16 pairs as any F32
+// conv weight; the 1×1 pass over 16·G² pixels disappears.
+int fold_neck0(s3e_model *m, int which) {
+    NeckScale &sc = m->necks[which].s[0];
+    const int64_t D = sc.c1.N;
+    if (sc.h_c1.size() != (size_t)(D * D) || sc.h_c1_b.size() != (size_t)D || sc.h_c3.size() != (size_t)(9 * D * D) ||
+        sc.h_c3_b.size() != (size_t)D)
+        return S3E_OK;  // F16 convs: the reference rounds the 1×1 output to fp16 first; keep both passes
+    std::vector<float> wf((size_t)(9 * D * D));
+    std::vector<double> acc((size_t)D), bt((size_t)(9 * D));
+    for (int64_t co = 0; co < D; co++)
+        for (int tap = 0; tap < 9; tap++) {
+            std::fill(acc.begin(), acc.end(), 0.0);
+            const float *w3 = sc.h_c3.data() + (size_t)(co * 9 * D + tap * D);
+            double b = 0.0;
+            for (int64_t c = 0; c < D; c++) {
+                const double w = w3[c];
+                const float *w1 = sc.h_c1.data() + (size_t)(c * D);
+                for (int64_t ci = 0; ci < D; ci++) acc[(size_t)ci] += w * (double)w1[ci];
+                b += w * (double)sc.h_c1_b[(size_t)c];
+            }
+            for (int64_t ci = 0; ci < D; ci++) wf[(size_t)(co * 9 * D + tap * D + ci)] = (float)acc[(size_t)ci];
+            bt[(size_t)(tap * D + co)] = b;
+        }
+    std::vector<float> b9((size_t)(9 * D));
+    for (int cy = 0; cy < 3; cy++)
+        for (int cx = 0; cx < 3; cx++)
+            for (int64_t co = 0; co < D; co++) {
+                double b = sc.h_c3_b[(size_t)co];
+                for (int ky = 0; ky < 3; ky++)
+                    for (int kx = 0; kx < 3; kx++) {
+                        const bool out = (cy == 0 && ky == 0) || (cy == 2 && ky == 2) || (cx == 0 && kx == 0) ||
+                                         (cx == 2 && kx == 2);
+                        if (!out) b += bt[(size_t)((ky * 3 + kx) * D + co)];
+                    }
+                b9[(size_t)((cy * 3 + cx) * D + co)] = (float)b;
+            }
+    int rc = upload_weight_split(wf.data(), 9 * D, D, sc.c3f, CONV_BN);
+    if (rc != S3E_OK) return rc;
+    void *p = nullptr;
+    HIP_TRY(hipMalloc(&p, b9.size() * 4));
+    m->owned.push_back(p);
+    HIP_TRY(hipMemcpy(p, b9.data(), b9.size() * 4, hipMemcpyHostToDevice));
+    sc.c3f_b = (float *)p;
+    std::vector<float>().swap(sc.h_c1);
+    std::vector<float>().swap(sc.h_c1_b);
+    std::vector<float>().swap(sc.h_c3);
+    std::vector<float>().swap(sc.h_c3_b);
+    return S3E_OK;
+}
+
 }  // namespace
 
 extern "C" void s3e_model_free(s3e_model *m) {
@@ -963,6 +1034,7 @@ extern "C" void s3e_model_free(s3e_model *m) {
             free_weight(sc.dc[1]);
             free_weight(sc.c1);
             free_weight(sc.c3);
+            free_weight(sc.c3f);
         }
     for (auto &b : m->blocks) {
         free_weight(b.qkv);
@@ -1150,7 +1222,8 @@ extern "C" int s3e_model_load(s3e_ctx *ctx, const char *path, s3e_model **out) t
     // necks: optional (an encoder-only file has none); a partial one is an error
     for (int which = 0; which < 2; which++) {
         if (m->necks[which].found == 0) continue;
-        const int rc = check_neck(m.get(), which);
+        int rc = check_neck(m.get(), which);
+        if (rc == S3E_OK) rc = fold_neck0(m.get(), which);
         if (rc != S3E_OK) return rc;
         m->necks_present |= which == 1 ? 1 : 2;
     }
@@ -1494,6 +1567,19 @@ hipError_t run_level(s3e_state *st, int which, int lvl, const float *x, hipStrea
         const Act a_1 = plane_act(act_kind_for(sc.c1.kind), st->lv_a[0], st->lv_a_cap[0], D);
         if ((err = deconv(sc.dc[0], sc.dc_b[0], x16, G, 1, a_dc)) != hipSuccess) return err;
         if ((err = deconv(sc.dc[1], sc.dc_b[1], a_dc, 2 * G, 0, a_1)) != hipSuccess) return err;
+        if (sc.c3f.q) {
+            // the 1×1 folded into the 3×3 (fold_neck0): straight from the deconvolution
+            EpiArgs e;
+            e.bias = sc.c3f_b;
+            e.bias_cls = 1;
+            e.y = st->neck_out[which][0];
+            e.ldy = D;
+            ConvGeom g;
+            g.w = g.h = side;
+            g.spt = (int)(D / 32);
+            g.zero = st->zero;
+            return launch_conv(sc.c3f, a_1, (int64_t)side * side, EPI_F32, e, &g, s);
+        }
         err = conv1(a_1, 16 * T);
     } else if (lvl == 1) {
         // 2×: deconv + bias, 1×1
