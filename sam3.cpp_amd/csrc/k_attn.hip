@@ -393,36 +393,44 @@ __global__ __launch_bounds__(NTHR, HD == 64 ? 3 : (HD == 128 ? 2 : 1)) void k_at
         if (CROP && dt * 32 >= hdo) break;
         if (out.kind == A_F6) {
             // the same Q8_0 codes in the A_F6 layout: this lane holds block
-            // positions 8g + 4·lh + i; each lane builds its fields of both
-            // parts, sends the partner the part it stores (h: lh = 0, l: lh = 1)
+            // positions 8g + 4·lh + i (i < 4), lane l ^ 32 the others.  Each
+            // value splits as q = 16h + l; one lane-half swap per pair leaves
+            // lanes 0-31 with the block's 32 h values (own in slots 8g + i,
+            // the partner's in 8g + 4 + i) and lanes 32-63 with its 32 l
+            // values, which one fp6 conversion packs into the 192-bit string
+            // of part lh
             float amax = 0.f;
 #pragma unroll
             for (int r = 0; r < 16; r++) amax = fmaxf(amax, fabsf(o[dt][r]));
             amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
             const float d = amax / 127.f;
             const float id = (amax != 0.f) ? 127.f / amax : 0.f;
-            uint32_t bh[6] = {0, 0, 0, 0, 0, 0}, bl[6] = {0, 0, 0, 0, 0, 0};
+            f32x16 ev, od;
 #pragma unroll
-            for (int g = 0; g < 4; g++)
+            for (int g = 0; g < 4; g++) {
+                float a[4], b[4];
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const int q = (int)__builtin_rintf(o[dt][4 * g + i] * id);
-                    const int hq = f6_hi(q);
-                    const uint32_t ch = f6_code(hq), cl = f6_code(q - 16 * hq);
-                    const int at = 6 * (8 * g + 4 * lh + i);
-                    bh[at / 32] |= ch << (at % 32);
-                    bl[at / 32] |= cl << (at % 32);
-                    if (at % 32 > 26) {
-                        bh[at / 32 + 1] |= ch >> (32 - at % 32);
-                        bl[at / 32 + 1] |= cl >> (32 - at % 32);
-                    }
+                    float hv, lv;
+                    f6_split(o[dt][4 * g + i], id, hv, lv);
+                    // lanes 0-31 keep hv and receive the partner's hv; lanes
+                    // 32-63 receive the partner's lv and keep lv
+                    const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, hv),
+                                                                     __builtin_bit_cast(uint32_t, lv), false, false);
+                    a[i] = __builtin_bit_cast(float, (uint32_t)sw[0]);
+                    b[i] = __builtin_bit_cast(float, (uint32_t)sw[1]);
                 }
-            uint32_t mine[6];
-#pragma unroll
-            for (int j = 0; j < 6; j++) {
-                const uint32_t other = __shfl_xor(lh ? bh[j] : bl[j], 32, 64);
-                mine[j] = (lh ? bl[j] : bh[j]) | other;
+                // slot 2k from ev[k], 2k + 1 from od[k]: slots 8g .. 8g + 3 ← a, 8g + 4 .. 8g + 7 ← b
+                ev[4 * g] = a[0];
+                od[4 * g] = a[1];
+                ev[4 * g + 1] = a[2];
+                od[4 * g + 1] = a[3];
+                ev[4 * g + 2] = b[0];
+                od[4 * g + 2] = b[1];
+                ev[4 * g + 3] = b[2];
+                od[4 * g + 3] = b[3];
             }
+            const u32x6 mine = pack_bf6(ev, od);
             if (ovalid) {
                 const int64_t blk = (colbase + dt * 32) / QK;
                 uint64_t *base = (uint64_t *)out.x;
