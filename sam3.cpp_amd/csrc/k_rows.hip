@@ -213,6 +213,8 @@ __global__ __launch_bounds__(64 * LNW) void k_layernorm_f6(const float *__restri
                                                       const float *__restrict__ b, Act o) {
     __shared__ __attribute__((aligned(16))) uint64_t stg[32 * NIT * LNF6_BSTRIDE];
     __shared__ __attribute__((aligned(16))) uint16_t stgd[8 * NIT][LNF6_ROWS][4];
+    // gamma and beta, read once per work-group (every wave's row uses all of them)
+    __shared__ __attribute__((aligned(16))) float swb[WB ? 2 * 1024 * NIT : 4];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nseg = (int)(E / 16), nblk = (int)(E / 32);
     const int64_t r0 = (int64_t)blockIdx.x * LNF6_ROWS;
@@ -247,6 +249,13 @@ __global__ __launch_bounds__(64 * LNW) void k_layernorm_f6(const float *__restri
     };
     constexpr int RPW = LNF6_ROWS / LNW;  // rows per wave
     if (r0 + wave * RPW < M) load_row(r0 + wave * RPW);
+    if constexpr (WB) {
+        for (int i = threadIdx.x; i < (int)E / 4; i += 64 * LNW) {
+            ((float4 *)swb)[i] = ((const float4 *)w)[i];
+            ((float4 *)swb)[256 * NIT + i] = ((const float4 *)b)[i];
+        }
+        __syncthreads();
+    }
     for (int k = 0; k < RPW; k++) {
         const int rr = wave * RPW + k;  // row within the group
         const int64_t row = r0 + rr;
@@ -288,8 +297,8 @@ __global__ __launch_bounds__(64 * LNW) void k_layernorm_f6(const float *__restri
             for (int j4 = 0; j4 < 4; j4++) {
                 float wv[4] = {1.f, 1.f, 1.f, 1.f}, bv[4] = {0.f, 0.f, 0.f, 0.f};
                 if constexpr (WB) {
-                    const float4 wf = ((const float4 *)w)[4 * seg + j4];
-                    const float4 bf = ((const float4 *)b)[4 * seg + j4];
+                    const float4 wf = ((const float4 *)swb)[4 * seg + j4];
+                    const float4 bf = ((const float4 *)swb)[256 * NIT + 4 * seg + j4];
                     wv[0] = wf.x; wv[1] = wf.y; wv[2] = wf.z; wv[3] = wf.w;
                     bv[0] = bf.x; bv[1] = bf.y; bv[2] = bf.z; bv[3] = bf.w;
                 }
