@@ -9,6 +9,8 @@
  *     asan_check MODEL.ggml [...]     also load each model and run its
  *                                     encoder (ViT + necks, or Hiera + FPN)
  *                                     and its memory attention, if present
+ *     asan_check --load-only FILE...  only load (and free) each file: for
+ *                                     damaged copies of a model
  */
 #include <math.h>
 #include <stdint.h>
@@ -264,6 +266,18 @@ static void model(const char *path) {
 }
 
 int main(int argc, char **argv) {
+    if (argc > 1 && strcmp(argv[1], "--load-only") == 0) {
+        /* damaged files: loading must end in a clean refusal or a model that
+           frees cleanly, with no sanitizer report either way */
+        int refused = 0;
+        for (int i = 2; i < argc; i++) {
+            orc_model *m = orc_model_load(argv[i]);
+            if (m) orc_model_free(m);
+            else refused++;
+        }
+        printf("asan_check: load-only ok (%d of %d refused)\n", refused, argc - 2);
+        return 0;
+    }
     formats();
     products();
     operators();

@@ -161,23 +161,36 @@ orc_model *orc_model_load(const char *path) {
         m->hp.visual_only = hpv[26];
     }
 tensors:
+    /* every record takes at least its 16-byte header: a count the file
+       cannot hold is refused before anything is allocated for it */
+    if (n_tensors < 0 || (size_t)n_tensors > (fsize - off) / 16) ORC_FAIL("bad tensor count %d", n_tensors);
     m->t = (orc_tensor *)calloc((size_t)(n_tensors > 0 ? n_tensors : 1), sizeof(orc_tensor));
+    if (!m->t) ORC_FAIL("out of memory");
     for (int ti = 0; ti < n_tensors; ti++) {
         int32_t n_dims, name_len, dtype;
         RD32(n_dims); RD32(name_len); RD32(dtype);
         if (n_dims < 1 || n_dims > 4) ORC_FAIL("bad n_dims %d", n_dims);
+        if (orc_type_size(dtype) == 0) ORC_FAIL("tensor %d: unsupported dtype %d", ti, dtype);
         orc_tensor *t = &m->t[m->n_tensors];
         int64_t n_el = 1;
         for (int i = 0; i < 4; i++) t->ne[i] = 1;
-        for (int i = 0; i < n_dims; i++) { int32_t d; RD32(d); t->ne[i] = d; n_el *= d; }
-        if (name_len <= 0 || name_len >= (int)sizeof t->name || off + (size_t)name_len > fsize) ORC_FAIL("bad name length");
+        for (int i = 0; i < n_dims; i++) {
+            int32_t d;
+            RD32(d);
+            /* positive, and no more elements than the file has bits (so the
+               products below cannot overflow) */
+            if (d <= 0 || n_el > (int64_t)(8 * fsize) / d) ORC_FAIL("tensor %d: bad dimension %d", ti, d);
+            t->ne[i] = d;
+            n_el *= d;
+        }
+        if (t->ne[0] % orc_blck_size(dtype) != 0) ORC_FAIL("tensor %d: ne0 %lld not a block multiple", ti, (long long)t->ne[0]);
+        if (name_len <= 0 || name_len >= (int)sizeof t->name || (size_t)name_len > fsize - off) ORC_FAIL("bad name length");
         memcpy(t->name, map + off, (size_t)name_len);
         t->name[name_len] = 0;
         off += (size_t)name_len;
         off += (32 - off % 32) % 32;
         const size_t bytes = orc_row_size(dtype, t->ne[0]) * (size_t)(n_el / t->ne[0]);
-        if (orc_type_size(dtype) == 0) ORC_FAIL("tensor %s: unsupported dtype %d", t->name, dtype);
-        if (off + bytes > fsize) ORC_FAIL("tensor %s: truncated data", t->name);
+        if (off > fsize || bytes > fsize - off) ORC_FAIL("tensor %s: truncated data", t->name);
         const uint8_t *src = map + off;
         off += bytes;
         /* encoder backbones, necks and the memory attention only */
@@ -189,6 +202,7 @@ tensors:
         t->type = rt;
         const size_t out_bytes = orc_row_size(rt, t->ne[0]) * (size_t)(n_el / t->ne[0]);
         t->data = malloc(out_bytes);
+        if (!t->data) ORC_FAIL("out of memory");
         if (rt == dtype) {
             memcpy(t->data, src, bytes);
         } else if (rt == ORC_TYPE_F32) {
@@ -201,6 +215,8 @@ tensors:
         } else if (rt == ORC_TYPE_F16 && dtype == ORC_TYPE_F32) {
             orc_fp32_to_fp16_row((const float *)src, (uint16_t *)t->data, n_el);
         } else {
+            free(t->data);
+            t->data = NULL;
             ORC_FAIL("tensor %s: unsupported conversion %d -> %d", t->name, dtype, rt);
         }
         m->n_tensors++;

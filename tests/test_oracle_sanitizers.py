@@ -13,6 +13,7 @@ import subprocess
 import pytest
 
 import s3e
+from model_damage import damaged
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ORACLE = os.path.join(ROOT, "oracle")
@@ -65,3 +66,23 @@ def test_encoders_clean(asan_bin, tmp_path):
     assert out.count("ViT encoder + trk neck") == 2 and "ViT encoder + det neck" in out
     assert "Hiera encoder + FPN" in out
     assert out.count("memory attention") == 2
+
+
+def test_damaged_files_load_clean(asan_bin, tmp_path):
+    """The oracle's loader on truncated and corrupted copies of a ViT and a
+    Hiera file: refusals or models that free cleanly, no memory errors."""
+    vq = str(tmp_path / "vit.ggml")
+    hb = str(tmp_path / "hiera.ggml")
+    s3e.synth_write(vq, img_size=84, patch=14, embed_dim=64, depth=2, heads=2, mlp_ratio_x1000=4000, window=3,
+                    global_idx=(1,), ftype="q4_0", seed=3, std=0.05, neck=2, neck_dim=64, mem_attn_layers=1)
+    s3e.synth_write_sam2(hb, "hiera_t", img_size=64, ftype="q8_0", seed=5, std=0.05, mem_attn_layers=1,
+                         embed_dim=32, stages=(1, 1, 1, 1), global_idx=(), window_spec=(4, 4, 2, 2))
+    files = []
+    for src in (vq, hb):
+        for what, b in damaged(open(src, "rb").read()):
+            p = tmp_path / f"{len(files)}_{what}.ggml"
+            p.write_bytes(b)
+            files.append(str(p))
+    r = _run(asan_bin, "--load-only", *files)
+    assert r.returncode == 0, r.stderr[-4000:]
+    assert f"of {len(files)} refused" in r.stdout
