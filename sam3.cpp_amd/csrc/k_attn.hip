@@ -16,10 +16,12 @@
 // keys of each K=16 MFMA step are the ones that lane already holds; thanks to
 // the vt_slot order the matching Vᵀ A-operand is one 16-byte LDS read.
 //
-// K and Vᵀ tiles of 64 keys stream through a 2-deep LDS ring filled by
-// global_load_lds_dwordx4 (rows of 128 bytes, 16-byte chunks XOR-swizzled
-// by row for the 64-bank LDS): tile j+1 is in flight while tile j is used,
-// one barrier per tile.
+// K and Vᵀ tiles of 32 keys stream through a 2-deep LDS ring filled by
+// buffer_load_dwordx4 ... lds (rows of 128 bytes, 16-byte chunks
+// XOR-swizzled by row for the 64-bank LDS): tile j+1 is in flight while tile
+// j is used, one barrier per tile.  The tile's position lives in the
+// buffer descriptor (scalar registers), so issuing a tile costs no vector
+// address arithmetic.
 //
 // Precision.  SPLIT = false rounds Q, K, V and P to fp16 (fp32 accumulate).
 // SPLIT = true carries every operand as an fp16 pair x = hi + lo (hi =
@@ -35,7 +37,7 @@
 // exceeds it by more than 8 (p ≤ 2^8 meanwhile, well inside fp16 and fp32),
 // so the rescale of Oᵀ by exp2(m_old − m_new) is rare; the result is the
 // same quotient.  The two lanes sharing a query (l, l^32) agree on m through
-// one cross-half shuffle per tile and add their partial l at the end.
+// one lane-half swap per tile and add their partial l at the end.
 //
 // The result leaves the kernel already in the next GEMM's activation format
 // (Q8_0 / Q8_1 per 32-d block exactly as ggml quantizes a row, fp16, or
@@ -154,39 +156,62 @@ __global__ __launch_bounds__(NTHR, HD == 64 ? 3 : (HD == 128 ? 2 : 1)) void k_at
     // DMA: per plane, a K tile is runs of 1 KB (8 rows of 128 B, or 4 of 256 B)
     // and a Vᵀ tile runs of 1 KB (16 rows of 64 B); wave w moves runs
     // w·RUNS .. w·RUNS + RUNS − 1.  A lane writes the 16 bytes at 16·lane of its
-    // run and fetches the chunk that belongs there.  Rows past the keys are
-    // clamped onto real ones (their scores are masked, and Vᵀ keys past Nkv
-    // are zero).
-    auto issue_k = [&](int tt) {
-        uint8_t *L = Kring + (tt & 1) * KBUF;
+    // run and fetches the chunk that belongs there.  The loads go through
+    // buffer descriptors whose base and record count carry the tile's
+    // position (scalar arithmetic), so each lane's offset is a constant and
+    // reads past the record count return zeros: K rows past the keys (their
+    // scores are masked).  In a tile that reaches past a Vᵀ row's vt_ld keys
+    // those chunks are clamped onto the row's last 8 keys (finite, and their
+    // probabilities are 0), never into the next row, which may be an
+    // unwritten padding row.
+    auto dma = [&](const void *base, uint32_t nrec, uint8_t *ldsp, int lane_off) {
+        const __amdgpu_buffer_rsrc_t r =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)nrec, 0x00020000);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, LDS_PTR(ldsp), 16, lane_off, 0, 0, 0);
+    };
+    int k_lane[G::KRUNS], v_lane[G::VRUNS];
+#pragma unroll
+    for (int j = 0; j < G::KRUNS; j++) {
         constexpr int RPR = 1024 / G::ROWK;      // rows per run
         constexpr int CPR = G::ROWK / 16;        // chunks per row
+        const int r = RPR * (wave * G::KRUNS + j) + lane / CPR;
+        k_lane[j] = r * G::ROWK + (((lane % CPR) ^ swzk_hd<HD>(r)) << 4);
+    }
+    int v_row[G::VRUNS], v_ch[G::VRUNS];
 #pragma unroll
-        for (int j = 0; j < G::KRUNS; j++) {
-            const int run = wave * G::KRUNS + j;
-            const int r = RPR * run + lane / CPR;
-            const int ch = (lane % CPR) ^ swzk_hd<HD>(r);
-            const int64_t key = min((t0 + tt) * KT + r, a.Nkv - 1);
+    for (int j = 0; j < G::VRUNS; j++) {
+        const int r = 16 * (wave * G::VRUNS + j) + (lane >> 2);
+        v_row[j] = r * ldv * 2;
+        v_ch[j] = (lane & 3) ^ swzv(r);
+        v_lane[j] = v_row[j] + (v_ch[j] << 4);
+    }
+    auto issue_k = [&](int tt) {
+        uint8_t *L = Kring + (tt & 1) * KBUF;
+        const int tile = t0 + tt;
+        const uint32_t nrec = (uint32_t)min(a.Nkv - tile * KT, KT) * G::ROWK;
 #pragma unroll
-            for (int pl = 0; pl < NP; pl++) {
-                const _Float16 *src = (pl == 0 ? a.k : a.k_lo) + koff + key * HD + ch * 8;
-                __builtin_amdgcn_global_load_lds((const void *)src, LDS_PTR(L + pl * KPL + run * 1024), 16, 0, 0);
-            }
+        for (int pl = 0; pl < NP; pl++) {
+            const _Float16 *base = (pl == 0 ? a.k : a.k_lo) + koff + (int64_t)tile * KT * HD;
+#pragma unroll
+            for (int j = 0; j < G::KRUNS; j++) dma(base, nrec, L + pl * KPL + (wave * G::KRUNS + j) * 1024, k_lane[j]);
         }
     };
     auto issue_v = [&](int tt) {
         uint8_t *L = Vring + (tt & 1) * VBUF;
+        const int tile = t0 + tt;
+        const uint32_t nrec = (uint32_t)(HD * ldv - tile * KT) * 2;
+        int off[G::VRUNS];
 #pragma unroll
-        for (int j = 0; j < G::VRUNS; j++) {
-            const int run = wave * G::VRUNS + j;
-            const int r = 16 * run + (lane >> 2);
-            const int ch = (lane & 3) ^ swzv(r);
-            const int k0 = min((t0 + tt) * KT + ch * 8, ldv - 8);
+        for (int j = 0; j < G::VRUNS; j++) off[j] = v_lane[j];
+        if (tile * KT + KT > ldv) {  // the row's end falls inside this tile
 #pragma unroll
-            for (int pl = 0; pl < NP; pl++) {
-                const _Float16 *src = (pl == 0 ? a.vt : a.vt_lo) + voff + (int64_t)r * ldv + k0;
-                __builtin_amdgcn_global_load_lds((const void *)src, LDS_PTR(L + pl * VPL + run * 1024), 16, 0, 0);
-            }
+            for (int j = 0; j < G::VRUNS; j++) off[j] = v_row[j] + 2 * min(8 * v_ch[j], ldv - 8 - tile * KT);
+        }
+#pragma unroll
+        for (int pl = 0; pl < NP; pl++) {
+            const _Float16 *base = (pl == 0 ? a.vt : a.vt_lo) + voff + (int64_t)tile * KT;
+#pragma unroll
+            for (int j = 0; j < G::VRUNS; j++) dma(base, nrec, L + pl * VPL + (wave * G::VRUNS + j) * 1024, off[j]);
         }
     };
 
@@ -226,12 +251,15 @@ __global__ __launch_bounds__(NTHR, HD == 64 ? 3 : (HD == 128 ? 2 : 1)) void k_at
                 o[dt] = mfma(vh, ph[jj], o[dt]);
             }
     };
-    // scaled maximum over the tile's 32 keys (both lane halves)
+    // scaled maximum over the tile's 32 keys (both lane halves): one lane-half
+    // swap leaves every lane with {own, partner} in some order, no LDS trip
     auto tmax = [&](const v16f &sv) {
         float m = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 16; r++) m = fmaxf(m, sv[r]);
-        return fmaxf(m, __shfl_xor(m, 32, 64)) * c;
+        const uint32_t mb = __builtin_bit_cast(uint32_t, m);
+        const auto sw = __builtin_amdgcn_permlane32_swap(mb, mb, false, false);
+        return fmaxf(__builtin_bit_cast(float, (uint32_t)sw[0]), __builtin_bit_cast(float, (uint32_t)sw[1])) * c;
     };
     // keys past Nkv score −inf (only the last, partial tile)
     auto mask = [&](v16f &sv, int tt) {
