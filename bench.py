@@ -437,7 +437,9 @@ def attention_fp16(s3e, ctx, ev, reps: int = 20) -> dict:
         flops = 4.0 * B * nh * N * N * D
         tf = flops / (us * 1e-6) / 1e12
         res[name] = {"windows": B, "tokens": N, "heads": nh, "us": round(us, 1), "TFLOPs": round(tf, 1),
-                     "frac_fp16_peak": round(tf / 2500.0, 4)}
+                     "frac_fp16_peak": round(tf / 2500.0, 4),
+                     "scope": "whole s3e_flash_attn_ext call: f32->fp16 operand conversion, attention, and the "
+                              "call's own synchronisation"}
         log(f"attention fp16 {name} {B}x{nh}x{N}: {us:.1f} us, {tf:.1f} TFLOP/s")
         for b in (q, k, v, o):
             b.free()
