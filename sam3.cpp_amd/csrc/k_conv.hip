@@ -14,10 +14,11 @@
 //
 // Tiling.  A work-group computes 128 pixels × 256 channels with 8 waves
 // (2 along M × 4 along N, 64×64 each: 2×2 MFMA tiles, so every A and B
-// fragment read from LDS feeds two MFMAs, four with the split planes).  K
-// advances in stages of 32 elements (64-byte rows per plane), streamed by
-// global_load_lds_dwordx4 through a 3-deep LDS ring: two stages are in
-// flight while one is consumed.  64-byte rows put four rows in one 256-byte
+// fragment read from LDS feeds two MFMAs, four with the split planes), or
+// 256 pixels with 16 waves for the large split 3×3.  K advances in stages
+// of 32 elements (64-byte rows per plane), streamed by
+// global_load_lds_dwordx4 through a 3-deep LDS ring (2-deep for 256
+// pixels): two stages (one) in flight while one is consumed.  64-byte rows put four rows in one 256-byte
 // bank cycle; 16-byte chunk c of row r sits at slot c ^ ((r >> 2) & 3), which
 // keeps the lane-ordered DMA writes and the 16-row MFMA operand reads free of
 // bank conflicts.
@@ -41,13 +42,17 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 
 #define LDS_PTR(p) ((__attribute__((address_space(3))) void *)(p))
 
-constexpr int BM = 128, BN = 256, WAVES = 8, NTH = 64 * WAVES;
+constexpr int BN = 256;
 constexpr int ROWB = 64;   // bytes per row per stage and plane (32 fp16)
-constexpr int NBUF = 3;
-constexpr int WM = 2, WN = 4, MT = 2, NT = 2;  // waves along M/N, 32×32 tiles per wave
+constexpr int WN = 4, MT = 2, NT = 2;  // waves along N, 32×32 tiles per wave
 
-template <bool SPLIT>
+// Tile height BM = 128 (8 waves, 3-deep ring) or 256 (16 waves, 2-deep ring:
+// every pixel tile streams the whole weight matrix, so taller tiles read it
+// half as often; used where there are enough pixels to fill the chip).
+template <bool SPLIT, int BM_>
 struct Lay {
+    static constexpr int BM = BM_, WAVES = BM / 16, NTH = 64 * WAVES, WM = BM / 64;
+    static constexpr int NBUF = BM == 256 ? 2 : 3;
     static constexpr int planes = SPLIT ? 2 : 1;
     static constexpr int A = BM * ROWB, B = BN * ROWB;  // bytes of one plane
     static constexpr int OFF_A = 0, OFF_ALO = A;
@@ -84,9 +89,13 @@ __device__ __forceinline__ void store_act(const Act &o, int64_t row, int64_t col
     if (o.kind == A_F16X2) ((_Float16 *)o.lo)[i] = (_Float16)(v - (float)h);
 }
 
-template <bool SPLIT, int CONV, int EPI>
-__global__ __launch_bounds__(NTH, SPLIT ? 1 : 2) void k_conv(ConvParams p) {
-    using L = Lay<SPLIT>;
+template <int BM_>
+constexpr int conv_nth = 64 * (BM_ / 16);  // threads of a work-group (Lay::NTH)
+
+template <bool SPLIT, int CONV, int EPI, int BM_>
+__global__ __launch_bounds__(conv_nth<BM_>, (SPLIT || BM_ == 256) ? 1 : 2) void k_conv(ConvParams p) {
+    using L = Lay<SPLIT, BM_>;
+    constexpr int BM = L::BM, WAVES = L::WAVES, NBUF = L::NBUF;
     __shared__ __attribute__((aligned(1024))) uint8_t lds[L::LDS];
 
     // ---- tile: each XCD (ids dealt round-robin over 8) takes a contiguous
@@ -228,12 +237,22 @@ __global__ __launch_bounds__(NTH, SPLIT ? 1 : 2) void k_conv(ConvParams p) {
     // ---- main loop: stages s+1 and s+2 in flight while stage s is consumed
     const int ns = p.nstages;
     issue(0);
-    if (ns > 1) issue(1);
-    for (int s = 0; s < ns; s++) {
-        if (s + 1 < ns) wait_and_barrier<L::NLOAD>();
-        else wait_and_barrier<0>();
-        if (s + 2 < ns) issue(s + 2);
-        compute(s);
+    if constexpr (NBUF == 3) {
+        if (ns > 1) issue(1);
+        for (int s = 0; s < ns; s++) {
+            if (s + 1 < ns) wait_and_barrier<L::NLOAD>();
+            else wait_and_barrier<0>();
+            if (s + 2 < ns) issue(s + 2);
+            compute(s);
+        }
+    } else {
+        // 2-deep: stage s landed and stage s−1's buffer released, then s+1 in
+        // flight while s is consumed
+        for (int s = 0; s < ns; s++) {
+            wait_and_barrier<0>();
+            if (s + 1 < ns) issue(s + 1);
+            compute(s);
+        }
     }
 
     // ---- epilogue from the accumulators: lane holds column lr of each 32×32
@@ -280,18 +299,24 @@ __global__ __launch_bounds__(NTH, SPLIT ? 1 : 2) void k_conv(ConvParams p) {
     }
 }
 
-template <bool SPLIT, int CONV, int EPI>
+template <bool SPLIT, int CONV, int EPI, int BM = 128>
 hipError_t launch_one(ConvParams &p, hipStream_t st) {
     p.tiles_m = (p.M + BM - 1) / BM;
     p.ntiles = p.tiles_m * p.tiles_n;
     const int grid = ((p.ntiles + 7) / 8) * 8;
-    hipLaunchKernelGGL((k_conv<SPLIT, CONV, EPI>), dim3(grid), dim3(NTH), 0, st, p);
+    hipLaunchKernelGGL((k_conv<SPLIT, CONV, EPI, BM>), dim3(grid), dim3(Lay<SPLIT, BM>::NTH), 0, st, p);
     return hipGetLastError();
 }
 
 template <bool SPLIT>
 hipError_t dispatch(Epi epi, bool conv3, ConvParams &p, hipStream_t st) {
-    if (conv3) return epi == EPI_F32 ? launch_one<SPLIT, 1, EPI_F32>(p, st) : hipErrorInvalidValue;
+    if (conv3) {
+        if (epi != EPI_F32) return hipErrorInvalidValue;
+        // split 3×3 with more than two 128-pixel tiles per CU: 256-pixel tiles
+        if constexpr (SPLIT)
+            if (p.M > 128 * 512) return launch_one<SPLIT, 1, EPI_F32, 256>(p, st);
+        return launch_one<SPLIT, 1, EPI_F32>(p, st);
+    }
     switch (epi) {
         case EPI_F32: return launch_one<SPLIT, 0, EPI_F32>(p, st);
         case EPI_ACT: return launch_one<SPLIT, 0, EPI_ACT>(p, st);
