@@ -630,8 +630,8 @@ def main() -> int:
     ap.add_argument("--sam2-run", default=None, help="with --only sam2: one encoder, e.g. hiera_t:f16")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (every run here uses one "
-              f"MI355X; the path shards by frame, see DESIGN.md)", file=sys.stderr)
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the encoder shards by "
+              f"frame: one process per GPU, whole frames dealt round-robin, no collective)", file=sys.stderr)
         return 2
     import s3e
 

@@ -2,7 +2,7 @@
  * asan_check.c — drives every entry point of the CPU oracle once on small,
  * odd-sized inputs, for the AddressSanitizer / UndefinedBehaviorSanitizer
  * build (`make -C oracle asan`).  TEST INFRASTRUCTURE ONLY, like the rest of
- * oracle/: the sanitizers are the checker here; the program itself only
+ * oracle/: the sanitizers do the checking here; the program itself only
  * checks that every output is finite.
  *
  *     asan_check                      formats, products and operators

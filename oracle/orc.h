@@ -5,10 +5,11 @@
  * that sam3.cpp's encoder graph performs through ggml's CPU backend
  * (ggml_mul_mat, ggml_flash_attn_ext, ggml_norm, ggml_gelu_erf, RoPE,
  * window partition, patch-embed conv).  Only tests/, __graft_entry__.smoke()
- * and bench.py's cpu_baseline leg may load it, and only as the checker or
- * the timed CPU baseline; the product path never links or calls it.
+ * and bench.py's cpu_baseline leg may load it, and only as the reference
+ * results to compare against or the timed CPU baseline; the product path
+ * never links or calls it.
  *
- * ggml itself is not available to this build (the submodule referenced by
+ * ggml itself is not available in this repository (the submodule referenced by
  * .gitmodules:1-3 is empty), so every ggml-internal behaviour restated here
  * is marked [ext] at its definition, with the public ggml source it follows.
  *

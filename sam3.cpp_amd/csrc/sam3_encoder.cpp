@@ -61,7 +61,7 @@ bool read_magic(const std::string &path, uint32_t *magic) {
 
 std::shared_ptr<sam3_model> sam3_load_model(const sam3_params &params) try {
     if (!params.use_gpu) {
-        fprintf(stderr, "%s: this build encodes on the MI355X only (use_gpu = false)\n", __func__);
+        fprintf(stderr, "%s: this encoder runs on the MI355X only (use_gpu = false)\n", __func__);
         return nullptr;
     }
     uint32_t magic = 0;

@@ -1,6 +1,6 @@
 """ctypes access to the CPU oracle (oracle/liboracle.so) for the tests.
 
-The oracle is the checker: a C restatement of ggml's CPU arithmetic on the
+The oracle is what the GPU results are compared against: a C restatement of ggml's CPU arithmetic on the
 sam3.cpp encoder path.  Only tests/, __graft_entry__.smoke() and bench.py's
 cpu_baseline leg load it.
 """

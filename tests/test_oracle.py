@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/) before the GPU results are compared against it.
 
 Each oracle function is checked against something it does not compute itself:
 hand-derived golden vectors (tests/golden/quant_golden.json), numpy's IEEE
