@@ -102,6 +102,31 @@ def test_c4_block(c4, ctx, bi):
     assert rl <= (2e-3 if ft == "f16" else 1e-3)
 
 
+def test_c4_neck_on_oracle_input(c4, ctx):
+    """The tracker neck at its real size on a given backbone output (72² tokens
+    of 1024), against the oracle's neck on the same input: levels of 288²,
+    144², 72² and 36².  Quantized files hold the neck in F32, computed on split
+    fp16 pairs (the 288² level's 3×3 in 256-pixel tiles, the others in 128);
+    F16 files in fp16."""
+    ft, om, gm, st, img, chw, x0 = c4
+    G, E = IMG // 14, 1024
+    x = np.random.default_rng(5).standard_normal((G * G, E)).astype(np.float32)
+    print(f"C4 {ft} neck on the oracle's input", flush=True)
+    xd = ctx.to_device(x)
+    st.run_neck(xd)
+    ctx.sync()
+    ref = om.neck(x, "trk")
+    tol = 2e-3 if ft == "f16" else 1e-4
+    for lvl in range(4):
+        got = st.tensor(f"neck_trk_{lvl}")
+        assert got.shape == ref[lvl].shape, lvl
+        rl, ma = _report(f"C4 {ft} neck_trk_{lvl} (oracle input)", got, ref[lvl])
+        assert rl <= tol, lvl
+        if ft != "f16":
+            assert ma <= 5e-3, lvl
+    xd.free()
+
+
 def test_c4_encode(c4, ctx):
     """F16: the specification end to end.  Quantized: Q4_0 only (the oracle's
     whole encoder takes about a minute per weight type on the host), against
