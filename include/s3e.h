@@ -128,9 +128,13 @@ int s3e_mul_mat_noalloc(s3e_ctx *ctx, const s3e_weight *w, const float *X, int64
  * s3e_quantize_rows for K = W's ne0 (layout there).  Launches the GEMM kernel
  * only, so it is also the entry point to time the kernel alone.  Products of
  * at most 64 rows with Q4_0/Q4_1/Q8_0/F16 weights run on the weight-streaming
- * kernel, whose block-interleaved copy of the weight is made (allocated and
- * packed on the device) by the first such call on that weight; every other
- * call allocates nothing. */
+ * kernel.  s3e_weight_upload makes everything that kernel needs: the
+ * block-interleaved copy of the weight and room in the uploading context's
+ * workspace for the partial sums of a K-split product of up to 64 rows.  So
+ * s3e_mul_mat_q allocates nothing and does not synchronise; on a context
+ * other than the upload's, a small product whose partial sums do not fit
+ * that context's workspace runs with K unsplit (same kernel, results equal
+ * up to fp32 summation order). */
 int s3e_mul_mat_q(s3e_ctx *ctx, const s3e_weight *w, const void *xq, const uint16_t *d,
                   const uint16_t *s, int64_t M, const float *bias, float *Y);
 /* No counterpart in the reference: s3e_mul_mat_q for Q4_0 weights with
@@ -319,8 +323,9 @@ int s3e_encode_vit_chw(s3e_state *st, const float *chw_device);
  * references): "vit.patch_embed.proj.weight" and the block linears
  * "vit.blocks.<i>.{attn.qkv,attn.proj,mlp.lin1,mlp.lin2}.{weight,bias}".
  * Weights come back only when stored F16 or F32 (quantized ones are
- * repacked on the device: S3E_ERR_UNSUPPORTED).  type and ne (ggml order)
- * are always written; host may be NULL to query them. */
+ * repacked on the device: S3E_ERR_UNSUPPORTED, with type and ne still
+ * written).  type and ne (ggml order) are written for every tensor found;
+ * host may be NULL to query them. */
 int s3e_model_tensor_get(const s3e_model *m, const char *name, int *type, int64_t ne[4], void *host, size_t bytes);
 /* Neck stage hook: run the model's necks on a backbone output given on the
  * device (W*H rows of E f32), filling the state's neck_* tensors exactly as

@@ -368,6 +368,10 @@ extern "C" int s3e_memcpy_d2h(s3e_ctx *ctx, void *dst, const void *src, size_t b
 } S3E_CATCH("s3e_memcpy_d2h")
 
 // ---- ggml_mul_mat ---------------------------------------------------------
+namespace {
+hipError_t sm_prepare(s3e_ctx *ctx, const s3e_weight *w);
+}  // namespace
+
 extern "C" int s3e_weight_upload(s3e_ctx *ctx, int type, int64_t ne0, int64_t ne1, const void *host_data,
                                  size_t nbytes, s3e_weight **out) try {
     if (!ctx || !host_data || !out) { set_error("s3e_weight_upload: NULL argument"); return S3E_ERR_INVALID; }
@@ -379,6 +383,14 @@ extern "C" int s3e_weight_upload(s3e_ctx *ctx, int type, int64_t ne0, int64_t ne
     if (rc != S3E_OK) {
         delete w;
         return rc;
+    }
+    // everything a product of at most 64 rows needs is made here, so that
+    // later products on this weight and context allocate nothing
+    const hipError_t e = sm_prepare(ctx, w);
+    if (e != hipSuccess) {
+        s3e_weight_free(w);
+        set_error("s3e_weight_upload: %s", hipGetErrorString(e));
+        return S3E_ERR_HIP;
     }
     *out = w;
     return S3E_OK;
@@ -486,12 +498,25 @@ hipError_t run_mul_mat(s3e_ctx *ctx, const s3e_weight *w, const Act &a, int64_t 
     const int cgs = sm_wgs(W.N, SM_KS);
     sa.kg = sm_kgroups(W);
     sa.rt = (SM_ROW_TILES && M > 32) ? 2 : 1;
-    if (sa.kg > 1) {
-        e = sk_workspace(ctx, (int64_t)sa.kg * M * W.N);
-        if (e != hipSuccess) return e;
-        sa.part = ctx->sk_part;
-    }
+    // the workspace was sized when the weight was uploaded on this context;
+    // a context that has not seen the weight before runs it unsplit rather
+    // than allocating inside the call
+    if (sa.kg > 1 && (int64_t)sa.kg * M * W.N > ctx->sk_part_cap) sa.kg = 1;
+    if (sa.kg > 1) sa.part = ctx->sk_part;
     return launch_gemm_sm(W.kind, sa, cgs * sa.kg * sa.rt, SM_KS, st);
+}
+
+// Called once per uploaded weight of a small-M type: the weight's
+// block-interleaved copy and room in the context's split workspace for the
+// partial sums of its largest small-M product (64 rows).
+hipError_t sm_prepare(s3e_ctx *ctx, const s3e_weight *w) {
+    const Weight &W = w->w;
+    if (!sm_eligible(W, 64)) return hipSuccess;
+    const uint8_t *wsm = nullptr;
+    hipError_t e = sm_weights(w, ctx->stream, &wsm);
+    if (e != hipSuccess) return e;
+    const int kg = sm_kgroups(W);
+    return kg > 1 ? sk_workspace(ctx, (int64_t)kg * 64 * W.N) : hipSuccess;
 }
 
 }  // namespace
@@ -1992,6 +2017,7 @@ extern "C" int s3e_model_tensor_get(const s3e_model *m, const char *name, int *t
         return S3E_OK;
     }
     if (w->kind != WK_F16 && w->kind != WK_F32) {
+        *type = w->ggml_type;  // the S3E_TYPE_* values are ggml's type ids
         set_error("s3e_model_tensor_get: '%s' is quantized; only F16 and F32 weights are returned", name);
         return S3E_ERR_UNSUPPORTED;
     }

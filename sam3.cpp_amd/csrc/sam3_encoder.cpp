@@ -374,101 +374,106 @@ bool sam3_test_run_vit_block_stage(const sam3_model &model, int block_idx, sam3_
                      });
 } SAM3_CATCH(false)
 
-// sam3.cpp:6512-6574: fp16 input and kernel, one f32 (or double) sum per output
+// sam3.cpp:6512-6574: the patch embedding as a plain product on the host —
+// input and kernel rounded to fp16, one f32 (or double) sum per output
 bool sam3_test_run_patch_mulmat_host_ref(const sam3_model &model, const float *input_data, const int64_t input_ne[4],
                                          bool use_double_accum, std::vector<float> &output_data,
                                          int64_t output_ne[4]) try {
     if (!input_data || !model.enc) return false;
-    int64_t ne[4];
-    for (int i = 0; i < 4; i++) ne[i] = (input_ne && input_ne[i] > 0) ? input_ne[i] : 1;
-    std::vector<uint8_t> w;
-    int64_t wne[4];
-    if (!model_tensor(model, "vit.patch_embed.proj.weight", S3E_TYPE_F16, w, wne, __func__)) return false;
-    const int64_t patch_k = wne[0] * wne[1] * wne[2], n_out = wne[3], n_img = model.hp[0] / model.hp[1];
-    if (ne[0] != patch_k || ne[1] != n_img || ne[2] != n_img) {
-        fprintf(stderr, "%s: patch_mulmat input shape mismatch [%lld,%lld,%lld,%lld]\n", __func__, (long long)ne[0],
-                (long long)ne[1], (long long)ne[2], (long long)ne[3]);
+    int64_t dims[4];
+    for (int i = 0; i < 4; i++) dims[i] = (input_ne && input_ne[i] > 0) ? input_ne[i] : 1;
+    std::vector<uint8_t> kern;
+    int64_t kne[4];
+    if (!model_tensor(model, "vit.patch_embed.proj.weight", S3E_TYPE_F16, kern, kne, __func__)) return false;
+    const int64_t kdim = kne[0] * kne[1] * kne[2], cout = kne[3], grid = model.hp[0] / model.hp[1];
+    if (dims[0] != kdim || dims[1] != grid || dims[2] != grid) {
+        fprintf(stderr, "%s: expected im2col rows of %lld values on a %lldx%lld grid, got dims %lld/%lld/%lld/%lld\n",
+                __func__, (long long)kdim, (long long)grid, (long long)grid, (long long)dims[0], (long long)dims[1],
+                (long long)dims[2], (long long)dims[3]);
         return false;
     }
-    const int64_t n_patch = ne[1] * ne[2] * ne[3];
-    std::vector<float> x((size_t)(patch_k * n_patch));
-    for (size_t i = 0; i < x.size(); i++) x[i] = host_h2f(host_f2h(input_data[i]));
-    const uint16_t *w16 = (const uint16_t *)w.data();
-    output_data.resize((size_t)(n_patch * n_out));
-    output_ne[0] = n_patch;
-    output_ne[1] = n_out;
+    const int64_t npix = dims[1] * dims[2] * dims[3];
+    std::vector<float> xr((size_t)(kdim * npix));
+    for (size_t i = 0; i < xr.size(); i++) xr[i] = host_h2f(host_f2h(input_data[i]));
+    const uint16_t *kh = (const uint16_t *)kern.data();
+    output_data.resize((size_t)(npix * cout));
+    output_ne[0] = npix;
+    output_ne[1] = cout;
     output_ne[2] = 1;
     output_ne[3] = 1;
-    for (int64_t oc = 0; oc < n_out; ++oc) {
-        const uint16_t *wr = w16 + oc * patch_k;
-        float *dst = output_data.data() + oc * n_patch;
-        for (int64_t p = 0; p < n_patch; ++p) {
-            const float *xr = x.data() + p * patch_k;
+    // output channel-major: channel c holds npix values
+    for (int64_t c = 0; c < cout; ++c) {
+        const uint16_t *krow = kh + c * kdim;
+        float *o = output_data.data() + c * npix;
+        for (int64_t px = 0; px < npix; ++px) {
+            const float *v = xr.data() + px * kdim;
             if (use_double_accum) {
-                double acc = 0.0;
-                for (int64_t k = 0; k < patch_k; ++k) acc += (double)xr[k] * (double)host_h2f(wr[k]);
-                dst[p] = (float)acc;
+                double sum = 0.0;
+                for (int64_t j = 0; j < kdim; ++j) sum += (double)v[j] * (double)host_h2f(krow[j]);
+                o[px] = (float)sum;
             } else {
-                float acc = 0.0f;
-                for (int64_t k = 0; k < patch_k; ++k) acc += xr[k] * host_h2f(wr[k]);
-                dst[p] = acc;
+                float sum = 0.0f;
+                for (int64_t j = 0; j < kdim; ++j) sum += v[j] * host_h2f(krow[j]);
+                o[px] = sum;
             }
         }
     }
     return true;
 } SAM3_CATCH(false)
 
-// sam3.cpp:6576-6674: bias + Σ fp16(w)·fp16(x), f32 (or double) accumulation
+// sam3.cpp:6576-6674: one block linear on the host — bias plus the sum of
+// fp16(w)·fp16(x), accumulated in f32 (or double) from the bias
 bool sam3_test_run_vit_block_linear_host_ref(const sam3_model &model, int block_idx, sam3_vit_block_stage stage,
                                              const float *input_data, const int64_t input_ne[4], bool use_double_accum,
                                              std::vector<float> &output_data, int64_t output_ne[4]) try {
     if (!input_data || !model.enc || block_idx < 0 || block_idx >= model.hp[3]) return false;
-    const char *lin = nullptr;
+    const char *layer = nullptr;
     switch (stage) {
-        case SAM3_VIT_BLOCK_STAGE_QKV_PROJ: lin = "attn.qkv"; break;
-        case SAM3_VIT_BLOCK_STAGE_ATTN_PROJ: lin = "attn.proj"; break;
-        case SAM3_VIT_BLOCK_STAGE_MLP_FC1: lin = "mlp.lin1"; break;
-        case SAM3_VIT_BLOCK_STAGE_MLP_FC2: lin = "mlp.lin2"; break;
+        case SAM3_VIT_BLOCK_STAGE_QKV_PROJ: layer = "attn.qkv"; break;
+        case SAM3_VIT_BLOCK_STAGE_ATTN_PROJ: layer = "attn.proj"; break;
+        case SAM3_VIT_BLOCK_STAGE_MLP_FC1: layer = "mlp.lin1"; break;
+        case SAM3_VIT_BLOCK_STAGE_MLP_FC2: layer = "mlp.lin2"; break;
         default:
-            fprintf(stderr, "%s: unsupported stage %d\n", __func__, (int)stage);
+            fprintf(stderr, "%s: stage %d is not one of the four block linears\n", __func__, (int)stage);
             return false;
     }
-    const std::string base = "vit.blocks." + std::to_string(block_idx) + "." + lin;
-    std::vector<uint8_t> w, b;
+    const std::string base = "vit.blocks." + std::to_string(block_idx) + "." + layer;
+    std::vector<uint8_t> wt, bs;
     int64_t wne[4], bne[4];
-    if (!model_tensor(model, base + ".weight", S3E_TYPE_F16, w, wne, __func__) ||
-        !model_tensor(model, base + ".bias", S3E_TYPE_F32, b, bne, __func__))
+    if (!model_tensor(model, base + ".weight", S3E_TYPE_F16, wt, wne, __func__) ||
+        !model_tensor(model, base + ".bias", S3E_TYPE_F32, bs, bne, __func__))
         return false;
-    int64_t ne[4];
-    for (int i = 0; i < 4; i++) ne[i] = (input_ne && input_ne[i] > 0) ? input_ne[i] : 1;
-    const int64_t k = wne[0], out_dim = wne[1], n_col = ne[1] * ne[2] * ne[3];
-    if (ne[0] != k) {
-        fprintf(stderr, "%s: linear input shape mismatch [%lld,%lld,%lld,%lld] for K=%lld\n", __func__,
-                (long long)ne[0], (long long)ne[1], (long long)ne[2], (long long)ne[3], (long long)k);
+    int64_t dims[4];
+    for (int i = 0; i < 4; i++) dims[i] = (input_ne && input_ne[i] > 0) ? input_ne[i] : 1;
+    const int64_t kdim = wne[0], nout = wne[1], ntok = dims[1] * dims[2] * dims[3];
+    if (dims[0] != kdim) {
+        fprintf(stderr, "%s: %s takes rows of %lld values, got dims %lld/%lld/%lld/%lld\n", __func__, base.c_str(),
+                (long long)kdim, (long long)dims[0], (long long)dims[1], (long long)dims[2], (long long)dims[3]);
         return false;
     }
-    const uint16_t *w16 = (const uint16_t *)w.data();
-    const float *bias = (const float *)b.data();
-    std::vector<float> x((size_t)(k * n_col));
-    for (size_t i = 0; i < x.size(); i++) x[i] = host_h2f(host_f2h(input_data[i]));
-    output_data.resize((size_t)(out_dim * n_col));
-    output_ne[0] = out_dim;
-    output_ne[1] = ne[1];
-    output_ne[2] = ne[2];
-    output_ne[3] = ne[3];
-    for (int64_t col = 0; col < n_col; ++col) {
-        const float *xc = x.data() + col * k;
-        float *dst = output_data.data() + col * out_dim;
-        for (int64_t oc = 0; oc < out_dim; ++oc) {
-            const uint16_t *wr = w16 + oc * k;
+    const uint16_t *wh = (const uint16_t *)wt.data();
+    const float *bias = (const float *)bs.data();
+    std::vector<float> xr((size_t)(kdim * ntok));
+    for (size_t i = 0; i < xr.size(); i++) xr[i] = host_h2f(host_f2h(input_data[i]));
+    output_data.resize((size_t)(nout * ntok));
+    output_ne[0] = nout;
+    output_ne[1] = dims[1];
+    output_ne[2] = dims[2];
+    output_ne[3] = dims[3];
+    // token-major output: token t holds nout values
+    for (int64_t t = 0; t < ntok; ++t) {
+        const float *v = xr.data() + t * kdim;
+        float *o = output_data.data() + t * nout;
+        for (int64_t c = 0; c < nout; ++c) {
+            const uint16_t *wrow = wh + c * kdim;
             if (use_double_accum) {
-                double acc = (double)bias[oc];
-                for (int64_t i = 0; i < k; ++i) acc += (double)host_h2f(wr[i]) * (double)xc[i];
-                dst[oc] = (float)acc;
+                double sum = (double)bias[c];
+                for (int64_t j = 0; j < kdim; ++j) sum += (double)host_h2f(wrow[j]) * (double)v[j];
+                o[c] = (float)sum;
             } else {
-                float acc = bias[oc];
-                for (int64_t i = 0; i < k; ++i) acc += host_h2f(wr[i]) * xc[i];
-                dst[oc] = acc;
+                float sum = bias[c];
+                for (int64_t j = 0; j < kdim; ++j) sum += host_h2f(wrow[j]) * v[j];
+                o[c] = sum;
             }
         }
     }
