@@ -374,12 +374,13 @@ def preprocess_leg(s3e, ctx, ev, st, S: int, encode_ms: float, reps: int = 20) -
     return res
 
 
-def encode_ms(s3e, ctx, ev, ftype: str, steps: int, warmup: int) -> float:
-    """ms/frame of the full 1008 px encoder (backbone + tracker neck) with the
-    ViT's linear weights in `ftype`, input resident in HBM."""
+def encode_ms(s3e, ctx, ev, ftype: str, steps: int, warmup: int, neck: int = 1) -> float:
+    """ms/frame of the full 1008 px encoder (backbone + tracker neck; with
+    neck=2 the full SAM 3 file's backbone + detector and tracker necks) with
+    the ViT's linear weights in `ftype`, input resident in HBM."""
     tmpdir = os.environ.get("TMPDIR", tempfile.gettempdir())
-    path = os.path.join(tmpdir, f"s3e_bench_sam3_vit_{ftype}.ggml")
-    s3e.synth_write(path, ftype=ftype, seed=0, std=0.02, **CFG)
+    path = os.path.join(tmpdir, f"s3e_bench_sam3_vit_{ftype}_n{neck}.ggml")
+    s3e.synth_write(path, ftype=ftype, seed=0, std=0.02, neck=neck, **CFG)
     model = s3e.Model(ctx, path)
     st = s3e.State(ctx, model)
     chw_d = ctx.to_device(preprocess(synthetic_image(CFG["img_size"])))
@@ -399,7 +400,7 @@ def encode_ms(s3e, ctx, ev, ftype: str, steps: int, warmup: int) -> float:
         os.remove(path)
     except OSError:
         pass
-    log(f"encode {ftype}: {ms:.3f} ms/frame over {steps} steps")
+    log(f"encode {ftype} ({neck} neck{'s' if neck > 1 else ''}): {ms:.3f} ms/frame over {steps} steps")
     return ms
 
 
@@ -407,24 +408,25 @@ ATTN_SHAPES = [("windowed", 9, 576), ("global", 1, 5184)]  # (name, windows B, t
 
 
 def attention_fp16(s3e, ctx, ev, reps: int = 20) -> dict:
-    """The ViT's attention at F16 precision (fp16 operands, fp32
-    accumulation: ggml_flash_attn_ext as the reference's F16-weight path
-    computes it, S3E_PREC_DEFAULT): 16 heads of 64 over 9 windows of 576
-    tokens and over the 5184-token global grid, through s3e_flash_attn_ext
-    (f32 Q, K, V in ggml's layout, converted to fp16 by the call).  FLOPs
-    4·B·heads·N²·64 (QKᵀ and PV), against the 2.5 PFLOP/s dense fp16 peak."""
+    """The ViT's attention at F16 precision (ggml_flash_attn_ext with F16
+    operands; fp16 probabilities, fp32 accumulation): 16 heads of 64 over 9
+    windows of 576 tokens and over the 5184-token global grid, through
+    s3e_flash_attn_ext_f16 with fp16 Q, K, V resident in ggml's contiguous
+    [B][heads][N][64] layout.  Calls run back to back on the stream; each is
+    one V transpose pass (V into the engine's key-slot layout; Q and K are
+    read in place) and the attention kernel, with no allocation or
+    synchronisation.  FLOPs 4·B·heads·N²·64 (QKᵀ and PV), against the
+    2.5 PFLOP/s dense fp16 peak."""
     res = {}
     rng = np.random.default_rng(7)
     nh, D = 16, 64
     e0, e1 = ev.create(), ev.create()
     for name, B, N in ATTN_SHAPES:
-        q = ctx.to_device(rng.standard_normal((B, nh, N, D)).astype(np.float32))
-        k = ctx.to_device(rng.standard_normal((B, nh, N, D)).astype(np.float32))
-        v = ctx.to_device(rng.standard_normal((B, N, nh, D)).astype(np.float32))
+        h16 = lambda: ctx.to_device(rng.standard_normal((B, nh, N, D)).astype(np.float16).view(np.uint16))
+        q, k, v = h16(), h16(), h16()
         o = ctx.buffer(B * N * nh * D * 4)
-        qk_nb = (1, D, N * D, nh * N * D)
-        v_nb = (1, nh * D, D, N * nh * D)
-        run = lambda: ctx.flash_attn_ext(q, qk_nb, k, qk_nb, v, v_nb, D, N, N, nh, B, 0.125, o, prec=0)
+        nb = (1, D, N * D, nh * N * D)
+        run = lambda: ctx.flash_attn_ext_f16(q, nb, k, nb, v, nb, D, N, N, nh, B, 0.125, o)
         for _ in range(3):
             run()
         ctx.sync()
@@ -438,8 +440,8 @@ def attention_fp16(s3e, ctx, ev, reps: int = 20) -> dict:
         tf = flops / (us * 1e-6) / 1e12
         res[name] = {"windows": B, "tokens": N, "heads": nh, "us": round(us, 1), "TFLOPs": round(tf, 1),
                      "frac_fp16_peak": round(tf / 2500.0, 4),
-                     "scope": "whole s3e_flash_attn_ext call: f32->fp16 operand conversion, attention, and the "
-                              "call's own synchronisation"}
+                     "scope": "s3e_flash_attn_ext_f16 calls back to back, fp16 operands resident: V transpose "
+                              "pass + attention kernel"}
         log(f"attention fp16 {name} {B}x{nh}x{N}: {us:.1f} us, {tf:.1f} TFLOP/s")
         for b in (q, k, v, o):
             b.free()
@@ -661,6 +663,7 @@ def main() -> int:
     if args.only == "c4":
         for ft in ("q8_0", "f16"):
             encode_ms(s3e, ctx, ev, ft, args.steps, args.warmup)
+        encode_ms(s3e, ctx, ev, "q4_0", args.steps, args.warmup, neck=2)
         return 0
 
     if args.only == "small_m":
@@ -724,6 +727,11 @@ def main() -> int:
         return 0
     c4 = {f"{ft}_ms": round(encode_ms(s3e, ctx, ev, ft, max(5, args.steps // 2), 2), 3)
           for ft in ("q4_0", "q8_0", "f16") if ft != args.ftype}
+    full_ms = encode_ms(s3e, ctx, ev, args.ftype, max(5, args.steps // 2), 2, neck=2)
+    full = {"ms_per_frame": round(full_ms, 3), "GFLOP": 5828.3,
+            "TFLOPs": round(5828.3 / full_ms, 1),
+            "workload": f"full SAM 3 file ({args.ftype.upper()} linear weights), 1008x1008: ViT backbone + "
+                        "detector and tracker SimpleFPN necks (sam3.cpp:6072-6075), image resident"}
     attn = attention_fp16(s3e, ctx, ev)
     sam2 = sam2_encoders(s3e, ctx, ev, max(3, args.steps // 2), 2)
     sm = small_m(s3e, ctx, ev, args.ftype) if args.ftype in BPW else None
@@ -772,6 +780,7 @@ def main() -> int:
                    "global_blocks": [7, 15, 23, 31], "neck_levels": [288, 144, 72, 36]},
         "breakdown": {"neck_ms": round(neck_ms, 3), "backbone_ms": round(ms_frame - neck_ms, 3)},
         "c4_other_weights": c4,
+        "full_sam3_two_necks": full,
         "attention_fp16": attn,
         "sam2_encoders": sam2,
         "small_m": sm,

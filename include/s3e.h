@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define S3E_ABI_VERSION 5
+#define S3E_ABI_VERSION 6
 
 enum s3e_status {
     S3E_OK = 0,
@@ -209,6 +209,24 @@ int s3e_flash_attn_ext(s3e_ctx *ctx,
                        const float *v, const int64_t v_nb[4],
                        int64_t D, int64_t Nq, int64_t Nkv, int64_t nh, int64_t B,
                        float scale, int prec, float *o);
+
+/* ggml_flash_attn_ext with F16 Q, K and V (ggml accepts F16 K/V tensors; the
+ * isolated attention microbench feeds fp16 operands): the same addressing,
+ * shapes and output as s3e_flash_attn_ext, q/k/v as IEEE fp16 bits, computed
+ * at S3E_PREC_DEFAULT (fp16 operands and probabilities, fp32 accumulation).
+ * Q and K are read in place when they are contiguous [B][nh][N][D] with D =
+ * 64 or 128 (else copied); V is transposed into the engine's layout by one
+ * pass.  Asynchronous on the context's stream: O is complete after
+ * s3e_ctx_sync.  The copies live in a context-owned workspace that a call
+ * grows (synchronising the stream, then hipMalloc) only when it needs more
+ * room than every earlier call on the context; calls that fit allocate
+ * nothing. */
+int s3e_flash_attn_ext_f16(s3e_ctx *ctx,
+                           const uint16_t *q, const int64_t q_nb[4],
+                           const uint16_t *k, const int64_t k_nb[4],
+                           const uint16_t *v, const int64_t v_nb[4],
+                           int64_t D, int64_t Nq, int64_t Nkv, int64_t nh, int64_t B,
+                           float scale, float *o);
 
 /* ---- encoder -------------------------------------------------------------
  * Load the image encoder of a sam3.cpp model file (sam3.cpp:3200-3344):

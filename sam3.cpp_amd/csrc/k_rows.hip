@@ -435,6 +435,56 @@ __global__ void k_attn_prep(const float *__restrict__ src, int64_t s1, int64_t s
     if (lo) lo[o] = (_Float16)(v - (float)hv);
 }
 
+// fp16 strided rows (head dim D) → fp16 [BH][N][hdp], channels D..hdp−1 zero
+// (Q or K of s3e_flash_attn_ext_f16 when they are not already in that
+// layout).  One thread per output element.
+__global__ void k_attn_prep16(const _Float16 *__restrict__ src, int64_t s1, int64_t s2, int64_t s3, int64_t N,
+                              int64_t nh, int64_t B, int D, int hdp, _Float16 *__restrict__ dst) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= B * nh * N * hdp) return;
+    const int64_t d = idx % hdp, i = (idx / hdp) % N, h = (idx / (hdp * N)) % nh, b = idx / (hdp * N * nh);
+    dst[idx] = d < D ? src[b * s3 + h * s2 + i * s1 + d] : (_Float16)0.f;
+}
+
+// fp16 V (key j of head h of batch b at v[b*s3 + h*s2 + j*s1 + d]) → Vᵀ
+// [BH][hdp][ldv], keys in vt_slot order, zero past Nkv and for d ≥ D.  One
+// thread per 8 slots × 8 channels: it reads the 8 keys those slots hold (16
+// bytes of channels each; VEC: one 16-byte load per key, else element by
+// element) and writes the 8 channel rows' 16-byte runs, transposing in
+// registers.  Slots 8c .. 8c + 7 of a 16-key group hold keys {0-3, 8-11}
+// (c even) or {4-7, 12-15} (c odd) of it.
+template <bool VEC>
+__global__ __launch_bounds__(256) void k_vt16(const _Float16 *__restrict__ v, int64_t s1, int64_t s2, int64_t s3,
+                                              int64_t Nkv, int64_t nh, int D, int hdp, int64_t ldv,
+                                              _Float16 *__restrict__ vt, int64_t total) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= total) return;
+    const int dch = hdp / 8;
+    const int64_t nsc = ldv / 8;
+    const int d0 = (int)(t % dch) * 8;
+    const int64_t sc = (t / dch) % nsc, bh = t / (dch * nsc);
+    const _Float16 *vb = v + (bh / nh) * s3 + (bh % nh) * s2;
+    const int64_t kbase = (sc >> 1) * 16 + (sc & 1) * 4;
+    _Float16 x[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int64_t key = kbase + (i & 3) + (i >> 2) * 8;
+        if (VEC && key < Nkv && d0 + 8 <= D) {
+            *(uint4 *)x[i] = *(const uint4 *)(vb + key * s1 + d0);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) x[i][j] = (key < Nkv && d0 + j < D) ? vb[key * s1 + d0 + j] : (_Float16)0.f;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        _Float16 run[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) run[i] = x[i][j];
+        *(uint4 *)(vt + (bh * hdp + d0 + j) * ldv + 8 * sc) = *(const uint4 *)run;
+    }
+}
+
 // NHWC f32 pixels → fp16 / split-fp16 activation rows, optionally through
 // the 2×2 stride-2 max pool (ggml_pool_2d MAX, sam3.cpp:3914): one thread per
 // 4 channels of an output pixel.
@@ -537,6 +587,33 @@ hipError_t launch_attn_prep(const float *q, const int64_t q_nb[4], const float *
                        k_nb[2], k_nb[3], Nkv, nh, B, D, hdp, k16, k_lo, (int64_t)0, 0);
     hipLaunchKernelGGL(k_attn_prep, dim3((unsigned)((tk + 255) / 256)), dim3(256), 0, st, v, v_nb[1],
                        v_nb[2], v_nb[3], Nkv, nh, B, D, hdp, vt16, vt_lo, ldv, 1);
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_prep16(const _Float16 *q, const int64_t q_nb[4], const _Float16 *k, const int64_t k_nb[4],
+                              const _Float16 *v, const int64_t v_nb[4], int64_t Nq, int64_t Nkv, int64_t nh,
+                              int64_t B, int D, int hdp, _Float16 *q16, _Float16 *k16, _Float16 *vt16, int64_t ldv,
+                              hipStream_t st) {
+    if (D <= 0 || D > hdp || hdp > 256 || ldv % 16 != 0 || ldv < Nkv) return hipErrorInvalidValue;
+    if (q16) {
+        const int64_t t = B * nh * Nq * hdp;
+        hipLaunchKernelGGL(k_attn_prep16, dim3((unsigned)((t + 255) / 256)), dim3(256), 0, st, q, q_nb[1], q_nb[2],
+                           q_nb[3], Nq, nh, B, D, hdp, q16);
+    }
+    if (k16) {
+        const int64_t t = B * nh * Nkv * hdp;
+        hipLaunchKernelGGL(k_attn_prep16, dim3((unsigned)((t + 255) / 256)), dim3(256), 0, st, k, k_nb[1], k_nb[2],
+                           k_nb[3], Nkv, nh, B, D, hdp, k16);
+    }
+    const int64_t total = B * nh * (ldv / 8) * (hdp / 8);
+    const bool vec = ((uintptr_t)v % 16 == 0) && v_nb[1] % 8 == 0 && v_nb[2] % 8 == 0 && v_nb[3] % 8 == 0;
+    const dim3 grid((unsigned)((total + 255) / 256));
+    if (vec)
+        hipLaunchKernelGGL(k_vt16<true>, grid, dim3(256), 0, st, v, v_nb[1], v_nb[2], v_nb[3], Nkv, nh, D, hdp, ldv,
+                           vt16, total);
+    else
+        hipLaunchKernelGGL(k_vt16<false>, grid, dim3(256), 0, st, v, v_nb[1], v_nb[2], v_nb[3], Nkv, nh, D, hdp, ldv,
+                           vt16, total);
     return hipGetLastError();
 }
 

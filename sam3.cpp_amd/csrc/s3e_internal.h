@@ -299,6 +299,13 @@ hipError_t launch_attn_prep(const float *q, const int64_t q_nb[4], const float *
                             int64_t Nq, int64_t Nkv, int64_t nh, int64_t B, int D, int hdp, _Float16 *q16,
                             _Float16 *k16, _Float16 *vt16, _Float16 *q_lo, _Float16 *k_lo,
                             _Float16 *vt_lo, int64_t ldv, hipStream_t st);
+// fp16 operands of s3e_flash_attn_ext_f16: Q and K (when q16 / k16 are
+// given) copied to [BH][N][hdp], V transposed to Vᵀ [BH][hdp][ldv] in
+// vt_slot order with zeros past Nkv (every slot of every row is written).
+hipError_t launch_attn_prep16(const _Float16 *q, const int64_t q_nb[4], const _Float16 *k, const int64_t k_nb[4],
+                              const _Float16 *v, const int64_t v_nb[4], int64_t Nq, int64_t Nkv, int64_t nh,
+                              int64_t B, int D, int hdp, _Float16 *q16, _Float16 *k16, _Float16 *vt16, int64_t ldv,
+                              hipStream_t st);
 hipError_t launch_im2col(const float *chw, int img, int P, int64_t ldk, AKind kind, void *out,
                          hipStream_t st);
 hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t st);

@@ -26,6 +26,9 @@ struct s3e_ctx {
     // partial sums of small-M products split over K across work-groups
     float *sk_part = nullptr;
     int64_t sk_part_cap = 0;
+    // s3e_flash_attn_ext_f16's operand copies and key-split partials
+    void *attn_ws = nullptr;
+    size_t attn_ws_cap = 0;
 };
 
 struct s3e_weight {

@@ -315,6 +315,7 @@ extern "C" void s3e_ctx_destroy(s3e_ctx *ctx) {
     (void)hipStreamDestroy(ctx->stream);
     if (ctx->sm_dev) (void)hipFree(ctx->sm_dev);
     if (ctx->sk_part) (void)hipFree(ctx->sk_part);
+    if (ctx->attn_ws) (void)hipFree(ctx->attn_ws);
     delete ctx;
 }
 
@@ -805,6 +806,88 @@ extern "C" int s3e_flash_attn_ext(s3e_ctx *ctx, const float *q, const int64_t q_
     if (e != hipSuccess) { set_error("s3e_flash_attn_ext: %s", hipGetErrorString(e)); return S3E_ERR_HIP; }
     return S3E_OK;
 } S3E_CATCH("s3e_flash_attn_ext")
+
+extern "C" int s3e_flash_attn_ext_f16(s3e_ctx *ctx, const uint16_t *q, const int64_t q_nb[4], const uint16_t *k,
+                                      const int64_t k_nb[4], const uint16_t *v, const int64_t v_nb[4], int64_t D,
+                                      int64_t Nq, int64_t Nkv, int64_t nh, int64_t B, float scale, float *o) try {
+    if (!ctx || !q || !k || !v || !o || !q_nb || !k_nb || !v_nb) {
+        set_error("s3e_flash_attn_ext_f16: NULL argument");
+        return S3E_ERR_INVALID;
+    }
+    if (Nq <= 0 || Nkv <= 0 || nh <= 0 || B <= 0 || D <= 0) { set_error("s3e_flash_attn_ext_f16: empty shape"); return S3E_ERR_INVALID; }
+    if (D % 4 != 0 || (D > 128 && D != 256)) {
+        set_error("s3e_flash_attn_ext_f16: head dim %lld not supported (multiples of 4 up to 128, or 256)", (long long)D);
+        return S3E_ERR_UNSUPPORTED;
+    }
+    if (B * nh > 65535 || Nq > (1 << 24) || Nkv > (1 << 24)) { set_error("s3e_flash_attn_ext_f16: shape too large"); return S3E_ERR_INVALID; }
+    for (int i = 1; i < 4; i++)
+        if (q_nb[i] < 0 || k_nb[i] < 0 || v_nb[i] < 0) { set_error("s3e_flash_attn_ext_f16: negative stride"); return S3E_ERR_INVALID; }
+    if (q_nb[0] != 1 || k_nb[0] != 1 || v_nb[0] != 1) {
+        set_error("s3e_flash_attn_ext_f16: the head dimension must be contiguous (nb[0] = 1)");
+        return S3E_ERR_INVALID;
+    }
+    HIP_TRY(hipSetDevice(ctx->device));
+    const int hdp = D <= 64 ? 64 : (D <= 128 ? 128 : 256);
+    const int64_t ldv = vt_ld_for(Nkv);
+    const int64_t BH = B * nh, qtiles = (Nq + 127) / 128, ktiles = (Nkv + 31) / 32;
+    // Q and K are read where they lie when they already are [B][nh][N][hdp]
+    auto plain = [&](const int64_t nb[4], int64_t N) {
+        return D == hdp && nb[1] == hdp && nb[2] == N * hdp && nb[3] == nh * N * hdp;
+    };
+    const bool q_in = plain(q_nb, Nq), k_in = plain(k_nb, Nkv);
+    int nsplit = 1;
+    const int64_t target = hdp == 256 ? 256 : 512;
+    if (D == hdp && qtiles * BH < target) {
+        const int64_t ns = std::min<int64_t>((target + qtiles * BH - 1) / (qtiles * BH), std::max<int64_t>(1, ktiles / 4));
+        const int64_t per = (ktiles + ns - 1) / ns;
+        nsplit = (int)((ktiles + per - 1) / per);
+    }
+    // workspace: [Vᵀ][Q copy][K copy][partials], 256-byte aligned pieces
+    auto al = [](size_t b) { return (b + 255) / 256 * 256; };
+    const size_t vb = al((size_t)(BH * hdp * ldv) * 2), qb = q_in ? 0 : al((size_t)(BH * Nq * hdp) * 2),
+                 kb = k_in ? 0 : al((size_t)(BH * Nkv * hdp) * 2);
+    const size_t po = (size_t)nsplit * BH * Nq * hdp, pml = (size_t)nsplit * BH * Nq * 2;
+    const size_t pb = nsplit > 1 ? (po + pml) * 4 : 0;
+    const size_t need = vb + qb + kb + pb;
+    if (need > ctx->attn_ws_cap) {
+        HIP_TRY(hipStreamSynchronize(ctx->stream));  // earlier calls may still read it
+        if (ctx->attn_ws) (void)hipFree(ctx->attn_ws);
+        ctx->attn_ws = nullptr;
+        ctx->attn_ws_cap = 0;
+        HIP_TRY(hipMalloc(&ctx->attn_ws, need));
+        ctx->attn_ws_cap = need;
+    }
+    uint8_t *ws = (uint8_t *)ctx->attn_ws;
+    _Float16 *vt16 = (_Float16 *)ws;
+    _Float16 *q16 = q_in ? nullptr : (_Float16 *)(ws + vb);
+    _Float16 *k16 = k_in ? nullptr : (_Float16 *)(ws + vb + qb);
+    hipError_t e = launch_attn_prep16((const _Float16 *)q, q_nb, (const _Float16 *)k, k_nb, (const _Float16 *)v, v_nb,
+                                      Nq, Nkv, nh, B, (int)D, hdp, q16, k16, vt16, ldv, ctx->stream);
+    if (e == hipSuccess) {
+        AttnArgs a;
+        a.q = q_in ? (const _Float16 *)q : q16;
+        a.k = k_in ? (const _Float16 *)k : k16;
+        a.vt = vt16;
+        a.Nq = (int)Nq;
+        a.Nkv = (int)Nkv;
+        a.NH = (int)nh;
+        a.BH = (int)BH;
+        a.hd = hdp;
+        a.hd_out = D == hdp ? 0 : (int)D;
+        a.scale = scale;
+        a.nsplit = nsplit;
+        if (nsplit > 1) {
+            a.part_o = (float *)(ws + vb + qb + kb);
+            a.part_ml = a.part_o + po;
+        }
+        a.out.kind = A_F32;
+        a.out.x = o;
+        a.out.ld = nh * D;
+        e = launch_attn(a, ctx->stream);
+    }
+    if (e != hipSuccess) { set_error("s3e_flash_attn_ext_f16: %s", hipGetErrorString(e)); return S3E_ERR_HIP; }
+    return S3E_OK;
+} S3E_CATCH("s3e_flash_attn_ext_f16")
 
 // ---- SAM 3 ViT model -------------------------------------------------------
 namespace {

@@ -43,7 +43,7 @@ def test_exports_every_declared_symbol(s3e):
     for n in names:
         assert hasattr(s3e.LIB, n), n
     assert sorted(s3e.DECLARED) == names
-    assert s3e.LIB.s3e_abi_version() == 5
+    assert s3e.LIB.s3e_abi_version() == 6
 
 
 def read_file(path):

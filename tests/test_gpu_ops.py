@@ -360,3 +360,58 @@ def test_flash_attn_rejects(ctx):
     for D, prec in [(130, 1), (6, 1), (256, 1), (192, 0), (0, 1)]:
         with pytest.raises(s3e.S3EError):
             ctx.flash_attn_ext(buf, nb, buf, nb, buf, nb, D, 8, 8, 1, 1, 0.125, buf, prec=prec)
+
+
+def _f16_bits(a):
+    return np.ascontiguousarray(a.astype(np.float16)).view(np.uint16)
+
+
+@pytest.mark.parametrize("D,B,nh,Nq,Nkv,layout", [
+    (64, 9, 16, 576, 576, "plain"), (64, 1, 16, 5184, 5184, "plain"), (64, 1, 2, 100, 130, "plain"),
+    (64, 2, 3, 200, 200, "tokens"), (96, 1, 4, 49, 196, "plain"), (128, 1, 2, 300, 300, "plain"),
+    (256, 1, 1, 512, 4096, "plain"), (64, 1, 1, 256, 4096, "tokens")],
+    ids=lambda x: str(x))
+def test_flash_attn_f16(ctx, D, B, nh, Nq, Nkv, layout):
+    """s3e_flash_attn_ext_f16: fp16 Q/K/V bits in ggml's strides.  "plain":
+    Q, K, V contiguous [B][nh][N][D] (Q and K read in place at D = 64 / 128);
+    "tokens": all three token-major [B][N][nh][D] (copied), like the ViT's
+    strided views.  Reference: f32 attention of the same fp16 values; the
+    kernel rounds the probabilities to fp16 (the F16 tolerance).  Two calls
+    in a row check that the workspace kept from the first (larger or
+    smaller) does not leak into the second."""
+    rng = np.random.default_rng(D + 3 * Nq + Nkv + (7 if layout == "tokens" else 0))
+    qt = rng.standard_normal((B, Nq, nh, D)).astype(np.float16)
+    kt = rng.standard_normal((B, Nkv, nh, D)).astype(np.float16)
+    vt = rng.standard_normal((B, Nkv, nh, D)).astype(np.float16)
+    q, k, v = (np.ascontiguousarray(a.transpose(0, 2, 1, 3)) for a in (qt, kt, vt))
+    scale = 1.0 / np.sqrt(D)
+    ref = orc.flash_attn(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32), scale)
+    if layout == "plain":
+        src = (q, k, v)
+        nbq, nbk = (1, D, Nq * D, nh * Nq * D), (1, D, Nkv * D, nh * Nkv * D)
+    else:
+        src = (qt, kt, vt)
+        nbq, nbk = (1, nh * D, D, Nq * nh * D), (1, nh * D, D, Nkv * nh * D)
+    qd, kd, vd = (ctx.to_device(_f16_bits(a)) for a in src)
+    od = ctx.buffer(B * Nq * nh * D * 4)
+    for call in range(2):
+        ctx.flash_attn_ext_f16(qd, nbq, kd, nbk, vd, nbk, D, Nq, Nkv, nh, B, scale, od)
+        ctx.sync()
+        out = od.download(np.float32, (B, Nq, nh, D))
+        err = orc.rel_l2(out, ref)
+        print(f"flash_attn_f16 D={D} B={B} nh={nh} Nq={Nq} Nkv={Nkv} {layout} call {call}: rel_l2={err:.3e}")
+        assert err <= 2e-3
+    for b in (qd, kd, vd, od):
+        b.free()
+
+
+def test_flash_attn_f16_rejects(ctx):
+    import s3e
+
+    x = ctx.buffer(64 * 64 * 2)
+    o = ctx.buffer(64 * 64 * 4)
+    nb = (1, 64, 64 * 64, 64 * 64)
+    with pytest.raises(s3e.S3EError):
+        ctx.flash_attn_ext_f16(x, nb, x, nb, x, nb, 60 + 2, 64, 64, 1, 1, 0.1, o)  # head dim not a multiple of 4
+    with pytest.raises(s3e.S3EError):
+        ctx.flash_attn_ext_f16(x, (2, 64, 4096, 4096), x, nb, x, nb, 64, 64, 64, 1, 1, 0.1, o)  # strided d
