@@ -251,6 +251,16 @@ int s3e_model_type(const s3e_model *m);
 /* Per-image state holding activations and outputs (sam3_create_state,
  * sam3.h:196; outputs of sam3.cpp:896-928). */
 int s3e_state_create(s3e_ctx *ctx, const s3e_model *m, s3e_state **out);
+/* sam3_create_state with sam3_params::encode_img_size (sam3.cpp:3392-3402,
+ * :245-257): the state encodes images of img_size pixels per side (0: the
+ * model's own).  For SAM 2.x files any multiple of 32 up to 4096: the token
+ * grids follow sam3_effective_feat_size's rule (img / 4, halved at every
+ * Q-stride block) and the Hiera positional embedding is recomputed for the
+ * new grid by the reference's bicubic resize (sam3.cpp:4114-4171); chw
+ * inputs are [3][img_size][img_size] and s3e_encode_image_u8 resizes to
+ * img_size.  SAM 3 files encode at their native size only
+ * (S3E_ERR_UNSUPPORTED otherwise). */
+int s3e_state_create_sized(s3e_ctx *ctx, const s3e_model *m, int img_size, s3e_state **out);
 void s3e_state_free(s3e_state *st);
 
 /* Encode a preprocessed CHW f32 image of img_size² (device pointer).

@@ -12,8 +12,11 @@
  *
  * Differences, all reported as failures rather than silently changed:
  *   - params.use_gpu == false is refused (the engine encodes on the GPU);
- *   - params.encode_img_size must be 0 or the model's img_size (the RoPE
- *     tables and positional embedding in the file fix the token grid);
+ *   - params.encode_img_size is honoured for SAM 2 files (any multiple of
+ *     32; the Hiera grids and positional embedding follow it, as in
+ *     sam3_create_state); SAM 3 files accept 0 or the model's img_size
+ *     only.  sam3_encode_image_from_preprocessed refuses a state whose
+ *     encode size is not the model's (it takes native-size input);
  *   - SAM 2 (Hiera) files are accepted and encoded; EdgeTAM files are
  *     refused;
  *   - the test-only stage hooks take inputs of at most the model's token

@@ -65,9 +65,22 @@ void orc_dequantize_row(int type, const void *x, float *y, int64_t k);
 
 /* ---- dot products (ggml vec_dot_<wtype>_<vec_dot_type>, AVX2 order) ---- */
 float orc_vec_dot(int wtype, int64_t n, const void *w_row, const void *x_row);
-/* 0 (default): ggml's x86 AVX2 evaluation order; 1: ggml's generic scalar
- * order.  Same block math, different fp32 rounding — for measuring the
- * order sensitivity of the reference itself. */
+/* Which ggml CPU build to restate.  Same block math, different fp32
+ * rounding — for measuring the order sensitivity of the reference itself:
+ *   ORC_VARIANT_X86 (default) x86 AVX2 dots and quantizers;
+ *   ORC_VARIANT_GENERIC       ggml's generic scalar dots;
+ *   ORC_VARIANT_ARM           the Apple M4 Pro build of the reference's
+ *                             published timings: tinyBLAS_Q0_ARM for Q4_0 /
+ *                             Q8_0, the i8mm vec_dot for Q4_1, NEON
+ *                             quantizers and f32 dots;
+ *   ORC_VARIANT_ARM_DOTPROD   NEON vec_dot with nrc = 1 for every quantized
+ *                             type (two alternating float32x4 accumulators);
+ *   ORC_VARIANT_ARM_I8MM      NEON vec_dot with nrc = 2 for every quantized
+ *                             type (one fp32 fma chain over exact block sums).
+ * The ARM variants also switch the Q8_0 / Q8_1 quantizers (id = 1/d) and
+ * the f32 dot (NEON order). */
+enum { ORC_VARIANT_X86 = 0, ORC_VARIANT_GENERIC = 1, ORC_VARIANT_ARM = 2, ORC_VARIANT_ARM_DOTPROD = 3,
+       ORC_VARIANT_ARM_I8MM = 4 };
 void  orc_set_variant(int v);
 /* Exact per-block integer sums Σ q_w·q_x of one (w row, x row) pair. */
 void  orc_block_isums(int wtype, int64_t n, const void *w_row, const void *x_row, int32_t *out);
@@ -133,6 +146,8 @@ typedef struct {
 int  orc_model_tensor(const orc_model *m, const char *prefix, const char *suffix, orc_tensor_view *out);
 /* NULL unless the model is a SAM 2 (Hiera) file */
 const orc_hiera_hp *orc_model_hiera(const orc_model *m);
+/* Encode size of the following Hiera calls (0 < img_size, a multiple of 32). */
+int orc_hiera_set_img_size(orc_model *m, int img_size);
 void orc_set_error(const char *fmt, ...);
 /* Prefix (patch embed + tiled pos + ln_pre): chw [3][img][img] → x [T][E]. */
 int  orc_vit_prefix(const orc_model *m, const float *chw, float *x, int nthreads);

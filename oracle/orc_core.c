@@ -243,10 +243,21 @@ void orc_quantize_row_q8_1_ref(const float *x, void *vy, int64_t k) {
     }
 }
 
+/* Which of ggml's CPU builds the quantized products, the activation
+ * quantizers and the f32 dots restate (orc_set_variant). */
+static int g_variant = ORC_VARIANT_X86;
+void orc_set_variant(int v) { g_variant = v; }
+static inline int arm_variant(void) {
+    return g_variant == ORC_VARIANT_ARM || g_variant == ORC_VARIANT_ARM_DOTPROD || g_variant == ORC_VARIANT_ARM_I8MM;
+}
+
 /* Activation quantizers: ggml-cpu x86 quantize_row_q8_0 / q8_1 (AVX2 path)
  * [ext]: maxScalar = max|x| over the block, d = maxScalar/127,
  * id = maxScalar != 0 ? 127/maxScalar : 0, q = round-half-even(x·id)
- * (_mm256_round_ps(.., _MM_ROUND_NEAREST)), q8_1 adds s = fp16(d·Σq). */
+ * (_mm256_round_ps(.., _MM_ROUND_NEAREST)), q8_1 adds s = fp16(d·Σq).
+ * The ARM NEON build (arch/arm/quants.c [ext]) takes id = d != 0 ? 1/d : 0
+ * instead — the same reciprocal in another rounding, so x·id can land on
+ * the other side of a .5 — and rounds with vcvtnq_s32_f32 (half to even). */
 static void quant_block_simd(const float *x, int8_t *q, float *d_out, int *sum_out) {
     float amax = 0.0f;
     for (int j = 0; j < QK; j++) {
@@ -254,7 +265,7 @@ static void quant_block_simd(const float *x, int8_t *q, float *d_out, int *sum_o
         amax = amax > v ? amax : v;
     }
     const float d = amax / 127.f;
-    const float id = (amax != 0.0f) ? 127.f / amax : 0.0f;
+    const float id = arm_variant() ? (d != 0.0f ? 1.0f / d : 0.0f) : ((amax != 0.0f) ? 127.f / amax : 0.0f);
     int sum = 0;
     for (int j = 0; j < QK; j++) {
         const float v = x[j] * id;
@@ -507,11 +518,129 @@ static float vec_dot_generic(int wtype, int64_t n, const void *w, const void *x)
     return (float)acc;
 }
 
-static int g_variant = 0;
-void orc_set_variant(int v) { g_variant = v; }
+/* ---- ARM NEON builds [ext] ------------------------------------------------
+ * The reference's published CPU timings come from an Apple M4 Pro
+ * (README.md:50-69), whose native build has the dotprod and i8mm
+ * extensions.  There ggml_mul_mat reaches three block-dot orders:
+ *
+ *  - llamafile's tinyBLAS_Q0_ARM (sgemm.cpp), tried first for Q4_0 / Q8_0
+ *    weights once src1 is in Q8_0: per output one float32x4 accumulator;
+ *    per block, lane i gets fma(Σ_{j∈{4i..4i+3} ∪ {16+4i..16+4i+3}} w_j·x_j,
+ *    d_w·d_x) (two vdotq_s32 over the block's low and high 16 bytes); the
+ *    four lanes are summed pairwise at the end (vaddvq_f32).
+ *  - ggml_vec_dot_*_q8_* with nrc = 2 (vmmlaq_s32, i8mm), used for Q4_1 and
+ *    whenever the product has even row counts: per output one fp32 chain
+ *    acc = fma(S_b, d_w·d_x, acc) over the exact block sums S_b; Q4_1 adds its
+ *    Σ m_w·s_x in a second chain and the two are added at the end.
+ *  - ggml_vec_dot_*_q8_* with nrc = 1 (dotprod only, e.g. without i8mm):
+ *    the tinyBLAS lanes, but blocks alternate between two float32x4
+ *    accumulators, vaddvq(sumv0) + vaddvq(sumv1) at the end; an odd last
+ *    block is added as ((S_b·d_w)·d_x) fused into the sum; Q4_1 keeps
+ *    Σ (m_w·s_x + m_w'·s_x') per block pair in one float added last.
+ * vmlaq_n_f32 / vmlaq_f32 compile to fused multiply-adds under clang's and
+ * gcc's default contraction, which is what is restated.  ORC_VARIANT_ARM is
+ * the M4 Pro's mixture: tinyBLAS for Q4_0 / Q8_0, nrc = 2 for Q4_1.
+ * The f32 dot (attention scores with F32 K, F32 convolutions) is
+ * ggml_vec_dot_f32 on NEON: four float32x4 accumulators over steps of 16,
+ * reduced (0+2, 1+3), then (0+1), then vaddvq_f32. */
+
+/* Exact int32 partial sums of one block: lane i = Σ_{j=4i}^{4i+3} w_j·x_j. */
+static inline __m256i block_p8(int wtype, const void *wb, const void *xb) {
+    if (wtype == ORC_TYPE_Q4_1) {
+        const __m256i qw = bytes_from_nibbles_32(((const blk_q4_1 *)wb)->qs);
+        const __m256i qx = _mm256_loadu_si256((const __m256i *)((const blk_q8_1 *)xb)->qs);
+        return _mm256_madd_epi16(_mm256_set1_epi16(1), _mm256_maddubs_epi16(qw, qx));
+    }
+    __m256i qw;
+    if (wtype == ORC_TYPE_Q4_0) qw = _mm256_sub_epi8(bytes_from_nibbles_32(((const blk_q4_0 *)wb)->qs), _mm256_set1_epi8(8));
+    else qw = _mm256_loadu_si256((const __m256i *)((const blk_q8_0 *)wb)->qs);
+    const __m256i qx = _mm256_loadu_si256((const __m256i *)((const blk_q8_0 *)xb)->qs);
+    const __m256i dot = _mm256_maddubs_epi16(_mm256_sign_epi8(qw, qw), _mm256_sign_epi8(qx, qw));
+    return _mm256_madd_epi16(_mm256_set1_epi16(1), dot);
+}
+
+static inline float vaddv4(const float a[4]) { return (a[0] + a[1]) + (a[2] + a[3]); }
+
+/* One (weight row, activation row) product in the ARM orders. */
+static float vec_dot_arm(int variant, int wtype, int64_t n, const char *w, const char *x) {
+    const int64_t nb = n / QK;
+    const size_t wbs = wtype == ORC_TYPE_Q4_0 ? sizeof(blk_q4_0) : wtype == ORC_TYPE_Q4_1 ? sizeof(blk_q4_1) : sizeof(blk_q8_0);
+    const size_t xbs = wtype == ORC_TYPE_Q4_1 ? sizeof(blk_q8_1) : sizeof(blk_q8_0);
+    const int q41 = wtype == ORC_TYPE_Q4_1;
+    if (variant == ORC_VARIANT_ARM) variant = q41 ? ORC_VARIANT_ARM_I8MM : -1; /* -1: tinyBLAS */
+    float acc = 0.0f, summs = 0.0f;
+    float v[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+    int64_t b = 0;
+    const int64_t npair = variant == ORC_VARIANT_ARM_DOTPROD ? nb & ~(int64_t)1 : nb;
+    for (; b < npair; b++) {
+        const char *wb = w + b * wbs, *xb = x + b * xbs;
+        const uint16_t wd = *(const uint16_t *)wb, xd = *(const uint16_t *)xb;
+        const float d = orc_fp16_to_fp32(wd) * orc_fp16_to_fp32(xd);
+        int32_t p[8];
+        _mm256_storeu_si256((__m256i *)p, block_p8(wtype, wb, xb));
+        if (variant == ORC_VARIANT_ARM_I8MM) {
+            const int32_t S = p[0] + p[1] + p[2] + p[3] + p[4] + p[5] + p[6] + p[7];
+            acc = fmaf((float)S, d, acc);
+            if (q41) summs = summs + orc_fp16_to_fp32(((const blk_q4_1 *)wb)->m) * orc_fp16_to_fp32(((const blk_q8_1 *)xb)->s);
+        } else {
+            float *a = v[variant == ORC_VARIANT_ARM_DOTPROD ? (b & 1) : 0];
+            for (int i = 0; i < 4; i++) a[i] = fmaf((float)(p[i] + p[i + 4]), d, a[i]);
+            if (q41 && (b & 1)) {
+                const blk_q4_1 *w0 = (const blk_q4_1 *)(wb - wbs), *w1 = (const blk_q4_1 *)wb;
+                const blk_q8_1 *x0 = (const blk_q8_1 *)(xb - xbs), *x1 = (const blk_q8_1 *)xb;
+                const float t = orc_fp16_to_fp32(w0->m) * orc_fp16_to_fp32(x0->s) +
+                                orc_fp16_to_fp32(w1->m) * orc_fp16_to_fp32(x1->s);
+                summs = summs + t;
+            }
+        }
+    }
+    float sumf;
+    if (variant == ORC_VARIANT_ARM_I8MM) return q41 ? acc + summs : acc;
+    if (variant == ORC_VARIANT_ARM_DOTPROD) {
+        sumf = vaddv4(v[0]) + vaddv4(v[1]);
+        if (q41) sumf = sumf + summs;
+        for (; b < nb; b++) { /* odd last block: the scalar tail */
+            const char *wb = w + b * wbs, *xb = x + b * xbs;
+            int32_t S = 0;
+            orc_block_isums(wtype, QK, wb, xb, &S);
+            const float dw = orc_fp16_to_fp32(*(const uint16_t *)wb), dx = orc_fp16_to_fp32(*(const uint16_t *)xb);
+            if (q41) {
+                const float t = fmaf(dw * dx, (float)S, orc_fp16_to_fp32(((const blk_q4_1 *)wb)->m) *
+                                                           orc_fp16_to_fp32(((const blk_q8_1 *)xb)->s));
+                sumf = sumf + t;
+            } else {
+                sumf = fmaf((float)S * dw, dx, sumf);
+            }
+        }
+        return sumf;
+    }
+    return vaddv4(v[0]); /* tinyBLAS_Q0_ARM: hsum of the one accumulator */
+}
+
+/* ggml_vec_dot_f32 on NEON (GGML_F32_STEP 16, four float32x4 accumulators). */
+static float vec_dot_f32_neon(int64_t n, const float *x, const float *y) {
+    const int64_t np = n & ~(int64_t)15;
+    float s[4][4] = {{0}};
+    for (int64_t i = 0; i < np; i += 16)
+        for (int j = 0; j < 4; j++)
+            for (int l = 0; l < 4; l++) s[j][l] = fmaf(x[i + 4 * j + l], y[i + 4 * j + l], s[j][l]);
+    for (int l = 0; l < 4; l++) {
+        s[0][l] = s[0][l] + s[2][l];
+        s[1][l] = s[1][l] + s[3][l];
+    }
+    for (int l = 0; l < 4; l++) s[0][l] = s[0][l] + s[1][l];
+    float sumf = vaddv4(s[0]);
+    for (int64_t i = np; i < n; ++i) sumf = fmaf(x[i], y[i], sumf);
+    return sumf;
+}
 
 float orc_vec_dot(int wtype, int64_t n, const void *w, const void *x) {
-    if (g_variant == 1 && n / QK <= 4096) return vec_dot_generic(wtype, n, w, x);
+    if (g_variant == ORC_VARIANT_GENERIC && n / QK <= 4096) return vec_dot_generic(wtype, n, w, x);
+    if (arm_variant()) {
+        if (wtype == ORC_TYPE_Q4_0 || wtype == ORC_TYPE_Q8_0 || wtype == ORC_TYPE_Q4_1)
+            return vec_dot_arm(g_variant, wtype, n, (const char *)w, (const char *)x);
+        if (wtype == ORC_TYPE_F32) return vec_dot_f32_neon(n, (const float *)w, (const float *)x);
+    }
     switch (wtype) {
         case ORC_TYPE_Q4_0: return vec_dot_q4_0_q8_0(n, (const blk_q4_0 *)w, (const blk_q8_0 *)x);
         case ORC_TYPE_Q8_0: return vec_dot_q8_0_q8_0(n, (const blk_q8_0 *)w, (const blk_q8_0 *)x);
@@ -625,7 +754,7 @@ void orc_mul_mat_preq(int wtype, const void *W, int64_t N, int64_t K,
     const size_t xrs = orc_row_size(vdt, K);
     const int64_t TM = 32, TN = 32;
     const int64_t tiles_m = (M + TM - 1) / TM, tiles_n = (N + TN - 1) / TN;
-    const int blocked = g_variant == 0 &&
+    const int blocked = g_variant == ORC_VARIANT_X86 &&
                         (wtype == ORC_TYPE_Q4_0 || wtype == ORC_TYPE_Q8_0 || wtype == ORC_TYPE_Q4_1);
     if (nthreads <= 0) nthreads = omp_get_max_threads();
 #pragma omp parallel for schedule(dynamic, 1) num_threads(nthreads)
@@ -766,7 +895,7 @@ void orc_flash_attn_ext(const float *q, int64_t qs1, int64_t qs2, int64_t qs3,
             for (int64_t j = 0; j < Nkv; j++) {
                 const float *kr = k + b * ks3 + h * ks2 + j * ks1;
                 /* K rows are contiguous in d (unit stride) in every caller. */
-                float s = vec_dot_f32(D, kr, Qrow);
+                float s = arm_variant() ? vec_dot_f32_neon(D, kr, Qrow) : vec_dot_f32(D, kr, Qrow);
                 s = s * scale;
                 const float Mold = M;
                 float ms = 1.0f, vs = 1.0f;

@@ -252,6 +252,20 @@ void orc_model_hparams(const orc_model *m, int32_t out[16]) {
 
 const orc_hiera_hp *orc_model_hiera(const orc_model *m) { return m->is_sam2 ? &m->h2 : NULL; }
 
+/* sam3_create_state's encode_img_size for a SAM 2 file (sam3.cpp:3392-3402):
+ * every later Hiera call builds its grids and positional embedding for
+ * img_size pixels per side (sam2_encode_image_hiera, :5862, uses the state's
+ * size; the PE is the bicubic resize for that grid, :4114-4171). */
+int orc_hiera_set_img_size(orc_model *m, int img_size) {
+    if (!m->is_sam2) { snprintf(g_err, sizeof g_err, "not a SAM 2 model"); return -1; }
+    if (img_size <= 0 || img_size % 32 != 0) {
+        snprintf(g_err, sizeof g_err, "image size %d is not a positive multiple of 32", img_size);
+        return -1;
+    }
+    m->h2.img_size = img_size;
+    return 0;
+}
+
 int orc_model_tensor(const orc_model *m, const char *prefix, const char *suffix, orc_tensor_view *out) {
     char buf[96];
     snprintf(buf, sizeof buf, "%s%s", prefix, suffix);

@@ -53,6 +53,10 @@ struct HieraModel {
     int64_t patch_k = 0;            // 3·7·7 padded to a multiple of 32
     Weight patch;
     float *patch_b = nullptr, *pe = nullptr;  // pe: [G][G][E0], bicubic background + tiled window
+    // the registered PE tensors as CHW on the host, for states encoding at
+    // another image size (the PE is recomputed for their grid)
+    std::vector<float> bkg_chw, win_chw;
+    int win_side = 0;
     std::vector<HBlock> blocks;
     Weight fpn[4];                  // fpn.convs.i, which maps stage 3 − i
     float *fpn_b[4] = {};
@@ -74,6 +78,12 @@ struct HieraModel {
 };
 
 struct HieraState {
+    // geometry of the image size this state encodes (sam3_effective_feat_size
+    // and the per-stage grids of sam2_build_hiera_graph for that size)
+    int img = 0, G = 0, side[4] = {};
+    std::vector<int> in_side;       // per block: tokens per side of its input
+    const float *pos = nullptr;     // [G][G][E0] PE: the model's, or pe_own
+    float *pe_own = nullptr;        // PE recomputed for a non-native size
     ActBuf col, a1, a2;             // im2col rows; GEMM inputs (E-wide, MLP-wide)
     float *xs[4] = {};              // stage residual streams = stage outputs
     float *qkv = nullptr, *dp = nullptr, *attn_f32 = nullptr;  // qkv: Q rows of Q-stride blocks
@@ -92,7 +102,7 @@ struct HieraState {
         a1.release();
         a2.release();
         for (void *p : {(void *)qkv, (void *)dp, (void *)attn_f32, (void *)q16, (void *)k16, (void *)vt16,
-                        (void *)fin, (void *)part, (void *)gws})
+                        (void *)fin, (void *)part, (void *)gws, (void *)pe_own})
             if (p) (void)hipFree(p);
         for (int i = 0; i < 4; i++)
             for (void *p : {(void *)xs[i], (void *)lat[i], (void *)pe[i]})
@@ -130,6 +140,24 @@ int upload_f32(HieraModel *m, const RawTensor &t, int64_t expect, float **dst) {
 // sam2_precompute_hiera_metadata (sam3.cpp:1676-1742): the window size lags
 // a block (a stage's first block keeps the previous stage's window); global
 // blocks have window 0; Q stride at the first block of stages 1..q_pool.
+// Grids for an image of img pixels per side: the patch embedding (7×7,
+// stride 4, pad 3) gives img / 4 tokens per side, every Q-stride block halves
+// it (sam3_effective_feat_size, sam3.cpp:245-257).  side[i]: stage i's grid;
+// in_side[b]: block b's input grid.
+void geometry(const HieraModel *m, int img, int side[4], std::vector<int> &in_side) {
+    int g = img / 4;
+    in_side.assign(m->blocks.size(), 0);
+    for (size_t i = 0; i < m->blocks.size(); i++) {
+        in_side[i] = g;
+        if (m->blocks[i].qs) g /= 2;
+    }
+    int s = img / 4;
+    for (int i = 0; i < 4; i++) {
+        if (i > 0 && i <= m->q_pool) s /= 2;
+        side[i] = s;
+    }
+}
+
 void block_metadata(HieraModel *m) {
     int total = 0, ends[4], cum = 0;
     for (int s = 0; s < 4; s++) { cum += m->stages[s]; ends[s] = cum - 1; total += m->stages[s]; }
@@ -153,18 +181,10 @@ void block_metadata(HieraModel *m) {
         b.qs = std::find(qblocks.begin(), qblocks.end(), i) != qblocks.end();
         dim = dout;
     }
-    int side = m->img / 4;
-    for (HBlock &b : m->blocks) {
-        b.in_side = side;
-        if (b.qs) side /= 2;
-    }
-    int s = m->img / 4, d = m->E0;
-    for (int i = 0; i < 4; i++) {
-        if (i > 0 && i <= m->q_pool) s /= 2;
-        m->side[i] = s;
-        m->width[i] = d;
-        d *= 2;
-    }
+    std::vector<int> in_side;
+    geometry(m, m->img, m->side, in_side);
+    for (size_t i = 0; i < m->blocks.size(); i++) m->blocks[i].in_side = in_side[i];
+    for (int i = 0, d = m->E0; i < 4; i++, d *= 2) m->width[i] = d;
 }
 
 // sam2_bicubic_interpolate_cpu (sam3.cpp:4072-4107): Keys cubic a = −0.75,
@@ -202,6 +222,20 @@ void bicubic(const float *src, int C, int Hi, int Wi, float *dst, int Ho, int Wo
 
 // ggml_gelu's fp16 table (ggml_vec_gelu_f32 with GGML_GELU_FP16):
 // fp16(0.5·v·(1 + tanhf(√(2/π)·v·(1 + 0.044715·v²)))) for every fp16 v.
+// sam2_compute_pos_embed (sam3.cpp:4114-4171) for a G × G token grid:
+// bicubic background + the window PE tiled, as [G][G][E0]
+std::vector<float> pos_embed(const HieraModel *m, int G) {
+    const int E = m->E0, ws = m->win_side;
+    std::vector<float> interp((size_t)E * G * G), pe((size_t)E * G * G);
+    bicubic(m->bkg_chw.data(), E, m->bkg_h, m->bkg_w, interp.data(), G, G);
+    for (int y = 0; y < G; ++y)
+        for (int x = 0; x < G; ++x)
+            for (int e = 0; e < E; ++e)
+                pe[((size_t)y * G + x) * E + e] = interp[(size_t)e * G * G + (size_t)y * G + x] +
+                                                  m->win_chw[(size_t)e * ws * ws + (y % ws) * ws + (x % ws)];
+    return pe;
+}
+
 std::vector<uint16_t> gelu_table() {
     std::vector<uint16_t> t(65536);
     const float SQRT_2_OVER_PI = 0.79788456080286535587989211986876f, A = 0.044715f;
@@ -398,15 +432,11 @@ int hiera_load(int device, std::ifstream &fin, int ftype, int32_t n_tensors, Hie
     }
     // positional embedding (sam2_compute_pos_embed, sam3.cpp:4114-4171): the
     // registered [bkg_w, bkg_h, E, 1] bytes are CHW [E][bkg_h][bkg_w]
+    m->bkg_chw = std::move(bkg);
+    m->win_chw = std::move(win);
+    m->win_side = (int)win_side;
     {
-        const int E = m->E0, G = m->G, ws = (int)win_side;
-        std::vector<float> interp((size_t)E * G * G), pe((size_t)E * G * G);
-        bicubic(bkg.data(), E, m->bkg_h, m->bkg_w, interp.data(), G, G);
-        for (int y = 0; y < G; ++y)
-            for (int x = 0; x < G; ++x)
-                for (int e = 0; e < E; ++e)
-                    pe[((size_t)y * G + x) * E + e] =
-                        interp[(size_t)e * G * G + (size_t)y * G + x] + win[(size_t)e * ws * ws + (y % ws) * ws + (x % ws)];
+        const std::vector<float> pe = pos_embed(m.get(), m->G);
         void *p = nullptr;
         if (hipMalloc(&p, pe.size() * 4) != hipSuccess || hipMemcpy(p, pe.data(), pe.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
             set_error("s3e_model_load: positional embedding upload failed");
@@ -450,10 +480,31 @@ void hiera_hparams(const HieraModel *m, int32_t out[16]) {
     out[15] = 1;
 }
 
-int hiera_state_create(const HieraModel *m, hipStream_t st, HieraState **out) {
+int hiera_state_create(const HieraModel *m, int img, hipStream_t st, HieraState **out) {
     *out = nullptr;
+    if (img == 0) img = m->img;
+    // the patch grid must halve evenly at every Q-stride block and at the
+    // FPN's top-down steps, as at the native size (a multiple of 32)
+    if (img < 32 || img % 32 != 0 || img > 4096) {
+        set_error("s3e_state_create: encode image size %d is not a multiple of 32 in [32, 4096]", img);
+        return S3E_ERR_UNSUPPORTED;
+    }
     std::unique_ptr<HieraState> s(new HieraState);
-    const int64_t G = m->G, T0 = G * G;
+    s->img = img;
+    s->G = img / 4;
+    geometry(m, img, s->side, s->in_side);
+    if (img == m->img) {
+        s->pos = m->pe;
+    } else {
+        const std::vector<float> pe = pos_embed(m, s->G);
+        if (hipMalloc(&s->pe_own, pe.size() * 4) != hipSuccess ||
+            hipMemcpy(s->pe_own, pe.data(), pe.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
+            set_error("s3e_state_create: positional embedding upload failed");
+            return S3E_ERR_NOMEM;
+        }
+        s->pos = s->pe_own;
+    }
+    const int64_t G = s->G, T0 = G * G;
     hipError_t e = s->col.alloc(T0, m->patch_k, st);
     int64_t emax = 0, qkv_cap = 0, dp_cap = 0, q_cap = 0, k_cap = 0, v_cap = 0, attn_cap = 0, part_cap = 0;
     int64_t gws_cap = 0;
@@ -486,7 +537,7 @@ int hiera_state_create(const HieraModel *m, hipStream_t st, HieraState **out) {
     if (e == hipSuccess) e = s->a1.alloc(T0, emax, st);
     if (e == hipSuccess) e = s->a2.alloc(T0, 4 * emax, st);
     for (int i = 0; i < 4 && e == hipSuccess; i++)
-        e = hipMalloc(&s->xs[i], (size_t)m->side[i] * m->side[i] * m->width[i] * 4);
+        e = hipMalloc(&s->xs[i], (size_t)s->side[i] * s->side[i] * m->width[i] * 4);
     if (e == hipSuccess) e = hipMalloc(&s->qkv, (size_t)std::max<int64_t>(qkv_cap, 1) * 4);
     if (e == hipSuccess) e = hipMalloc(&s->dp, (size_t)dp_cap * 4);
     if (e == hipSuccess) e = hipMalloc(&s->attn_f32, (size_t)attn_cap * 4);
@@ -501,11 +552,11 @@ int hiera_state_create(const HieraModel *m, hipStream_t st, HieraState **out) {
     if (e == hipSuccess) e = hipMalloc(&s->k16, (size_t)k_cap * 2 * 2);
     if (e == hipSuccess) e = hipMalloc(&s->vt16, (size_t)v_cap * 2 * 2);
     s->fin_cap = 0;
-    for (int i = 0; i < 4; i++) s->fin_cap = std::max<int64_t>(s->fin_cap, (int64_t)m->side[i] * m->side[i] * m->width[i]);
+    for (int i = 0; i < 4; i++) s->fin_cap = std::max<int64_t>(s->fin_cap, (int64_t)s->side[i] * s->side[i] * m->width[i]);
     if (e == hipSuccess) e = hipMalloc(&s->fin, (size_t)s->fin_cap * 2 * 2);
-    for (int i = 0; i < 4 && e == hipSuccess; i++) e = hipMalloc(&s->lat[i], (size_t)m->side[i] * m->side[i] * m->D * 4);
+    for (int i = 0; i < 4 && e == hipSuccess; i++) e = hipMalloc(&s->lat[i], (size_t)s->side[i] * s->side[i] * m->D * 4);
     for (int i = 0; i < 4 - m->scalp && e == hipSuccess; i++) {
-        const std::vector<float> pe = sinusoidal_pe_2d(m->side[i], m->side[i], m->D);
+        const std::vector<float> pe = sinusoidal_pe_2d(s->side[i], s->side[i], m->D);
         e = hipMalloc(&s->pe[i], pe.size() * 4);
         if (e == hipSuccess) e = hipMemcpy(s->pe[i], pe.data(), pe.size() * 4, hipMemcpyHostToDevice);
     }
@@ -519,13 +570,16 @@ int hiera_state_create(const HieraModel *m, hipStream_t st, HieraState **out) {
 
 void hiera_state_free(HieraState *s) { delete s; }
 
+int hiera_state_img(const HieraState *s) { return s->img; }
+
 hipError_t hiera_block(const HieraModel *m, HieraState *s, int bi, const float *x, int H, int W, float *y,
                        hipStream_t st) {
     if (bi < 0 || bi >= (int)m->blocks.size()) return hipErrorInvalidValue;
     const HBlock &b = m->blocks[(size_t)bi];
     // the state's buffers are sized for the encoder's grids; a block that
     // changes size cannot run in place
-    if (H <= 0 || W <= 0 || H > b.in_side || W > b.in_side || (b.qs && (H % 2 || W % 2)) ||
+    const int in_side = s->in_side[(size_t)bi];
+    if (H <= 0 || W <= 0 || H > in_side || W > in_side || (b.qs && (H % 2 || W % 2)) ||
         (x == y && (b.qs || b.din != b.dout)))
         return hipErrorInvalidValue;
     const int64_t T = (int64_t)H * W;
@@ -651,16 +705,16 @@ hipError_t hiera_block(const HieraModel *m, HieraState *s, int bi, const float *
 }
 
 hipError_t hiera_encode(const HieraModel *m, HieraState *s, const float *chw, hipStream_t st) {
-    const int G = m->G;
+    const int G = s->G;
     // patch embedding 7×7 / 4 / 3 + bias + positional embedding
     const AKind pk = m->patch.kind == WK_F16 ? A_F16 : A_F32;
-    hipError_t e = launch_im2col_conv(chw, m->img, 7, 4, 3, m->patch_k, pk, s->col.x, st);
+    hipError_t e = launch_im2col_conv(chw, s->img, 7, 4, 3, m->patch_k, pk, s->col.x, st);
     if (e != hipSuccess) return e;
     EpiArgs ea;
     ea.bias = m->patch_b;
     ea.y = s->xs[0];
     ea.ldy = m->E0;
-    ea.pos = m->pe;
+    ea.pos = s->pos;
     ea.pos_grid = G;
     ea.grid = G;
     if ((e = launch_gemm(m->patch, s->col.as(pk, m->patch_k), (int64_t)G * G, EPI_POS, ea, st)) != hipSuccess) return e;
@@ -677,7 +731,7 @@ hipError_t hiera_encode(const HieraModel *m, HieraState *s, const float *chw, hi
     // FPN: lateral 1×1 (+ bias) per stage, then nearest ×2 top-down adds
     for (int i = 0; i < 4; i++) {
         const Weight &w = m->fpn[3 - i];
-        const int sd = m->side[i], ch = m->width[i];
+        const int sd = s->side[i], ch = m->width[i];
         const Act in = plane_act(act_kind_for(w.kind), s->fin, s->fin_cap, ch);
         if ((e = launch_pool_act(s->xs[i], sd, sd, ch, 1, in, st)) != hipSuccess) return e;
         EpiArgs el;
@@ -692,8 +746,8 @@ hipError_t hiera_encode(const HieraModel *m, HieraState *s, const float *chw, hi
         for (int j = 0; j < m->td_n; j++)
             if (m->td[j] == i) td = true;
         if (td && prev >= 0) {
-            if (m->side[i] != 2 * m->side[prev]) return hipErrorInvalidValue;
-            if ((e = launch_upsample_add(s->lat[i], s->lat[prev], m->side[i], m->D, st)) != hipSuccess) return e;
+            if (s->side[i] != 2 * s->side[prev]) return hipErrorInvalidValue;
+            if ((e = launch_upsample_add(s->lat[i], s->lat[prev], s->side[i], m->D, st)) != hipSuccess) return e;
             prev = i;
         } else if (td || prev < 0) {
             prev = i;
@@ -715,16 +769,16 @@ const float *hiera_find_tensor(const HieraModel *m, const HieraState *s, const c
     const int n_out = 4 - m->scalp;
     if (level("neck_trk_pe_", &i) || level("pe_", &i)) {
         if (i >= n_out) return nullptr;
-        ne[0] = m->D; ne[1] = m->side[i]; ne[2] = m->side[i]; ne[3] = 1;
+        ne[0] = m->D; ne[1] = s->side[i]; ne[2] = s->side[i]; ne[3] = 1;
         return s->pe[i];
     }
     if (level("neck_trk_", &i)) {
         if (i >= n_out) return nullptr;
-        ne[0] = m->D; ne[1] = m->side[i]; ne[2] = m->side[i]; ne[3] = 1;
+        ne[0] = m->D; ne[1] = s->side[i]; ne[2] = s->side[i]; ne[3] = 1;
         return s->lat[i];
     }
     if (level("hiera_stage_", &i)) {
-        ne[0] = m->width[i]; ne[1] = m->side[i]; ne[2] = m->side[i]; ne[3] = 1;
+        ne[0] = m->width[i]; ne[1] = s->side[i]; ne[2] = s->side[i]; ne[3] = 1;
         return s->xs[i];
     }
     return nullptr;

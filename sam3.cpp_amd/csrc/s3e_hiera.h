@@ -24,8 +24,11 @@ void hiera_free(HieraModel *m);
 void hiera_hparams(const HieraModel *m, int32_t out[16]);
 int hiera_img_size(const HieraModel *m);
 
-int hiera_state_create(const HieraModel *m, hipStream_t st, HieraState **out);
+// img: the image size this state encodes (0: the model's own); the token
+// grids, buffers and positional embedding follow it
+int hiera_state_create(const HieraModel *m, int img, hipStream_t st, HieraState **out);
 void hiera_state_free(HieraState *s);
+int hiera_state_img(const HieraState *s);
 // chw: preprocessed image on the device ([3][S][S] f32)
 hipError_t hiera_encode(const HieraModel *m, HieraState *s, const float *chw, hipStream_t st);
 // Block idx on x ([H·W][dim_in] f32, device) into y ([Ho·Wo][dim_out]).

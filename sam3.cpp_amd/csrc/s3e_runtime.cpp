@@ -1367,6 +1367,7 @@ extern "C" int s3e_model_hparams(const s3e_model *m, int32_t out[16]) try {
 struct s3e_state {
     s3e_ctx *ctx = nullptr;
     const s3e_model *m = nullptr;
+    int img = 0;                  // image size this state encodes (the model's, or a SAM 2 override)
     MemAttnState *mas = nullptr;  // memory-attention scratch, made at first use
     int64_t T = 0;
     float *x = nullptr;       // residual stream, T × E f32 ("vit_output" after encode)
@@ -1485,16 +1486,29 @@ hipError_t alloc_neck(s3e_state *st) {
 
 }  // namespace
 
-extern "C" int s3e_state_create(s3e_ctx *ctx, const s3e_model *m, s3e_state **out) try {
+extern "C" int s3e_state_create(s3e_ctx *ctx, const s3e_model *m, s3e_state **out) {
+    return s3e_state_create_sized(ctx, m, 0, out);
+}
+
+extern "C" int s3e_state_create_sized(s3e_ctx *ctx, const s3e_model *m, int img_size, s3e_state **out) try {
     if (!ctx || !m || !out) { set_error("s3e_state_create: NULL argument"); return S3E_ERR_INVALID; }
     *out = nullptr;
+    if (img_size < 0) { set_error("s3e_state_create: negative image size"); return S3E_ERR_INVALID; }
+    // sam3_create_state (sam3.cpp:3392-3402): a state may encode at another
+    // image size than the model's; the engine builds SAM 2.x (Hiera)
+    // encoders for any multiple of 32 and the SAM 3 ViT at its native grid
+    if (!m->hiera && img_size != 0 && img_size != m->img) {
+        set_error("s3e_state_create: a SAM 3 file encodes at its native %d px (asked %d)", m->img, img_size);
+        return S3E_ERR_UNSUPPORTED;
+    }
     HIP_TRY(hipSetDevice(ctx->device));
     auto *st = new s3e_state;
     st->ctx = ctx;
     st->m = m;
+    st->img = img_size > 0 ? img_size : m->img;
     if (m->hiera) {
-        hipError_t e = hipMalloc(&st->chw, (size_t)3 * m->img * m->img * 4);
-        const int rc = e == hipSuccess ? hiera_state_create(m->hiera, ctx->stream, &st->hst) : (int)S3E_ERR_NOMEM;
+        hipError_t e = hipMalloc(&st->chw, (size_t)3 * st->img * st->img * 4);
+        const int rc = e == hipSuccess ? hiera_state_create(m->hiera, st->img, ctx->stream, &st->hst) : (int)S3E_ERR_NOMEM;
         if (rc != S3E_OK) {
             if (e != hipSuccess) set_error("s3e_state_create: %s", hipGetErrorString(e));
             s3e_state_free(st);
@@ -2174,7 +2188,7 @@ extern "C" int s3e_hiera_block(s3e_state *st, int idx, const float *x_device, in
 extern "C" int s3e_encode_chw_host(s3e_state *st, const float *chw_host) try {
     if (!st || !chw_host) { set_error("s3e_encode_chw_host: NULL argument"); return S3E_ERR_INVALID; }
     HIP_TRY(hipSetDevice(st->ctx->device));
-    HIP_TRY(hipMemcpyAsync(st->chw, chw_host, (size_t)3 * st->m->img * st->m->img * 4, hipMemcpyHostToDevice,
+    HIP_TRY(hipMemcpyAsync(st->chw, chw_host, (size_t)3 * st->img * st->img * 4, hipMemcpyHostToDevice,
                            st->ctx->stream));
     return s3e_encode_chw(st, st->chw);
 } S3E_CATCH("s3e_encode_chw_host")
@@ -2208,7 +2222,7 @@ extern "C" int s3e_encode_image_u8(s3e_state *st, const uint8_t *hwc, int width,
     }
     HIP_TRY(hipMemcpyAsync(st->img8, hwc, bytes, hipMemcpyHostToDevice, st->ctx->stream));
     const int norm = st->m->hiera ? S3E_NORM_IMAGENET : S3E_NORM_SAM3;
-    int rc = s3e_preprocess_image(st->ctx, st->img8, width, height, st->m->img, norm, st->chw);
+    int rc = s3e_preprocess_image(st->ctx, st->img8, width, height, st->img, norm, st->chw);
     if (rc == S3E_OK) rc = s3e_encode_chw(st, st->chw);
     if (rc != S3E_OK) return rc;
     return s3e_ctx_sync(st->ctx);

@@ -31,6 +31,7 @@ struct sam3_model {
 struct sam3_state {
     const sam3_model *model = nullptr;
     s3e_state *st = nullptr;
+    int img = 0;            // image size this state encodes (encode_img_size or the model's)
     bool vit_only = false;  // after sam3_encode_vit_from_preprocessed_selective
     ~sam3_state() { sam3_free_state(*this); }
 };
@@ -109,15 +110,14 @@ sam3_state_ptr sam3_create_state(const sam3_model &model, const sam3_params &par
         fprintf(stderr, "%s: model is not loaded\n", __func__);
         return nullptr;
     }
-    if (params.encode_img_size != 0 && params.encode_img_size != model.hp[HP_IMG]) {
-        fprintf(stderr, "%s: encode_img_size %d is not supported (the model's grid is fixed at %d)\n", __func__,
-                params.encode_img_size, model.hp[HP_IMG]);
-        return nullptr;
-    }
     sam3_state_ptr st(new (std::nothrow) sam3_state);
     if (!st) return nullptr;
     st->model = &model;
-    if (s3e_state_create(model.ctx, model.enc, &st->st) != S3E_OK) {
+    st->img = params.encode_img_size > 0 ? params.encode_img_size : model.hp[HP_IMG];
+    if (st->img != model.hp[HP_IMG])
+        fprintf(stderr, "%s: encode_img_size=%d (model native=%d)\n", __func__, st->img, model.hp[HP_IMG]);
+    if (s3e_state_create_sized(model.ctx, model.enc, params.encode_img_size > 0 ? params.encode_img_size : 0,
+                               &st->st) != S3E_OK) {
         fprintf(stderr, "%s: %s\n", __func__, s3e_last_error());
         return nullptr;
     }
@@ -156,6 +156,11 @@ bool sam3_encode_image_from_preprocessed(sam3_state &state, const sam3_model &mo
     }
     if (img_size != model.hp[HP_IMG]) {
         fprintf(stderr, "%s: img_size mismatch: got %d, expected %d\n", __func__, img_size, model.hp[HP_IMG]);
+        return false;
+    }
+    if (state.img != img_size) {
+        fprintf(stderr, "%s: the state encodes %d px images (encode_img_size); use sam3_encode_image\n", __func__,
+                state.img);
         return false;
     }
     if (s3e_encode_chw_host(state.st, chw_data) != S3E_OK || s3e_ctx_sync(model.ctx) != S3E_OK) {

@@ -154,7 +154,7 @@ int run_stages(const sam3_model &model, sam3_state &state, const std::vector<flo
 int usage() {
     fprintf(stderr,
             "usage: sam3_encode -m model.ggml (-i image.ppm | -p chw.f32 -s img_size) -o out_prefix\n"
-            "                   [-t name,name,...] [-r repeats] [(-b | -B) block]\n");
+            "                   [-t name,name,...] [-r repeats] [(-b | -B) block] [-e encode_img_size]\n");
     return 1;
 }
 
@@ -162,7 +162,7 @@ int usage() {
 
 int main(int argc, char **argv) {
     std::string model_path, image_path, chw_path, out = "./", tensors;
-    int img_size = 0, repeats = 1, stage_block = -1;
+    int img_size = 0, repeats = 1, stage_block = -1, encode_img_size = 0;
     bool stage_global = false;
     for (int i = 1; i < argc; i++) {
         const std::string a = argv[i];
@@ -175,6 +175,7 @@ int main(int argc, char **argv) {
         else if (a == "-o") out = v;
         else if (a == "-t") tensors = v;
         else if (a == "-r") repeats = std::atoi(v.c_str());
+        else if (a == "-e") encode_img_size = std::atoi(v.c_str());
         else if (a == "-b" || a == "-B") {
             stage_block = std::atoi(v.c_str());
             stage_global = a == "-B";
@@ -185,6 +186,7 @@ int main(int argc, char **argv) {
 
     sam3_params params;
     params.model_path = model_path;
+    params.encode_img_size = encode_img_size;
     auto model = sam3_load_model(params);
     if (!model) return 1;
     auto state = sam3_create_state(*model, params);

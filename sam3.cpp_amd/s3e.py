@@ -100,6 +100,7 @@ def _load() -> ctypes.CDLL:
         "s3e_model_free": (None, [c_void_p]),
         "s3e_model_hparams": (c_int, [c_void_p, POINTER(c_int32)]),
         "s3e_state_create": (c_int, [c_void_p, c_void_p, POINTER(c_void_p)]),
+        "s3e_state_create_sized": (c_int, [c_void_p, c_void_p, c_int, POINTER(c_void_p)]),
         "s3e_state_free": (None, [c_void_p]),
         "s3e_encode_chw": (c_int, [c_void_p, c_void_p]),
         "s3e_encode_chw_host": (c_int, [c_void_p, c_void_p]),
@@ -136,7 +137,7 @@ DECLARED = [
     "s3e_malloc", "s3e_free", "s3e_memcpy_h2d", "s3e_memcpy_d2h", "s3e_weight_upload", "s3e_weight_free",
     "s3e_weight_info", "s3e_mul_mat", "s3e_mul_mat_noalloc", "s3e_mul_mat_q", "s3e_mul_mat_q_f6", "s3e_mul_mat_q_batch", "s3e_quantize_rows", "s3e_layer_norm", "s3e_copy",
     "s3e_flash_attn_ext", "s3e_flash_attn_ext_f16", "s3e_model_load",
-    "s3e_model_free", "s3e_model_hparams", "s3e_state_create", "s3e_state_free", "s3e_encode_chw",
+    "s3e_model_free", "s3e_model_hparams", "s3e_state_create", "s3e_state_create_sized", "s3e_state_free", "s3e_encode_chw",
     "s3e_encode_chw_host", "s3e_encode_image_u8", "s3e_preprocess_image", "s3e_vit_prefix", "s3e_vit_block", "s3e_vit_block_stage", "s3e_vit_prefix_stage", "s3e_encode_vit_chw", "s3e_model_tensor_get", "s3e_run_neck", "s3e_hiera_block", "s3e_model_type", "s3e_mem_attn_dims", "s3e_mem_attn",
     "s3e_state_tensor_info",
     "s3e_state_tensor_get", "s3e_state_tensor_device", "s3e_synth_write", "s3e_synth_write_sam2",
@@ -407,10 +408,13 @@ class Model:
 
 
 class State:
-    def __init__(self, ctx: Context, model: Model):
+    def __init__(self, ctx: Context, model: Model, img_size: int = 0):
+        """img_size: the image size this state encodes (0: the model's own;
+        SAM 2 files accept any multiple of 32)."""
         self.ctx, self.model = ctx, model
         h = c_void_p()
-        check(LIB.s3e_state_create(ctx.handle, model.handle, ctypes.byref(h)), "s3e_state_create")
+        check(LIB.s3e_state_create_sized(ctx.handle, model.handle, int(img_size), ctypes.byref(h)),
+              "s3e_state_create_sized")
         self.handle = h.value
 
     def encode_chw(self, chw: DeviceBuffer):

@@ -89,6 +89,7 @@ def _load():
         "orc_hiera_block": (c_int, [P, c_int, P, c_int, c_int, P, P, P, c_int]),
         "orc_hiera_fpn": (c_int, [P, P, P, P, c_int]),
         "orc_hiera_encode": (c_int, [P, P, P, P, c_int]),
+        "orc_hiera_set_img_size": (c_int, [P, c_int]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -294,9 +295,19 @@ class OracleHiera:
         self.hp = HieraHp.from_address(hp)
         self.img = self.hp.img_size
         self.nblocks = LIB.orc_hiera_num_blocks(self.h)
+        self._dims()
+
+    def _dims(self):
         side, width = np.zeros(4, np.int32), np.zeros(4, np.int32)
         LIB.orc_hiera_dims(self.h, ptr(side), ptr(width))
         self.side, self.width = [int(v) for v in side], [int(v) for v in width]
+
+    def set_img_size(self, img: int):
+        """Encode at img pixels per side from now on (sam3_create_state's
+        encode_img_size)."""
+        assert LIB.orc_hiera_set_img_size(self.h, img) == 0, LIB.orc_last_error()
+        self.img = img
+        self._dims()
 
     def block_info(self, i: int):
         out = np.zeros(7, np.int32)

@@ -246,3 +246,31 @@ def test_encode_full_size(variant, ft, tmpdir_session, ctx):
     finally:
         st.free()
         gm.free()
+
+
+@pytest.mark.parametrize("variant,native,size,ft", [("hiera_t", 1024, 512, "f16"), ("hiera_b+", 512, 256, "q4_0"),
+                                                    ("small", 192, 128, "q8_0"), ("small", 192, 288, "f32")])
+def test_encode_at_state_image_size(variant, native, size, ft, tmpdir_session, ctx):
+    """A state encoding at another image size than the model's
+    (sam3_create_state with encode_img_size, sam3.cpp:3392-3402; the grids
+    of sam3_effective_feat_size, :245-257; the PE bicubic-resized for the
+    new grid, :4114-4171): smaller and larger than native, against the
+    oracle set to the same size."""
+    import s3e
+
+    path = os.path.join(str(tmpdir_session), f"{variant}_{native}_{ft}_sized.ggml")
+    _write(path, variant, native, ft)
+    om = orc.OracleHiera(path)
+    om.set_img_size(size)
+    gm = s3e.Model(ctx, path)
+    st = s3e.State(ctx, gm, img_size=size)
+    try:
+        img = np.random.default_rng(7).integers(0, 256, (size + 37, size - 21, 3), dtype=np.uint8)
+        print(f"{variant}@{native} {ft} encoded at {size}", flush=True)
+        _encode_and_compare(f"{variant}@{native}->{size} {ft}", ft, om, st, img)
+        assert st.tensor("neck_trk_0").shape == ((size // 4) ** 2, om.hp.neck_dim)
+        with pytest.raises(s3e.S3EError):
+            s3e.State(ctx, gm, img_size=size + 16)  # not a multiple of 32
+    finally:
+        st.free()
+        gm.free()

@@ -232,3 +232,42 @@ def test_encode_composes_the_stages(small_hiera):
     lv = om.fpn(st)
     for a, b in zip(outs, lv):
         assert np.array_equal(a, b)
+
+
+def test_encode_at_another_image_size(small_hiera):
+    """sam3_create_state's encode_img_size on a SAM 2 file (sam3.cpp:3392-3402,
+    :245-257, :5862): the same model encoding 128 px images instead of its
+    native 192 — a 32 × 32 patch grid, stage grids 32/16/8/4, the positional
+    embedding bicubic-resized to 32 × 32 plus the window PE tiled, and every
+    block on the smaller grid (windows now padded differently) — against the
+    float64 torch restatement."""
+    p, _, tensors = small_hiera
+    om = orc.OracleHiera(p)
+    om.set_img_size(128)
+    assert om.side == [32, 16, 8, 4]
+    rng = np.random.default_rng(9)
+    chw = rng.standard_normal((3, 128, 128)).astype(np.float32)
+    x = om.prefix(chw)
+    w = _w(tensors, "hiera.patch_embed.weight")
+    conv = F.conv2d(t64(chw)[None], w, _w(tensors, "hiera.patch_embed.bias"), stride=4, padding=3)[0]
+    bkg = _w(tensors, "hiera.pos_embed")[0]
+    win = _w(tensors, "hiera.pos_embed_window")[0]
+    pe = F.interpolate(bkg[None], size=(32, 32), mode="bicubic", align_corners=False)[0] + win.repeat(1, 4, 4)
+    assert orc.rel_l2(x, (conv + pe).permute(1, 2, 0).reshape(32 * 32, 32).numpy()) < 1e-6
+    H = W = 32
+    stages = []
+    for bi in range(om.nblocks):
+        info = om.block_info(bi)
+        got, Ho, Wo = om.block(bi, x, H, W)
+        ref, Hr, Wr = _torch_block(x, H, W, tensors, bi, info, gelu=_table_gelu)
+        assert (Ho, Wo) == (Hr, Wr)
+        assert orc.rel_l2(got, ref) < 3e-5, (bi, info)
+        x, H, W = got, Ho, Wo
+        if info["stage_end"]:
+            stages.append(x)
+    outs, st = om.encode(chw)
+    assert [o.shape[0] for o in outs] == [32 * 32, 16 * 16, 8 * 8]
+    for a, b in zip(stages, st):
+        assert np.array_equal(a, b)
+    with pytest.raises(AssertionError):
+        om.set_img_size(100)  # not a multiple of 32

@@ -251,3 +251,53 @@ def test_example_stage_hooks_match_oracle(tmp_path, s3e_lib):
             assert ne == one and orc.rel_l2(got, ref) <= 1e-5, nm
         got, ne = dump("vit_output")
         assert orc.rel_l2(got, om.encode(chw).ravel()) <= 2e-3
+
+
+@pytest.mark.gpu
+def test_example_encode_img_size(tmp_path, s3e_lib):
+    """sam3_params::encode_img_size through the sam3.h API: a SAM 2 file with
+    a 512 px native size encoded at 256 px (sam3_create_state, sam3.cpp:
+    3392-3402; the Hiera grids halve and the positional embedding is
+    re-interpolated) against the oracle at that size; a SAM 3 file refuses a
+    non-native size at sam3_create_state."""
+    import ctypes
+
+    path = str(tmp_path / "h.ggml")
+    s3e_lib.synth_write_sam2(path, "hiera_t", img_size=512, ftype="q8_0", seed=29, std=0.05, random_affine=True)
+    img = np.random.default_rng(12).integers(0, 256, (300, 380, 3), dtype=np.uint8)
+    _write_ppm(str(tmp_path / "img.ppm"), img)
+    out = str(tmp_path / "h_")
+    print("sam3_encode (SAM 2, encode_img_size 256)", flush=True)
+    r = subprocess.run([EXE, "-m", path, "-i", str(tmp_path / "img.ppm"), "-o", out, "-e", "256"],
+                       capture_output=True, text=True, timeout=120)
+    print(r.stdout, r.stderr[-2000:], flush=True)
+    assert r.returncode == 0
+    assert "encode_img_size=256 (model native=512)" in r.stderr
+    om = orc.OracleHiera(path)
+    om.set_img_size(256)
+    chw = orc.preprocess_sam2(img, 256)
+    orc.LIB.orc_set_variant.argtypes = [ctypes.c_int]
+    refs = []
+    for variant in (0, 1):
+        orc.LIB.orc_set_variant(variant)
+        try:
+            levels, stages = om.encode(chw)
+            refs.append(levels + stages)
+        finally:
+            orc.LIB.orc_set_variant(0)
+    names = [f"neck_trk_{i}" for i in range(3)] + [f"hiera_stage_{i}" for i in range(4)]
+    shapes = [[256, s, s] for s in (64, 32, 16)] + [[96 << i, 64 >> i, 64 >> i] for i in range(4)]
+    for k, (name, shp) in enumerate(zip(names, shapes)):
+        shape, got = _read_dump(out + name)
+        assert shape == shp, name
+        ref = refs[0][k].ravel()
+        gap, gma = orc.rel_l2(refs[1][k], refs[0][k]), orc.max_abs(refs[1][k], refs[0][k])
+        rl, ma = orc.rel_l2(got, ref), orc.max_abs(got, ref)
+        print(f"{name} @256: rel_l2={rl:.3e} max_abs={ma:.3e} (ggml order gap {gap:.2e}/{gma:.2e})", flush=True)
+        assert rl <= max(1e-3, 2.0 * gap) and ma <= max(5e-3, 2.0 * gma), name
+    # a SAM 3 file keeps its native grid
+    p3 = str(tmp_path / "v.ggml")
+    s3e_lib.synth_write(p3, img_size=336, depth=1, window=8, global_idx=(0,), ftype="q8_0", seed=2)
+    r = subprocess.run([EXE, "-m", p3, "-i", str(tmp_path / "img.ppm"), "-o", out, "-e", "224"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode != 0 and "native 336 px" in r.stderr, r.stderr[-1000:]
