@@ -415,3 +415,61 @@ def test_flash_attn_f16_rejects(ctx):
         ctx.flash_attn_ext_f16(x, nb, x, nb, x, nb, 60 + 2, 64, 64, 1, 1, 0.1, o)  # head dim not a multiple of 4
     with pytest.raises(s3e.S3EError):
         ctx.flash_attn_ext_f16(x, (2, 64, 4096, 4096), x, nb, x, nb, 64, 64, 64, 1, 1, 0.1, o)  # strided d
+
+
+def _ggml_q8_0_rows(codes: np.ndarray, d_bits: np.ndarray) -> np.ndarray:
+    """ggml block_q8_0 rows (fp16 d, then 32 int8 codes per block) from codes
+    [M][K] and scale bits [M][K/32]."""
+    M, K = codes.shape
+    out = np.empty((M, K // 32, 34), np.uint8)
+    out[:, :, :2] = d_bits.astype(np.uint16).view(np.uint8).reshape(M, K // 32, 2)
+    out[:, :, 2:] = codes.reshape(M, K // 32, 32).view(np.uint8)
+    return out.reshape(M, -1)
+
+
+@pytest.mark.parametrize("wt", [orc.Q4_0, orc.Q8_0], ids=["q4_0", "q8_0"])
+@pytest.mark.parametrize("M,N,K", [(1024, 4096, 1024), (5184, 1024, 4736), (300, 2304, 96)])
+def test_mul_mat_q_equals_ggml_i8mm_order(ctx, wt, M, N, K):
+    """ggml's ARM vec_dot with two rows per call (vmmlaq_s32, the i8mm path
+    of arch/arm/quants.c [ext]) forms every output as one fp32 chain
+    acc = fma(S_b, d_w·d_x, acc) over the exact integer block sums S_b, which
+    is the engine's order for Q4_0 and Q8_0 products.  On the same
+    quantized activations the GPU (int8 kernel; for Q4_0 also the fp6
+    kernel) equals the oracle's restatement of that order bit for bit: two
+    independent implementations of it agree.  Shapes with enough tiles that
+    no K split applies, K a multiple of 128 or not."""
+    import s3e
+
+    rng = np.random.default_rng(M + N + K + wt)
+    W = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    wb = orc.to_weight_bytes(wt, W)
+    w = ctx.weight(wt, K, N, wb)
+    Xd = ctx.to_device(X)
+    ns = s3e.act_scale_elems(M, K)
+    q8, d8 = ctx.buffer(M * K), ctx.buffer(ns * 2)
+    ctx.quantize_rows(s3e.TYPE_Q8_0, Xd, M, K, q8, d8, None)
+    Y = ctx.buffer(M * N * 4)
+    ctx.mul_mat_q(w, q8, d8, None, M, Y)
+    ctx.sync()
+    got = Y.download(np.float32, (M, N))
+    codes = q8.download(np.int8, (M, K))
+    dbits = s3e.unstage_scales(d8.download(np.uint16, (ns,)), M, K)
+    xq = _ggml_q8_0_rows(codes, dbits)
+    ref = np.empty((M, N), np.float32)
+    orc.LIB.orc_set_variant(4)  # ORC_VARIANT_ARM_I8MM
+    try:
+        orc.LIB.orc_mul_mat_preq(wt, orc.ptr(wb), N, K, orc.ptr(xq), M, orc.ptr(ref), 0)
+    finally:
+        orc.LIB.orc_set_variant(0)
+    diff = np.count_nonzero(got != ref)
+    print(f"i8mm order wt={wt} M={M} N={N} K={K}: {diff} of {got.size} differ, rel_l2={orc.rel_l2(got, ref):.3e}")
+    assert diff == 0
+    if wt == orc.Q4_0 and K % 128 == 0:
+        f6, d6 = ctx.buffer((M + 63) // 64 * 64 * K * 3 // 2), ctx.buffer(ns * 2)
+        ctx.quantize_rows(s3e.TYPE_Q8_0_F6X2, Xd, M, K, f6, d6, None)
+        Y6 = ctx.buffer(M * N * 4)
+        ctx.mul_mat_q_f6(w, f6, d6, M, Y6)
+        ctx.sync()
+        assert np.array_equal(Y6.download(np.float32, (M, N)), ref)
+    w.free()

@@ -369,3 +369,94 @@ def test_single_window_equals_global(s3e_mod, tmp_path):
     a, b = orc.OracleModel(pw), orc.OracleModel(pg)
     x = np.random.default_rng(1).standard_normal((144, 1024)).astype(np.float32)
     assert np.array_equal(a.block(0, x), b.block(0, x))
+
+
+# ---- ggml's ARM NEON evaluation orders (orc_set_variant 2, 3, 4) ----------------
+ARM_VARIANTS = [2, 3, 4]  # M4 Pro build (tinyBLAS for Q4_0/Q8_0), vec_dot nrc = 1, vec_dot nrc = 2
+
+
+@pytest.mark.parametrize("v", ARM_VARIANTS)
+@pytest.mark.parametrize("t", [orc.Q4_0, orc.Q4_1, orc.Q8_0])
+def test_arm_orders_vs_f64(t, v):
+    """Each ARM order, with its own (NEON) activation quantizer, against the
+    float64 product of the same dequantized operands: K = 288 (nine blocks:
+    an odd last block takes the nrc = 1 path's scalar tail)."""
+    rng = np.random.default_rng(31 + t + v)
+    M, N, K = 21, 40, 288
+    W = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    wb = orc.to_weight_bytes(t, W)
+    vdt = orc.VEC_DOT[t]
+    L.orc_set_variant(v)
+    try:
+        Y = orc.mul_mat(t, wb, N, K, X)
+        xq = orc.from_float(vdt, X)
+    finally:
+        L.orc_set_variant(0)
+    ref = orc.dequantize(vdt, xq, M, K).astype(np.float64) @ orc.dequantize(t, wb, N, K).astype(np.float64).T
+    if t == orc.Q4_1:  # s = fp16(d·Σq) stands in for the exact block sum, as in every ggml order
+        qx, dx, sx = orc.split_q8(vdt, xq, M, K)
+        _, _, mw = _unpack(t, wb, N, K)
+        exact_s = dx.view(np.float16).astype(np.float64) * qx.reshape(M, K // 32, 32).sum(axis=2)
+        ref += (sx.view(np.float16).astype(np.float64) - exact_s) @ mw.T
+    assert orc.rel_l2(Y, ref) <= 2e-7
+
+
+@pytest.mark.parametrize("v", [0, 1] + ARM_VARIANTS)
+def test_orders_exact_on_integer_data(v):
+    """Q8_0 weights and activations whose scales are exactly 1 and whose
+    codes are small integers: every product and partial sum is an exact
+    integer in fp32, so every order must return the exact integer dot — a
+    lane partition that dropped or repeated a group of four, or a block
+    counted twice, would not."""
+    rng = np.random.default_rng(40 + v)
+    N, M, K = 7, 5, 320  # ten blocks
+    qw = rng.integers(-9, 10, (N, K)).astype(np.int8)
+    qx = rng.integers(-9, 10, (M, K)).astype(np.int8)
+    one = np.uint16(0x3C00)  # fp16 1.0
+    def blocks(q):
+        R = q.shape[0]
+        b = np.empty((R, K // 32, 34), np.uint8)
+        b[:, :, :2] = np.full((R, K // 32), one, np.uint16).view(np.uint8).reshape(R, K // 32, 2)
+        b[:, :, 2:] = q.reshape(R, K // 32, 32).view(np.uint8)
+        return b.reshape(R, -1)
+    wb, xb = blocks(qw), blocks(qx)
+    Y = np.empty((M, N), np.float32)
+    L.orc_set_variant(v)
+    try:
+        L.orc_mul_mat_preq(orc.Q8_0, orc.ptr(wb), N, K, orc.ptr(xb), M, orc.ptr(Y), 1)
+    finally:
+        L.orc_set_variant(0)
+    assert np.array_equal(Y, (qx.astype(np.int64) @ qw.astype(np.int64).T).astype(np.float32))
+
+
+def test_arm_quantizer_is_the_reference_quantizer_on_non_ties():
+    """ggml's NEON quantize_row_q8_0 takes id = 1/d like the generic
+    quantize_row_q8_0_ref (pinned by the golden fixtures) and differs from it
+    only in rounding exact .5 ties (half to even instead of away), which
+    random data does not hit; the x86 quantizer (id = 127/amax) lands on the
+    other side of some rounding boundaries."""
+    rng = np.random.default_rng(12)
+    X = (rng.standard_normal((400, 1024)) * rng.uniform(0.1, 5, (400, 1))).astype(np.float32)
+    ref = orc.quantize_ref(orc.Q8_0, X)
+    L.orc_set_variant(2)
+    try:
+        arm = orc.from_float(orc.Q8_0, X)
+    finally:
+        L.orc_set_variant(0)
+    assert np.array_equal(arm, ref)
+    # known answer: amax = 1.4442534 (0x3fb8dd4c), x = 0.017058112
+    # (0x3c8bbd74).  x86: id = fp32(127/amax) = 87.93471, x·id rounds to
+    # 1.5000001 → code 2; NEON: id = fp32(1/fp32(amax/127)) = 87.9347, x·id
+    # rounds to 1.4999999 → code 1 (the generic reference quantizer agrees)
+    blk = np.zeros((1, 32), np.float32)
+    blk[0, :2] = np.array([0x3FB8DD4C, 0x3C8BBD74], np.uint32).view(np.float32)
+    x86 = orc.from_float(orc.Q8_0, blk)
+    L.orc_set_variant(2)
+    try:
+        arm = orc.from_float(orc.Q8_0, blk)
+    finally:
+        L.orc_set_variant(0)
+    ref = orc.quantize_ref(orc.Q8_0, blk)
+    assert (x86[2:4].view(np.int8).tolist(), arm[2:4].view(np.int8).tolist()) == ([127, 2], [127, 1])
+    assert np.array_equal(arm, ref)
