@@ -186,6 +186,14 @@ __device__ __forceinline__ void quant_block32_f6(const float *v, uint64_t *base,
 #endif
 __device__ __forceinline__ int swz(int r) { return (r >> S3E_SWZ_SHIFT) & 7; }
 
+// 4 bytes per lane, likewise (scale planes).  A buffer load, unlike
+// global_load_lds, is not a flat-segment access, so the compiler keeps the
+// LDS read counter in order and can wait for operand reads one by one.
+__device__ __forceinline__ void dma4_buf(const void *base, int nrec, void *lds, int voff, int soff) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, nrec, 0x00020000);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, LDS_PTR(lds), 4, voff, soff, 0, 0);
+}
+
 // 16 bytes per lane from base + voff + soff (a raw buffer of nrec bytes) into
 // LDS at lds + 16·lane.  base, nrec and soff are wave-uniform, so the buffer
 // descriptor lives in scalar registers and the uniform part of the address
@@ -401,7 +409,14 @@ __device__ __forceinline__ void epilogue(const GemmParams &p, const float *Ct, i
             const int gm = m0 + row;
             const int gn0 = n0 + cc * 32;
             if (gm >= p.M || gn0 >= p.N) continue;
-            float v[32];
+            float v[32], bias[32];
+            // the bias of the 32 columns is loaded up front: its loads are in
+            // flight together instead of each behind the previous group's math
+#pragma unroll
+            for (int j = 0; j < 32; j += 4) {
+                const float4 bb = *(const float4 *)(e.bias + gn0 + j);
+                bias[j] = bb.x; bias[j + 1] = bb.y; bias[j + 2] = bb.z; bias[j + 3] = bb.w;
+            }
 #pragma unroll
             for (int j = 0; j < 32; j += 4) {
                 const float4 x = *(const float4 *)(Ct + row * CLD + cc * 32 + j);
@@ -409,39 +424,34 @@ __device__ __forceinline__ void epilogue(const GemmParams &p, const float *Ct, i
             }
             if (e.gelu_tab) {
                 // ggml_vec_gelu_f32 with GGML_GELU_FP16: x ≤ −10 → 0, x ≥ 10 → x,
-                // else the table entry at fp16(x)
+                // else the table entry at fp16(x).  All 32 table indices are
+                // formed before the first lookup, so the lookups are in flight
+                // together (the fp16 rounding's asm fence would otherwise hold
+                // each lookup behind the previous one's result).
+                uint16_t idx[32];
 #pragma unroll
-                for (int j = 0; j < 32; j += 4) {
-                    const float4 bb = *(const float4 *)(e.bias + gn0 + j);
-                    const float bj[4] = {bb.x, bb.y, bb.z, bb.w};
+                for (int j = 0; j < 32; j++) {
+                    v[j] = __fadd_rn(v[j], bias[j]);
+                    idx[j] = half_bits(v[j]);
+                }
+                uint16_t tv[32];
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const float x = __fadd_rn(v[j + i], bj[i]);
-                        const float t = (float)__builtin_bit_cast(_Float16, e.gelu_tab[half_bits(x)]);
-                        v[j + i] = x <= -10.f ? 0.f : (x >= 10.f ? x : t);
-                    }
+                for (int j = 0; j < 32; j++) tv[j] = e.gelu_tab[idx[j]];
+#pragma unroll
+                for (int j = 0; j < 32; j++) {
+                    const float x = v[j], t = (float)__builtin_bit_cast(_Float16, tv[j]);
+                    v[j] = x <= -10.f ? 0.f : (x >= 10.f ? x : t);
                 }
             } else if (e.relu) {
                 // ggml_relu: x > 0 ? x : 0
 #pragma unroll
-                for (int j = 0; j < 32; j += 4) {
-                    const float4 bb = *(const float4 *)(e.bias + gn0 + j);
-                    const float bj[4] = {bb.x, bb.y, bb.z, bb.w};
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const float x = __fadd_rn(v[j + i], bj[i]);
-                        v[j + i] = x > 0.f ? x : 0.f;
-                    }
+                for (int j = 0; j < 32; j++) {
+                    const float x = __fadd_rn(v[j], bias[j]);
+                    v[j] = x > 0.f ? x : 0.f;
                 }
             } else {
 #pragma unroll
-                for (int j = 0; j < 32; j += 4) {
-                    const float4 bb = *(const float4 *)(e.bias + gn0 + j);
-                    v[j] = gelu_erf(__fadd_rn(v[j], bb.x));
-                    v[j + 1] = gelu_erf(__fadd_rn(v[j + 1], bb.y));
-                    v[j + 2] = gelu_erf(__fadd_rn(v[j + 2], bb.z));
-                    v[j + 3] = gelu_erf(__fadd_rn(v[j + 3], bb.w));
-                }
+                for (int j = 0; j < 32; j++) v[j] = gelu_erf(__fadd_rn(v[j], bias[j]));
             }
             const Act &o = e.out;
             if (o.kind == A_F16) {
@@ -473,6 +483,39 @@ __device__ __forceinline__ void epilogue(const GemmParams &p, const float *Ct, i
         const int f = t & 31;
         const int gn = n0 + 4 * f;
         const bool vec = (p.N % 4) == 0 && gn + 3 < p.N;
+        constexpr int RPT = BM / (NT_ / 32);  // rows per thread
+        if constexpr (EPI == EPI_RESID) {
+            if (vec) {
+                // the bias, and every residual row of this thread, are loaded
+                // before the first store: y and bias may alias as far as the
+                // compiler knows, so a load placed after a store would wait
+                // for that store
+                const float4 bb = e.bias ? *(const float4 *)(e.bias + gn) : make_float4(0.f, 0.f, 0.f, 0.f);
+                const float bj[4] = {bb.x, bb.y, bb.z, bb.w};
+                float4 res[RPT];
+#pragma unroll
+                for (int k = 0; k < RPT; k++) {
+                    const int gm = m0 + (t >> 5) + k * (NT_ / 32);
+                    res[k] = gm < p.M ? *(const float4 *)(e.y + (int64_t)gm * e.ldy + gn)
+                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+#pragma unroll
+                for (int k = 0; k < RPT; k++) {
+                    const int row = (t >> 5) + k * (NT_ / 32), gm = m0 + row;
+                    if (gm >= p.M) continue;
+                    const float4 x = *(const float4 *)(Ct + row * CLD + 4 * f);
+                    float v[4] = {x.x, x.y, x.z, x.w};
+                    if (e.bias) {
+#pragma unroll
+                        for (int j = 0; j < 4; j++) v[j] = __fadd_rn(v[j], bj[j]);
+                    }
+                    *(float4 *)(e.y + (int64_t)gm * e.ldy + gn) =
+                        make_float4(__fadd_rn(res[k].x, v[0]), __fadd_rn(res[k].y, v[1]),
+                                    __fadd_rn(res[k].z, v[2]), __fadd_rn(res[k].w, v[3]));
+                }
+                return;
+            }
+        }
         for (int row = t >> 5; row < BM; row += NT_ / 32) {
             const int gm = m0 + row;
             if (gm >= p.M || gn >= p.N) continue;
@@ -859,24 +902,26 @@ __global__ __launch_bounds__(256, 3) void k_gemm_f6(GemmParams p) {
     const int lr = lane & 31, lh = lane >> 5;
 
     // DMA: wave w copies 1 KB runs 3w .. 3w+2 of the stage's A and of its B,
-    // and 256-byte scale runs w and w + 4 (A: runs 0-1, B: runs 2-5)
+    // and 256-byte scale runs w and w + 4 (A: runs 0-1, rows m0..; B: runs
+    // 2-5, columns n0..)
     const int a_tile = tm * p.nstages * 12288, b_tile = tn * p.nstages * 12288;
+    const int a_drec = p.nstages * (int)p.a_mp * 8, b_drec = p.nstages * (int)p.b_np * 8;
     int s_n = 0;
-    const uint8_t *s_src[2];
-    int64_t s_step[2];
-    int s_dst[2];
+    int s_voff[2], s_dst[2], s_step[2];
+    bool s_a[2];
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         const int k = wave + 4 * j;
         if (k >= 6) break;
         s_n++;
+        s_a[j] = k < 2;
         if (k < 2) {
-            s_src[j] = p.a_d + ((int64_t)m0 * 4) * 2 + k * 256 + lane * 4;
-            s_step[j] = p.a_mp * 8;
+            s_voff[j] = m0 * 8 + k * 256 + lane * 4;
+            s_step[j] = (int)p.a_mp * 8;
             s_dst[j] = OFF_AD + k * 256;
         } else {
-            s_src[j] = p.b_d + ((int64_t)n0 * 4) * 2 + (k - 2) * 256 + lane * 4;
-            s_step[j] = p.b_np * 8;
+            s_voff[j] = n0 * 8 + (k - 2) * 256 + lane * 4;
+            s_step[j] = (int)p.b_np * 8;
             s_dst[j] = OFF_BD + (k - 2) * 256;
         }
     }
@@ -890,9 +935,12 @@ __global__ __launch_bounds__(256, 3) void k_gemm_f6(GemmParams p) {
         }
 #pragma unroll
         for (int j = 0; j < 2; j++)
-            if (j < s_n)
-                __builtin_amdgcn_global_load_lds((const void *)(s_src[j] + s * s_step[j]), LDS_PTR(L + s_dst[j]), 4,
-                                                 0, 0);
+            if (j < s_n) {
+                // the stage offset is wave-uniform: keep it in a scalar register
+                const int so = __builtin_amdgcn_readfirstlane(s * s_step[j]);
+                if (s_a[j]) dma4_buf(p.a_d, a_drec, L + s_dst[j], s_voff[j], so);
+                else dma4_buf(p.b_d, b_drec, L + s_dst[j], s_voff[j], so);
+            }
     };
 
     // per-lane LDS operand offsets: A row wm·32 + lr, part lh; B column
@@ -1137,7 +1185,9 @@ hipError_t launch_gemm(const Weight &w, const Act &a, int64_t M, Epi epi, const 
         p.tiles_m = (int)((M + 63) / 64);
         p.ntiles = p.tiles_m * p.tiles_n;
         const int64_t arec = (int64_t)p.tiles_m * p.nstages * 12288, brec = (int64_t)p.tiles_n * p.nstages * 12288;
-        if (arec > INT32_MAX || brec > INT32_MAX) return hipErrorInvalidValue;
+        if (arec > INT32_MAX || brec > INT32_MAX || (int64_t)p.nstages * a.mp * 8 > INT32_MAX ||
+            (int64_t)p.nstages * w.Np * 8 > INT32_MAX)
+            return hipErrorInvalidValue;
         p.a_rec = (int)arec;
         p.b_rec = (int)brec;
         const int grid = ((p.ntiles * p.ksplit + 7) / 8) * 8;
