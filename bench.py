@@ -67,6 +67,9 @@ METRIC = "image-encoder ms/frame (SAM3 ViT 1008², q4_0/q8_0/f16) + % MFMA/HBM p
 PEAK_TOPS = {"q4_0": 5000.0, "q4_1": 5000.0, "q8_0": 5000.0, "f16": 2500.0, "f32": 157.3}
 CFG = dict(img_size=1008, patch=14, embed_dim=1024, depth=32, heads=16, mlp_ratio_x1000=4625, window=24,
            global_idx=(7, 15, 23, 31))
+# the measured_peaks entry the fc1 kernel's roofline is also read against
+MEASURED_PEAK = {"q4_0": "mfma_i8_32x32x32_TOPS", "q4_1": "mfma_i8_32x32x32_TOPS", "q8_0": "mfma_i8_32x32x32_TOPS",
+                 "f16": "mfma_f16_32x32x16_TOPS"}
 GEMM_KERNEL = {"q4_0": "k_gemm_f6", "q4_1": "k_gemm", "q8_0": "k_gemm", "f16": "k_gemm", "f32": "k_gemm"}
 SAM2_RUNS = [("hiera_t", "f16"), ("hiera_b+", "q8_0")]
 
@@ -153,7 +156,7 @@ BPW = {"q4_0": 18 / 32, "q4_1": 20 / 32, "q8_0": 34 / 32, "f16": 2.0}
 VIT_LINEARS = [(3072, 1024), (1024, 1024), (4736, 1024), (1024, 4736)]  # qkv, proj, fc1, fc2 (N, K)
 
 
-def small_m(s3e, ctx, ev, ftype: str, reps: int = 10) -> dict:
+def small_m(s3e, ctx, ev, ftype: str, reps: int = 10, hbm_read: float | None = None) -> dict:
     """Weight streaming at M = 64 rows: fc1 and fc2 alone (s3e_mul_mat_q), and
     the four ViT linears of enough distinct layers for ≈ 500 MB of weights in
     one batched launch (s3e_mul_mat_q_batch; 64 layers of Q4_0), twice the
@@ -218,6 +221,8 @@ def small_m(s3e, ctx, ev, ftype: str, reps: int = 10) -> dict:
     gbps = total / (us * 1e-6) / 1e9
     res["sweep"] = {"products": len(ws), "layers": layers, "bytes": int(total), "us": round(us, 1),
                     "GBps": round(gbps, 1), "frac_hbm": round(gbps / 8000.0, 4)}
+    if hbm_read:
+        res["sweep"]["frac_measured_read"] = round(gbps / hbm_read, 4)
     for w in ws:
         w.free()
     log(f"small-M {ftype}: fc1 {res['fc1_us']} us ({res['fc1_GBps']} GB/s), fc2 {res['fc2_us']} us "
@@ -402,6 +407,59 @@ def encode_ms(s3e, ctx, ev, ftype: str, steps: int, warmup: int, neck: int = 1) 
         pass
     log(f"encode {ftype} ({neck} neck{'s' if neck > 1 else ''}): {ms:.3f} ms/frame over {steps} steps")
     return ms
+
+
+MFMA_FORMS = [("i8_32x32x32", 0, 65536), ("f16_32x32x16", 1, 32768), ("fp6_scaled_32x32x64", 2, 131072),
+              ("f16_32x32x8", 3, 16384)]
+
+
+def measured_peaks(s3e, ctx, ev, reps: int = 5) -> dict:
+    """What this GPU reaches (s3e_probe_stream / s3e_probe_mfma): HBM read,
+    copy and write rates over buffers far larger than the 256 MB Infinity
+    Cache, and each MFMA form's issue rate with eight independent chains per
+    wave and no memory traffic."""
+    res = {}
+    e0, e1 = ev.create(), ev.create()
+    nbytes = 4 << 30
+    a, b = ctx.buffer(nbytes), ctx.buffer(nbytes // 2)
+    for name, mode, nb, moved in (("read", 0, nbytes, nbytes), ("write", 2, nbytes, nbytes),
+                                  ("copy", 1, nbytes // 2, nbytes)):
+        src, dst = (a, None) if mode == 0 else ((None, a) if mode == 2 else (a, b))
+        ctx.probe_stream(mode, dst, src, nb)
+        ctx.sync()
+        ev.record(e0, ctx.stream)
+        for _ in range(reps):
+            ctx.probe_stream(mode, dst, src, nb)
+        ev.record(e1, ctx.stream)
+        ms = ev.elapsed_ms(e0, e1) / reps
+        res[f"hbm_{name}_GBps"] = round(moved / ms / 1e6, 1)
+        log(f"HBM {name}: {moved / 2**30:.0f} GiB moved in {ms:.3f} ms = {moved / ms / 1e6:.1f} GB/s")
+    a.free()
+    b.free()
+    cus = ctx_cus()
+    for name, kind, ops in MFMA_FORMS:
+        wps, iters = 2, 4096
+        ctx.probe_mfma(kind, 64, wps)
+        ctx.sync()
+        ev.record(e0, ctx.stream)
+        ctx.probe_mfma(kind, iters, wps)
+        ev.record(e1, ctx.stream)
+        ms = ev.elapsed_ms(e0, e1)
+        n = cus * 4 * wps * iters * 8
+        tops = n * ops / (ms * 1e-3) / 1e12
+        res[f"mfma_{name}_TOPS"] = round(tops, 1)
+        log(f"MFMA {name}: {tops:.1f} T(FL)OP/s ({n} instructions in {ms:.3f} ms)")
+    ctx.sync()
+    return res
+
+
+def ctx_cus() -> int:
+    import ctypes
+
+    hip = ctypes.CDLL("libamdhip64.so")
+    v = ctypes.c_int()
+    hip.hipDeviceGetAttribute(ctypes.byref(v), 63, 0)  # hipDeviceAttributeMultiprocessorCount
+    return v.value
 
 
 ATTN_SHAPES = [("windowed", 9, 576), ("global", 1, 5184)]  # (name, windows B, tokens N); 16 heads, head dim 64
@@ -627,7 +685,7 @@ def main() -> int:
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "gemm_fc1_q4_0_counters.txt"))
     ap.add_argument("--only", choices=["encode", "gemm", "copy", "neck", "preprocess", "sam2", "small_m", "c4",
-                                       "attn"], default=None,
+                                       "attn", "peaks"], default=None,
                     help="run one leg only (for profiling runs)")
     ap.add_argument("--sam2-run", default=None, help="with --only sam2: one encoder, e.g. hiera_t:f16")
     args = ap.parse_args()
@@ -660,6 +718,10 @@ def main() -> int:
         attention_fp16(s3e, ctx, ev)
         return 0
 
+    if args.only == "peaks":
+        measured_peaks(s3e, ctx, ev)
+        return 0
+
     if args.only == "c4":
         for ft in ("q8_0", "f16"):
             encode_ms(s3e, ctx, ev, ft, args.steps, args.warmup)
@@ -676,6 +738,8 @@ def main() -> int:
         sam2_encoders(s3e, ctx, ev, args.steps, args.warmup, runs)
         return 0
 
+    if args.only is None:
+        out["peaks"] = measured_peaks(s3e, ctx, ev)
     if args.only in (None, "gemm"):
         ms, tops, ops = gemm_roofline(s3e, ctx, ev, args.ftype, args.gemm_reps)
         log(f"fc1 GEMM {args.ftype}: {ms * 1e3:.1f} us/launch, {tops:.1f} TOPS")
@@ -734,7 +798,8 @@ def main() -> int:
                         "detector and tracker SimpleFPN necks (sam3.cpp:6072-6075), image resident"}
     attn = attention_fp16(s3e, ctx, ev)
     sam2 = sam2_encoders(s3e, ctx, ev, max(3, args.steps // 2), 2)
-    sm = small_m(s3e, ctx, ev, args.ftype) if args.ftype in BPW else None
+    peaks = out["peaks"]
+    sm = small_m(s3e, ctx, ev, args.ftype, hbm_read=peaks["hbm_read_GBps"]) if args.ftype in BPW else None
 
     gms, gtops, gops = out["gemm"]
     peak = PEAK_TOPS[args.ftype]
@@ -788,7 +853,11 @@ def main() -> int:
         "roofline": {"kernel": f"{GEMM_KERNEL[args.ftype]} fc1 M=5184 N=4736 K=1024 ({args.ftype})", "bound": "mfma",
                      "achieved": round(gtops, 1), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(gtops / peak, 4), "traffic": traffic,
-                     "us_per_launch": round(gms * 1e3, 2), "ops_per_launch": gops},
+                     "us_per_launch": round(gms * 1e3, 2), "ops_per_launch": gops,
+                     "peak_measured": peaks.get(MEASURED_PEAK.get(args.ftype, ""), None),
+                     "frac_of_measured": (round(gtops / peaks[MEASURED_PEAK[args.ftype]], 4)
+                                          if args.ftype in MEASURED_PEAK else None)},
+        "measured_peaks": peaks,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -228,6 +228,21 @@ int s3e_flash_attn_ext_f16(s3e_ctx *ctx,
                            int64_t D, int64_t Nq, int64_t Nkv, int64_t nh, int64_t B,
                            float scale, float *o);
 
+/* ---- measurement ---------------------------------------------------------
+ * No counterpart in the reference: the rates this GPU reaches, against which
+ * the benchmark reads its roofline fractions next to the published peaks.
+ * s3e_probe_stream moves `bytes` (a multiple of 16) through HBM with 64-byte
+ * steps per thread and 8 work-groups of 4 waves per CU: mode 0 reads src,
+ * 1 copies src to dst, 2 writes dst.  s3e_probe_mfma runs, on every SIMD,
+ * waves_per_simd (1-4) waves of `iters` steps of eight independent MFMAs of
+ * one form with operands in registers: kind 0 v_mfma_i32_32x32x32_i8
+ * (65 536 ops each), 1 v_mfma_f32_32x32x16_f16 (32 768), 2 the scaled
+ * 32x32x64 f8f6f4 form on fp6 operands (131 072), 3 v_mfma_f32_32x32x8_f16
+ * (16 384).  Both are asynchronous; time them with events on the context's
+ * stream.  The first call allocates a small output array on the context. */
+int s3e_probe_stream(s3e_ctx *ctx, int mode, void *dst, const void *src, size_t bytes);
+int s3e_probe_mfma(s3e_ctx *ctx, int kind, int64_t iters, int waves_per_simd);
+
 /* ---- encoder -------------------------------------------------------------
  * Load the image encoder of a sam3.cpp model file (sam3.cpp:3200-3344):
  * for SAM 3 files (magic "sam3", version 3) the ViT backbone ("vit.") and

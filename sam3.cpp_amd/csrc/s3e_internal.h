@@ -306,6 +306,13 @@ hipError_t launch_attn_prep16(const _Float16 *q, const int64_t q_nb[4], const _F
                               const _Float16 *v, const int64_t v_nb[4], int64_t Nq, int64_t Nkv, int64_t nh,
                               int64_t B, int D, int hdp, _Float16 *q16, _Float16 *k16, _Float16 *vt16, int64_t ldv,
                               hipStream_t st);
+// Measurement kernels (k_probe.hip).  Stream: mode 0 read (sink: blocks·256
+// words), 1 copy, 2 write; bytes a multiple of 16.  MFMA: kind 0 i8
+// 32×32×32, 1 f16 32×32×16, 2 scaled fp6 32×32×64, 3 f16 32×32×8; iters
+// steps of eight MFMAs per wave; sink: blocks·4 words.
+hipError_t launch_probe_stream(int mode, void *dst, const void *src, size_t bytes, uint32_t *sink, int blocks,
+                               hipStream_t st);
+hipError_t launch_probe_mfma(int kind, int64_t iters, int blocks, uint32_t *sink, hipStream_t st);
 hipError_t launch_im2col(const float *chw, int img, int P, int64_t ldk, AKind kind, void *out,
                          hipStream_t st);
 hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t st);

@@ -29,6 +29,9 @@ struct s3e_ctx {
     // s3e_flash_attn_ext_f16's operand copies and key-split partials
     void *attn_ws = nullptr;
     size_t attn_ws_cap = 0;
+    // the measurement kernels' output words (made at first use)
+    uint32_t *probe_sink = nullptr;
+    int64_t probe_sink_cap = 0;
 };
 
 struct s3e_weight {

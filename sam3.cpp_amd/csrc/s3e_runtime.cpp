@@ -316,6 +316,7 @@ extern "C" void s3e_ctx_destroy(s3e_ctx *ctx) {
     if (ctx->sm_dev) (void)hipFree(ctx->sm_dev);
     if (ctx->sk_part) (void)hipFree(ctx->sk_part);
     if (ctx->attn_ws) (void)hipFree(ctx->attn_ws);
+    if (ctx->probe_sink) (void)hipFree(ctx->probe_sink);
     delete ctx;
 }
 
@@ -888,6 +889,58 @@ extern "C" int s3e_flash_attn_ext_f16(s3e_ctx *ctx, const uint16_t *q, const int
     if (e != hipSuccess) { set_error("s3e_flash_attn_ext_f16: %s", hipGetErrorString(e)); return S3E_ERR_HIP; }
     return S3E_OK;
 } S3E_CATCH("s3e_flash_attn_ext_f16")
+
+// ---- measurement ---------------------------------------------------------
+namespace {
+
+// The measurement kernels' sink (one word per thread or per wave), grown on
+// the first calls.
+hipError_t probe_setup(s3e_ctx *ctx, int64_t words) {
+    if (words <= ctx->probe_sink_cap) return hipSuccess;
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return e;
+    if (ctx->probe_sink) (void)hipFree(ctx->probe_sink);
+    ctx->probe_sink = nullptr;
+    ctx->probe_sink_cap = 0;
+    e = hipMalloc(&ctx->probe_sink, (size_t)words * 4);
+    if (e == hipSuccess) ctx->probe_sink_cap = words;
+    return e;
+}
+
+}  // namespace
+
+extern "C" int s3e_probe_stream(s3e_ctx *ctx, int mode, void *dst, const void *src, size_t bytes) try {
+    if (!ctx || (mode != 0 && !dst) || (mode != 2 && !src)) { set_error("s3e_probe_stream: NULL argument"); return S3E_ERR_INVALID; }
+    if (mode < 0 || mode > 2 || bytes == 0 || bytes % 16 != 0) {
+        set_error("s3e_probe_stream: mode %d / %zu bytes (modes 0-2, a multiple of 16 bytes)", mode, bytes);
+        return S3E_ERR_INVALID;
+    }
+    HIP_TRY(hipSetDevice(ctx->device));
+    int cus = 0;
+    HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ctx->device));
+    const int blocks = 8 * cus;  // 8 work-groups of 4 waves per CU
+    hipError_t e = probe_setup(ctx, (int64_t)blocks * 256);
+    if (e == hipSuccess) e = launch_probe_stream(mode, dst, src, bytes, ctx->probe_sink, blocks, ctx->stream);
+    if (e != hipSuccess) { set_error("s3e_probe_stream: %s", hipGetErrorString(e)); return S3E_ERR_HIP; }
+    return S3E_OK;
+} S3E_CATCH("s3e_probe_stream")
+
+extern "C" int s3e_probe_mfma(s3e_ctx *ctx, int kind, int64_t iters, int waves_per_simd) try {
+    if (!ctx) { set_error("s3e_probe_mfma: NULL context"); return S3E_ERR_INVALID; }
+    if (kind < 0 || kind > 3 || iters <= 0 || iters > (1 << 24) || waves_per_simd < 1 || waves_per_simd > 4) {
+        set_error("s3e_probe_mfma: kind %d (0-3), %lld steps, %d waves per SIMD (1-4)", kind, (long long)iters,
+                  waves_per_simd);
+        return S3E_ERR_INVALID;
+    }
+    HIP_TRY(hipSetDevice(ctx->device));
+    int cus = 0;
+    HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ctx->device));
+    const int blocks = cus * waves_per_simd;  // 4 waves (one per SIMD) per work-group
+    hipError_t e = probe_setup(ctx, (int64_t)blocks * 4);
+    if (e == hipSuccess) e = launch_probe_mfma(kind, iters, blocks, ctx->probe_sink, ctx->stream);
+    if (e != hipSuccess) { set_error("s3e_probe_mfma: %s", hipGetErrorString(e)); return S3E_ERR_HIP; }
+    return S3E_OK;
+} S3E_CATCH("s3e_probe_mfma")
 
 // ---- SAM 3 ViT model -------------------------------------------------------
 namespace {

@@ -96,6 +96,8 @@ def _load() -> ctypes.CDLL:
                                        c_int64, c_int64, c_int64, c_int64, c_int64, c_float, c_int, c_void_p]),
         "s3e_flash_attn_ext_f16": (c_int, [c_void_p, c_void_p, P64, c_void_p, P64, c_void_p, P64,
                                            c_int64, c_int64, c_int64, c_int64, c_int64, c_float, c_void_p]),
+        "s3e_probe_stream": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_size_t]),
+        "s3e_probe_mfma": (c_int, [c_void_p, c_int, c_int64, c_int]),
         "s3e_model_load": (c_int, [c_void_p, c_char_p, POINTER(c_void_p)]),
         "s3e_model_free": (None, [c_void_p]),
         "s3e_model_hparams": (c_int, [c_void_p, POINTER(c_int32)]),
@@ -136,7 +138,7 @@ DECLARED = [
     "s3e_last_error", "s3e_abi_version", "s3e_ctx_create", "s3e_ctx_destroy", "s3e_ctx_sync", "s3e_ctx_stream",
     "s3e_malloc", "s3e_free", "s3e_memcpy_h2d", "s3e_memcpy_d2h", "s3e_weight_upload", "s3e_weight_free",
     "s3e_weight_info", "s3e_mul_mat", "s3e_mul_mat_noalloc", "s3e_mul_mat_q", "s3e_mul_mat_q_f6", "s3e_mul_mat_q_batch", "s3e_quantize_rows", "s3e_layer_norm", "s3e_copy",
-    "s3e_flash_attn_ext", "s3e_flash_attn_ext_f16", "s3e_model_load",
+    "s3e_flash_attn_ext", "s3e_flash_attn_ext_f16", "s3e_probe_stream", "s3e_probe_mfma", "s3e_model_load",
     "s3e_model_free", "s3e_model_hparams", "s3e_state_create", "s3e_state_create_sized", "s3e_state_free", "s3e_encode_chw",
     "s3e_encode_chw_host", "s3e_encode_image_u8", "s3e_preprocess_image", "s3e_vit_prefix", "s3e_vit_block", "s3e_vit_block_stage", "s3e_vit_prefix_stage", "s3e_encode_vit_chw", "s3e_model_tensor_get", "s3e_run_neck", "s3e_hiera_block", "s3e_model_type", "s3e_mem_attn_dims", "s3e_mem_attn",
     "s3e_state_tensor_info",
@@ -364,6 +366,13 @@ class Context:
         a = lambda nb: (c_int64 * 4)(*[int(x) for x in nb])
         check(LIB.s3e_flash_attn_ext(self.handle, q.ptr, a(q_nb), k.ptr, a(k_nb), v.ptr, a(v_nb),
                                      D, Nq, Nkv, nh, B, c_float(scale), prec, o.ptr), "s3e_flash_attn_ext")
+
+    def probe_stream(self, mode: int, dst: DeviceBuffer | None, src: DeviceBuffer | None, nbytes: int):
+        check(LIB.s3e_probe_stream(self.handle, mode, dst.ptr if dst else None, src.ptr if src else None, nbytes),
+              "s3e_probe_stream")
+
+    def probe_mfma(self, kind: int, iters: int, waves_per_simd: int = 2):
+        check(LIB.s3e_probe_mfma(self.handle, kind, iters, waves_per_simd), "s3e_probe_mfma")
 
     def flash_attn_ext_f16(self, q: DeviceBuffer, q_nb, k: DeviceBuffer, k_nb, v: DeviceBuffer, v_nb,
                            D: int, Nq: int, Nkv: int, nh: int, B: int, scale: float, o: DeviceBuffer):
