@@ -274,3 +274,37 @@ def test_encode_at_state_image_size(variant, native, size, ft, tmpdir_session, c
     finally:
         st.free()
         gm.free()
+
+
+@pytest.mark.parametrize("variant,img,ft", [("hiera_s", 1024, "f16"), ("hiera_l", 512, "f16"), ("hiera_s", 512, "q8_0")])
+def test_encode_other_variants(variant, img, ft, tmpdir_session, ctx):
+    """SAM 2.1 Hiera-S (stages 1/2/11/2) and Hiera-L (width 144, 2 heads of
+    72 channels run zero-padded to 128, stages 2/6/36/4, windows 8/4/16/8)
+    — the converter's other two variants (convert_sam2_to_ggml.py:79-106) —
+    end to end against the oracle: F16 to the F16 specification, Q8_0
+    within the quantized bound against ggml's own order gap."""
+    import s3e
+
+    path = os.path.join(str(tmpdir_session), f"{variant}_{img}_{ft}.ggml")
+    _write(path, variant, img, ft)
+    om = orc.OracleHiera(path)
+    gm = s3e.Model(ctx, path)
+    st = s3e.State(ctx, gm)
+    try:
+        img_hwc = np.random.default_rng(8).integers(0, 256, (img, img, 3), dtype=np.uint8)
+        print(f"{variant}@{img} {ft}: encode", flush=True)
+        if ft == "f16":
+            chw = orc.preprocess_sam2(img_hwc, om.img)
+            levels, stages = om.encode(chw)
+            st.encode_image_u8(img_hwc)
+            for i, s in enumerate(stages):
+                rl, _ = _report(f"{variant}@{img} {ft}", f"hiera_stage_{i}", st.tensor(f"hiera_stage_{i}"), s)
+                assert rl <= 2e-3, i
+            for i, lv in enumerate(levels):
+                rl, _ = _report(f"{variant}@{img} {ft}", f"neck_trk_{i}", st.tensor(f"neck_trk_{i}"), lv)
+                assert rl <= 2e-3, i
+        else:
+            _encode_and_compare(f"{variant}@{img} {ft}", ft, om, st, img_hwc)
+    finally:
+        st.free()
+        gm.free()
