@@ -9,15 +9,21 @@ levels of a backend against the CPU path).
 Random-init weights N(0, 0.02) with random biases and LayerNorm affine,
 seed 0; a uniform random uint8 image, seed 0.
 
-* F16 end to end (vit_output and neck_trk_0..3): relative L2 ≤ 2e-3.
+* F16 end to end (vit_output and neck_trk_0..3): relative L2 ≤ 1e-3 (the
+  specification allows 2e-3); blocks 0 and 7 on the oracle's input ≤ 5e-4.
 * Q4_0 / Q8_0 block 0 (windowed) and block 7 (global), each fed the
-  oracle's own input: relative L2 ≤ 1e-3.  The max-abs distance is reported
-  next to ggml's own AVX2-vs-generic distance on the same block: ggml's two
-  evaluation orders are already 9e-3 apart in max-abs after one block at
-  this size, above the nominal 5e-3.
-* Q4_0 end to end: reported against that distance on the whole encoder
+  oracle's own input: relative L2 ≤ 1e-3, and max-abs within
+  max(5e-3, 1.5 × the largest distance between ggml's own CPU builds on
+  the same block).
+* Q4_0 / Q8_0 end to end: relative L2 and max-abs each within
+  max(bound, 1.5 × the largest distance between ggml's own CPU builds) —
+  x86 AVX2, generic C, and three ARM NEON forms including the Apple M4 Pro
+  build of the reference's published timings — on the same model and image
   (tests/golden/c4_order_gap.json, written by tests/golden/make_c4_gap.py:
-  ggml's generic order takes minutes on the whole encoder).
+  the builds' orders take about an hour together on the host).  Each
+  quantized linear re-quantizes its input per 32-block, so a last-bit
+  difference ahead of a rounding decision flips a code; ggml's builds
+  already disagree this way with one another.
 """
 import ctypes
 import json
@@ -33,12 +39,21 @@ pytestmark = pytest.mark.gpu
 orc.LIB.orc_set_variant.argtypes = [ctypes.c_int]
 GOLD = os.path.join(os.path.dirname(__file__), "golden", "c4_order_gap.json")
 IMG = 1008
+FLOOR = 1.5  # allowed multiple of the largest distance between ggml's own builds
 
 
-def c4_model(path, ft):
+def _gap(ft, name):
+    """Largest distance between two of ggml's CPU builds for this output."""
+    with open(GOLD) as f:
+        return json.load(f)[ft][name]["max_pair"]
+
+
+def c4_model(path, ft, neck=1):
+    """neck=1: the visual-only file (tracker neck); neck=2: the full SAM 3
+    file of the same seed (detector and tracker necks, same backbone)."""
     import s3e
 
-    s3e.synth_write(path, img_size=IMG, ftype=ft, seed=0, random_affine=True)
+    s3e.synth_write(path, img_size=IMG, ftype=ft, seed=0, random_affine=True, neck=neck)
 
 
 def c4_image():
@@ -89,17 +104,17 @@ def test_c4_block(c4, ctx, bi):
     ref = om.block(bi, x0)
     gap = None
     if ft != "f16":
-        orc.LIB.orc_set_variant(1)
-        try:
-            alt = om.block(bi, x0)
-        finally:
-            orc.LIB.orc_set_variant(0)
-        gap = (orc.rel_l2(alt, ref), orc.max_abs(alt, ref))
+        g = _gap(ft, f"block_{bi}")
+        gap = (g["rel_l2"], g["max_abs"])
     xd = ctx.to_device(x0)
     st.block(bi, xd)
     ctx.sync()
     rl, ma = _report(f"C4 {ft} block {bi}", xd.download(np.float32, x0.shape), ref, gap)
-    assert rl <= (2e-3 if ft == "f16" else 1e-3)
+    if ft == "f16":
+        assert rl <= 5e-4
+    else:
+        assert rl <= 1e-3
+        assert ma <= max(5e-3, FLOOR * gap[1])
 
 
 def test_c4_neck_on_oracle_input(c4, ctx):
@@ -127,36 +142,93 @@ def test_c4_neck_on_oracle_input(c4, ctx):
     xd.free()
 
 
+_BACKBONE = {}  # weight type -> the oracle's vit_output (shared with the full file's test)
+
+
 def test_c4_encode(c4, ctx):
-    """F16: the specification end to end.  Quantized: Q4_0 only (the oracle's
-    whole encoder takes about a minute per weight type on the host), against
-    the committed order gap of the same model and image."""
+    """The whole encoder from the uint8 image: vit_output and the tracker
+    neck's four levels, against the oracle (ggml's x86 order)."""
     ft, om, gm, st, img, chw, x0 = c4
-    if ft == "q8_0":
-        pytest.skip("end to end runs for F16 and Q4_0; Q8_0 is covered block by block")
     print(f"C4 {ft} encode: oracle", flush=True)
     ref = om.encode(chw)
+    _BACKBONE[ft] = ref
     st.encode_image_u8(img)
-    got = st.tensor("vit_output")
-    gap = None
-    if ft == "q4_0":
-        g = json.load(open(GOLD))["q4_0"]
-        gap = (g["vit_output"]["rel_l2"], g["vit_output"]["max_abs"])
-    rl, ma = _report(f"C4 {ft} vit_output", got, ref, gap)
-    if ft == "f16":
-        assert rl <= 2e-3
-    else:
-        assert rl <= max(1e-3, 1.5 * gap[0])
     levels = om.neck(ref, "trk")
-    for i, lv in enumerate(levels):
-        g = st.tensor(f"neck_trk_{i}")
-        assert g.shape == lv.shape
-        lgap = None
-        if ft == "q4_0":
-            e = json.load(open(GOLD))["q4_0"][f"neck_trk_{i}"]
-            lgap = (e["rel_l2"], e["max_abs"])
-        rl, ma = _report(f"C4 {ft} neck_trk_{i}", g, lv, lgap)
+    outs = [("vit_output", st.tensor("vit_output"), ref)]
+    outs += [(f"neck_trk_{i}", st.tensor(f"neck_trk_{i}"), lv) for i, lv in enumerate(levels)]
+    for name, got, want in outs:
+        assert got.shape == want.shape, name
+        gap = None
+        if ft != "f16":
+            g = _gap(ft, name)
+            gap = (g["rel_l2"], g["max_abs"])
+        rl, ma = _report(f"C4 {ft} {name}", got, want, gap)
         if ft == "f16":
-            assert rl <= 2e-3
+            assert rl <= 1e-3, name
         else:
-            assert rl <= max(1e-3, 1.5 * lgap[0])
+            assert rl <= max(1e-3, FLOOR * gap[0]), name
+            assert ma <= max(5e-3, FLOOR * gap[1]), name
+
+
+# ---- the full SAM 3 file: detector and tracker necks ------------------------
+@pytest.fixture(scope="module")
+def c4_full(tmpdir_session, ctx):
+    import s3e
+
+    path = os.path.join(str(tmpdir_session), "c4_q4_0_full.ggml")
+    print("C4 full q4_0: writing the model", flush=True)
+    c4_model(path, "q4_0", neck=2)
+    om = orc.OracleModel(path)
+    gm = s3e.Model(ctx, path)
+    st = s3e.State(ctx, gm)
+    yield om, gm, st
+    st.free()
+    gm.free()
+    os.remove(path)
+
+
+def test_c4_full_necks_on_oracle_input(c4_full, ctx):
+    """Both SimpleFPN necks of a full SAM 3 file (sam3.cpp:6072-6075) at the
+    real size on a given backbone output, against the oracle's necks on the
+    same input: 8 levels, F32 convolutions on split fp16 pairs."""
+    om, gm, st = c4_full
+    G, E = IMG // 14, 1024
+    x = np.random.default_rng(6).standard_normal((G * G, E)).astype(np.float32)
+    print("C4 full q4_0 necks on the oracle's input", flush=True)
+    xd = ctx.to_device(x)
+    st.run_neck(xd)
+    ctx.sync()
+    for which in ("det", "trk"):
+        ref = om.neck(x, which)
+        for lvl in range(4):
+            got = st.tensor(f"neck_{which}_{lvl}")
+            assert got.shape == ref[lvl].shape, (which, lvl)
+            rl, ma = _report(f"C4 full neck_{which}_{lvl} (oracle input)", got, ref[lvl])
+            assert rl <= 1e-4, (which, lvl)
+            assert ma <= 5e-3, (which, lvl)
+    xd.free()
+
+
+def test_c4_full_encode(c4_full, ctx):
+    """The full file end to end from the uint8 image: vit_output and the
+    eight neck levels against the oracle, each within max(bound, 1.5 × the
+    largest distance between ggml's own CPU builds)."""
+    om, gm, st = c4_full
+    img = c4_image()
+    ref = _BACKBONE.get("q4_0")
+    if ref is None:
+        print("C4 full q4_0 encode: oracle", flush=True)
+        ref = om.encode(orc.preprocess_sam3(img, IMG))
+    st.encode_image_u8(img)
+    outs = [("vit_output", st.tensor("vit_output"), ref, _gap("q4_0", "vit_output"))]
+    with open(GOLD) as f:
+        full_gap = json.load(f)["q4_0_full"]
+    for which in ("det", "trk"):
+        for i, lv in enumerate(om.neck(ref, which)):
+            name = f"neck_{which}_{i}"
+            outs.append((name, st.tensor(name), lv, full_gap[name]["max_pair"]))
+    for name, got, want, g in outs:
+        assert got.shape == want.shape, name
+        rl, ma = _report(f"C4 full q4_0 {name}", got, want, (g["rel_l2"], g["max_abs"]))
+        assert rl <= max(1e-3, FLOOR * g["rel_l2"]), name
+        assert ma <= max(5e-3, FLOOR * g["max_abs"]), name

@@ -21,9 +21,11 @@ with the specification as the lower bound (F32: relative L2 ≤ 2e-4;
 quantized: relative L2 ≤ 1e-3 and max-abs ≤ 5e-3).
 
 The noise floor is what the reference itself moves by when nothing but fp32
-evaluation order changes.  End to end it is the distance between ggml's two
-dot-product evaluation orders (AVX2 and generic C, both restated in the
-oracle) on the same model and image.  Per block it is the larger of that and
+evaluation order changes.  End to end it is the distance between ggml's
+AVX2 and generic-C dot-product orders (both restated in the oracle) on the
+same model and image; for the tracking frame's encoder (Hiera-B+ Q8_0 at
+1024 px) it is the largest distance between any two of ggml's CPU builds,
+the three ARM NEON forms included (tests/golden/hiera_order_gap.json).  Per block it is the larger of that and
 the block's largest response to four seeded 2e-7 relative (one- to
 two-ulp) perturbations of its input: every GEMM input is re-quantized to Q8 per 32-block and every
 hidden unit goes through ggml's fp16 GELU table, so a last-bit difference
@@ -187,19 +189,37 @@ def test_block_in_place_and_rejections(hiera, ctx):
         st.hiera_block(om.nblocks, big, 2, 2, xd)
 
 
-def _encode_and_compare(tag, ft, om, st, img_hwc):
+GAP_FILE = os.path.join(os.path.dirname(__file__), "golden", "hiera_order_gap.json")
+
+
+def _pair_gap(key, name, gap):
+    """The live AVX2-vs-generic gap, widened to the largest distance between
+    any two of ggml's CPU builds where tests/golden/hiera_order_gap.json
+    (tests/golden/make_hiera_gap.py) has the case."""
+    import json
+
+    if key is None or not os.path.exists(GAP_FILE):
+        return gap
+    with open(GAP_FILE) as f:
+        e = json.load(f).get(key, {}).get(name)
+    if not e:
+        return gap
+    return (max(gap[0], e["max_pair"]["rel_l2"]), max(gap[1], e["max_pair"]["max_abs"]))
+
+
+def _encode_and_compare(tag, ft, om, st, img_hwc, key=None):
     chw = orc.preprocess_sam2(img_hwc, om.img)
     (levels, stages), (alt_levels, alt_stages) = _variant_gap(lambda: om.encode(chw))
     st.encode_image_u8(img_hwc)
     for i, s in enumerate(stages):
         got = st.tensor(f"hiera_stage_{i}")
-        gap = (orc.rel_l2(alt_stages[i], s), orc.max_abs(alt_stages[i], s))
+        gap = _pair_gap(key, f"hiera_stage_{i}", (orc.rel_l2(alt_stages[i], s), orc.max_abs(alt_stages[i], s)))
         rl, ma = _report(tag, f"hiera_stage_{i}", got, s, gap)
         _check(ft, rl, ma, gap, f"stage {i}")
     for i, lv in enumerate(levels):
         got = st.tensor(f"neck_trk_{i}")
         assert got.shape == lv.shape
-        gap = (orc.rel_l2(alt_levels[i], lv), orc.max_abs(alt_levels[i], lv))
+        gap = _pair_gap(key, f"neck_trk_{i}", (orc.rel_l2(alt_levels[i], lv), orc.max_abs(alt_levels[i], lv)))
         rl, ma = _report(tag, f"neck_trk_{i}", got, lv, gap)
         _check(ft, rl, ma, gap, f"level {i}")
         pe = st.tensor(f"neck_trk_pe_{i}")
@@ -242,7 +262,7 @@ def test_encode_full_size(variant, ft, tmpdir_session, ctx):
     try:
         img = np.random.default_rng(6).integers(0, 256, (1024, 1024, 3), dtype=np.uint8)
         print(f"{variant}@1024 {ft}: encode", flush=True)
-        _encode_and_compare(f"{variant}@1024 {ft}", ft, om, st, img)
+        _encode_and_compare(f"{variant}@1024 {ft}", ft, om, st, img, key=f"{variant}@1024:{ft}")
     finally:
         st.free()
         gm.free()
