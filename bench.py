@@ -471,9 +471,8 @@ def attention_fp16(s3e, ctx, ev, reps: int = 20) -> dict:
     windows of 576 tokens and over the 5184-token global grid, through
     s3e_flash_attn_ext_f16 with fp16 Q, K, V resident in ggml's contiguous
     [B][heads][N][64] layout.  Calls run back to back on the stream; each is
-    one V transpose pass (V into the engine's key-slot layout; Q and K are
-    read in place) and the attention kernel, with no allocation or
-    synchronisation.  FLOPs 4·B·heads·N²·64 (QKᵀ and PV), against the
+    the attention kernel alone (Q, K and V read where they lie), with no
+    allocation or synchronisation.  FLOPs 4·B·heads·N²·64 (QKᵀ and PV), against the
     2.5 PFLOP/s dense fp16 peak."""
     res = {}
     rng = np.random.default_rng(7)
@@ -498,8 +497,8 @@ def attention_fp16(s3e, ctx, ev, reps: int = 20) -> dict:
         tf = flops / (us * 1e-6) / 1e12
         res[name] = {"windows": B, "tokens": N, "heads": nh, "us": round(us, 1), "TFLOPs": round(tf, 1),
                      "frac_fp16_peak": round(tf / 2500.0, 4),
-                     "scope": "s3e_flash_attn_ext_f16 calls back to back, fp16 operands resident: V transpose "
-                              "pass + attention kernel"}
+                     "scope": "s3e_flash_attn_ext_f16 calls back to back, fp16 operands resident and read in "
+                              "place: the attention kernel alone"}
         log(f"attention fp16 {name} {B}x{nh}x{N}: {us:.1f} us, {tf:.1f} TFLOP/s")
         for b in (q, k, v, o):
             b.free()

@@ -214,9 +214,9 @@ int s3e_flash_attn_ext(s3e_ctx *ctx,
  * isolated attention microbench feeds fp16 operands): the same addressing,
  * shapes and output as s3e_flash_attn_ext, q/k/v as IEEE fp16 bits, computed
  * at S3E_PREC_DEFAULT (fp16 operands and probabilities, fp32 accumulation).
- * Q and K are read in place when they are contiguous [B][nh][N][D] with D =
- * 64 or 128 (else copied); V is transposed into the engine's layout by one
- * pass.  Asynchronous on the context's stream: O is complete after
+ * Q, K and V are read in place when they are contiguous [B][nh][N][D] with
+ * D = 64 or 128 (else copied to that layout, zero-padded to 64 / 128; at
+ * D = 256 V is transposed into the engine's layout by one pass).  Asynchronous on the context's stream: O is complete after
  * s3e_ctx_sync.  The copies live in a context-owned workspace that a call
  * grows (synchronising the stream, then hipMalloc) only when it needs more
  * room than every earlier call on the context; calls that fit allocate

@@ -15,6 +15,10 @@
 // registers straight into the B operand (fp16) with no data movement, and the
 // keys of each K=16 MFMA step are the ones that lane already holds; thanks to
 // the vt_slot order the matching Vᵀ A-operand is one 16-byte LDS read.
+// The VN variant (fp16 operands, head dims 64 / 128) reads V as ggml holds
+// it, [BH][Nkv][hd]: its tiles are laid out like K tiles, and each Vᵀ
+// A-operand is two LDS transpose loads (ds_read_b64_tr_b16), which hand every
+// lane one channel of four keys.
 //
 // K and Vᵀ tiles of 32 keys stream through a 2-deep LDS ring filled by
 // buffer_load_dwordx4 ... lds (rows of 128 bytes, 16-byte chunks
@@ -91,6 +95,32 @@ __device__ __forceinline__ int swzk256(int r) { return r & 15; }
 template <int HD>
 __device__ __forceinline__ int swzk_hd(int r) { return HD == 64 ? swzk(r) : swzk256(r); }
 __device__ __forceinline__ int swzv(int r) { return (r >> 2) & 3; }
+// Natural V tiles (VN): a transpose load reads 64 bytes of each of four
+// consecutive rows per lane half, so those rows must land in distinct bank
+// groups, and the DMA and the rows' 16-byte chunks stay a bijection.  HD 64
+// (128-byte rows, r and r + 2 share banks): the three bits of (r >> 1)
+// reversed, which puts rows 4i and 4i + 2 in different 64-byte halves of the
+// bank space; HD 128 (256-byte rows): the two low row bits pick the 64-byte
+// group.
+template <int HD>
+__device__ __forceinline__ int swzvn(int r) {
+    if constexpr (HD == 64) {
+        const int x = (r >> 1) & 7;
+        return ((x & 1) << 2) | (x & 2) | (x >> 2);
+    } else {
+        return ((r & 3) << 2) | ((r >> 2) & 3);
+    }
+}
+
+typedef __fp16 v4fp16 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives element
+// i % 4 of the 8 bytes addressed by lanes 4j + i / 4, j = 0..3
+__device__ __forceinline__ v4h lds_tr16(const uint8_t *p) {
+    const v4fp16 r = __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) v4fp16 *)(p));
+    return __builtin_bit_cast(v4h, r);
+}
 
 // p − h for the fp16 value h in the low or high half of h2, exact, in one
 // v_fma_mix_f32 (h2·(−1) + p with h2 read as fp16)
@@ -107,8 +137,9 @@ __device__ __forceinline__ float sub_hi_half(float p, uint32_t h2) {
 
 // CROP: the windowed, cropped output mapping and narrower real heads
 // (a.wo, a.hd_out; the Hiera layouts), kept out of the plain variants.
-template <bool SPLIT, int HD, bool CROP>
+template <bool SPLIT, int HD, bool CROP, bool VN = false>
 __global__ __launch_bounds__(NTHR, HD == 64 ? 3 : (HD == 128 ? 2 : 1)) void k_attn(AttnArgs a, int ldv) {
+    static_assert(!VN || (!SPLIT && HD <= 128), "natural V: fp16 operands, head dim 64 or 128");
     using G = AG<HD>;
     constexpr int NP = SPLIT ? 2 : 1;  // planes: hi (and lo)
     constexpr int KPL = G::KPL, VPL = G::VPL;
@@ -177,6 +208,14 @@ __global__ __launch_bounds__(NTHR, HD == 64 ? 3 : (HD == 128 ? 2 : 1)) void k_at
         const int r = RPR * (wave * G::KRUNS + j) + lane / CPR;
         k_lane[j] = r * G::ROWK + (((lane % CPR) ^ swzk_hd<HD>(r)) << 4);
     }
+    int vn_lane[G::KRUNS];  // VN: V tiles as K tiles, own swizzle
+#pragma unroll
+    for (int j = 0; j < G::KRUNS; j++) {
+        constexpr int RPR = 1024 / G::ROWK;
+        constexpr int CPR = G::ROWK / 16;
+        const int r = RPR * (wave * G::KRUNS + j) + lane / CPR;
+        vn_lane[j] = r * G::ROWK + (((lane % CPR) ^ swzvn<HD>(r)) << 4);
+    }
     int v_row[G::VRUNS], v_ch[G::VRUNS];
 #pragma unroll
     for (int j = 0; j < G::VRUNS; j++) {
@@ -199,6 +238,14 @@ __global__ __launch_bounds__(NTHR, HD == 64 ? 3 : (HD == 128 ? 2 : 1)) void k_at
     auto issue_v = [&](int tt) {
         uint8_t *L = Vring + (tt & 1) * VBUF;
         const int tile = t0 + tt;
+        if constexpr (VN) {
+            // rows past the keys read as zeros (their probabilities are 0)
+            const uint32_t nk = (uint32_t)min(a.Nkv - tile * KT, KT) * G::ROWK;
+            const _Float16 *base = a.v + koff + (int64_t)tile * KT * HD;
+#pragma unroll
+            for (int j = 0; j < G::KRUNS; j++) dma(base, nk, L + (wave * G::KRUNS + j) * 1024, vn_lane[j]);
+            return;
+        }
         const uint32_t nrec = (uint32_t)(HD * ldv - tile * KT) * 2;
         int off[G::VRUNS];
 #pragma unroll
@@ -235,8 +282,29 @@ __global__ __launch_bounds__(NTHR, HD == 64 ? 3 : (HD == 128 ? 2 : 1)) void k_at
         return acc;
     };
     // Oᵀ += Vᵀ·Pᵀ for the 32 keys of tile tt
+    // VN: lane L = 16g + 4j + q (g = 2·lh + gc) addresses key row
+    // 16·jj + 4·lh + j (+ 8 for the second load) at channels dt·32 + 16·gc +
+    // 4q .. + 3, so each lane receives channel dt·32 + L % 32 of keys
+    // 16·jj + 4·lh + 0..3 and + 8..11: the keys its K slots hold
+    const int tr_j = (lane & 15) >> 2, tr_q = lane & 3, tr_gc = (lane >> 4) & 1;
+    auto tr_off = [&](int dt, int jj, int half) {
+        const int row = 16 * jj + 8 * half + 4 * lh + tr_j;
+        const int chunk = 4 * dt + 2 * tr_gc + (tr_q >> 1);
+        return row * G::ROWK + ((chunk ^ swzvn<HD>(row)) << 4) + 8 * (tr_q & 1);
+    };
     auto pv = [&](int tt, const v8h (&ph)[2], const v8h (&pl)[2]) {
         const uint8_t *L = Vring + (tt & 1) * VBUF;
+        if constexpr (VN) {
+#pragma unroll
+            for (int dt = 0; dt < G::DT; dt++)
+#pragma unroll
+                for (int jj = 0; jj < 2; jj++) {
+                    const v4h v0 = lds_tr16(L + tr_off(dt, jj, 0)), v1 = lds_tr16(L + tr_off(dt, jj, 1));
+                    const v8h vh = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+                    o[dt] = mfma(vh, ph[jj], o[dt]);
+                }
+            return;
+        }
 #pragma unroll
         for (int dt = 0; dt < G::DT; dt++)
 #pragma unroll
@@ -586,7 +654,13 @@ hipError_t launch_attn(const AttnArgs &a, hipStream_t st) {
         return hipErrorInvalidValue;
     const dim3 grid((unsigned)((a.Nq + QT - 1) / QT), (unsigned)a.BH, (unsigned)a.nsplit);
     const bool crop = a.wo > 0 || (a.hd_out > 0 && a.hd_out != hd);
-    if (hd == 256) {
+    if (a.v) {
+        // natural V: fp16 operands, head dim 64 or 128
+        if (a.q_lo || a.k_lo || hd == 256) return hipErrorInvalidValue;
+        if (hd == 64 && !crop) hipLaunchKernelGGL((k_attn<false, 64, false, true>), grid, dim3(NTHR), 0, st, a, ldv);
+        else if (hd == 64) hipLaunchKernelGGL((k_attn<false, 64, true, true>), grid, dim3(NTHR), 0, st, a, ldv);
+        else hipLaunchKernelGGL((k_attn<false, 128, true, true>), grid, dim3(NTHR), 0, st, a, ldv);
+    } else if (hd == 256) {
         hipLaunchKernelGGL((k_attn<false, 256, false>), grid, dim3(NTHR), 0, st, a, ldv);
     } else if (hd == 64 && !crop) {
         if (a.q_lo) hipLaunchKernelGGL((k_attn<true, 64, false>), grid, dim3(NTHR), 0, st, a, ldv);

@@ -592,9 +592,9 @@ hipError_t launch_attn_prep(const float *q, const int64_t q_nb[4], const float *
 
 hipError_t launch_attn_prep16(const _Float16 *q, const int64_t q_nb[4], const _Float16 *k, const int64_t k_nb[4],
                               const _Float16 *v, const int64_t v_nb[4], int64_t Nq, int64_t Nkv, int64_t nh,
-                              int64_t B, int D, int hdp, _Float16 *q16, _Float16 *k16, _Float16 *vt16, int64_t ldv,
-                              hipStream_t st) {
-    if (D <= 0 || D > hdp || hdp > 256 || ldv % 16 != 0 || ldv < Nkv) return hipErrorInvalidValue;
+                              int64_t B, int D, int hdp, _Float16 *q16, _Float16 *k16, _Float16 *v16,
+                              _Float16 *vt16, int64_t ldv, hipStream_t st) {
+    if (D <= 0 || D > hdp || hdp > 256 || (vt16 && (ldv % 16 != 0 || ldv < Nkv))) return hipErrorInvalidValue;
     if (q16) {
         const int64_t t = B * nh * Nq * hdp;
         hipLaunchKernelGGL(k_attn_prep16, dim3((unsigned)((t + 255) / 256)), dim3(256), 0, st, q, q_nb[1], q_nb[2],
@@ -605,6 +605,12 @@ hipError_t launch_attn_prep16(const _Float16 *q, const int64_t q_nb[4], const _F
         hipLaunchKernelGGL(k_attn_prep16, dim3((unsigned)((t + 255) / 256)), dim3(256), 0, st, k, k_nb[1], k_nb[2],
                            k_nb[3], Nkv, nh, B, D, hdp, k16);
     }
+    if (v16) {
+        const int64_t t = B * nh * Nkv * hdp;
+        hipLaunchKernelGGL(k_attn_prep16, dim3((unsigned)((t + 255) / 256)), dim3(256), 0, st, v, v_nb[1], v_nb[2],
+                           v_nb[3], Nkv, nh, B, D, hdp, v16);
+    }
+    if (!vt16) return hipGetLastError();
     const int64_t total = B * nh * (ldv / 8) * (hdp / 8);
     const bool vec = ((uintptr_t)v % 16 == 0) && v_nb[1] % 8 == 0 && v_nb[2] % 8 == 0 && v_nb[3] % 8 == 0;
     const dim3 grid((unsigned)((total + 255) / 256));

@@ -212,6 +212,10 @@ struct AttnArgs {
     const _Float16 *q = nullptr;   // [BH][Nq][hd]
     const _Float16 *k = nullptr;   // [BH][Nkv][hd]
     const _Float16 *vt = nullptr;  // [BH][hd][vt_ld_for(Nkv)], keys in vt_slot order
+    // V as ggml holds it, fp16 [BH][Nkv][hd] (hd 64 or 128, no lo planes):
+    // when set the kernel reads V where it lies (LDS transpose loads) and vt
+    // is not used
+    const _Float16 *v = nullptr;
     // low halves (x = hi + lo) for split-precision attention, else null
     const _Float16 *q_lo = nullptr, *k_lo = nullptr, *vt_lo = nullptr;
     int Nq = 0, Nkv = 0, NH = 0, BH = 0;
@@ -299,13 +303,14 @@ hipError_t launch_attn_prep(const float *q, const int64_t q_nb[4], const float *
                             int64_t Nq, int64_t Nkv, int64_t nh, int64_t B, int D, int hdp, _Float16 *q16,
                             _Float16 *k16, _Float16 *vt16, _Float16 *q_lo, _Float16 *k_lo,
                             _Float16 *vt_lo, int64_t ldv, hipStream_t st);
-// fp16 operands of s3e_flash_attn_ext_f16: Q and K (when q16 / k16 are
-// given) copied to [BH][N][hdp], V transposed to Vᵀ [BH][hdp][ldv] in
-// vt_slot order with zeros past Nkv (every slot of every row is written).
+// fp16 operands of s3e_flash_attn_ext_f16: Q, K and V (when q16 / k16 /
+// v16 are given) copied to [BH][N][hdp] with zeros for d ≥ D; when vt16 is
+// given V is transposed to Vᵀ [BH][hdp][ldv] in vt_slot order with zeros past
+// Nkv (every slot of every row is written).
 hipError_t launch_attn_prep16(const _Float16 *q, const int64_t q_nb[4], const _Float16 *k, const int64_t k_nb[4],
                               const _Float16 *v, const int64_t v_nb[4], int64_t Nq, int64_t Nkv, int64_t nh,
-                              int64_t B, int D, int hdp, _Float16 *q16, _Float16 *k16, _Float16 *vt16, int64_t ldv,
-                              hipStream_t st);
+                              int64_t B, int D, int hdp, _Float16 *q16, _Float16 *k16, _Float16 *v16,
+                              _Float16 *vt16, int64_t ldv, hipStream_t st);
 // Measurement kernels (k_probe.hip).  Stream: mode 0 read (sink: blocks·256
 // words), 1 copy, 2 write; bytes a multiple of 16.  MFMA: kind 0 i8
 // 32×32×32, 1 f16 32×32×16, 2 scaled fp6 32×32×64, 3 f16 32×32×8; iters

@@ -836,6 +836,9 @@ extern "C" int s3e_flash_attn_ext_f16(s3e_ctx *ctx, const uint16_t *q, const int
         return D == hdp && nb[1] == hdp && nb[2] == N * hdp && nb[3] == nh * N * hdp;
     };
     const bool q_in = plain(q_nb, Nq), k_in = plain(k_nb, Nkv);
+    // V: read where it lies as well (head dims up to 128), else copied to the
+    // plain layout; head dim 256 goes through the Vᵀ layout
+    const bool vnat = hdp <= 128, v_in = vnat && plain(v_nb, Nkv);
     int nsplit = 1;
     const int64_t target = hdp == 256 ? 256 : 512;
     if (D == hdp && qtiles * BH < target) {
@@ -843,9 +846,9 @@ extern "C" int s3e_flash_attn_ext_f16(s3e_ctx *ctx, const uint16_t *q, const int
         const int64_t per = (ktiles + ns - 1) / ns;
         nsplit = (int)((ktiles + per - 1) / per);
     }
-    // workspace: [Vᵀ][Q copy][K copy][partials], 256-byte aligned pieces
+    // workspace: [V copy or Vᵀ][Q copy][K copy][partials], 256-byte aligned pieces
     auto al = [](size_t b) { return (b + 255) / 256 * 256; };
-    const size_t vb = al((size_t)(BH * hdp * ldv) * 2), qb = q_in ? 0 : al((size_t)(BH * Nq * hdp) * 2),
+    const size_t vb = vnat ? (v_in ? 0 : al((size_t)(BH * Nkv * hdp) * 2)) : al((size_t)(BH * hdp * ldv) * 2), qb = q_in ? 0 : al((size_t)(BH * Nq * hdp) * 2),
                  kb = k_in ? 0 : al((size_t)(BH * Nkv * hdp) * 2);
     const size_t po = (size_t)nsplit * BH * Nq * hdp, pml = (size_t)nsplit * BH * Nq * 2;
     const size_t pb = nsplit > 1 ? (po + pml) * 4 : 0;
@@ -859,16 +862,20 @@ extern "C" int s3e_flash_attn_ext_f16(s3e_ctx *ctx, const uint16_t *q, const int
         ctx->attn_ws_cap = need;
     }
     uint8_t *ws = (uint8_t *)ctx->attn_ws;
-    _Float16 *vt16 = (_Float16 *)ws;
+    _Float16 *vt16 = vnat ? nullptr : (_Float16 *)ws;
+    _Float16 *v16 = (vnat && !v_in) ? (_Float16 *)ws : nullptr;
     _Float16 *q16 = q_in ? nullptr : (_Float16 *)(ws + vb);
     _Float16 *k16 = k_in ? nullptr : (_Float16 *)(ws + vb + qb);
-    hipError_t e = launch_attn_prep16((const _Float16 *)q, q_nb, (const _Float16 *)k, k_nb, (const _Float16 *)v, v_nb,
-                                      Nq, Nkv, nh, B, (int)D, hdp, q16, k16, vt16, ldv, ctx->stream);
+    hipError_t e = hipSuccess;
+    if (!q_in || !k_in || !v_in)
+        e = launch_attn_prep16((const _Float16 *)q, q_nb, (const _Float16 *)k, k_nb, (const _Float16 *)v, v_nb, Nq,
+                               Nkv, nh, B, (int)D, hdp, q16, k16, v16, vt16, ldv, ctx->stream);
     if (e == hipSuccess) {
         AttnArgs a;
         a.q = q_in ? (const _Float16 *)q : q16;
         a.k = k_in ? (const _Float16 *)k : k16;
-        a.vt = vt16;
+        if (vnat) a.v = v_in ? (const _Float16 *)v : v16;
+        else a.vt = vt16;
         a.Nq = (int)Nq;
         a.Nkv = (int)Nkv;
         a.NH = (int)nh;
