@@ -1524,11 +1524,6 @@ hipError_t alloc_neck(s3e_state *st) {
         if (a_cap[i]) e = hipMalloc(&st->lv_a[i], (size_t)a_cap[i] * 2 * 2);
         if (e == hipSuccess) e = hipMalloc(&st->lv_b[i], (size_t)st->lv_b_cap[i] * 2 * 2);
     }
-    for (int i = 0; i < 2 && e == hipSuccess; i++) {
-        e = hipStreamCreateWithFlags(&st->aux[i], hipStreamNonBlocking);
-        if (e == hipSuccess) e = hipEventCreateWithFlags(&st->ev_join[i], hipEventDisableTiming);
-    }
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&st->ev_fork, hipEventDisableTiming);
     if (e == hipSuccess) e = hipMalloc(&st->zero, 256);
     if (e == hipSuccess) e = hipMemsetAsync(st->zero, 0, 256, st->ctx->stream);
     for (int which = 0; which < 2 && e == hipSuccess; which++) {
@@ -1596,6 +1591,13 @@ extern "C" int s3e_state_create_sized(s3e_ctx *ctx, const s3e_model *m, int img_
     }
     st->vt_elems = vt_elems;
     if (e == hipSuccess) e = hipMalloc(&st->vt16, (size_t)(vt_elems * 2 * 2));
+    // two side streams (default priority) and their events: the windowed
+    // blocks' row bands and the neck levels run on them
+    for (int i = 0; i < 2 && e == hipSuccess; i++) {
+        e = hipStreamCreateWithFlags(&st->aux[i], hipStreamNonBlocking);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&st->ev_join[i], hipEventDisableTiming);
+    }
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&st->ev_fork, hipEventDisableTiming);
     if (e == hipSuccess) e = alloc_neck(st);
     if (e != hipSuccess) {
         s3e_state_free(st);
@@ -1627,80 +1629,211 @@ hipError_t run_prefix(s3e_state *st, const float *chw, float *x) {
     return launch_layernorm(x, st->T, m->E, 1e-5f, m->ln_pre_w, m->ln_pre_b, none, x, s);
 }
 
-// sam3_vit_block_forward (sam3.cpp:3710-3801) as 7 launches.
-hipError_t run_block(s3e_state *st, int bi, float *x) {
+// Rows [r0, ...) of an activation as an activation of their own (r0 a
+// multiple of 64): codes and values by row (A_F6 by 64-row tile), the scale
+// planes by row inside each stage (their stage pitch mp stays the buffer's).
+Act act_rows(const Act &a, int64_t r0) {
+    Act o = a;
+    switch (a.kind) {
+        case A_F6: o.x = (uint8_t *)a.x + (r0 / 64) * (a.ld / 128) * 12288; break;
+        case A_Q8_0: case A_Q8_1: o.x = (int8_t *)a.x + r0 * a.ld; break;
+        case A_F16: o.x = (_Float16 *)a.x + r0 * a.ld; break;
+        case A_F16X2:
+            o.x = (_Float16 *)a.x + r0 * a.ld;
+            o.lo = (_Float16 *)a.lo + r0 * a.ld;
+            break;
+        default: o.x = (float *)a.x + r0 * a.ld; break;
+    }
+    if (a.d) o.d = a.d + r0 * 4;
+    if (a.s) o.s = a.s + r0 * 4;
+    return o;
+}
+
+// Phases of a block: A = LN1 + QKV, B = attention, C = proj + LN2 + fc1 + fc2.
+enum : int { PH_A = 1, PH_B = 2, PH_C = 4, PH_ALL = 7 };
+
+// sam3_vit_block_forward (sam3.cpp:3710-3801) as 7 launches on stream s, for
+// the token rows [r0, r0 + rows) (r0 and rows multiples of 64).  Phases A and
+// C work token by token, and a windowed block's attention stays inside its
+// windows, so a band of whole window rows is a block of its own: its
+// activations, Q/K/Vᵀ windows and residual rows are disjoint parts of the
+// state's buffers.  A global block's attention (phase B) needs every row;
+// its phases A and C take any band, with the band's rows at their positions
+// in the one window.
+hipError_t run_block_rows(s3e_state *st, int bi, float *x, int64_t r0, int64_t rows, hipStream_t s,
+                          int phases = PH_ALL) {
     const s3e_model *m = st->m;
     const Block &b = m->blocks[(size_t)bi];
-    hipStream_t s = st->ctx->stream;
-    const int64_t T = st->T, E = m->E;
+    const int64_t T = rows, E = m->E;
     const int WS = b.global ? m->grid : m->window;
-    const int Nw = WS * WS, NW = (m->grid / WS) * (m->grid / WS);
-    // LN1 → activation for the QKV weight
-    const Act a_qkv = st->a1.as(act_kind_gemm(b.qkv), E);
-    hipError_t e = launch_layernorm(x, T, E, 1e-5f, b.n1w, b.n1b, a_qkv, nullptr, s);
-    if (e != hipSuccess) return e;
-    // QKV GEMM + bias + RoPE → fp16 Q, K, Vᵀ in window layout
-    EpiArgs eq;
-    eq.bias = b.qkv_b;
-    eq.grid = m->grid;
-    eq.window = WS;
-    eq.E = (int)E;
-    eq.HD = 64;
-    eq.NH = m->heads;
-    eq.freqs = b.freqs;
-    eq.q = st->q16;
-    eq.k = st->k16;
-    eq.vt = st->vt16;
+    const int Nw = WS * WS;
+    if (b.global && (phases & PH_B) && (r0 != 0 || rows != st->T)) return hipErrorInvalidValue;
+    // the band's Q/K/Vᵀ: windowed blocks from its first window on (windows
+    // row-major over the grid); the global block's one window from position
+    // r0 on (r0 a multiple of 16 keeps Vᵀ's slot groups whole)
+    int64_t qoff, voff, foff = 0, NW;
+    if (b.global) {
+        qoff = r0 * 64;
+        voff = r0;
+        foff = r0 * 64;
+        NW = 1;
+    } else {
+        const int64_t w0 = r0 / ((int64_t)WS * m->grid) * (m->grid / WS);
+        qoff = w0 * m->heads * Nw * 64;
+        voff = w0 * m->heads * 64 * vt_ld_for(Nw);
+        NW = rows / ((int64_t)WS * m->grid) * (m->grid / WS);
+    }
+    float *xb = x + r0 * E;
     // Quantized (and F32) projections re-quantize the attention output: run
     // attention split so it matches f32 attention; F16 models use plain fp16.
     const bool split = b.proj.kind != WK_F16;
-    if (split) {
-        eq.q_lo = st->q16 + T * E;
-        eq.k_lo = st->k16 + T * E;
-        eq.vt_lo = st->vt16 + st->vt_elems;
+    _Float16 *q = st->q16 + qoff, *k = st->k16 + qoff, *vt = st->vt16 + voff;
+    _Float16 *q_lo = split ? st->q16 + st->T * E + qoff : nullptr, *k_lo = split ? st->k16 + st->T * E + qoff : nullptr;
+    _Float16 *vt_lo = split ? st->vt16 + st->vt_elems + voff : nullptr;
+    const Act a_proj = act_rows(st->a1.as(act_kind_gemm(b.proj), E), r0);
+    hipError_t e = hipSuccess;
+    if (phases & PH_A) {
+        // LN1 → activation for the QKV weight
+        const Act a_qkv = act_rows(st->a1.as(act_kind_gemm(b.qkv), E), r0);
+        e = launch_layernorm(xb, T, E, 1e-5f, b.n1w, b.n1b, a_qkv, nullptr, s);
+        if (e != hipSuccess) return e;
+        // QKV GEMM + bias + RoPE → fp16 Q, K, Vᵀ in window layout
+        EpiArgs eq;
+        eq.bias = b.qkv_b;
+        eq.grid = m->grid;
+        eq.window = WS;
+        eq.E = (int)E;
+        eq.HD = 64;
+        eq.NH = m->heads;
+        eq.freqs = b.freqs ? b.freqs + foff : nullptr;
+        eq.q = q;
+        eq.k = k;
+        eq.vt = vt;
+        eq.q_lo = q_lo;
+        eq.k_lo = k_lo;
+        eq.vt_lo = vt_lo;
+        eq.vt_ld = (int)vt_ld_for(Nw);
+        e = launch_gemm(b.qkv, a_qkv, T, EPI_QKV, eq, s);
+        if (e != hipSuccess) return e;
     }
-    eq.vt_ld = (int)vt_ld_for(Nw);
-    e = launch_gemm(b.qkv, a_qkv, T, EPI_QKV, eq, s);
-    if (e != hipSuccess) return e;
-    // attention → activation for the proj weight, un-partitioned
-    AttnArgs aa;
-    aa.q = st->q16;
-    aa.k = st->k16;
-    aa.vt = st->vt16;
-    aa.q_lo = eq.q_lo;
-    aa.k_lo = eq.k_lo;
-    aa.vt_lo = eq.vt_lo;
-    aa.Nq = Nw;
-    aa.Nkv = Nw;
-    aa.NH = m->heads;
-    aa.BH = NW * m->heads;
-    aa.scale = 1.0f / std::sqrt(64.0f);
-    aa.grid = m->grid;
-    aa.window = WS;
-    aa.out = st->a1.as(act_kind_gemm(b.proj), E);
-    e = launch_attn(aa, s);
-    if (e != hipSuccess) return e;
-    // proj + bias + residual
-    EpiArgs ep;
-    ep.bias = b.proj_b;
-    ep.y = x;
-    ep.ldy = E;
-    e = launch_gemm(b.proj, aa.out, T, EPI_RESID, ep, s);
-    if (e != hipSuccess) return e;
-    // LN2 → fc1 + bias + GELU(erf) → activation for fc2 → fc2 + bias + residual
-    const Act a_fc1 = st->a1.as(act_kind_gemm(b.fc1), E);
-    e = launch_layernorm(x, T, E, 1e-5f, b.n2w, b.n2b, a_fc1, nullptr, s);
-    if (e != hipSuccess) return e;
-    EpiArgs e1;
-    e1.bias = b.fc1_b;
-    e1.out = st->a2.as(act_kind_gemm(b.fc2), m->mlp);
-    e = launch_gemm(b.fc1, a_fc1, T, EPI_GELU, e1, s);
-    if (e != hipSuccess) return e;
-    EpiArgs e2;
-    e2.bias = b.fc2_b;
-    e2.y = x;
-    e2.ldy = E;
-    return launch_gemm(b.fc2, e1.out, T, EPI_RESID, e2, s);
+    if (phases & PH_B) {
+        // attention → activation for the proj weight, un-partitioned
+        AttnArgs aa;
+        aa.q = q;
+        aa.k = k;
+        aa.vt = vt;
+        aa.q_lo = q_lo;
+        aa.k_lo = k_lo;
+        aa.vt_lo = vt_lo;
+        aa.Nq = Nw;
+        aa.Nkv = Nw;
+        aa.NH = m->heads;
+        aa.BH = (int)NW * m->heads;
+        aa.scale = 1.0f / std::sqrt(64.0f);
+        aa.grid = m->grid;
+        aa.window = WS;
+        aa.out = a_proj;
+        e = launch_attn(aa, s);
+        if (e != hipSuccess) return e;
+    }
+    if (phases & PH_C) {
+        // proj + bias + residual
+        EpiArgs ep;
+        ep.bias = b.proj_b;
+        ep.y = xb;
+        ep.ldy = E;
+        e = launch_gemm(b.proj, a_proj, T, EPI_RESID, ep, s);
+        if (e != hipSuccess) return e;
+        // LN2 → fc1 + bias + GELU(erf) → activation for fc2 → fc2 + bias + residual
+        const Act a_fc1 = act_rows(st->a1.as(act_kind_gemm(b.fc1), E), r0);
+        e = launch_layernorm(xb, T, E, 1e-5f, b.n2w, b.n2b, a_fc1, nullptr, s);
+        if (e != hipSuccess) return e;
+        EpiArgs e1;
+        e1.bias = b.fc1_b;
+        e1.out = act_rows(st->a2.as(act_kind_gemm(b.fc2), m->mlp), r0);
+        e = launch_gemm(b.fc1, a_fc1, T, EPI_GELU, e1, s);
+        if (e != hipSuccess) return e;
+        EpiArgs e2;
+        e2.bias = b.fc2_b;
+        e2.y = xb;
+        e2.ldy = E;
+        e = launch_gemm(b.fc2, e1.out, T, EPI_RESID, e2, s);
+    }
+    return e;
+}
+
+hipError_t run_block(s3e_state *st, int bi, float *x) {
+    return run_block_rows(st, bi, x, 0, st->T, st->ctx->stream);
+}
+
+// Bands of window rows: up to three, each on its own stream (the context's
+// and the state's two side streams).  Each stream runs its band through the
+// blocks while the others do the same, joined only around the global blocks'
+// attention, so one band's single-round kernel tails, epilogue bursts and
+// short LayerNorm passes overlap the other bands' main loops.  1 when the grid
+// has fewer than two window rows or a window row is not a multiple of 64
+// tokens.
+int vit_bands(const s3e_state *st) {
+    const s3e_model *m = st->m;
+    const int nwr = m->grid / m->window;
+    if (nwr < 2 || ((int64_t)m->window * m->grid) % 64 != 0 || !st->aux[0] || !st->aux[1]) return 1;
+    return std::min(nwr, 3);
+}
+
+// The side streams wait for the context stream's work so far.
+hipError_t fork_bands(s3e_state *st, int nb) {
+    hipError_t e = hipEventRecord(st->ev_fork, st->ctx->stream);
+    for (int k = 0; k < nb - 1 && e == hipSuccess; k++) e = hipStreamWaitEvent(st->aux[k], st->ev_fork, 0);
+    return e;
+}
+
+// The context stream waits for the side streams' work so far (recorded also
+// after an error, so that the context stream never runs ahead of work already
+// queued on the side streams).
+hipError_t join_bands(s3e_state *st, int nb, hipError_t e) {
+    for (int k = 0; k < nb - 1; k++) {
+        const hipError_t r = hipEventRecord(st->ev_join[k], st->aux[k]);
+        const hipError_t w = r == hipSuccess ? hipStreamWaitEvent(st->ctx->stream, st->ev_join[k], 0) : r;
+        if (e == hipSuccess) e = w;
+    }
+    return e;
+}
+
+// The backbone's blocks on x, in vit_bands() bands.
+hipError_t run_blocks(s3e_state *st, float *x) {
+    const s3e_model *m = st->m;
+    const int nb = vit_bands(st);
+    if (nb == 1) {
+        for (int i = 0; i < m->depth; i++) {
+            const hipError_t e = run_block(st, i, x);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
+    const int nwr = m->grid / m->window;
+    const int64_t wrow = (int64_t)m->window * m->grid;
+    auto bands = [&](int bi, int phases) {
+        hipError_t e = hipSuccess;
+        for (int band = 0; band < nb && e == hipSuccess; band++) {
+            const int64_t wr0 = (int64_t)nwr * band / nb, wr1 = (int64_t)nwr * (band + 1) / nb;
+            e = run_block_rows(st, bi, x, wr0 * wrow, (wr1 - wr0) * wrow, band == 0 ? st->ctx->stream : st->aux[band - 1],
+                               phases);
+        }
+        return e;
+    };
+    hipError_t e = fork_bands(st, nb);
+    for (int i = 0; i < m->depth && e == hipSuccess; i++) {
+        if (!m->blocks[(size_t)i].global) {
+            e = bands(i, PH_ALL);
+            continue;
+        }
+        e = bands(i, PH_A);
+        e = join_bands(st, nb, e);
+        if (e == hipSuccess) e = run_block_rows(st, i, x, 0, st->T, st->ctx->stream, PH_B);
+        if (e == hipSuccess) e = fork_bands(st, nb);
+        if (e == hipSuccess) e = bands(i, PH_C);
+    }
+    return join_bands(st, nb, e);
 }
 
 Act plane_act(AKind kind, _Float16 *base, int64_t cap, int64_t ld) {
@@ -2132,7 +2265,7 @@ extern "C" int s3e_encode_vit_chw(s3e_state *st, const float *chw_device) try {
     if (st->m->hiera) { set_error("s3e_encode_vit_chw: the model is a SAM 2 (Hiera) encoder"); return S3E_ERR_INVALID; }
     HIP_TRY(hipSetDevice(st->ctx->device));
     HIP_TRY(run_prefix(st, chw_device, st->x));
-    for (int i = 0; i < st->m->depth; i++) HIP_TRY(run_block(st, i, st->x));
+    HIP_TRY(run_blocks(st, st->x));
     return S3E_OK;
 } S3E_CATCH("s3e_encode_vit_chw")
 
@@ -2195,7 +2328,7 @@ extern "C" int s3e_encode_chw(s3e_state *st, const float *chw_device) try {
         return S3E_OK;
     }
     HIP_TRY(run_prefix(st, chw_device, st->x));
-    for (int i = 0; i < st->m->depth; i++) HIP_TRY(run_block(st, i, st->x));
+    HIP_TRY(run_blocks(st, st->x));
     HIP_TRY(run_necks(st, st->x));
     return S3E_OK;
 } S3E_CATCH("s3e_encode_chw")

@@ -116,3 +116,26 @@ def test_encode_image(small, ctx):
     else:
         assert rl <= max(1e-3, FLOOR_FACTOR * frl)
         assert ma <= max(5e-3, FLOOR_FACTOR * fma)
+
+
+def test_banded_encode_equals_block_chain(small, ctx):
+    """The encoder runs each run of windowed blocks as bands of window rows
+    on three streams (24×24 tokens, window 8: three bands of 192 rows).
+    Every element is computed as in the one-stream chain of s3e_vit_prefix +
+    s3e_vit_block, so vit_output must equal that chain bit for bit, for each
+    activation format (fp6 split, Q8_0, Q8_1, fp16)."""
+    ft, om, gm, st, img, chw = small
+    chw_d = ctx.to_device(chw)
+    st.encode_chw(chw_d)
+    banded = st.tensor("vit_output")
+    xd = ctx.buffer(banded.nbytes)
+    st.prefix(chw_d, xd)
+    for i in range(om.depth):
+        st.block(i, xd)
+    ctx.sync()
+    chain = xd.download(np.float32, banded.shape)
+    ndiff = int(np.count_nonzero(banded != chain))
+    print(f"{ft} banded vs chain: {ndiff} differing elements")
+    assert ndiff == 0
+    for b in (chw_d, xd):
+        b.free()
