@@ -156,7 +156,7 @@ __global__ __launch_bounds__(NTHR, HD == 64 ? 3 : (HD == 128 ? 2 : 1)) void k_at
 
     v8h qf[NP][G::DS];
     {
-        const int64_t off = ((int64_t)bh * a.Nq + (qvalid ? qi : 0)) * HD;
+        const int64_t off = (int64_t)bh * (a.q_hs > 0 ? a.q_hs : (int64_t)a.Nq * HD) + (int64_t)(qvalid ? qi : 0) * HD;
 #pragma unroll
         for (int pl = 0; pl < NP; pl++) {
             const _Float16 *qrow = (pl == 0 ? a.q : a.q_lo) + off;
@@ -636,6 +636,7 @@ hipError_t launch_attn(const AttnArgs &a, hipStream_t st) {
         return hipErrorInvalidValue;
     const int ntiles = (a.Nkv + 31) / 32;
     if (a.nsplit < 1 || a.nsplit > ntiles) return hipErrorInvalidValue;
+    if (a.q_hs != 0 && a.q_hs < (int64_t)a.Nq * hd) return hipErrorInvalidValue;
     if (a.nsplit > 1) {
         // every range must hold a tile; plain layouts (narrower heads allowed),
         // f32 or fp16 output

@@ -219,6 +219,9 @@ struct AttnArgs {
     // low halves (x = hi + lo) for split-precision attention, else null
     const _Float16 *q_lo = nullptr, *k_lo = nullptr, *vt_lo = nullptr;
     int Nq = 0, Nkv = 0, NH = 0, BH = 0;
+    // elements between the Q rows of consecutive (batch, head) pairs (0:
+    // Nq·hd): a band of queries of a longer sequence reads its rows in place
+    int64_t q_hs = 0;
     int hd = 64;                   // head dim of the q/k/vt rows: 64, or 128 (narrower heads zero-padded)
     int hd_out = 0;                // real head dim (0: = hd); output columns h·hd_out + d for d < hd_out
     float scale = 0.f;

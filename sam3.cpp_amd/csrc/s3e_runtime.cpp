@@ -1659,7 +1659,8 @@ enum : int { PH_A = 1, PH_B = 2, PH_C = 4, PH_ALL = 7 };
 // activations, Q/K/Vᵀ windows and residual rows are disjoint parts of the
 // state's buffers.  A global block's attention (phase B) needs every row;
 // its phases A and C take any band, with the band's rows at their positions
-// in the one window.
+// in the one window; its attention takes a band of queries too, against
+// all keys, once every band's phase A is done.
 hipError_t run_block_rows(s3e_state *st, int bi, float *x, int64_t r0, int64_t rows, hipStream_t s,
                           int phases = PH_ALL) {
     const s3e_model *m = st->m;
@@ -1667,7 +1668,6 @@ hipError_t run_block_rows(s3e_state *st, int bi, float *x, int64_t r0, int64_t r
     const int64_t T = rows, E = m->E;
     const int WS = b.global ? m->grid : m->window;
     const int Nw = WS * WS;
-    if (b.global && (phases & PH_B) && (r0 != 0 || rows != st->T)) return hipErrorInvalidValue;
     // the band's Q/K/Vᵀ: windowed blocks from its first window on (windows
     // row-major over the grid); the global block's one window from position
     // r0 on (r0 a multiple of 16 keeps Vᵀ's slot groups whole)
@@ -1720,13 +1720,23 @@ hipError_t run_block_rows(s3e_state *st, int bi, float *x, int64_t r0, int64_t r
         // attention → activation for the proj weight, un-partitioned
         AttnArgs aa;
         aa.q = q;
-        aa.k = k;
-        aa.vt = vt;
         aa.q_lo = q_lo;
-        aa.k_lo = k_lo;
-        aa.vt_lo = vt_lo;
-        aa.Nq = Nw;
+        aa.Nq = (int)(b.global ? rows : Nw);
         aa.Nkv = Nw;
+        if (b.global) {
+            // the band's queries (rows of the one window, heads Nw rows apart)
+            // against every key
+            aa.q_hs = (int64_t)Nw * 64;
+            aa.k = st->k16;
+            aa.vt = st->vt16;
+            aa.k_lo = split ? st->k16 + st->T * E : nullptr;
+            aa.vt_lo = split ? st->vt16 + st->vt_elems : nullptr;
+        } else {
+            aa.k = k;
+            aa.vt = vt;
+            aa.k_lo = k_lo;
+            aa.vt_lo = vt_lo;
+        }
         aa.NH = m->heads;
         aa.BH = (int)NW * m->heads;
         aa.scale = 1.0f / std::sqrt(64.0f);
@@ -1821,17 +1831,22 @@ hipError_t run_blocks(s3e_state *st, float *x) {
         }
         return e;
     };
+    hipStream_t bs[3] = {st->ctx->stream, st->aux[0], st->aux[1]};
+    hipEvent_t done_a[3] = {st->ev_fork, st->ev_join[0], st->ev_join[1]};
     hipError_t e = fork_bands(st, nb);
     for (int i = 0; i < m->depth && e == hipSuccess; i++) {
         if (!m->blocks[(size_t)i].global) {
             e = bands(i, PH_ALL);
             continue;
         }
+        // a global block: every band's QKV, then each band waits for the
+        // others' and runs the attention of its own queries and its phase C
         e = bands(i, PH_A);
-        e = join_bands(st, nb, e);
-        if (e == hipSuccess) e = run_block_rows(st, i, x, 0, st->T, st->ctx->stream, PH_B);
-        if (e == hipSuccess) e = fork_bands(st, nb);
-        if (e == hipSuccess) e = bands(i, PH_C);
+        for (int band = 0; band < nb && e == hipSuccess; band++) e = hipEventRecord(done_a[band], bs[band]);
+        for (int band = 0; band < nb && e == hipSuccess; band++)
+            for (int o = 0; o < nb && e == hipSuccess; o++)
+                if (o != band) e = hipStreamWaitEvent(bs[band], done_a[o], 0);
+        if (e == hipSuccess) e = bands(i, PH_B | PH_C);
     }
     return join_bands(st, nb, e);
 }
