@@ -1437,6 +1437,12 @@ struct s3e_state {
     ActBuf a1, a2, col;       // E-wide, MLP-wide and im2col activations
     _Float16 *q16 = nullptr, *k16 = nullptr, *vt16 = nullptr;  // [hi plane | lo plane]
     int64_t vt_elems = 0;
+    // Q, K, Vᵀ (hi + lo planes) of the global blocks when the blocks run in
+    // bands: two sets used in turn, apart from the windowed blocks' q16 / k16 /
+    // vt16, because a band that moves on to the next block writes its rows of
+    // that block's layout while the other bands may still read theirs
+    _Float16 *gq16[2] = {nullptr, nullptr}, *gk16[2] = {nullptr, nullptr}, *gvt16[2] = {nullptr, nullptr};
+    int64_t gvt_elems = 0;
     // necks: level sides, outputs (f32 [side²][D]) per neck, the shared PEs,
     // and fp16 work planes, each [hi | lo] of cap halves
     int64_t side[4] = {0, 0, 0, 0};
@@ -1474,6 +1480,11 @@ extern "C" void s3e_state_free(s3e_state *st) {
     if (st->q16) (void)hipFree(st->q16);
     if (st->k16) (void)hipFree(st->k16);
     if (st->vt16) (void)hipFree(st->vt16);
+    for (int i = 0; i < 2; i++) {
+        if (st->gq16[i]) (void)hipFree(st->gq16[i]);
+        if (st->gk16[i]) (void)hipFree(st->gk16[i]);
+        if (st->gvt16[i]) (void)hipFree(st->gvt16[i]);
+    }
     for (auto &lv : st->neck_out)
         for (float *p : lv)
             if (p) (void)hipFree(p);
@@ -1541,6 +1552,10 @@ hipError_t alloc_neck(s3e_state *st) {
 
 }  // namespace
 
+namespace {
+int vit_bands(const s3e_state *st);
+}  // namespace
+
 extern "C" int s3e_state_create(s3e_ctx *ctx, const s3e_model *m, s3e_state **out) {
     return s3e_state_create_sized(ctx, m, 0, out);
 }
@@ -1598,6 +1613,16 @@ extern "C" int s3e_state_create_sized(s3e_ctx *ctx, const s3e_model *m, int img_
         if (e == hipSuccess) e = hipEventCreateWithFlags(&st->ev_join[i], hipEventDisableTiming);
     }
     if (e == hipSuccess) e = hipEventCreateWithFlags(&st->ev_fork, hipEventDisableTiming);
+    if (e == hipSuccess && vit_bands(st) > 1) {
+        bool any_global = false;
+        for (const Block &b : m->blocks) any_global = any_global || b.global;
+        st->gvt_elems = m->heads * 64 * vt_ld_for(T);
+        for (int i = 0; i < 2 && any_global && e == hipSuccess; i++) {
+            e = hipMalloc(&st->gq16[i], (size_t)(T * E * 2 * 2));
+            if (e == hipSuccess) e = hipMalloc(&st->gk16[i], (size_t)(T * E * 2 * 2));
+            if (e == hipSuccess) e = hipMalloc(&st->gvt16[i], (size_t)(st->gvt_elems * 2 * 2));
+        }
+    }
     if (e == hipSuccess) e = alloc_neck(st);
     if (e != hipSuccess) {
         s3e_state_free(st);
@@ -1662,7 +1687,7 @@ enum : int { PH_A = 1, PH_B = 2, PH_C = 4, PH_ALL = 7 };
 // in the one window; its attention takes a band of queries too, against
 // all keys, once every band's phase A is done.
 hipError_t run_block_rows(s3e_state *st, int bi, float *x, int64_t r0, int64_t rows, hipStream_t s,
-                          int phases = PH_ALL) {
+                          int phases = PH_ALL, int gset = -1) {
     const s3e_model *m = st->m;
     const Block &b = m->blocks[(size_t)bi];
     const int64_t T = rows, E = m->E;
@@ -1687,9 +1712,13 @@ hipError_t run_block_rows(s3e_state *st, int bi, float *x, int64_t r0, int64_t r
     // Quantized (and F32) projections re-quantize the attention output: run
     // attention split so it matches f32 attention; F16 models use plain fp16.
     const bool split = b.proj.kind != WK_F16;
-    _Float16 *q = st->q16 + qoff, *k = st->k16 + qoff, *vt = st->vt16 + voff;
-    _Float16 *q_lo = split ? st->q16 + st->T * E + qoff : nullptr, *k_lo = split ? st->k16 + st->T * E + qoff : nullptr;
-    _Float16 *vt_lo = split ? st->vt16 + st->vt_elems + voff : nullptr;
+    // Q/K/Vᵀ planes: the state's own, or global set gset (banded runs)
+    _Float16 *Q = gset >= 0 ? st->gq16[gset] : st->q16, *K = gset >= 0 ? st->gk16[gset] : st->k16;
+    _Float16 *VT = gset >= 0 ? st->gvt16[gset] : st->vt16;
+    const int64_t vte = gset >= 0 ? st->gvt_elems : st->vt_elems;
+    _Float16 *q = Q + qoff, *k = K + qoff, *vt = VT + voff;
+    _Float16 *q_lo = split ? Q + st->T * E + qoff : nullptr, *k_lo = split ? K + st->T * E + qoff : nullptr;
+    _Float16 *vt_lo = split ? VT + vte + voff : nullptr;
     const Act a_proj = act_rows(st->a1.as(act_kind_gemm(b.proj), E), r0);
     hipError_t e = hipSuccess;
     if (phases & PH_A) {
@@ -1727,10 +1756,10 @@ hipError_t run_block_rows(s3e_state *st, int bi, float *x, int64_t r0, int64_t r
             // the band's queries (rows of the one window, heads Nw rows apart)
             // against every key
             aa.q_hs = (int64_t)Nw * 64;
-            aa.k = st->k16;
-            aa.vt = st->vt16;
-            aa.k_lo = split ? st->k16 + st->T * E : nullptr;
-            aa.vt_lo = split ? st->vt16 + st->vt_elems : nullptr;
+            aa.k = K;
+            aa.vt = VT;
+            aa.k_lo = split ? K + st->T * E : nullptr;
+            aa.vt_lo = split ? VT + vte : nullptr;
         } else {
             aa.k = k;
             aa.vt = vt;
@@ -1822,31 +1851,42 @@ hipError_t run_blocks(s3e_state *st, float *x) {
     }
     const int nwr = m->grid / m->window;
     const int64_t wrow = (int64_t)m->window * m->grid;
-    auto bands = [&](int bi, int phases) {
+    auto bands = [&](int bi, int phases, int gset) {
         hipError_t e = hipSuccess;
         for (int band = 0; band < nb && e == hipSuccess; band++) {
             const int64_t wr0 = (int64_t)nwr * band / nb, wr1 = (int64_t)nwr * (band + 1) / nb;
             e = run_block_rows(st, bi, x, wr0 * wrow, (wr1 - wr0) * wrow, band == 0 ? st->ctx->stream : st->aux[band - 1],
-                               phases);
+                               phases, gset);
         }
         return e;
     };
     hipStream_t bs[3] = {st->ctx->stream, st->aux[0], st->aux[1]};
     hipEvent_t done_a[3] = {st->ev_fork, st->ev_join[0], st->ev_join[1]};
+    // Hazards between bands.  Consecutive windowed blocks: each band writes
+    // and reads only its own windows.  A global block: each band writes its
+    // rows of a global Q/K/Vᵀ set and reads all of them only after the other
+    // bands' phase A (the cross waits below), and the windowed blocks keep
+    // their own planes, so a band entering or leaving a global block never
+    // writes what another band may still read.  Global blocks use the two
+    // sets in turn: a band rewrites a set only after the cross waits of the
+    // global block in between, which every band passes after finishing the
+    // attention that read that set.
+    int nglobal = 0;
     hipError_t e = fork_bands(st, nb);
     for (int i = 0; i < m->depth && e == hipSuccess; i++) {
         if (!m->blocks[(size_t)i].global) {
-            e = bands(i, PH_ALL);
+            e = bands(i, PH_ALL, -1);
             continue;
         }
         // a global block: every band's QKV, then each band waits for the
         // others' and runs the attention of its own queries and its phase C
-        e = bands(i, PH_A);
+        const int gset = nglobal++ & 1;
+        e = bands(i, PH_A, gset);
         for (int band = 0; band < nb && e == hipSuccess; band++) e = hipEventRecord(done_a[band], bs[band]);
         for (int band = 0; band < nb && e == hipSuccess; band++)
             for (int o = 0; o < nb && e == hipSuccess; o++)
                 if (o != band) e = hipStreamWaitEvent(bs[band], done_a[o], 0);
-        if (e == hipSuccess) e = bands(i, PH_B | PH_C);
+        if (e == hipSuccess) e = bands(i, PH_B | PH_C, gset);
     }
     return join_bands(st, nb, e);
 }

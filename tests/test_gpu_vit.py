@@ -123,8 +123,18 @@ def test_banded_encode_equals_block_chain(small, ctx):
     on three streams (24×24 tokens, window 8: three bands of 192 rows).
     Every element is computed as in the one-stream chain of s3e_vit_prefix +
     s3e_vit_block, so vit_output must equal that chain bit for bit, for each
-    activation format (fp6 split, Q8_0, Q8_1, fp16)."""
+    activation format (fp6 split, Q8_0, Q8_1, fp16).
+
+    First the blocks run one at a time on another input, so that the state's
+    Q/K/Vᵀ planes hold other values in both layouts: a band that overwrote
+    planes another band still reads (a windowed block's windows and a global
+    block's rows alias in one buffer) showed up here as a different result."""
     ft, om, gm, st, img, chw = small
+    other = ctx.to_device(np.random.default_rng(11).standard_normal((576, 1024)).astype(np.float32))
+    for i in range(om.depth):
+        st.block(i, other)
+    ctx.sync()
+    other.free()
     chw_d = ctx.to_device(chw)
     st.encode_chw(chw_d)
     banded = st.tensor("vit_output")
