@@ -1810,12 +1810,20 @@ hipError_t run_block(s3e_state *st, int bi, float *x) {
 // blocks while the others do the same, joined only around the global blocks'
 // attention, so one band's single-round kernel tails, epilogue bursts and
 // short LayerNorm passes overlap the other bands' main loops.  1 when the grid
-// has fewer than two window rows or a window row is not a multiple of 64
-// tokens.
+// has fewer than two window rows, a window row is not a multiple of 64
+// tokens, or the linears of the blocks read an activation buffer in more than
+// one format (the formats' rows differ in bytes — fp6 tiles, Q8, fp16, f32 —
+// so one band's rows in one format would overlap another band's in another).
 int vit_bands(const s3e_state *st) {
     const s3e_model *m = st->m;
     const int nwr = m->grid / m->window;
-    if (nwr < 2 || ((int64_t)m->window * m->grid) % 64 != 0 || !st->aux[0] || !st->aux[1]) return 1;
+    if (nwr < 2 || ((int64_t)m->window * m->grid) % 64 != 0 || !st->aux[0] || !st->aux[1] || m->blocks.empty())
+        return 1;
+    const AKind k1 = act_kind_gemm(m->blocks[0].qkv), k2 = act_kind_gemm(m->blocks[0].fc2);
+    for (const Block &b : m->blocks)
+        if (act_kind_gemm(b.qkv) != k1 || act_kind_gemm(b.proj) != k1 || act_kind_gemm(b.fc1) != k1 ||
+            act_kind_gemm(b.fc2) != k2)
+            return 1;
     return std::min(nwr, 3);
 }
 
