@@ -131,6 +131,27 @@ struct Weight {
 // fp6 copy run on the fp6 MFMA (A_F6), everything else as act_kind_for.
 inline AKind act_kind_gemm(const Weight &w) { return (w.kind == WK_Q4_0 && w.f6) ? A_F6 : act_kind_for(w.kind); }
 
+// Rows [r0, ...) of an activation as an activation of their own (r0 a
+// multiple of 64 for A_F6): codes and values by row (A_F6 by 64-row tile),
+// the scale planes by row inside each stage (their stage pitch mp stays the
+// buffer's).
+inline Act act_rows(const Act &a, int64_t r0) {
+    Act o = a;
+    switch (a.kind) {
+        case A_F6: o.x = (uint8_t *)a.x + (r0 / 64) * (a.ld / 128) * 12288; break;
+        case A_Q8_0: case A_Q8_1: o.x = (int8_t *)a.x + r0 * a.ld; break;
+        case A_F16: o.x = (_Float16 *)a.x + r0 * a.ld; break;
+        case A_F16X2:
+            o.x = (_Float16 *)a.x + r0 * a.ld;
+            o.lo = (_Float16 *)a.lo + r0 * a.ld;
+            break;
+        default: o.x = (float *)a.x + r0 * a.ld; break;
+    }
+    if (a.d) o.d = a.d + r0 * 4;
+    if (a.s) o.s = a.s + r0 * 4;
+    return o;
+}
+
 // GEMM epilogues.
 enum Epi : int {
     EPI_F32 = 0,     // y = acc + bias

@@ -1654,26 +1654,6 @@ hipError_t run_prefix(s3e_state *st, const float *chw, float *x) {
     return launch_layernorm(x, st->T, m->E, 1e-5f, m->ln_pre_w, m->ln_pre_b, none, x, s);
 }
 
-// Rows [r0, ...) of an activation as an activation of their own (r0 a
-// multiple of 64): codes and values by row (A_F6 by 64-row tile), the scale
-// planes by row inside each stage (their stage pitch mp stays the buffer's).
-Act act_rows(const Act &a, int64_t r0) {
-    Act o = a;
-    switch (a.kind) {
-        case A_F6: o.x = (uint8_t *)a.x + (r0 / 64) * (a.ld / 128) * 12288; break;
-        case A_Q8_0: case A_Q8_1: o.x = (int8_t *)a.x + r0 * a.ld; break;
-        case A_F16: o.x = (_Float16 *)a.x + r0 * a.ld; break;
-        case A_F16X2:
-            o.x = (_Float16 *)a.x + r0 * a.ld;
-            o.lo = (_Float16 *)a.lo + r0 * a.ld;
-            break;
-        default: o.x = (float *)a.x + r0 * a.ld; break;
-    }
-    if (a.d) o.d = a.d + r0 * 4;
-    if (a.s) o.s = a.s + r0 * 4;
-    return o;
-}
-
 // Phases of a block: A = LN1 + QKV, B = attention, C = proj + LN2 + fc1 + fc2.
 enum : int { PH_A = 1, PH_B = 2, PH_C = 4, PH_ALL = 7 };
 
