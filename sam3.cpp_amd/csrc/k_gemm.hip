@@ -1105,8 +1105,30 @@ hipError_t dispatch_epi(Epi epi, const GemmParams &p, hipStream_t st) {
     return hipErrorInvalidValue;
 }
 
+// fp16 products with work-groups to spare and a long K run on 128 × 128 tiles
+// (each wave 64 × 64: every operand read feeds two MFMAs), two work-groups per
+// CU.  fc1 at 5184 rows (1517 such tiles): 85-92 → 73-78 µs; in the banded
+// ViT frame (518 per band) and on short K (Hiera's first stages) the 64-row
+// tiles' three work-groups per CU measured as fast or faster.
+constexpr int64_t F16_WIDE_MIN_TILES = 1200;
+constexpr int64_t F16_WIDE_MIN_K = 512;
+
 template <int WK>
 hipError_t dispatch_waves(Epi epi, GemmParams &p, hipStream_t st) {
+    if constexpr (WK == WK_F16) {
+        const int64_t t128 = (int64_t)(p.M + 127) / 128 * p.tiles_n;
+        if (p.ksplit == 1 && t128 >= F16_WIDE_MIN_TILES && p.a_kbytes >= 2 * F16_WIDE_MIN_K &&
+            (epi == EPI_F32 || epi == EPI_GELU || epi == EPI_QKV || epi == EPI_HQKV)) {
+            p.tiles_m = (p.M + 127) / 128;
+            p.ntiles = p.tiles_m * p.tiles_n;
+            switch (epi) {
+                case EPI_F32: return launch_one<WK, EPI_F32, 128, 4>(p, st);
+                case EPI_GELU: return launch_one<WK, EPI_GELU, 128, 4>(p, st);
+                case EPI_QKV: return launch_one<WK, EPI_QKV, 128, 4>(p, st);
+                default: return launch_one<WK, EPI_HQKV, 128, 4>(p, st);
+            }
+        }
+    }
     constexpr int BM = 64;
     p.tiles_m = (p.M + BM - 1) / BM;
     p.ntiles = p.tiles_m * p.tiles_n;
