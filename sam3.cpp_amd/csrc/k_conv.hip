@@ -1,10 +1,11 @@
 // k_conv.hip — the SimpleFPN neck's GEMMs on gfx950 fp16 MFMA
-// (sam3_build_neck_graph, sam3.cpp:3863-3921): 2×2 stride-2 transposed
-// convolutions, 1×1 convolutions and 3×3 implicit-GEMM convolutions over
-// NHWC activations (a pixel is a row of channels).
+// (sam3_build_neck_graph, sam3.cpp:3863-3921): 1×1 convolutions and 3×3
+// implicit-GEMM convolutions over NHWC activations (a pixel is a row of
+// channels).  The 2×2 stride-2 transposed convolutions, whose fp16 kernels
+// are plain fp16 GEMMs with a scattering epilogue, run in k_gemm
+// (EPI_DECONV).
 //
-// Operands.  F16 weights (F16 files, and every transposed-convolution kernel,
-// which ggml casts to F16) meet fp16 activations: one
+// Operands.  F16 weights (F16 files) meet fp16 activations: one
 // v_mfma_f32_32x32x16_f16 per 32×32×16 step, exactly ggml's fp16 products
 // with fp32 accumulation.  F32 weights (quantized files) are held as two
 // fp16 planes w·2^k = wh + wl and meet activations held the same way
@@ -29,9 +30,7 @@
 // outside the image, so no im2col buffer exists.
 //
 // Epilogues write straight from the accumulators (lane = column, 16 rows
-// per 32×32 tile): + bias, optional gelu_erf, into f32, fp16 or split-fp16
-// rows; the transposed convolution scatters GEMM column (2·ky + kx)·Cout + co
-// of input pixel (y, x) to output pixel (2y + ky, 2x + kx), channel co.
+// per 32×32 tile): + bias into f32, fp16 or split-fp16 rows.
 #include "s3e_internal.h"
 
 namespace s3e {
@@ -263,11 +262,7 @@ __global__ __launch_bounds__(conv_nth<BM_>, (SPLIT || BM_ == 256) ? 1 : 2) void 
     for (int n = 0; n < NT; n++) {
         const int gn = n0 + wn * 64 + 32 * n + lr;
         if (gn >= p.N) continue;
-        int q = 0, co = gn;
-        if constexpr (EPI == EPI_DECONV) {
-            q = gn / e.dc_cout;  // kernel tap: ky = q / 2, kx = q % 2
-            co = gn - q * e.dc_cout;
-        }
+        const int co = gn;
         const float bv = e.bias[co];
 #pragma unroll
         for (int i = 0; i < MT; i++)
@@ -285,16 +280,8 @@ __global__ __launch_bounds__(conv_nth<BM_>, (SPLIT || BM_ == 256) ? 1 : 2) void 
                     }
                 }
                 float v = __fadd_rn(acc[i][n][r] * alpha, b);
-                if constexpr (EPI == EPI_F32) {
-                    e.y[(int64_t)gm * e.ldy + gn] = v;
-                } else if constexpr (EPI == EPI_ACT) {
-                    store_act(e.out, gm, gn, v);
-                } else {
-                    if (e.gelu) v = gelu_erf(v);
-                    const int iy = gm / e.dc_w, ix = gm - iy * e.dc_w;
-                    const int64_t orow = (int64_t)(2 * iy + (q >> 1)) * (2 * e.dc_w) + 2 * ix + (q & 1);
-                    store_act(e.out, orow, co, v);
-                }
+                if constexpr (EPI == EPI_F32) e.y[(int64_t)gm * e.ldy + gn] = v;
+                else store_act(e.out, gm, gn, v);
             }
     }
 }
@@ -320,7 +307,6 @@ hipError_t dispatch(Epi epi, bool conv3, ConvParams &p, hipStream_t st) {
     switch (epi) {
         case EPI_F32: return launch_one<SPLIT, 0, EPI_F32>(p, st);
         case EPI_ACT: return launch_one<SPLIT, 0, EPI_ACT>(p, st);
-        case EPI_DECONV: return launch_one<SPLIT, 0, EPI_DECONV>(p, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -359,8 +345,6 @@ hipError_t launch_conv(const Weight &w, const Act &a, int64_t M, Epi epi, const 
         p.spt = g->spt;
         p.zero = (const uint8_t *)g->zero;
     }
-    if (epi == EPI_DECONV && (ea.dc_w <= 0 || ea.dc_cout <= 0 || w.N % ea.dc_cout != 0 || M % ea.dc_w != 0))
-        return hipErrorInvalidValue;
     return split ? dispatch<true>(epi, g != nullptr, p, st) : dispatch<false>(epi, g != nullptr, p, st);
 }
 

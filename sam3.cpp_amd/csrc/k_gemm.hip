@@ -477,6 +477,47 @@ __device__ __forceinline__ void epilogue(const GemmParams &p, const float *Ct, i
                               o.kind == A_Q8_1 ? o.s + blk : nullptr);
             }
         }
+    } else if constexpr (EPI == EPI_DECONV) {
+        // 2×2 stride-2 transposed convolution: column (2·ky + kx)·Cout + co of
+        // input pixel iy·W + ix goes to output pixel (2·iy + ky, 2·ix + kx),
+        // channel co.  Lane ↔ 4 consecutive columns (Cout % 4 == 0, so the
+        // four share one tap and one output row); + bias, optional gelu_erf,
+        // into f32, fp16 or split-fp16 rows.
+        const int f = t & 31;
+        const int gn = n0 + 4 * f;
+        if (gn >= p.N) return;
+        const int q = gn / e.dc_cout, co = gn - q * e.dc_cout;
+        const float4 bb = *(const float4 *)(e.bias + co);
+        const float bj[4] = {bb.x, bb.y, bb.z, bb.w};
+        const Act &o = e.out;
+        for (int row = t >> 5; row < BM; row += NT_ / 32) {
+            const int gm = m0 + row;
+            if (gm >= p.M) break;
+            const float4 x = *(const float4 *)(Ct + row * CLD + 4 * f);
+            float v[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                v[j] = __fadd_rn(v[j], bj[j]);
+                if (e.gelu) v[j] = gelu_erf(v[j]);
+            }
+            const int iy = gm / e.dc_w, ix = gm - iy * e.dc_w;
+            const int64_t orow = (int64_t)(2 * iy + (q >> 1)) * (2 * e.dc_w) + 2 * ix + (q & 1);
+            const int64_t i = orow * o.ld + co;
+            if (o.kind == A_F32) {
+                *(float4 *)((float *)o.x + i) = make_float4(v[0], v[1], v[2], v[3]);
+                continue;
+            }
+            uint32_t w[2], wl[2];
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const _Float16 h0 = to_half(v[2 * j]), h1 = to_half(v[2 * j + 1]);
+                w[j] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+                const _Float16 l0 = (_Float16)(v[2 * j] - (float)h0), l1 = (_Float16)(v[2 * j + 1] - (float)h1);
+                wl[j] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+            }
+            *(uint2 *)((_Float16 *)o.x + i) = make_uint2(w[0], w[1]);
+            if (o.kind == A_F16X2) *(uint2 *)((_Float16 *)o.lo + i) = make_uint2(wl[0], wl[1]);
+        }
     } else {
         // EPI_F32 / EPI_RESID / EPI_POS: lane ↔ 4 consecutive columns, so that one
         // wave store covers 2 rows × 512 contiguous bytes
@@ -1100,7 +1141,11 @@ hipError_t dispatch_epi(Epi epi, const GemmParams &p, hipStream_t st) {
         case EPI_GELU: return launch_one<WK, EPI_GELU, 64, WAVES>(p, st);
         case EPI_QKV: return launch_one<WK, EPI_QKV, 64, WAVES>(p, st);
         case EPI_HQKV: return launch_one<WK, EPI_HQKV, 64, WAVES>(p, st);
-        default: break;  // the neck epilogues belong to k_conv
+        case EPI_DECONV:
+            // the neck's transposed convolutions (fp16 kernels)
+            if constexpr (WK == WK_F16) return launch_one<WK, EPI_DECONV, 64, WAVES>(p, st);
+            break;
+        default: break;  // EPI_ACT belongs to k_conv
     }
     return hipErrorInvalidValue;
 }
@@ -1118,13 +1163,14 @@ hipError_t dispatch_waves(Epi epi, GemmParams &p, hipStream_t st) {
     if constexpr (WK == WK_F16) {
         const int64_t t128 = (int64_t)(p.M + 127) / 128 * p.tiles_n;
         if (p.ksplit == 1 && t128 >= F16_WIDE_MIN_TILES && p.a_kbytes >= 2 * F16_WIDE_MIN_K &&
-            (epi == EPI_F32 || epi == EPI_GELU || epi == EPI_QKV || epi == EPI_HQKV)) {
+            (epi == EPI_F32 || epi == EPI_GELU || epi == EPI_QKV || epi == EPI_HQKV || epi == EPI_DECONV)) {
             p.tiles_m = (p.M + 127) / 128;
             p.ntiles = p.tiles_m * p.tiles_n;
             switch (epi) {
                 case EPI_F32: return launch_one<WK, EPI_F32, 128, 4>(p, st);
                 case EPI_GELU: return launch_one<WK, EPI_GELU, 128, 4>(p, st);
                 case EPI_QKV: return launch_one<WK, EPI_QKV, 128, 4>(p, st);
+                case EPI_DECONV: return launch_one<WK, EPI_DECONV, 128, 4>(p, st);
                 default: return launch_one<WK, EPI_HQKV, 128, 4>(p, st);
             }
         }
@@ -1197,6 +1243,14 @@ hipError_t launch_gemm(const Weight &w, const Act &a, int64_t M, Epi epi, const 
             ea.hdp < ea.HD || ea.hdp % 8 != 0 || ea.NH * ea.HD != ea.E || ea.grid <= 0 || ea.grid_h <= 0 ||
             (int64_t)ea.grid * ea.grid_h != M || ea.window < 0 || !ea.bias || !ea.k || !ea.vt || ea.vt_ld <= 0 ||
             (ea.qpool ? (!ea.y || ea.ldy < ea.E) : !ea.q))
+            return hipErrorInvalidValue;
+    }
+    if (epi == EPI_DECONV) {
+        // fp16 kernels on fp16 rows, four taps of Cout columns, whole input rows
+        const Act &o = ea.out;
+        if (w.kind != WK_F16 || a.kind != A_F16 || ea.dc_w <= 0 || ea.dc_cout <= 0 || ea.dc_cout % 4 != 0 ||
+            w.N != 4LL * ea.dc_cout || M % ea.dc_w != 0 || !ea.bias || !o.x || o.ld % 4 != 0 || o.ld < ea.dc_cout ||
+            (o.kind != A_F16 && o.kind != A_F16X2 && o.kind != A_F32) || (o.kind == A_F16X2 && !o.lo))
             return hipErrorInvalidValue;
     }
     if (a.kind == A_F6) {

@@ -296,6 +296,8 @@ struct SmArgs {
 // Floats of workspace a product of M rows against w would use when split over
 // K (0: it runs unsplit): products with fewer tiles than CUs and a long K.
 int64_t gemm_splitk_floats(const Weight &w, int64_t M);
+// Products against uploaded weights (k_gemm.hip): every epilogue but EPI_ACT;
+// EPI_DECONV takes WK_F16 weights and A_F16 rows.
 hipError_t launch_gemm(const Weight &w, const Act &a, int64_t M, Epi epi, const EpiArgs &ea,
                        hipStream_t st);
 // Small-M products (k_gemm_sm.hip): Q4_0 / Q4_1 / Q8_0 / F16 weights, M ≤ 64.
@@ -310,8 +312,8 @@ hipError_t launch_gemm_sm(WKind kind, const SmArgs &a, int wgs, int ks, hipStrea
 // LDS; wgs = total of sm_wgs(N, 1).
 hipError_t launch_gemm_smb(WKind kind, const SmArgs &a, int wgs, hipStream_t st);
 // Neck GEMMs (k_conv.hip; WK_F16 or WK_F16X3 weights with N padded to
-// CONV_BN): EPI_DECONV / EPI_ACT / EPI_F32 on plain rows, or EPI_F32 as a
-// 3×3 implicit GEMM when g is given.
+// CONV_BN): EPI_ACT / EPI_F32 on plain rows, or EPI_F32 as a 3×3 implicit
+// GEMM when g is given.
 hipError_t launch_conv(const Weight &w, const Act &a, int64_t M, Epi epi, const EpiArgs &ea,
                        const ConvGeom *g, hipStream_t st);
 // NHWC f32 [h][w][c] → act (A_F16 or A_F16X2) of the same pixels (pool = 1)

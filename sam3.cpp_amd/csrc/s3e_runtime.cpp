@@ -1915,7 +1915,7 @@ hipError_t run_level(s3e_state *st, int which, int lvl, const float *x, hipStrea
         e.dc_cout = (int)(w.N / 4);
         e.gelu = gelu;
         e.out = o;
-        return launch_conv(w, in, (int64_t)in_side * in_side, EPI_DECONV, e, nullptr, s);
+        return launch_gemm(w, in, (int64_t)in_side * in_side, EPI_DECONV, e, s);
     };
     const Act x16 = plane_act(A_F16, st->nx, st->nx_cap, E);  // fp16(x): the deconvolutions' input
     hipError_t err = hipSuccess;
