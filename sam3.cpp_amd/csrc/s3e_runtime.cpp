@@ -1654,8 +1654,12 @@ hipError_t run_prefix(s3e_state *st, const float *chw, float *x) {
     return launch_layernorm(x, st->T, m->E, 1e-5f, m->ln_pre_w, m->ln_pre_b, none, x, s);
 }
 
-// Phases of a block: A = LN1 + QKV, B = attention, C = proj + LN2 + fc1 + fc2.
-enum : int { PH_A = 1, PH_B = 2, PH_C = 4, PH_ALL = 7 };
+// The launches of a block, one bit each, and its phases: A = LN1 + QKV,
+// B = attention, C = proj + LN2 + fc1 + fc2.
+enum : int {
+    ST_LN1 = 1, ST_QKV = 2, ST_ATTN = 4, ST_PROJ = 8, ST_LN2 = 16, ST_FC1 = 32, ST_FC2 = 64,
+    PH_A = ST_LN1 | ST_QKV, PH_B = ST_ATTN, PH_C = ST_PROJ | ST_LN2 | ST_FC1 | ST_FC2, PH_ALL = PH_A | PH_B | PH_C
+};
 
 // sam3_vit_block_forward (sam3.cpp:3710-3801) as 7 launches on stream s, for
 // the token rows [r0, r0 + rows) (r0 and rows multiples of 64).  Phases A and
@@ -1700,12 +1704,16 @@ hipError_t run_block_rows(s3e_state *st, int bi, float *x, int64_t r0, int64_t r
     _Float16 *q_lo = split ? Q + st->T * E + qoff : nullptr, *k_lo = split ? K + st->T * E + qoff : nullptr;
     _Float16 *vt_lo = split ? VT + vte + voff : nullptr;
     const Act a_proj = act_rows(st->a1.as(act_kind_gemm(b.proj), E), r0);
+    const Act a_qkv = act_rows(st->a1.as(act_kind_gemm(b.qkv), E), r0);
+    const Act a_fc1 = act_rows(st->a1.as(act_kind_gemm(b.fc1), E), r0);
+    const Act a_fc2 = act_rows(st->a2.as(act_kind_gemm(b.fc2), m->mlp), r0);
     hipError_t e = hipSuccess;
-    if (phases & PH_A) {
+    if (phases & ST_LN1) {
         // LN1 → activation for the QKV weight
-        const Act a_qkv = act_rows(st->a1.as(act_kind_gemm(b.qkv), E), r0);
         e = launch_layernorm(xb, T, E, 1e-5f, b.n1w, b.n1b, a_qkv, nullptr, s);
         if (e != hipSuccess) return e;
+    }
+    if (phases & ST_QKV) {
         // QKV GEMM + bias + RoPE → fp16 Q, K, Vᵀ in window layout
         EpiArgs eq;
         eq.bias = b.qkv_b;
@@ -1725,7 +1733,7 @@ hipError_t run_block_rows(s3e_state *st, int bi, float *x, int64_t r0, int64_t r
         e = launch_gemm(b.qkv, a_qkv, T, EPI_QKV, eq, s);
         if (e != hipSuccess) return e;
     }
-    if (phases & PH_B) {
+    if (phases & ST_ATTN) {
         // attention → activation for the proj weight, un-partitioned
         AttnArgs aa;
         aa.q = q;
@@ -1755,7 +1763,7 @@ hipError_t run_block_rows(s3e_state *st, int bi, float *x, int64_t r0, int64_t r
         e = launch_attn(aa, s);
         if (e != hipSuccess) return e;
     }
-    if (phases & PH_C) {
+    if (phases & ST_PROJ) {
         // proj + bias + residual
         EpiArgs ep;
         ep.bias = b.proj_b;
@@ -1763,20 +1771,25 @@ hipError_t run_block_rows(s3e_state *st, int bi, float *x, int64_t r0, int64_t r
         ep.ldy = E;
         e = launch_gemm(b.proj, a_proj, T, EPI_RESID, ep, s);
         if (e != hipSuccess) return e;
-        // LN2 → fc1 + bias + GELU(erf) → activation for fc2 → fc2 + bias + residual
-        const Act a_fc1 = act_rows(st->a1.as(act_kind_gemm(b.fc1), E), r0);
+    }
+    // LN2 → fc1 + bias + GELU(erf) → activation for fc2 → fc2 + bias + residual
+    if (phases & ST_LN2) {
         e = launch_layernorm(xb, T, E, 1e-5f, b.n2w, b.n2b, a_fc1, nullptr, s);
         if (e != hipSuccess) return e;
+    }
+    if (phases & ST_FC1) {
         EpiArgs e1;
         e1.bias = b.fc1_b;
-        e1.out = act_rows(st->a2.as(act_kind_gemm(b.fc2), m->mlp), r0);
+        e1.out = a_fc2;
         e = launch_gemm(b.fc1, a_fc1, T, EPI_GELU, e1, s);
         if (e != hipSuccess) return e;
+    }
+    if (phases & ST_FC2) {
         EpiArgs e2;
         e2.bias = b.fc2_b;
         e2.y = xb;
         e2.ldy = E;
-        e = launch_gemm(b.fc2, e1.out, T, EPI_RESID, e2, s);
+        e = launch_gemm(b.fc2, a_fc2, T, EPI_RESID, e2, s);
     }
     return e;
 }
@@ -1839,12 +1852,17 @@ hipError_t run_blocks(s3e_state *st, float *x) {
     }
     const int nwr = m->grid / m->window;
     const int64_t wrow = (int64_t)m->window * m->grid;
+    // the launches of the bands are enqueued step by step (each band's LN1,
+    // then each band's QKV, ...), in the order the bands will need them
     auto bands = [&](int bi, int phases, int gset) {
         hipError_t e = hipSuccess;
-        for (int band = 0; band < nb && e == hipSuccess; band++) {
-            const int64_t wr0 = (int64_t)nwr * band / nb, wr1 = (int64_t)nwr * (band + 1) / nb;
-            e = run_block_rows(st, bi, x, wr0 * wrow, (wr1 - wr0) * wrow, band == 0 ? st->ctx->stream : st->aux[band - 1],
-                               phases, gset);
+        for (int step = ST_LN1; step <= ST_FC2 && e == hipSuccess; step <<= 1) {
+            if (!(phases & step)) continue;
+            for (int band = 0; band < nb && e == hipSuccess; band++) {
+                const int64_t wr0 = (int64_t)nwr * band / nb, wr1 = (int64_t)nwr * (band + 1) / nb;
+                e = run_block_rows(st, bi, x, wr0 * wrow, (wr1 - wr0) * wrow,
+                                   band == 0 ? st->ctx->stream : st->aux[band - 1], step, gset);
+            }
         }
         return e;
     };
