@@ -24,8 +24,8 @@
 // sums in index order.  The next stage is loaded while one is
 // consumed.  Per 32-element block and 32-row tile
 // the arithmetic is the large-M kernel's: the exact integer block sum on
-// v_mfma_i32_32x32x32_i8 (the Q4_0 offset −8 applied by a second MFMA against
-// a constant −8 operand, so the nibbles need only a mask or a shift), the
+// v_mfma_i32_32x32x32_i8 (Q4_0 nibbles n become the signed codes n − 8 four
+// bytes at a time: (n + 0x78) ^ 0x80 per byte, no carry between bytes), the
 // exact scale product 2·dx·dw on a one-hot v_mfma_f32_32x32x16_f16, and
 // acc += float(S)·c on the VALU; Q4_1 adds Σ m_w·s_x per stage on fp16 MFMA.
 // F16 weights run on v_mfma_f32_32x32x16_f16 directly.
@@ -134,7 +134,6 @@ __global__ __launch_bounds__(64 * SM_WAVES, 2) void k_gemm_sm(SmArgs p) {
         if constexpr (C::quant) {
             const v16i zi = {};
             const v16f zf = {};
-            const v4i minus8 = {(int)0xF8F8F8F8, (int)0xF8F8F8F8, (int)0xF8F8F8F8, (int)0xF8F8F8F8};
             const uint32_t wdw[2] = {f.wd.x, f.wd.y};
 #pragma unroll
             for (int j = 0; j < 4; j++) {
@@ -145,6 +144,9 @@ __global__ __launch_bounds__(64 * SM_WAVES, 2) void k_gemm_sm(SmArgs p) {
                     b[1] = (int)((f.w[j].y >> sh) & 0x0F0F0F0Fu);
                     b[2] = (int)((f.w[j].z >> sh) & 0x0F0F0F0Fu);
                     b[3] = (int)((f.w[j].w >> sh) & 0x0F0F0F0Fu);
+                    if constexpr (WK == WK_Q4_0)
+#pragma unroll
+                        for (int e = 0; e < 4; e++) b[e] = (int)(((uint32_t)b[e] + 0x78787878u) ^ 0x80808080u);
                 } else {
                     b = __builtin_bit_cast(v4i, f.w[j]);
                 }
@@ -154,7 +156,6 @@ __global__ __launch_bounds__(64 * SM_WAVES, 2) void k_gemm_sm(SmArgs p) {
                 for (int i = 0; i < MT; i++) {
                     const v4i a = __builtin_bit_cast(v4i, f.a[i][j]);
                     v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, zi, 0, 0, 0);
-                    if constexpr (WK == WK_Q4_0) S = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, minus8, S, 0, 0, 0);
                     const uint32_t adw[2] = {f.ad[i].x, f.ad[i].y};
                     const uint32_t ha_ = (adw[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
                     const v4u ha = {ha_, 0u, 0u, 0u};
@@ -404,7 +405,6 @@ __global__ __launch_bounds__(64 * SM_WAVES, 2) void k_gemm_smb(SmArgs p) {
             const uint8_t *Wl = L + B::W_OFF + wave * B::WW;
             const v16i zi = {};
             const v16f zf = {};
-            const v4i minus8 = {(int)0xF8F8F8F8, (int)0xF8F8F8F8, (int)0xF8F8F8F8, (int)0xF8F8F8F8};
             // the rows' 4 block scales are the raw K = 8 operand of the scale
             // product; the weight side is one-hot at block j (both K halves)
             v4h ha[MT];
@@ -424,6 +424,9 @@ __global__ __launch_bounds__(64 * SM_WAVES, 2) void k_gemm_smb(SmArgs p) {
                     const int sh = 4 * lh;  // low nibbles: elements 0..15, high: 16..31
 #pragma unroll
                     for (int e = 0; e < 4; e++) b[e] = (int)(((uint32_t)wq[e] >> sh) & 0x0F0F0F0Fu);
+                    if constexpr (WK == WK_Q4_0)
+#pragma unroll
+                        for (int e = 0; e < 4; e++) b[e] = (int)(((uint32_t)b[e] + 0x78787878u) ^ 0x80808080u);
                 } else {
                     b = *(const v4i *)(Wl + (j * 32 + lr) * 32 + lh * 16);
                 }
@@ -435,7 +438,6 @@ __global__ __launch_bounds__(64 * SM_WAVES, 2) void k_gemm_smb(SmArgs p) {
                     const int r = 32 * i + lr;
                     const v4i a = *(const v4i *)(L + r * B::ROWB + (((2 * j + lh) ^ smb_swz<B::ROWB>(r)) << 4));
                     v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, zi, 0, 0, 0);
-                    if constexpr (WK == WK_Q4_0) S = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, minus8, S, 0, 0, 0);
                     const v16f Cs = __builtin_amdgcn_mfma_f32_32x32x8f16(ha[i], hb, zf, 0, 0, 0);
 #pragma unroll
                     for (int r2 = 0; r2 < 16; r2++) acc[i][r2] = __builtin_fmaf((float)S[r2], Cs[r2], acc[i][r2]);
