@@ -129,6 +129,40 @@ def test_mul_mat(ctx, wt, M, N, K):
     assert err <= 1e-5
 
 
+def _random_shapes(n, seed):
+    """Ragged products for every weight type: M from 1 to 900 (the small-M
+    kernels up to 64 rows, split-K below a CU's worth of tiles, partial row
+    and column tiles), N from 1 to 1500 (not a multiple of 4 or 128), K a
+    multiple of 32 (a ggml block) that need not be one of 128 (a stage)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        wt = WTYPES[i % len(WTYPES)]
+        M = int(rng.integers(1, 65)) if i % 3 == 0 else int(rng.integers(65, 901))
+        out.append((wt, M, int(rng.integers(1, 1501)), 32 * int(rng.integers(1, 81))))
+    return out
+
+
+@pytest.mark.parametrize("wt,M,N,K", _random_shapes(20, 2026),
+                         ids=lambda v: str(v) if not isinstance(v, tuple) else None)
+def test_mul_mat_ragged_shapes(ctx, wt, M, N, K):
+    rng = np.random.default_rng(M * 131 + N * 7 + K + wt)
+    W = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    bias = rng.normal(0, 0.1, N).astype(np.float32)
+    wb = orc.to_weight_bytes(wt, W)
+    ref = orc.mul_mat(wt, wb, N, K, X) + bias
+    w = ctx.weight(wt, K, N, wb)
+    Xd, bd, Yd = ctx.to_device(X), ctx.to_device(bias), ctx.buffer(M * N * 4)
+    ctx.mul_mat(w, Xd, M, Yd, bd)
+    ctx.sync()
+    Y = Yd.download(np.float32, (M, N))
+    err = orc.rel_l2(Y, ref)
+    print(f"ragged mul_mat type={wt} M={M} N={N} K={K}: rel_l2={err:.3e} max_abs={orc.max_abs(Y, ref):.3e}", flush=True)
+    assert np.all(np.isfinite(Y))
+    assert err <= 1e-5
+
+
 @pytest.mark.parametrize("M,N,K", [(100, 384, 1024), (777, 1024, 4736), (5184, 4736, 1024)])
 def test_mul_mat_q_f6(ctx, M, N, K):
     """Q4_0 products on the fp6 kernel (activations as S3E_TYPE_Q8_0_F6X2)
