@@ -388,6 +388,40 @@ def test_flash_attn_head_dims(ctx, D, B, nh, Nq, Nkv, prec):
     assert err <= (2e-3 if prec == 0 else 1e-5)
 
 
+def _ragged_attn(n, seed):
+    """Edge and ragged attention shapes: a single query and key, fewer keys than
+    one 32-key tile, then random Nq and Nkv up to 900 with head dims 64 and 128,
+    both precisions."""
+    out = [(64, 1, 1, 1, 1, 1), (64, 1, 2, 3, 17, 0), (128, 2, 1, 33, 5, 1)]
+    rng = np.random.default_rng(seed)
+    for i in range(n):
+        out.append((64 if i % 2 == 0 else 128, int(rng.integers(1, 3)), int(rng.integers(1, 5)),
+                    int(rng.integers(1, 901)), int(rng.integers(1, 901)), i % 3 != 0))
+    return [tuple(int(v) for v in c) for c in out]
+
+
+@pytest.mark.parametrize("D,B,nh,Nq,Nkv,prec", _ragged_attn(7, 2027), ids=lambda x: str(x))
+def test_flash_attn_ragged(ctx, D, B, nh, Nq, Nkv, prec):
+    rng = np.random.default_rng(D + 3 * Nq + 5 * Nkv + 7 * nh + B)
+    q = rng.standard_normal((B, nh, Nq, D)).astype(np.float32)
+    k = rng.standard_normal((B, nh, Nkv, D)).astype(np.float32)
+    v_tok = rng.standard_normal((B, Nkv, nh, D)).astype(np.float32)
+    v = np.ascontiguousarray(v_tok.transpose(0, 2, 1, 3))
+    scale = 1.0 / np.sqrt(D)
+    ref = orc.flash_attn(q, k, v, scale)
+    qd, kd, vd = ctx.to_device(q), ctx.to_device(k), ctx.to_device(v_tok)
+    od = ctx.buffer(B * Nq * nh * D * 4)
+    print(f"ragged flash_attn D={D} B={B} nh={nh} Nq={Nq} Nkv={Nkv} prec={prec}", flush=True)
+    ctx.flash_attn_ext(qd, (1, D, Nq * D, nh * Nq * D), kd, (1, D, Nkv * D, nh * Nkv * D), vd,
+                       (1, nh * D, D, Nkv * nh * D), D, Nq, Nkv, nh, B, scale, od, prec=prec)
+    ctx.sync()
+    out = od.download(np.float32, (B, Nq, nh, D))
+    err = orc.rel_l2(out, ref)
+    print(f"  rel_l2={err:.3e} max_abs={orc.max_abs(out, ref):.3e}", flush=True)
+    assert np.all(np.isfinite(out))
+    assert err <= (2e-3 if prec == 0 else 1e-5)
+
+
 def test_flash_attn_rejects(ctx):
     buf = ctx.buffer(1 << 20)
     nb = (1, 64, 64 * 64, 64 * 64)
