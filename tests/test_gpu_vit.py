@@ -149,3 +149,44 @@ def test_banded_encode_equals_block_chain(small, ctx):
     assert ndiff == 0
     for b in (chw_d, xd):
         b.free()
+
+
+@pytest.mark.parametrize("ft", ["q4_0", "q8_0", "f16"])
+def test_two_bands_and_both_global_plane_sets(tmpdir_session, ctx, ft):
+    """A grid of two window rows (48×48 tokens, window 24) runs in two bands,
+    and two global blocks (1 and 3) use the two global Q/K/Vᵀ plane sets in
+    turn: the banded encode equals the one-stream chain bit for bit, with the
+    planes first filled from another input as in the three-band test."""
+    import s3e
+
+    path = os.path.join(str(tmpdir_session), f"vit_two_bands_{ft}.ggml")
+    s3e.synth_write(path, img_size=672, patch=14, embed_dim=512, depth=5, heads=8, window=24, mlp_ratio_x1000=4500,
+                    global_idx=(1, 3), ftype=ft, seed=9, std=0.02, random_affine=True, neck=0)
+    gm = s3e.Model(ctx, path)
+    st = s3e.State(ctx, gm)
+    try:
+        rng = np.random.default_rng(12)
+        other = ctx.to_device(rng.standard_normal((2304, 512)).astype(np.float32))
+        for i in range(5):
+            st.block(i, other)
+        ctx.sync()
+        other.free()
+        chw = orc.preprocess_sam3(rng.integers(0, 256, (672, 672, 3), dtype=np.uint8), 672)
+        chw_d = ctx.to_device(chw)
+        st.encode_chw(chw_d)
+        banded = st.tensor("vit_output")
+        xd = ctx.buffer(banded.nbytes)
+        st.prefix(chw_d, xd)
+        for i in range(5):
+            st.block(i, xd)
+        ctx.sync()
+        chain = xd.download(np.float32, banded.shape)
+        ndiff = int(np.count_nonzero(banded != chain))
+        print(f"{ft} two bands vs chain: {ndiff} differing elements, |x|max={np.abs(chain).max():.3f}", flush=True)
+        assert np.all(np.isfinite(chain))
+        assert ndiff == 0
+        for b in (chw_d, xd):
+            b.free()
+    finally:
+        st.free()
+        gm.free()
