@@ -15,7 +15,11 @@
 // own accumulator.  Q4_0 weights with an fp6 copy run in k_gemm_f6 (below),
 // where the block sum comes out of the fp6 MFMA already in fp32.  F16
 // weights run on fp16 MFMA against activations rounded to fp16; F32 weights
-// run on fp32 MFMA.
+// run on fp32 MFMA, or, uploaded as fp16 pairs (WK_F16X3: w·2^k = wh + wl)
+// against activations held the same way (x = xh + xl), as xh·wh + xh·wl +
+// xl·wh on fp16 MFMA — each product exact in fp32, the dropped xl·wl ~2^-22
+// relative — in stages of 32 K whose hi and lo planes are 64-byte LDS rows
+// (chunk c of row r at slot c ^ ((r >> 2) & 3)).
 //
 // Per work-group: a 64×128 output tile and 4 waves (2 along M × 2 along N,
 // each 32×64; three work-groups per CU) or, for Q4_1, 8 waves (2 × 4, each
@@ -69,13 +73,17 @@ struct Cfg {
     static constexpr int NTH = 64 * WAVES;
     static constexpr bool quant = (WK == WK_Q4_0 || WK == WK_Q4_1 || WK == WK_Q8_0);
     static constexpr bool q41 = (WK == WK_Q4_1);
-    static constexpr int esize = quant ? 1 : (WK == WK_F16 ? 2 : 4);
+    // WK_F16X3: fp32 operands as fp16 pairs x = hi + lo, each plane of a stage
+    // 32 K wide (64-byte rows: the hi plane of the tile, then the lo plane)
+    static constexpr bool split = (WK == WK_F16X3);
+    static constexpr int esize = quant ? 1 : ((WK == WK_F16 || split) ? 2 : 4);
     static constexpr int WM = 2, WN = WAVES / 2;
     static constexpr int MT = BM / (32 * WM);            // 32-row MFMA tiles per wave
     static constexpr int NT = BN / (32 * WN);            // 32-column MFMA tiles per wave
     static constexpr int NBUF = WAVES == 4 ? 2 : 3;      // LDS ring depth
     static constexpr int OFF_A = 0;
     static constexpr int OFF_B = BM * ROWB;
+    static constexpr int OFF_ALO = BM * 64, OFF_BLO = OFF_B + BN * 64;  // split: lo planes
     static constexpr int OFF_SC = OFF_B + BN * ROWB;     // scales: AD | BD | AS | BMIN
     static constexpr int OFF_AD = OFF_SC;
     static constexpr int OFF_BD = OFF_AD + (quant ? BM * 8 : 0);
@@ -107,6 +115,8 @@ struct GemmParams {
     const uint8_t *b_d, *b_m;     // stage-major fp16 planes, b_np rows per group
     int64_t b_ld, b_np;
     int M, N, nstages, tiles_m, tiles_n, ntiles;
+    const uint8_t *a_lo, *b_lo;   // WK_F16X3: the lo planes (same layouts as a / b)
+    float alpha;                  // WK_F16X3: the weight planes hold w·2^k; alpha = 2^−k
     EpiArgs e;
 };
 
@@ -185,6 +195,9 @@ __device__ __forceinline__ void quant_block32_f6(const float *v, uint64_t *base,
 #define S3E_SWZ_SHIFT 1
 #endif
 __device__ __forceinline__ int swz(int r) { return (r >> S3E_SWZ_SHIFT) & 7; }
+// Rows of 64 bytes (split planes): four rows share a 256-byte bank cycle;
+// 16-byte chunk c of row r sits at slot c ^ ((r >> 2) & 3).
+__device__ __forceinline__ int swz64(int r) { return (r >> 2) & 3; }
 
 // 4 bytes per lane, likewise (scale planes).  A buffer load, unlike
 // global_load_lds, is not a flat-segment access, so the compiler keeps the
@@ -465,6 +478,23 @@ __device__ __forceinline__ void epilogue(const GemmParams &p, const float *Ct, i
                 d4[1] = make_uint4(w[4], w[5], w[6], w[7]);
                 d4[2] = make_uint4(w[8], w[9], w[10], w[11]);
                 d4[3] = make_uint4(w[12], w[13], w[14], w[15]);
+            } else if (o.kind == A_F16X2) {
+                // fp16 pairs: hi = fp16(v), lo = fp16(v − hi)
+                _Float16 *dst = (_Float16 *)o.x + (int64_t)gm * o.ld + gn0;
+                _Float16 *dlo = (_Float16 *)o.lo + (int64_t)gm * o.ld + gn0;
+                uint32_t w[16], wl[16];
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    const _Float16 h0 = to_half(v[2 * j]), h1 = to_half(v[2 * j + 1]);
+                    w[j] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+                    const _Float16 l0 = (_Float16)(v[2 * j] - (float)h0), l1 = (_Float16)(v[2 * j + 1] - (float)h1);
+                    wl[j] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+                }
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    ((uint4 *)dst)[j] = make_uint4(w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]);
+                    ((uint4 *)dlo)[j] = make_uint4(wl[4 * j], wl[4 * j + 1], wl[4 * j + 2], wl[4 * j + 3]);
+                }
             } else if (o.kind == A_F32) {
                 float4 *dst = (float4 *)((float *)o.x + (int64_t)gm * o.ld + gn0);
 #pragma unroll
@@ -631,18 +661,34 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 3 : 256 / BM) void k_gemm(
     // vector ALU work.
     const int dma_row = lane >> 3;
     int a_vo[C::NA], a_cofs[C::NA], b_vo[C::NB];
+    // split: a 1 KB run is 16 rows of 64 bytes of one plane (runs of the hi
+    // plane first, then the lo plane's, so the run's LDS place is the same
+    // formula); lane writes slot lane & 3 of row lane >> 2
+    constexpr int AR = BM / 16, BR = BN / 16;  // split: runs per plane
 #pragma unroll
     for (int j = 0; j < C::NA; j++) {
-        const int row = 8 * (wave * C::NA + j) + dma_row;
-        const int gm = min(m0 + row, p.M - 1);
-        a_cofs[j] = ((lane & 7) ^ swz(row)) << 4;
-        a_vo[j] = gm * (int)p.a_ld + a_cofs[j];
+        if constexpr (C::split) {
+            const int row = 16 * ((wave * C::NA + j) % AR) + (lane >> 2);
+            const int gm = min(m0 + row, p.M - 1);
+            a_cofs[j] = ((lane & 3) ^ swz64(row)) << 4;
+            a_vo[j] = gm * (int)p.a_ld + a_cofs[j];
+        } else {
+            const int row = 8 * (wave * C::NA + j) + dma_row;
+            const int gm = min(m0 + row, p.M - 1);
+            a_cofs[j] = ((lane & 7) ^ swz(row)) << 4;
+            a_vo[j] = gm * (int)p.a_ld + a_cofs[j];
+        }
     }
     const int a_kb = (int)p.a_kbytes, a_last = a_kb - 16;
 #pragma unroll
     for (int j = 0; j < C::NB; j++) {
-        const int col = 8 * (wave * C::NB + j) + dma_row;
-        b_vo[j] = (n0 + col) * (int)p.b_ld + (((lane & 7) ^ swz(col)) << 4);
+        if constexpr (C::split) {
+            const int col = 16 * ((wave * C::NB + j) % BR) + (lane >> 2);
+            b_vo[j] = (n0 + col) * (int)p.b_ld + (((lane & 3) ^ swz64(col)) << 4);
+        } else {
+            const int col = 8 * (wave * C::NB + j) + dma_row;
+            b_vo[j] = (n0 + col) * (int)p.b_ld + (((lane & 7) ^ swz(col)) << 4);
+        }
     }
     const uint8_t *s_src[C::NS > 0 ? C::NS : 1];
     int64_t s_step[C::NS > 0 ? C::NS : 1];
@@ -676,6 +722,22 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 3 : 256 / BM) void k_gemm(
     // stage s into ring buffer `buf`
     auto issue = [&](int s, int buf) {
         uint8_t *L = lds + buf * C::STAGE;
+        if constexpr (C::split) {
+            // 32 K (64 bytes) of each plane per stage; the plane is uniform per run
+            constexpr int SB = 64;
+#pragma unroll
+            for (int j = 0; j < C::NA; j++) {
+                const uint8_t *base = (wave * C::NA + j) < AR ? p.a : p.a_lo;
+                const int vo = (s + 1) * SB <= a_kb ? a_vo[j] + s * SB : min(a_vo[j] + s * SB, a_vo[j] - a_cofs[j] + a_last);
+                dma16_buf(base, p.a_rec, L + C::OFF_A + (wave * C::NA + j) * 1024, vo, 0);
+            }
+#pragma unroll
+            for (int j = 0; j < C::NB; j++) {
+                const uint8_t *base = (wave * C::NB + j) < BR ? p.b : p.b_lo;
+                dma16_buf(base, p.b_rec, L + C::OFF_B + (wave * C::NB + j) * 1024, b_vo[j], s * SB);
+            }
+            return;
+        }
         if ((s + 1) * ROWB <= a_kb) {
 #pragma unroll
             for (int j = 0; j < C::NA; j++)
@@ -718,6 +780,16 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 3 : 256 / BM) void k_gemm(
     int cofs[4];
 #pragma unroll
     for (int q = 0; q < 4; q++) cofs[q] = ((2 * q + lh) ^ xr) << 4;
+    if constexpr (C::split) {
+        // 64-byte rows; tile rows start at multiples of 32, so the swizzle of
+        // row base + lr is swz64(lr); K = 16 step ks reads chunk 2·ks + lh
+#pragma unroll
+        for (int i = 0; i < MT; i++) a_off[i] = C::OFF_A + (wm * (32 * MT) + 32 * i + lr) * 64;
+#pragma unroll
+        for (int n = 0; n < NT; n++) b_off[n] = C::OFF_B + (wn * (32 * NT) + 32 * n + lr) * 64;
+#pragma unroll
+        for (int q = 0; q < 2; q++) cofs[q] = ((2 * q + lh) ^ swz64(lr)) << 4;
+    }
 
     v16f acc[MT][NT], accm[MT][NT];
 #pragma unroll
@@ -815,6 +887,38 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 3 : 256 / BM) void k_gemm(
                     }
                 }
             }
+        } else if constexpr (C::split) {
+            // x·w = (xh + xl)(wh + wl) ≈ xh·wh + xh·wl + xl·wh: each product
+            // exact in fp32 (the dropped xl·wl is ~2^-22 relative)
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                v8h bh[NT], bl[NT], ah[MT], al[MT];
+#pragma unroll
+                for (int n = 0; n < NT; n++) {
+                    bh[n] = *(const v8h *)(L + b_off[n] + cofs[ks]);
+                    bl[n] = *(const v8h *)(L + b_off[n] + BN * 64 + cofs[ks]);
+                }
+#pragma unroll
+                for (int i = 0; i < MT; i++) {
+                    ah[i] = *(const v8h *)(L + a_off[i] + cofs[ks]);
+                    al[i] = *(const v8h *)(L + a_off[i] + BM * 64 + cofs[ks]);
+                }
+#pragma unroll
+                for (int i = 0; i < MT; i++)
+#pragma unroll
+                    for (int n = 0; n < NT; n++)
+                        acc[i][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bh[n], acc[i][n], 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < MT; i++)
+#pragma unroll
+                    for (int n = 0; n < NT; n++)
+                        acc[i][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bl[n], acc[i][n], 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < MT; i++)
+#pragma unroll
+                    for (int n = 0; n < NT; n++)
+                        acc[i][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bh[n], acc[i][n], 0, 0, 0);
+            }
         } else if constexpr (WK == WK_F16) {
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) {
@@ -882,7 +986,7 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 3 : 256 / BM) void k_gemm(
                 const int row = wm * (32 * MT) + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
                 float v = acc[i][n][r];
                 if constexpr (C::q41) v += accm[i][n][r];
-                Ct[row * CLD + wn * (32 * NT) + 32 * n + lr] = v * kScale;
+                Ct[row * CLD + wn * (32 * NT) + 32 * n + lr] = v * (C::split ? p.alpha : kScale);
             }
     __syncthreads();
 
@@ -1190,7 +1294,7 @@ hipError_t dispatch_waves(Epi epi, GemmParams &p, hipStream_t st) {
 // stages.
 int splitk_of(const Weight &w, int64_t M) {
     const int esize = (w.kind == WK_F16) ? 2 : (w.kind == WK_F32 ? 4 : 1);
-    const int64_t ns = w.Kp * esize / 128, tiles = (M + 63) / 64 * (w.Np / BN);
+    const int64_t ns = w.kind == WK_F16X3 ? w.Kp / 32 : w.Kp * esize / 128, tiles = (M + 63) / 64 * (w.Np / BN);
     if (tiles >= 256 || ns < 8 || w.N % 4 != 0) return 1;
     int64_t ks = std::min<int64_t>((512 + tiles - 1) / tiles, ns / 4);
     const int64_t per = (ns + ks - 1) / ks;
@@ -1208,8 +1312,15 @@ hipError_t launch_gemm(const Weight &w, const Act &a, int64_t M, Epi epi, const 
                        hipStream_t st) {
     if (M <= 0) return hipSuccess;
     GemmParams p{};
-    const int esize = (w.kind == WK_F16) ? 2 : (w.kind == WK_F32 ? 4 : 1);
+    const bool split = w.kind == WK_F16X3;
+    // split: fp16 hi / lo planes of the same row layout on both sides, rows
+    // whole 16-byte chunks
+    if (split && (a.kind != A_F16X2 || !a.lo || !w.lo || w.Kp % 64 != 0 || w.K % 8 != 0)) return hipErrorInvalidValue;
+    const int esize = (w.kind == WK_F16 || split) ? 2 : (w.kind == WK_F32 ? 4 : 1);
     p.a = (const uint8_t *)a.x;
+    p.a_lo = (const uint8_t *)a.lo;
+    p.b_lo = (const uint8_t *)w.lo;
+    p.alpha = w.alpha;
     p.a_d = (const uint8_t *)a.d;
     p.a_s = (const uint8_t *)a.s;
     p.a_ld = a.ld * esize;
@@ -1234,7 +1345,7 @@ hipError_t launch_gemm(const Weight &w, const Act &a, int64_t M, Epi epi, const 
             p.part = ea.ws;
         }
     }
-    p.nstages = (int)(w.Kp / stage_k(w.kind));
+    p.nstages = (int)(w.Kp / (split ? 32 : stage_k(w.kind)));
     p.tiles_n = (int)(w.Np / BN);
     p.e = ea;
     if (epi == EPI_HQKV) {
@@ -1245,6 +1356,9 @@ hipError_t launch_gemm(const Weight &w, const Act &a, int64_t M, Epi epi, const 
             (ea.qpool ? (!ea.y || ea.ldy < ea.E) : !ea.q))
             return hipErrorInvalidValue;
     }
+    if (epi == EPI_GELU && ea.out.kind == A_F16X2 &&
+        (!ea.out.lo || ea.out.ld % 8 != 0 || (uintptr_t)ea.out.x % 16 != 0 || (uintptr_t)ea.out.lo % 16 != 0))
+        return hipErrorInvalidValue;  // whole 16-byte stores of both planes
     if (epi == EPI_DECONV) {
         // fp16 kernels on fp16 rows, four taps of Cout columns, whole input rows
         const Act &o = ea.out;
@@ -1293,6 +1407,7 @@ hipError_t launch_gemm(const Weight &w, const Act &a, int64_t M, Epi epi, const 
         case WK_Q8_0: e = dispatch_waves<WK_Q8_0>(epi, p, st); break;
         case WK_F16: e = dispatch_waves<WK_F16>(epi, p, st); break;
         case WK_F32: e = dispatch_waves<WK_F32>(epi, p, st); break;
+        case WK_F16X3: e = dispatch_waves<WK_F16X3>(epi, p, st); break;
         default: return hipErrorInvalidValue;
     }
     if (e == hipSuccess && p.ksplit > 1) {

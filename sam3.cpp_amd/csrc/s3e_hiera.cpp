@@ -380,8 +380,11 @@ int hiera_load(int device, std::ifstream &fin, int ftype, int32_t n_tensors, Hie
             if (dot == std::string::npos || bi < 0 || bi >= (int)m->blocks.size()) { set_error("tensor '%s' has a bad block index", name.c_str()); return S3E_ERR_IO; }
             HBlock &b = m->blocks[(size_t)bi];
             const std::string f = name.substr(dot + 1);
+            // F32 linears (the first stage's, whose width is no Q8 block
+            // multiple) run as split fp16 pairs on the fp16 MFMA
             auto lin = [&](Weight &w, int64_t K, int64_t N) {
                 if (t.ne[0] != K || t.ne[1] != N) { set_error("'%s': expected [%lld, %lld]", name.c_str(), (long long)K, (long long)N); return (int)S3E_ERR_IO; }
+                if (t.type == 0 && K % 8 == 0) return upload_weight_split((const float *)t.data.data(), K, N, w, GEMM_BN);
                 return upload_weight(0, t.type, K, N, t.data.data(), t.data.size(), w);
             };
             if (f == "norm1.weight") rc = upload_f32(m.get(), t, b.din, &b.n1w);
