@@ -13,7 +13,7 @@ namespace {
 // type), K ordered [c][ky][kx] as the kernel rows are; taps outside the image
 // and columns K..ldk are zero.
 __global__ void k_im2col_conv(const float *__restrict__ chw, int S, int k, int stride, int pad, int OW, int64_t T,
-                              int64_t ldk, int kind, void *out) {
+                              int64_t ldk, int kind, void *out, _Float16 *lo) {
     // 32-bit index arithmetic (the launcher keeps T·ldk below 2^31)
     const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (uint32_t)(T * ldk)) return;
@@ -26,8 +26,13 @@ __global__ void k_im2col_conv(const float *__restrict__ chw, int S, int k, int s
         const int iy = oy * stride + ky - pad, ix = ox * stride + kx - pad;
         if (iy >= 0 && iy < S && ix >= 0 && ix < S) val = chw[(int64_t)c * S * S + (int64_t)iy * S + ix];
     }
-    if (kind == A_F16) ((_Float16 *)out)[idx] = to_half(val);
-    else ((float *)out)[idx] = val;
+    if (kind == A_F16 || kind == A_F16X2) {
+        const _Float16 h = to_half(val);
+        ((_Float16 *)out)[idx] = h;
+        if (kind == A_F16X2) lo[idx] = (_Float16)(val - (float)h);  // fp16 of the exact difference
+    } else {
+        ((float *)out)[idx] = val;
+    }
 }
 
 // Attention operands of one Hiera block from the QKV GEMM output (f32
@@ -162,13 +167,14 @@ __global__ void k_upsample_add(float *__restrict__ dst, const float *__restrict_
 }  // namespace
 
 hipError_t launch_im2col_conv(const float *chw, int S, int k, int stride, int pad, int64_t ldk, AKind kind,
-                              void *out, hipStream_t st) {
+                              void *out, hipStream_t st, void *lo) {
     const int O = (S + 2 * pad - k) / stride + 1;
-    if ((kind != A_F16 && kind != A_F32) || ldk < 3LL * k * k) return hipErrorInvalidValue;
+    if ((kind != A_F16 && kind != A_F32 && kind != A_F16X2) || (kind == A_F16X2 && !lo) || ldk < 3LL * k * k)
+        return hipErrorInvalidValue;
     const int64_t T = (int64_t)O * O, total = T * ldk;
     if (total >= INT32_MAX) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_im2col_conv, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, chw, S, k, stride,
-                       pad, O, T, ldk, (int)kind, out);
+                       pad, O, T, ldk, (int)kind, out, (_Float16 *)lo);
     return hipGetLastError();
 }
 

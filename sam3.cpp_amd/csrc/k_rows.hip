@@ -395,7 +395,7 @@ __global__ __launch_bounds__(256) void k_rows_quant(const float *__restrict__ x,
 // im2col for ggml_conv_2d_sk_p0 with a P×P kernel and stride P on a CHW image:
 // row t = py*G + px, column k = (c*P + ky)*P + kx, zero for k >= 3·P².
 __global__ void k_im2col(const float *__restrict__ chw, int img, int P, int64_t ldk, int kind,
-                         void *out) {
+                         void *out, _Float16 *lo) {
     // 32-bit index arithmetic (the launcher keeps G²·ldk below 2^31)
     const int G = img / P;
     const uint32_t T = (uint32_t)(G * G);
@@ -409,8 +409,13 @@ __global__ void k_im2col(const float *__restrict__ chw, int img, int P, int64_t 
         const int py = (int)(t / (uint32_t)G), px = (int)(t - (uint32_t)py * G);
         val = chw[(int64_t)c * img * img + (int64_t)(py * P + ky) * img + px * P + kx];
     }
-    if (kind == A_F16) ((_Float16 *)out)[idx] = to_half(val);
-    else ((float *)out)[idx] = val;
+    if (kind == A_F16 || kind == A_F16X2) {
+        const _Float16 h = to_half(val);
+        ((_Float16 *)out)[idx] = h;
+        if (kind == A_F16X2) lo[idx] = (_Float16)(val - (float)h);  // fp16 of the exact difference
+    } else {
+        ((float *)out)[idx] = val;
+    }
 }
 
 // f32 strided Q/K/V (head dim D) → fp16 [BH][N][hdp] for Q and K,
@@ -565,12 +570,13 @@ hipError_t launch_rows_quant(AKind kind, const float *x, int64_t M, int64_t K, c
 }
 
 hipError_t launch_im2col(const float *chw, int img, int P, int64_t ldk, AKind kind, void *out,
-                         hipStream_t st) {
+                         hipStream_t st, void *lo) {
+    if (kind == A_F16X2 && !lo) return hipErrorInvalidValue;
     const int G = img / P;
     const int64_t total = (int64_t)G * G * ldk;
     if (total >= INT32_MAX) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_im2col, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, chw, img, P,
-                       ldk, (int)kind, out);
+                       ldk, (int)kind, out, (_Float16 *)lo);
     return hipGetLastError();
 }
 

@@ -360,7 +360,9 @@ int hiera_load(int device, std::ifstream &fin, int ftype, int32_t n_tensors, Hie
             for (int64_t n = 0; n < m->E0; n++)
                 std::memcpy(&padded[(size_t)(n * Kp * es)], &t.data[(size_t)(n * K * es)], (size_t)(K * es));
             m->patch_k = Kp;
-            rc = upload_weight(0, t.type, Kp, m->E0, padded.data(), padded.size(), m->patch);
+            // an F32 kernel runs as split fp16 pairs on the fp16 MFMA
+            if (t.type == 0) rc = upload_weight_split((const float *)padded.data(), Kp, m->E0, m->patch, GEMM_BN);
+            else rc = upload_weight(0, t.type, Kp, m->E0, padded.data(), padded.size(), m->patch);
             m->found_misc++;
         } else if (name == "hiera.patch_embed.bias") {
             rc = upload_f32(m.get(), t, m->E0, &m->patch_b);
@@ -710,8 +712,9 @@ hipError_t hiera_block(const HieraModel *m, HieraState *s, int bi, const float *
 hipError_t hiera_encode(const HieraModel *m, HieraState *s, const float *chw, hipStream_t st) {
     const int G = s->G;
     // patch embedding 7×7 / 4 / 3 + bias + positional embedding
-    const AKind pk = m->patch.kind == WK_F16 ? A_F16 : A_F32;
-    hipError_t e = launch_im2col_conv(chw, s->img, 7, 4, 3, m->patch_k, pk, s->col.x, st);
+    const AKind pk = act_kind_for(m->patch.kind);
+    const Act col = s->col.as(pk, m->patch_k);
+    hipError_t e = launch_im2col_conv(chw, s->img, 7, 4, 3, m->patch_k, pk, col.x, st, col.lo);
     if (e != hipSuccess) return e;
     EpiArgs ea;
     ea.bias = m->patch_b;
@@ -720,7 +723,7 @@ hipError_t hiera_encode(const HieraModel *m, HieraState *s, const float *chw, hi
     ea.pos = s->pos;
     ea.pos_grid = G;
     ea.grid = G;
-    if ((e = launch_gemm(m->patch, s->col.as(pk, m->patch_k), (int64_t)G * G, EPI_POS, ea, st)) != hipSuccess) return e;
+    if ((e = launch_gemm(m->patch, col, (int64_t)G * G, EPI_POS, ea, st)) != hipSuccess) return e;
     // blocks: a stage's first block writes the stage's own buffer
     int H = G, W = G;
     float *x = s->xs[0];

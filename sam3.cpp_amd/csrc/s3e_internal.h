@@ -344,8 +344,9 @@ hipError_t launch_attn_prep16(const _Float16 *q, const int64_t q_nb[4], const _F
 hipError_t launch_probe_stream(int mode, void *dst, const void *src, size_t bytes, uint32_t *sink, int blocks,
                                hipStream_t st);
 hipError_t launch_probe_mfma(int kind, int64_t iters, int blocks, uint32_t *sink, hipStream_t st);
+// Rows of ldk per patch (A_F32, A_F16, or A_F16X2 with the lo plane at lo).
 hipError_t launch_im2col(const float *chw, int img, int P, int64_t ldk, AKind kind, void *out,
-                         hipStream_t st);
+                         hipStream_t st, void *lo = nullptr);
 hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t st);
 // y = a + b·s elementwise (n floats; y may alias a)
 hipError_t launch_add_scaled(float *y, const float *a, const float *b, float s, int64_t n, hipStream_t st);
@@ -371,7 +372,7 @@ hipError_t launch_add_pos(const float *x, const float *pos, float *y, int G, int
 // ---- Hiera (k_hiera.hip) ----
 // Patch-embedding im2col: CHW f32 [3][S][S], k×k / stride / pad → rows of ldk.
 hipError_t launch_im2col_conv(const float *chw, int S, int k, int stride, int pad, int64_t ldk, AKind kind,
-                              void *out, hipStream_t st);
+                              void *out, hipStream_t st, void *lo = nullptr);
 // Attention operands of a Hiera block from its QKV GEMM output (window
 // partition with bias-valued padding, Q max-pool, head split, zero-padded
 // head dim, fp16 hi/lo).

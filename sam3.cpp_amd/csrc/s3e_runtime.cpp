@@ -991,6 +991,9 @@ struct s3e_model {
     int32_t img = 0, patch = 0, E = 0, depth = 0, heads = 0, mlp = 0, window = 0, n_global = 0, gidx[4] = {0, 0, 0, 0};
     int grid = 0, pos_grid = 0;
     Weight patch_w;  // K = 3·P², N = E
+    // an F32 patch kernel again as split fp16 pairs (K padded like patch_w),
+    // the form the encoder's patch GEMM runs; patch_w serves the readers
+    Weight patch_split;
     float *pos = nullptr, *ln_pre_w = nullptr, *ln_pre_b = nullptr;
     std::vector<Block> blocks;
     Neck necks[2];              // 0 = "neck.det.", 1 = "neck.trk."
@@ -1196,6 +1199,7 @@ extern "C" void s3e_model_free(s3e_model *m) {
     if (m->hiera) hiera_free(m->hiera);
     if (m->ma) memattn_free(m->ma);
     free_weight(m->patch_w);
+    free_weight(m->patch_split);
     for (auto &nk : m->necks)
         for (auto &sc : nk.s) {
             free_weight(sc.dc[0]);
@@ -1340,6 +1344,8 @@ extern "C" int s3e_model_load(s3e_ctx *ctx, const char *path, s3e_model **out) t
             std::vector<uint8_t> padded((size_t)(E * Kp * es), 0);
             for (int64_t n = 0; n < E; n++) std::memcpy(&padded[(size_t)(n * Kp * es)], &t.data[(size_t)(n * K * es)], (size_t)(K * es));
             rc = upload_weight(ctx->device, t.type, Kp, E, padded.data(), padded.size(), m->patch_w);
+            if (rc == S3E_OK && t.type == 0)
+                rc = upload_weight_split((const float *)padded.data(), Kp, E, m->patch_split, GEMM_BN);
         } else if (name == "vit.pos_embed") {
             m->pos_grid = (int)t.ne[1];
             if (t.ne[0] != E || t.ne[1] != t.ne[2] || m->pos_grid <= 0) { set_error("pos_embed shape mismatch"); return S3E_ERR_IO; }
@@ -1635,20 +1641,28 @@ extern "C" int s3e_state_create_sized(s3e_ctx *ctx, const s3e_model *m, int img_
 
 namespace {
 
+// The patch embedding's im2col and GEMM into y with epilogue epi (EPI_POS
+// or EPI_F32): an F32 kernel runs as split fp16 pairs on the fp16 MFMA.
+hipError_t patch_gemm(s3e_state *st, const float *chw, Epi epi, const EpiArgs &ea, hipStream_t s) {
+    const s3e_model *m = st->m;
+    const Weight &w = m->patch_split.q ? m->patch_split : m->patch_w;
+    const int64_t ldk = m->patch_w.K;  // 3·P² padded to 32
+    const Act col = st->col.as(act_kind_for(w.kind), ldk);
+    hipError_t e = launch_im2col(chw, m->img, m->patch, ldk, col.kind, col.x, s, col.lo);
+    if (e == hipSuccess) e = launch_gemm(w, col, st->T, epi, ea, s);
+    return e;
+}
+
 hipError_t run_prefix(s3e_state *st, const float *chw, float *x) {
     const s3e_model *m = st->m;
     hipStream_t s = st->ctx->stream;
-    const AKind pk = (m->patch_w.kind == WK_F16) ? A_F16 : A_F32;
-    const int64_t ldk = m->patch_w.K;  // 3·P² padded to 32
-    hipError_t e = launch_im2col(chw, m->img, m->patch, ldk, pk, st->col.x, s);
-    if (e != hipSuccess) return e;
     EpiArgs ea;
     ea.y = x;
     ea.ldy = m->E;
     ea.pos = m->pos;
     ea.pos_grid = m->pos_grid;
     ea.grid = m->grid;
-    e = launch_gemm(m->patch_w, st->col.as(pk, ldk), st->T, EPI_POS, ea, s);
+    hipError_t e = patch_gemm(st, chw, EPI_POS, ea, s);
     if (e != hipSuccess) return e;
     Act none;
     return launch_layernorm(x, st->T, m->E, 1e-5f, m->ln_pre_w, m->ln_pre_b, none, x, s);
@@ -2279,11 +2293,10 @@ extern "C" int s3e_vit_prefix_stage(s3e_state *st, int stage, const float *in_de
     const int64_t ldk = m->patch_w.K;  // 3·P² padded to 32
     switch (stage) {
         case PS_PATCH_EMBED: {
-            HIP_TRY(launch_im2col(in_device, m->img, m->patch, ldk, pk, st->col.x, s));
             EpiArgs ea;
             ea.y = out_device;
             ea.ldy = E;
-            HIP_TRY(launch_gemm(m->patch_w, st->col.as(pk, ldk), T, EPI_F32, ea, s));
+            HIP_TRY(patch_gemm(st, in_device, EPI_F32, ea, s));
         } break;
         case PS_PATCH_IM2COL:
             HIP_TRY(launch_im2col(in_device, m->img, m->patch, ldk, pk, st->col.x, s));
