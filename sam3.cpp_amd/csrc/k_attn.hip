@@ -581,6 +581,18 @@ __global__ __launch_bounds__(NTHR, HD == 64 ? 3 : (HD == 128 ? 2 : 1)) void k_at
                     const uint32_t w0 = (uint32_t)f2h_bits(o[dt][4 * g]) | ((uint32_t)f2h_bits(o[dt][4 * g + 1]) << 16);
                     const uint32_t w1 = (uint32_t)f2h_bits(o[dt][4 * g + 2]) | ((uint32_t)f2h_bits(o[dt][4 * g + 3]) << 16);
                     *(uint2 *)((_Float16 *)out.x + orow * out.ld + col) = make_uint2(w0, w1);
+                    if (out.kind == A_F16X2) {
+                        // the pair's low half: fp16 of the exact difference
+                        uint32_t l[4];
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            const float v = o[dt][4 * g + i];
+                            const _Float16 hv = __builtin_bit_cast(_Float16, (uint16_t)f2h_bits(v));
+                            l[i] = __builtin_bit_cast(uint16_t, (_Float16)(v - (float)hv));
+                        }
+                        *(uint2 *)((_Float16 *)out.lo + orow * out.ld + col) =
+                            make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
+                    }
                 }
             }
         }
@@ -653,6 +665,7 @@ hipError_t launch_attn(const AttnArgs &a, hipStream_t st) {
         return hipErrorInvalidValue;
     if ((a.out.kind == A_Q8_0 || a.out.kind == A_Q8_1) && a.hd_out > 0 && a.hd_out % 32 != 0)
         return hipErrorInvalidValue;
+    if (a.out.kind == A_F16X2 && (!a.out.lo || a.out.ld % 4 != 0)) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((a.Nq + QT - 1) / QT), (unsigned)a.BH, (unsigned)a.nsplit);
     const bool crop = a.wo > 0 || (a.hd_out > 0 && a.hd_out != hd);
     if (a.v) {

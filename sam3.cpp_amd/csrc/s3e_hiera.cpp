@@ -677,9 +677,9 @@ hipError_t hiera_block(const HieraModel *m, HieraState *s, int bi, const float *
         aa.part_o = s->part;
         aa.part_ml = s->part + po;
     }
-    // a Q8 block must lie inside one head; split pairs go through f32, as
-    // does a key-split attention into a Q8 format
-    const bool direct = kp != A_F16X2 && (!q8 || HD % 32 == 0) && (ns == 1 || kp == A_F16);
+    // a Q8 block must lie inside one head; a key-split attention into a Q8
+    // format or fp16 pairs goes through f32
+    const bool direct = (!q8 || HD % 32 == 0) && (ns == 1 || kp == A_F16);
     const Act a_proj = s->a1.as(kp, C);
     aa.out = direct ? a_proj : f32_act(s->attn_f32, C);
     if ((e = launch_attn(aa, st)) != hipSuccess) return e;
