@@ -535,6 +535,15 @@ def cpu_baseline(path: str, img: np.ndarray, threads: int):
 
 
 def _short_kernel(name: str) -> str:
+    if name.startswith("_Z"):
+        # Left mangled by the profiler (it does not demangle _Float16
+        # parameters): take the length-prefixed source name k_....
+        for m in re.finditer(r"(\d+)(?=k_)", name):
+            digits, at = m.group(1), m.end()
+            for i in range(len(digits)):
+                n = int(digits[i:])
+                if name[at + n:at + n + 1] in ("E", "I"):
+                    return name[at:at + n]
     m = re.search(r"(k_\w+(<[^>]*>)?)", name)
     return m.group(1) if m else name.split("(")[0][:60]
 
@@ -544,10 +553,10 @@ def summarize_stats(stats_csv: str, frames: int) -> str:
     import csv
 
     rows = list(csv.DictReader(open(stats_csv)))
-    lines = [f"{'kernel':28s} {'calls':>7s} {'avg_us':>9s} {'ms/frame':>9s} {'share':>7s}"]
+    lines = [f"{'kernel':34s} {'calls':>7s} {'avg_us':>9s} {'ms/frame':>9s} {'share':>7s}"]
     for r in rows:
         tot = float(r["TotalDurationNs"]) / 1e6
-        lines.append(f"{_short_kernel(r['Name']):28s} {int(r['Calls']):7d} {float(r['AverageNs']) / 1e3:9.1f} "
+        lines.append(f"{_short_kernel(r['Name']):34s} {int(r['Calls']):7d} {float(r['AverageNs']) / 1e3:9.1f} "
                      f"{tot / frames:9.3f} {float(r['Percentage']):6.2f}%")
     return "\n".join(lines)
 
@@ -568,9 +577,9 @@ def summarize_trace(trace_csv: str, marker: str, first: int, last: int, frames: 
         if first <= seen < last:
             agg[k].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
     tot = sum(sum(v) for v in agg.values())
-    lines = [f"{'kernel':28s} {'calls':>7s} {'avg_us':>9s} {'ms/frame':>9s} {'share':>7s}"]
+    lines = [f"{'kernel':34s} {'calls':>7s} {'avg_us':>9s} {'ms/frame':>9s} {'share':>7s}"]
     for k, v in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
-        lines.append(f"{k:28s} {len(v):7d} {sum(v) / len(v):9.1f} {sum(v) / 1e3 / frames:9.3f} "
+        lines.append(f"{k:34s} {len(v):7d} {sum(v) / len(v):9.1f} {sum(v) / 1e3 / frames:9.3f} "
                      f"{100 * sum(v) / tot:6.2f}%")
     return "\n".join(lines)
 
@@ -586,9 +595,9 @@ def summarize_grids(trace_csv: str, frames: int) -> str:
     for r in csv.DictReader(open(trace_csv)):
         key = (_short_kernel(r["Kernel_Name"]), f"{r['Grid_Size_X']}x{r['Grid_Size_Y']}x{r['Grid_Size_Z']}")
         agg[key].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
-    lines = [f"{'kernel':28s} {'grid (threads)':>18s} {'calls':>6s} {'avg_us':>9s} {'ms/frame':>9s}"]
+    lines = [f"{'kernel':34s} {'grid (threads)':>18s} {'calls':>6s} {'avg_us':>9s} {'ms/frame':>9s}"]
     for (k, g), v in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
-        lines.append(f"{k:28s} {g:>18s} {len(v):6d} {sum(v) / len(v):9.1f} {sum(v) / 1e3 / frames:9.3f}")
+        lines.append(f"{k:34s} {g:>18s} {len(v):6d} {sum(v) / len(v):9.1f} {sum(v) / 1e3 / frames:9.3f}")
     return "\n".join(lines)
 
 

@@ -163,11 +163,12 @@ def test_mul_mat_ragged_shapes(ctx, wt, M, N, K):
     assert err <= 1e-5
 
 
-@pytest.mark.parametrize("M,N,K", [(100, 384, 1024), (777, 1024, 4736), (5184, 4736, 1024)])
+@pytest.mark.parametrize("M,N,K", [(100, 384, 1024), (777, 1024, 4736), (5184, 4736, 1024), (2000, 4096, 256)])
 def test_mul_mat_q_f6(ctx, M, N, K):
     """Q4_0 products on the fp6 kernel (activations as S3E_TYPE_Q8_0_F6X2)
     equal the int8 kernel's bit for bit (the same exact block sums, the same
-    scale products and FMA order), and the oracle to fp32 order noise."""
+    scale products and FMA order), and the oracle to fp32 order noise
+    (2000 rows end inside a 64-row unit of the fp6 activation layout)."""
     import s3e
 
     rng = np.random.default_rng(M + N + K)
