@@ -134,13 +134,13 @@ def test_mem_attn_vs_torch(model):
     assert rl <= (1e-5 if ft == "f32" else 2e-2)
 
 
+@pytest.mark.parametrize("model", ["f32"], indirect=True)
 def test_pointer_tokens_skip_rope(model):
     """A plant on the CPU: rotating the pointer keys as well must change the
     result (the excluded tail is observable), and leaving every key
-    unrotated must too (the spatial keys are rotated)."""
+    unrotated must too (the spatial keys are rotated).  A structure check,
+    on the F32 file only."""
     ft, h, tensors = model
-    if ft != "f32":
-        pytest.skip("structure check on the F32 file")
     L, D, MD, FFN = orc.mem_attn_dims(h)
     curr, src_pos, prompt, prompt_pos, rope_q, rope_k = make_inputs(D, MD)
     base = orc.mem_attn(h, curr, src_pos, prompt, prompt_pos, N_PTR, rope_q, rope_k)
@@ -157,10 +157,9 @@ def test_pointer_tokens_skip_rope(model):
     assert orc.rel_l2(alt2, base) > 1e-4
 
 
+@pytest.mark.parametrize("model", ["f32"], indirect=True)
 def test_no_pointer_tokens(model):
     ft, h, tensors = model
-    if ft != "f32":
-        pytest.skip("structure check on the F32 file")
     L, D, MD, FFN = orc.mem_attn_dims(h)
     curr, src_pos, prompt, prompt_pos, rope_q, rope_k = make_inputs(D, MD, n_ptr=0)
     got = orc.mem_attn(h, curr, src_pos, prompt, prompt_pos, 0, rope_q, rope_k)
