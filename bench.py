@@ -152,6 +152,46 @@ def gemm_roofline(s3e, ctx, ev, ftype: str, reps: int):
     return ms, tops, ops
 
 
+def vendor_gemms(reps: int = 50) -> dict:
+    """A yardstick, not the engine: the ViT's GEMM shapes on the vendor
+    library through torch (hipBLASLt), fp16 × fp16 (F.linear, weight [N][K])
+    and plain int8 × int8 → int32 (torch._int_mm: no per-block scales, so
+    less work than a Q4_0 × Q8_0 product), µs per call over `reps` calls."""
+    import torch
+    import torch.nn.functional as F
+
+    dev = "cuda:0"
+    res = {}
+
+    def timeit(f):
+        for _ in range(5):
+            f()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            f()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e3
+
+    g = torch.Generator(device=dev).manual_seed(0)
+    for name, M, N, K in (("fc1", 5184, 4736, 1024), ("qkv", 5184, 3072, 1024), ("fc2", 5184, 1024, 4736),
+                          ("proj", 5184, 1024, 1024)):
+        a = torch.randn(M, K, device=dev, dtype=torch.float16, generator=g)
+        w = torch.randn(N, K, device=dev, dtype=torch.float16, generator=g)
+        ai = torch.randint(-127, 128, (M, K), device=dev, dtype=torch.int8, generator=g)
+        wi = torch.randint(-8, 8, (N, K), device=dev, dtype=torch.int8, generator=g)
+        ops = 2.0 * M * N * K
+        us16 = timeit(lambda: F.linear(a, w))
+        us8 = timeit(lambda: torch._int_mm(ai, wi.t()))
+        res[name] = {"M": M, "N": N, "K": K, "fp16_us": round(us16, 1), "fp16_TFLOPs": round(ops / us16 / 1e6, 1),
+                     "int8_us": round(us8, 1), "int8_TOPS": round(ops / us8 / 1e6, 1)}
+        log(f"vendor {name} M={M} N={N} K={K}: fp16 {us16:.1f} us ({ops / us16 / 1e6:.0f} TFLOP/s), "
+            f"int8 {us8:.1f} us ({ops / us8 / 1e6:.0f} TOPS)")
+    return res
+
+
 BPW = {"q4_0": 18 / 32, "q4_1": 20 / 32, "q8_0": 34 / 32, "f16": 2.0}
 VIT_LINEARS = [(3072, 1024), (1024, 1024), (4736, 1024), (1024, 4736)]  # qkv, proj, fc1, fc2 (N, K)
 
@@ -693,7 +733,7 @@ def main() -> int:
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "gemm_fc1_q4_0_counters.txt"))
     ap.add_argument("--only", choices=["encode", "gemm", "copy", "neck", "preprocess", "sam2", "small_m", "c4",
-                                       "attn", "peaks"], default=None,
+                                       "attn", "peaks", "vendor"], default=None,
                     help="run one leg only (for profiling runs)")
     ap.add_argument("--sam2-run", default=None, help="with --only sam2: one encoder, e.g. hiera_t:f16")
     args = ap.parse_args()
@@ -728,6 +768,15 @@ def main() -> int:
 
     if args.only == "peaks":
         measured_peaks(s3e, ctx, ev)
+        return 0
+
+    if args.only == "vendor":
+        # the vendor library's fp16 and plain int8 GEMMs, then this engine's fc1
+        # for each weight type, on the same box
+        vendor_gemms()
+        for ft in ("q4_0", "q8_0", "f16"):
+            ms, tops, _ = gemm_roofline(s3e, ctx, ev, ft, args.gemm_reps)
+            log(f"fc1 GEMM {ft}: {ms * 1e3:.1f} us/launch, {tops:.1f} TOPS")
         return 0
 
     if args.only == "c4":
