@@ -104,11 +104,11 @@ def read_traffic(path: str):
     return None
 
 
-def gemm_roofline(s3e, ctx, ev, ftype: str, reps: int):
-    """Time the fc1 GEMM kernel alone on pre-converted activations: for Q4_0
-    the fp6 kernel the encoder runs (s3e_mul_mat_q_f6 on S3E_TYPE_Q8_0_F6X2),
-    otherwise s3e_mul_mat_q."""
-    M, N, K = 5184, 4736, 1024
+def gemm_roofline(s3e, ctx, ev, ftype: str, reps: int, shape=(5184, 4736, 1024)):
+    """Time one GEMM kernel alone (default: fc1) on pre-converted activations:
+    for Q4_0 the fp6 kernel the encoder runs (s3e_mul_mat_q_f6 on
+    S3E_TYPE_Q8_0_F6X2), otherwise s3e_mul_mat_q."""
+    M, N, K = shape
     rng = np.random.default_rng(1)
     tmap = {"q4_0": s3e.TYPE_Q4_0, "q4_1": s3e.TYPE_Q4_1, "q8_0": s3e.TYPE_Q8_0, "f16": s3e.TYPE_F16,
             "f32": s3e.TYPE_F32}
@@ -774,9 +774,11 @@ def main() -> int:
         # the vendor library's fp16 and plain int8 GEMMs, then this engine's fc1
         # for each weight type, on the same box
         vendor_gemms()
-        for ft in ("q4_0", "q8_0", "f16"):
-            ms, tops, _ = gemm_roofline(s3e, ctx, ev, ft, args.gemm_reps)
-            log(f"fc1 GEMM {ft}: {ms * 1e3:.1f} us/launch, {tops:.1f} TOPS")
+        for name, shape in (("fc1", (5184, 4736, 1024)), ("qkv", (5184, 3072, 1024)), ("fc2", (5184, 1024, 4736)),
+                            ("proj", (5184, 1024, 1024))):
+            for ft in ("q4_0", "q8_0", "f16"):
+                ms, tops, _ = gemm_roofline(s3e, ctx, ev, ft, args.gemm_reps, shape)
+                log(f"{name} GEMM {ft}: {ms * 1e3:.1f} us/launch, {tops:.1f} TOPS")
         return 0
 
     if args.only == "c4":
