@@ -242,12 +242,12 @@ def test_mul_mat_small_m(ctx, wt, N, K):
 def test_mul_mat_small_m_split_repeats(ctx, wt):
     """Lone small-M products whose K range is split across work-groups (few
     32-column strips, long K: the fc2 shape has 32 strips over 37 stages of
-    128) give the same bits on every call, also with products of other
-    widths in between (each launch leaves its arrival counters at zero for
-    the next), and match the oracle."""
+    128; 96 × 2048 and 96 × 1024 split into 4 and 2 ranges) give the same
+    bits on every call, also with products of other widths in between, and
+    match the oracle."""
     rng = np.random.default_rng(wt + 11)
     cases = []
-    for N, K, M in [(1024, 4736, 64), (4736, 1024, 7), (96, 2048, 33), (1024, 4736, 1)]:
+    for N, K, M in [(1024, 4736, 64), (4736, 1024, 7), (96, 2048, 33), (1024, 4736, 1), (96, 1024, 33)]:
         W = rng.normal(0, 0.02, (N, K)).astype(np.float32)
         wb = orc.to_weight_bytes(wt, W)
         X = rng.standard_normal((M, K)).astype(np.float32)
