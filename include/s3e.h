@@ -104,7 +104,8 @@ int s3e_weight_info(const s3e_weight *w, int64_t out[4]);
  * Replaces ggml_mul_mat + ggml_add at sam3.cpp:3738-3739, 3779-3780,
  * 3792-3796.  Above 64 rows the converted X (M rows of K bytes for Q8, 2·K
  * for F16, 4·K for F32, padded to 128-byte stages) and the repacked W must
- * each stay below 2 GiB; larger products return S3E_ERR_HIP. */
+ * each stay below 2 GiB; larger products return S3E_ERR_HIP.  M = 0 (an
+ * empty batch) succeeds and writes nothing; M < 0 is S3E_ERR_INVALID. */
 int s3e_mul_mat(s3e_ctx *ctx, const s3e_weight *w, const float *X, int64_t M,
                 const float *bias, float *Y);
 
@@ -174,7 +175,9 @@ int s3e_mul_mat_q_batch(s3e_ctx *ctx, int n, const s3e_weight *const *w, const v
  * tile t, stage g (128 columns), block b < 4 of the stage, part p (0 h, 1 l)
  * and word w < 3, the 64 rows' 8-byte words of the 192-bit E3M2 strings
  * (code j of the block in bits [6j, 6j + 6)), as word
- * ((((t·G + g)·4 + b)·2 + p)·3 + w)·64 + row % 64. */
+ * ((((t·G + g)·4 + b)·2 + p)·3 + w)·64 + row % 64.
+ * M = 0 (an empty batch) succeeds and writes nothing; M < 0 is
+ * S3E_ERR_INVALID. */
 int s3e_quantize_rows(s3e_ctx *ctx, int type, const float *X, int64_t M, int64_t K,
                       void *qs, uint16_t *d, uint16_t *s);
 

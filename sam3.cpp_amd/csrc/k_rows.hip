@@ -563,6 +563,7 @@ hipError_t launch_rows_quant(AKind kind, const float *x, int64_t M, int64_t K, c
     const bool q8 = out.kind == A_Q8_0 || out.kind == A_Q8_1;
     if ((q8 && K % 32 != 0) || K % 4 != 0 || (out.kind == A_F6 && (K % 128 != 0 || out.ld != K)))
         return hipErrorInvalidValue;
+    if (M <= 0) return hipSuccess;  // no rows: a launch would have an empty grid
     const int64_t nf4 = (K + 127) / 128 * 32;  // float4 up to the 128-element group
     const dim3 grid((unsigned)((nf4 + 63) / 64), (unsigned)((M + 3) / 4));
     hipLaunchKernelGGL(k_rows_quant, grid, dim3(256), 0, st, x, M, K, out);

@@ -535,7 +535,8 @@ extern "C" int s3e_weight_info(const s3e_weight *w, int64_t out[4]) try {
 extern "C" int s3e_quantize_rows(s3e_ctx *ctx, int type, const float *X, int64_t M, int64_t K, void *qs,
                                  uint16_t *d, uint16_t *s) try {
     if (!ctx || !X || !qs) { set_error("s3e_quantize_rows: NULL argument"); return S3E_ERR_INVALID; }
-    if (K % 32 != 0 || M < 0) { set_error("s3e_quantize_rows: K=%lld must be a multiple of 32", (long long)K); return S3E_ERR_INVALID; }
+    if (M < 0) { set_error("s3e_quantize_rows: negative M"); return S3E_ERR_INVALID; }
+    if (K % 32 != 0) { set_error("s3e_quantize_rows: K=%lld must be a multiple of 32", (long long)K); return S3E_ERR_INVALID; }
     Act a;
     a.x = qs;
     a.d = d;
@@ -552,6 +553,7 @@ extern "C" int s3e_quantize_rows(s3e_ctx *ctx, int type, const float *X, int64_t
         return S3E_ERR_INVALID;
     }
     if ((a.kind != A_F16 && !d) || (a.kind == A_Q8_1 && !s)) { set_error("s3e_quantize_rows: missing scale buffer"); return S3E_ERR_INVALID; }
+    if (M == 0) return S3E_OK;  // an empty batch: nothing to convert
     HIP_TRY(hipSetDevice(ctx->device));
     HIP_TRY(launch_rows_quant(a.kind, X, M, K, a, ctx->stream));
     return S3E_OK;

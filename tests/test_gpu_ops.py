@@ -431,6 +431,37 @@ def test_flash_attn_rejects(ctx):
             ctx.flash_attn_ext(buf, nb, buf, nb, buf, nb, D, 8, 8, 1, 1, 0.125, buf, prec=prec)
 
 
+@pytest.mark.parametrize("wt", [orc.Q4_0, orc.Q4_1, orc.Q8_0, orc.F16, orc.F32],
+                         ids=lambda t: {0: "f32", 1: "f16", 2: "q4_0", 3: "q4_1", 8: "q8_0"}[t])
+def test_empty_shapes(ctx, wt):
+    """An empty batch: ggml_mul_mat over zero rows of X is a no-op (the call
+    succeeds and writes nothing, also through the activation conversion),
+    a negative row count is refused, and flash attention refuses an empty
+    query, key, head or batch extent."""
+    rng = np.random.default_rng(wt + 21)
+    N, K = 64, 128
+    w = ctx.weight(wt, K, N, orc.to_weight_bytes(wt, rng.normal(0, 0.02, (N, K)).astype(np.float32)))
+    X = ctx.to_device(rng.standard_normal((2, K)).astype(np.float32))
+    sentinel = np.full((2, N), 7.0, np.float32)
+    Yd = ctx.to_device(sentinel)
+    ctx.mul_mat(w, X, 0, Yd)
+    ctx.sync()
+    assert np.array_equal(Yd.download(np.float32, (2, N)), sentinel)
+    with pytest.raises(s3e.S3EError):
+        ctx.mul_mat(w, X, -1, Yd)
+    if wt != orc.F32:
+        vdt = orc.VEC_DOT[wt]
+        qs = ctx.buffer(4096)
+        ctx.quantize_rows(vdt, X, 0, K, qs, qs if vdt != orc.F16 else None, qs if vdt == orc.Q8_1 else None)
+        ctx.sync()
+    w.free()
+    buf = ctx.buffer(1 << 20)
+    nb = (1, 64, 64 * 64, 64 * 64)
+    for Nq, Nkv, nh, B in [(0, 8, 1, 1), (8, 0, 1, 1), (8, 8, 0, 1), (8, 8, 1, 0)]:
+        with pytest.raises(s3e.S3EError):
+            ctx.flash_attn_ext(buf, nb, buf, nb, buf, nb, 64, Nq, Nkv, nh, B, 0.125, buf, prec=1)
+
+
 def _f16_bits(a):
     return np.ascontiguousarray(a.astype(np.float16)).view(np.uint16)
 
