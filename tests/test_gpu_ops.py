@@ -429,6 +429,11 @@ def test_flash_attn_rejects(ctx):
     for D, prec in [(130, 1), (6, 1), (256, 1), (192, 0), (0, 1)]:
         with pytest.raises(s3e.S3EError):
             ctx.flash_attn_ext(buf, nb, buf, nb, buf, nb, D, 8, 8, 1, 1, 0.125, buf, prec=prec)
+    # past the launch limits (batch × heads on one grid axis, 2^24 tokens);
+    # refused on the host before anything is read
+    for Nq, Nkv, nh, B in [(8, 8, 65536, 1), (8, 8, 256, 256), ((1 << 24) + 1, 8, 1, 1), (8, (1 << 24) + 1, 1, 1)]:
+        with pytest.raises(s3e.S3EError):
+            ctx.flash_attn_ext(buf, nb, buf, nb, buf, nb, 64, Nq, Nkv, nh, B, 0.125, buf, prec=1)
 
 
 @pytest.mark.parametrize("wt", [orc.Q4_0, orc.Q4_1, orc.Q8_0, orc.F16, orc.F32],
@@ -515,6 +520,11 @@ def test_flash_attn_f16_rejects(ctx):
         ctx.flash_attn_ext_f16(x, nb, x, nb, x, nb, 60 + 2, 64, 64, 1, 1, 0.1, o)  # head dim not a multiple of 4
     with pytest.raises(s3e.S3EError):
         ctx.flash_attn_ext_f16(x, (2, 64, 4096, 4096), x, nb, x, nb, 64, 64, 64, 1, 1, 0.1, o)  # strided d
+    # empty extents, and past the launch limits; refused on the host
+    for Nq, Nkv, nh, B in [(0, 64, 1, 1), (64, 0, 1, 1), (64, 64, 0, 1), (64, 64, 1, 0), (8, 8, 65536, 1),
+                           ((1 << 24) + 1, 8, 1, 1)]:
+        with pytest.raises(s3e.S3EError):
+            ctx.flash_attn_ext_f16(x, nb, x, nb, x, nb, 64, Nq, Nkv, nh, B, 0.1, o)
 
 
 def _ggml_q8_0_rows(codes: np.ndarray, d_bits: np.ndarray) -> np.ndarray:
